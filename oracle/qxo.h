@@ -1,0 +1,66 @@
+/* ORACLE — test infrastructure only.  A scalar CPU restatement of the reference's
+ * f32 decode path (reference src/qx_format.c), used by tests/, smoke() and the
+ * cpu_baseline leg of bench.py as the checker.  The product path never links it.
+ *
+ * Every function cites the reference lines it restates.  Numeric contract
+ * ("f32" activation mode): weights decode to f32 with the reference's op order,
+ * products widen to double and accumulate in double in index order, results
+ * narrow to float. */
+#ifndef QXO_H
+#define QXO_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct qxo_model qxo_model;
+
+float qxo_fp16_to_f32(uint16_t h);
+/* 256 values of one block of ggml type 12/14/17/18/23; returns 0 on unknown type */
+int qxo_decode_block(uint32_t ggml_type, const uint8_t *raw, float out[256]);
+uint64_t qxo_fnv1a64(const void *p, uint64_t n);
+
+qxo_model *qxo_open(const char *path);            /* NULL on failure */
+void qxo_close(qxo_model *m);
+const uint8_t *qxo_tensor(const qxo_model *m, const char *name, uint32_t *type, uint64_t dims[4], uint64_t *bytes);
+
+/* primitives */
+void qxo_rmsnorm(const float *x, const float *w, float *y, uint32_t n, double *rms_out);
+void qxo_head_rmsnorm(float *v, const float *w, uint32_t heads, uint32_t head_dim);
+void qxo_rope(float *v, uint32_t heads, uint32_t head_dim, uint32_t pos, double theta);
+float qxo_quantize_int8(const float *src, int8_t *dst, uint32_t n);
+/* y[r] = (float) sum double(w) * double(x); non-finite -> 0 */
+void qxo_matvec(uint32_t ggml_type, const uint8_t *w, uint32_t rows, uint32_t in_dims, const float *x, float *y);
+
+/* Q6_K head on a residual: output_norm then 151936 (vocab) rows; top_n <= 32 ids
+ * ordered by (double logit desc, index asc).  Returns 0 on a non-finite logit. */
+int qxo_final_head(qxo_model *m, const float *residual, float *norm_out, float *logits,
+                   uint32_t top_n, uint32_t *top_ids, double *top_logits);
+
+/* MoE block on ffn_inp: writes layer_out = ffn_inp + moe (and moe_out if non-NULL). */
+int qxo_moe_layer(qxo_model *m, uint32_t layer, const float *ffn_inp, float *layer_out, float *moe_out,
+                  uint32_t ids[8], double weights[8]);
+
+/* Attention block for one token at `pos`: attn RMSNorm, K/V projection, k norm +
+ * RoPE, INT8 quantize + store at [layer][pos], then Q projection/norm/RoPE, GQA
+ * softmax over positions 0..pos and the O projection.  attn_out = O·ctx (no
+ * residual).  kcache/vcache are [layers][ctx][512] int8, scales [layers*ctx]. */
+int qxo_attention_layer(qxo_model *m, uint32_t layer, uint32_t pos, uint32_t ctx,
+                        const float *x_in, int8_t *kcache, int8_t *vcache, float *kscales, float *vscales,
+                        float *attn_out, float *kqv_out, float *vcur_out);
+
+/* One full token: embedding (Q4_K row), layers [0, layers), optional head.
+ * layer_out (may be NULL) receives layers x 2048 floats of per-layer outputs. */
+int qxo_decode_token(qxo_model *m, uint32_t token, uint32_t pos, uint32_t ctx, uint32_t layers,
+                     int8_t *kcache, int8_t *vcache, float *kscales, float *vscales,
+                     float *residual_out, float *layer_out, int run_head, float *logits,
+                     uint32_t top_n, uint32_t *top_ids, double *top_logits);
+
+/* Decodes the Q4_K embedding row of `token` (reference src/qx_format.c:3759-3793). */
+int qxo_embed(qxo_model *m, uint32_t token, float *x);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
