@@ -1,0 +1,169 @@
+"""Batch-1 decode benchmark of the 48-layer Qwen3-30B-A3B-shaped random-init model
+(config 4 of the hot path) on one MI355X, with the roofline of the dominant
+kernel and the oracle's CPU time on a bounded sample of the same workload.
+
+A step is one greedy decode token: Q4_K embedding, 48 x (attention with INT8 KV +
+top-8 MoE), output RMSNorm and the full Q6_K head with argmax fed back on the
+device.  Prints one JSON line."""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qx-mini-c_amd"))
+
+HBM_PEAK_GBS = 8000.0
+LAYERS, VOCAB, EXPERTS = 48, 151936, 128
+# algorithmic bytes (weights read once per use; 74/98/136/210/144-byte blocks)
+GATE_UP_WEIGHTS = 8 * 2 * 768 * 8 * 74          # 8 experts x (gate, up) x 768 rows x 8 blocks
+DOWN_WEIGHTS = 8 * 2048 * 3 * 98
+ATTN_WEIGHTS = (4096 + 512 + 512) * 8 * 136 + 2048 * 16 * 136
+ROUTER = 128 * 2048 * 4
+NORMS = 2048 * 4 * 2 + 128 * 4 * 2
+LAYER_BYTES = GATE_UP_WEIGHTS + DOWN_WEIGHTS + ATTN_WEIGHTS + ROUTER + NORMS      # 23,184,384
+HEAD_BYTES = VOCAB * 8 * 210
+TOKEN_BYTES = LAYERS * LAYER_BYTES + HEAD_BYTES + 2048 * 4 + 8 * 144            # 1,368,112,256
+KERNEL_BYTES = {
+    # weights + activations read + outputs written, per launch
+    "gate_up": GATE_UP_WEIGHTS + 2048 * 4 * 2 + 8 * 768 * 4,
+    "down": DOWN_WEIGHTS + 8 * 768 * 4 + 2048 * 4 * 2,
+    "qkv": (4096 + 512 + 512) * 8 * 136 + 2048 * 4 * 2 + 5120 * 4,
+    "oproj": 2048 * 16 * 136 + 4096 * 4 + 2048 * 4 * 2,
+    "head": HEAD_BYTES + 2048 * 4 * 2 + VOCAB * 4,
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def kv_bytes(p0, n):
+    """INT8 K+V rows (512 B each) and two f32 scales per position, 48 layers, positions p0..p0+n-1."""
+    return sum(LAYERS * (p + 1) * 1032 for p in range(p0, p0 + n))
+
+
+def cpu_baseline(model_path, tokens, budget_s):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import qxo
+    m = qxo.Model(model_path)
+    kv = qxo.KV(LAYERS, 16)
+    done, t0, c0 = 0, time.perf_counter(), time.process_time()
+    tok = tokens[0]
+    while done < 2:
+        _, _, _, ids, _ = qxo.decode_token(m, tok, done, kv, LAYERS, True, VOCAB, 1)
+        tok = int(ids[0])
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    wall, cpu = time.perf_counter() - t0, time.process_time() - c0
+    m.close()
+    return {"value": done / wall, "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{done} greedy decode tokens at positions 0..{done - 1} of the same model (oracle/qxo.c, "
+                      f"scalar, 1 thread); wall {wall:.2f} s, process CPU {cpu:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--roofline-kernel", default="gate_up", choices=sorted(KERNEL_BYTES))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=25.0)
+    ap.add_argument("--seed", type=int, default=1)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(1)
+    import qxg
+
+    prompt_len = 8
+    if prompt_len + max(args.steps, args.warmup) > 4096:
+        sys.exit("steps exceed the 4096-token context")
+    ctx_tokens = prompt_len + max(args.steps, args.warmup) + 1
+    prompt = np.random.default_rng(args.seed).integers(0, VOCAB, size=prompt_len).astype(np.uint32)
+
+    t0 = time.perf_counter()
+    model = qxg.MemModel(LAYERS, VOCAB, EXPERTS, True, True, seed=args.seed)
+    log(f"generated the {LAYERS}-layer model in memory in {time.perf_counter() - t0:.1f} s ({model.path})")
+    ctx = qxg.Context(0)
+    t0 = time.perf_counter()
+    info = ctx.load(model.path, verify=False)
+    log(f"uploaded {info.tensors} tensors, {info.tensor_bytes / 1e9:.3f} GB in {time.perf_counter() - t0:.1f} s")
+
+    def prefill():
+        ctx.kv_create(LAYERS, ctx_tokens)
+        first, _ = ctx.generate(prompt, 1, 0)          # 8 steps, last one yields the first token
+        return int(first[0])
+
+    # warmup
+    first = prefill()
+    ctx.generate([first], max(args.warmup, 1), prompt_len)
+    log(f"warmup done ({args.warmup} tokens)")
+    # timed: K decode tokens at positions 8 .. 8+K-1, in-situ events around the roofline kernel
+    first = prefill()
+    which = qxg.KERNELS[args.roofline_kernel]
+    ctx.profile_kernel(which)
+    t0 = time.perf_counter()
+    toks, dev_ms = ctx.generate([first], args.steps, prompt_len)
+    wall = time.perf_counter() - t0
+    launches, kern_ms = ctx.profile_result()
+    ctx.profile_kernel(-1)
+    log(f"timed {args.steps} tokens: device {dev_ms:.2f} ms, wall {wall * 1e3:.2f} ms; "
+        f"{args.roofline_kernel}: {launches} launches, {kern_ms:.2f} ms")
+    # same region without event pairs, for the headline number
+    first = prefill()
+    t0 = time.perf_counter()
+    toks2, dev_ms2 = ctx.generate([first], args.steps, prompt_len)
+    wall2 = time.perf_counter() - t0
+    assert list(toks2) == list(toks), "greedy sequence changed between identical runs"
+    tok_s = args.steps / wall2
+    avg_kernel_s = kern_ms / 1e3 / max(launches, 1)
+    kb = KERNEL_BYTES[args.roofline_kernel]
+    achieved = kb / avg_kernel_s / 1e9
+    token_bytes = TOKEN_BYTES + kv_bytes(prompt_len, args.steps) / args.steps
+    out = {
+        "metric": "batch-1 decode tok/s (48 layers + Q6_K head)",
+        "value": round(tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall2 * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded random-init QXF1 (generator qxgen.c), seeded 8-token prompt",
+        "config": {"workload": "config4: Qwen3-30B-A3B-shaped decode, 48 layers + Q6_K head 2048x151936, "
+                               "greedy tokens after an 8-token prompt, INT8 KV",
+                   "layers": LAYERS, "vocab": VOCAB, "experts": EXPERTS, "top_k": 8, "prompt_tokens": prompt_len,
+                   "quant_mix": "IQ4_XS attn, IQ2_XS gate/up, IQ3_XXS down, Q6_K head, Q4_K embedding",
+                   "kv": "int8", "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "kernel": args.roofline_kernel, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": kb, "avg_launch_us": round(avg_kernel_s * 1e6, 3),
+                     "launches": launches},
+        "token_roofline": {"algorithmic_bytes_per_token": int(token_bytes),
+                           "achieved_GBs": round(token_bytes * tok_s / 1e9, 1),
+                           "frac": round(token_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+                           "device_ms_per_token": round(dev_ms2 / args.steps, 4)},
+        "first_tokens": [int(t) for t in toks[:8]],
+    }
+    ctx.close()
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle, 1 thread) ...")
+        out["cpu_baseline"] = cpu_baseline(model.path, [int(prompt[0])], args.cpu_budget)
+    else:
+        out["cpu_baseline"] = None
+    model.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -98,6 +98,22 @@ int qxgen_memfd(const qxgen_spec *spec, char *path_out, uint64_t path_len, int *
 void qxgen_memfd_close(int fd);
 
 /* ---- GPU-backed probes with the reference's entry-point semantics ---- */
+struct qxg_ctx;
+
+typedef struct qx_gpu_model_info {
+    uint32_t layers, vocab, experts;
+    int has_embedding, has_head;
+    uint64_t tensor_bytes;      /* sum of uploaded tensor bytes */
+    uint32_t tensors;
+} qx_gpu_model_info;
+
+/* Opens a QXF1 file (qxf_open), optionally verifies every tensor's FNV-1a-64
+ * (the reference verifies the head's on every token, src/qx_format.c:3631-3632;
+ * here it is done once, at load), uploads every tensor with qxg_upload_tensor and
+ * binds layers [0, manifest.layers).  Files without token_embd / output tensors
+ * bind without them. */
+int qx_gpu_load(struct qxg_ctx *ctx, const char *path, int verify_checksums, qx_gpu_model_info *info,
+                char *err, uint64_t err_len);
 
 /* reference qx_dump_decode_block_summary (include/qx_format.h:140): decodes one
  * 256-value block of tensor `name` on the GPU and prints its FNV over the floats. */

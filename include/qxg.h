@@ -1,0 +1,133 @@
+/* qxg — C ABI to the MI355X (gfx950) decode path.
+ *
+ * The reference has no process or device boundary: its state loop calls static
+ * C functions over mmap'd weight spans (reference src/qx_format.c:5970-6733).  This
+ * ABI is the seam that replaces those calls.  Each entry point below names the
+ * reference function(s) it stands in for.  Conventions follow the reference C API
+ * (reference include/qx_format.h:104-172): return 1 on success and 0 on failure,
+ * with a message written into (err, err_len).  Pointers are host pointers, sizes
+ * are plain integers, and calls are synchronous unless stated otherwise.  Each
+ * context owns one HIP stream and its device buffers.  A context is not
+ * thread-safe (the reference is single-threaded, src/qx_format.c:5984-5995).
+ *
+ * Fixed model geometry (reference --final-head manifest check,
+ * src/qx_format.c:6120-6124): hidden 2048, 32 q heads / 4 kv heads of 128,
+ * moe_intermediate 768, top-8 experts; vocab, experts (8..128) and layer count
+ * come from the uploaded tensors.
+ */
+#ifndef QXG_H
+#define QXG_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct qxg_ctx qxg_ctx;
+
+/* Creates a context on HIP device `device`: stream, codebooks, RoPE table.
+ * Stands in for the per-call setup of the reference state loop
+ * (src/qx_format.c:6044-6160). */
+int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len);
+void qxg_close(qxg_ctx *ctx);
+
+/* Uploads one tensor of the QXF1 file (bytes = the tensor's mmap span) and repacks
+ * quantized blocks on the device.  Replaces the per-call weight reads
+ * qx_read_raw_span / qx_acquire_span (src/qx_format.c:1757-1773, 858-893).
+ * ggml_type: 0 F32, 12 Q4_K, 14 Q6_K, 17 IQ2_XS, 18 IQ3_XXS, 23 IQ4_XS. */
+int qxg_upload_tensor(qxg_ctx *ctx, const char *name, uint32_t ggml_type, const uint64_t dims[4],
+                      const void *host_bytes, uint64_t nbytes, char *err, uint64_t err_len);
+
+/* Resolves the uploaded tensors into layers [0, layers), checks every shape and
+ * type (the checks of src/qx_format.c:5216-5235, 3610-3629), and sizes work
+ * buffers.  need_head / need_embedding select whether output.* / token_embd.* must
+ * be present. */
+int qxg_bind_model(qxg_ctx *ctx, uint32_t layers, int need_embedding, int need_head, char *err, uint64_t err_len);
+
+/* Persistent INT8 KV cache [layers][ctx_tokens][512] for K and V plus one f32 scale
+ * per (layer, position).  Same layout as the reference state loop
+ * (src/qx_format.c:6138-6160, 6343-6400).  kv_format must be 1 (int8). */
+int qxg_kv_create(qxg_ctx *ctx, uint32_t layers, uint32_t ctx_tokens, uint32_t kv_format, char *err, uint64_t err_len);
+/* Copies rows [pos0, pos0+count) of one layer into / out of the device cache.
+ * k, v: count*512 int8; kscale, vscale: count floats.  Used for QXKVSNP1
+ * import/export (src/qx_format.c:5860-5968) and for seeded long-context tests. */
+int qxg_kv_write(qxg_ctx *ctx, uint32_t layer, uint32_t pos0, uint32_t count, const int8_t *k, const int8_t *v,
+                 const float *kscale, const float *vscale, char *err, uint64_t err_len);
+int qxg_kv_read(qxg_ctx *ctx, uint32_t layer, uint32_t pos0, uint32_t count, int8_t *k, int8_t *v,
+                float *kscale, float *vscale, char *err, uint64_t err_len);
+
+/* One full token at `position`: Q4_K embedding, every bound layer (attention with
+ * INT8 KV append, then MoE), and if run_head the output RMSNorm, Q6_K head and
+ * top_n (<= 32) ids by (logit desc, index asc).  The loop body of
+ * qx_dump_prompt_state_loop_probe_summary (src/qx_format.c:6250-6627).
+ * Any output pointer may be NULL.  layer_out: layers*2048 floats (the per-layer
+ * "output" residual dumps, src/qx_format.c:6439).  Returns 0 on a non-finite
+ * logit (src/qx_format.c:3715). */
+int qxg_decode_token(qxg_ctx *ctx, uint32_t token, uint32_t position, int run_head,
+                     float *residual_out, float *layer_out, float *logits, uint32_t top_n,
+                     uint32_t *top_ids, double *top_logits, char *err, uint64_t err_len);
+
+/* Greedy loop on the device: feeds prompt[0..n_prompt) at positions pos0.., then
+ * generates n_gen tokens by argmax with the next token fed back on the device
+ * (no host round trip per step).  tokens_out receives the n_gen generated ids.
+ * Matches the step/phase sequence of src/qx_format.c:6250-6627 with temperature 0
+ * (qx_sample_from_top, src/qx_format.c:3045-3057).  If elapsed_ms is non-NULL it
+ * receives the device time of the whole loop (HIP events on the context stream). */
+int qxg_generate(qxg_ctx *ctx, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_gen, uint32_t pos0,
+                 uint32_t *tokens_out, float *elapsed_ms, char *err, uint64_t err_len);
+
+/* ---- same-input replay seams (host pointers in and out, synchronous) ---- */
+
+/* Q4_K embedding row of `token` as 2048 floats, no norm on the full-MoE path:
+ * replaces qx_fill_residual_vector_from_embedding (src/qx_format.c:3759-3793). */
+int qxg_embed_token(qxg_ctx *ctx, uint32_t token, float *x_out, char *err, uint64_t err_len);
+
+/* Decodes `nblocks` consecutive 256-value blocks of one type to f32, on the
+ * device, from the repacked layout, with the reference's op order (bit-exact with
+ * qx_decode_supported_block, src/qx_format.c:2206-2217). */
+int qxg_dequant_blocks(qxg_ctx *ctx, uint32_t ggml_type, const void *raw, uint64_t nblocks, float *out,
+                       char *err, uint64_t err_len);
+
+/* Attention block of `layer` for one token at `position` on residual x_in:
+ * attn RMSNorm, K/V projections, k norm + RoPE, INT8 append at [layer][position],
+ * Q projection/norm/RoPE, GQA softmax over 0..position, O projection.
+ * attn_out = O*ctx (without the residual).  Replaces the attention half of the
+ * layer loop (src/qx_format.c:6282-6423 and qx_rope_gqa_attention_partial,
+ * 5051-5196).  kqv_out: 4096 floats, vcur_out: 512 floats (dump phases
+ * "kqv-out" and "v-cur"). */
+int qxg_attention_layer(qxg_ctx *ctx, uint32_t layer, uint32_t position, const float *x_in, float *attn_out,
+                        float *kqv_out, float *vcur_out, char *err, uint64_t err_len);
+
+/* MoE block of `layer` on ffn_inp: replaces qx_apply_real_moe_layer
+ * (src/qx_format.c:5198-5317).  layer_out = ffn_inp + moe; moe_out (may be NULL)
+ * = the "ffn-moe-out" dump; ids/weights = selected experts in rank order. */
+int qxg_moe_layer(qxg_ctx *ctx, uint32_t layer, const float *ffn_inp, float *layer_out, float *moe_out,
+                  uint32_t ids[8], double weights[8], char *err, uint64_t err_len);
+
+/* Output head on a residual: replaces qx_compute_real_final_head
+ * (src/qx_format.c:3554-3738) as used by qx_dump_final_head_probe_summary
+ * (src/qx_format.c:5369-5411).  norm_out: 2048 floats, logits: vocab floats. */
+int qxg_final_head(qxg_ctx *ctx, const float *residual, float *norm_out, float *logits, uint32_t top_n,
+                   uint32_t *top_ids, double *top_logits, char *err, uint64_t err_len);
+
+/* ---- measurement (no reference counterpart: the reference times with clock(),
+ *      src/qx_format.c:6245, 6642-6653) ---- */
+
+/* Average device time (ms) of one launch of kernel `which` over `iters` launches,
+ * bracketed by HIP events on the context stream.  which: 0 gate/up experts,
+ * 1 down experts, 2 Q/K/V projection, 3 O projection, 4 Q6_K head, 5 attention,
+ * 6 router.  Uses layer `layer`'s weights and the current routing/KV state. */
+int qxg_time_kernel(qxg_ctx *ctx, int which, uint32_t layer, uint32_t iters, float *avg_ms, char *err, uint64_t err_len);
+/* Device bytes held by uploaded tensors (repacked; equal to the QXF1 tensor bytes). */
+uint64_t qxg_device_bytes(const qxg_ctx *ctx);
+/* In-situ timing: while enabled, qxg_generate / qxg_decode_token record a HIP
+ * event pair around every launch of kernel `which` (numbering of
+ * qxg_time_kernel; -1 disables).  qxg_profile_result sums the pairs. */
+int qxg_profile_kernel(qxg_ctx *ctx, int which);
+int qxg_profile_result(qxg_ctx *ctx, uint32_t *launches, double *total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

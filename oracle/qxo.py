@@ -1,0 +1,129 @@
+"""ORACLE — test infrastructure only.  ctypes binding of liboracle.so (qxo.h), the
+scalar CPU restatement of the reference's f32 path.  Imported by tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg only, as the checker."""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_path = os.path.join(HERE, "liboracle.so")
+if not os.path.exists(_path):
+    raise RuntimeError(f"{_path} is not built: run `make -C {HERE} oracle`")
+_o = ctypes.CDLL(_path)
+vp, u32, u64, c_int = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
+
+
+def _sig(name, args, res=c_int):
+    f = getattr(_o, name)
+    f.argtypes = args
+    f.restype = res
+
+
+_sig("qxo_open", [ctypes.c_char_p], vp)
+_sig("qxo_close", [vp], None)
+_sig("qxo_fp16_to_f32", [ctypes.c_uint16], ctypes.c_float)
+_sig("qxo_decode_block", [u32, vp, vp])
+_sig("qxo_fnv1a64", [vp, u64], u64)
+_sig("qxo_tensor", [vp, ctypes.c_char_p, ctypes.POINTER(u32), vp, ctypes.POINTER(u64)], vp)
+_sig("qxo_final_head", [vp, vp, vp, vp, u32, vp, vp])
+_sig("qxo_moe_layer", [vp, u32, vp, vp, vp, vp, vp])
+_sig("qxo_attention_layer", [vp, u32, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp])
+_sig("qxo_decode_token", [vp, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp, c_int, vp, u32, vp, vp])
+_sig("qxo_embed", [vp, u32, vp])
+_sig("qxo_matvec", [u32, vp, u32, u32, vp, vp], None)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(vp)
+
+
+def fnv1a64(a):
+    a = np.ascontiguousarray(a)
+    return int(_o.qxo_fnv1a64(_p(a), a.nbytes))
+
+
+def fp16_to_f32(h):
+    return float(_o.qxo_fp16_to_f32(h))
+
+
+def decode_block(ggml_type, raw):
+    raw = np.ascontiguousarray(raw, np.uint8)
+    out = np.zeros(256, np.float32)
+    if not _o.qxo_decode_block(ggml_type, _p(raw), _p(out)):
+        raise ValueError("unsupported type")
+    return out
+
+
+class Model:
+    """A QXF1 file opened by the oracle (mmap)."""
+
+    def __init__(self, path):
+        self._m = _o.qxo_open(str(path).encode())
+        if not self._m:
+            raise RuntimeError(f"oracle cannot open {path}")
+
+    def close(self):
+        if self._m:
+            _o.qxo_close(self._m)
+            self._m = None
+
+    def tensor(self, name):
+        t = u32(); n = u64(); dims = np.zeros(4, np.uint64)
+        p = _o.qxo_tensor(self._m, name.encode(), ctypes.byref(t), _p(dims), ctypes.byref(n))
+        if not p:
+            raise KeyError(name)
+        buf = (ctypes.c_uint8 * n.value).from_address(p)
+        return t.value, dims, np.frombuffer(buf, np.uint8)
+
+    def final_head(self, residual, vocab, top_n=8):
+        r = np.ascontiguousarray(residual, np.float32)
+        nrm = np.zeros(2048, np.float32); lg = np.zeros(vocab, np.float32)
+        ids = np.zeros(top_n, np.uint32); tl = np.zeros(top_n)
+        if not _o.qxo_final_head(self._m, _p(r), _p(nrm), _p(lg), top_n, _p(ids), _p(tl)):
+            raise RuntimeError("oracle final head failed (non-finite logit?)")
+        return nrm, lg, ids, tl
+
+    def moe_layer(self, layer, x):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(2048, np.float32); moe = np.zeros(2048, np.float32)
+        ids = np.zeros(8, np.uint32); w = np.zeros(8)
+        if not _o.qxo_moe_layer(self._m, layer, _p(x), _p(y), _p(moe), _p(ids), _p(w)):
+            raise RuntimeError("oracle MoE failed")
+        return y, moe, ids, w
+
+    def embed(self, token):
+        x = np.zeros(2048, np.float32)
+        if not _o.qxo_embed(self._m, token, _p(x)):
+            raise RuntimeError("oracle embed failed")
+        return x
+
+
+class KV:
+    """Host INT8 KV cache in the reference layout [layers][ctx][512]."""
+
+    def __init__(self, layers, ctx):
+        self.layers, self.ctx = layers, ctx
+        self.k = np.zeros((layers, ctx, 512), np.int8)
+        self.v = np.zeros((layers, ctx, 512), np.int8)
+        self.ks = np.zeros((layers, ctx), np.float32)
+        self.vs = np.zeros((layers, ctx), np.float32)
+
+
+def attention_layer(model, layer, pos, kv, x):
+    x = np.ascontiguousarray(x, np.float32)
+    a = np.zeros(2048, np.float32); kqv = np.zeros(4096, np.float32); vcur = np.zeros(512, np.float32)
+    if not _o.qxo_attention_layer(model._m, layer, pos, kv.ctx, _p(x), _p(kv.k), _p(kv.v), _p(kv.ks), _p(kv.vs),
+                                  _p(a), _p(kqv), _p(vcur)):
+        raise RuntimeError("oracle attention failed")
+    return a, kqv, vcur
+
+
+def decode_token(model, token, pos, kv, layers, run_head, vocab, top_n=8):
+    res = np.zeros(2048, np.float32); lay = np.zeros((layers, 2048), np.float32)
+    lg = np.zeros(vocab, np.float32) if run_head else None
+    ids = np.zeros(top_n, np.uint32); tl = np.zeros(top_n)
+    if not _o.qxo_decode_token(model._m, token, pos, kv.ctx, layers, _p(kv.k), _p(kv.v), _p(kv.ks), _p(kv.vs),
+                               _p(res), _p(lay), int(run_head), _p(lg), top_n, _p(ids), _p(tl)):
+        raise RuntimeError("oracle decode failed")
+    return res, lay, lg, ids, tl

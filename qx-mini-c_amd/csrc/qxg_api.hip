@@ -1,0 +1,709 @@
+// C-ABI implementation of include/qxg.h: context, tensor upload + repack,
+// model binding, INT8 KV cache, and the launch sequence of one decode step.
+#include "qxg.h"
+#include "qxg_internal.h"
+#include "qx_grids.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+extern "C" {
+__global__ void qxk_embed(const uint8_t *, uint64_t, const uint32_t *, const DevState *, float *);
+__global__ void qxk_qk_rope_kv(float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
+                               uint32_t, uint32_t, const DevState *, float *);
+__global__ void qxk_attn(const float *, const int8_t *, const int8_t *, const float *, const float *, uint32_t,
+                         uint32_t, double, const DevState *, float *);
+__global__ void qxk_router(const float *, const float *, const float *, uint32_t, double *, DevState *);
+__global__ void qxk_topk(const float *, uint32_t, uint32_t, float *, uint32_t *, float *, uint32_t *, uint32_t *,
+                         DevState *);
+__global__ void qxk_advance(DevState *);
+__global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
+                            uint64_t, float *);
+__global__ void qxk_repack(uint32_t, const uint8_t *, uint64_t, uint8_t *, uint8_t *, uint8_t *, uint16_t *);
+void qxl_qkv(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, const QTensor *, float *);
+void qxl_oproj(hipStream_t, const float *, const QTensor *, float *, float *);
+void qxl_gate_up(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, Tables, const DevState *,
+                 float *);
+void qxl_down(hipStream_t, const float *, const QTensor *, Tables, const DevState *, float *, float *);
+void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32_t, DevState *, float *, float *);
+}
+
+namespace {
+constexpr uint32_t TOPK_BLOCKS = 128;
+
+void set_err(char *err, uint64_t n, const char *msg) {
+    if (err && n) snprintf(err, (size_t)n, "%s", msg);
+}
+
+bool hip_ok(hipError_t e, char *err, uint64_t n, const char *what) {
+    if (e == hipSuccess) return true;
+    if (err && n) snprintf(err, (size_t)n, "%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+uint64_t align256(uint64_t v) { return (v + 255) & ~255ull; }
+
+bool block_geom(uint32_t t, uint64_t &bv, uint64_t &bb) {
+    switch (t) {
+    case 0: bv = 1; bb = 4; return true;
+    case 12: bv = 256; bb = 144; return true;
+    case 14: bv = 256; bb = 210; return true;
+    case 17: bv = 256; bb = 74; return true;
+    case 18: bv = 256; bb = 98; return true;
+    case 23: bv = 256; bb = 136; return true;
+    default: return false;
+    }
+}
+
+struct KernelTiming {
+    int which = -1;
+    std::vector<hipEvent_t> ev;   // pairs
+    uint32_t used = 0;
+};
+}  // namespace
+
+struct qxg_ctx {
+    int device = 0;
+    hipStream_t s = nullptr;
+    Tables T{};
+    std::map<std::string, QTensor> tens;
+    uint64_t dev_bytes = 0;
+    // bound model
+    bool bound = false;
+    uint32_t layers = 0, vocab = 0, experts = 0;
+    std::vector<LayerW> L;
+    const uint8_t *emb = nullptr;
+    uint64_t emb_row = 0;
+    const float *out_norm = nullptr;
+    const QTensor *head = nullptr;
+    // KV
+    int8_t *kc = nullptr, *vc = nullptr;
+    float *ks = nullptr, *vs = nullptr;
+    uint32_t kv_layers = 0, kv_ctx = 0;
+    // work buffers
+    float *x = nullptr, *qkv = nullptr, *ctxv = nullptr, *h = nullptr, *logits = nullptr;
+    float *vcur = nullptr, *attn = nullptr, *moe = nullptr, *norm = nullptr, *layer_dump = nullptr;
+    double *rlog = nullptr;
+    float *cand_v = nullptr, *top_v = nullptr;
+    uint32_t *cand_i = nullptr, *top_i = nullptr, *tokens = nullptr;
+    DevState *st = nullptr;
+    uint8_t *staging = nullptr;
+    uint64_t staging_bytes = 0;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    KernelTiming kt;
+};
+
+namespace {
+bool upload_planes(qxg_ctx *c, QTensor &t, const void *host, uint64_t nbytes, char *err, uint64_t n) {
+    uint64_t bv = 0, bb = 0;
+    block_geom(t.type, bv, bb);
+    t.bytes = nbytes;
+    t.nblocks = nbytes / bb;
+    uint64_t sz[4] = {0, 0, 0, 0};   // p0, p1, p2, d
+    const uint64_t nb = t.nblocks;
+    switch (t.type) {
+    case 23: sz[0] = 128 * nb; sz[1] = 8 * nb; break;
+    case 17: sz[0] = 64 * nb; sz[1] = 8 * nb; sz[3] = 2 * nb; break;
+    case 18: sz[0] = 64 * nb; sz[1] = 32 * nb; sz[3] = 2 * nb; break;
+    case 14: sz[0] = 128 * nb; sz[1] = 64 * nb; sz[2] = 16 * nb; sz[3] = 2 * nb; break;
+    default: sz[0] = nbytes; break;   // F32, Q4_K: original bytes
+    }
+    const uint64_t total = align256(sz[0]) + align256(sz[1]) + align256(sz[2]) + align256(sz[3]);
+    if (!hip_ok(hipMalloc(&t.base, total), err, n, "hipMalloc tensor")) return false;
+    c->dev_bytes += nbytes;
+    uint8_t *p = t.base;
+    uint8_t *pl[4];
+    for (int i = 0; i < 4; ++i) { pl[i] = sz[i] ? p : nullptr; p += align256(sz[i]); }
+    t.p0 = pl[0]; t.p1 = pl[1]; t.p2 = pl[2]; t.d = (const uint16_t *)pl[3];
+    if (t.type == 0 || t.type == 12) {
+        return hip_ok(hipMemcpy(t.base, host, nbytes, hipMemcpyHostToDevice), err, n, "upload");
+    }
+    if (c->staging_bytes < nbytes) {
+        if (c->staging) (void)hipFree(c->staging);
+        c->staging = nullptr;
+        c->staging_bytes = 0;
+        if (!hip_ok(hipMalloc(&c->staging, nbytes), err, n, "hipMalloc staging")) return false;
+        c->staging_bytes = nbytes;
+    }
+    if (!hip_ok(hipMemcpy(c->staging, host, nbytes, hipMemcpyHostToDevice), err, n, "upload")) return false;
+    const unsigned grid = (unsigned)((nb + 255) / 256);
+    hipLaunchKernelGGL(qxk_repack, dim3(grid), dim3(256), 0, c->s, t.type, c->staging, nb, pl[0], pl[1], pl[2],
+                       (uint16_t *)pl[3]);
+    if (!hip_ok(hipGetLastError(), err, n, "repack launch")) return false;
+    return hip_ok(hipStreamSynchronize(c->s), err, n, "repack");
+}
+
+void free_tensor(QTensor &t) {
+    if (t.base) (void)hipFree(t.base);
+    t.base = nullptr;
+}
+
+void build_tables(std::vector<uint4> &g2, std::vector<uint2> &g3, std::vector<uint2> &sel) {
+    g2.resize(512);
+    for (int i = 0; i < 512; ++i) {
+        uint32_t pos[2] = {0, 0}, neg[2] = {0, 0};
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t v = qx_iq2xs_levels[(qx_iq2xs_packed[i] >> (2 * j)) & 3];
+            pos[j >> 2] |= v << (8 * (j & 3));
+            neg[j >> 2] |= ((256u - v) & 255u) << (8 * (j & 3));
+        }
+        g2[i] = make_uint4(pos[0], pos[1], neg[0], neg[1]);
+    }
+    g3.resize(256);
+    for (int i = 0; i < 256; ++i) {
+        uint32_t pos = 0, neg = 0;
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t v = qx_iq3xxs_levels[(qx_iq3xxs_packed[i] >> (3 * j)) & 7];
+            pos |= v << (8 * j);
+            neg |= ((256u - v) & 255u) << (8 * j);
+        }
+        g3[i] = make_uint2(pos, neg);
+    }
+    sel.resize(128);
+    for (uint32_t i = 0; i < 128; ++i) {
+        const uint32_t s = i | ((uint32_t)(__builtin_popcount(i) & 1) << 7);   // ksigns (ggml)
+        uint32_t a = 0, b = 0;
+        for (int j = 0; j < 4; ++j) {
+            a |= (uint32_t)(j + 4 * ((s >> j) & 1)) << (8 * j);
+            b |= (uint32_t)(j + 4 * ((s >> (j + 4)) & 1)) << (8 * j);
+        }
+        sel[i] = make_uint2(a, b);
+    }
+}
+
+void write_state(qxg_ctx *c, uint32_t pos0, uint32_t step, uint32_t n_prompt, uint32_t force_head) {
+    DevState h{};
+    h.pos0 = pos0; h.step = step; h.n_prompt = n_prompt; h.force_head = force_head;
+    (void)hipMemcpyAsync(c->st, &h, offsetof(DevState, moe_ids), hipMemcpyHostToDevice, c->s);
+}
+
+const QTensor *find(qxg_ctx *c, const std::string &name) {
+    auto it = c->tens.find(name);
+    return it == c->tens.end() ? nullptr : &it->second;
+}
+
+void timed_begin(qxg_ctx *c, int which) {
+    if (c->kt.which != which) return;
+    if (c->kt.used * 2 + 2 > c->kt.ev.size()) {
+        for (int i = 0; i < 256; ++i) { hipEvent_t e; (void)hipEventCreate(&e); c->kt.ev.push_back(e); }
+    }
+    (void)hipEventRecord(c->kt.ev[2 * c->kt.used], c->s);
+}
+
+void timed_end(qxg_ctx *c, int which) {
+    if (c->kt.which != which) return;
+    (void)hipEventRecord(c->kt.ev[2 * c->kt.used + 1], c->s);
+    ++c->kt.used;
+}
+
+// ---- launch sequences (all asynchronous on c->s) ----
+void launch_attention(qxg_ctx *c, uint32_t l, float *x, float *attn_dump, float *vcur_dump) {
+    const LayerW &w = c->L[l];
+    timed_begin(c, 2);
+    qxl_qkv(c->s, x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv);
+    timed_end(c, 2);
+    hipLaunchKernelGGL(qxk_qk_rope_kv, dim3(33), dim3(128), 0, c->s, c->qkv, w.q_norm, w.k_norm, c->T, c->kc, c->vc,
+                       c->ks, c->vs, l, c->kv_ctx, c->st, vcur_dump);
+    timed_begin(c, 5);
+    hipLaunchKernelGGL(qxk_attn, dim3(32), dim3(512), (size_t)c->kv_ctx * sizeof(double), c->s, c->qkv, c->kc,
+                       c->vc, c->ks, c->vs, l, c->kv_ctx, std::sqrt(128.0), c->st, c->ctxv);
+    timed_end(c, 5);
+    timed_begin(c, 3);
+    qxl_oproj(c->s, c->ctxv, w.wo, x, attn_dump);
+    timed_end(c, 3);
+}
+
+void launch_moe(qxg_ctx *c, uint32_t l, float *x, float *moe_dump) {
+    const LayerW &w = c->L[l];
+    timed_begin(c, 6);
+    hipLaunchKernelGGL(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, x, w.ffn_norm, w.router,
+                       c->experts, c->rlog, c->st);
+    timed_end(c, 6);
+    timed_begin(c, 0);
+    qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->st, c->h);
+    timed_end(c, 0);
+    timed_begin(c, 1);
+    qxl_down(c->s, c->h, w.down, c->T, c->st, x, moe_dump);
+    timed_end(c, 1);
+}
+
+void launch_head(qxg_ctx *c, uint32_t top_n, float *norm_dump) {
+    timed_begin(c, 4);
+    qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, norm_dump);
+    timed_end(c, 4);
+    hipLaunchKernelGGL(qxk_topk, dim3(TOPK_BLOCKS), dim3(256), 0, c->s, c->logits, c->vocab, top_n, c->cand_v,
+                       c->cand_i, c->top_v, c->top_i, c->tokens, c->st);
+}
+
+void launch_step(qxg_ctx *c, uint32_t top_n, bool dump_layers) {
+    hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
+    for (uint32_t l = 0; l < c->layers; ++l) {
+        launch_attention(c, l, c->x, nullptr, nullptr);
+        launch_moe(c, l, c->x, nullptr);
+        if (dump_layers)
+            (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * sizeof(float), hipMemcpyDeviceToDevice, c->s);
+    }
+    if (c->head) launch_head(c, top_n, nullptr);
+}
+
+bool check_ready(qxg_ctx *c, bool need_kv, char *err, uint64_t n) {
+    if (!c) { set_err(err, n, "invalid context"); return false; }
+    if (!c->bound) { set_err(err, n, "model not bound"); return false; }
+    if (need_kv && !c->kc) { set_err(err, n, "KV cache not created"); return false; }
+    return true;
+}
+
+bool finish(qxg_ctx *c, char *err, uint64_t n) {
+    if (!hip_ok(hipGetLastError(), err, n, "launch")) return false;
+    return hip_ok(hipStreamSynchronize(c->s), err, n, "stream");
+}
+
+bool read_state(qxg_ctx *c, DevState &h, char *err, uint64_t n) {
+    return hip_ok(hipMemcpyAsync(&h, c->st, sizeof(h), hipMemcpyDeviceToHost, c->s), err, n, "state read") &&
+           hip_ok(hipStreamSynchronize(c->s), err, n, "stream");
+}
+}  // namespace
+
+extern "C" {
+
+int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
+    if (!out) { set_err(err, err_len, "invalid argument"); return 0; }
+    *out = nullptr;
+    int count = 0;
+    if (!hip_ok(hipGetDeviceCount(&count), err, err_len, "hipGetDeviceCount")) return 0;
+    if (device < 0 || device >= count) { set_err(err, err_len, "no such HIP device"); return 0; }
+    if (!hip_ok(hipSetDevice(device), err, err_len, "hipSetDevice")) return 0;
+    hipDeviceProp_t prop;
+    if (!hip_ok(hipGetDeviceProperties(&prop, device), err, err_len, "hipGetDeviceProperties")) return 0;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        if (err && err_len) snprintf(err, (size_t)err_len, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+        return 0;
+    }
+    qxg_ctx *c = new qxg_ctx();
+    c->device = device;
+    bool ok = hip_ok(hipStreamCreateWithFlags(&c->s, hipStreamNonBlocking), err, err_len, "stream");
+    std::vector<uint4> g2;
+    std::vector<uint2> g3, sel;
+    build_tables(g2, g3, sel);
+    std::vector<double> rc((size_t)QXG_MAX_CTX * 64), rs((size_t)QXG_MAX_CTX * 64);
+    // reference qx_apply_rope (src/qx_format.c:4625-4641): f = pow(theta, -(2i)/hd), angle = pos*f,
+    // double cos/sin -- evaluated once here with the host libm.
+    for (uint32_t p = 0; p < QXG_MAX_CTX; ++p)
+        for (uint32_t i = 0; i < 64; ++i) {
+            const double f = pow(1000000.0, -(2.0 * (double)i) / 128.0);
+            const double a = (double)p * f;
+            rc[p * 64 + i] = cos(a);
+            rs[p * 64 + i] = sin(a);
+        }
+    ok = ok && hip_ok(hipMalloc(&c->T.g2, g2.size() * sizeof(uint4)), err, err_len, "tables") &&
+         hip_ok(hipMalloc(&c->T.g3, g3.size() * sizeof(uint2)), err, err_len, "tables") &&
+         hip_ok(hipMalloc(&c->T.sel, sel.size() * sizeof(uint2)), err, err_len, "tables") &&
+         hip_ok(hipMalloc(&c->T.rope_cos, rc.size() * sizeof(double)), err, err_len, "tables") &&
+         hip_ok(hipMalloc(&c->T.rope_sin, rs.size() * sizeof(double)), err, err_len, "tables");
+    ok = ok && hip_ok(hipMemcpy(c->T.g2, g2.data(), g2.size() * sizeof(uint4), hipMemcpyHostToDevice), err, err_len, "tables") &&
+         hip_ok(hipMemcpy(c->T.g3, g3.data(), g3.size() * sizeof(uint2), hipMemcpyHostToDevice), err, err_len, "tables") &&
+         hip_ok(hipMemcpy(c->T.sel, sel.data(), sel.size() * sizeof(uint2), hipMemcpyHostToDevice), err, err_len, "tables") &&
+         hip_ok(hipMemcpy(c->T.rope_cos, rc.data(), rc.size() * sizeof(double), hipMemcpyHostToDevice), err, err_len, "tables") &&
+         hip_ok(hipMemcpy(c->T.rope_sin, rs.data(), rs.size() * sizeof(double), hipMemcpyHostToDevice), err, err_len, "tables");
+    ok = ok && hip_ok(hipMalloc(&c->st, sizeof(DevState)), err, err_len, "state") &&
+         hip_ok(hipMemset(c->st, 0, sizeof(DevState)), err, err_len, "state");
+    ok = ok && hip_ok(hipEventCreate(&c->e0), err, err_len, "event") && hip_ok(hipEventCreate(&c->e1), err, err_len, "event");
+    if (!ok) { qxg_close(c); return 0; }
+    *out = c;
+    return 1;
+}
+
+void qxg_close(qxg_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->s) (void)hipStreamSynchronize(c->s);
+    for (auto &kv : c->tens) free_tensor(kv.second);
+    void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->kc, c->vc, c->ks, c->vs, c->x,
+                    c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
+                    c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->st, c->staging};
+    for (void *p : bufs) if (p) (void)hipFree(p);
+    for (hipEvent_t e : c->kt.ev) (void)hipEventDestroy(e);
+    if (c->e0) (void)hipEventDestroy(c->e0);
+    if (c->e1) (void)hipEventDestroy(c->e1);
+    if (c->s) (void)hipStreamDestroy(c->s);
+    delete c;
+}
+
+int qxg_upload_tensor(qxg_ctx *c, const char *name, uint32_t type, const uint64_t dims[4], const void *host,
+                      uint64_t nbytes, char *err, uint64_t err_len) {
+    if (!c || !name || !dims || !host || !nbytes) { set_err(err, err_len, "invalid argument"); return 0; }
+    uint64_t bv = 0, bb = 0;
+    if (!block_geom(type, bv, bb)) { set_err(err, err_len, "unsupported ggml type"); return 0; }
+    uint64_t elems = 1;
+    for (int i = 0; i < 4; ++i) if (dims[i]) elems *= dims[i];
+    if (dims[0] % bv || elems / bv * bb != nbytes) { set_err(err, err_len, "tensor byte size inconsistent with dimensions"); return 0; }
+    (void)hipSetDevice(c->device);
+    auto it = c->tens.find(name);
+    if (it != c->tens.end()) { free_tensor(it->second); c->dev_bytes -= it->second.bytes; c->tens.erase(it); }
+    QTensor t;
+    t.type = type;
+    for (int i = 0; i < 4; ++i) t.dims[i] = dims[i];
+    if (!upload_planes(c, t, host, nbytes, err, err_len)) { free_tensor(t); return 0; }
+    c->tens[name] = t;
+    c->bound = false;
+    return 1;
+}
+
+int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_head, char *err, uint64_t err_len) {
+    if (!c) { set_err(err, err_len, "invalid context"); return 0; }
+    (void)hipSetDevice(c->device);
+    c->bound = false;
+    c->L.assign(layers, LayerW{});
+    c->experts = 0;
+    char msg[256];
+    auto bad = [&](const std::string &nm, const char *why) {
+        snprintf(msg, sizeof(msg), "%s: %s", nm.c_str(), why);
+        set_err(err, err_len, msg);
+        return 0;
+    };
+    for (uint32_t l = 0; l < layers; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        struct { const char *sfx; uint32_t type; uint64_t d0, d1; const QTensor **slot; } q[] = {
+            {"attn_q.weight", 23, 2048, 4096, &c->L[l].wq}, {"attn_k.weight", 23, 2048, 512, &c->L[l].wk},
+            {"attn_v.weight", 23, 2048, 512, &c->L[l].wv}, {"attn_output.weight", 23, 4096, 2048, &c->L[l].wo},
+            {"ffn_gate_exps.weight", 17, 2048, 768, &c->L[l].gate}, {"ffn_up_exps.weight", 17, 2048, 768, &c->L[l].up},
+            {"ffn_down_exps.weight", 18, 768, 2048, &c->L[l].down}};
+        for (auto &e : q) {
+            const QTensor *t = find(c, p + e.sfx);
+            if (!t) return bad(p + e.sfx, "not uploaded");
+            if (t->type != e.type || t->dims[0] != e.d0 || t->dims[1] != e.d1) return bad(p + e.sfx, "unsupported type or shape");
+            *e.slot = t;
+        }
+        const uint32_t E = (uint32_t)c->L[l].gate->dims[2];
+        if (E < 8 || E > 128 || c->L[l].up->dims[2] != E || c->L[l].down->dims[2] != E) return bad(p + "ffn_*_exps.weight", "expert count");
+        if (l == 0) c->experts = E;
+        else if (E != c->experts) return bad(p + "ffn_gate_exps.weight", "expert count differs between layers");
+        struct { const char *sfx; uint64_t d0, d1; const float **slot; } f[] = {
+            {"attn_norm.weight", 2048, 0, &c->L[l].attn_norm}, {"attn_q_norm.weight", 128, 0, &c->L[l].q_norm},
+            {"attn_k_norm.weight", 128, 0, &c->L[l].k_norm}, {"ffn_norm.weight", 2048, 0, &c->L[l].ffn_norm},
+            {"ffn_gate_inp.weight", 2048, E, &c->L[l].router}};
+        for (auto &e : f) {
+            const QTensor *t = find(c, p + e.sfx);
+            if (!t) return bad(p + e.sfx, "not uploaded");
+            if (t->type != 0 || t->dims[0] != e.d0 || t->dims[1] != e.d1) return bad(p + e.sfx, "must be F32 of the expected shape");
+            *e.slot = (const float *)t->p0;
+        }
+    }
+    c->layers = layers;
+    c->emb = nullptr; c->head = nullptr; c->out_norm = nullptr; c->vocab = 0;
+    if (need_embedding) {
+        const QTensor *t = find(c, "token_embd.weight");
+        if (!t) return bad("token_embd.weight", "not uploaded");
+        if (t->type != 12 || t->dims[0] != 2048) return bad("token_embd.weight", "must be Q4_K [2048, vocab]");
+        c->emb = t->p0;
+        c->vocab = (uint32_t)t->dims[1];
+        c->emb_row = t->bytes / t->dims[1];
+    }
+    if (need_head) {
+        const QTensor *t = find(c, "output.weight"), *nw = find(c, "output_norm.weight");
+        if (!t || !nw) return bad("output.weight", "output.weight and output_norm.weight must be uploaded");
+        if (t->type != 14 || t->dims[0] != 2048) return bad("output.weight", "final head requires Q6_K output.weight");
+        if (nw->type != 0 || nw->dims[0] != 2048) return bad("output_norm.weight", "must be F32 [2048]");
+        if (c->vocab && c->vocab != t->dims[1]) return bad("output.weight", "vocab differs from token_embd.weight");
+        c->head = t;
+        c->out_norm = (const float *)nw->p0;
+        c->vocab = (uint32_t)t->dims[1];
+    }
+    // work buffers (re)sized for this binding
+    void **bufs[] = {(void **)&c->x, (void **)&c->qkv, (void **)&c->ctxv, (void **)&c->h, (void **)&c->logits,
+                     (void **)&c->vcur, (void **)&c->attn, (void **)&c->moe, (void **)&c->norm,
+                     (void **)&c->layer_dump, (void **)&c->rlog, (void **)&c->cand_v, (void **)&c->top_v,
+                     (void **)&c->cand_i, (void **)&c->top_i, (void **)&c->tokens};
+    for (void **b : bufs) if (*b) { (void)hipFree(*b); *b = nullptr; }
+    const uint64_t V = c->vocab ? c->vocab : 1;
+    const uint64_t sizes[] = {2048 * 4, 5120 * 4, 4096 * 4, 8 * 768 * 4, V * 4, 512 * 4, 2048 * 4, 2048 * 4, 2048 * 4,
+                              (uint64_t)(layers ? layers : 1) * 2048 * 4, 128 * 8, TOPK_BLOCKS * QXG_MAX_TOPN * 4,
+                              QXG_MAX_TOPN * 4, TOPK_BLOCKS * QXG_MAX_TOPN * 4, QXG_MAX_TOPN * 4,
+                              (QXG_MAX_CTX + 2) * 4};
+    for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i)
+        if (!hip_ok(hipMalloc(bufs[i], sizes[i]), err, err_len, "work buffers")) return 0;
+    if (!hip_ok(hipMemset(c->tokens, 0, sizes[15]), err, err_len, "work buffers")) return 0;
+    c->bound = true;
+    return 1;
+}
+
+int qxg_kv_create(qxg_ctx *c, uint32_t layers, uint32_t ctx_tokens, uint32_t kv_format, char *err, uint64_t err_len) {
+    if (!c) { set_err(err, err_len, "invalid context"); return 0; }
+    if (kv_format != 1) { set_err(err, err_len, "only INT8 KV (kv_format 1) is supported"); return 0; }
+    if (!ctx_tokens || ctx_tokens > QXG_MAX_CTX) { set_err(err, err_len, "state loop context must be between 1 and 4096"); return 0; }
+    if (!layers) { set_err(err, err_len, "invalid layer count"); return 0; }
+    (void)hipSetDevice(c->device);
+    void *b[] = {c->kc, c->vc, c->ks, c->vs};
+    for (void *p : b) if (p) (void)hipFree(p);
+    c->kc = c->vc = nullptr; c->ks = c->vs = nullptr;
+    const uint64_t slots = (uint64_t)layers * ctx_tokens;
+    if (!hip_ok(hipMalloc(&c->kc, slots * 512), err, err_len, "kv") || !hip_ok(hipMalloc(&c->vc, slots * 512), err, err_len, "kv") ||
+        !hip_ok(hipMalloc(&c->ks, slots * 4), err, err_len, "kv") || !hip_ok(hipMalloc(&c->vs, slots * 4), err, err_len, "kv"))
+        return 0;
+    // calloc semantics, as the reference (src/qx_format.c:6151-6156)
+    if (!hip_ok(hipMemset(c->kc, 0, slots * 512), err, err_len, "kv") || !hip_ok(hipMemset(c->vc, 0, slots * 512), err, err_len, "kv") ||
+        !hip_ok(hipMemset(c->ks, 0, slots * 4), err, err_len, "kv") || !hip_ok(hipMemset(c->vs, 0, slots * 4), err, err_len, "kv"))
+        return 0;
+    c->kv_layers = layers;
+    c->kv_ctx = ctx_tokens;
+    return 1;
+}
+
+static int kv_copy(qxg_ctx *c, uint32_t layer, uint32_t pos0, uint32_t count, int8_t *k, int8_t *v, float *ksc,
+                   float *vsc, bool to_dev, char *err, uint64_t err_len) {
+    if (!c || !c->kc) { set_err(err, err_len, "KV cache not created"); return 0; }
+    if (layer >= c->kv_layers || pos0 > c->kv_ctx || count > c->kv_ctx - pos0) { set_err(err, err_len, "KV range outside cache"); return 0; }
+    (void)hipSetDevice(c->device);
+    const uint64_t slot = (uint64_t)layer * c->kv_ctx + pos0;
+    const hipMemcpyKind kind = to_dev ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+    struct { void *dev; void *host; uint64_t bytes; } m[] = {
+        {c->kc + slot * 512, k, (uint64_t)count * 512}, {c->vc + slot * 512, v, (uint64_t)count * 512},
+        {c->ks + slot, ksc, (uint64_t)count * 4}, {c->vs + slot, vsc, (uint64_t)count * 4}};
+    for (auto &e : m) {
+        if (!e.host || !e.bytes) continue;
+        hipError_t r = to_dev ? hipMemcpyAsync(e.dev, e.host, e.bytes, kind, c->s) : hipMemcpyAsync(e.host, e.dev, e.bytes, kind, c->s);
+        if (!hip_ok(r, err, err_len, "kv copy")) return 0;
+    }
+    return hip_ok(hipStreamSynchronize(c->s), err, err_len, "kv copy");
+}
+
+int qxg_kv_write(qxg_ctx *c, uint32_t layer, uint32_t pos0, uint32_t count, const int8_t *k, const int8_t *v,
+                 const float *ks, const float *vs, char *err, uint64_t err_len) {
+    return kv_copy(c, layer, pos0, count, (int8_t *)k, (int8_t *)v, (float *)ks, (float *)vs, true, err, err_len);
+}
+
+int qxg_kv_read(qxg_ctx *c, uint32_t layer, uint32_t pos0, uint32_t count, int8_t *k, int8_t *v, float *ks,
+                float *vs, char *err, uint64_t err_len) {
+    return kv_copy(c, layer, pos0, count, k, v, ks, vs, false, err, err_len);
+}
+
+int qxg_decode_token(qxg_ctx *c, uint32_t token, uint32_t position, int run_head, float *residual_out,
+                     float *layer_out, float *logits, uint32_t top_n, uint32_t *top_ids, double *top_logits,
+                     char *err, uint64_t err_len) {
+    if (!check_ready(c, true, err, err_len)) return 0;
+    if (!c->emb) { set_err(err, err_len, "token_embd.weight not bound"); return 0; }
+    if (run_head && !c->head) { set_err(err, err_len, "head not bound"); return 0; }
+    if (token >= c->vocab) { set_err(err, err_len, "token id out of range"); return 0; }
+    if (position >= c->kv_ctx || c->layers > c->kv_layers) { set_err(err, err_len, "position or layers outside KV cache"); return 0; }
+    if (top_n == 0) top_n = 1;
+    if (top_n > QXG_MAX_TOPN) top_n = QXG_MAX_TOPN;
+    (void)hipSetDevice(c->device);
+    (void)hipMemcpyAsync(c->tokens, &token, 4, hipMemcpyHostToDevice, c->s);
+    write_state(c, position, 0, run_head ? 1 : 2, 0);
+    hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
+    for (uint32_t l = 0; l < c->layers; ++l) {
+        launch_attention(c, l, c->x, nullptr, nullptr);
+        launch_moe(c, l, c->x, nullptr);
+        if (layer_out)
+            (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * 4, hipMemcpyDeviceToDevice, c->s);
+    }
+    if (run_head) launch_head(c, top_n, nullptr);
+    if (!finish(c, err, err_len)) return 0;
+    if (residual_out && !hip_ok(hipMemcpy(residual_out, c->x, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (layer_out && !hip_ok(hipMemcpy(layer_out, c->layer_dump, 2048ull * 4 * c->layers, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (!run_head) return 1;
+    DevState h;
+    if (!read_state(c, h, err, err_len)) return 0;
+    if (logits && !hip_ok(hipMemcpy(logits, c->logits, (uint64_t)c->vocab * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    float tv[QXG_MAX_TOPN];
+    uint32_t ti[QXG_MAX_TOPN];
+    if (!hip_ok(hipMemcpy(tv, c->top_v, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read") ||
+        !hip_ok(hipMemcpy(ti, c->top_i, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    for (uint32_t i = 0; i < top_n; ++i) {
+        if (top_ids) top_ids[i] = ti[i];
+        if (top_logits) top_logits[i] = (double)tv[i];
+    }
+    if (h.nonfinite) { write_state(c, 0, 0, 0, 0); set_err(err, err_len, "non-finite final logit"); return 0; }
+    return 1;
+}
+
+int qxg_generate(qxg_ctx *c, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_gen, uint32_t pos0,
+                 uint32_t *tokens_out, float *elapsed_ms, char *err, uint64_t err_len) {
+    if (!check_ready(c, true, err, err_len)) return 0;
+    if (!c->emb || !c->head) { set_err(err, err_len, "generation needs token_embd.weight and output.weight bound"); return 0; }
+    if (!prompt || !n_prompt || !n_gen) { set_err(err, err_len, "generation needs >= 1 prompt token and >= 1 generated token"); return 0; }
+    const uint64_t steps = (uint64_t)n_prompt + n_gen - 1;
+    if (pos0 + steps > c->kv_ctx || c->layers > c->kv_layers) { set_err(err, err_len, "prompt plus generation exceeds the KV context"); return 0; }
+    for (uint32_t i = 0; i < n_prompt; ++i)
+        if (prompt[i] >= c->vocab) { set_err(err, err_len, "prompt token out of range"); return 0; }
+    (void)hipSetDevice(c->device);
+    (void)hipMemcpyAsync(c->tokens, prompt, (uint64_t)n_prompt * 4, hipMemcpyHostToDevice, c->s);
+    write_state(c, pos0, 0, n_prompt, 0);
+    c->kt.used = 0;
+    (void)hipEventRecord(c->e0, c->s);
+    for (uint64_t s = 0; s < steps; ++s) {
+        launch_step(c, 1, false);
+        hipLaunchKernelGGL(qxk_advance, dim3(1), dim3(64), 0, c->s, c->st);
+    }
+    (void)hipEventRecord(c->e1, c->s);
+    if (!finish(c, err, err_len)) return 0;
+    if (elapsed_ms) (void)hipEventElapsedTime(elapsed_ms, c->e0, c->e1);
+    DevState h;
+    if (!read_state(c, h, err, err_len)) return 0;
+    if (tokens_out && !hip_ok(hipMemcpy(tokens_out, c->tokens + n_prompt, (uint64_t)n_gen * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (h.nonfinite) { write_state(c, 0, 0, 0, 0); set_err(err, err_len, "non-finite final logit"); return 0; }
+    return 1;
+}
+
+int qxg_dequant_blocks(qxg_ctx *c, uint32_t type, const void *raw, uint64_t nblocks, float *out, char *err, uint64_t err_len) {
+    if (!c || !raw || !out || !nblocks) { set_err(err, err_len, "invalid argument"); return 0; }
+    uint64_t bv = 0, bb = 0;
+    if (!block_geom(type, bv, bb) || type == 0) { set_err(err, err_len, "unsupported GGML type for decode-block"); return 0; }
+    (void)hipSetDevice(c->device);
+    QTensor t;
+    t.type = type;
+    t.dims[0] = 256 * nblocks;
+    const uint64_t before = c->dev_bytes;
+    if (!upload_planes(c, t, raw, nblocks * bb, err, err_len)) { free_tensor(t); c->dev_bytes = before; return 0; }
+    c->dev_bytes = before;
+    float *d = nullptr;
+    int ok = hip_ok(hipMalloc(&d, nblocks * 256 * 4), err, err_len, "hipMalloc");
+    if (ok) {
+        hipLaunchKernelGGL(qxk_dequant, dim3((unsigned)nblocks), dim3(256), 0, c->s, type, t.p0, t.p1, t.p2, t.d, c->T,
+                           nblocks, d);
+        ok = finish(c, err, err_len) && hip_ok(hipMemcpy(out, d, nblocks * 256 * 4, hipMemcpyDeviceToHost), err, err_len, "read");
+    }
+    if (d) (void)hipFree(d);
+    free_tensor(t);
+    return ok;
+}
+
+int qxg_embed_token(qxg_ctx *c, uint32_t token, float *x_out, char *err, uint64_t err_len) {
+    if (!check_ready(c, false, err, err_len)) return 0;
+    if (!c->emb) { set_err(err, err_len, "token_embd.weight not bound"); return 0; }
+    if (token >= c->vocab || !x_out) { set_err(err, err_len, "token id out of range"); return 0; }
+    (void)hipSetDevice(c->device);
+    (void)hipMemcpyAsync(c->tokens, &token, 4, hipMemcpyHostToDevice, c->s);
+    write_state(c, 0, 0, 1, 1);
+    hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
+    if (!finish(c, err, err_len)) return 0;
+    return hip_ok(hipMemcpy(x_out, c->x, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read");
+}
+
+int qxg_attention_layer(qxg_ctx *c, uint32_t layer, uint32_t position, const float *x_in, float *attn_out,
+                        float *kqv_out, float *vcur_out, char *err, uint64_t err_len) {
+    if (!check_ready(c, true, err, err_len)) return 0;
+    if (!x_in || layer >= c->layers || layer >= c->kv_layers || position >= c->kv_ctx) { set_err(err, err_len, "invalid attention layer argument"); return 0; }
+    (void)hipSetDevice(c->device);
+    (void)hipMemcpyAsync(c->x, x_in, 2048 * 4, hipMemcpyHostToDevice, c->s);
+    write_state(c, position, 0, 1, 1);
+    launch_attention(c, layer, c->x, c->attn, c->vcur);
+    if (!finish(c, err, err_len)) return 0;
+    if (attn_out && !hip_ok(hipMemcpy(attn_out, c->attn, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (kqv_out && !hip_ok(hipMemcpy(kqv_out, c->ctxv, 4096 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (vcur_out && !hip_ok(hipMemcpy(vcur_out, c->vcur, 512 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    return 1;
+}
+
+int qxg_moe_layer(qxg_ctx *c, uint32_t layer, const float *ffn_inp, float *layer_out, float *moe_out, uint32_t ids[8],
+                  double weights[8], char *err, uint64_t err_len) {
+    if (!check_ready(c, false, err, err_len)) return 0;
+    if (!ffn_inp || layer >= c->layers) { set_err(err, err_len, "invalid MoE layer argument"); return 0; }
+    (void)hipSetDevice(c->device);
+    (void)hipMemcpyAsync(c->x, ffn_inp, 2048 * 4, hipMemcpyHostToDevice, c->s);
+    write_state(c, 0, 0, 1, 1);
+    launch_moe(c, layer, c->x, c->moe);
+    if (!finish(c, err, err_len)) return 0;
+    DevState h;
+    if (!read_state(c, h, err, err_len)) return 0;
+    if (layer_out && !hip_ok(hipMemcpy(layer_out, c->x, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (moe_out && !hip_ok(hipMemcpy(moe_out, c->moe, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    for (int r = 0; r < 8; ++r) {
+        if (ids) ids[r] = h.moe_ids[r];
+        if (weights) weights[r] = h.moe_w[r];
+    }
+    return 1;
+}
+
+int qxg_final_head(qxg_ctx *c, const float *residual, float *norm_out, float *logits, uint32_t top_n,
+                   uint32_t *top_ids, double *top_logits, char *err, uint64_t err_len) {
+    if (!check_ready(c, false, err, err_len)) return 0;
+    if (!c->head) { set_err(err, err_len, "final head requires Q6_K output.weight"); return 0; }
+    if (!residual) { set_err(err, err_len, "invalid final head argument"); return 0; }
+    if (top_n == 0) top_n = 1;
+    if (top_n > QXG_MAX_TOPN) top_n = QXG_MAX_TOPN;
+    (void)hipSetDevice(c->device);
+    (void)hipMemcpyAsync(c->x, residual, 2048 * 4, hipMemcpyHostToDevice, c->s);
+    write_state(c, 0, 0, 1, 1);
+    launch_head(c, top_n, c->norm);
+    if (!finish(c, err, err_len)) return 0;
+    DevState h;
+    if (!read_state(c, h, err, err_len)) return 0;
+    if (norm_out && !hip_ok(hipMemcpy(norm_out, c->norm, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (logits && !hip_ok(hipMemcpy(logits, c->logits, (uint64_t)c->vocab * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    float tv[QXG_MAX_TOPN];
+    uint32_t ti[QXG_MAX_TOPN];
+    if (!hip_ok(hipMemcpy(tv, c->top_v, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read") ||
+        !hip_ok(hipMemcpy(ti, c->top_i, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    for (uint32_t i = 0; i < top_n; ++i) {
+        if (top_ids) top_ids[i] = ti[i];
+        if (top_logits) top_logits[i] = (double)tv[i];
+    }
+    if (h.nonfinite) { write_state(c, 0, 0, 0, 0); set_err(err, err_len, "non-finite final logit"); return 0; }
+    return 1;
+}
+
+int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float *avg_ms, char *err, uint64_t err_len) {
+    if (!check_ready(c, which == 5 || which == 2, err, err_len)) return 0;
+    if (which < 0 || which > 6 || !iters || layer >= c->layers) { set_err(err, err_len, "invalid timing argument"); return 0; }
+    if (which == 4 && !c->head) { set_err(err, err_len, "head not bound"); return 0; }
+    (void)hipSetDevice(c->device);
+    // rotate over layers so repeated launches stream distinct weights (> the 256 MB MALL)
+    (void)hipEventRecord(c->e0, c->s);
+    for (uint32_t i = 0; i < iters; ++i) {
+        const uint32_t l = (layer + i) % c->layers;
+        const LayerW &w = c->L[l];
+        switch (which) {
+        case 0: qxl_gate_up(c->s, c->x, w.ffn_norm, w.gate, w.up, c->T, c->st, c->h); break;
+        case 1: qxl_down(c->s, c->h, w.down, c->T, c->st, c->attn, nullptr); break;
+        case 2: qxl_qkv(c->s, c->x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv); break;
+        case 3: qxl_oproj(c->s, c->ctxv, w.wo, c->attn, nullptr); break;
+        case 4: qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, nullptr); break;
+        case 5:
+            hipLaunchKernelGGL(qxk_attn, dim3(32), dim3(512), (size_t)c->kv_ctx * sizeof(double), c->s, c->qkv, c->kc,
+                               c->vc, c->ks, c->vs, l % c->kv_layers, c->kv_ctx, std::sqrt(128.0), c->st, c->ctxv);
+            break;
+        case 6:
+            hipLaunchKernelGGL(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, c->x, w.ffn_norm, w.router,
+                               c->experts, c->rlog, c->st);
+            break;
+        }
+    }
+    (void)hipEventRecord(c->e1, c->s);
+    if (!finish(c, err, err_len)) return 0;
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, c->e0, c->e1);
+    if (avg_ms) *avg_ms = ms / (float)iters;
+    return 1;
+}
+
+uint64_t qxg_device_bytes(const qxg_ctx *c) { return c ? c->dev_bytes : 0; }
+
+/* In-situ timing of one kernel kind inside qxg_generate / qxg_decode_token:
+ * an event pair is recorded around every launch of kernel `which` (numbering of
+ * qxg_time_kernel; -1 disables). */
+int qxg_profile_kernel(qxg_ctx *c, int which) {
+    if (!c) return 0;
+    c->kt.which = which;
+    c->kt.used = 0;
+    return 1;
+}
+
+int qxg_profile_result(qxg_ctx *c, uint32_t *launches, double *total_ms) {
+    if (!c) return 0;
+    double tot = 0.0;
+    for (uint32_t i = 0; i < c->kt.used; ++i) {
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, c->kt.ev[2 * i], c->kt.ev[2 * i + 1]);
+        tot += ms;
+    }
+    if (launches) *launches = c->kt.used;
+    if (total_ms) *total_ms = tot;
+    return 1;
+}
+
+}  // extern "C"

@@ -1,0 +1,60 @@
+// Internal declarations shared by the device kernels and the C-ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QXG_HIDDEN 2048
+#define QXG_QDIM 4096
+#define QXG_KVDIM 512
+#define QXG_HEADS 32
+#define QXG_KVHEADS 4
+#define QXG_HEAD_DIM 128
+#define QXG_FFN 768
+#define QXG_TOPK 8
+#define QXG_MAX_CTX 4096
+#define QXG_MAX_TOPN 32
+
+// Repacked quantized tensor: every field of the original block in its own array,
+// so each lane's load is aligned.  Bytes per block are unchanged.
+//   IQ4_XS : qs[nb][128], meta[nb][8] = {d, scales_h, scales_l[4]}
+//   IQ2_XS : qs[nb][64] (32 x u16), sc[nb][8], d[nb]
+//   IQ3_XXS: qs[nb][64], aux[nb][32] (8 x u32), d[nb]
+//   Q6_K   : ql[nb][128], qh[nb][64], sc[nb][16] (int8), d[nb]
+//   Q4_K, F32: the original bytes
+struct QTensor {
+    uint32_t type = 0;
+    uint64_t dims[4] = {0, 0, 0, 0};
+    uint64_t nblocks = 0, bytes = 0;
+    uint8_t *base = nullptr;      // device allocation
+    const uint8_t *p0 = nullptr;  // qs / ql / raw
+    const uint8_t *p1 = nullptr;  // meta / sc / aux / qh
+    const uint8_t *p2 = nullptr;  // Q6_K sc
+    const uint16_t *d = nullptr;  // fp16 d per block
+};
+
+struct LayerW {
+    const float *attn_norm, *q_norm, *k_norm, *ffn_norm, *router;
+    const QTensor *wq, *wk, *wv, *wo, *gate, *up, *down;
+};
+
+// Device-resident step state: kernels read the position from here so one
+// recorded step can be replayed for every token.
+struct DevState {
+    uint32_t pos0;          // position of local step 0
+    uint32_t step;          // local step
+    uint32_t n_prompt;      // steps < n_prompt-1 are prompt steps (no head)
+    uint32_t nonfinite;     // set by the head on a non-finite logit
+    uint32_t ctr_router;    // last-block tickets (reset by the last block)
+    uint32_t ctr_topk;
+    uint32_t force_head;    // run the head on every step
+    uint32_t pad;
+    uint32_t moe_ids[QXG_TOPK];
+    double moe_w[QXG_TOPK];
+};
+
+struct Tables {
+    uint4 *g2;     // IQ2_XS grid: 512 x {pos lo, pos hi, neg lo, neg hi}
+    uint2 *g3;     // IQ3_XXS grid: 256 x {pos, neg}
+    uint2 *sel;    // sign index (7 bits) -> v_perm selectors for 8 values
+    double *rope_cos, *rope_sin;  // [QXG_MAX_CTX][64]
+};

@@ -1,7 +1,9 @@
 /* QXF1 reader: validation rules of the reference loader (src/qx_format.c:438-460,
  * 652-841 of the reference), mmap-only (the GPU build uploads every tensor once,
  * so the buffered per-call read path has no use here). */
+#ifndef _GNU_SOURCE
 #define _GNU_SOURCE
+#endif
 #include "qx_host.h"
 
 #include <errno.h>

@@ -12,7 +12,9 @@
  *   IQ3_XXS down      : d = fp16(U[1e-4,3e-4]); qs bytes and aux32 words uniform
  *   F32 norms         : U(0.5,1.5);  router ffn_gate_inp: N(0, 0.02)
  * The fp16 ranges keep every projection output O(1) over 48 layers. */
+#ifndef _GNU_SOURCE
 #define _GNU_SOURCE
+#endif
 #include "qx_host.h"
 
 #include <errno.h>

@@ -1,0 +1,222 @@
+"""ctypes binding of the C ABI in include/qxg.h and include/qx_host.h.
+
+Loads lib/libqxg.so and lib/libqxhost.so built in-tree by the Makefile next to
+this file; raises if they are missing (there is no fallback path)."""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+
+
+def _load(name):
+    path = os.path.join(LIB_DIR, name)
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run `make -C {HERE}` (or __graft_entry__.build())")
+    return ctypes.CDLL(path)
+
+
+_g = _load("libqxg.so")
+_h = _load("libqxhost.so")
+
+u32, u64, c_int, c_float, c_double, vp, cp = (ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_float,
+                                               ctypes.c_double, ctypes.c_void_p, ctypes.c_char_p)
+ERR = (cp, u64)
+
+
+def _sig(lib, name, args, res=c_int):
+    f = getattr(lib, name)
+    f.argtypes = list(args)
+    f.restype = res
+    return f
+
+
+class GenSpec(ctypes.Structure):
+    _fields_ = [("layers", u32), ("vocab", u32), ("experts", u32), ("with_embedding", u32), ("with_head", u32),
+                ("seed", u64), ("threads", u32)]
+
+
+class ModelInfo(ctypes.Structure):
+    _fields_ = [("layers", u32), ("vocab", u32), ("experts", u32), ("has_embedding", c_int), ("has_head", c_int),
+                ("tensor_bytes", u64), ("tensors", u32)]
+
+
+_sig(_g, "qxg_open", [c_int, ctypes.POINTER(vp), *ERR])
+_sig(_g, "qxg_close", [vp], None)
+_sig(_g, "qxg_upload_tensor", [vp, cp, u32, ctypes.POINTER(u64), vp, u64, *ERR])
+_sig(_g, "qxg_bind_model", [vp, u32, c_int, c_int, *ERR])
+_sig(_g, "qxg_kv_create", [vp, u32, u32, u32, *ERR])
+_sig(_g, "qxg_kv_write", [vp, u32, u32, u32, vp, vp, vp, vp, *ERR])
+_sig(_g, "qxg_kv_read", [vp, u32, u32, u32, vp, vp, vp, vp, *ERR])
+_sig(_g, "qxg_decode_token", [vp, u32, u32, c_int, vp, vp, vp, u32, vp, vp, *ERR])
+_sig(_g, "qxg_generate", [vp, vp, u32, u32, u32, vp, ctypes.POINTER(c_float), *ERR])
+_sig(_g, "qxg_embed_token", [vp, u32, vp, *ERR])
+_sig(_g, "qxg_dequant_blocks", [vp, u32, vp, u64, vp, *ERR])
+_sig(_g, "qxg_attention_layer", [vp, u32, u32, vp, vp, vp, vp, *ERR])
+_sig(_g, "qxg_moe_layer", [vp, u32, vp, vp, vp, vp, vp, *ERR])
+_sig(_g, "qxg_final_head", [vp, vp, vp, vp, u32, vp, vp, *ERR])
+_sig(_g, "qxg_time_kernel", [vp, c_int, u32, u32, ctypes.POINTER(c_float), *ERR])
+_sig(_g, "qxg_device_bytes", [vp], u64)
+_sig(_g, "qxg_profile_kernel", [vp, c_int])
+_sig(_g, "qxg_profile_result", [vp, ctypes.POINTER(u32), ctypes.POINTER(c_double)])
+_sig(_h, "qxgen_write", [cp, ctypes.POINTER(GenSpec), ctypes.POINTER(u64), *ERR])
+_sig(_h, "qxgen_memfd", [ctypes.POINTER(GenSpec), cp, u64, ctypes.POINTER(c_int), *ERR])
+_sig(_h, "qxgen_memfd_close", [c_int], None)
+_sig(_h, "qx_gpu_load", [vp, cp, c_int, ctypes.POINTER(ModelInfo), *ERR])
+_sig(_h, "qxf_fnv1a64", [vp, u64], u64)
+
+
+class QxgError(RuntimeError):
+    pass
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(vp)
+
+
+def fnv1a64(a):
+    a = np.ascontiguousarray(a)
+    return int(_h.qxf_fnv1a64(_p(a), a.nbytes))
+
+
+def generate_model(path, layers=1, vocab=4096, experts=128, embedding=True, head=True, seed=1, threads=0):
+    """Writes the seeded random-init QXF1 model; returns its size in bytes."""
+    sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads)
+    err = ctypes.create_string_buffer(512)
+    size = u64()
+    if not _h.qxgen_write(str(path).encode(), ctypes.byref(sp), ctypes.byref(size), err, 512):
+        raise QxgError(err.value.decode())
+    return size.value
+
+
+class MemModel:
+    """Seeded QXF1 model in an anonymous in-memory file (path /proc/self/fd/N)."""
+
+    def __init__(self, layers=48, vocab=151936, experts=128, embedding=True, head=True, seed=1, threads=0):
+        sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads)
+        err = ctypes.create_string_buffer(512)
+        path = ctypes.create_string_buffer(128)
+        fd = c_int()
+        if not _h.qxgen_memfd(ctypes.byref(sp), path, 128, ctypes.byref(fd), err, 512):
+            raise QxgError(err.value.decode())
+        self.path = path.value.decode()
+        self.fd = fd.value
+
+    def close(self):
+        if self.fd >= 0:
+            _h.qxgen_memfd_close(self.fd)
+            self.fd = -1
+
+
+class Context:
+    """One qxg_ctx (one HIP stream) on `device`."""
+
+    def __init__(self, device=0):
+        self._c = vp()
+        self._err = ctypes.create_string_buffer(1024)
+        self._check(_g.qxg_open(device, ctypes.byref(self._c), self._err, 1024))
+        self.info = None
+
+    def _check(self, ok):
+        if not ok:
+            raise QxgError(self._err.value.decode())
+
+    def close(self):
+        if self._c:
+            _g.qxg_close(self._c)
+            self._c = vp()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def load(self, path, verify=True):
+        info = ModelInfo()
+        self._check(_h.qx_gpu_load(self._c, str(path).encode(), int(verify), ctypes.byref(info), self._err, 1024))
+        self.info = info
+        return info
+
+    def kv_create(self, layers, ctx_tokens):
+        self._check(_g.qxg_kv_create(self._c, layers, ctx_tokens, 1, self._err, 1024))
+
+    def kv_write(self, layer, pos0, k, v, ks, vs):
+        k, v = np.ascontiguousarray(k, np.int8), np.ascontiguousarray(v, np.int8)
+        ks, vs = np.ascontiguousarray(ks, np.float32), np.ascontiguousarray(vs, np.float32)
+        self._check(_g.qxg_kv_write(self._c, layer, pos0, len(ks), _p(k), _p(v), _p(ks), _p(vs), self._err, 1024))
+
+    def kv_read(self, layer, pos0, count):
+        k = np.zeros((count, 512), np.int8); v = np.zeros((count, 512), np.int8)
+        ks = np.zeros(count, np.float32); vs = np.zeros(count, np.float32)
+        self._check(_g.qxg_kv_read(self._c, layer, pos0, count, _p(k), _p(v), _p(ks), _p(vs), self._err, 1024))
+        return k, v, ks, vs
+
+    def dequant(self, ggml_type, raw, nblocks):
+        raw = np.ascontiguousarray(raw, np.uint8)
+        out = np.zeros(nblocks * 256, np.float32)
+        self._check(_g.qxg_dequant_blocks(self._c, ggml_type, _p(raw), nblocks, _p(out), self._err, 1024))
+        return out
+
+    def embed(self, token):
+        x = np.zeros(2048, np.float32)
+        self._check(_g.qxg_embed_token(self._c, token, _p(x), self._err, 1024))
+        return x
+
+    def attention_layer(self, layer, pos, x):
+        x = np.ascontiguousarray(x, np.float32)
+        a = np.zeros(2048, np.float32); kqv = np.zeros(4096, np.float32); vcur = np.zeros(512, np.float32)
+        self._check(_g.qxg_attention_layer(self._c, layer, pos, _p(x), _p(a), _p(kqv), _p(vcur), self._err, 1024))
+        return a, kqv, vcur
+
+    def moe_layer(self, layer, x):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(2048, np.float32); moe = np.zeros(2048, np.float32)
+        ids = np.zeros(8, np.uint32); w = np.zeros(8, np.float64)
+        self._check(_g.qxg_moe_layer(self._c, layer, _p(x), _p(y), _p(moe), _p(ids), _p(w), self._err, 1024))
+        return y, moe, ids, w
+
+    def final_head(self, residual, top_n=8):
+        r = np.ascontiguousarray(residual, np.float32)
+        nrm = np.zeros(2048, np.float32); lg = np.zeros(self.info.vocab, np.float32)
+        ids = np.zeros(top_n, np.uint32); tl = np.zeros(top_n, np.float64)
+        self._check(_g.qxg_final_head(self._c, _p(r), _p(nrm), _p(lg), top_n, _p(ids), _p(tl), self._err, 1024))
+        return nrm, lg, ids, tl
+
+    def decode_token(self, token, pos, run_head=True, top_n=8, want_layers=False, want_logits=False):
+        res = np.zeros(2048, np.float32)
+        lay = np.zeros((self.info.layers, 2048), np.float32) if want_layers else None
+        lg = np.zeros(self.info.vocab, np.float32) if want_logits else None
+        ids = np.zeros(top_n, np.uint32); tl = np.zeros(top_n, np.float64)
+        self._check(_g.qxg_decode_token(self._c, token, pos, int(run_head), _p(res), _p(lay), _p(lg), top_n, _p(ids),
+                                        _p(tl), self._err, 1024))
+        return res, lay, lg, ids, tl
+
+    def generate(self, prompt, n_gen, pos0=0):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(n_gen, np.uint32)
+        ms = c_float()
+        self._check(_g.qxg_generate(self._c, _p(prompt), len(prompt), n_gen, pos0, _p(out), ctypes.byref(ms),
+                                    self._err, 1024))
+        return out, ms.value
+
+    def time_kernel(self, which, layer=0, iters=20):
+        ms = c_float()
+        self._check(_g.qxg_time_kernel(self._c, which, layer, iters, ctypes.byref(ms), self._err, 1024))
+        return ms.value
+
+    def profile_kernel(self, which):
+        _g.qxg_profile_kernel(self._c, which)
+
+    def profile_result(self):
+        n = u32(); ms = c_double()
+        _g.qxg_profile_result(self._c, ctypes.byref(n), ctypes.byref(ms))
+        return n.value, ms.value
+
+    def device_bytes(self):
+        return int(_g.qxg_device_bytes(self._c))
+
+
+KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "oproj": 3, "head": 4, "attention": 5, "router": 6}

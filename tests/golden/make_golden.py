@@ -1,0 +1,102 @@
+"""Writes tests/golden/golden.json from the reference CLI compiled in this container
+(oracle/_ref/qxqxf, built by `make -C oracle ref` from /root/reference sources).
+
+Inputs are QXF1 models written by this build's seeded generator
+(qx-mini-c_amd/host/qxgen.c), so a test can regenerate identical bytes anywhere.
+Only numeric summaries are stored: FNV-1a-64 of the reference's f32 outputs,
+argmax/top tokens and a few sampled values.  Re-run here after changing the
+generator:  python3 tests/golden/make_golden.py
+"""
+import json
+import os
+import re
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, os.path.join(ROOT, "qx-mini-c_amd"))
+import qxg  # noqa: E402
+
+REF = os.path.join(ROOT, "oracle", "_ref", "qxqxf")
+
+# model specs used by the golden checks (layers, vocab, experts, seed)
+MODELS = {
+    "A": dict(layers=1, vocab=1024, experts=16, seed=1234),
+    "B": dict(layers=2, vocab=2048, experts=128, seed=77),
+}
+DECODE_BLOCKS = [("token_embd.weight", [0, 1, 4095]), ("output.weight", [0, 7, 8191]),
+                 ("blk.0.attn_q.weight", [0, 3, 32767]), ("blk.0.attn_output.weight", [5]),
+                 ("blk.0.ffn_gate_exps.weight", [0, 1, 98303]), ("blk.0.ffn_up_exps.weight", [12345]),
+                 ("blk.0.ffn_down_exps.weight", [0, 2, 98303])]
+PHASES = ["input", "v-cur", "kqv-out", "ffn-inp", "ffn-moe-out", "output"]
+
+
+def run(args):
+    r = subprocess.run([REF] + args, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{args[0]} failed: {r.stderr}")
+    return r.stdout
+
+
+def fnv_file(path):
+    return qxg.fnv1a64(np.fromfile(path, np.uint8))
+
+
+def main():
+    if not os.path.exists(REF):
+        sys.exit(f"{REF} missing: run make -C oracle ref (needs /root/reference)")
+    out = {"models": MODELS, "decode_block": {}, "final_head": {}, "state_loop": {}}
+    with tempfile.TemporaryDirectory() as d:
+        paths = {}
+        for k, spec in MODELS.items():
+            paths[k] = os.path.join(d, f"{k}.qxf")
+            qxg.generate_model(paths[k], **spec)
+        # block decoders (reference decode-block, src/qx_format.c:2219-2264)
+        for name, blocks in DECODE_BLOCKS:
+            for b in blocks:
+                j = json.loads(run(["decode-block", "--in", paths["A"], "--name", name, "--block", str(b)]))
+                out["decode_block"][f"{name}#{b}"] = {"f32_checksum": str(j["f32_checksum"]),
+                                                       "first8": j["first8"]}
+        # final head probe (src/qx_format.c:5369-5411) on seeded residuals
+        for k in ("A", "B"):
+            for seed in (1, 2):
+                x = np.random.default_rng(seed).standard_normal(2048).astype(np.float32)
+                rp = os.path.join(d, f"r{k}{seed}.f32")
+                x.tofile(rp)
+                od = os.path.join(d, f"h{k}{seed}")
+                os.mkdir(od)
+                j = json.loads(run(["final-head-probe", "--in", paths[k], "--residual", rp, "--out-dir", od]))
+                lg = np.fromfile(os.path.join(od, "logits.f32"), np.float32)
+                order = np.lexsort((np.arange(len(lg)), -lg.astype(np.float64)))[:8]
+                out["final_head"][f"{k}/seed{seed}"] = {
+                    "normalized_checksum": str(j["normalized_checksum"]), "logits_checksum": str(j["logits_checksum"]),
+                    "argmax_token": j["argmax_token"], "argmax_logit": j["argmax_logit"],
+                    "top8_by_float": [int(i) for i in order], "logits_sample": [float(v) for v in lg[:4]]}
+        # full-MoE state loop with INT8 KV and per-layer dumps (src/qx_format.c:5970-6719)
+        for k, steps in (("A", 5), ("B", 4)):
+            dd = os.path.join(d, f"s{k}")
+            os.mkdir(dd)
+            layers = MODELS[k]["layers"]
+            txt = run(["state-loop-probe", "--in", paths[k], "--prompt-token", "17", "--steps", str(steps),
+                       "--layers", str(layers), "--ctx", "8", "--kv", "int8", "--full-moe", "--dump-residuals", dd])
+            toks = [int(t) for t in re.findall(r'"input_token": (\d+)', txt)]
+            experts = [[int(e) for e in re.findall(r"\d+", m)]
+                       for m in re.findall(r'"selected_experts": \[([0-9, ]*)\]', txt)]
+            dumps = {}
+            for s in range(steps):
+                for layer in range(layers):
+                    for ph in PHASES:
+                        dumps[f"{s}/{layer}/{ph}"] = str(fnv_file(os.path.join(dd, f"step-{s}-layer-{layer}-{ph}.f32")))
+            out["state_loop"][k] = {"input_tokens": toks, "steps": steps, "ctx": 8, "dumps": dumps,
+                                    "selected_experts": experts}
+    dst = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden.json")
+    with open(dst, "w") as f:
+        json.dump(out, f, indent=1, sort_keys=True)
+    print(f"wrote {dst}")
+
+
+if __name__ == "__main__":
+    main()

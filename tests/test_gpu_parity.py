@@ -1,0 +1,135 @@
+"""HIP path vs the oracle on identical seeded inputs (configs 1-3 of the hot path,
+plus a small full-token decode).  Runs through the C ABI (include/qxg.h)."""
+import numpy as np
+import pytest
+
+import qxo
+import qxg
+from helpers import REL_L2, rel_l2, seeded_kv, seeded_normal, topk_consistent
+
+pytestmark = pytest.mark.gpu
+
+BLOCK_BYTES = {12: 144, 14: 210, 17: 74, 18: 98, 23: 136}
+D_OFFSET = {12: 0, 14: 208, 17: 0, 18: 0, 23: 0}
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = qxg.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("ggml_type", [12, 14, 17, 18, 23])
+def test_dequant_bit_exact(ctx, ggml_type):
+    """Random blocks plus every fp16 value of d (including exponent 31 -> 65504)."""
+    bb = BLOCK_BYTES[ggml_type]
+    rng = np.random.default_rng(100 + ggml_type)
+    rand = rng.integers(0, 256, size=(2048, bb), dtype=np.uint8)
+    sweep = np.repeat(rng.integers(0, 256, size=(1, bb), dtype=np.uint8), 65536, axis=0)
+    d = np.arange(65536, dtype=np.uint16)
+    off = D_OFFSET[ggml_type]
+    sweep[:, off] = (d & 255).astype(np.uint8)
+    sweep[:, off + 1] = (d >> 8).astype(np.uint8)
+    blocks = np.concatenate([rand, sweep])
+    gpu = ctx.dequant(ggml_type, blocks, len(blocks)).reshape(-1, 256)
+    ref = np.stack([qxo.decode_block(ggml_type, b) for b in blocks])
+    assert gpu.view(np.uint32).tobytes() == ref.view(np.uint32).tobytes()
+
+
+@pytest.fixture(scope="module")
+def head_model(tmp_path_factory):
+    p = tmp_path_factory.mktemp("head") / "head.qxf"
+    qxg.generate_model(p, layers=0, vocab=151936, embedding=False, head=True, seed=11)
+    return p
+
+
+def test_final_head_config1(ctx, head_model):
+    """Config 1: Q6_K head 2048 -> 151936 on x ~ N(0,1)."""
+    ctx.load(head_model)
+    x = seeded_normal(1)
+    nrm, lg, ids, tl = ctx.final_head(x, top_n=8)
+    om = qxo.Model(head_model)
+    onrm, olg, oids, otl = om.final_head(x, 151936, top_n=8)
+    om.close()
+    assert rel_l2(nrm, onrm) <= 1e-7
+    assert rel_l2(lg, olg) <= REL_L2, rel_l2(lg, olg)
+    ok, why = topk_consistent(ids, oids, olg)
+    assert ok, why
+
+
+@pytest.fixture(scope="module")
+def layer_model(tmp_path_factory):
+    p = tmp_path_factory.mktemp("layer") / "layer.qxf"
+    qxg.generate_model(p, layers=1, vocab=1024, experts=128, embedding=True, head=True, seed=22)
+    return p
+
+
+def test_moe_block_config2(ctx, layer_model):
+    """Config 2: one MoE FFN block (128 experts, top-8) on x ~ N(0,1)."""
+    ctx.load(layer_model)
+    om = qxo.Model(layer_model)
+    for seed in (2, 3, 4):
+        x = seeded_normal(seed)
+        y, moe, ids, w = ctx.moe_layer(0, x)
+        oy, omoe, oids, ow = om.moe_layer(0, x)
+        assert list(ids) == list(oids)
+        assert np.allclose(w, ow, rtol=1e-9, atol=0)
+        assert rel_l2(moe, omoe) <= REL_L2, rel_l2(moe, omoe)
+        assert rel_l2(y, oy) <= REL_L2
+    om.close()
+
+
+@pytest.mark.parametrize("pos", [0, 5, 2047])
+def test_attention_block_config3(ctx, layer_model, pos):
+    """Config 3: attention at `pos` with positions 0..pos-1 prefilled by seeded INT8 rows."""
+    ctx.load(layer_model)
+    ctx.kv_create(1, 2048)
+    okv = qxo.KV(1, 2048)
+    if pos:
+        k, v, ks, vs = seeded_kv(33, pos)
+        ctx.kv_write(0, 0, k, v, ks, vs)
+        okv.k[0, :pos], okv.v[0, :pos], okv.ks[0, :pos], okv.vs[0, :pos] = k, v, ks, vs
+    x = seeded_normal(7)
+    a, kqv, vcur = ctx.attention_layer(0, pos, x)
+    om = qxo.Model(layer_model)
+    oa, okqv, ovcur = qxo.attention_layer(om, 0, pos, okv, x)
+    om.close()
+    assert rel_l2(vcur, ovcur) <= REL_L2
+    assert rel_l2(kqv, okqv) <= REL_L2, rel_l2(kqv, okqv)
+    assert rel_l2(a, oa) <= REL_L2, rel_l2(a, oa)
+    gk, gv, gks, gvs = ctx.kv_read(0, pos, 1)
+    assert np.abs(gk[0].astype(int) - okv.k[0, pos].astype(int)).max() <= 1
+    assert np.abs(gv[0].astype(int) - okv.v[0, pos].astype(int)).max() <= 1
+    assert abs(gks[0] / okv.ks[0, pos] - 1) < 1e-5 and abs(gvs[0] / okv.vs[0, pos] - 1) < 1e-5
+
+
+def test_decode_two_layers_greedy(ctx, tmp_path):
+    """Embedding + 2 layers + head, 5 greedy steps; per-step residual and tokens."""
+    p = tmp_path / "two.qxf"
+    qxg.generate_model(p, layers=2, vocab=4096, experts=32, seed=44)
+    ctx.load(p)
+    ctx.kv_create(2, 16)
+    om = qxo.Model(p)
+    okv = qxo.KV(2, 16)
+    tok_g = tok_o = 17
+    for s in range(5):
+        res, lay, lg, ids, tl = ctx.decode_token(tok_g, s, True, 4, want_layers=True, want_logits=True)
+        ores, olay, olg, oids, otl = qxo.decode_token(om, tok_o, s, okv, 2, True, 4096, 4)
+        assert rel_l2(lay, olay) <= 1e-4, (s, rel_l2(lay, olay))
+        assert rel_l2(lg, olg) <= 1e-4
+        ok, why = topk_consistent(ids, oids, olg)
+        assert ok, why
+        tok_g, tok_o = int(ids[0]), int(oids[0])
+    om.close()
+    # device-resident greedy loop gives the same tokens as the step-by-step path
+    ctx.kv_create(2, 16)
+    gen, ms = ctx.generate([17], 5)
+    ctx.kv_create(2, 16)
+    toks = []
+    t = 17
+    for s in range(5):
+        _, _, _, ids, _ = ctx.decode_token(t, s, True, 1)
+        t = int(ids[0])
+        toks.append(t)
+    assert list(gen) == toks
