@@ -13,10 +13,8 @@
 
 extern "C" {
 __global__ void qxk_embed(const uint8_t *, uint64_t, const uint32_t *, const DevState *, float *);
-__global__ void qxk_qk_rope_kv(float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
-                               uint32_t, uint32_t, const DevState *, float *);
-__global__ void qxk_attn(const float *, const int8_t *, const int8_t *, const float *, const float *, uint32_t,
-                         uint32_t, double, const DevState *, float *);
+__global__ void qxk_attn(const float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
+                         uint32_t, uint32_t, double, const DevState *, float *, float *);
 __global__ void qxk_router(const float *, const float *, const float *, uint32_t, double *, DevState *);
 __global__ void qxk_topk(const float *, uint32_t, uint32_t, float *, uint32_t *, float *, uint32_t *, uint32_t *,
                          DevState *);
@@ -29,7 +27,8 @@ void qxl_oproj(hipStream_t, const float *, const QTensor *, float *, float *);
 void qxl_gate_up(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, Tables, const DevState *,
                  float *);
 void qxl_down(hipStream_t, const float *, const QTensor *, Tables, const DevState *, float *, float *);
-void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32_t, DevState *, float *, float *);
+void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32_t, DevState *, float *, float *,
+              uint32_t *);
 }
 
 namespace {
@@ -89,7 +88,7 @@ struct qxg_ctx {
     float *vcur = nullptr, *attn = nullptr, *moe = nullptr, *norm = nullptr, *layer_dump = nullptr;
     double *rlog = nullptr;
     float *cand_v = nullptr, *top_v = nullptr;
-    uint32_t *cand_i = nullptr, *top_i = nullptr, *tokens = nullptr;
+    uint32_t *cand_i = nullptr, *top_i = nullptr, *tokens = nullptr, *dig = nullptr;
     DevState *st = nullptr;
     uint8_t *staging = nullptr;
     uint64_t staging_bytes = 0;
@@ -206,11 +205,10 @@ void launch_attention(qxg_ctx *c, uint32_t l, float *x, float *attn_dump, float 
     timed_begin(c, 2);
     qxl_qkv(c->s, x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv);
     timed_end(c, 2);
-    hipLaunchKernelGGL(qxk_qk_rope_kv, dim3(33), dim3(128), 0, c->s, c->qkv, w.q_norm, w.k_norm, c->T, c->kc, c->vc,
-                       c->ks, c->vs, l, c->kv_ctx, c->st, vcur_dump);
     timed_begin(c, 5);
-    hipLaunchKernelGGL(qxk_attn, dim3(32), dim3(512), (size_t)c->kv_ctx * sizeof(double), c->s, c->qkv, c->kc,
-                       c->vc, c->ks, c->vs, l, c->kv_ctx, std::sqrt(128.0), c->st, c->ctxv);
+    hipLaunchKernelGGL(qxk_attn, dim3(32), dim3(256), (size_t)c->kv_ctx * sizeof(double), c->s, c->qkv, w.q_norm,
+                       w.k_norm, c->T, c->kc, c->vc, c->ks, c->vs, l, c->kv_ctx, std::sqrt(128.0), c->st, c->ctxv,
+                       vcur_dump);
     timed_end(c, 5);
     timed_begin(c, 3);
     qxl_oproj(c->s, c->ctxv, w.wo, x, attn_dump);
@@ -233,7 +231,7 @@ void launch_moe(qxg_ctx *c, uint32_t l, float *x, float *moe_dump) {
 
 void launch_head(qxg_ctx *c, uint32_t top_n, float *norm_dump) {
     timed_begin(c, 4);
-    qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, norm_dump);
+    qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, norm_dump, c->dig);
     timed_end(c, 4);
     hipLaunchKernelGGL(qxk_topk, dim3(TOPK_BLOCKS), dim3(256), 0, c->s, c->logits, c->vocab, top_n, c->cand_v,
                        c->cand_i, c->top_v, c->top_i, c->tokens, c->st);
@@ -324,7 +322,7 @@ void qxg_close(qxg_ctx *c) {
     for (auto &kv : c->tens) free_tensor(kv.second);
     void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
-                    c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->st, c->staging};
+                    c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging};
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (hipEvent_t e : c->kt.ev) (void)hipEventDestroy(e);
     if (c->e0) (void)hipEventDestroy(c->e0);
@@ -417,13 +415,13 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     void **bufs[] = {(void **)&c->x, (void **)&c->qkv, (void **)&c->ctxv, (void **)&c->h, (void **)&c->logits,
                      (void **)&c->vcur, (void **)&c->attn, (void **)&c->moe, (void **)&c->norm,
                      (void **)&c->layer_dump, (void **)&c->rlog, (void **)&c->cand_v, (void **)&c->top_v,
-                     (void **)&c->cand_i, (void **)&c->top_i, (void **)&c->tokens};
+                     (void **)&c->cand_i, (void **)&c->top_i, (void **)&c->tokens, (void **)&c->dig};
     for (void **b : bufs) if (*b) { (void)hipFree(*b); *b = nullptr; }
     const uint64_t V = c->vocab ? c->vocab : 1;
     const uint64_t sizes[] = {2048 * 4, 5120 * 4, 4096 * 4, 8 * 768 * 4, V * 4, 512 * 4, 2048 * 4, 2048 * 4, 2048 * 4,
                               (uint64_t)(layers ? layers : 1) * 2048 * 4, 128 * 8, TOPK_BLOCKS * QXG_MAX_TOPN * 4,
                               QXG_MAX_TOPN * 4, TOPK_BLOCKS * QXG_MAX_TOPN * 4, QXG_MAX_TOPN * 4,
-                              (QXG_MAX_CTX + 2) * 4};
+                              (QXG_MAX_CTX + 2) * 4, (64 * 28 + 4) * 4};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i)
         if (!hip_ok(hipMalloc(bufs[i], sizes[i]), err, err_len, "work buffers")) return 0;
     if (!hip_ok(hipMemset(c->tokens, 0, sizes[15]), err, err_len, "work buffers")) return 0;
@@ -662,10 +660,11 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
         case 1: qxl_down(c->s, c->h, w.down, c->T, c->st, c->attn, nullptr); break;
         case 2: qxl_qkv(c->s, c->x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv); break;
         case 3: qxl_oproj(c->s, c->ctxv, w.wo, c->attn, nullptr); break;
-        case 4: qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, nullptr); break;
+        case 4: qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, nullptr, c->dig); break;
         case 5:
-            hipLaunchKernelGGL(qxk_attn, dim3(32), dim3(512), (size_t)c->kv_ctx * sizeof(double), c->s, c->qkv, c->kc,
-                               c->vc, c->ks, c->vs, l % c->kv_layers, c->kv_ctx, std::sqrt(128.0), c->st, c->ctxv);
+            hipLaunchKernelGGL(qxk_attn, dim3(32), dim3(256), (size_t)c->kv_ctx * sizeof(double), c->s, c->qkv,
+                               w.q_norm, w.k_norm, c->T, c->kc, c->vc, c->ks, c->vs, l % c->kv_layers, c->kv_ctx,
+                               std::sqrt(128.0), c->st, c->ctxv, nullptr);
             break;
         case 6:
             hipLaunchKernelGGL(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, c->x, w.ffn_norm, w.router,

@@ -40,55 +40,55 @@ DEV float fp16_exact(uint32_t h) {
     return __uint_as_float(bits);
 }
 
-DEV float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
-DEV double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
 DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 DEV uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
+
+// ---- DPP lane exchanges (VALU latency; __shfl_xor lowers to ds_bpermute through LDS).
+// quad_perm xor1 = [1,0,3,2], xor2 = [2,3,0,1]; row_ror:4/8 rotate within a 16-lane
+// row; row_half_mirror pairs lane i with 7-i inside each group of 8.
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128, DPP_HALF_MIRROR = 0x141 };
+
+template <int CTRL>
+DEV float dppf(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false)); }
+template <int CTRL>
+DEV int dppi(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+template <int CTRL>
+DEV double dppd(double v) {
+    const int2 h = *reinterpret_cast<int2 *>(&v);
+    int2 r;
+    r.x = __builtin_amdgcn_update_dpp(0, h.x, CTRL, 0xf, 0xf, false);
+    r.y = __builtin_amdgcn_update_dpp(0, h.y, CTRL, 0xf, 0xf, false);
+    return *reinterpret_cast<double *>(&r);
+}
+DEV float rdlanef(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+DEV double rdlaned(double v, int l) {
+    const int2 h = *reinterpret_cast<int2 *>(&v);
+    int2 r;
+    r.x = __builtin_amdgcn_readlane(h.x, l);
+    r.y = __builtin_amdgcn_readlane(h.y, l);
+    return *reinterpret_cast<double *>(&r);
+}
+// sum over each 16-lane row, result in every lane of the row
+DEV double row16_sum_d(double v) {
+    v += dppd<DPP_XOR1>(v); v += dppd<DPP_XOR2>(v); v += dppd<DPP_ROR4>(v); v += dppd<DPP_ROR8>(v);
+    return v;
+}
+// wave totals, uniform (rows combined in lane order 0, 16, 32, 48)
+DEV double wave_total_d(double v) {
+    v = row16_sum_d(v);
+    return (rdlaned(v, 0) + rdlaned(v, 16)) + (rdlaned(v, 32) + rdlaned(v, 48));
+}
+DEV double wave_max_d(double v) {
+    v = fmax(v, dppd<DPP_XOR1>(v)); v = fmax(v, dppd<DPP_XOR2>(v));
+    v = fmax(v, dppd<DPP_ROR4>(v)); v = fmax(v, dppd<DPP_ROR8>(v));
+    return fmax(fmax(rdlaned(v, 0), rdlaned(v, 16)), fmax(rdlaned(v, 32), rdlaned(v, 48)));
+}
 
 // 32 activations of one group as three int8 digit planes and a power-of-two scale
 struct Dig {
     uint32_t h[8], m[8], l[8];
     float s;
 };
-
-// returns false if any value is non-finite
-DEV bool make_digits(const float *v, Dig &g) {
-    float mx = 0.0f;
-    bool fin = true;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) { fin = fin && isfinite(v[i]); mx = fmaxf(mx, fabsf(v[i])); }
-    int e = 0;
-    if (fin && mx > 0.0f) (void)frexpf(mx, &e);   // 2^(e-1) <= mx < 2^e
-    else if (!fin) mx = 0.0f;
-    g.s = mx > 0.0f ? ldexpf(1.0f, e - 22) : 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        uint32_t ph = 0, pm = 0, pl = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            int X = mx > 0.0f ? (int)rintf(ldexpf(v[4 * k + j], 22 - e)) : 0;  // |X| <= 2^22
-            int L = ((X + 128) & 255) - 128;
-            int X1 = (X - L) >> 8;
-            int M = ((X1 + 128) & 255) - 128;
-            int H = (X1 - M) >> 8;
-            ph |= (uint32_t)(H & 255) << (8 * j);
-            pm |= (uint32_t)(M & 255) << (8 * j);
-            pl |= (uint32_t)(L & 255) << (8 * j);
-        }
-        g.h[k] = ph; g.m[k] = pm; g.l[k] = pl;
-    }
-    return fin;
-}
 
 DEV float combine(int aH, int aM, int aL) {
     return fmaf((float)aH, 65536.0f, fmaf((float)aM, 256.0f, (float)aL));
@@ -211,53 +211,178 @@ DEV float dot_q6(uint4 ql0, uint4 ql1, uint4 qh0, uint4 qh1, int sc0, int sc1, u
 }
 
 // ---------------------------------------------------------------- prologues
-// reference qx_apply_f32_rmsnorm (src/qx_format.c:3358-3371): double sum of
-// squares, rms = sqrt(ss/n + 1e-6), y = (float)(x/rms) * w.  Lane handles the
-// 32 values [32*lane, 32*lane+32) of a 2048-vector; the wave reduces.
-DEV bool norm_digits_2048(const float *x, const float *w, int lane, Dig &g) {
-    float v[32];
-    const float4 *xp = reinterpret_cast<const float4 *>(x + 32 * lane);
+DEV void load32(const float *p, float *v) {
+    const float4 *q = reinterpret_cast<const float4 *>(p);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float4 t = xp[i];
+        const float4 t = q[i];
         v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
     }
+}
+
+// reference qx_apply_f32_rmsnorm (src/qx_format.c:3358-3371): double sum of
+// squares, rms = sqrt(ss/n + 1e-6), y = (float)(x/rms) * w.  The lane holds the
+// 32 values [32*lane, 32*lane+32) of a 2048-vector (already loaded); the wave
+// reduces.  x/rms is formed as x*(1/rms) in double; after the cast to f32 the two
+// differ only when x/rms lies within 2^-53 relative of an f32 rounding boundary.
+DEV void rmsnorm32(float *v, const float *w) {
     double ss = 0.0;
 #pragma unroll
     for (int i = 0; i < 32; ++i) ss += (double)v[i] * (double)v[i];
-    ss = wave_sum_d(ss);
-    const double rms = sqrt(ss / 2048.0 + 1.0e-6);
-    const float4 *wp = reinterpret_cast<const float4 *>(w + 32 * lane);
+    ss = wave_total_d(ss);
+    const double inv = 1.0 / sqrt(ss / 2048.0 + 1.0e-6);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = (float)((double)v[i] * inv) * w[i];
+}
+
+
+// ---- block-cooperative activation digits.  The digit planes of all N/32 groups of
+// a vector are computed once per block into LDS (DIG_STRIDE dwords per group: h[8],
+// m[8], l[8], scale bits), 8 consecutive values per thread; the 4 threads of a group
+// form a quad, so the group max is two in-quad DPP exchanges.  With NORM, the vector
+// is first RMS-normalised with weights w (reference src/qx_format.c:3358-3371).
+constexpr int DIG_STRIDE = 28;   // 16-byte aligned rows for ds_read_b128
+
+DEV void digits8(const float *y, float mx, uint32_t &ph0, uint32_t &ph1, uint32_t &pm0, uint32_t &pm1, uint32_t &pl0,
+                 uint32_t &pl1, float &scale) {
+    int e = 0;
+    if (mx > 0.0f) (void)frexpf(mx, &e);
+    scale = mx > 0.0f ? ldexpf(1.0f, e - 22) : 0.0f;
+    uint32_t H[2] = {0, 0}, M[2] = {0, 0}, L[2] = {0, 0};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float4 t = wp[i];
-        v[4 * i] = (float)((double)v[4 * i] / rms) * t.x;
-        v[4 * i + 1] = (float)((double)v[4 * i + 1] / rms) * t.y;
-        v[4 * i + 2] = (float)((double)v[4 * i + 2] / rms) * t.z;
-        v[4 * i + 3] = (float)((double)v[4 * i + 3] / rms) * t.w;
+        const int X = mx > 0.0f ? (int)rintf(ldexpf(y[i], 22 - e)) : 0;
+        const int l = ((X + 128) & 255) - 128;
+        const int X1 = (X - l) >> 8;
+        const int m = ((X1 + 128) & 255) - 128;
+        const int hh = (X1 - m) >> 8;
+        H[i >> 2] |= (uint32_t)(hh & 255) << (8 * (i & 3));
+        M[i >> 2] |= (uint32_t)(m & 255) << (8 * (i & 3));
+        L[i >> 2] |= (uint32_t)(l & 255) << (8 * (i & 3));
     }
-    return make_digits(v, g);
+    ph0 = H[0]; ph1 = H[1]; pm0 = M[0]; pm1 = M[1]; pl0 = L[0]; pl1 = L[1];
 }
 
-DEV bool plain_digits(const float *x, Dig &g) {
-    float v[32];
-    const float4 *xp = reinterpret_cast<const float4 *>(x);
+// returns true when every value is finite (block-uniform); ends with a block barrier
+template <int N, bool NORM>
+DEV bool block_digits(const float *x, const float *w, uint32_t *s_dig, double *s_red, float *norm_out = nullptr) {
+    constexpr int NCH = N / 8, PER = (NCH + 255) / 256;
+    const int tid = threadIdx.x;
+    float v[PER][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 t = xp[i];
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    for (int it = 0; it < PER; ++it) {
+        const int c = tid + 256 * it;
+        if (c < NCH) {
+            const float4 a = reinterpret_cast<const float4 *>(x)[2 * c], b = reinterpret_cast<const float4 *>(x)[2 * c + 1];
+            v[it][0] = a.x; v[it][1] = a.y; v[it][2] = a.z; v[it][3] = a.w;
+            v[it][4] = b.x; v[it][5] = b.y; v[it][6] = b.z; v[it][7] = b.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = 0.0f;
+        }
     }
-    return make_digits(v, g);
+    if constexpr (NORM) {
+        static_assert(PER == 1, "normalised vectors are 2048 long");
+        const float4 a = reinterpret_cast<const float4 *>(w)[2 * tid], b = reinterpret_cast<const float4 *>(w)[2 * tid + 1];
+        const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += (double)v[0][i] * (double)v[0][i];
+        ss = wave_total_d(ss);
+        if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+        __syncthreads();
+        const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+        const double inv = 1.0 / sqrt(tot / (double)N + 1.0e-6);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[0][i] = (float)((double)v[0][i] * inv) * wv[i];
+        if (norm_out) {
+            reinterpret_cast<float4 *>(norm_out)[2 * tid] = make_float4(v[0][0], v[0][1], v[0][2], v[0][3]);
+            reinterpret_cast<float4 *>(norm_out)[2 * tid + 1] = make_float4(v[0][4], v[0][5], v[0][6], v[0][7]);
+        }
+    }
+    bool fin = true;
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+        const int c = tid + 256 * it;
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { fin = fin && isfinite(v[it][i]); mx = fmaxf(mx, fabsf(v[it][i])); }
+        mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
+        mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
+        if (c < NCH) {
+            uint32_t h0, h1, m0, m1, l0, l1;
+            float sc;
+            digits8(v[it], isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
+            uint32_t *d = s_dig + (c >> 2) * DIG_STRIDE;
+            const int q = c & 3;
+            *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
+            *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
+            if (q == 0) d[24] = __float_as_uint(sc);
+        }
+    }
+    return __syncthreads_or(!fin) == 0;
 }
 
-DEV bool wave_all(bool b) { return __all(b) != 0; }
-
-DEV void load_g2(uint4 *s_g2, uint2 *s_sel, const Tables &T) {
-    for (int i = threadIdx.x; i < 512; i += blockDim.x) s_g2[i] = T.g2[i];
-    for (int i = threadIdx.x; i < 128; i += blockDim.x) s_sel[i] = T.sel[i];
+DEV void load_dig(const uint32_t *__restrict__ s_dig, int g, Dig &d) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(s_dig + g * DIG_STRIDE);
+    const uint4 a = p[0], b = p[1], c = p[2], e = p[3], f = p[4], k = p[5];
+    d.h[0] = a.x; d.h[1] = a.y; d.h[2] = a.z; d.h[3] = a.w; d.h[4] = b.x; d.h[5] = b.y; d.h[6] = b.z; d.h[7] = b.w;
+    d.m[0] = c.x; d.m[1] = c.y; d.m[2] = c.z; d.m[3] = c.w; d.m[4] = e.x; d.m[5] = e.y; d.m[6] = e.z; d.m[7] = e.w;
+    d.l[0] = f.x; d.l[1] = f.y; d.l[2] = f.z; d.l[3] = f.w; d.l[4] = k.x; d.l[5] = k.y; d.l[6] = k.z; d.l[7] = k.w;
+    d.s = __uint_as_float(s_dig[g * DIG_STRIDE + 24]);
 }
+
 
 DEV uint32_t cur_pos(const DevState *st) { return st->pos0 + st->step; }
+
+// R per-lane partial sums (one per row, R in {1,2,4,8}) reduced over the wave:
+// up to two split rounds inside each quad (a lane keeps half of the rows and adds
+// its partner's half), then row16 sums, then the four rows of the wave through
+// readlane.  out[r] is the total of row r, wave-uniform.
+template <int R>
+DEV void rows_reduce(float (&v)[R], float (&out)[R], int lane) {
+    constexpr int S = R >= 4 ? 2 : (R == 2 ? 1 : 0);   // quad split rounds
+    constexpr int K = R >> S;                          // values left per lane
+    const bool b0 = lane & 1, b1 = (lane >> 1) & 1;
+    if constexpr (S >= 1) {
+        constexpr int half = R / 2;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float send = b0 ? v[i] : v[half + i];
+            const float keep = b0 ? v[half + i] : v[i];
+            v[i] = keep + dppf<DPP_XOR1>(send);
+        }
+    }
+    if constexpr (S >= 2) {
+        constexpr int half = R / 4;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float send = b1 ? v[i] : v[half + i];
+            const float keep = b1 ? v[half + i] : v[i];
+            v[i] = keep + dppf<DPP_XOR2>(send);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        if constexpr (S == 0) { v[i] += dppf<DPP_XOR1>(v[i]); }
+        if constexpr (S <= 1) { v[i] += dppf<DPP_XOR2>(v[i]); }
+        v[i] += dppf<DPP_ROR4>(v[i]);
+        v[i] += dppf<DPP_ROR8>(v[i]);
+    }
+    // lane L (low bits b0,b1) holds rows base..base+K-1 with base = K*(2^(S-1)*b0 + ...)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        int l0, j;
+        if constexpr (S == 0) { l0 = 0; j = r; }
+        else if constexpr (S == 1) { l0 = r / K; j = r % K; }               // b0 = subset
+        else { const int sub = r / K; l0 = (sub >> 1) | ((sub & 1) << 1); j = r % K; }  // subset = 2*b0 + b1
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < K; ++i) if (i == j) t = v[i];
+        out[r] = (rdlanef(t, l0) + rdlanef(t, l0 + 16)) + (rdlanef(t, l0 + 32) + rdlanef(t, l0 + 48));
+    }
+}
 
 }  // namespace
 
@@ -289,174 +414,195 @@ extern "C" __global__ __launch_bounds__(256) void qxk_embed(const uint8_t *emb, 
 }
 
 // attn RMSNorm + Q/K/V IQ4_XS projections (2048 -> 4096 | 512 | 512) into qkv[5120].
-// Wave per RPW consecutive rows; lane = 8*block + sub-block.
+// Wave per RPW consecutive rows; lane = 8*block + sub-block.  Every global load of
+// the wave is issued before the norm/digit prologue so their latencies overlap.
 template <int RPW>
 __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm_w,
         const uint8_t *q_qs, const uint8_t *q_meta, const uint8_t *k_qs, const uint8_t *k_meta,
         const uint8_t *v_qs, const uint8_t *v_meta, float *qkv) {
+    __shared__ uint32_t s_dig[64 * DIG_STRIDE];
+    __shared__ double s_red[4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int b = lane >> 3, ib = lane & 7;
-    Dig g;
-    const bool ok = wave_all(norm_digits_2048(x, norm_w, lane, g));
-    const int r0 = (blockIdx.x * 4 + wave) * RPW;
+    const int r0 = (blockIdx.x * 4 + wave) * RPW;   // grid covers exactly 5120 rows
+    uint4 qv[RPW];
+    uint2 mv[RPW];
+#pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
         const int r = r0 + rr;
-        if (r >= 5120) break;
         const uint8_t *qs, *meta;
         int lr;
         if (r < 4096) { qs = q_qs; meta = q_meta; lr = r; }
         else if (r < 4608) { qs = k_qs; meta = k_meta; lr = r - 4096; }
         else { qs = v_qs; meta = v_meta; lr = r - 4608; }
         const uint64_t blk = (uint64_t)lr * 8 + b;
-        const uint4 qv = reinterpret_cast<const uint4 *>(qs + blk * 128)[ib];
-        const uint2 mv = *reinterpret_cast<const uint2 *>(meta + blk * 8);
-        const float s = wave_sum(dot_iq4(qv, mv, ib, g));
-        if (lane == 0) qkv[r] = (ok && isfinite(s)) ? s : 0.0f;
+        qv[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[ib];
+        mv[rr] = *reinterpret_cast<const uint2 *>(meta + blk * 8);
     }
+    const bool ok = block_digits<2048, true>(x, norm_w, s_dig, s_red);
+    Dig g;
+    load_dig(s_dig, lane, g);
+    float part[RPW];
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) part[rr] = dot_iq4(qv[rr], mv[rr], ib, g);
+    float out[RPW];
+    rows_reduce<RPW>(part, out, lane);
+    float mine = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) if (lane == rr) mine = out[rr];
+    if (lane < RPW) qkv[r0 + lane] = (ok && isfinite(mine)) ? mine : 0.0f;
 }
 
-// per-head q/k RMSNorm (src/qx_format.c:3740-3757) + split-half RoPE (4625-4641,
-// cos/sin from the host-computed table) + INT8 K/V quantize (4449-4463) and store
-// at [layer][pos].  Blocks 0..31: q heads; block 32: k heads then K/V quantize.
+// Attention for one q head, with the per-head q/k RMSNorm (src/qx_format.c:3740-3757),
+// split-half RoPE (4625-4641; cos/sin from the host-computed table) and INT8 K/V
+// quantization (4449-4463) of the current position fused in: every block derives the
+// same K/V row (the scale spans all 512 values), block 0 stores it at [layer][pos],
+// and each block uses its own copy for position pos.  Scores (double) over 0..pos,
+// double softmax, f32 context accumulation per position in position order within
+// each of two position halves (reference src/qx_format.c:5127-5172).
 namespace {
-DEV double block_sum_d128(double v, double *red) {
-    v = wave_sum_d(v);
+DEV float block_max256(float v, float *red) {
+    v = fmaxf(v, dppf<DPP_XOR1>(v)); v = fmaxf(v, dppf<DPP_XOR2>(v));
+    v = fmaxf(v, dppf<DPP_ROR4>(v)); v = fmaxf(v, dppf<DPP_ROR8>(v));
+    v = fmaxf(fmaxf(rdlanef(v, 0), rdlanef(v, 16)), fmaxf(rdlanef(v, 32), rdlanef(v, 48)));
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return red[0] + red[1];
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-DEV void head_norm_rope(float *p, const float *w, uint32_t pos, const Tables &T, double *red, float *sv) {
-    const int d = threadIdx.x;
-    const float v = p[d];
-    const double ss = block_sum_d128((double)v * (double)v, red);
+// 128 values of one head held as (lane, lane+64) by a wave: per-head RMSNorm then RoPE
+DEV void head_norm_rope_wave(float &x0, float &x1, float w0, float w1, double c, double s) {
+    const double ss = wave_total_d((double)x0 * (double)x0 + (double)x1 * (double)x1);
     const double inv = 1.0 / sqrt(ss / 128.0 + 1.0e-6);
-    sv[d] = (float)((double)v * inv * (double)w[d]);
-    __syncthreads();
-    if (d < 64) {
-        const double c = T.rope_cos[pos * 64 + d], s = T.rope_sin[pos * 64 + d];
-        const float x0 = sv[d], x1 = sv[d + 64];
-        p[d] = (float)((double)x0 * c - (double)x1 * s);
-        p[d + 64] = (float)((double)x0 * s + (double)x1 * c);
-    }
-    __syncthreads();
-}
-
-DEV void quantize512(const float *src, int8_t *dst, float *scale_out, float *red) {
-    float mx = 0.0f;
-    for (int i = threadIdx.x; i < 512; i += 128) {
-        const float a = isfinite(src[i]) ? fabsf(src[i]) : 0.0f;
-        mx = fmaxf(mx, a);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(red[0], red[1]);
-    const float scale = mx > 0.0f ? mx / 127.0f : 1.0f;
-    for (int i = threadIdx.x; i < 512; i += 128) {
-        int q = isfinite(src[i]) ? (int)rintf(src[i] / scale) : 0;
-        q = q < -127 ? -127 : q > 127 ? 127 : q;
-        dst[i] = (int8_t)q;
-    }
-    if (threadIdx.x == 0) *scale_out = scale;
-    __syncthreads();
+    const float n0 = (float)((double)x0 * inv * (double)w0);
+    const float n1 = (float)((double)x1 * inv * (double)w1);
+    x0 = (float)((double)n0 * c - (double)n1 * s);
+    x1 = (float)((double)n0 * s + (double)n1 * c);
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(128) void qxk_qk_rope_kv(float *qkv, const float *q_norm, const float *k_norm,
-        Tables T, int8_t *kc, int8_t *vc, float *ks, float *vs, uint32_t layer, uint32_t ctx, const DevState *st,
-        float *vcur_dump) {
-    __shared__ double red[2];
-    __shared__ float redf[2];
-    __shared__ float sv[128];
-    const uint32_t pos = cur_pos(st);
-    if (blockIdx.x < 32) {
-        head_norm_rope(qkv + 128 * blockIdx.x, q_norm, pos, T, red, sv);
-        return;
-    }
-    for (int h = 0; h < 4; ++h) head_norm_rope(qkv + 4096 + 128 * h, k_norm, pos, T, red, sv);
-    const uint64_t slot = (uint64_t)layer * ctx + pos;
-    quantize512(qkv + 4096, kc + slot * 512, ks + slot, redf);
-    quantize512(qkv + 4608, vc + slot * 512, vs + slot, redf);
-    if (vcur_dump)
-        for (int i = threadIdx.x; i < 512; i += 128) vcur_dump[i] = qkv[4608 + i];
-}
-
-// GQA decode attention (reference src/qx_format.c:5127-5172): block per q head,
-// double scores over positions 0..pos, double softmax, context accumulated in
-// f32 per position (position order kept within each of NCH position chunks).
-extern "C" __global__ __launch_bounds__(512) void qxk_attn(const float *qkv, const int8_t *kc, const int8_t *vc,
-        const float *ks, const float *vs, uint32_t layer, uint32_t ctx, double inv_sqrt_divisor, const DevState *st,
-        float *ctx_out) {
-    extern __shared__ double s_sc[];
+extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, const float *q_norm, const float *k_norm,
+        Tables T, int8_t *kc, int8_t *vc, float *ks, float *vs, uint32_t layer, uint32_t ctx, double sqrt_hd,
+        const DevState *st, float *ctx_out, float *vcur_dump) {
+    extern __shared__ double s_sc[];               // ctx scores
+    __shared__ float s_k[512], s_v[512];
     __shared__ double s_q[128];
-    __shared__ double red[8];
-    __shared__ float s_part[4][128];
-    const int tid = threadIdx.x;
+    __shared__ float red[4];
+    __shared__ float s_part[2][128];
+    __shared__ int8_t s_k8[128], s_v8[128];
+    __shared__ float s_scale[2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qh = blockIdx.x, kvh = qh >> 3;
-    const uint32_t n = cur_pos(st) + 1;
+    const uint32_t pos = cur_pos(st), n = pos + 1;
     const uint64_t base = (uint64_t)layer * ctx;
-    if (tid < 128) s_q[tid] = (double)qkv[qh * 128 + tid];
+    // loads: k head `wave`, v (2 per thread), q head (wave 0 after k), norms, rope row
+    float k0 = qkv[4096 + 128 * wave + lane], k1 = qkv[4096 + 128 * wave + 64 + lane];
+    const float v0 = qkv[4608 + tid], v1 = qkv[4608 + 256 + tid];
+    float q0 = qkv[128 * qh + lane], q1 = qkv[128 * qh + 64 + lane];
+    const float kw0 = k_norm[lane], kw1 = k_norm[64 + lane], qw0 = q_norm[lane], qw1 = q_norm[64 + lane];
+    const double c = T.rope_cos[pos * 64 + lane], s = T.rope_sin[pos * 64 + lane];
+    head_norm_rope_wave(k0, k1, kw0, kw1, c, s);
+    s_k[128 * wave + lane] = k0;
+    s_k[128 * wave + 64 + lane] = k1;
+    s_v[tid] = v0;
+    s_v[256 + tid] = v1;
+    if (wave == 0) {
+        head_norm_rope_wave(q0, q1, qw0, qw1, c, s);
+        s_q[lane] = (double)q0;
+        s_q[64 + lane] = (double)q1;
+    }
+    // INT8 quantize K and V over all 512 values (scale = max|x|/127, 1 if zero)
+    float ka = 0.0f, va = 0.0f;
+    {
+        const float a0 = isfinite(k0) ? fabsf(k0) : 0.0f, a1 = isfinite(k1) ? fabsf(k1) : 0.0f;
+        ka = fmaxf(a0, a1);
+        const float b0 = isfinite(v0) ? fabsf(v0) : 0.0f, b1 = isfinite(v1) ? fabsf(v1) : 0.0f;
+        va = fmaxf(b0, b1);
+    }
+    ka = block_max256(ka, red);
+    va = block_max256(va, red);
+    const float kscale = ka > 0.0f ? ka / 127.0f : 1.0f, vscale = va > 0.0f ? va / 127.0f : 1.0f;
+    const uint64_t slot = base + pos;
+    for (int i = tid; i < 512; i += 256) {
+        const float kx = s_k[i], vx = s_v[i];
+        int qk = isfinite(kx) ? (int)rintf(kx / kscale) : 0;
+        int qv = isfinite(vx) ? (int)rintf(vx / vscale) : 0;
+        qk = qk < -127 ? -127 : qk > 127 ? 127 : qk;
+        qv = qv < -127 ? -127 : qv > 127 ? 127 : qv;
+        if (blockIdx.x == 0) { kc[slot * 512 + i] = (int8_t)qk; vc[slot * 512 + i] = (int8_t)qv; }
+        if ((i >> 7) == kvh) { s_k8[i & 127] = (int8_t)qk; s_v8[i & 127] = (int8_t)qv; }
+    }
+    if (blockIdx.x == 0 && tid == 0) { ks[slot] = kscale; vs[slot] = vscale; }
+    if (blockIdx.x == 0 && vcur_dump) { vcur_dump[tid] = v0; vcur_dump[256 + tid] = v1; }
+    if (tid == 0) { s_scale[0] = kscale; s_scale[1] = vscale; }
     __syncthreads();
-    double mx = -1.0e300;
-    for (uint32_t t = tid; t < n; t += 512) {
-        const int8_t *kp = kc + (base + t) * 512 + kvh * 128;
-        const float ksc = ks[base + t];
-        double s = 0.0;
-        for (int c = 0; c < 8; ++c) {
-            const int4 kk = reinterpret_cast<const int4 *>(kp)[c];
-            const int w[4] = {kk.x, kk.y, kk.z, kk.w};
+    // scores: 16 lanes per position, 8 dims per lane
+    {
+        const int sub = lane >> 4, dl = lane & 15;
+        double qd[8];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int8_t kb = (int8_t)((w[j >> 2] >> (8 * (j & 3))) & 255);
-                s += s_q[16 * c + j] * (double)((float)kb * ksc);
+        for (int j = 0; j < 8; ++j) qd[j] = s_q[8 * dl + j];
+        for (uint32_t t0 = 4 * wave; t0 < n; t0 += 16) {
+            const uint32_t t = t0 + sub;
+            double acc = 0.0;
+            if (t < n) {
+                uint2 kk;
+                float ksc;
+                if (t == pos) {
+                    kk = *reinterpret_cast<const uint2 *>(s_k8 + 8 * dl);
+                    ksc = s_scale[0];
+                } else {
+                    kk = *reinterpret_cast<const uint2 *>(kc + (base + t) * 512 + kvh * 128 + 8 * dl);
+                    ksc = ks[base + t];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int8_t kb = (int8_t)(((j < 4 ? kk.x : kk.y) >> (8 * (j & 3))) & 255u);
+                    acc += qd[j] * (double)((float)kb * ksc);
+                }
+            }
+            acc = row16_sum_d(acc);   // 16 lanes = one position
+            if (t < n && dl == 0) {
+                double sc = acc / sqrt_hd;
+                if (!isfinite(sc)) sc = 0.0;
+                s_sc[t] = sc;
             }
         }
-        s = s / inv_sqrt_divisor;
-        if (!isfinite(s)) s = 0.0;
-        s_sc[t] = s;
-        mx = fmax(mx, s);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
-    mx = red[0];
-    for (int i = 1; i < 8; ++i) mx = fmax(mx, red[i]);
+    // softmax in double
+    double mx = -1.0e300;
+    for (uint32_t t = tid; t < n; t += 256) mx = fmax(mx, s_sc[t]);
+    mx = wave_max_d(mx);
+    __shared__ double redd[4];
+    if (lane == 0) redd[wave] = mx;
     __syncthreads();
+    mx = fmax(fmax(redd[0], redd[1]), fmax(redd[2], redd[3]));
     double den = 0.0;
-    for (uint32_t t = tid; t < n; t += 512) {
+    for (uint32_t t = tid; t < n; t += 256) {
         const double e = exp(s_sc[t] - mx);
         s_sc[t] = e;
         den += e;
     }
-    den = wave_sum_d(den);
-    if ((tid & 63) == 0) red[tid >> 6] = den;
+    den = wave_total_d(den);
     __syncthreads();
-    den = 0.0;
-    for (int i = 0; i < 8; ++i) den += red[i];
+    if (lane == 0) redd[wave] = den;
+    __syncthreads();
+    den = (redd[0] + redd[1]) + (redd[2] + redd[3]);
     if (!isfinite(den) || den <= 0.0) den = 1.0;
-    const int nch = n <= 128 ? 1 : 4;
-    const int d = tid & 127, c = tid >> 7;
-    if (c < nch) {
-        const uint32_t t0 = (uint32_t)(((uint64_t)n * c) / nch), t1 = (uint32_t)(((uint64_t)n * (c + 1)) / nch);
-        float acc = 0.0f;
-        for (uint32_t t = t0; t < t1; ++t) {
-            const double w = s_sc[t] / den;
-            const float vv = (float)vc[(base + t) * 512 + kvh * 128 + d] * vs[base + t];
-            acc += (float)(w * (double)vv);
-        }
-        s_part[c][d] = acc;
+    // context: thread (d, half); positions of each half in order
+    const int d = tid & 127, hf = tid >> 7;
+    const uint32_t t0 = hf ? n / 2 : 0, t1 = hf ? n : n / 2;
+    float acc = 0.0f;
+    for (uint32_t t = t0; t < t1; ++t) {
+        const double wgt = s_sc[t] / den;
+        const float vv = t == pos ? (float)s_v8[d] * s_scale[1] : (float)vc[(base + t) * 512 + kvh * 128 + d] * vs[base + t];
+        acc += (float)(wgt * (double)vv);
     }
+    s_part[hf][d] = acc;
     __syncthreads();
-    if (tid < 128) {
-        float out = s_part[0][tid];
-        for (int i = 1; i < nch; ++i) out += s_part[i][tid];
-        ctx_out[qh * 128 + tid] = out;
-    }
+    if (tid < 128) ctx_out[qh * 128 + tid] = s_part[0][tid] + s_part[1][tid];
 }
 
 // O projection IQ4_XS 4096 -> 2048 on ctx, then x[r] += o[r] (src/qx_format.c:6420-6423).
@@ -464,136 +610,172 @@ extern "C" __global__ __launch_bounds__(512) void qxk_attn(const float *qkv, con
 template <int RPW>
 __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_t *qs, const uint8_t *meta,
                                                   float *x, float *attn_dump) {
+    __shared__ uint32_t s_dig[128 * DIG_STRIDE];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ib = lane & 7, b0 = lane >> 3, b1 = 8 + (lane >> 3);
-    Dig g0, g1;
-    const bool f0 = plain_digits(ctxv + 32 * lane, g0);
-    const bool f1 = plain_digits(ctxv + 32 * (lane + 64), g1);
-    const bool ok = wave_all(f0 && f1);
     const int r0 = (blockIdx.x * 4 + wave) * RPW;
+    uint4 q0[RPW], q1[RPW];
+    uint2 m0[RPW], m1[RPW];
+#pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
-        const int r = r0 + rr;
-        if (r >= 2048) break;
-        const uint64_t k0 = (uint64_t)r * 16 + b0, k1 = (uint64_t)r * 16 + b1;
-        const uint4 q0 = reinterpret_cast<const uint4 *>(qs + k0 * 128)[ib];
-        const uint4 q1 = reinterpret_cast<const uint4 *>(qs + k1 * 128)[ib];
-        const uint2 m0 = *reinterpret_cast<const uint2 *>(meta + k0 * 8);
-        const uint2 m1 = *reinterpret_cast<const uint2 *>(meta + k1 * 8);
-        const float s = wave_sum(dot_iq4(q0, m0, ib, g0) + dot_iq4(q1, m1, ib, g1));
-        if (lane == 0) {
-            const float o = (ok && isfinite(s)) ? s : 0.0f;
-            if (attn_dump) attn_dump[r] = o;
-            x[r] = x[r] + o;
-        }
+        const uint64_t k0 = (uint64_t)(r0 + rr) * 16 + b0, k1 = (uint64_t)(r0 + rr) * 16 + b1;
+        q0[rr] = reinterpret_cast<const uint4 *>(qs + k0 * 128)[ib];
+        q1[rr] = reinterpret_cast<const uint4 *>(qs + k1 * 128)[ib];
+        m0[rr] = *reinterpret_cast<const uint2 *>(meta + k0 * 8);
+        m1[rr] = *reinterpret_cast<const uint2 *>(meta + k1 * 8);
+    }
+    const bool ok = block_digits<4096, false>(ctxv, nullptr, s_dig, nullptr);
+    Dig g0, g1;
+    load_dig(s_dig, lane, g0);
+    load_dig(s_dig, lane + 64, g1);
+    float part[RPW];
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) part[rr] = dot_iq4(q0[rr], m0[rr], ib, g0) + dot_iq4(q1[rr], m1[rr], ib, g1);
+    float out[RPW];
+    rows_reduce<RPW>(part, out, lane);
+    float mine = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) if (lane == rr) mine = out[rr];
+    if (lane < RPW) {
+        const int r = r0 + lane;
+        const float o = (ok && isfinite(mine)) ? mine : 0.0f;
+        if (attn_dump) attn_dump[r] = o;
+        x[r] = x[r] + o;
     }
 }
 
-// ffn RMSNorm + F32 router (double dot) over E experts; the last block to finish
-// does the double softmax, top-8 (strict >, lowest index on ties) and the
-// renormalisation (reference src/qx_format.c:5254-5285).  Wave per expert row.
+// ffn RMSNorm + F32 router logits in double (reference src/qx_format.c:5254-5264);
+// wave per expert row.  The last block to finish (ticket counter, reset by that
+// block) does the double softmax and the top-8 (src/qx_format.c:5265-5285) and
+// publishes ids and renormalised weights in st for the expert kernels.  Top-8 is a
+// rank count: candidate c's rank is the number of experts j with p_j > p_c or
+// (p_j == p_c and j < c), i.e. its position in the order in which the reference's
+// repeated strict-> scans pick experts.
 extern "C" __global__ __launch_bounds__(256) void qxk_router(const float *x, const float *norm_w, const float *router,
         uint32_t experts, double *logits, DevState *st) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float v[32];
-    {
-        const float4 *xp = reinterpret_cast<const float4 *>(x + 32 * lane);
-        for (int i = 0; i < 8; ++i) { const float4 t = xp[i]; v[4*i] = t.x; v[4*i+1] = t.y; v[4*i+2] = t.z; v[4*i+3] = t.w; }
-        double ss = 0.0;
-        for (int i = 0; i < 32; ++i) ss += (double)v[i] * (double)v[i];
-        ss = wave_sum_d(ss);
-        const double rms = sqrt(ss / 2048.0 + 1.0e-6);
-        const float4 *wp = reinterpret_cast<const float4 *>(norm_w + 32 * lane);
-        for (int i = 0; i < 8; ++i) {
-            const float4 t = wp[i];
-            v[4*i] = (float)((double)v[4*i] / rms) * t.x; v[4*i+1] = (float)((double)v[4*i+1] / rms) * t.y;
-            v[4*i+2] = (float)((double)v[4*i+2] / rms) * t.z; v[4*i+3] = (float)((double)v[4*i+3] / rms) * t.w;
-        }
-    }
-    const uint32_t e = blockIdx.x * 4 + wave;
-    if (e < experts) {
-        const float4 *rp = reinterpret_cast<const float4 *>(router + (uint64_t)e * 2048 + 32 * lane);
-        double acc = 0.0;
-        for (int i = 0; i < 8; ++i) {
-            const float4 t = rp[i];
-            acc += (double)t.x * (double)v[4*i]; acc += (double)t.y * (double)v[4*i+1];
-            acc += (double)t.z * (double)v[4*i+2]; acc += (double)t.w * (double)v[4*i+3];
-        }
-        acc = wave_sum_d(acc);
-        if (lane == 0) logits[e] = acc;
-    }
     __shared__ uint32_t ticket;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) ticket = atomicAdd(&st->ctr_router, 1u);
-    __syncthreads();
-    if (ticket != gridDim.x - 1 || wave != 0) return;
-    __threadfence();
-    // one wave: lane holds experts lane and lane+64
-    const volatile double *lg = logits;
-    double p0 = lane < (int)experts ? lg[lane] : -1.0e300;
-    double p1 = lane + 64 < (int)experts ? lg[lane + 64] : -1.0e300;
-    double mx = fmax(p0, p1);
-    for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
-    p0 = lane < (int)experts ? exp(p0 - mx) : 0.0;
-    p1 = lane + 64 < (int)experts ? exp(p1 - mx) : 0.0;
-    const double den = wave_sum_d(p0 + p1);
-    p0 /= den; p1 /= den;
-    if (lane >= (int)experts) p0 = -2.0;
-    if (lane + 64 >= (int)experts) p1 = -2.0;
-    uint32_t ids[QXG_TOPK];
-    double w[QXG_TOPK];
-    for (int r = 0; r < QXG_TOPK; ++r) {
-        // best by (p desc, index asc)
-        double bp = p0; int bi = lane;
-        if (p1 > bp) { bp = p1; bi = lane + 64; }
-        for (int o = 32; o > 0; o >>= 1) {
-            const double op = __shfl_xor(bp, o);
-            const int oi = __shfl_xor(bi, o);
-            if (op > bp || (op == bp && oi < bi)) { bp = op; bi = oi; }
-        }
-        ids[r] = bi < (int)experts ? (uint32_t)bi : 0u;   // never address past the expert array
-        w[r] = bp;
-        if (bi == lane) p0 = -2.0;
-        if (bi == lane + 64) p1 = -2.0;
+    __shared__ double s_p[128], s_red[4];
+    __shared__ int s_cnt[2][128];
+    __shared__ uint32_t s_id[8];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t e = blockIdx.x * 4 + wave;
+    float v[32], w[32], r[32];
+    load32(x + 32 * lane, v);
+    load32(norm_w + 32 * lane, w);
+    if (e < experts) load32(router + (uint64_t)e * 2048 + 32 * lane, r);
+    rmsnorm32(v, w);
+    if (e < experts) {
+        double acc = 0.0;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc += (double)r[i] * (double)v[i];
+        acc = wave_total_d(acc);
+        // device-scope store: written through to memory, visible to every XCD once acknowledged
+        if (lane == 0) __hip_atomic_store(logits + e, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (lane == 0) {
+    // wait for this block's stores to be acknowledged, then take a ticket; no L2 write-back
+    // is needed because the only data handed over was stored at device scope
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (tid == 0) ticket = __hip_atomic_fetch_add(&st->ctr_router, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (ticket != gridDim.x - 1) return;
+    const int E = (int)experts;
+    // softmax over E <= 128 logits held by threads 0..127 (waves 0, 1), read at device scope
+    const double l = tid < E ? __hip_atomic_load(logits + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1.0e300;
+    double mx = wave_max_d(l);
+    if (lane == 0) s_red[wave] = mx;
+    __syncthreads();
+    mx = fmax(s_red[0], s_red[1]);
+    const double ex = tid < E ? exp(l - mx) : 0.0;
+    double den = wave_total_d(ex);
+    __syncthreads();
+    if (lane == 0) s_red[wave] = den;
+    __syncthreads();
+    den = s_red[0] + s_red[1];
+    if (tid < 128) s_p[tid] = tid < E ? ex / den : -1.0;
+    if (tid < QXG_TOPK) s_id[tid] = 0;   // defined even if non-finite logits leave a rank unassigned
+    __syncthreads();
+    // rank count: thread (c, half) scans experts [64*half, 64*half + 64)
+    const int c = tid & 127, half = tid >> 7;
+    const double pc = s_p[c];
+    int cnt = 0;
+#pragma unroll 8
+    for (int j = 64 * half; j < 64 * half + 64; ++j) {
+        const double pj = s_p[j];
+        cnt += (pj > pc || (pj == pc && j < c)) ? 1 : 0;
+    }
+    s_cnt[half][c] = cnt;
+    __syncthreads();
+    if (tid < E) {
+        const int rank = s_cnt[0][tid] + s_cnt[1][tid];
+        if (rank < QXG_TOPK) s_id[rank] = (uint32_t)tid;
+    }
+    __syncthreads();
+    if (tid == 0) {
         double sel = 0.0;
-        for (int r = 0; r < QXG_TOPK; ++r) sel += w[r];
-        for (int r = 0; r < QXG_TOPK; ++r) { st->moe_ids[r] = ids[r]; st->moe_w[r] = w[r] / sel; }
+        for (int q = 0; q < QXG_TOPK; ++q) sel += s_p[s_id[q] < experts ? s_id[q] : 0u];
+        for (int q = 0; q < QXG_TOPK; ++q) {
+            const uint32_t id = s_id[q] < experts ? s_id[q] : 0u;   // never address past the expert array
+            st->moe_ids[q] = id;
+            st->moe_w[q] = s_p[id] / sel;
+        }
         st->ctr_router = 0;
     }
 }
 
-// gate/up IQ2_XS (2048 -> 768, 8 selected experts) + SwiGLU
+// gate/up IQ2_XS (2048 -> 768) for the 8 routed experts (ids from st) + SwiGLU
 // h[r][i] = (float)(silu((double)g) * (double)u) (src/qx_format.c:5298, 2511-2513).
+// Weight loads are issued first; the codebook tables go to LDS while they fly.
+// Units are processed in a rolled loop whose prefetch registers shift by one unit per
+// iteration (static indices keep them in VGPRs).
 template <int UPW>
 __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *norm_w,
         const uint8_t *g_qs, const uint8_t *g_sc, const uint16_t *g_d,
-        const uint8_t *u_qs, const uint8_t *u_sc, const uint16_t *u_d,
-        Tables T, const DevState *st, float *h) {
+        const uint8_t *u_qs, const uint8_t *u_sc, const uint16_t *u_d, Tables T, const DevState *st, float *h) {
     __shared__ uint4 s_g2[512];
     __shared__ uint2 s_sel[128];
-    load_g2(s_g2, s_sel, T);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ uint32_t s_dig[64 * DIG_STRIDE];
+    __shared__ double s_red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int b = lane >> 3, ib = lane & 7;
-    Dig g;
-    const bool ok = wave_all(norm_digits_2048(x, norm_w, lane, g));
-    __syncthreads();
-    const int u0 = (blockIdx.x * 4 + wave) * UPW;
+    const int u0 = (blockIdx.x * 4 + wave) * UPW;   // grid covers exactly 8*768 units
+    uint2 gq[UPW], uq[UPW];
+    uint32_t gs[UPW], us[UPW], gd[UPW], ud[UPW];
+#pragma unroll
     for (int uu = 0; uu < UPW; ++uu) {
         const int unit = u0 + uu;
-        if (unit >= QXG_TOPK * QXG_FFN) break;
         const int r = unit / QXG_FFN, i = unit - r * QXG_FFN;
-        const uint64_t blk = ((uint64_t)st->moe_ids[r] * QXG_FFN + i) * 8 + b;
-        const uint2 gq = reinterpret_cast<const uint2 *>(g_qs + blk * 64)[ib];
-        const uint2 uq = reinterpret_cast<const uint2 *>(u_qs + blk * 64)[ib];
-        const float gs = wave_sum(dot_iq2(gq, g_sc[blk * 8 + ib], g_d[blk], g, s_g2, s_sel));
-        const float us = wave_sum(dot_iq2(uq, u_sc[blk * 8 + ib], u_d[blk], g, s_g2, s_sel));
-        if (lane == 0) {
-            const float gv = (ok && isfinite(gs)) ? gs : 0.0f;
-            const float uv = (ok && isfinite(us)) ? us : 0.0f;
+        const uint32_t e = __builtin_amdgcn_readfirstlane(st->moe_ids[r]);
+        const uint64_t blk = ((uint64_t)e * QXG_FFN + i) * 8 + b;
+        gq[uu] = reinterpret_cast<const uint2 *>(g_qs + blk * 64)[ib];
+        uq[uu] = reinterpret_cast<const uint2 *>(u_qs + blk * 64)[ib];
+        gs[uu] = g_sc[blk * 8 + ib];
+        us[uu] = u_sc[blk * 8 + ib];
+        gd[uu] = g_d[blk];
+        ud[uu] = u_d[blk];
+    }
+    const uint4 t0 = T.g2[tid], t1 = T.g2[tid + 256];
+    const uint2 t2 = T.sel[tid & 127];
+    s_g2[tid] = t0;
+    s_g2[tid + 256] = t1;
+    if (tid < 128) s_sel[tid] = t2;
+    const bool ok = block_digits<2048, true>(x, norm_w, s_dig, s_red);   // ends with a barrier
+    Dig g;
+    load_dig(s_dig, lane, g);
+#pragma unroll 1
+    for (int uu = 0; uu < UPW; ++uu) {
+        float p[2] = {dot_iq2(gq[0], gs[0], gd[0], g, s_g2, s_sel), dot_iq2(uq[0], us[0], ud[0], g, s_g2, s_sel)};
+        float o[2];
+        rows_reduce<2>(p, o, lane);
+        if (lane == uu) {
+            const float gv = (ok && isfinite(o[0])) ? o[0] : 0.0f;
+            const float uv = (ok && isfinite(o[1])) ? o[1] : 0.0f;
             const double sg = (double)gv / (1.0 + exp(-(double)gv));
-            h[unit] = (float)(sg * (double)uv);
+            h[u0 + uu] = (float)(sg * (double)uv);
+        }
+#pragma unroll
+        for (int k = 0; k + 1 < UPW; ++k) {
+            gq[k] = gq[k + 1]; uq[k] = uq[k + 1]; gs[k] = gs[k + 1]; us[k] = us[k + 1]; gd[k] = gd[k + 1]; ud[k] = ud[k + 1];
         }
     }
 }
@@ -606,38 +788,46 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, const uint8_t *d
         const uint16_t *d_d, Tables T, const DevState *st, float *x, float *moe_dump) {
     __shared__ uint2 s_g3[256];
     __shared__ uint2 s_sel[128];
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) s_g3[i] = T.g3[i];
-    for (int i = threadIdx.x; i < 128; i += blockDim.x) s_sel[i] = T.sel[i];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ uint32_t s_dig[192 * DIG_STRIDE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane >> 3, k = lane & 7;
     const uint32_t e = st->moe_ids[r];
-    Dig g[3];
-    bool fin = true;
+    const int r0 = (blockIdx.x * 4 + wave) * RPW;   // grid covers exactly 2048 rows
+    uint2 qv[RPW][3];
+    uint32_t aux[RPW][3], dd[RPW][3];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) fin &= plain_digits(h + r * QXG_FFN + 256 * j + 32 * k, g[j]);
-    const bool ok = wave_all(fin);
-    __syncthreads();
-    const int r0 = (blockIdx.x * 4 + wave) * RPW;
-    for (int rr = 0; rr < RPW; ++rr) {
-        const int row = r0 + rr;
-        if (row >= 2048) break;
-        float part = 0.0f;
+    for (int rr = 0; rr < RPW; ++rr)
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
-            const uint64_t blk = ((uint64_t)e * 2048 + row) * 3 + j;
-            const uint2 qv = reinterpret_cast<const uint2 *>(d_qs + blk * 64)[k];
-            const uint32_t aux = reinterpret_cast<const uint32_t *>(d_aux + blk * 32)[k];
-            part += dot_iq3(qv, aux, d_d[blk], g[j], s_g3, s_sel);
+            const uint64_t blk = ((uint64_t)e * 2048 + r0 + rr) * 3 + j;
+            qv[rr][j] = reinterpret_cast<const uint2 *>(d_qs + blk * 64)[k];
+            aux[rr][j] = reinterpret_cast<const uint32_t *>(d_aux + blk * 32)[k];
+            dd[rr][j] = d_d[blk];
         }
+    const uint2 t0 = T.g3[tid], t1 = T.sel[tid & 127];
+    double wr[8];
 #pragma unroll
-        for (int o = 4; o > 0; o >>= 1) part += __shfl_xor(part, o);
+    for (int q = 0; q < 8; ++q) wr[q] = st->moe_w[q];
+    s_g3[tid] = t0;
+    if (tid < 128) s_sel[tid] = t1;
+    const bool ok = block_digits<QXG_TOPK * QXG_FFN, false>(h, nullptr, s_dig, nullptr);   // ends with a barrier
+    Dig g[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) load_dig(s_dig, 24 * r + 8 * j + k, g[j]);
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+        float part = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) part += dot_iq3(qv[rr][j], aux[rr][j], dd[rr][j], g[j], s_g3, s_sel);
+        part += dppf<DPP_XOR1>(part);
+        part += dppf<DPP_XOR2>(part);
+        part += dppf<DPP_HALF_MIRROR>(part);   // lanes 8q..8q+7 now hold expert rank q's row
         const float y = (ok && isfinite(part)) ? part : 0.0f;
         float moe = 0.0f;
-        for (int q = 0; q < QXG_TOPK; ++q) {
-            const float yq = __shfl(y, 8 * q);
-            moe += (float)(st->moe_w[q] * (double)yq);
-        }
+#pragma unroll
+        for (int q = 0; q < QXG_TOPK; ++q) moe += (float)(wr[q] * (double)rdlanef(y, 8 * q));
         if (lane == 0) {
+            const int row = r0 + rr;
             if (moe_dump) moe_dump[row] = moe;
             x[row] = x[row] + moe;
         }
@@ -646,43 +836,54 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, const uint8_t *d
 
 // output RMSNorm + Q6_K head (2048 -> vocab) -> f32 logits (src/qx_format.c:3554-3738).
 // Skipped on prompt steps unless forced.  A non-finite logit sets st->nonfinite.
+// output RMSNorm + digits once per token into a global buffer (64 groups of
+// DIG_STRIDE dwords, then the all-finite flag); the head waves load their group.
+extern "C" __global__ __launch_bounds__(256) void qxk_norm_digits(const float *x, const float *norm_w, uint32_t *dig,
+                                                                   float *norm_dump, const DevState *st) {
+    if (!st->force_head && st->step + 1 < st->n_prompt) return;
+    __shared__ uint32_t s_dig[64 * DIG_STRIDE];
+    __shared__ double s_red[4];
+    const bool ok = block_digits<2048, true>(x, norm_w, s_dig, s_red, norm_dump);
+    for (int i = threadIdx.x; i < 64 * DIG_STRIDE; i += 256) dig[i] = s_dig[i];
+    if (threadIdx.x == 0) dig[64 * DIG_STRIDE] = ok ? 1u : 0u;
+}
+
 template <int RPW>
-__global__ __launch_bounds__(256) void qxk_head(const float *x, const float *norm_w, const uint8_t *ql,
-        const uint8_t *qh, const int8_t *sc, const uint16_t *dd, uint32_t vocab, DevState *st, float *logits,
-        float *norm_dump) {
+__global__ __launch_bounds__(256) void qxk_head(const uint32_t *dig, const uint8_t *ql,
+        const uint8_t *qh, const int8_t *sc, const uint16_t *dd, uint32_t vocab, DevState *st, float *logits) {
     if (!st->force_head && st->step + 1 < st->n_prompt) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int b = lane >> 3, ib = lane & 7, hh = ib >> 2, k = ib & 3;
-    Dig g;
-    bool fin;
-    {
-        float v[32];
-        const float4 *xp = reinterpret_cast<const float4 *>(x + 32 * lane);
-        for (int i = 0; i < 8; ++i) { const float4 t = xp[i]; v[4*i] = t.x; v[4*i+1] = t.y; v[4*i+2] = t.z; v[4*i+3] = t.w; }
-        double ss = 0.0;
-        for (int i = 0; i < 32; ++i) ss += (double)v[i] * (double)v[i];
-        ss = wave_sum_d(ss);
-        const double rms = sqrt(ss / 2048.0 + 1.0e-6);
-        for (int i = 0; i < 32; ++i) v[i] = (float)((double)v[i] / rms) * norm_w[32 * lane + i];
-        if (norm_dump && blockIdx.x == 0 && wave == 0)
-            for (int i = 0; i < 32; ++i) norm_dump[32 * lane + i] = v[i];
-        fin = make_digits(v, g);
-    }
-    const bool ok = wave_all(fin);
-    const Q6Bias bias = q6_bias(g);
     const uint32_t r0 = (blockIdx.x * 4 + wave) * RPW;
+    uint4 l0[RPW], l1[RPW], h0[RPW], h1[RPW];
+    int s0[RPW], s1[RPW];
+    uint32_t d16[RPW];
+#pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
-        const uint32_t r = r0 + rr;
-        if (r >= vocab) break;
+        const uint32_t r = min(r0 + rr, vocab - 1);   // tail rows re-read the last row; not stored
         const uint64_t blk = (uint64_t)r * 8 + b;
         const uint4 *lp = reinterpret_cast<const uint4 *>(ql + blk * 128 + 64 * hh + 32 * (k & 1));
         const uint4 *hp = reinterpret_cast<const uint4 *>(qh + blk * 64 + 32 * hh);
+        l0[rr] = lp[0]; l1[rr] = lp[1]; h0[rr] = hp[0]; h1[rr] = hp[1];
         const int8_t *sp = sc + blk * 16 + 8 * hh + 2 * k;
-        const float s = wave_sum(dot_q6(lp[0], lp[1], hp[0], hp[1], sp[0], sp[1], dd[blk], ib, g, bias));
-        if (lane == 0) {
-            logits[r] = s;
-            if (!ok || !isfinite(s)) st->nonfinite = 1u;
-        }
+        s0[rr] = sp[0]; s1[rr] = sp[1];
+        d16[rr] = dd[blk];
+    }
+    Dig g;
+    load_dig(dig, lane, g);
+    const bool ok = dig[64 * DIG_STRIDE] != 0u;
+    const Q6Bias bias = q6_bias(g);
+    float part[RPW];
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) part[rr] = dot_q6(l0[rr], l1[rr], h0[rr], h1[rr], s0[rr], s1[rr], d16[rr], ib, g, bias);
+    float out[RPW];
+    rows_reduce<RPW>(part, out, lane);
+    float mine = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) if (lane == rr) mine = out[rr];
+    if (lane < RPW && r0 + lane < vocab) {
+        logits[r0 + lane] = mine;
+        if (!ok || !isfinite(mine)) st->nonfinite = 1u;
     }
 }
 
@@ -879,10 +1080,11 @@ void qxl_down(hipStream_t s, const float *h, const QTensor *d, Tables T, const D
     hipLaunchKernelGGL(qxk_down<RPW>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, h, d->p0, d->p1, d->d, T, st, x, dump);
 }
 void qxl_head(hipStream_t s, const float *x, const float *nw, const QTensor *w, uint32_t vocab, DevState *st,
-              float *logits, float *norm_dump) {
-    constexpr int RPW = 8;
+              float *logits, float *norm_dump, uint32_t *dig) {
+    constexpr int RPW = 4;
+    hipLaunchKernelGGL(qxk_norm_digits, dim3(1), dim3(256), 0, s, x, nw, dig, norm_dump, st);
     const uint32_t grid = (vocab + 4 * RPW - 1) / (4 * RPW);
-    hipLaunchKernelGGL(qxk_head<RPW>, dim3(grid), dim3(256), 0, s, x, nw, w->p0, w->p1, (const int8_t *)w->p2, w->d,
-                       vocab, st, logits, norm_dump);
+    hipLaunchKernelGGL(qxk_head<RPW>, dim3(grid), dim3(256), 0, s, dig, w->p0, w->p1, (const int8_t *)w->p2, w->d,
+                       vocab, st, logits);
 }
 }
