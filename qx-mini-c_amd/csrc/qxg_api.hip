@@ -94,6 +94,9 @@ struct qxg_ctx {
     uint64_t staging_bytes = 0;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     KernelTiming kt;
+    // one decode step (embed .. head, top-1, step advance) recorded once and replayed
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
 };
 
 namespace {
@@ -134,6 +137,13 @@ bool upload_planes(qxg_ctx *c, QTensor &t, const void *host, uint64_t nbytes, ch
                        (uint16_t *)pl[3]);
     if (!hip_ok(hipGetLastError(), err, n, "repack launch")) return false;
     return hip_ok(hipStreamSynchronize(c->s), err, n, "repack");
+}
+
+void drop_graph(qxg_ctx *c) {
+    if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    c->graph_exec = nullptr;
+    c->graph = nullptr;
 }
 
 void free_tensor(QTensor &t) {
@@ -319,6 +329,7 @@ void qxg_close(qxg_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     if (c->s) (void)hipStreamSynchronize(c->s);
+    drop_graph(c);
     for (auto &kv : c->tens) free_tensor(kv.second);
     void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
@@ -340,6 +351,7 @@ int qxg_upload_tensor(qxg_ctx *c, const char *name, uint32_t type, const uint64_
     for (int i = 0; i < 4; ++i) if (dims[i]) elems *= dims[i];
     if (dims[0] % bv || elems / bv * bb != nbytes) { set_err(err, err_len, "tensor byte size inconsistent with dimensions"); return 0; }
     (void)hipSetDevice(c->device);
+    drop_graph(c);
     auto it = c->tens.find(name);
     if (it != c->tens.end()) { free_tensor(it->second); c->dev_bytes -= it->second.bytes; c->tens.erase(it); }
     QTensor t;
@@ -354,6 +366,7 @@ int qxg_upload_tensor(qxg_ctx *c, const char *name, uint32_t type, const uint64_
 int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_head, char *err, uint64_t err_len) {
     if (!c) { set_err(err, err_len, "invalid context"); return 0; }
     (void)hipSetDevice(c->device);
+    drop_graph(c);
     c->bound = false;
     c->L.assign(layers, LayerW{});
     c->experts = 0;
@@ -435,6 +448,7 @@ int qxg_kv_create(qxg_ctx *c, uint32_t layers, uint32_t ctx_tokens, uint32_t kv_
     if (!ctx_tokens || ctx_tokens > QXG_MAX_CTX) { set_err(err, err_len, "state loop context must be between 1 and 4096"); return 0; }
     if (!layers) { set_err(err, err_len, "invalid layer count"); return 0; }
     (void)hipSetDevice(c->device);
+    drop_graph(c);
     void *b[] = {c->kc, c->vc, c->ks, c->vs};
     for (void *p : b) if (p) (void)hipFree(p);
     c->kc = c->vc = nullptr; c->ks = c->vs = nullptr;
@@ -532,10 +546,29 @@ int qxg_generate(qxg_ctx *c, const uint32_t *prompt, uint32_t n_prompt, uint32_t
     (void)hipMemcpyAsync(c->tokens, prompt, (uint64_t)n_prompt * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, pos0, 0, n_prompt, 0);
     c->kt.used = 0;
-    (void)hipEventRecord(c->e0, c->s);
-    for (uint64_t s = 0; s < steps; ++s) {
+    const bool use_graph = c->kt.which < 0;   // in-situ kernel timing records events per launch: run eagerly
+    if (use_graph && !c->graph_exec) {
+        // every kernel reads the position/step from the device state, so one recorded
+        // step serves all steps; no memset nodes are recorded
+        if (!hip_ok(hipStreamBeginCapture(c->s, hipStreamCaptureModeThreadLocal), err, err_len, "capture")) return 0;
         launch_step(c, 1, false);
         hipLaunchKernelGGL(qxk_advance, dim3(1), dim3(64), 0, c->s, c->st);
+        hipGraph_t g = nullptr;
+        if (!hip_ok(hipStreamEndCapture(c->s, &g), err, err_len, "capture")) return 0;
+        c->graph = g;
+        if (!hip_ok(hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0), err, err_len, "graph instantiate")) {
+            drop_graph(c);
+            return 0;
+        }
+    }
+    (void)hipEventRecord(c->e0, c->s);
+    for (uint64_t s = 0; s < steps; ++s) {
+        if (use_graph) {
+            if (!hip_ok(hipGraphLaunch(c->graph_exec, c->s), err, err_len, "graph launch")) return 0;
+        } else {
+            launch_step(c, 1, false);
+            hipLaunchKernelGGL(qxk_advance, dim3(1), dim3(64), 0, c->s, c->st);
+        }
     }
     (void)hipEventRecord(c->e1, c->s);
     if (!finish(c, err, err_len)) return 0;

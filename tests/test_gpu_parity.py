@@ -122,9 +122,8 @@ def test_decode_two_layers_greedy(ctx, tmp_path):
         assert ok, why
         tok_g, tok_o = int(ids[0]), int(oids[0])
     om.close()
-    # device-resident greedy loop gives the same tokens as the step-by-step path
-    ctx.kv_create(2, 16)
-    gen, ms = ctx.generate([17], 5)
+    # the device-resident greedy loop (one recorded step replayed per token) gives the
+    # same tokens as the eager step-by-step path, on every replay, interleaved with eager work
     ctx.kv_create(2, 16)
     toks = []
     t = 17
@@ -132,4 +131,18 @@ def test_decode_two_layers_greedy(ctx, tmp_path):
         _, _, _, ids, _ = ctx.decode_token(t, s, True, 1)
         t = int(ids[0])
         toks.append(t)
-    assert list(gen) == toks
+    for rep in range(3):
+        ctx.kv_create(2, 16)
+        gen, ms = ctx.generate([17], 5)
+        assert list(gen) == toks, rep
+        ctx.kv_create(2, 16)
+        ctx.decode_token(17, 0, True, 1)             # eager work between replays
+        gen2, _ = ctx.generate([toks[0]], 4, pos0=1)  # continue from position 1
+        assert list(gen2) == toks[1:], rep
+    # eager (per-launch timed) loop agrees with the replayed one
+    ctx.kv_create(2, 16)
+    ctx.profile_kernel(qxg.KERNELS["gate_up"])
+    gen3, _ = ctx.generate([17], 5)
+    n, _ = ctx.profile_result()
+    ctx.profile_kernel(-1)
+    assert list(gen3) == toks and n == 5 * 2
