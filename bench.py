@@ -66,6 +66,35 @@ def cpu_baseline(model_path, tokens, budget_s):
                       f"scalar, 1 thread); wall {wall:.2f} s, process CPU {cpu:.2f} s"}
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a plain
+    device copy of known size); None when no summary is committed for it."""
+    path = os.path.join(ROOT, "profiles", "decode_config4_traffic.md")
+    if not os.path.exists(path):
+        return None
+    key = f"traffic_bytes_per_launch[{kernel}]="
+    with open(path) as f:
+        for line in f:
+            if line.startswith(key):
+                return int(line[len(key):])
+    return None
+
+
+def copy_calibration(mib):
+    """Copies a mib-MiB device buffer 4 times (and fills it once): the known-size
+    kernels whose FETCH_SIZE / WRITE_SIZE readings scale the decode kernels' counters."""
+    import torch
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    a.fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(4):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "copies": 4}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -75,11 +104,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=25.0)
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only copy a MIB-sized device buffer (HBM counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     import qxg
 
     prompt_len = 8
@@ -147,7 +181,7 @@ def main():
                    "kv": "int8", "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "kernel": args.roofline_kernel, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": kb, "avg_launch_us": round(avg_kernel_s * 1e6, 3),
+                     "traffic": measured_traffic(args.roofline_kernel), "bytes_per_launch": kb, "avg_launch_us": round(avg_kernel_s * 1e6, 3),
                      "launches": launches},
         "token_roofline": {"algorithmic_bytes_per_token": int(token_bytes),
                            "achieved_GBs": round(token_bytes * tok_s / 1e9, 1),

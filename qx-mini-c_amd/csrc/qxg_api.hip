@@ -22,13 +22,15 @@ __global__ void qxk_advance(DevState *);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
                             uint64_t, float *);
 __global__ void qxk_repack(uint32_t, const uint8_t *, uint64_t, uint8_t *, uint8_t *, uint8_t *, uint16_t *);
-void qxl_qkv(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, const QTensor *, float *);
-void qxl_oproj(hipStream_t, const float *, const QTensor *, float *, float *);
+void qxl_qkv(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, const QTensor *, float *,
+             Timer = Timer());
+void qxl_oproj(hipStream_t, const float *, const QTensor *, float *, float *, Timer = Timer());
 void qxl_gate_up(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, Tables, const DevState *,
-                 float *);
-void qxl_down(hipStream_t, const float *, const QTensor *, Tables, const DevState *, float *, float *);
+                 float *, Timer = Timer());
+void qxl_down(hipStream_t, const float *, const QTensor *, Tables, const DevState *, float *, float *,
+              Timer = Timer());
 void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32_t, DevState *, float *, float *,
-              uint32_t *);
+              uint32_t *, Timer = Timer());
 }
 
 namespace {
@@ -195,54 +197,44 @@ const QTensor *find(qxg_ctx *c, const std::string &name) {
     return it == c->tens.end() ? nullptr : &it->second;
 }
 
-void timed_begin(qxg_ctx *c, int which) {
-    if (c->kt.which != which) return;
+// Start/stop events for the next launch of kernel `which` while in-situ timing of
+// that kernel is enabled; an empty Timer otherwise.
+Timer timer_for(qxg_ctx *c, int which) {
+    if (c->kt.which != which) return Timer();
     if (c->kt.used * 2 + 2 > c->kt.ev.size()) {
-        for (int i = 0; i < 256; ++i) { hipEvent_t e; (void)hipEventCreate(&e); c->kt.ev.push_back(e); }
+        for (int i = 0; i < 256; ++i) {
+            hipEvent_t e;
+            (void)hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
+            c->kt.ev.push_back(e);
+        }
     }
-    (void)hipEventRecord(c->kt.ev[2 * c->kt.used], c->s);
-}
-
-void timed_end(qxg_ctx *c, int which) {
-    if (c->kt.which != which) return;
-    (void)hipEventRecord(c->kt.ev[2 * c->kt.used + 1], c->s);
+    Timer t;
+    t.e0 = c->kt.ev[2 * c->kt.used];
+    t.e1 = c->kt.ev[2 * c->kt.used + 1];
     ++c->kt.used;
+    return t;
 }
 
 // ---- launch sequences (all asynchronous on c->s) ----
 void launch_attention(qxg_ctx *c, uint32_t l, float *x, float *attn_dump, float *vcur_dump) {
     const LayerW &w = c->L[l];
-    timed_begin(c, 2);
-    qxl_qkv(c->s, x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv);
-    timed_end(c, 2);
-    timed_begin(c, 5);
-    hipLaunchKernelGGL(qxk_attn, dim3(32), dim3(256), (size_t)c->kv_ctx * sizeof(double), c->s, c->qkv, w.q_norm,
-                       w.k_norm, c->T, c->kc, c->vc, c->ks, c->vs, l, c->kv_ctx, std::sqrt(128.0), c->st, c->ctxv,
-                       vcur_dump);
-    timed_end(c, 5);
-    timed_begin(c, 3);
-    qxl_oproj(c->s, c->ctxv, w.wo, x, attn_dump);
-    timed_end(c, 3);
+    qxl_qkv(c->s, x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv, timer_for(c, 2));
+    qx_launch(qxk_attn, dim3(32), dim3(256), (uint32_t)(c->kv_ctx * sizeof(double)), c->s, timer_for(c, 5), c->qkv,
+              w.q_norm, w.k_norm, c->T, c->kc, c->vc, c->ks, c->vs, l, c->kv_ctx, std::sqrt(128.0),
+              (const DevState *)c->st, c->ctxv, vcur_dump);
+    qxl_oproj(c->s, c->ctxv, w.wo, x, attn_dump, timer_for(c, 3));
 }
 
 void launch_moe(qxg_ctx *c, uint32_t l, float *x, float *moe_dump) {
     const LayerW &w = c->L[l];
-    timed_begin(c, 6);
-    hipLaunchKernelGGL(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, x, w.ffn_norm, w.router,
-                       c->experts, c->rlog, c->st);
-    timed_end(c, 6);
-    timed_begin(c, 0);
-    qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->st, c->h);
-    timed_end(c, 0);
-    timed_begin(c, 1);
-    qxl_down(c->s, c->h, w.down, c->T, c->st, x, moe_dump);
-    timed_end(c, 1);
+    qx_launch(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, timer_for(c, 6), (const float *)x,
+              w.ffn_norm, w.router, c->experts, c->rlog, c->st);
+    qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->st, c->h, timer_for(c, 0));
+    qxl_down(c->s, c->h, w.down, c->T, c->st, x, moe_dump, timer_for(c, 1));
 }
 
 void launch_head(qxg_ctx *c, uint32_t top_n, float *norm_dump) {
-    timed_begin(c, 4);
-    qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, norm_dump, c->dig);
-    timed_end(c, 4);
+    qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, norm_dump, c->dig, timer_for(c, 4));
     hipLaunchKernelGGL(qxk_topk, dim3(TOPK_BLOCKS), dim3(256), 0, c->s, c->logits, c->vocab, top_n, c->cand_v,
                        c->cand_i, c->top_v, c->top_i, c->tokens, c->st);
 }

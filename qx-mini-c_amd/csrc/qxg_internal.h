@@ -58,3 +58,17 @@ struct Tables {
     uint2 *sel;    // sign index (7 bits) -> v_perm selectors for 8 values
     double *rope_cos, *rope_sin;  // [QXG_MAX_CTX][64]
 };
+
+// Optional start/stop events recorded around one launch on its stream.  Created with
+// hipEventDisableSystemFence, the markers skip the system-scope cache writeback, so
+// their elapsed time stays close to the kernel's own duration.
+struct Timer {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+};
+
+template <typename F, typename... A>
+inline void qx_launch(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t s, Timer t, A... args) {
+    if (t.e0) (void)hipEventRecord(t.e0, s);
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+    if (t.e1) (void)hipEventRecord(t.e1, s);
+}

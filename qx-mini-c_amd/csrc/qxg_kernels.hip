@@ -1061,30 +1061,30 @@ extern "C" __global__ __launch_bounds__(256) void qxk_repack(uint32_t type, cons
 
 // ----------------------------------------------------------------- launch wrappers
 extern "C" {
-void qxl_qkv(hipStream_t s, const float *x, const float *nw, const QTensor *q, const QTensor *k, const QTensor *v, float *qkv) {
+void qxl_qkv(hipStream_t s, const float *x, const float *nw, const QTensor *q, const QTensor *k, const QTensor *v, float *qkv, Timer t) {
     constexpr int RPW = 4;
-    hipLaunchKernelGGL(qxk_qkv<RPW>, dim3(5120 / (4 * RPW)), dim3(256), 0, s, x, nw, q->p0, q->p1, k->p0, k->p1, v->p0, v->p1, qkv);
+    qx_launch(qxk_qkv<RPW>, dim3(5120 / (4 * RPW)), dim3(256), 0, s, t, x, nw, q->p0, q->p1, k->p0, k->p1, v->p0, v->p1, qkv);
 }
-void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, float *dump) {
+void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, float *dump, Timer t) {
     constexpr int RPW = 2;
-    hipLaunchKernelGGL(qxk_oproj<RPW>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, ctxv, o->p0, o->p1, x, dump);
+    qx_launch(qxk_oproj<RPW>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, t, ctxv, o->p0, o->p1, x, dump);
 }
 void qxl_gate_up(hipStream_t s, const float *x, const float *nw, const QTensor *g, const QTensor *u, Tables T,
-                 const DevState *st, float *h) {
+                 const DevState *st, float *h, Timer t) {
     constexpr int UPW = 4;
-    hipLaunchKernelGGL(qxk_gate_up<UPW>, dim3(QXG_TOPK * QXG_FFN / (4 * UPW)), dim3(256), 0, s, x, nw,
+    qx_launch(qxk_gate_up<UPW>, dim3(QXG_TOPK * QXG_FFN / (4 * UPW)), dim3(256), 0, s, t, x, nw,
                        g->p0, g->p1, g->d, u->p0, u->p1, u->d, T, st, h);
 }
-void qxl_down(hipStream_t s, const float *h, const QTensor *d, Tables T, const DevState *st, float *x, float *dump) {
+void qxl_down(hipStream_t s, const float *h, const QTensor *d, Tables T, const DevState *st, float *x, float *dump, Timer t) {
     constexpr int RPW = 2;
-    hipLaunchKernelGGL(qxk_down<RPW>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, h, d->p0, d->p1, d->d, T, st, x, dump);
+    qx_launch(qxk_down<RPW>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, t, h, d->p0, d->p1, d->d, T, st, x, dump);
 }
 void qxl_head(hipStream_t s, const float *x, const float *nw, const QTensor *w, uint32_t vocab, DevState *st,
-              float *logits, float *norm_dump, uint32_t *dig) {
+              float *logits, float *norm_dump, uint32_t *dig, Timer t) {
     constexpr int RPW = 4;
     hipLaunchKernelGGL(qxk_norm_digits, dim3(1), dim3(256), 0, s, x, nw, dig, norm_dump, st);
     const uint32_t grid = (vocab + 4 * RPW - 1) / (4 * RPW);
-    hipLaunchKernelGGL(qxk_head<RPW>, dim3(grid), dim3(256), 0, s, dig, w->p0, w->p1, (const int8_t *)w->p2, w->d,
+    qx_launch(qxk_head<RPW>, dim3(grid), dim3(256), 0, s, t, dig, w->p0, w->p1, (const int8_t *)w->p2, w->d,
                        vocab, st, logits);
 }
 }
