@@ -440,6 +440,18 @@ int qxg_kv_create(qxg_ctx *c, uint32_t layers, uint32_t ctx_tokens, uint32_t kv_
     if (!ctx_tokens || ctx_tokens > QXG_MAX_CTX) { set_err(err, err_len, "state loop context must be between 1 and 4096"); return 0; }
     if (!layers) { set_err(err, err_len, "invalid layer count"); return 0; }
     (void)hipSetDevice(c->device);
+    {   // the attention kernel keeps one double score per position in LDS
+        hipFuncAttributes fa;
+        int max_lds = 0;
+        if (!hip_ok(hipFuncGetAttributes(&fa, (const void *)qxk_attn), err, err_len, "attention attributes") ||
+            !hip_ok(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, c->device), err, err_len,
+                    "device attributes"))
+            return 0;
+        if (fa.sharedSizeBytes + (size_t)ctx_tokens * sizeof(double) > (size_t)max_lds) {
+            set_err(err, err_len, "context too long for the attention kernel's LDS on this device");
+            return 0;
+        }
+    }
     drop_graph(c);
     void *b[] = {c->kc, c->vc, c->ks, c->vs};
     for (void *p : b) if (p) (void)hipFree(p);

@@ -72,3 +72,19 @@ inline void qx_launch(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t
     hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
     if (t.e1) (void)hipEventRecord(t.e1, s);
 }
+
+// Phase timestamps for development builds only (-DQXG_TRACE): lane 0 of each wave
+// stores s_memrealtime (100 MHz) into qxg_trace_buf[kernel][wave][point]; read back
+// with qxg_trace_read.  Normal builds compile the markers out.
+#ifdef QXG_TRACE
+extern __device__ unsigned long long qxg_trace_buf[8][8192][8];
+#define QXG_MARK(kind, point)                                                                  \
+    do {                                                                                       \
+        const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                        \
+        if ((threadIdx.x & 63) == 0) qxg_trace_buf[kind][blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)][point] = t_; \
+    } while (0)
+#define QXG_ANCHOR(v) asm volatile("" ::"v"(v))
+#else
+#define QXG_MARK(kind, point) ((void)0)
+#define QXG_ANCHOR(v) ((void)0)
+#endif

@@ -263,56 +263,74 @@ DEV void digits8(const float *y, float mx, uint32_t &ph0, uint32_t &ph1, uint32_
     ph0 = H[0]; ph1 = H[1]; pm0 = M[0]; pm1 = M[1]; pl0 = L[0]; pl1 = L[1];
 }
 
-// returns true when every value is finite (block-uniform); ends with a block barrier
+// The vector (and norm weights) as loaded by one thread: 8 consecutive values per
+// chunk.  Kernels issue these loads before their weight loads, so the activation
+// arrives first and the digit work overlaps the weight fetch.
 template <int N, bool NORM>
-DEV bool block_digits(const float *x, const float *w, uint32_t *s_dig, double *s_red, float *norm_out = nullptr) {
-    constexpr int NCH = N / 8, PER = (NCH + 255) / 256;
-    const int tid = threadIdx.x;
+struct DigIn {
+    static constexpr int NCH = N / 8, PER = (NCH + 255) / 256;
     float v[PER][8];
+    float w[NORM ? 8 : 1];
+};
+
+template <int N, bool NORM>
+DEV void digits_load(const float *x, const float *w, DigIn<N, NORM> &in) {
+    using D = DigIn<N, NORM>;
+    const int tid = threadIdx.x;
 #pragma unroll
-    for (int it = 0; it < PER; ++it) {
+    for (int it = 0; it < D::PER; ++it) {
         const int c = tid + 256 * it;
-        if (c < NCH) {
+        if (c < D::NCH) {
             const float4 a = reinterpret_cast<const float4 *>(x)[2 * c], b = reinterpret_cast<const float4 *>(x)[2 * c + 1];
-            v[it][0] = a.x; v[it][1] = a.y; v[it][2] = a.z; v[it][3] = a.w;
-            v[it][4] = b.x; v[it][5] = b.y; v[it][6] = b.z; v[it][7] = b.w;
+            in.v[it][0] = a.x; in.v[it][1] = a.y; in.v[it][2] = a.z; in.v[it][3] = a.w;
+            in.v[it][4] = b.x; in.v[it][5] = b.y; in.v[it][6] = b.z; in.v[it][7] = b.w;
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[it][i] = 0.0f;
+            for (int i = 0; i < 8; ++i) in.v[it][i] = 0.0f;
         }
     }
     if constexpr (NORM) {
-        static_assert(PER == 1, "normalised vectors are 2048 long");
+        static_assert(D::PER == 1, "normalised vectors are 2048 long");
         const float4 a = reinterpret_cast<const float4 *>(w)[2 * tid], b = reinterpret_cast<const float4 *>(w)[2 * tid + 1];
-        const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        in.w[0] = a.x; in.w[1] = a.y; in.w[2] = a.z; in.w[3] = a.w;
+        in.w[4] = b.x; in.w[5] = b.y; in.w[6] = b.z; in.w[7] = b.w;
+    }
+}
+
+// returns true when every value is finite (block-uniform); ends with a block barrier
+template <int N, bool NORM>
+DEV bool block_digits(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float *norm_out = nullptr) {
+    using D = DigIn<N, NORM>;
+    const int tid = threadIdx.x;
+    if constexpr (NORM) {
         double ss = 0.0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ss += (double)v[0][i] * (double)v[0][i];
+        for (int i = 0; i < 8; ++i) ss += (double)in.v[0][i] * (double)in.v[0][i];
         ss = wave_total_d(ss);
         if ((tid & 63) == 0) s_red[tid >> 6] = ss;
         __syncthreads();
         const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
         const double inv = 1.0 / sqrt(tot / (double)N + 1.0e-6);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[0][i] = (float)((double)v[0][i] * inv) * wv[i];
+        for (int i = 0; i < 8; ++i) in.v[0][i] = (float)((double)in.v[0][i] * inv) * in.w[i];
         if (norm_out) {
-            reinterpret_cast<float4 *>(norm_out)[2 * tid] = make_float4(v[0][0], v[0][1], v[0][2], v[0][3]);
-            reinterpret_cast<float4 *>(norm_out)[2 * tid + 1] = make_float4(v[0][4], v[0][5], v[0][6], v[0][7]);
+            reinterpret_cast<float4 *>(norm_out)[2 * tid] = make_float4(in.v[0][0], in.v[0][1], in.v[0][2], in.v[0][3]);
+            reinterpret_cast<float4 *>(norm_out)[2 * tid + 1] = make_float4(in.v[0][4], in.v[0][5], in.v[0][6], in.v[0][7]);
         }
     }
     bool fin = true;
 #pragma unroll
-    for (int it = 0; it < PER; ++it) {
+    for (int it = 0; it < D::PER; ++it) {
         const int c = tid + 256 * it;
         float mx = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { fin = fin && isfinite(v[it][i]); mx = fmaxf(mx, fabsf(v[it][i])); }
+        for (int i = 0; i < 8; ++i) { fin = fin && isfinite(in.v[it][i]); mx = fmaxf(mx, fabsf(in.v[it][i])); }
         mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
         mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
-        if (c < NCH) {
+        if (c < D::NCH) {
             uint32_t h0, h1, m0, m1, l0, l1;
             float sc;
-            digits8(v[it], isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
+            digits8(in.v[it], isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
             uint32_t *d = s_dig + (c >> 2) * DIG_STRIDE;
             const int q = c & 3;
             *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
@@ -386,6 +404,17 @@ DEV void rows_reduce(float (&v)[R], float (&out)[R], int lane) {
 
 }  // namespace
 
+#ifdef QXG_TRACE
+__device__ unsigned long long qxg_trace_buf[8][8192][8];
+extern "C" int qxg_trace_read(unsigned long long *out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(qxg_trace_buf), sizeof(qxg_trace_buf)) == hipSuccess;
+}
+extern "C" int qxg_trace_clear() {
+    static unsigned long long zero[8 * 8192 * 8];
+    return hipMemcpyToSymbol(HIP_SYMBOL(qxg_trace_buf), zero, sizeof(zero)) == hipSuccess;
+}
+#endif
+
 // ================================================================= kernels
 
 // Q4_K embedding row of tokens[step] -> x (reference src/qx_format.c:2079-2110,
@@ -425,6 +454,9 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int b = lane >> 3, ib = lane & 7;
     const int r0 = (blockIdx.x * 4 + wave) * RPW;   // grid covers exactly 5120 rows
+    QXG_MARK(3, 0);
+    DigIn<2048, true> din;
+    digits_load(x, norm_w, din);
     uint4 qv[RPW];
     uint2 mv[RPW];
 #pragma unroll
@@ -439,18 +471,25 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
         qv[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[ib];
         mv[rr] = *reinterpret_cast<const uint2 *>(meta + blk * 8);
     }
-    const bool ok = block_digits<2048, true>(x, norm_w, s_dig, s_red);
+    __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
+    QXG_ANCHOR(din.v[0][7]);
+    QXG_MARK(3, 1);
+    const bool ok = block_digits(din, s_dig, s_red);
+    QXG_MARK(3, 2);
     Dig g;
     load_dig(s_dig, lane, g);
     float part[RPW];
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) part[rr] = dot_iq4(qv[rr], mv[rr], ib, g);
+    QXG_ANCHOR(part[0]); QXG_ANCHOR(part[RPW - 1]);
+    QXG_MARK(3, 3);
     float out[RPW];
     rows_reduce<RPW>(part, out, lane);
     float mine = 0.0f;
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) if (lane == rr) mine = out[rr];
     if (lane < RPW) qkv[r0 + lane] = (ok && isfinite(mine)) ? mine : 0.0f;
+    QXG_MARK(3, 4);
 }
 
 // Attention for one q head, with the per-head q/k RMSNorm (src/qx_format.c:3740-3757),
@@ -460,6 +499,9 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
 // and each block uses its own copy for position pos.  Scores (double) over 0..pos,
 // double softmax, f32 context accumulation per position in position order within
 // each of two position halves (reference src/qx_format.c:5127-5172).
+// The cached K/V rows of positions [0, min(pos, ATT_STAGE)) and their scales are
+// loaded at kernel start, together with q/k/v, and staged in LDS while the norm,
+// RoPE and quantization run; later positions are read from global memory.
 namespace {
 DEV float block_max256(float v, float *red) {
     v = fmaxf(v, dppf<DPP_XOR1>(v)); v = fmaxf(v, dppf<DPP_XOR2>(v));
@@ -482,10 +524,14 @@ DEV void head_norm_rope_wave(float &x0, float &x1, float w0, float w1, double c,
 }
 }  // namespace
 
+constexpr int ATT_STAGE = 128;   // positions staged in LDS (4 uint4 of K and of V per thread)
+
 extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, const float *q_norm, const float *k_norm,
         Tables T, int8_t *kc, int8_t *vc, float *ks, float *vs, uint32_t layer, uint32_t ctx, double sqrt_hd,
         const DevState *st, float *ctx_out, float *vcur_dump) {
     extern __shared__ double s_sc[];               // ctx scores
+    __shared__ uint4 s_kst[ATT_STAGE * 8], s_vst[ATT_STAGE * 8];   // staged rows of this kv head
+    __shared__ float s_kss[ATT_STAGE], s_vss[ATT_STAGE];
     __shared__ float s_k[512], s_v[512];
     __shared__ double s_q[128];
     __shared__ float red[4];
@@ -496,12 +542,27 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     const int qh = blockIdx.x, kvh = qh >> 3;
     const uint32_t pos = cur_pos(st), n = pos + 1;
     const uint64_t base = (uint64_t)layer * ctx;
+    const uint32_t nst = pos < (uint32_t)ATT_STAGE ? pos : (uint32_t)ATT_STAGE;   // staged positions
+    // cached rows first: 16 bytes of row (tid>>3) + 32*i, chunk tid&7, i < 4
+    uint4 kst[4], vst[4];
+    float kss = 0.0f, vss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = (tid >> 3) + 32 * i;
+        if (t < nst) {
+            const uint64_t off = (base + t) * 512 + kvh * 128 + 16 * (tid & 7);
+            kst[i] = *reinterpret_cast<const uint4 *>(kc + off);
+            vst[i] = *reinterpret_cast<const uint4 *>(vc + off);
+        }
+    }
+    if ((uint32_t)tid < nst) { kss = ks[base + tid]; vss = vs[base + tid]; }
     // loads: k head `wave`, v (2 per thread), q head (wave 0 after k), norms, rope row
     float k0 = qkv[4096 + 128 * wave + lane], k1 = qkv[4096 + 128 * wave + 64 + lane];
     const float v0 = qkv[4608 + tid], v1 = qkv[4608 + 256 + tid];
     float q0 = qkv[128 * qh + lane], q1 = qkv[128 * qh + 64 + lane];
     const float kw0 = k_norm[lane], kw1 = k_norm[64 + lane], qw0 = q_norm[lane], qw1 = q_norm[64 + lane];
     const double c = T.rope_cos[pos * 64 + lane], s = T.rope_sin[pos * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     head_norm_rope_wave(k0, k1, kw0, kw1, c, s);
     s_k[128 * wave + lane] = k0;
     s_k[128 * wave + 64 + lane] = k1;
@@ -536,6 +597,12 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     if (blockIdx.x == 0 && tid == 0) { ks[slot] = kscale; vs[slot] = vscale; }
     if (blockIdx.x == 0 && vcur_dump) { vcur_dump[tid] = v0; vcur_dump[256 + tid] = v1; }
     if (tid == 0) { s_scale[0] = kscale; s_scale[1] = vscale; }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = (tid >> 3) + 32 * i;
+        if (t < nst) { s_kst[t * 8 + (tid & 7)] = kst[i]; s_vst[t * 8 + (tid & 7)] = vst[i]; }
+    }
+    if ((uint32_t)tid < nst) { s_kss[tid] = kss; s_vss[tid] = vss; }
     __syncthreads();
     // scores: 16 lanes per position, 8 dims per lane
     {
@@ -552,6 +619,9 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
                 if (t == pos) {
                     kk = *reinterpret_cast<const uint2 *>(s_k8 + 8 * dl);
                     ksc = s_scale[0];
+                } else if (t < nst) {
+                    kk = reinterpret_cast<const uint2 *>(s_kst)[t * 16 + dl];
+                    ksc = s_kss[t];
                 } else {
                     kk = *reinterpret_cast<const uint2 *>(kc + (base + t) * 512 + kvh * 128 + 8 * dl);
                     ksc = ks[base + t];
@@ -597,7 +667,9 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     float acc = 0.0f;
     for (uint32_t t = t0; t < t1; ++t) {
         const double wgt = s_sc[t] / den;
-        const float vv = t == pos ? (float)s_v8[d] * s_scale[1] : (float)vc[(base + t) * 512 + kvh * 128 + d] * vs[base + t];
+        const float vv = t == pos ? (float)s_v8[d] * s_scale[1]
+                         : t < nst ? (float)reinterpret_cast<const int8_t *>(s_vst)[t * 128 + d] * s_vss[t]
+                                   : (float)vc[(base + t) * 512 + kvh * 128 + d] * vs[base + t];
         acc += (float)(wgt * (double)vv);
     }
     s_part[hf][d] = acc;
@@ -614,6 +686,10 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ib = lane & 7, b0 = lane >> 3, b1 = 8 + (lane >> 3);
     const int r0 = (blockIdx.x * 4 + wave) * RPW;
+    QXG_MARK(0, 0);
+    DigIn<4096, false> din;
+    digits_load(ctxv, nullptr, din);
+    const float xr = lane < RPW ? x[r0 + lane] : 0.0f;
     uint4 q0[RPW], q1[RPW];
     uint2 m0[RPW], m1[RPW];
 #pragma unroll
@@ -624,13 +700,19 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
         m0[rr] = *reinterpret_cast<const uint2 *>(meta + k0 * 8);
         m1[rr] = *reinterpret_cast<const uint2 *>(meta + k1 * 8);
     }
-    const bool ok = block_digits<4096, false>(ctxv, nullptr, s_dig, nullptr);
+    __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
+    QXG_ANCHOR(din.v[1][7]);
+    QXG_MARK(0, 1);
+    const bool ok = block_digits(din, s_dig, nullptr);
+    QXG_MARK(0, 2);
     Dig g0, g1;
     load_dig(s_dig, lane, g0);
     load_dig(s_dig, lane + 64, g1);
     float part[RPW];
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) part[rr] = dot_iq4(q0[rr], m0[rr], ib, g0) + dot_iq4(q1[rr], m1[rr], ib, g1);
+    QXG_ANCHOR(part[0]); QXG_ANCHOR(part[RPW - 1]);
+    QXG_MARK(0, 3);
     float out[RPW];
     rows_reduce<RPW>(part, out, lane);
     float mine = 0.0f;
@@ -640,8 +722,9 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
         const int r = r0 + lane;
         const float o = (ok && isfinite(mine)) ? mine : 0.0f;
         if (attn_dump) attn_dump[r] = o;
-        x[r] = x[r] + o;
+        x[r] = xr + o;
     }
+    QXG_MARK(0, 4);
 }
 
 // ffn RMSNorm + F32 router logits in double (reference src/qx_format.c:5254-5264);
@@ -739,13 +822,18 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int b = lane >> 3, ib = lane & 7;
     const int u0 = (blockIdx.x * 4 + wave) * UPW;   // grid covers exactly 8*768 units
+    QXG_MARK(1, 0);
+    // the expert id heads the longest chain (id -> weights): load it first
+    const uint32_t e = __builtin_amdgcn_readfirstlane(st->moe_ids[u0 / QXG_FFN]);   // 4 | 768: one expert per wave
+    DigIn<2048, true> din;
+    digits_load(x, norm_w, din);
+    const uint4 t0 = T.g2[tid], t1 = T.g2[tid + 256];
+    const uint2 t2 = T.sel[tid & 127];
     uint2 gq[UPW], uq[UPW];
     uint32_t gs[UPW], us[UPW], gd[UPW], ud[UPW];
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu) {
-        const int unit = u0 + uu;
-        const int r = unit / QXG_FFN, i = unit - r * QXG_FFN;
-        const uint32_t e = __builtin_amdgcn_readfirstlane(st->moe_ids[r]);
+        const int i = (u0 + uu) % QXG_FFN;
         const uint64_t blk = ((uint64_t)e * QXG_FFN + i) * 8 + b;
         gq[uu] = reinterpret_cast<const uint2 *>(g_qs + blk * 64)[ib];
         uq[uu] = reinterpret_cast<const uint2 *>(u_qs + blk * 64)[ib];
@@ -754,30 +842,47 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
         gd[uu] = g_d[blk];
         ud[uu] = u_d[blk];
     }
-    const uint4 t0 = T.g2[tid], t1 = T.g2[tid + 256];
-    const uint2 t2 = T.sel[tid & 127];
+    __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     s_g2[tid] = t0;
     s_g2[tid + 256] = t1;
     if (tid < 128) s_sel[tid] = t2;
-    const bool ok = block_digits<2048, true>(x, norm_w, s_dig, s_red);   // ends with a barrier
+    QXG_ANCHOR(din.v[0][7]);
+    QXG_MARK(1, 1);
+    const bool ok = block_digits(din, s_dig, s_red);   // ends with a barrier
+    QXG_MARK(1, 2);
     Dig g;
     load_dig(s_dig, lane, g);
+    // dots unit by unit in a rolled loop (prefetch registers and results shift by one
+    // slot per iteration, so every index is static), then one reduction for all units
+    float pg[UPW], pu[UPW];
 #pragma unroll 1
     for (int uu = 0; uu < UPW; ++uu) {
-        float p[2] = {dot_iq2(gq[0], gs[0], gd[0], g, s_g2, s_sel), dot_iq2(uq[0], us[0], ud[0], g, s_g2, s_sel)};
-        float o[2];
-        rows_reduce<2>(p, o, lane);
-        if (lane == uu) {
-            const float gv = (ok && isfinite(o[0])) ? o[0] : 0.0f;
-            const float uv = (ok && isfinite(o[1])) ? o[1] : 0.0f;
-            const double sg = (double)gv / (1.0 + exp(-(double)gv));
-            h[u0 + uu] = (float)(sg * (double)uv);
-        }
+        const float a = dot_iq2(gq[0], gs[0], gd[0], g, s_g2, s_sel);
+        const float c = dot_iq2(uq[0], us[0], ud[0], g, s_g2, s_sel);
 #pragma unroll
         for (int k = 0; k + 1 < UPW; ++k) {
             gq[k] = gq[k + 1]; uq[k] = uq[k + 1]; gs[k] = gs[k + 1]; us[k] = us[k + 1]; gd[k] = gd[k + 1]; ud[k] = ud[k + 1];
+            pg[k] = pg[k + 1]; pu[k] = pu[k + 1];
         }
+        pg[UPW - 1] = a;
+        pu[UPW - 1] = c;
     }
+    QXG_ANCHOR(pg[0]);
+    QXG_MARK(1, 3);
+    float p[2 * UPW], o[2 * UPW];
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) { p[k] = pg[k]; p[UPW + k] = pu[k]; }
+    rows_reduce<2 * UPW>(p, o, lane);
+    float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) if (lane == k) { gv = o[k]; uv = o[UPW + k]; }
+    if (lane < UPW) {
+        gv = (ok && isfinite(gv)) ? gv : 0.0f;
+        uv = (ok && isfinite(uv)) ? uv : 0.0f;
+        const double sg = (double)gv / (1.0 + exp(-(double)gv));
+        h[u0 + lane] = (float)(sg * (double)uv);
+    }
+    QXG_MARK(1, 4);
 }
 
 // down IQ3_XXS (768 -> 2048) for the 8 experts, rank-ordered weighted f32 sum and
@@ -791,8 +896,18 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, const uint8_t *d
     __shared__ uint32_t s_dig[192 * DIG_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane >> 3, k = lane & 7;
-    const uint32_t e = st->moe_ids[r];
     const int r0 = (blockIdx.x * 4 + wave) * RPW;   // grid covers exactly 2048 rows
+    QXG_MARK(2, 0);
+    const uint32_t e = st->moe_ids[r];   // heads the id -> weights chain: loaded first
+    double wr[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) wr[q] = st->moe_w[q];
+    DigIn<QXG_TOPK * QXG_FFN, false> din;
+    digits_load(h, nullptr, din);
+    float xr[RPW];
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) xr[rr] = x[r0 + rr];
+    const uint2 t0 = T.g3[tid], t1 = T.sel[tid & 127];
     uint2 qv[RPW][3];
     uint32_t aux[RPW][3], dd[RPW][3];
 #pragma unroll
@@ -804,13 +919,13 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, const uint8_t *d
             aux[rr][j] = reinterpret_cast<const uint32_t *>(d_aux + blk * 32)[k];
             dd[rr][j] = d_d[blk];
         }
-    const uint2 t0 = T.g3[tid], t1 = T.sel[tid & 127];
-    double wr[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) wr[q] = st->moe_w[q];
+    __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     s_g3[tid] = t0;
     if (tid < 128) s_sel[tid] = t1;
-    const bool ok = block_digits<QXG_TOPK * QXG_FFN, false>(h, nullptr, s_dig, nullptr);   // ends with a barrier
+    QXG_ANCHOR(din.v[din.PER - 1][7]);
+    QXG_MARK(2, 1);
+    const bool ok = block_digits(din, s_dig, nullptr);   // ends with a barrier
+    QXG_MARK(2, 2);
     Dig g[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) load_dig(s_dig, 24 * r + 8 * j + k, g[j]);
@@ -829,9 +944,11 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, const uint8_t *d
         if (lane == 0) {
             const int row = r0 + rr;
             if (moe_dump) moe_dump[row] = moe;
-            x[row] = x[row] + moe;
+            x[row] = xr[rr] + moe;
         }
+        if (rr == 0) QXG_MARK(2, 3);
     }
+    QXG_MARK(2, 4);
 }
 
 // output RMSNorm + Q6_K head (2048 -> vocab) -> f32 logits (src/qx_format.c:3554-3738).
@@ -843,7 +960,9 @@ extern "C" __global__ __launch_bounds__(256) void qxk_norm_digits(const float *x
     if (!st->force_head && st->step + 1 < st->n_prompt) return;
     __shared__ uint32_t s_dig[64 * DIG_STRIDE];
     __shared__ double s_red[4];
-    const bool ok = block_digits<2048, true>(x, norm_w, s_dig, s_red, norm_dump);
+    DigIn<2048, true> din;
+    digits_load(x, norm_w, din);
+    const bool ok = block_digits(din, s_dig, s_red, norm_dump);
     for (int i = threadIdx.x; i < 64 * DIG_STRIDE; i += 256) dig[i] = s_dig[i];
     if (threadIdx.x == 0) dig[64 * DIG_STRIDE] = ok ? 1u : 0u;
 }

@@ -80,12 +80,14 @@ def test_moe_block_config2(ctx, layer_model):
     om.close()
 
 
-@pytest.mark.parametrize("pos", [0, 5, 2047])
-def test_attention_block_config3(ctx, layer_model, pos):
-    """Config 3: attention at `pos` with positions 0..pos-1 prefilled by seeded INT8 rows."""
+@pytest.mark.parametrize("pos,ctx_tokens", [(0, 2048), (5, 2048), (127, 2048), (128, 2048), (130, 2048),
+                                            (2047, 2048), (4095, 4096)])
+def test_attention_block_config3(ctx, layer_model, pos, ctx_tokens):
+    """Config 3: attention at `pos` with positions 0..pos-1 prefilled by seeded INT8 rows
+    (positions around the 128-row LDS staging window, and the maximum context)."""
     ctx.load(layer_model)
-    ctx.kv_create(1, 2048)
-    okv = qxo.KV(1, 2048)
+    ctx.kv_create(1, ctx_tokens)
+    okv = qxo.KV(1, ctx_tokens)
     if pos:
         k, v, ks, vs = seeded_kv(33, pos)
         ctx.kv_write(0, 0, k, v, ks, vs)
