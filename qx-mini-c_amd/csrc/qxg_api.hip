@@ -15,7 +15,7 @@ extern "C" {
 __global__ void qxk_embed(const uint8_t *, uint64_t, const uint32_t *, const DevState *, float *);
 __global__ void qxk_attn(const float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
                          uint32_t, uint32_t, double, const DevState *, float *, float *);
-__global__ void qxk_router(const float *, const float *, const float *, uint32_t, double *, DevState *);
+__global__ void qxk_router(const float *, const float *, const float *, uint32_t, double *);
 __global__ void qxk_topk(const float *, uint32_t, uint32_t, float *, uint32_t *, float *, uint32_t *, uint32_t *,
                          DevState *);
 __global__ void qxk_advance(DevState *);
@@ -25,8 +25,8 @@ __global__ void qxk_repack(uint32_t, const uint8_t *, uint64_t, uint8_t *, uint8
 void qxl_qkv(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, const QTensor *, float *,
              Timer = Timer());
 void qxl_oproj(hipStream_t, const float *, const QTensor *, float *, float *, Timer = Timer());
-void qxl_gate_up(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, Tables, const DevState *,
-                 float *, Timer = Timer());
+void qxl_gate_up(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, Tables, const double *,
+                 uint32_t, DevState *, float *, Timer = Timer());
 void qxl_down(hipStream_t, const float *, const QTensor *, Tables, const DevState *, float *, float *,
               Timer = Timer());
 void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32_t, DevState *, float *, float *,
@@ -228,8 +228,8 @@ void launch_attention(qxg_ctx *c, uint32_t l, float *x, float *attn_dump, float 
 void launch_moe(qxg_ctx *c, uint32_t l, float *x, float *moe_dump) {
     const LayerW &w = c->L[l];
     qx_launch(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, timer_for(c, 6), (const float *)x,
-              w.ffn_norm, w.router, c->experts, c->rlog, c->st);
-    qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->st, c->h, timer_for(c, 0));
+              w.ffn_norm, w.router, c->experts, c->rlog);
+    qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h, timer_for(c, 0));
     qxl_down(c->s, c->h, w.down, c->T, c->st, x, moe_dump, timer_for(c, 1));
 }
 
@@ -693,7 +693,7 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
         const uint32_t l = (layer + i) % c->layers;
         const LayerW &w = c->L[l];
         switch (which) {
-        case 0: qxl_gate_up(c->s, c->x, w.ffn_norm, w.gate, w.up, c->T, c->st, c->h); break;
+        case 0: qxl_gate_up(c->s, c->x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h); break;
         case 1: qxl_down(c->s, c->h, w.down, c->T, c->st, c->attn, nullptr); break;
         case 2: qxl_qkv(c->s, c->x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv); break;
         case 3: qxl_oproj(c->s, c->ctxv, w.wo, c->attn, nullptr); break;
@@ -705,7 +705,7 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
             break;
         case 6:
             hipLaunchKernelGGL(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, c->x, w.ffn_norm, w.router,
-                               c->experts, c->rlog, c->st);
+                               c->experts, c->rlog);
             break;
         }
     }

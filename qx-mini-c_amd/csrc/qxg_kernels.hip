@@ -728,83 +728,97 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
 }
 
 // ffn RMSNorm + F32 router logits in double (reference src/qx_format.c:5254-5264);
-// wave per expert row.  The last block to finish (ticket counter, reset by that
-// block) does the double softmax and the top-8 (src/qx_format.c:5265-5285) and
-// publishes ids and renormalised weights in st for the expert kernels.  Top-8 is a
-// rank count: candidate c's rank is the number of experts j with p_j > p_c or
-// (p_j == p_c and j < c), i.e. its position in the order in which the reference's
-// repeated strict-> scans pick experts.
+// wave per expert row.  The softmax and top-8 run in the prologue of the gate/up
+// kernel, where the expert ids are needed.
 extern "C" __global__ __launch_bounds__(256) void qxk_router(const float *x, const float *norm_w, const float *router,
-        uint32_t experts, double *logits, DevState *st) {
-    __shared__ uint32_t ticket;
-    __shared__ double s_p[128], s_red[4];
-    __shared__ int s_cnt[2][128];
-    __shared__ uint32_t s_id[8];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        uint32_t experts, double *logits) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t e = blockIdx.x * 4 + wave;
+    if (e >= experts) return;
     float v[32], w[32], r[32];
+    load32(router + (uint64_t)e * 2048 + 32 * lane, r);
     load32(x + 32 * lane, v);
     load32(norm_w + 32 * lane, w);
-    if (e < experts) load32(router + (uint64_t)e * 2048 + 32 * lane, r);
     rmsnorm32(v, w);
-    if (e < experts) {
-        double acc = 0.0;
+    double acc = 0.0;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) acc += (double)r[i] * (double)v[i];
-        acc = wave_total_d(acc);
-        // device-scope store: written through to memory, visible to every XCD once acknowledged
-        if (lane == 0) __hip_atomic_store(logits + e, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // wait for this block's stores to be acknowledged, then take a ticket; no L2 write-back
-    // is needed because the only data handed over was stored at device scope
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    if (tid == 0) ticket = __hip_atomic_fetch_add(&st->ctr_router, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (ticket != gridDim.x - 1) return;
-    const int E = (int)experts;
-    // softmax over E <= 128 logits held by threads 0..127 (waves 0, 1), read at device scope
-    const double l = tid < E ? __hip_atomic_load(logits + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1.0e300;
-    double mx = wave_max_d(l);
-    if (lane == 0) s_red[wave] = mx;
-    __syncthreads();
-    mx = fmax(s_red[0], s_red[1]);
-    const double ex = tid < E ? exp(l - mx) : 0.0;
-    double den = wave_total_d(ex);
-    __syncthreads();
-    if (lane == 0) s_red[wave] = den;
-    __syncthreads();
-    den = s_red[0] + s_red[1];
-    if (tid < 128) s_p[tid] = tid < E ? ex / den : -1.0;
-    if (tid < QXG_TOPK) s_id[tid] = 0;   // defined even if non-finite logits leave a rank unassigned
-    __syncthreads();
-    // rank count: thread (c, half) scans experts [64*half, 64*half + 64)
-    const int c = tid & 127, half = tid >> 7;
-    const double pc = s_p[c];
-    int cnt = 0;
-#pragma unroll 8
-    for (int j = 64 * half; j < 64 * half + 64; ++j) {
-        const double pj = s_p[j];
-        cnt += (pj > pc || (pj == pc && j < c)) ? 1 : 0;
-    }
-    s_cnt[half][c] = cnt;
-    __syncthreads();
-    if (tid < E) {
-        const int rank = s_cnt[0][tid] + s_cnt[1][tid];
-        if (rank < QXG_TOPK) s_id[rank] = (uint32_t)tid;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        double sel = 0.0;
-        for (int q = 0; q < QXG_TOPK; ++q) sel += s_p[s_id[q] < experts ? s_id[q] : 0u];
-        for (int q = 0; q < QXG_TOPK; ++q) {
-            const uint32_t id = s_id[q] < experts ? s_id[q] : 0u;   // never address past the expert array
-            st->moe_ids[q] = id;
-            st->moe_w[q] = s_p[id] / sel;
-        }
-        st->ctr_router = 0;
-    }
+    for (int i = 0; i < 32; ++i) acc += (double)r[i] * (double)v[i];
+    acc = wave_total_d(acc);
+    if (lane == 0) logits[e] = acc;
 }
+
+namespace {
+// order-preserving int32 image of a float (NaN sorts below everything)
+DEV int order_key(double v) {
+    if (v != v) return INT_MIN;
+    const int b = __float_as_int((float)v);
+    return b ^ ((b >> 31) & 0x7fffffff);
+}
+DEV int wave_max_i(int v) {
+    v = max(v, dppi<DPP_XOR1>(v)); v = max(v, dppi<DPP_XOR2>(v));
+    v = max(v, dppi<DPP_ROR4>(v)); v = max(v, dppi<DPP_ROR8>(v));
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Router top-8 and renormalised weights (src/qx_format.c:5265-5285), by every wave of
+// the expert kernel on its own (no block barrier).  Lane l holds the logits of experts
+// l and l+64 (double).  The reference picks by softmax probability with repeated
+// strict-> scans (larger first, lower index on ties); the probability is a
+// non-decreasing function of the logit, so picking by logit gives the same experts
+// except where two probabilities round to the same double (a zero margin).  Each round
+// takes the largest f32 key (float rounding is monotone); when several experts share
+// that key the doubles decide, lower index on ties.  The weights p_r / sum_q p_q equal
+// e_r / sum_q e_q with e = exp(l - l_max), since the softmax denominator cancels.
+// ids[r] and w[r] are wave-uniform.
+DEV void wave_top8(double l0, double l1, int E, uint32_t (&ids)[QXG_TOPK], double (&w)[QXG_TOPK]) {
+    const int lane = threadIdx.x & 63;
+    int k0 = lane < E ? order_key(l0) : INT_MIN, k1 = lane + 64 < E ? order_key(l1) : INT_MIN;
+#pragma unroll
+    for (int r = 0; r < QXG_TOPK; ++r) {
+        const int m = wave_max_i(max(k0, k1));
+        const uint64_t b0 = __ballot(k0 == m), b1 = __ballot(k1 == m);
+        uint32_t id = 0;
+        if (m == INT_MIN) {
+            id = 0;                                  // nothing left (non-finite logits)
+        } else if (__popcll(b0) + __popcll(b1) == 1) {
+            id = b0 ? (uint32_t)__builtin_ctzll(b0) : 64u + (uint32_t)__builtin_ctzll(b1);
+        } else {                                     // equal f32 keys: compare the doubles
+            double best = 0.0;
+            bool found = false;
+            for (uint64_t b = b0; b; b &= b - 1) {
+                const int j = __builtin_ctzll(b);
+                const double v = rdlaned(l0, j);
+                if (!found || v > best) { best = v; id = (uint32_t)j; found = true; }
+            }
+            for (uint64_t b = b1; b; b &= b - 1) {
+                const int j = __builtin_ctzll(b);
+                const double v = rdlaned(l1, j);
+                if (!found || v > best) { best = v; id = 64u + (uint32_t)j; found = true; }
+            }
+        }
+        ids[r] = id;
+        if (m != INT_MIN && lane == (int)(id & 63u)) {
+            if (id < 64u) k0 = INT_MIN; else k1 = INT_MIN;
+        }
+    }
+    // lane q < 8 takes the logit of pick q; e_q = exp(l_q - l_0), l_0 the largest
+    double lq = 0.0;
+#pragma unroll
+    for (int q = 0; q < QXG_TOPK; ++q) {
+        const double v = ids[q] < 64u ? rdlaned(l0, (int)ids[q]) : rdlaned(l1, (int)(ids[q] - 64u));
+        if (lane == q) lq = v;
+    }
+    const double lmax = rdlaned(lq, 0);
+    const double eq = lane < QXG_TOPK ? exp(lq - lmax) : 0.0;
+    double sel = 0.0;
+#pragma unroll
+    for (int q = 0; q < QXG_TOPK; ++q) sel += rdlaned(eq, q);   // rank order, as the reference
+    const double wq = eq / sel;
+#pragma unroll
+    for (int q = 0; q < QXG_TOPK; ++q) w[q] = rdlaned(wq, q);
+}
+}  // namespace
 
 // gate/up IQ2_XS (2048 -> 768) for the 8 routed experts (ids from st) + SwiGLU
 // h[r][i] = (float)(silu((double)g) * (double)u) (src/qx_format.c:5298, 2511-2513).
@@ -814,7 +828,8 @@ extern "C" __global__ __launch_bounds__(256) void qxk_router(const float *x, con
 template <int UPW>
 __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *norm_w,
         const uint8_t *g_qs, const uint8_t *g_sc, const uint16_t *g_d,
-        const uint8_t *u_qs, const uint8_t *u_sc, const uint16_t *u_d, Tables T, const DevState *st, float *h) {
+        const uint8_t *u_qs, const uint8_t *u_sc, const uint16_t *u_d, Tables T, const double *logits,
+        uint32_t experts, DevState *st, float *h) {
     __shared__ uint4 s_g2[512];
     __shared__ uint2 s_sel[128];
     __shared__ uint32_t s_dig[64 * DIG_STRIDE];
@@ -822,13 +837,31 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int b = lane >> 3, ib = lane & 7;
     const int u0 = (blockIdx.x * 4 + wave) * UPW;   // grid covers exactly 8*768 units
+    const int E = (int)experts;
     QXG_MARK(1, 0);
-    // the expert id heads the longest chain (id -> weights): load it first
-    const uint32_t e = __builtin_amdgcn_readfirstlane(st->moe_ids[u0 / QXG_FFN]);   // 4 | 768: one expert per wave
+    // the router logits head the longest chain (logits -> top-8 -> weights): loaded first
+    const double l0 = lane < E ? logits[lane] : 0.0, l1 = lane + 64 < E ? logits[lane + 64] : 0.0;
     DigIn<2048, true> din;
     digits_load(x, norm_w, din);
     const uint4 t0 = T.g2[tid], t1 = T.g2[tid + 256];
     const uint2 t2 = T.sel[tid & 127];
+    QXG_ANCHOR(l1);
+    QXG_MARK(1, 5);
+    uint32_t ids[QXG_TOPK];
+    double wts[QXG_TOPK];
+    wave_top8(l0, l1, E, ids, wts);
+    QXG_MARK(1, 6);
+#pragma unroll
+    for (int q = 0; q < QXG_TOPK; ++q) ids[q] = ids[q] < experts ? ids[q] : 0u;   // never address past the experts
+    if (blockIdx.x == 0 && wave == 0) {   // the down kernel reads ids and renormalised weights from st
+#pragma unroll
+        for (int q = 0; q < QXG_TOPK; ++q)
+            if (lane == q) { st->moe_ids[q] = ids[q]; st->moe_w[q] = wts[q]; }
+    }
+    uint32_t e = ids[0];
+#pragma unroll
+    for (int q = 1; q < QXG_TOPK; ++q) if (u0 / QXG_FFN == q) e = ids[q];   // 4 | 768: one expert per wave
+    e = __builtin_amdgcn_readfirstlane(e);
     uint2 gq[UPW], uq[UPW];
     uint32_t gs[UPW], us[UPW], gd[UPW], ud[UPW];
 #pragma unroll
@@ -843,6 +876,7 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
         ud[uu] = u_d[blk];
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
+    QXG_MARK(1, 7);
     s_g2[tid] = t0;
     s_g2[tid + 256] = t1;
     if (tid < 128) s_sel[tid] = t2;
@@ -1189,10 +1223,10 @@ void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, flo
     qx_launch(qxk_oproj<RPW>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, t, ctxv, o->p0, o->p1, x, dump);
 }
 void qxl_gate_up(hipStream_t s, const float *x, const float *nw, const QTensor *g, const QTensor *u, Tables T,
-                 const DevState *st, float *h, Timer t) {
+                 const double *logits, uint32_t experts, DevState *st, float *h, Timer t) {
     constexpr int UPW = 4;
     qx_launch(qxk_gate_up<UPW>, dim3(QXG_TOPK * QXG_FFN / (4 * UPW)), dim3(256), 0, s, t, x, nw,
-                       g->p0, g->p1, g->d, u->p0, u->p1, u->d, T, st, h);
+                       g->p0, g->p1, g->d, u->p0, u->p1, u->d, T, logits, experts, st, h);
 }
 void qxl_down(hipStream_t s, const float *h, const QTensor *d, Tables T, const DevState *st, float *x, float *dump, Timer t) {
     constexpr int RPW = 2;

@@ -80,6 +80,51 @@ def test_moe_block_config2(ctx, layer_model):
     om.close()
 
 
+def _tensor_span(path, name):
+    """(offset, size) of a tensor in a QXF1 file (header and 208-byte directory entries)."""
+    raw = np.fromfile(path, np.uint8)
+    n = int(raw[16:20].view(np.uint32)[0])
+    d0 = int(raw[24:32].view(np.uint64)[0])
+    for i in range(n):
+        e = raw[d0 + 208 * i: d0 + 208 * (i + 1)]
+        if bytes(e[:96]).split(b"\0")[0].decode() == name:
+            return int(e[144:152].view(np.uint64)[0]), int(e[152:160].view(np.uint64)[0])
+    raise KeyError(name)
+
+
+def test_moe_router_ties(ctx, tmp_path):
+    """Router rows copied so that experts tie exactly (equal logits: the lower index is
+    picked first) or nearly (one weight 1 ulp apart: equal f32 keys, different doubles)."""
+    p = tmp_path / "ties.qxf"
+    qxg.generate_model(p, layers=1, vocab=1024, experts=128, embedding=True, head=True, seed=22)
+    x = seeded_normal(2)
+    om = qxo.Model(p)
+    _, _, oids, _ = om.moe_layer(0, x)
+    om.close()
+    a, b = int(oids[0]), int(oids[2])
+    off, size = _tensor_span(p, "blk.0.ffn_gate_inp.weight")
+    mm = np.memmap(p, np.uint8, mode="r+", offset=off, shape=(size,))
+    router = mm.view(np.float32).reshape(128, 2048)
+    for dst in sorted({0, 127, (a + 1) % 128, (a + 40) % 128} - {a, b}):
+        router[dst] = router[a]                       # exact ties with the top expert
+    near = (b + 64) % 128
+    if near not in (a, b, 0, 127, (a + 1) % 128, (a + 40) % 128):
+        router[near] = router[b]
+        router[near, 7] = np.nextafter(router[b, 7], np.float32(np.inf))   # a near tie
+    mm.flush()
+    del router, mm
+    ctx.load(p, verify=False)
+    om = qxo.Model(p)
+    for seed in (2, 5):
+        xs = seeded_normal(seed)
+        y, moe, ids, w = ctx.moe_layer(0, xs)
+        oy, omoe, oids2, ow = om.moe_layer(0, xs)
+        assert list(ids) == list(oids2), (seed, list(ids), list(oids2))
+        assert np.allclose(w, ow, rtol=1e-9, atol=0)
+        assert rel_l2(moe, omoe) <= REL_L2
+    om.close()
+
+
 @pytest.mark.parametrize("pos,ctx_tokens", [(0, 2048), (5, 2048), (127, 2048), (128, 2048), (130, 2048),
                                             (2047, 2048), (4095, 4096)])
 def test_attention_block_config3(ctx, layer_model, pos, ctx_tokens):
