@@ -34,6 +34,8 @@ KERNEL_BYTES = {
     "qkv": (4096 + 512 + 512) * 8 * 136 + 2048 * 4 * 2 + 5120 * 4,
     "oproj": 2048 * 16 * 136 + 4096 * 4 + 2048 * 4 * 2,
     "head": HEAD_BYTES + 2048 * 4 * 2 + VOCAB * 4,
+    # the persistent layer kernel: all 48 layers of one token (KV reads added per position)
+    "layers": LAYERS * LAYER_BYTES + 2048 * 4 * 2,
 }
 
 
@@ -100,7 +102,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--roofline-kernel", default="gate_up", choices=sorted(KERNEL_BYTES))
+    ap.add_argument("--roofline-kernel", default=None, choices=sorted(KERNEL_BYTES),
+                    help="kernel timed in situ for the roofline (default: layers on the persistent path, else gate_up)")
+    ap.add_argument("--layer-path", type=int, default=0, choices=[0, 1],
+                    help="0: one kernel per phase; 1: the persistent layer kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=25.0)
     ap.add_argument("--seed", type=int, default=1)
@@ -126,6 +131,9 @@ def main():
     model = qxg.MemModel(LAYERS, VOCAB, EXPERTS, True, True, seed=args.seed)
     log(f"generated the {LAYERS}-layer model in memory in {time.perf_counter() - t0:.1f} s ({model.path})")
     ctx = qxg.Context(0)
+    ctx.set_layer_path(args.layer_path)
+    if args.roofline_kernel is None:
+        args.roofline_kernel = "layers" if args.layer_path else "gate_up"
     t0 = time.perf_counter()
     info = ctx.load(model.path, verify=False)
     log(f"uploaded {info.tensors} tensors, {info.tensor_bytes / 1e9:.3f} GB in {time.perf_counter() - t0:.1f} s")
@@ -159,6 +167,8 @@ def main():
     tok_s = args.steps / wall2
     avg_kernel_s = kern_ms / 1e3 / max(launches, 1)
     kb = KERNEL_BYTES[args.roofline_kernel]
+    if args.roofline_kernel == "layers":   # plus the INT8 KV rows the attention reads at positions 8..8+K-1
+        kb += kv_bytes(prompt_len, args.steps) // args.steps
     achieved = kb / avg_kernel_s / 1e9
     token_bytes = TOKEN_BYTES + kv_bytes(prompt_len, args.steps) / args.steps
     out = {
@@ -178,7 +188,8 @@ def main():
                                "greedy tokens after an 8-token prompt, INT8 KV",
                    "layers": LAYERS, "vocab": VOCAB, "experts": EXPERTS, "top_k": 8, "prompt_tokens": prompt_len,
                    "quant_mix": "IQ4_XS attn, IQ2_XS gate/up, IQ3_XXS down, Q6_K head, Q4_K embedding",
-                   "kv": "int8", "parallelism": "none (1 GPU)"},
+                   "kv": "int8", "parallelism": "none (1 GPU)",
+                   "layer_path": "persistent" if args.layer_path else "per_phase"},
         "roofline": {"bound": "hbm", "kernel": args.roofline_kernel, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(args.roofline_kernel), "bytes_per_launch": kb, "avg_launch_us": round(avg_kernel_s * 1e6, 3),

@@ -111,6 +111,13 @@ int qxg_moe_layer(qxg_ctx *ctx, uint32_t layer, const float *ffn_inp, float *lay
 int qxg_final_head(qxg_ctx *ctx, const float *residual, float *norm_out, float *logits, uint32_t top_n,
                    uint32_t *top_ids, double *top_logits, char *err, uint64_t err_len);
 
+/* How the layers of a token are launched (no reference counterpart: the reference
+ * runs one thread on the CPU).  0: one kernel per phase, six per layer; 1: one
+ * persistent kernel for all layers of the token, one workgroup per CU, phases handed
+ * over through epoch-tagged device words.  Both give the same results to the stated
+ * tolerance; the default is 0.  Drops the recorded decode graph. */
+int qxg_set_layer_path(qxg_ctx *ctx, int persistent);
+
 /* ---- measurement (no reference counterpart: the reference times with clock(),
  *      src/qx_format.c:6245, 6642-6653) ---- */
 

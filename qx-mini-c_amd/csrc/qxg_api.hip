@@ -19,6 +19,7 @@ __global__ void qxk_router(const float *, const float *, const float *, uint32_t
 __global__ void qxk_topk(const float *, uint32_t, uint32_t, float *, uint32_t *, float *, uint32_t *, uint32_t *,
                          DevState *);
 __global__ void qxk_advance(DevState *);
+__global__ void qxk_layers(QxPArgs);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
                             uint64_t, float *);
 __global__ void qxk_repack(uint32_t, const uint8_t *, uint64_t, uint8_t *, uint8_t *, uint8_t *, uint16_t *);
@@ -96,6 +97,12 @@ struct qxg_ctx {
     uint64_t staging_bytes = 0;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     KernelTiming kt;
+    // persistent layer kernel: per-layer pointer table, tagged exchange buffers, abort flag
+    bool persist = false;            // layer path: persistent kernel (true) or one kernel per phase
+    std::vector<void *> arenas;      // per-plane arenas of all layers' weights
+    QxPlane planes[PL_COUNT] = {};
+    uint64_t *xch = nullptr;
+    uint32_t *abort = nullptr;
     // one decode step (embed .. head, top-1, step advance) recorded once and replayed
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -239,15 +246,67 @@ void launch_head(qxg_ctx *c, uint32_t top_n, float *norm_dump) {
                        c->cand_i, c->top_v, c->top_i, c->tokens, c->st);
 }
 
+// Sizes of the tagged exchange buffers (per slot; two slots each, layer parity).
+constexpr uint64_t XCH_XA = 2048, XCH_XB = 2048, XCH_QKV = 5120, XCH_CX = 4096, XCH_LG = 256,
+                   XCH_HB = QXG_TOPK * QXG_FFN;
+constexpr uint64_t XCH_TOTAL = 2 * (XCH_XA + XCH_XB + XCH_QKV + XCH_CX + XCH_LG + XCH_HB);
+constexpr uint64_t PERSIST_TIMEOUT_TICKS = 200000000ull;   // 2 s of the 100 MHz wall clock
+
+struct Dumps {
+    float *layer = nullptr, *attn = nullptr, *moe = nullptr, *vcur = nullptr, *ctx = nullptr;
+};
+
+// Sub-layers [s0, s1) of the token in one persistent launch (2l: attention half of
+// layer l, 2l+1: its MoE half), residual x_in -> x_out (device buffers).
+void launch_layers(qxg_ctx *c, uint32_t s0, uint32_t s1, const float *x_in, float *x_out, const Dumps &d) {
+    QxPArgs a{};
+    for (int i = 0; i < PL_COUNT; ++i) a.P[i] = c->planes[i];
+    a.s0 = s0; a.s1 = s1;
+    a.experts = c->experts;
+    a.ctx = c->kv_ctx;
+    a.T = c->T;
+    a.kc = c->kc; a.vc = c->vc; a.ks = c->ks; a.vs = c->vs;
+    a.st_w = c->st;
+    uint64_t *p = c->xch;
+    a.xa = p; p += 2 * XCH_XA;
+    a.xb = p; p += 2 * XCH_XB;
+    a.qkv = p; p += 2 * XCH_QKV;
+    a.cx = p; p += 2 * XCH_CX;
+    a.lg = p; p += 2 * XCH_LG;
+    a.hb = p;
+    a.x_in = x_in; a.x_out = x_out;
+    a.d_layer = d.layer; a.d_attn = d.attn; a.d_moe = d.moe; a.d_vcur = d.vcur; a.d_ctx = d.ctx;
+    a.abort = c->abort;
+    a.timeout = PERSIST_TIMEOUT_TICKS;
+    a.sqrt_hd = std::sqrt(128.0);
+    qx_launch(qxk_layers, dim3(QXG_PBLOCKS), dim3(256), 0, c->s, timer_for(c, 7), a);
+}
+
 void launch_step(qxg_ctx *c, uint32_t top_n, bool dump_layers) {
     hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
-    for (uint32_t l = 0; l < c->layers; ++l) {
-        launch_attention(c, l, c->x, nullptr, nullptr);
-        launch_moe(c, l, c->x, nullptr);
-        if (dump_layers)
-            (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * sizeof(float), hipMemcpyDeviceToDevice, c->s);
+    Dumps d;
+    if (dump_layers) d.layer = c->layer_dump;
+    if (c->persist) {
+        if (c->layers) launch_layers(c, 0, 2 * c->layers, c->x, c->x, d);
+    } else {
+        for (uint32_t l = 0; l < c->layers; ++l) {
+            launch_attention(c, l, c->x, nullptr, nullptr);
+            launch_moe(c, l, c->x, nullptr);
+            if (dump_layers)
+                (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * sizeof(float), hipMemcpyDeviceToDevice, c->s);
+        }
     }
     if (c->head) launch_head(c, top_n, nullptr);
+}
+
+// A persistent launch whose waits timed out leaves the abort flag set: report and clear it.
+bool check_abort(qxg_ctx *c, char *err, uint64_t n) {
+    uint32_t f = 0;
+    if (!hip_ok(hipMemcpy(&f, c->abort, 4, hipMemcpyDeviceToHost), err, n, "abort flag")) return false;
+    if (!f) return true;
+    (void)hipMemset(c->abort, 0, 4);
+    set_err(err, n, "persistent layer kernel: a wait timed out (a workgroup never produced its phase output)");
+    return false;
 }
 
 bool check_ready(qxg_ctx *c, bool need_kv, char *err, uint64_t n) {
@@ -259,12 +318,92 @@ bool check_ready(qxg_ctx *c, bool need_kv, char *err, uint64_t n) {
 
 bool finish(qxg_ctx *c, char *err, uint64_t n) {
     if (!hip_ok(hipGetLastError(), err, n, "launch")) return false;
-    return hip_ok(hipStreamSynchronize(c->s), err, n, "stream");
+    if (!hip_ok(hipStreamSynchronize(c->s), err, n, "stream")) return false;
+    return !c->abort || check_abort(c, err, n);
 }
 
 bool read_state(qxg_ctx *c, DevState &h, char *err, uint64_t n) {
     return hip_ok(hipMemcpyAsync(&h, c->st, sizeof(h), hipMemcpyDeviceToHost, c->s), err, n, "state read") &&
            hip_ok(hipStreamSynchronize(c->s), err, n, "stream");
+}
+// Every per-layer weight plane (norms, router, the quantized planes of Q/K/V/O and
+// of the expert tensors) is copied into one arena per plane kind, layers back to
+// back at a 256-byte-aligned stride; the tensors are re-pointed into the arenas and
+// their own allocations released.  The decode kernel then forms layer l's pointers
+// as base + l * stride from its arguments.
+bool build_arenas(qxg_ctx *c, char *err, uint64_t n) {
+    const uint32_t L = c->layers ? c->layers : (uint32_t)c->L.size();
+    std::vector<void *> old = std::move(c->arenas);
+    c->arenas.clear();
+    struct Src { const uint8_t *p; uint64_t bytes; };
+    auto src = [&](int id, uint32_t l) -> Src {
+        const LayerW &w = c->L[l];
+        const uint64_t E = c->experts;
+        switch (id) {
+        case PL_ATTN_NORM: return {(const uint8_t *)w.attn_norm, 2048 * 4};
+        case PL_Q_NORM: return {(const uint8_t *)w.q_norm, 128 * 4};
+        case PL_K_NORM: return {(const uint8_t *)w.k_norm, 128 * 4};
+        case PL_FFN_NORM: return {(const uint8_t *)w.ffn_norm, 2048 * 4};
+        case PL_ROUTER: return {(const uint8_t *)w.router, E * 2048 * 4};
+        case PL_Q_QS: return {w.wq->p0, w.wq->nblocks * 128};
+        case PL_Q_META: return {w.wq->p1, w.wq->nblocks * 8};
+        case PL_K_QS: return {w.wk->p0, w.wk->nblocks * 128};
+        case PL_K_META: return {w.wk->p1, w.wk->nblocks * 8};
+        case PL_V_QS: return {w.wv->p0, w.wv->nblocks * 128};
+        case PL_V_META: return {w.wv->p1, w.wv->nblocks * 8};
+        case PL_O_QS: return {w.wo->p0, w.wo->nblocks * 128};
+        case PL_O_META: return {w.wo->p1, w.wo->nblocks * 8};
+        case PL_G_QS: return {w.gate->p0, w.gate->nblocks * 64};
+        case PL_G_SC: return {w.gate->p1, w.gate->nblocks * 8};
+        case PL_G_D: return {(const uint8_t *)w.gate->d, w.gate->nblocks * 2};
+        case PL_U_QS: return {w.up->p0, w.up->nblocks * 64};
+        case PL_U_SC: return {w.up->p1, w.up->nblocks * 8};
+        case PL_U_D: return {(const uint8_t *)w.up->d, w.up->nblocks * 2};
+        case PL_D_QS: return {w.down->p0, w.down->nblocks * 64};
+        case PL_D_AUX: return {w.down->p1, w.down->nblocks * 32};
+        default: return {(const uint8_t *)w.down->d, w.down->nblocks * 2};
+        }
+    };
+    for (int id = 0; id < PL_COUNT; ++id) {
+        const uint64_t stride = align256(src(id, 0).bytes);
+        uint8_t *ar = nullptr;
+        if (!hip_ok(hipMalloc(&ar, stride * L), err, n, "weight arena")) return false;
+        c->arenas.push_back(ar);
+        for (uint32_t l = 0; l < L; ++l) {
+            const Src sp = src(id, l);
+            if (!hip_ok(hipMemcpyAsync(ar + l * stride, sp.p, sp.bytes, hipMemcpyDeviceToDevice, c->s), err, n, "weight arena"))
+                return false;
+        }
+        c->planes[id] = {ar, stride};
+    }
+    if (!hip_ok(hipStreamSynchronize(c->s), err, n, "weight arena")) return false;
+    auto at = [&](int id, uint32_t l) { return c->planes[id].base + (uint64_t)l * c->planes[id].stride; };
+    for (uint32_t l = 0; l < L; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        struct { const char *sfx; int p0, p1, d; } q[] = {
+            {"attn_q.weight", PL_Q_QS, PL_Q_META, -1}, {"attn_k.weight", PL_K_QS, PL_K_META, -1},
+            {"attn_v.weight", PL_V_QS, PL_V_META, -1}, {"attn_output.weight", PL_O_QS, PL_O_META, -1},
+            {"ffn_gate_exps.weight", PL_G_QS, PL_G_SC, PL_G_D}, {"ffn_up_exps.weight", PL_U_QS, PL_U_SC, PL_U_D},
+            {"ffn_down_exps.weight", PL_D_QS, PL_D_AUX, PL_D_D}, {"attn_norm.weight", PL_ATTN_NORM, -1, -1},
+            {"attn_q_norm.weight", PL_Q_NORM, -1, -1}, {"attn_k_norm.weight", PL_K_NORM, -1, -1},
+            {"ffn_norm.weight", PL_FFN_NORM, -1, -1}, {"ffn_gate_inp.weight", PL_ROUTER, -1, -1}};
+        for (auto &e : q) {
+            QTensor &t = c->tens[p + e.sfx];
+            free_tensor(t);
+            t.p0 = at(e.p0, l);
+            t.p1 = e.p1 >= 0 ? at(e.p1, l) : nullptr;
+            t.p2 = nullptr;
+            t.d = e.d >= 0 ? (const uint16_t *)at(e.d, l) : nullptr;
+        }
+        LayerW &w = c->L[l];
+        w.attn_norm = (const float *)at(PL_ATTN_NORM, l);
+        w.q_norm = (const float *)at(PL_Q_NORM, l);
+        w.k_norm = (const float *)at(PL_K_NORM, l);
+        w.ffn_norm = (const float *)at(PL_FFN_NORM, l);
+        w.router = (const float *)at(PL_ROUTER, l);
+    }
+    for (void *pp : old) (void)hipFree(pp);
+    return true;
 }
 }  // namespace
 
@@ -282,6 +421,16 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         if (err && err_len) snprintf(err, (size_t)err_len, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
         return 0;
+    }
+    {   // the persistent layer kernel keeps one workgroup resident on each of QXG_PBLOCKS CUs
+        int occ = 0;
+        if (prop.multiProcessorCount < QXG_PBLOCKS ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_layers, 256, 0) != hipSuccess || occ < 1) {
+            if (err && err_len)
+                snprintf(err, (size_t)err_len, "device %d has %d CUs; the persistent decode kernel needs %d resident workgroups",
+                         device, prop.multiProcessorCount, QXG_PBLOCKS);
+            return 0;
+        }
     }
     qxg_ctx *c = new qxg_ctx();
     c->device = device;
@@ -311,6 +460,11 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
          hip_ok(hipMemcpy(c->T.rope_sin, rs.data(), rs.size() * sizeof(double), hipMemcpyHostToDevice), err, err_len, "tables");
     ok = ok && hip_ok(hipMalloc(&c->st, sizeof(DevState)), err, err_len, "state") &&
          hip_ok(hipMemset(c->st, 0, sizeof(DevState)), err, err_len, "state");
+    // tagged exchange buffers start at epoch 0, which no launch uses
+    ok = ok && hip_ok(hipMalloc(&c->xch, XCH_TOTAL * 8), err, err_len, "exchange buffers") &&
+         hip_ok(hipMemset(c->xch, 0, XCH_TOTAL * 8), err, err_len, "exchange buffers") &&
+         hip_ok(hipMalloc(&c->abort, 4), err, err_len, "abort flag") &&
+         hip_ok(hipMemset(c->abort, 0, 4), err, err_len, "abort flag");
     ok = ok && hip_ok(hipEventCreate(&c->e0), err, err_len, "event") && hip_ok(hipEventCreate(&c->e1), err, err_len, "event");
     if (!ok) { qxg_close(c); return 0; }
     *out = c;
@@ -325,8 +479,10 @@ void qxg_close(qxg_ctx *c) {
     for (auto &kv : c->tens) free_tensor(kv.second);
     void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
-                    c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging};
+                    c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging,
+                    c->xch, c->abort};
     for (void *p : bufs) if (p) (void)hipFree(p);
+    for (void *p : c->arenas) (void)hipFree(p);
     for (hipEvent_t e : c->kt.ev) (void)hipEventDestroy(e);
     if (c->e0) (void)hipEventDestroy(c->e0);
     if (c->e1) (void)hipEventDestroy(c->e1);
@@ -430,6 +586,7 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i)
         if (!hip_ok(hipMalloc(bufs[i], sizes[i]), err, err_len, "work buffers")) return 0;
     if (!hip_ok(hipMemset(c->tokens, 0, sizes[15]), err, err_len, "work buffers")) return 0;
+    if (layers && !build_arenas(c, err, err_len)) return 0;
     c->bound = true;
     return 1;
 }
@@ -511,11 +668,17 @@ int qxg_decode_token(qxg_ctx *c, uint32_t token, uint32_t position, int run_head
     (void)hipMemcpyAsync(c->tokens, &token, 4, hipMemcpyHostToDevice, c->s);
     write_state(c, position, 0, run_head ? 1 : 2, 0);
     hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
-    for (uint32_t l = 0; l < c->layers; ++l) {
-        launch_attention(c, l, c->x, nullptr, nullptr);
-        launch_moe(c, l, c->x, nullptr);
-        if (layer_out)
-            (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * 4, hipMemcpyDeviceToDevice, c->s);
+    Dumps d;
+    if (layer_out) d.layer = c->layer_dump;
+    if (c->persist) {
+        if (c->layers) launch_layers(c, 0, 2 * c->layers, c->x, c->x, d);
+    } else {
+        for (uint32_t l = 0; l < c->layers; ++l) {
+            launch_attention(c, l, c->x, nullptr, nullptr);
+            launch_moe(c, l, c->x, nullptr);
+            if (layer_out)
+                (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * 4, hipMemcpyDeviceToDevice, c->s);
+        }
     }
     if (run_head) launch_head(c, top_n, nullptr);
     if (!finish(c, err, err_len)) return 0;
@@ -626,7 +789,13 @@ int qxg_attention_layer(qxg_ctx *c, uint32_t layer, uint32_t position, const flo
     (void)hipSetDevice(c->device);
     (void)hipMemcpyAsync(c->x, x_in, 2048 * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, position, 0, 1, 1);
-    launch_attention(c, layer, c->x, c->attn, c->vcur);
+    if (c->persist) {
+        Dumps d;
+        d.attn = c->attn; d.vcur = c->vcur; d.ctx = c->ctxv;
+        launch_layers(c, 2 * layer, 2 * layer + 1, c->x, c->x, d);
+    } else {
+        launch_attention(c, layer, c->x, c->attn, c->vcur);
+    }
     if (!finish(c, err, err_len)) return 0;
     if (attn_out && !hip_ok(hipMemcpy(attn_out, c->attn, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
     if (kqv_out && !hip_ok(hipMemcpy(kqv_out, c->ctxv, 4096 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
@@ -641,7 +810,13 @@ int qxg_moe_layer(qxg_ctx *c, uint32_t layer, const float *ffn_inp, float *layer
     (void)hipSetDevice(c->device);
     (void)hipMemcpyAsync(c->x, ffn_inp, 2048 * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, 0, 0, 1, 1);
-    launch_moe(c, layer, c->x, c->moe);
+    if (c->persist) {
+        Dumps d;
+        d.moe = c->moe;
+        launch_layers(c, 2 * layer + 1, 2 * layer + 2, c->x, c->x, d);
+    } else {
+        launch_moe(c, layer, c->x, c->moe);
+    }
     if (!finish(c, err, err_len)) return 0;
     DevState h;
     if (!read_state(c, h, err, err_len)) return 0;
@@ -718,6 +893,17 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
 }
 
 uint64_t qxg_device_bytes(const qxg_ctx *c) { return c ? c->dev_bytes : 0; }
+
+int qxg_set_layer_path(qxg_ctx *c, int persistent) {
+    if (!c) return 0;
+    if (c->persist != (persistent != 0)) {
+        (void)hipSetDevice(c->device);
+        if (c->s) (void)hipStreamSynchronize(c->s);
+        drop_graph(c);
+        c->persist = persistent != 0;
+    }
+    return 1;
+}
 
 /* In-situ timing of one kernel kind inside qxg_generate / qxg_decode_token:
  * an event pair is recorded around every launch of kernel `which` (numbering of

@@ -1,0 +1,507 @@
+// Device helpers shared by the decode kernels: exact fp16 decode, DPP lane
+// exchanges, the activation digit scheme and the per-format sub-block dots,
+// per-head norm/RoPE and the router top-8.  Header-only (internal linkage).
+#pragma once
+#include "qxg_internal.h"
+#include <climits>
+
+#define DEV __device__ __forceinline__
+
+namespace {
+
+// ---------------------------------------------------------------- helpers
+// reference qx_fp16_to_f32 (src/qx_format.c:1854-1876): exact, exponent 31 -> +-65504
+DEV float fp16_exact(uint32_t h) {
+    uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu, bits;
+    if (e == 0) {
+        if (m == 0) bits = sign;
+        else {
+            int sh = __builtin_clz(m) - 21;          // shifts until bit 10 is set
+            bits = sign | ((uint32_t)(113 - sh) << 23) | (((m << sh) & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x477fe000u;
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+DEV uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
+
+// ---- DPP lane exchanges (VALU latency; __shfl_xor lowers to ds_bpermute through LDS).
+// quad_perm xor1 = [1,0,3,2], xor2 = [2,3,0,1]; row_ror:4/8 rotate within a 16-lane
+// row; row_half_mirror pairs lane i with 7-i inside each group of 8.
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128, DPP_HALF_MIRROR = 0x141 };
+
+template <int CTRL>
+DEV float dppf(float v) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false)); }
+template <int CTRL>
+DEV int dppi(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+template <int CTRL>
+DEV double dppd(double v) {
+    const int2 h = *reinterpret_cast<int2 *>(&v);
+    int2 r;
+    r.x = __builtin_amdgcn_update_dpp(0, h.x, CTRL, 0xf, 0xf, false);
+    r.y = __builtin_amdgcn_update_dpp(0, h.y, CTRL, 0xf, 0xf, false);
+    return *reinterpret_cast<double *>(&r);
+}
+DEV float rdlanef(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+DEV double rdlaned(double v, int l) {
+    const int2 h = *reinterpret_cast<int2 *>(&v);
+    int2 r;
+    r.x = __builtin_amdgcn_readlane(h.x, l);
+    r.y = __builtin_amdgcn_readlane(h.y, l);
+    return *reinterpret_cast<double *>(&r);
+}
+// sum over each 16-lane row, result in every lane of the row
+DEV double row16_sum_d(double v) {
+    v += dppd<DPP_XOR1>(v); v += dppd<DPP_XOR2>(v); v += dppd<DPP_ROR4>(v); v += dppd<DPP_ROR8>(v);
+    return v;
+}
+// wave totals, uniform (rows combined in lane order 0, 16, 32, 48)
+DEV double wave_total_d(double v) {
+    v = row16_sum_d(v);
+    return (rdlaned(v, 0) + rdlaned(v, 16)) + (rdlaned(v, 32) + rdlaned(v, 48));
+}
+DEV double wave_max_d(double v) {
+    v = fmax(v, dppd<DPP_XOR1>(v)); v = fmax(v, dppd<DPP_XOR2>(v));
+    v = fmax(v, dppd<DPP_ROR4>(v)); v = fmax(v, dppd<DPP_ROR8>(v));
+    return fmax(fmax(rdlaned(v, 0), rdlaned(v, 16)), fmax(rdlaned(v, 32), rdlaned(v, 48)));
+}
+
+// 32 activations of one group as three int8 digit planes and a power-of-two scale
+struct Dig {
+    uint32_t h[8], m[8], l[8];
+    float s;
+};
+
+DEV float combine(int aH, int aM, int aL) {
+    return fmaf((float)aH, 65536.0f, fmaf((float)aM, 256.0f, (float)aL));
+}
+
+// IQ4_XS codebook (reference qx_kvalues_iq4nl, src/qx_format.c:2032) as 4 byte-lanes
+constexpr int8_t KV[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+constexpr uint32_t kvw(int i) {
+    return (uint32_t)(uint8_t)KV[i] | ((uint32_t)(uint8_t)KV[i + 1] << 8) | ((uint32_t)(uint8_t)KV[i + 2] << 16) |
+           ((uint32_t)(uint8_t)KV[i + 3] << 24);
+}
+
+// 4 nibbles (one per byte, values 0..15) -> 4 signed codebook bytes
+DEV uint32_t kv_lookup(uint32_t n) {
+    const uint32_t n7 = n & 0x07070707u;
+    const uint32_t lo = perm(kvw(4), kvw(0), n7);
+    const uint32_t hi = perm(kvw(12), kvw(8), n7);
+    return perm(hi, lo, ((n >> 1) & 0x04040404u) | 0x03020100u);
+}
+
+// ---------------------------------------------------------------- per-format sub-block dots
+// IQ4_XS sub-block ib (32 values): codes kvalue[nibble], scale d*(ls-32)
+DEV float dot_iq4(uint4 qs, uint2 meta, int ib, const Dig &g) {
+    const uint32_t sh = meta.x >> 16, sl = meta.y;
+    const int ls = ((sl >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
+    const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+    int aH = 0, aM = 0, aL = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t wlo = kv_lookup(q[k] & 0x0f0f0f0fu);
+        const uint32_t whi = kv_lookup((q[k] >> 4) & 0x0f0f0f0fu);
+        aH = sdot4(wlo, g.h[k], aH); aH = sdot4(whi, g.h[4 + k], aH);
+        aM = sdot4(wlo, g.m[k], aM); aM = sdot4(whi, g.m[4 + k], aM);
+        aL = sdot4(wlo, g.l[k], aL); aL = sdot4(whi, g.l[4 + k], aL);
+    }
+    const float dl = fp16_exact(meta.x & 0xffffu) * (float)(ls - 32);
+    return (dl * g.s) * combine(aH, aM, aL);
+}
+
+// IQ2_XS sub-block (32 values = 4 grid entries of 8): halves scaled d*(2s+1)/8
+DEV float dot_iq2(uint2 qs, uint32_t sc, uint32_t d16, const Dig &g, const uint4 *G2, const uint2 *SEL) {
+    const uint32_t qv[4] = {qs.x & 0xffffu, qs.x >> 16, qs.y & 0xffffu, qs.y >> 16};
+    int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const uint4 gg = G2[qv[l] & 511u];
+        const uint2 sl = SEL[qv[l] >> 9];
+        const uint32_t w0 = perm(gg.z, gg.x, sl.x), w1 = perm(gg.w, gg.y, sl.y);
+        if (l < 2) {
+            h0 = sdot4(w0, g.h[2 * l], h0); h0 = sdot4(w1, g.h[2 * l + 1], h0);
+            m0 = sdot4(w0, g.m[2 * l], m0); m0 = sdot4(w1, g.m[2 * l + 1], m0);
+            l0 = sdot4(w0, g.l[2 * l], l0); l0 = sdot4(w1, g.l[2 * l + 1], l0);
+        } else {
+            h1 = sdot4(w0, g.h[2 * l], h1); h1 = sdot4(w1, g.h[2 * l + 1], h1);
+            m1 = sdot4(w0, g.m[2 * l], m1); m1 = sdot4(w1, g.m[2 * l + 1], m1);
+            l1 = sdot4(w0, g.l[2 * l], l1); l1 = sdot4(w1, g.l[2 * l + 1], l1);
+        }
+    }
+    const int k0 = 2 * (int)(sc & 15u) + 1, k1 = 2 * (int)(sc >> 4) + 1;
+    const float v = combine(k0 * h0 + k1 * h1, k0 * m0 + k1 * m1, k0 * l0 + k1 * l1);
+    return ((fp16_exact(d16) * 0.125f) * g.s) * v;
+}
+
+// IQ3_XXS sub-block: 8 grid indices (4 values each), scale d*(2a+1)/4
+DEV float dot_iq3(uint2 qs, uint32_t aux, uint32_t d16, const Dig &g, const uint2 *G3, const uint2 *SEL) {
+    int aH = 0, aM = 0, aL = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const uint32_t word = l < 2 ? qs.x : qs.y;
+        const uint32_t b1 = (word >> (16 * (l & 1))) & 255u, b2 = (word >> (16 * (l & 1) + 8)) & 255u;
+        const uint2 g1 = G3[b1], g2 = G3[b2];
+        const uint2 sl = SEL[(aux >> (7 * l)) & 127u];
+        const uint32_t w0 = perm(g1.y, g1.x, sl.x), w1 = perm(g2.y, g2.x, sl.y);
+        aH = sdot4(w0, g.h[2 * l], aH); aH = sdot4(w1, g.h[2 * l + 1], aH);
+        aM = sdot4(w0, g.m[2 * l], aM); aM = sdot4(w1, g.m[2 * l + 1], aM);
+        aL = sdot4(w0, g.l[2 * l], aL); aL = sdot4(w1, g.l[2 * l + 1], aL);
+    }
+    const int k = 2 * (int)(aux >> 28) + 1;
+    return ((fp16_exact(d16) * 0.25f) * g.s) * combine(k * aH, k * aM, k * aL);
+}
+
+// Q6_K sub-block ib: values 128h+32k+l (h=ib/4, k=ib%4), two 16-value scale segments.
+// Codes are taken unsigned (0..63); the -32 offset enters through the digit
+// sums bias[seg] = -32 * sum(digits of the segment), precomputed per lane.
+struct Q6Bias { int h[2], m[2], l[2]; };
+
+DEV Q6Bias q6_bias(const Dig &g) {
+    Q6Bias b;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        int sh = 0, sm = 0, sl = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            sh = sdot4(0x01010101u, g.h[4 * s + k], sh);
+            sm = sdot4(0x01010101u, g.m[4 * s + k], sm);
+            sl = sdot4(0x01010101u, g.l[4 * s + k], sl);
+        }
+        b.h[s] = -32 * sh; b.m[s] = -32 * sm; b.l[s] = -32 * sl;
+    }
+    return b;
+}
+
+DEV float dot_q6(uint4 ql0, uint4 ql1, uint4 qh0, uint4 qh1, int sc0, int sc1, uint32_t d16, int ib,
+                 const Dig &g, const Q6Bias &bias) {
+    const int k = ib & 3;
+    const uint32_t shl = 4 * (k >> 1), shh = 2 * k;
+    const uint32_t ql[8] = {ql0.x, ql0.y, ql0.z, ql0.w, ql1.x, ql1.y, ql1.z, ql1.w};
+    const uint32_t qh[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
+    int aH[2] = {bias.h[0], bias.h[1]}, aM[2] = {bias.m[0], bias.m[1]}, aL[2] = {bias.l[0], bias.l[1]};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t u = ((ql[j] >> shl) & 0x0f0f0f0fu) | (((qh[j] >> shh) & 0x03030303u) << 4);
+        const int s = j >> 2;
+        aH[s] = sdot4(u, g.h[j], aH[s]);
+        aM[s] = sdot4(u, g.m[j], aM[s]);
+        aL[s] = sdot4(u, g.l[j], aL[s]);
+    }
+    const float v = combine(sc0 * aH[0] + sc1 * aH[1], sc0 * aM[0] + sc1 * aM[1], sc0 * aL[0] + sc1 * aL[1]);
+    return (fp16_exact(d16) * g.s) * v;
+}
+
+// ---------------------------------------------------------------- prologues
+DEV void load32(const float *p, float *v) {
+    const float4 *q = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 t = q[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+
+// reference qx_apply_f32_rmsnorm (src/qx_format.c:3358-3371): double sum of
+// squares, rms = sqrt(ss/n + 1e-6), y = (float)(x/rms) * w.  The lane holds the
+// 32 values [32*lane, 32*lane+32) of a 2048-vector (already loaded); the wave
+// reduces.  x/rms is formed as x*(1/rms) in double; after the cast to f32 the two
+// differ only when x/rms lies within 2^-53 relative of an f32 rounding boundary.
+DEV void rmsnorm32(float *v, const float *w) {
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ss += (double)v[i] * (double)v[i];
+    ss = wave_total_d(ss);
+    const double inv = 1.0 / sqrt(ss / 2048.0 + 1.0e-6);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = (float)((double)v[i] * inv) * w[i];
+}
+
+
+// ---- block-cooperative activation digits.  The digit planes of all N/32 groups of
+// a vector are computed once per block into LDS (DIG_STRIDE dwords per group: h[8],
+// m[8], l[8], scale bits), 8 consecutive values per thread; the 4 threads of a group
+// form a quad, so the group max is two in-quad DPP exchanges.  With NORM, the vector
+// is first RMS-normalised with weights w (reference src/qx_format.c:3358-3371).
+constexpr int DIG_STRIDE = 28;   // 16-byte aligned rows for ds_read_b128
+
+DEV void digits8(const float *y, float mx, uint32_t &ph0, uint32_t &ph1, uint32_t &pm0, uint32_t &pm1, uint32_t &pl0,
+                 uint32_t &pl1, float &scale) {
+    int e = 0;
+    if (mx > 0.0f) (void)frexpf(mx, &e);
+    scale = mx > 0.0f ? ldexpf(1.0f, e - 22) : 0.0f;
+    uint32_t H[2] = {0, 0}, M[2] = {0, 0}, L[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int X = mx > 0.0f ? (int)rintf(ldexpf(y[i], 22 - e)) : 0;
+        const int l = ((X + 128) & 255) - 128;
+        const int X1 = (X - l) >> 8;
+        const int m = ((X1 + 128) & 255) - 128;
+        const int hh = (X1 - m) >> 8;
+        H[i >> 2] |= (uint32_t)(hh & 255) << (8 * (i & 3));
+        M[i >> 2] |= (uint32_t)(m & 255) << (8 * (i & 3));
+        L[i >> 2] |= (uint32_t)(l & 255) << (8 * (i & 3));
+    }
+    ph0 = H[0]; ph1 = H[1]; pm0 = M[0]; pm1 = M[1]; pl0 = L[0]; pl1 = L[1];
+}
+
+// The vector (and norm weights) as loaded by one thread: 8 consecutive values per
+// chunk.  Kernels issue these loads before their weight loads, so the activation
+// arrives first and the digit work overlaps the weight fetch.
+template <int N, bool NORM>
+struct DigIn {
+    static constexpr int NCH = N / 8, PER = (NCH + 255) / 256;
+    float v[PER][8];
+    float w[NORM ? 8 : 1];
+};
+
+template <int N, bool NORM>
+DEV void digits_load(const float *x, const float *w, DigIn<N, NORM> &in) {
+    using D = DigIn<N, NORM>;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int it = 0; it < D::PER; ++it) {
+        const int c = tid + 256 * it;
+        if (c < D::NCH) {
+            const float4 a = reinterpret_cast<const float4 *>(x)[2 * c], b = reinterpret_cast<const float4 *>(x)[2 * c + 1];
+            in.v[it][0] = a.x; in.v[it][1] = a.y; in.v[it][2] = a.z; in.v[it][3] = a.w;
+            in.v[it][4] = b.x; in.v[it][5] = b.y; in.v[it][6] = b.z; in.v[it][7] = b.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) in.v[it][i] = 0.0f;
+        }
+    }
+    if constexpr (NORM) {
+        static_assert(D::PER == 1, "normalised vectors are 2048 long");
+        const float4 a = reinterpret_cast<const float4 *>(w)[2 * tid], b = reinterpret_cast<const float4 *>(w)[2 * tid + 1];
+        in.w[0] = a.x; in.w[1] = a.y; in.w[2] = a.z; in.w[3] = a.w;
+        in.w[4] = b.x; in.w[5] = b.y; in.w[6] = b.z; in.w[7] = b.w;
+    }
+}
+
+// returns true when every value is finite (block-uniform); ends with a block barrier
+template <int N, bool NORM>
+DEV bool block_digits(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float *norm_out = nullptr) {
+    using D = DigIn<N, NORM>;
+    const int tid = threadIdx.x;
+    if constexpr (NORM) {
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += (double)in.v[0][i] * (double)in.v[0][i];
+        ss = wave_total_d(ss);
+        if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+        __syncthreads();
+        const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+        const double inv = 1.0 / sqrt(tot / (double)N + 1.0e-6);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) in.v[0][i] = (float)((double)in.v[0][i] * inv) * in.w[i];
+        if (norm_out) {
+            reinterpret_cast<float4 *>(norm_out)[2 * tid] = make_float4(in.v[0][0], in.v[0][1], in.v[0][2], in.v[0][3]);
+            reinterpret_cast<float4 *>(norm_out)[2 * tid + 1] = make_float4(in.v[0][4], in.v[0][5], in.v[0][6], in.v[0][7]);
+        }
+    }
+    bool fin = true;
+#pragma unroll
+    for (int it = 0; it < D::PER; ++it) {
+        const int c = tid + 256 * it;
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { fin = fin && isfinite(in.v[it][i]); mx = fmaxf(mx, fabsf(in.v[it][i])); }
+        mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
+        mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
+        if (c < D::NCH) {
+            uint32_t h0, h1, m0, m1, l0, l1;
+            float sc;
+            digits8(in.v[it], isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
+            uint32_t *d = s_dig + (c >> 2) * DIG_STRIDE;
+            const int q = c & 3;
+            *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
+            *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
+            if (q == 0) d[24] = __float_as_uint(sc);
+        }
+    }
+    return __syncthreads_or(!fin) == 0;
+}
+
+DEV void load_dig(const uint32_t *__restrict__ s_dig, int g, Dig &d) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(s_dig + g * DIG_STRIDE);
+    const uint4 a = p[0], b = p[1], c = p[2], e = p[3], f = p[4], k = p[5];
+    d.h[0] = a.x; d.h[1] = a.y; d.h[2] = a.z; d.h[3] = a.w; d.h[4] = b.x; d.h[5] = b.y; d.h[6] = b.z; d.h[7] = b.w;
+    d.m[0] = c.x; d.m[1] = c.y; d.m[2] = c.z; d.m[3] = c.w; d.m[4] = e.x; d.m[5] = e.y; d.m[6] = e.z; d.m[7] = e.w;
+    d.l[0] = f.x; d.l[1] = f.y; d.l[2] = f.z; d.l[3] = f.w; d.l[4] = k.x; d.l[5] = k.y; d.l[6] = k.z; d.l[7] = k.w;
+    d.s = __uint_as_float(s_dig[g * DIG_STRIDE + 24]);
+}
+
+
+DEV uint32_t cur_pos(const DevState *st) { return st->pos0 + st->step; }
+
+// R per-lane partial sums (one per row, R in {1,2,4,8}) reduced over the wave:
+// up to two split rounds inside each quad (a lane keeps half of the rows and adds
+// its partner's half), then row16 sums, then the four rows of the wave through
+// readlane.  out[r] is the total of row r, wave-uniform.
+template <int R>
+DEV void rows_reduce(float (&v)[R], float (&out)[R], int lane) {
+    constexpr int S = R >= 4 ? 2 : (R == 2 ? 1 : 0);   // quad split rounds
+    constexpr int K = R >> S;                          // values left per lane
+    const bool b0 = lane & 1, b1 = (lane >> 1) & 1;
+    if constexpr (S >= 1) {
+        constexpr int half = R / 2;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float send = b0 ? v[i] : v[half + i];
+            const float keep = b0 ? v[half + i] : v[i];
+            v[i] = keep + dppf<DPP_XOR1>(send);
+        }
+    }
+    if constexpr (S >= 2) {
+        constexpr int half = R / 4;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float send = b1 ? v[i] : v[half + i];
+            const float keep = b1 ? v[half + i] : v[i];
+            v[i] = keep + dppf<DPP_XOR2>(send);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        if constexpr (S == 0) { v[i] += dppf<DPP_XOR1>(v[i]); }
+        if constexpr (S <= 1) { v[i] += dppf<DPP_XOR2>(v[i]); }
+        v[i] += dppf<DPP_ROR4>(v[i]);
+        v[i] += dppf<DPP_ROR8>(v[i]);
+    }
+    // lane L (low bits b0,b1) holds rows base..base+K-1 with base = K*(2^(S-1)*b0 + ...)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        int l0, j;
+        if constexpr (S == 0) { l0 = 0; j = r; }
+        else if constexpr (S == 1) { l0 = r / K; j = r % K; }               // b0 = subset
+        else { const int sub = r / K; l0 = (sub >> 1) | ((sub & 1) << 1); j = r % K; }  // subset = 2*b0 + b1
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < K; ++i) if (i == j) t = v[i];
+        out[r] = (rdlanef(t, l0) + rdlanef(t, l0 + 16)) + (rdlanef(t, l0 + 32) + rdlanef(t, l0 + 48));
+    }
+}
+
+
+DEV float block_max256(float v, float *red) {
+    v = fmaxf(v, dppf<DPP_XOR1>(v)); v = fmaxf(v, dppf<DPP_XOR2>(v));
+    v = fmaxf(v, dppf<DPP_ROR4>(v)); v = fmaxf(v, dppf<DPP_ROR8>(v));
+    v = fmaxf(fmaxf(rdlanef(v, 0), rdlanef(v, 16)), fmaxf(rdlanef(v, 32), rdlanef(v, 48)));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// 128 values of one head held as (lane, lane+64) by a wave: per-head RMSNorm then RoPE
+DEV void head_norm_rope_wave(float &x0, float &x1, float w0, float w1, double c, double s) {
+    const double ss = wave_total_d((double)x0 * (double)x0 + (double)x1 * (double)x1);
+    const double inv = 1.0 / sqrt(ss / 128.0 + 1.0e-6);
+    const float n0 = (float)((double)x0 * inv * (double)w0);
+    const float n1 = (float)((double)x1 * inv * (double)w1);
+    x0 = (float)((double)n0 * c - (double)n1 * s);
+    x1 = (float)((double)n0 * s + (double)n1 * c);
+}
+
+// order-preserving unsigned image of a double: a > b  <=>  key(a) > key(b); NaN -> 0,
+// below every number
+DEV uint64_t dkey(double v) {
+    if (v != v) return 0ull;
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+template <int CTRL>
+DEV uint64_t dppu64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+DEV uint64_t rdlaneu64(uint64_t v, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+DEV uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// wave-uniform maximum of a 64-bit key
+DEV uint64_t wave_max_u64(uint64_t v) {
+    v = umax64(v, dppu64<DPP_XOR1>(v)); v = umax64(v, dppu64<DPP_XOR2>(v));
+    v = umax64(v, dppu64<DPP_ROR4>(v)); v = umax64(v, dppu64<DPP_ROR8>(v));
+    return umax64(umax64(rdlaneu64(v, 0), rdlaneu64(v, 16)), umax64(rdlaneu64(v, 32), rdlaneu64(v, 48)));
+}
+
+// order-preserving unsigned image of (float)v (f32 rounding is monotone); NaN -> 0
+DEV uint32_t fkey(double v) {
+    const float f = (float)v;
+    if (f != f) return 0u;
+    const uint32_t b = __float_as_uint(f);
+    return (b >> 31) ? ~b : (b | 0x80000000u);
+}
+DEV uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dppi<DPP_XOR1>((int)v)); v = max(v, (uint32_t)dppi<DPP_XOR2>((int)v));
+    v = max(v, (uint32_t)dppi<DPP_ROR4>((int)v)); v = max(v, (uint32_t)dppi<DPP_ROR8>((int)v));
+    return max(max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
+               max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
+}
+
+// 8 rounds of "largest key, lowest expert index among equal keys, then retire it";
+// returns true when some round had several experts at the maximum key.
+template <typename K, typename MaxF>
+DEV bool top8_rounds(K k0, K k1, MaxF wmax, uint32_t (&ids)[QXG_TOPK]) {
+    const int lane = threadIdx.x & 63;
+    bool tie = false;
+#pragma unroll
+    for (int r = 0; r < QXG_TOPK; ++r) {
+        const K m = wmax(k0 > k1 ? k0 : k1);
+        const uint64_t b0 = __ballot(m != 0 && k0 == m), b1 = __ballot(m != 0 && k1 == m);
+        tie = tie || (__popcll(b0) + __popcll(b1) > 1);
+        // nothing left (non-finite logits): expert 0, as the reference's scan leaves it
+        const uint32_t id = b0 ? (uint32_t)__builtin_ctzll(b0) : b1 ? 64u + (uint32_t)__builtin_ctzll(b1) : 0u;
+        ids[r] = id;
+        if (lane == (int)(id & 63u)) {
+            if (id < 64u) k0 = 0; else k1 = 0;
+        }
+    }
+    return tie;
+}
+
+// Router top-8 and renormalised weights (src/qx_format.c:5265-5285), by every wave on
+// its own (no block barrier).  Lane l holds the logits of experts l and l+64 (double).
+// The reference picks by softmax probability with repeated strict-> scans (larger
+// first, lower index on ties); the probability is a non-decreasing function of the
+// logit, so picking by logit gives the same experts except where two probabilities
+// round to the same double (a zero margin).  The picks use 32-bit keys of the logits
+// rounded to f32: a unique maximal f32 key is also the maximal double.  Only when a
+// round sees several experts at the maximal f32 key are the picks redone with the
+// exact 64-bit keys of the doubles.  The weights p_r / sum_q p_q equal
+// e_r / sum_q e_q with e = exp(l - l_max), since the softmax denominator cancels.
+// ids[r] and w[r] are wave-uniform.
+DEV void wave_top8(double l0, double l1, int E, uint32_t (&ids)[QXG_TOPK], double (&w)[QXG_TOPK]) {
+    const int lane = threadIdx.x & 63;
+    const bool tie = top8_rounds<uint32_t>(lane < E ? fkey(l0) : 0u, lane + 64 < E ? fkey(l1) : 0u,
+                                           [](uint32_t v) { return wave_max_u32(v); }, ids);
+    if (tie)
+        (void)top8_rounds<uint64_t>(lane < E ? dkey(l0) : 0ull, lane + 64 < E ? dkey(l1) : 0ull,
+                                    [](uint64_t v) { return wave_max_u64(v); }, ids);
+    double lq = 0.0;   // lane q < 8: logit of pick q
+#pragma unroll
+    for (int q = 0; q < QXG_TOPK; ++q) {
+        const double v = ids[q] < 64u ? rdlaned(l0, (int)ids[q]) : rdlaned(l1, (int)(ids[q] - 64u));
+        if (lane == q) lq = v;
+    }
+    const double lmax = rdlaned(lq, 0);
+    const double eq = lane < QXG_TOPK ? exp(lq - lmax) : 0.0;
+    double sel = 0.0;
+#pragma unroll
+    for (int q = 0; q < QXG_TOPK; ++q) sel += rdlaned(eq, q);   // rank order, as the reference
+    const double wq = eq / sel;
+#pragma unroll
+    for (int q = 0; q < QXG_TOPK; ++q) w[q] = rdlaned(wq, q);
+}
+}  // namespace

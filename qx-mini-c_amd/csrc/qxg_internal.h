@@ -50,6 +50,8 @@ struct DevState {
     uint32_t pad;
     uint32_t moe_ids[QXG_TOPK];
     double moe_w[QXG_TOPK];
+    uint32_t epoch;         // exchange-buffer epoch of the persistent kernel (device-advanced)
+    uint32_t pad2;
 };
 
 struct Tables {
@@ -57,6 +59,43 @@ struct Tables {
     uint2 *g3;     // IQ3_XXS grid: 256 x {pos, neg}
     uint2 *sel;    // sign index (7 bits) -> v_perm selectors for 8 values
     double *rope_cos, *rope_sin;  // [QXG_MAX_CTX][64]
+};
+
+// Persistent decode kernel (qxk_layers): per-layer weight pointers and launch arguments.
+#define QXG_PBLOCKS 256   // workgroups of the persistent kernel: one per CU of an MI355X
+
+// One plane of a per-layer tensor kind: the planes of all layers lie back to back in
+// one device arena, layer l's at base + l * stride, so a kernel forms every layer's
+// pointers with scalar arithmetic on its arguments (no pointer-table loads).
+struct QxPlane {
+    const uint8_t *base;
+    uint64_t stride;
+};
+enum QxPlaneId : int {
+    PL_ATTN_NORM, PL_Q_NORM, PL_K_NORM, PL_FFN_NORM, PL_ROUTER,   // F32
+    PL_Q_QS, PL_Q_META, PL_K_QS, PL_K_META, PL_V_QS, PL_V_META,    // IQ4_XS
+    PL_O_QS, PL_O_META,
+    PL_G_QS, PL_G_SC, PL_G_D, PL_U_QS, PL_U_SC, PL_U_D,            // IQ2_XS
+    PL_D_QS, PL_D_AUX, PL_D_D,                                     // IQ3_XXS
+    PL_COUNT
+};
+
+struct QxPArgs {
+    QxPlane P[PL_COUNT];        // per-layer weight planes
+    uint32_t s0, s1;            // sub-layers [s0, s1): 2l = attention half of layer l, 2l+1 = its MoE half
+    uint32_t experts, ctx;      // routed experts; KV context length
+    Tables T;
+    int8_t *kc, *vc;
+    float *ks, *vs;
+    DevState *st_w;
+    // tagged exchange buffers, two slots each (layer parity)
+    uint64_t *xa, *xb, *qkv, *cx, *lg, *hb;
+    const float *x_in;          // residual entering sub-layer s0
+    float *x_out;               // residual leaving sub-layer s1-1 (may alias x_in)
+    float *d_layer, *d_attn, *d_moe, *d_vcur, *d_ctx;   // optional dumps (null: off)
+    uint32_t *abort;            // set on a timed-out wait; the host reports it
+    uint64_t timeout;           // wait deadline in 100 MHz ticks from kernel start
+    double sqrt_hd;
 };
 
 // Optional start/stop events recorded around one launch on its stream.  Created with

@@ -57,6 +57,7 @@ _sig(_g, "qxg_dequant_blocks", [vp, u32, vp, u64, vp, *ERR])
 _sig(_g, "qxg_attention_layer", [vp, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_moe_layer", [vp, u32, vp, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_final_head", [vp, vp, vp, vp, u32, vp, vp, *ERR])
+_sig(_g, "qxg_set_layer_path", [vp, c_int])
 _sig(_g, "qxg_time_kernel", [vp, c_int, u32, u32, ctypes.POINTER(c_float), *ERR])
 _sig(_g, "qxg_device_bytes", [vp], u64)
 _sig(_g, "qxg_profile_kernel", [vp, c_int])
@@ -202,6 +203,10 @@ class Context:
                                     self._err, 1024))
         return out, ms.value
 
+    def set_layer_path(self, persistent):
+        """0: one kernel per phase (default); 1: the persistent layer kernel."""
+        self._check(_g.qxg_set_layer_path(self._c, int(persistent)))
+
     def time_kernel(self, which, layer=0, iters=20):
         ms = c_float()
         self._check(_g.qxg_time_kernel(self._c, which, layer, iters, ctypes.byref(ms), self._err, 1024))
@@ -219,4 +224,4 @@ class Context:
         return int(_g.qxg_device_bytes(self._c))
 
 
-KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "oproj": 3, "head": 4, "attention": 5, "router": 6}
+KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "oproj": 3, "head": 4, "attention": 5, "router": 6, "layers": 7}

@@ -13,9 +13,12 @@ BLOCK_BYTES = {12: 144, 14: 210, 17: 74, 18: 98, 23: 136}
 D_OFFSET = {12: 0, 14: 208, 17: 0, 18: 0, 23: 0}
 
 
-@pytest.fixture(scope="module")
-def ctx():
+@pytest.fixture(scope="module", params=[0, 1], ids=["per_phase", "persistent"])
+def ctx(request):
+    """Both layer paths: one kernel per phase, and the persistent layer kernel."""
     c = qxg.Context(0)
+    c.set_layer_path(request.param)
+    c.layer_path = request.param
     yield c
     c.close()
 
@@ -188,8 +191,9 @@ def test_decode_two_layers_greedy(ctx, tmp_path):
         assert list(gen2) == toks[1:], rep
     # eager (per-launch timed) loop agrees with the replayed one
     ctx.kv_create(2, 16)
-    ctx.profile_kernel(qxg.KERNELS["gate_up"])
+    ctx.profile_kernel(qxg.KERNELS["layers" if ctx.layer_path else "gate_up"])
     gen3, _ = ctx.generate([17], 5)
     n, _ = ctx.profile_result()
     ctx.profile_kernel(-1)
-    assert list(gen3) == toks and n == 5 * 2
+    # one persistent launch per step, or one gate/up launch per layer and step
+    assert list(gen3) == toks and n == (5 if ctx.layer_path else 5 * 2)
