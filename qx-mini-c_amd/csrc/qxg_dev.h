@@ -27,6 +27,10 @@ DEV float fp16_exact(uint32_t h) {
     return __uint_as_float(bits);
 }
 
+// the wave's index in its workgroup, in a scalar register (the divergence analysis
+// does not know that threadIdx.x / 64 is the same in every lane of a wave)
+DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 DEV uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
 

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
         const uint8_t *v_qs, const uint8_t *v_meta, float *qkv) {
     __shared__ uint32_t s_dig[64 * DIG_STRIDE];
     __shared__ double s_red[4];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int b = lane >> 3, ib = lane & 7;
     const int r0 = (blockIdx.x * 4 + wave) * RPW;   // grid covers exactly 5120 rows
     QXG_MARK(3, 0);
@@ -131,7 +131,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     __shared__ float s_part[2][128];
     __shared__ int8_t s_k8[128], s_v8[128];
     __shared__ float s_scale[2];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int qh = blockIdx.x, kvh = qh >> 3;
     const uint32_t pos = cur_pos(st), n = pos + 1;
     const uint64_t base = (uint64_t)layer * ctx;
@@ -276,7 +276,7 @@ template <int RPW>
 __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_t *qs, const uint8_t *meta,
                                                   float *x, float *attn_dump) {
     __shared__ uint32_t s_dig[128 * DIG_STRIDE];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int ib = lane & 7, b0 = lane >> 3, b1 = 8 + (lane >> 3);
     const int r0 = (blockIdx.x * 4 + wave) * RPW;
     QXG_MARK(0, 0);
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
 // kernel, where the expert ids are needed.
 extern "C" __global__ __launch_bounds__(256) void qxk_router(const float *x, const float *norm_w, const float *router,
         uint32_t experts, double *logits) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t e = blockIdx.x * 4 + wave;
     if (e >= experts) return;
     float v[32], w[32], r[32];
@@ -355,7 +355,7 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     __shared__ uint2 s_sel[128];
     __shared__ uint32_t s_dig[64 * DIG_STRIDE];
     __shared__ double s_red[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int b = lane >> 3, ib = lane & 7;
     const int u0 = (blockIdx.x * 4 + wave) * UPW;   // grid covers exactly 8*768 units
     const int E = (int)experts;
@@ -449,7 +449,7 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, const uint8_t *d
     __shared__ uint2 s_g3[256];
     __shared__ uint2 s_sel[128];
     __shared__ uint32_t s_dig[192 * DIG_STRIDE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int r = lane >> 3, k = lane & 7;
     const int r0 = (blockIdx.x * 4 + wave) * RPW;   // grid covers exactly 2048 rows
     QXG_MARK(2, 0);
@@ -526,7 +526,7 @@ template <int RPW>
 __global__ __launch_bounds__(256) void qxk_head(const uint32_t *dig, const uint8_t *ql,
         const uint8_t *qh, const int8_t *sc, const uint16_t *dd, uint32_t vocab, DevState *st, float *logits) {
     if (!st->force_head && st->step + 1 < st->n_prompt) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int b = lane >> 3, ib = lane & 7, hh = ib >> 2, k = ib & 3;
     const uint32_t r0 = (blockIdx.x * 4 + wave) * RPW;
     uint4 l0[RPW], l1[RPW], h0[RPW], h1[RPW];

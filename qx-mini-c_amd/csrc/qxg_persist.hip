@@ -45,11 +45,32 @@ extern "C" int qxg_ptrace_read(unsigned long long *out) {
 
 namespace {
 
-DEV uint64_t ld_tag(const uint64_t *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-DEV void st_bits(uint64_t *p, uint32_t bits, uint32_t ep) {
+#define GLB __attribute__((address_space(1)))
+
+// Wave-uniform values.  The compiler's divergence analysis neither knows that
+// threadIdx.x / 64 is the same in every lane of a wave nor that a pointer read from
+// LDS is; readfirstlane puts such values in scalar registers, so the per-wave
+// arithmetic and branches are scalar and the pointers address global memory (not flat).
+DEV uint64_t uni64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+template <typename T>
+DEV const GLB T *gptr(const T *p) { return (const GLB T *)uni64((uint64_t)p); }
+template <typename T>
+DEV GLB T *gptrw(T *p) { return (GLB T *)uni64((uint64_t)p); }
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+DEV uint4 gld4(const GLB void *p) { const u32x4 v = *(const GLB u32x4 *)p; return make_uint4(v.x, v.y, v.z, v.w); }
+DEV uint2 gld2(const GLB void *p) { const u32x2 v = *(const GLB u32x2 *)p; return make_uint2(v.x, v.y); }
+
+DEV uint64_t ld_tag(const GLB uint64_t *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+DEV void st_bits(GLB uint64_t *p, uint32_t bits, uint32_t ep) {
     __hip_atomic_store(p, ((uint64_t)ep << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-DEV void st_tag(uint64_t *p, float v, uint32_t ep) { st_bits(p, __float_as_uint(v), ep); }
+DEV void st_tag(GLB uint64_t *p, float v, uint32_t ep) { st_bits(p, __float_as_uint(v), ep); }
 
 struct Ctl {
     uint64_t deadline;
@@ -70,7 +91,7 @@ DEV bool keep_waiting(uint32_t &it, const Ctl &c) {
 // Waits until every p[idx[k]] carries epoch ep; the f32 payloads go to v.  All loads
 // are issued before the first check; later rounds reload only the stale words.
 template <int K>
-DEV bool wait_tagged(const uint64_t *p, const int (&idx)[K], uint32_t ep, uint32_t (&v)[K], const Ctl &c) {
+DEV bool wait_tagged(const GLB uint64_t *p, const int (&idx)[K], uint32_t ep, uint32_t (&v)[K], const Ctl &c) {
     uint64_t w[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) w[k] = ld_tag(p + idx[k]);
@@ -99,14 +120,14 @@ constexpr int CPOL_SC1 = 16;   // agent-scope coherent access (bypasses the non-
 // tagged vector, loaded straight into the LDS stage (raw {f32 bits, epoch} pairs) with
 // agent-coherent direct-to-LDS loads: lane i fetches words 2i, 2i+1 of a chunk.  Stale
 // chunks are fetched again until every word carries the epoch.  false on timeout/abort.
-DEV bool wave_poll_chunks(const uint64_t *src, uint32_t ep, uint2 *stage, int nchunks, const Ctl &c) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+DEV bool wave_poll_chunks(const GLB uint64_t *src, uint32_t ep, uint2 *stage, int nchunks, const Ctl &c) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int mine = (nchunks - wave + 3) >> 2;
     uint32_t pending = mine >= 32 ? 0xffffffffu : (1u << mine) - 1u, it = 0;
     for (;;) {
         for (uint32_t m = pending; m; m &= m - 1) {
             const int ch = wave + 4 * __builtin_ctz(m);
-            __builtin_amdgcn_global_load_lds(src + 128 * ch + 2 * lane, lds_ptr(stage + 128 * ch), 16, 0, CPOL_SC1);
+            __builtin_amdgcn_global_load_lds((const GLB void *)(src + 128 * ch + 2 * lane), lds_ptr(stage + 128 * ch), 16, 0, CPOL_SC1);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the LDS copies have landed
         uint32_t stale = 0;
@@ -122,7 +143,7 @@ DEV bool wave_poll_chunks(const uint64_t *src, uint32_t ep, uint2 *stage, int nc
 }
 
 // the stage from a plain f32 vector (the residual entering the launch's first sub-layer)
-DEV void stage_plain(const float *x, int n, uint2 *stage) {
+DEV void stage_plain(const GLB float *x, int n, uint2 *stage) {
     for (int i = threadIdx.x; i < n; i += 256) stage[i] = make_uint2(__float_as_uint(x[i]), 0u);
 }
 
@@ -237,15 +258,22 @@ DEV void top8_lanes(double l0, double l1, int E, uint32_t &my_id, double &my_w) 
     my_w = eq / sel;
 }
 
-// layer l's plane `id` (scalar arithmetic on kernel arguments)
+// layer l's plane `id` (scalar arithmetic on the arguments)
 template <typename T>
-DEV const T *plane(const QxPArgs &a, int id, uint32_t l) {
-    return reinterpret_cast<const T *>(a.P[id].base + (uint64_t)l * a.P[id].stride);
+DEV const GLB T *plane(const QxPArgs &a, int id, uint32_t l) {
+    return (const GLB T *)(uni64((uint64_t)a.P[id].base) + (uint64_t)l * uni64(a.P[id].stride));
 }
 
-DEV void load8(const float *p, float (&w)[8]) {
-    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+DEV void load8(const GLB float *p, float (&w)[8]) {
+    const f32x4 a = ((const GLB f32x4 *)p)[0], b = ((const GLB f32x4 *)p)[1];
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+DEV void load32g(const GLB float *p, float *v) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const f32x4 t = ((const GLB f32x4 *)p)[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
 }
 
 constexpr int ATT_STAGE = 128;   // cached KV positions staged in LDS by the attention workgroups
@@ -300,22 +328,22 @@ DEV void attn_prefetch(const QxPArgs &a, uint32_t l, uint32_t pos, AttnPre &p) {
         const uint32_t t = (tid >> 3) + 32 * i;
         if (t < nst) {
             const uint64_t off = (base + t) * 512 + kvh * 128 + 16 * (tid & 7);
-            p.kst[i] = *reinterpret_cast<const uint4 *>(a.kc + off);
-            p.vst[i] = *reinterpret_cast<const uint4 *>(a.vc + off);
+            p.kst[i] = gld4(gptr(a.kc) + off);
+            p.vst[i] = gld4(gptr(a.vc) + off);
         }
     }
-    p.kss = (uint32_t)tid < nst ? a.ks[base + tid] : 0.0f;
-    p.vss = (uint32_t)tid < nst ? a.vs[base + tid] : 0.0f;
-    const float *kn = plane<float>(a, PL_K_NORM, l), *qn = plane<float>(a, PL_Q_NORM, l);
+    p.kss = (uint32_t)tid < nst ? gptr(a.ks)[base + tid] : 0.0f;
+    p.vss = (uint32_t)tid < nst ? gptr(a.vs)[base + tid] : 0.0f;
+    const GLB float *kn = plane<float>(a, PL_K_NORM, l), *qn = plane<float>(a, PL_Q_NORM, l);
     p.kw0 = kn[lane]; p.kw1 = kn[64 + lane];
     p.qw0 = qn[lane]; p.qw1 = qn[64 + lane];
-    p.cs = a.T.rope_cos[pos * 64 + lane];
-    p.sn = a.T.rope_sin[pos * 64 + lane];
+    p.cs = gptr(a.T.rope_cos)[pos * 64 + lane];
+    p.sn = gptr(a.T.rope_sin)[pos * 64 + lane];
 }
 
-DEV bool attn_phase(const QxPArgs &a, uint32_t l, uint32_t pos, const uint64_t *qkv, uint64_t *cx, uint32_t ep,
+DEV bool attn_phase(const QxPArgs &a, uint32_t l, uint32_t pos, const GLB uint64_t *qkv, GLB uint64_t *cx, uint32_t ep,
                     const AttnPre &p, AttnLds &S, const Ctl &c) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int qh = blockIdx.x, kvh = qh >> 3;
     const uint32_t n = pos + 1;
     const uint64_t base = (uint64_t)l * a.ctx;
@@ -356,11 +384,11 @@ DEV bool attn_phase(const QxPArgs &a, uint32_t l, uint32_t pos, const uint64_t *
         int qv = isfinite(vx) ? (int)rintf(vx / vscale) : 0;
         qk = qk < -127 ? -127 : qk > 127 ? 127 : qk;
         qv = qv < -127 ? -127 : qv > 127 ? 127 : qv;
-        if (blockIdx.x == 0) { a.kc[slot * 512 + i] = (int8_t)qk; a.vc[slot * 512 + i] = (int8_t)qv; }
+        if (blockIdx.x == 0) { gptrw(a.kc)[slot * 512 + i] = (int8_t)qk; gptrw(a.vc)[slot * 512 + i] = (int8_t)qv; }
         if ((i >> 7) == kvh) { S.k8[i & 127] = (int8_t)qk; S.v8[i & 127] = (int8_t)qv; }
     }
-    if (blockIdx.x == 0 && tid == 0) { a.ks[slot] = kscale; a.vs[slot] = vscale; }
-    if (blockIdx.x == 0 && a.d_vcur) { a.d_vcur[tid] = v0; a.d_vcur[256 + tid] = v1; }
+    if (blockIdx.x == 0 && tid == 0) { gptrw(a.ks)[slot] = kscale; gptrw(a.vs)[slot] = vscale; }
+    if (blockIdx.x == 0 && a.d_vcur) { gptrw(a.d_vcur)[tid] = v0; gptrw(a.d_vcur)[256 + tid] = v1; }
     if (tid == 0) { S.scale[0] = kscale; S.scale[1] = vscale; }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -388,8 +416,8 @@ DEV bool attn_phase(const QxPArgs &a, uint32_t l, uint32_t pos, const uint64_t *
                     kk = reinterpret_cast<const uint2 *>(S.kst)[t * 16 + dl];
                     ksc = S.kss[t];
                 } else {
-                    kk = *reinterpret_cast<const uint2 *>(a.kc + (base + t) * 512 + kvh * 128 + 8 * dl);
-                    ksc = a.ks[base + t];
+                    kk = gld2(gptr(a.kc) + (base + t) * 512 + kvh * 128 + 8 * dl);
+                    ksc = gptr(a.ks)[base + t];
                 }
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -433,7 +461,7 @@ DEV bool attn_phase(const QxPArgs &a, uint32_t l, uint32_t pos, const uint64_t *
         const double wgt = S.sc[t] / den;
         const float vv = t == pos ? (float)S.v8[d] * S.scale[1]
                          : t < nst ? (float)reinterpret_cast<const int8_t *>(S.vst)[t * 128 + d] * S.vss[t]
-                                   : (float)a.vc[(base + t) * 512 + kvh * 128 + d] * a.vs[base + t];
+                                   : (float)gptr(a.vc)[(base + t) * 512 + kvh * 128 + d] * gptr(a.vs)[base + t];
         acc += (float)(wgt * (double)vv);
     }
     S.part[hf][d] = acc;
@@ -441,7 +469,7 @@ DEV bool attn_phase(const QxPArgs &a, uint32_t l, uint32_t pos, const uint64_t *
     if (tid < 128) {
         const float o = S.part[0][tid] + S.part[1][tid];
         st_tag(cx + qh * 128 + tid, o, ep);
-        if (a.d_ctx) a.d_ctx[qh * 128 + tid] = o;
+        if (a.d_ctx) gptrw(a.d_ctx)[qh * 128 + tid] = o;
     }
     __syncthreads();   // the LDS area is reused as the next phase's stage
     return true;
@@ -457,14 +485,14 @@ DEV void load_p1(const QxPArgs &a, uint32_t l, int gw, int lane, P1W &w) {
 #pragma unroll
     for (int rr = 0; rr < 5; ++rr) {
         const int r = 5 * gw + rr;
-        const uint8_t *qs, *meta;
+        const GLB uint8_t *qs, *meta;
         int lr;
         if (r < 4096) { qs = plane<uint8_t>(a, PL_Q_QS, l); meta = plane<uint8_t>(a, PL_Q_META, l); lr = r; }
         else if (r < 4608) { qs = plane<uint8_t>(a, PL_K_QS, l); meta = plane<uint8_t>(a, PL_K_META, l); lr = r - 4096; }
         else { qs = plane<uint8_t>(a, PL_V_QS, l); meta = plane<uint8_t>(a, PL_V_META, l); lr = r - 4608; }
         const uint64_t blk = (uint64_t)lr * 8 + b;
-        w.q[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[ib];
-        w.m[rr] = *reinterpret_cast<const uint2 *>(meta + blk * 8);
+        w.q[rr] = gld4(qs + blk * 128 + 16 * ib);
+        w.m[rr] = gld2(meta + blk * 8);
     }
 }
 // P3 weights of one wave: O rows 2gw, 2gw+1 (16 blocks per row; lane takes blocks lane/8 and 8+lane/8)
@@ -474,14 +502,14 @@ struct P3W {
 };
 DEV void load_p3(const QxPArgs &a, uint32_t l, int gw, int lane, P3W &w) {
     const int ib = lane & 7, b0 = lane >> 3, b1 = 8 + (lane >> 3);
-    const uint8_t *oq = plane<uint8_t>(a, PL_O_QS, l), *om = plane<uint8_t>(a, PL_O_META, l);
+    const GLB uint8_t *oq = plane<uint8_t>(a, PL_O_QS, l), *om = plane<uint8_t>(a, PL_O_META, l);
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
         const uint64_t k0 = (uint64_t)(2 * gw + rr) * 16 + b0, k1 = (uint64_t)(2 * gw + rr) * 16 + b1;
-        w.q0[rr] = reinterpret_cast<const uint4 *>(oq + k0 * 128)[ib];
-        w.q1[rr] = reinterpret_cast<const uint4 *>(oq + k1 * 128)[ib];
-        w.m0[rr] = *reinterpret_cast<const uint2 *>(om + k0 * 8);
-        w.m1[rr] = *reinterpret_cast<const uint2 *>(om + k1 * 8);
+        w.q0[rr] = gld4(oq + k0 * 128 + 16 * ib);
+        w.q1[rr] = gld4(oq + k1 * 128 + 16 * ib);
+        w.m0[rr] = gld2(om + k0 * 8);
+        w.m1[rr] = gld2(om + k1 * 8);
     }
 }
 
@@ -494,7 +522,7 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
     // cannot be hoisted across the phase barriers, so the ~40 pointers are not held in
     // scalar registers for the whole launch.
     __shared__ QxPArgs a;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     static_assert(sizeof(QxPArgs) % 8 == 0 && sizeof(QxPArgs) <= 256 * 8, "argument copy");
     if (tid < (int)(sizeof(QxPArgs) / 8))
         reinterpret_cast<uint64_t *>(&a)[tid] = reinterpret_cast<const uint64_t *>(&args)[tid];
@@ -510,15 +538,15 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
         load_p1(a, l0, gw, lane, w1);
         load8(plane<float>(a, PL_ATTN_NORM, l0) + 8 * tid, anw);
     }
-    S.g2[tid] = a.T.g2[tid];
-    S.g2[tid + 256] = a.T.g2[tid + 256];
-    S.g3[tid] = a.T.g3[tid];
-    if (tid < 128) S.sel[tid] = a.T.sel[tid];
-    const DevState *st = a.st_w;
-    const uint32_t pos = st->pos0 + st->step;
-    const uint32_t ep_base = st->epoch;
+    S.g2[tid] = gld4(gptr(a.T.g2) + tid);
+    S.g2[tid + 256] = gld4(gptr(a.T.g2) + tid + 256);
+    S.g3[tid] = gld2(gptr(a.T.g3) + tid);
+    if (tid < 128) S.sel[tid] = gld2(gptr(a.T.sel) + tid);
+    const GLB DevState *st = gptr(a.st_w);
+    const uint32_t pos = __builtin_amdgcn_readfirstlane(st->pos0 + st->step);
+    const uint32_t ep_base = __builtin_amdgcn_readfirstlane(st->epoch);
     // residual rows 2gw, 2gw+1 live in this wave (wave-uniform) for the whole launch
-    float xo0 = a.x_in[2 * gw], xo1 = a.x_in[2 * gw + 1];
+    float xo0 = gptr(a.x_in)[2 * gw], xo1 = gptr(a.x_in)[2 * gw + 1];
     const int E = (int)a.experts;
     __syncthreads();
 #pragma unroll 1
@@ -531,14 +559,14 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
         float rw[32], fnw[8];
         if (run_a) {
             // ------------------------------------------------ P1: RMSNorm + Q/K/V rows
-            uint64_t *qkv = a.qkv + slot * 5120;
+            GLB uint64_t *qkv = gptrw(a.qkv) + slot * 5120;
             PMARK(sa, 0);
             P3W w3;
             AttnPre ap;
             {
                 bool got = true;
-                if (sa == a.s0) stage_plain(a.x_in, 2048, S.stage);
-                else got = wave_poll_chunks(a.xb + ((l + 1) & 1) * 2048, epa - 1, S.stage, 16, ctl);
+                if (sa == a.s0) stage_plain(gptr(a.x_in), 2048, S.stage);
+                else got = wave_poll_chunks(gptr(a.xb) + ((l + 1) & 1) * 2048, epa - 1, S.stage, 16, ctl);
                 if (__syncthreads_or(!got)) return;
                 PMARK(sa, 1);
                 load_p3(a, l, gw, lane, w3);
@@ -566,7 +594,7 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
                 PMARK(sa, 3);
             }
             // ------------------------------------------------ P2: attention (q head per workgroup)
-            uint64_t *cx = a.cx + slot * 4096;
+            GLB uint64_t *cx = gptrw(a.cx) + slot * 4096;
             if (blockIdx.x < QXG_HEADS) {
                 if (!attn_phase(a, l, pos, qkv, cx, epa, ap, S.att, ctl)) return;
                 PMARK(sa, 5);
@@ -576,7 +604,7 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
                 const bool got = wave_poll_chunks(cx, epa, S.stage, 32, ctl);
                 if (__syncthreads_or(!got)) return;
                 PMARK(sa, 6);
-                if (router) load32(plane<float>(a, PL_ROUTER, l) + (uint64_t)gw * 2048 + 32 * lane, rw);
+                if (router) load32g(plane<float>(a, PL_ROUTER, l) + (uint64_t)gw * 2048 + 32 * lane, rw);
                 load8(plane<float>(a, PL_FFN_NORM, l) + 8 * tid, fnw);
                 const bool ok = digits_stage(S.stage, 512, nullptr, S.dig, S.red, nullptr);
                 PMARK(sa, 7);
@@ -592,13 +620,13 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
                     part[1] = d;
                 }
                 rows_reduce<2>(part, out, lane);
-                uint64_t *xa = a.xa + slot * 2048;
+                GLB uint64_t *xa = gptrw(a.xa) + slot * 2048;
                 const float o0 = (ok && isfinite(out[0])) ? out[0] : 0.0f, o1 = (ok && isfinite(out[1])) ? out[1] : 0.0f;
                 xo0 = xo0 + o0;
                 xo1 = xo1 + o1;
                 if (lane < 2) {
                     st_tag(xa + 2 * gw + lane, lane ? xo1 : xo0, epa);
-                    if (a.d_attn) a.d_attn[2 * gw + lane] = lane ? o1 : o0;
+                    if (a.d_attn) gptrw(a.d_attn)[2 * gw + lane] = lane ? o1 : o0;
                 }
                 PMARK(sa, 8);
             }
@@ -607,18 +635,18 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
             // ------------------------------------------------ P4: ffn RMSNorm + digits, router logits
             PMARK(sm, 0);
             if (!run_a) {
-                if (router) load32(plane<float>(a, PL_ROUTER, l) + (uint64_t)gw * 2048 + 32 * lane, rw);
+                if (router) load32g(plane<float>(a, PL_ROUTER, l) + (uint64_t)gw * 2048 + 32 * lane, rw);
                 load8(plane<float>(a, PL_FFN_NORM, l) + 8 * tid, fnw);
             }
             bool got = true;
-            if (sm == a.s0) stage_plain(a.x_in, 2048, S.stage);
-            else got = wave_poll_chunks(a.xa + slot * 2048, epm - 1, S.stage, 16, ctl);
+            if (sm == a.s0) stage_plain(gptr(a.x_in), 2048, S.stage);
+            else got = wave_poll_chunks(gptr(a.xa) + slot * 2048, epm - 1, S.stage, 16, ctl);
             if (__syncthreads_or(!got)) return;
             PMARK(sm, 1);
             // digits of the normalised input (for P5); xn kept in LDS for the router waves
             const bool ok = digits_stage(S.stage, 256, fnw, S.dig, S.red, S.xn);
             PMARK(sm, 2);
-            uint64_t *lg = a.lg + slot * 256;
+            GLB uint64_t *lg = gptrw(a.lg) + slot * 256;
             if (router) {
                 // reference src/qx_format.c:5254-5264: logit_e = sum_i double(W[e,i]) * double(xn_i)
                 double acc = 0.0;
@@ -633,7 +661,7 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
                 PMARK(sm, 3);
             }
             // ------------------------------------------------ P5: top-8, gate/up + SwiGLU
-            uint64_t *hb = a.hb + slot * (QXG_TOPK * QXG_FFN);
+            GLB uint64_t *hb = gptrw(a.hb) + slot * (QXG_TOPK * QXG_FFN);
             {   // one wave polls the 2E logit words (fewer pollers on a few hot lines)
                 bool got2 = true;
                 if (wave == 0) {
@@ -659,17 +687,17 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
             const int b = lane >> 3;
             const int u0 = 6 * gw;                    // 768 = 128 * 6: one expert per wave
             const uint32_t ue = (uint32_t)__builtin_amdgcn_readlane((int)my_id, u0 / QXG_FFN);
-            const uint8_t *g_qs = plane<uint8_t>(a, PL_G_QS, l), *g_sc = plane<uint8_t>(a, PL_G_SC, l);
-            const uint8_t *u_qs = plane<uint8_t>(a, PL_U_QS, l), *u_sc = plane<uint8_t>(a, PL_U_SC, l);
-            const uint16_t *g_d = plane<uint16_t>(a, PL_G_D, l), *u_d = plane<uint16_t>(a, PL_U_D, l);
+            const GLB uint8_t *g_qs = plane<uint8_t>(a, PL_G_QS, l), *g_sc = plane<uint8_t>(a, PL_G_SC, l);
+            const GLB uint8_t *u_qs = plane<uint8_t>(a, PL_U_QS, l), *u_sc = plane<uint8_t>(a, PL_U_SC, l);
+            const GLB uint16_t *g_d = plane<uint16_t>(a, PL_G_D, l), *u_d = plane<uint16_t>(a, PL_U_D, l);
             uint2 gq[6], uq[6];
             uint32_t gs[6], us[6], gd[6], ud[6];
 #pragma unroll
             for (int uu = 0; uu < 6; ++uu) {
                 const int i = (u0 + uu) % QXG_FFN;
                 const uint64_t blk = ((uint64_t)ue * QXG_FFN + i) * 8 + b;
-                gq[uu] = reinterpret_cast<const uint2 *>(g_qs + blk * 64)[ib];
-                uq[uu] = reinterpret_cast<const uint2 *>(u_qs + blk * 64)[ib];
+                gq[uu] = gld2(g_qs + blk * 64 + 8 * ib);
+                uq[uu] = gld2(u_qs + blk * 64 + 8 * ib);
                 gs[uu] = g_sc[blk * 8 + ib];
                 us[uu] = u_sc[blk * 8 + ib];
                 gd[uu] = g_d[blk];
@@ -678,20 +706,20 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
             // down weights of P6 (rows 2gw, 2gw+1): lanes 8r..8r+7 hold rank r, lane 8r+k sub-block k of 3 blocks
             const int dr = lane >> 3, dk = lane & 7;
             const uint32_t de = (uint32_t)__shfl((int)my_id, dr);
-            const uint8_t *d_qs = plane<uint8_t>(a, PL_D_QS, l), *d_aux = plane<uint8_t>(a, PL_D_AUX, l);
-            const uint16_t *d_d = plane<uint16_t>(a, PL_D_D, l);
+            const GLB uint8_t *d_qs = plane<uint8_t>(a, PL_D_QS, l), *d_aux = plane<uint8_t>(a, PL_D_AUX, l);
+            const GLB uint16_t *d_d = plane<uint16_t>(a, PL_D_D, l);
             uint2 dq[6];
             uint32_t dax[6], ddv[6];
 #pragma unroll
             for (int t = 0; t < 6; ++t) {   // t = 3*row + block
                 const uint64_t blk = ((uint64_t)de * 2048 + 2 * gw + t / 3) * 3 + t % 3;
-                dq[t] = reinterpret_cast<const uint2 *>(d_qs + blk * 64)[dk];
-                dax[t] = reinterpret_cast<const uint32_t *>(d_aux + blk * 32)[dk];
+                dq[t] = gld2(d_qs + blk * 64 + 8 * dk);
+                dax[t] = *(const GLB uint32_t *)(d_aux + blk * 32 + 4 * dk);
                 ddv[t] = d_d[blk];
             }
             if (blockIdx.x == 0 && wave == 0 && lane < QXG_TOPK) {   // ids and weights for the MoE replay seam
-                a.st_w->moe_ids[lane] = my_id;
-                a.st_w->moe_w[lane] = my_w;
+                gptrw(a.st_w)->moe_ids[lane] = my_id;
+                gptrw(a.st_w)->moe_w[lane] = my_w;
             }
             PMARK(sm, 5);
             {
@@ -740,7 +768,7 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
                 }
                 const bool okh = digits_stage(S.stage, 768, nullptr, S.dig, S.red, nullptr);
                 PMARK(sm, 8);
-                uint64_t *xb = a.xb + slot * 2048;
+                GLB uint64_t *xb = gptrw(a.xb) + slot * 2048;
 #pragma unroll 1
                 for (int rr = 0; rr < 2; ++rr) {
                     float part = 0.0f;
@@ -764,16 +792,16 @@ extern "C" __global__ __launch_bounds__(256, 1) void qxk_layers(QxPArgs args) {
                     if (rr) xo1 = xn; else xo0 = xn;
                     if (lane == 0) {
                         st_tag(xb + 2 * gw + rr, xn, epm);
-                        if (a.d_moe) a.d_moe[2 * gw + rr] = moe;
-                        if (a.d_layer) a.d_layer[(uint64_t)l * 2048 + 2 * gw + rr] = xn;
+                        if (a.d_moe) gptrw(a.d_moe)[2 * gw + rr] = moe;
+                        if (a.d_layer) gptrw(a.d_layer)[(uint64_t)l * 2048 + 2 * gw + rr] = xn;
                     }
                 }
                 PMARK(sm, 9);
             }
         }
     }
-    if (lane < 2) a.x_out[2 * gw + lane] = lane ? xo1 : xo0;
+    if (lane < 2) gptrw(a.x_out)[2 * gw + lane] = lane ? xo1 : xo0;
     // the epoch advances once every workgroup has read it (any workgroup finishing
     // implies all have passed their first phase)
-    if (blockIdx.x == 0 && tid == 0) a.st_w->epoch = ep_base + (a.s1 - a.s0) + 1;
+    if (blockIdx.x == 0 && tid == 0) gptrw(a.st_w)->epoch = ep_base + (a.s1 - a.s0) + 1;
 }
