@@ -111,6 +111,27 @@ int qxg_moe_layer(qxg_ctx *ctx, uint32_t layer, const float *ffn_inp, float *lay
 int qxg_final_head(qxg_ctx *ctx, const float *residual, float *norm_out, float *logits, uint32_t top_n,
                    uint32_t *top_ids, double *top_logits, char *err, uint64_t err_len);
 
+/* Batched prefill: tokens[0..n) at positions position0.. through every bound layer
+ * together (projection and expert GEMMs on the matrix cores), INT8 KV appended at
+ * [layer][position0+i]; then, if run_head, the output RMSNorm, Q6_K head and top_n on
+ * the last token.  Stands in for the reference's prompt steps, which run one token at a
+ * time through the decode step with the head only on the last prompt token
+ * (src/qx_format.c:6250-6547, sampling_step at 6253).  Chunks of 512 tokens run in
+ * order.  residual_out (may be NULL): n*2048 floats, each token's residual after the
+ * last layer.  logits / top_* as in qxg_decode_token.  elapsed_ms: device time of the
+ * whole call (HIP events on the context stream). */
+int qxg_prefill(qxg_ctx *ctx, const uint32_t *tokens, uint32_t n, uint32_t position0, int run_head,
+                float *residual_out, float *logits, uint32_t top_n, uint32_t *top_ids, double *top_logits,
+                float *elapsed_ms, char *err, uint64_t err_len);
+
+/* Same-input replay of one prefill layer: n <= 512 residual rows x_in (n*2048) at
+ * positions position0.. (KV rows appended as in qxg_prefill).  ffn_inp_out = x_in +
+ * attention (the MoE input, dump phase "ffn-inp"), moe_out = the weighted expert sum
+ * ("ffn-moe-out"), x_out = ffn_inp + moe; any output may be NULL.  The reference's
+ * counterpart is n successive layer steps (src/qx_format.c:6282-6423, 5198-5317). */
+int qxg_prefill_layer(qxg_ctx *ctx, uint32_t layer, uint32_t n, uint32_t position0, const float *x_in,
+                      float *ffn_inp_out, float *moe_out, float *x_out, char *err, uint64_t err_len);
+
 /* How the layers of a token are launched (no reference counterpart: the reference
  * runs one thread on the CPU).  0: one kernel per phase, six per layer; 1: one
  * persistent kernel for all layers of the token, one workgroup per CU, phases handed

@@ -32,6 +32,19 @@ void qxl_down(hipStream_t, const float *, const QTensor *, Tables, const DevStat
               Timer = Timer());
 void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32_t, DevState *, float *, float *,
               uint32_t *, Timer = Timer());
+__global__ void qxp_embed(const uint8_t *, uint64_t, const uint32_t *, float *);
+__global__ void qxp_norm(const float *, const float *, uint32_t, float *);
+__global__ void qxp_qk(const float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
+                       uint32_t, uint32_t, uint32_t, float *);
+__global__ void qxp_attn(const float *, const int8_t *, const int8_t *, const float *, const float *, uint32_t, uint32_t,
+                         uint32_t, double, float *);
+__global__ void qxp_router(const float *, const float *, uint32_t, uint32_t, double *);
+__global__ void qxp_route(const double *, uint32_t, uint32_t, uint32_t *, double *);
+__global__ void qxp_group(const uint32_t *, uint32_t, uint32_t, uint32_t, int32_t *, uint32_t *, uint32_t *, uint32_t *);
+__global__ void qxp_combine(const float *, const float *, const uint32_t *, const double *, float *, float *);
+void qxp_launch_gemm(hipStream_t, int, const PfGemm &, const PfTables &, uint32_t, uint32_t, Timer);
+void qxp_launch_pack(hipStream_t, int, const float *, const int32_t *, const uint32_t *, uint32_t, uint32_t, uint4 *,
+                     float *);
 }
 
 namespace {
@@ -106,6 +119,18 @@ struct qxg_ctx {
     // one decode step (embed .. head, top-1, step advance) recorded once and replayed
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    // batched prefill: codebooks and work buffers for chunks of up to QXP_MAX tokens
+    struct Prefill {
+        bool ready = false;
+        PfTables P{};
+        float *X = nullptr, *X1 = nullptr, *XN = nullptr, *QKV = nullptr, *QR = nullptr, *CTX = nullptr;
+        float *H = nullptr, *Y = nullptr, *rscale = nullptr, *dump = nullptr;
+        uint4 *apk = nullptr;
+        double *lg = nullptr, *w = nullptr;
+        uint32_t *ids = nullptr, *tok_slot = nullptr, *mgroups = nullptr, *meta = nullptr, *tokens = nullptr;
+        int32_t *slot_token = nullptr;
+        std::vector<void *> all;
+    } pf;
 };
 
 namespace {
@@ -405,6 +430,121 @@ bool build_arenas(qxg_ctx *c, char *err, uint64_t n) {
     for (void *pp : old) (void)hipFree(pp);
     return true;
 }
+
+// ---- batched prefill
+constexpr uint32_t PF_EXPERT_MT = 2;                              // row tiles per expert GEMM wave
+constexpr uint32_t PF_SLOTS = QXP_MAX * QXG_TOPK + 32 * 128;       // expert slots, padded per expert
+constexpr uint32_t PF_MGROUPS = QXP_MAX * QXG_TOPK / 32 + 128;     // bound on expert m-groups
+
+// fp16 bits of a small integer (|v| < 2048: exact)
+uint16_t f16_int(int v) {
+    if (v == 0) return 0;
+    const uint16_t sign = v < 0 ? 0x8000 : 0;
+    uint32_t a = (uint32_t)(v < 0 ? -v : v);
+    int e = 31 - __builtin_clz(a);
+    const uint32_t mant = (a << (10 - e)) & 0x3ffu;
+    return (uint16_t)(sign | ((uint32_t)(e + 15) << 10) | mant);
+}
+
+bool prefill_ready(qxg_ctx *c, char *err, uint64_t n) {
+    auto &B = c->pf;
+    if (B.ready) return true;
+    auto alloc = [&](void **p, uint64_t bytes) {
+        if (!hip_ok(hipMalloc(p, bytes), err, n, "prefill buffers")) return false;
+        B.all.push_back(*p);
+        return true;
+    };
+    const uint64_t T = QXP_MAX;
+    bool ok = alloc((void **)&B.X, T * 2048 * 4) && alloc((void **)&B.X1, T * 2048 * 4) &&
+              alloc((void **)&B.XN, T * 2048 * 4) && alloc((void **)&B.QKV, T * 5120 * 4) &&
+              alloc((void **)&B.QR, T * 4096 * 4) && alloc((void **)&B.CTX, T * 4096 * 4) &&
+              alloc((void **)&B.H, (uint64_t)PF_SLOTS * QXG_FFN * 4) && alloc((void **)&B.Y, (uint64_t)PF_SLOTS * 2048 * 4) &&
+              alloc((void **)&B.rscale, (uint64_t)PF_SLOTS * 4) && alloc((void **)&B.dump, T * 2048 * 4) &&
+              alloc((void **)&B.apk, (uint64_t)PF_SLOTS * 2048 * 4) && alloc((void **)&B.lg, T * 128 * 8) &&
+              alloc((void **)&B.w, T * 8 * 8) && alloc((void **)&B.ids, T * 8 * 4) && alloc((void **)&B.tok_slot, T * 8 * 4) &&
+              alloc((void **)&B.mgroups, PF_MGROUPS * 4) && alloc((void **)&B.meta, 16) && alloc((void **)&B.tokens, T * 4) &&
+              alloc((void **)&B.slot_token, (uint64_t)PF_SLOTS * 4);
+    // codebooks: IQ2_XS / IQ3_XXS grids and the IQ4_XS byte table as fp16, sign masks
+    std::vector<uint16_t> g2(512 * 8), g3(256 * 4), sg(128 * 8);
+    std::vector<uint32_t> kv2(256);
+    for (int i = 0; i < 512; ++i)
+        for (int j = 0; j < 8; ++j) g2[i * 8 + j] = f16_int(qx_iq2xs_levels[(qx_iq2xs_packed[i] >> (2 * j)) & 3]);
+    for (int i = 0; i < 256; ++i)
+        for (int j = 0; j < 4; ++j) g3[i * 4 + j] = f16_int(qx_iq3xxs_levels[(qx_iq3xxs_packed[i] >> (3 * j)) & 7]);
+    for (uint32_t i = 0; i < 128; ++i) {
+        const uint32_t sbits = i | ((uint32_t)(__builtin_popcount(i) & 1) << 7);   // ksigns (ggml)
+        for (int j = 0; j < 8; ++j) sg[i * 8 + j] = ((sbits >> j) & 1) ? 0x8000 : 0;
+    }
+    for (uint32_t b = 0; b < 256; ++b)
+        kv2[b] = (uint32_t)f16_int(qx_iq4nl_values[b & 15]) | ((uint32_t)f16_int(qx_iq4nl_values[b >> 4]) << 16);
+    ok = ok && alloc((void **)&B.P.g2h, g2.size() * 2) && alloc((void **)&B.P.g3h, g3.size() * 2) &&
+         alloc((void **)&B.P.sgn, sg.size() * 2) && alloc((void **)&B.P.kv2, kv2.size() * 4);
+    ok = ok && hip_ok(hipMemcpy(B.P.g2h, g2.data(), g2.size() * 2, hipMemcpyHostToDevice), err, n, "prefill tables") &&
+         hip_ok(hipMemcpy(B.P.g3h, g3.data(), g3.size() * 2, hipMemcpyHostToDevice), err, n, "prefill tables") &&
+         hip_ok(hipMemcpy(B.P.sgn, sg.data(), sg.size() * 2, hipMemcpyHostToDevice), err, n, "prefill tables") &&
+         hip_ok(hipMemcpy(B.P.kv2, kv2.data(), kv2.size() * 4, hipMemcpyHostToDevice), err, n, "prefill tables");
+    if (!ok) {
+        for (void *p : B.all) (void)hipFree(p);
+        B.all.clear();
+        return false;
+    }
+    B.ready = true;
+    return true;
+}
+
+PfMat pf_mat(const QTensor *t) { return PfMat{t->p0, t->p1, t->d}; }
+
+// One layer over the T tokens of a chunk at positions p0..p0+T-1: pf.X -> pf.X (pf.X1
+// holds the attention half's result, the MoE input).  Asynchronous on c->s.
+void prefill_layer(qxg_ctx *c, uint32_t l, uint32_t T, uint32_t p0, float *moe_dump) {
+    auto &B = c->pf;
+    const LayerW &w = c->L[l];
+    hipStream_t s = c->s;
+    const uint32_t mt = (T + 31) / 32, E = c->experts;
+    const uint32_t none = 0xffffffffu;
+    // attention half: RMSNorm, Q/K/V GEMM, q/k norm + RoPE + INT8 append, attention, O GEMM + residual
+    hipLaunchKernelGGL(qxp_norm, dim3((T + 3) / 4), dim3(256), 0, s, (const float *)B.X, w.attn_norm, T, B.XN);
+    qxp_launch_pack(s, 2048, B.XN, nullptr, nullptr, mt * 32, T, B.apk, B.rscale);
+    PfGemm g{};
+    g.w[0] = pf_mat(w.wq); g.w[1] = pf_mat(w.wk); g.w[2] = pf_mat(w.wv);
+    g.w_start[0] = 0; g.w_start[1] = 4096; g.w_start[2] = 4608;
+    g.kb = 8; g.apk = B.apk; g.rscale = B.rscale; g.mtiles = mt; g.nvalid = T; g.out = B.QKV; g.ld = 5120;
+    qxp_launch_gemm(s, 0, g, B.P, 5120 / 128, mt, timer_for(c, 8));
+    hipLaunchKernelGGL(qxp_qk, dim3(T), dim3(256), 0, s, (const float *)B.QKV, w.q_norm, w.k_norm, c->T, c->kc, c->vc,
+                       c->ks, c->vs, l, c->kv_ctx, p0, B.QR);
+    hipLaunchKernelGGL(qxp_attn, dim3(32, T), dim3(256), (uint32_t)((p0 + T) * sizeof(double)), s, (const float *)B.QR,
+                       (const int8_t *)c->kc, (const int8_t *)c->vc, (const float *)c->ks, (const float *)c->vs, l,
+                       c->kv_ctx, p0, std::sqrt(128.0), B.CTX);
+    qxp_launch_pack(s, 4096, B.CTX, nullptr, nullptr, mt * 32, T, B.apk, B.rscale);
+    g = PfGemm{};
+    g.w[0] = pf_mat(w.wo); g.w_start[1] = none; g.w_start[2] = none;
+    g.kb = 16; g.apk = B.apk; g.rscale = B.rscale; g.mtiles = mt; g.nvalid = T; g.out = B.X1; g.ld = 2048;
+    g.resid = B.X;
+    qxp_launch_gemm(s, 1, g, B.P, 2048 / 128, mt, timer_for(c, 9));
+    // MoE half: RMSNorm, router logits, top-8, grouping by expert, gate/up + SwiGLU, down, combine
+    hipLaunchKernelGGL(qxp_norm, dim3((T + 3) / 4), dim3(256), 0, s, (const float *)B.X1, w.ffn_norm, T, B.XN);
+    hipLaunchKernelGGL(qxp_router, dim3((T + 15) / 16, (E + 31) / 32), dim3(256), 0, s, (const float *)B.XN, w.router, T,
+                       E, B.lg);
+    hipLaunchKernelGGL(qxp_route, dim3((T + 3) / 4), dim3(256), 0, s, (const double *)B.lg, T, E, B.ids, B.w);
+    hipLaunchKernelGGL(qxp_group, dim3(1), dim3(1024), 0, s, (const uint32_t *)B.ids, T, E, PF_EXPERT_MT, B.slot_token,
+                       B.tok_slot, B.mgroups, B.meta);
+    const uint32_t slots_ub = T * QXG_TOPK + 32 * E;        // padded slots never exceed this
+    const uint32_t mg_ub = (T * QXG_TOPK + 31) / 32 + E;      // nor the m-groups this
+    qxp_launch_pack(s, 2048, B.XN, B.slot_token, B.meta, slots_ub, none, B.apk, B.rscale);
+    g = PfGemm{};
+    g.w[0] = pf_mat(w.gate); g.w[1] = pf_mat(w.up); g.w_start[1] = none; g.w_start[2] = none;
+    g.rows = QXG_FFN; g.kb = 8; g.apk = B.apk; g.rscale = B.rscale; g.mgroups = B.mgroups; g.meta = B.meta;
+    g.out = B.H; g.ld = QXG_FFN;
+    qxp_launch_gemm(s, 2, g, B.P, QXG_FFN / 128, mg_ub, timer_for(c, 10));
+    qxp_launch_pack(s, 768, B.H, nullptr, B.meta, slots_ub, none, B.apk, B.rscale);
+    g = PfGemm{};
+    g.w[0] = pf_mat(w.down); g.w_start[1] = none; g.w_start[2] = none;
+    g.rows = 2048; g.kb = 3; g.apk = B.apk; g.rscale = B.rscale; g.mgroups = B.mgroups; g.meta = B.meta;
+    g.out = B.Y; g.ld = 2048;
+    qxp_launch_gemm(s, 3, g, B.P, 2048 / 128, mg_ub, timer_for(c, 11));
+    hipLaunchKernelGGL(qxp_combine, dim3(T), dim3(256), 0, s, (const float *)B.X1, (const float *)B.Y,
+                       (const uint32_t *)B.tok_slot, (const double *)B.w, B.X, moe_dump);
+}
 }  // namespace
 
 extern "C" {
@@ -483,6 +623,7 @@ void qxg_close(qxg_ctx *c) {
                     c->xch, c->abort};
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (void *p : c->arenas) (void)hipFree(p);
+    for (void *p : c->pf.all) (void)hipFree(p);
     for (hipEvent_t e : c->kt.ev) (void)hipEventDestroy(e);
     if (c->e0) (void)hipEventDestroy(c->e0);
     if (c->e1) (void)hipEventDestroy(c->e1);
@@ -902,6 +1043,82 @@ int qxg_set_layer_path(qxg_ctx *c, int persistent) {
         drop_graph(c);
         c->persist = persistent != 0;
     }
+    return 1;
+}
+
+int qxg_prefill(qxg_ctx *c, const uint32_t *tokens, uint32_t n, uint32_t position0, int run_head, float *residual_out,
+                float *logits, uint32_t top_n, uint32_t *top_ids, double *top_logits, float *elapsed_ms, char *err,
+                uint64_t err_len) {
+    if (!check_ready(c, true, err, err_len)) return 0;
+    if (!c->emb) { set_err(err, err_len, "token_embd.weight not bound"); return 0; }
+    if (run_head && !c->head) { set_err(err, err_len, "head not bound"); return 0; }
+    if (!tokens || !n) { set_err(err, err_len, "prefill needs >= 1 token"); return 0; }
+    if ((uint64_t)position0 + n > c->kv_ctx || c->layers > c->kv_layers) { set_err(err, err_len, "prefill exceeds the KV context"); return 0; }
+    for (uint32_t i = 0; i < n; ++i)
+        if (tokens[i] >= c->vocab) { set_err(err, err_len, "prompt token out of range"); return 0; }
+    if (top_n == 0) top_n = 1;
+    if (top_n > QXG_MAX_TOPN) top_n = QXG_MAX_TOPN;
+    (void)hipSetDevice(c->device);
+    if (!prefill_ready(c, err, err_len)) return 0;
+    auto &B = c->pf;
+    c->kt.used = 0;
+    if (!hip_ok(hipMemcpy(B.tokens, tokens, 4ull * (n < QXP_MAX ? n : QXP_MAX), hipMemcpyHostToDevice), err, err_len, "tokens"))
+        return 0;
+    (void)hipEventRecord(c->e0, c->s);
+    for (uint32_t c0 = 0; c0 < n; c0 += QXP_MAX) {
+        const uint32_t T = n - c0 < QXP_MAX ? n - c0 : QXP_MAX;
+        if (c0) {   // earlier chunks are done with the token buffer once the stream reaches this copy
+            if (!hip_ok(hipStreamSynchronize(c->s), err, err_len, "stream") ||
+                !hip_ok(hipMemcpy(B.tokens, tokens + c0, 4ull * T, hipMemcpyHostToDevice), err, err_len, "tokens"))
+                return 0;
+        }
+        hipLaunchKernelGGL(qxp_embed, dim3(T), dim3(256), 0, c->s, c->emb, c->emb_row, (const uint32_t *)B.tokens, B.X);
+        for (uint32_t l = 0; l < c->layers; ++l) prefill_layer(c, l, T, position0 + c0, nullptr);
+        if (residual_out &&
+            !hip_ok(hipMemcpyAsync(residual_out + 2048ull * c0, B.X, 2048ull * 4 * T, hipMemcpyDeviceToHost, c->s), err, err_len, "read"))
+            return 0;
+        if (c0 + T == n && run_head) {
+            (void)hipMemcpyAsync(c->x, B.X + 2048ull * (T - 1), 2048 * 4, hipMemcpyDeviceToDevice, c->s);
+            write_state(c, position0 + n - 1, 0, 1, 1);
+            launch_head(c, top_n, nullptr);
+        }
+    }
+    (void)hipEventRecord(c->e1, c->s);
+    if (!finish(c, err, err_len)) return 0;
+    if (elapsed_ms) (void)hipEventElapsedTime(elapsed_ms, c->e0, c->e1);
+    if (!run_head) return 1;
+    DevState h;
+    if (!read_state(c, h, err, err_len)) return 0;
+    if (logits && !hip_ok(hipMemcpy(logits, c->logits, (uint64_t)c->vocab * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    float tv[QXG_MAX_TOPN];
+    uint32_t ti[QXG_MAX_TOPN];
+    if (!hip_ok(hipMemcpy(tv, c->top_v, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read") ||
+        !hip_ok(hipMemcpy(ti, c->top_i, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    for (uint32_t i = 0; i < top_n; ++i) {
+        if (top_ids) top_ids[i] = ti[i];
+        if (top_logits) top_logits[i] = (double)tv[i];
+    }
+    if (h.nonfinite) { write_state(c, 0, 0, 0, 0); set_err(err, err_len, "non-finite final logit"); return 0; }
+    return 1;
+}
+
+int qxg_prefill_layer(qxg_ctx *c, uint32_t layer, uint32_t n, uint32_t position0, const float *x_in, float *ffn_inp_out,
+                      float *moe_out, float *x_out, char *err, uint64_t err_len) {
+    if (!check_ready(c, true, err, err_len)) return 0;
+    if (!x_in || !n || n > QXP_MAX || layer >= c->layers || layer >= c->kv_layers || (uint64_t)position0 + n > c->kv_ctx) {
+        set_err(err, err_len, "invalid prefill layer argument");
+        return 0;
+    }
+    (void)hipSetDevice(c->device);
+    if (!prefill_ready(c, err, err_len)) return 0;
+    auto &B = c->pf;
+    c->kt.used = 0;
+    if (!hip_ok(hipMemcpyAsync(B.X, x_in, 2048ull * 4 * n, hipMemcpyHostToDevice, c->s), err, err_len, "upload")) return 0;
+    prefill_layer(c, layer, n, position0, moe_out ? B.dump : nullptr);
+    if (!finish(c, err, err_len)) return 0;
+    if (ffn_inp_out && !hip_ok(hipMemcpy(ffn_inp_out, B.X1, 2048ull * 4 * n, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (moe_out && !hip_ok(hipMemcpy(moe_out, B.dump, 2048ull * 4 * n, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (x_out && !hip_ok(hipMemcpy(x_out, B.X, 2048ull * 4 * n, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
     return 1;
 }
 

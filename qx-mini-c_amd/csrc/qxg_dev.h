@@ -201,6 +201,28 @@ DEV float dot_q6(uint4 ql0, uint4 ql1, uint4 qh0, uint4 qh1, int sc0, int sc1, u
     return (fp16_exact(d16) * g.s) * v;
 }
 
+// Q4_K embedding row (8 blocks) -> 2048 floats (reference src/qx_format.c:2079-2110,
+// 3759-3793); 256 threads, thread (b, l) produces 8 values of block b.
+DEV void embed_q4k_row(const uint8_t *row, float *x) {
+    const int b = threadIdx.x >> 5, l = threadIdx.x & 31;
+    const uint8_t *blk = row + 144 * b;
+    const float d = fp16_exact(blk[0] | (blk[1] << 8)), dmin = fp16_exact(blk[2] | (blk[3] << 8));
+    const uint8_t *sc = blk + 4, *q = blk + 16;
+    for (int j = 0; j < 4; ++j) {
+        uint32_t s0, m0, s1, m1;
+        const int i0 = 2 * j, i1 = 2 * j + 1;
+        if (i0 < 4) { s0 = sc[i0] & 63u; m0 = sc[i0 + 4] & 63u; }
+        else { s0 = (sc[i0 + 4] & 15u) | ((uint32_t)(sc[i0 - 4] >> 6) << 4); m0 = (sc[i0 + 4] >> 4) | ((uint32_t)(sc[i0] >> 6) << 4); }
+        if (i1 < 4) { s1 = sc[i1] & 63u; m1 = sc[i1 + 4] & 63u; }
+        else { s1 = (sc[i1 + 4] & 15u) | ((uint32_t)(sc[i1 - 4] >> 6) << 4); m1 = (sc[i1 + 4] >> 4) | ((uint32_t)(sc[i1] >> 6) << 4); }
+        const float d1 = d * (float)s0, mm1 = dmin * (float)m0;
+        const float d2 = d * (float)s1, mm2 = dmin * (float)m1;
+        const uint8_t qq = q[32 * j + l];
+        x[256 * b + 64 * j + l] = d1 * (float)(qq & 15) - mm1;
+        x[256 * b + 64 * j + 32 + l] = d2 * (float)(qq >> 4) - mm2;
+    }
+}
+
 // ---------------------------------------------------------------- prologues
 DEV void load32(const float *p, float *v) {
     const float4 *q = reinterpret_cast<const float4 *>(p);

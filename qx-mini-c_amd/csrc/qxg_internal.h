@@ -98,6 +98,42 @@ struct QxPArgs {
     double sqrt_hd;
 };
 
+// ---- batched prefill (qxg_prefill.hip)
+#define QXP_MAX 512   // tokens per prefill chunk
+
+// fp16 codebooks of the prefill GEMMs (built on the host at first use)
+struct PfTables {
+    uint4 *g2h;      // IQ2_XS grid: 512 x 8 fp16 values
+    uint2 *g3h;      // IQ3_XXS grid: 256 x 4 fp16 values
+    uint4 *sgn;      // 7-bit sign index -> 8 fp16 sign masks (0x8000 where negative)
+    uint32_t *kv2;   // IQ4_XS byte -> {fp16 kvalue[low nibble], fp16 kvalue[high nibble]}
+};
+
+// One quantized matrix [rows x K] in the repacked layout (expert e's rows follow e*rows).
+struct PfMat {
+    const uint8_t *qs, *p1;   // qs plane; IQ4_XS meta / IQ2_XS scales / IQ3_XXS aux
+    const uint16_t *d;        // fp16 d per block (IQ2_XS, IQ3_XXS)
+};
+
+// Arguments of one prefill GEMM launch: Y[row][col] = sum_k A[row][k] * W[col][k], A the
+// packed activations (rows = tokens or expert slots), W up to three matrices stacked
+// along the output columns (Q, K, V) or, for the expert GEMMs, expert e's slice.
+struct PfGemm {
+    PfMat w[3];
+    uint32_t w_start[3];       // first output column of each stacked matrix
+    uint32_t rows;             // rows of one expert's matrix (expert GEMMs)
+    uint32_t kb;               // 256-value blocks per matrix row (K / 256)
+    const uint4 *apk;          // packed activations
+    const float *rscale;       // per packed row: 1/s, 0 for a non-finite row
+    const uint32_t *mgroups;   // expert GEMMs: {expert, first m-tile, m-tiles}; null: dense
+    const uint32_t *meta;      // expert GEMMs: meta[0] = number of m-groups
+    uint32_t mtiles, nvalid;   // dense: m-tiles of 32 rows, valid rows
+    float *out;                // output rows of ld floats
+    uint32_t ld;
+    const float *resid;        // residual added by the O projection epilogue
+    float *dump;               // O projection output without the residual (optional)
+};
+
 // Optional start/stop events recorded around one launch on its stream.  Created with
 // hipEventDisableSystemFence, the markers skip the system-scope cache writeback, so
 // their elapsed time stays close to the kernel's own duration.

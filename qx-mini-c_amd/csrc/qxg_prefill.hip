@@ -1,0 +1,643 @@
+// Batched prefill (CDNA4, gfx950): the T tokens of a prompt chunk go through each
+// layer together.  The reference runs a prompt one token at a time through its
+// decode step (src/qx_format.c:6250-6547 of the reference); here every projection
+// and every expert matrix is one GEMM over the tokens (or over the tokens routed to
+// that expert) on the matrix cores.
+//
+// Precision scheme of the GEMMs (fp16 MFMA 32x32x16, f32 accumulation).  Every
+// weight of the formats used is, exactly,
+//     IQ2_XS   w = (d/8) * [(2s+1) * grid * sign]        |code| <= 31*43 = 1333
+//     IQ3_XXS  w = (d/4) * [(2a+1) * grid * sign]        |code| <= 31*62 = 1922
+//     IQ4_XS   w = (d*(ls-32)) * kvalue                  |code| <= 127
+// (the f32 products the reference forms, src/qx_format.c:1914-2053, are exact), and
+// each bracketed integer code is exact in fp16.  Each activation row is scaled by a
+// power of two s (max |x*s| in [2^13, 2^14)) and split as x*s = hi + lo (+ e), hi and
+// lo fp16, |e| <= 2^-22 |x*s|.  A code times an fp16 value is exact in f32; the matrix
+// cores sum the products in f32 over one block (IQ2_XS, IQ3_XXS: 256 values) or one
+// group (IQ4_XS: 32 values), that partial sum is multiplied by its f32 scale once, and
+// the row result is divided by s.  The integer codes come from fp16 codebooks in LDS.
+//
+// MFMA operand layout (v_mfma_f32_32x32x16_f16): lane l holds, for A, row l%32 and
+// k = 8*(l/32) + j (j < 8); for B, column l%32 and the same k; result register r of
+// lane l is (row 8*(r/4) + 4*(l/32) + r%4, column l%32).  Rows are tokens (or expert
+// slots), columns are weight rows, so each lane's results share one weight row and
+// its scale.  Activations are packed once per GEMM in exactly this fragment order:
+//     apk[((mtile * KS + kstep) * 2 + piece) * 64 + lane] = 8 fp16 values (uint4).
+#include "qxg_dev.h"
+
+namespace {
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+
+enum { FMT_IQ4 = 0, FMT_IQ2 = 1, FMT_IQ3 = 2 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+
+DEV f16x mfma(uint4 a, uint4 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, a), __builtin_bit_cast(h8v, b), c, 0, 0, 0);
+}
+
+DEV uint32_t hmul2(uint32_t v, h2v m) { return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, v) * m); }
+DEV uint4 hmul8(uint4 v, uint32_t mul) {
+    const _Float16 f = (_Float16)(float)mul;   // 1..31: exact
+    const h2v m = {f, f};
+    return make_uint4(hmul2(v.x, m), hmul2(v.y, m), hmul2(v.z, m), hmul2(v.w, m));
+}
+DEV uint32_t comp(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+// ---------------------------------------------------------------- weight blocks per lane
+// The lane's share of one 256-value block of its weight row: lane half h = l/32 takes
+// k = 16*s + 8*h + j of every k-step s (16 per block).
+template <int F> struct Blk;
+template <> struct Blk<FMT_IQ2> { uint4 q[4]; uint2 sc; uint32_t d; };    // qs (32 x u16), scales, d
+template <> struct Blk<FMT_IQ3> { uint4 q[4]; uint4 a[2]; uint32_t d; };  // qs (64 x u8), aux (8 x u32), d
+template <> struct Blk<FMT_IQ4> { uint2 q[8]; uint2 m; };                 // qs bytes 16ib+8h..+8, meta
+
+DEV void blk_load(Blk<FMT_IQ2> &b, const PfMat &w, uint64_t bi, int) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(w.qs + bi * 64);
+    b.q[0] = p[0]; b.q[1] = p[1]; b.q[2] = p[2]; b.q[3] = p[3];
+    b.sc = *reinterpret_cast<const uint2 *>(w.p1 + bi * 8);
+    b.d = w.d[bi];
+}
+DEV void blk_load(Blk<FMT_IQ3> &b, const PfMat &w, uint64_t bi, int) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(w.qs + bi * 64);
+    b.q[0] = p[0]; b.q[1] = p[1]; b.q[2] = p[2]; b.q[3] = p[3];
+    const uint4 *a = reinterpret_cast<const uint4 *>(w.p1 + bi * 32);
+    b.a[0] = a[0]; b.a[1] = a[1];
+    b.d = w.d[bi];
+}
+DEV void blk_load(Blk<FMT_IQ4> &b, const PfMat &w, uint64_t bi, int h) {
+    const uint8_t *q = w.qs + bi * 128 + 8 * h;
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) b.q[ib] = *reinterpret_cast<const uint2 *>(q + 16 * ib);
+    b.m = *reinterpret_cast<const uint2 *>(w.p1 + bi * 8);
+}
+
+// B fragment of k-step s (8 fp16 codes).  IQ2_XS (src/qx_format.c:1914-1933): element
+// 32ib+8l+j = db(l<2 ? lo : hi nibble of scales[ib]) * grid[q&511][j] * sign, q = qs[4ib+l];
+// k-step s = 2ib + l/2, so q = qs[2s + h] and the nibble is s&1.
+DEV uint4 frag(const Blk<FMT_IQ2> &b, int s, int h, const uint4 *G2, const uint4 *SG, const uint32_t *) {
+    const uint32_t q = (comp(b.q[s >> 2], s & 3) >> (16 * h)) & 0xffffu;
+    const uint32_t scb = ((s >> 1) < 4 ? b.sc.x : b.sc.y) >> (8 * ((s >> 1) & 3));
+    const uint32_t nib = (scb >> (4 * (s & 1))) & 15u;
+    uint4 g = G2[q & 511u];
+    const uint4 m = SG[q >> 9];
+    g.x ^= m.x; g.y ^= m.y; g.z ^= m.z; g.w ^= m.w;
+    return hmul8(g, 2u * nib + 1u);
+}
+// IQ3_XXS (src/qx_format.c:1935-1959): element 32ib+8l+j (j<4) from grid3[qs[8ib+2l]],
+// j>=4 from grid3[qs[8ib+2l+1]], signs ksigns[(aux[ib] >> 7l) & 127], scale
+// d*(2(aux>>28)+1)/4; k-step s = 2ib + l/2.
+DEV uint4 frag(const Blk<FMT_IQ3> &b, int s, int h, const uint4 *, const uint4 *SG, const uint32_t *G3) {
+    const int ib = s >> 1, l = 2 * (s & 1) + h;
+    const uint32_t dw = comp(b.q[ib >> 1], (2 * ib + (s & 1)) & 3) >> (16 * h);
+    const uint32_t aux = comp(b.a[ib >> 2], ib & 3);
+    const uint2 g1 = reinterpret_cast<const uint2 *>(G3)[dw & 255u];
+    const uint2 g2 = reinterpret_cast<const uint2 *>(G3)[(dw >> 8) & 255u];
+    const uint4 m = SG[(aux >> (7 * l)) & 127u];
+    const uint4 g = make_uint4(g1.x ^ m.x, g1.y ^ m.y, g2.x ^ m.z, g2.y ^ m.w);
+    return hmul8(g, 2u * (aux >> 28) + 1u);
+}
+// IQ4_XS (src/qx_format.c:2032-2053): element 32ib+j = kvalue[qs[16ib+j] & 15],
+// 32ib+16+j = kvalue[qs[16ib+j] >> 4]; k-step 2ib takes the low nibbles of the lane's
+// 8 bytes, 2ib+1 the high nibbles.
+DEV uint4 frag(const Blk<FMT_IQ4> &b, int s, int, const uint4 *, const uint4 *, const uint32_t *KV2) {
+    const uint2 q = b.q[s >> 1];
+    uint32_t p[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        p[j] = KV2[(q.x >> (8 * j)) & 255u];
+        p[4 + j] = KV2[(q.y >> (8 * j)) & 255u];
+    }
+    const uint32_t sel = (s & 1) ? 0x07060302u : 0x05040100u;
+    return make_uint4(perm(p[1], p[0], sel), perm(p[3], p[2], sel), perm(p[5], p[4], sel), perm(p[7], p[6], sel));
+}
+// f32 scale of the partial sums: the block's d/8 or d/4; IQ4_XS: group ib's d*(ls-32)
+DEV float blk_scale(const Blk<FMT_IQ2> &b, int) { return fp16_exact(b.d) * 0.125f; }
+DEV float blk_scale(const Blk<FMT_IQ3> &b, int) { return fp16_exact(b.d) * 0.25f; }
+DEV float blk_scale(const Blk<FMT_IQ4> &b, int ib) {
+    const uint32_t sh = b.m.x >> 16, sl = (b.m.y >> (8 * (ib >> 1))) & 255u;
+    const int ls = (int)(((sl >> (4 * (ib & 1))) & 15u) | (((sh >> (2 * ib)) & 3u) << 4));
+    return fp16_exact(b.m.x & 0xffffu) * (float)(ls - 32);
+}
+
+DEV f16x zero16() {
+    f16x z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+    return z;
+}
+}  // namespace
+
+// ================================================================= GEMM
+// One wave: NSUB column tiles of 32 weight rows x MT row tiles of 32 tokens/slots, over
+// all of K.  GU: the two column tiles are gate and up at the same rows (SwiGLU epilogue).
+// Workgroup = 4 waves on 4 consecutive column tiles of the same row tiles.
+template <int F, int NSUB, int MT, int EPI>
+__global__ __launch_bounds__(256, 2) void qxp_gemm(PfGemm g, PfTables P) {
+    constexpr bool GU = EPI == EPI_SWIGLU;
+    uint32_t e = 0, mt0, nmt;
+    if (g.mgroups) {
+        if (blockIdx.y >= g.meta[0]) return;   // whole workgroup
+        const uint32_t mg = g.mgroups[blockIdx.y];
+        e = mg & 255u; mt0 = (mg >> 8) & 0xfffu; nmt = mg >> 20;
+    } else {
+        mt0 = blockIdx.y * MT;
+        nmt = min((uint32_t)MT, g.mtiles - mt0);
+    }
+    __shared__ uint4 s_g2[F == FMT_IQ2 ? 512 : 1];
+    __shared__ uint4 s_sg[F == FMT_IQ4 ? 1 : 128];
+    __shared__ uint32_t s_t[F == FMT_IQ3 ? 512 : F == FMT_IQ4 ? 256 : 1];
+    const int tid = threadIdx.x;
+    if (F == FMT_IQ2) { s_g2[tid] = P.g2h[tid]; s_g2[tid + 256] = P.g2h[tid + 256]; }
+    if (F != FMT_IQ4 && tid < 128) s_sg[tid] = P.sgn[tid];
+    if (F == FMT_IQ3) { s_t[tid] = reinterpret_cast<const uint32_t *>(P.g3h)[tid];
+                        s_t[tid + 256] = reinterpret_cast<const uint32_t *>(P.g3h)[tid + 256]; }
+    if (F == FMT_IQ4) s_t[tid] = P.kv2[tid];
+    __syncthreads();
+
+    const int lane = tid & 63, wave = wave_id(), h = lane >> 5, col = lane & 31;
+    const uint32_t KB = g.kb, KS = 16 * KB;
+    const uint32_t nt = blockIdx.x * 4 + wave;            // column tile group of this wave
+    const uint32_t c0 = GU ? 32 * nt : 32 * NSUB * nt;     // first output column
+    // matrix and row of each column tile (stacked matrices: uniform per wave)
+    PfMat W[NSUB];
+    uint64_t rowblk[NSUB];
+#pragma unroll
+    for (int n = 0; n < NSUB; ++n) {
+        const uint32_t c = GU ? c0 : c0 + 32 * n;
+        const int mi = GU ? n : (c >= g.w_start[2] ? 2 : c >= g.w_start[1] ? 1 : 0);
+        W[n] = g.w[mi];
+        const uint32_t r = (GU ? c0 : c - g.w_start[mi]) + col;
+        rowblk[n] = ((uint64_t)e * g.rows + r) * KB;
+    }
+    const uint4 *A = g.apk + (uint64_t)mt0 * KS * 128 + lane;
+
+    f16x acc[NSUB][MT], G[NSUB][MT];
+#pragma unroll
+    for (int n = 0; n < NSUB; ++n)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[n][m] = zero16();
+    Blk<F> cur[NSUB];
+#pragma unroll
+    for (int n = 0; n < NSUB; ++n) blk_load(cur[n], W[n], rowblk[n], h);
+
+#pragma unroll 1
+    for (uint32_t kb = 0; kb < KB; ++kb) {
+        Blk<F> nxt[NSUB];
+        if (kb + 1 < KB) {
+#pragma unroll
+            for (int n = 0; n < NSUB; ++n) blk_load(nxt[n], W[n], rowblk[n] + kb + 1, h);
+        }
+#pragma unroll
+        for (int n = 0; n < NSUB; ++n)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) G[n][m] = zero16();
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            uint4 ah[MT], al[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (m < (int)nmt) {
+                    const uint4 *p = A + ((uint64_t)m * KS + kb * 16 + s) * 128;
+                    ah[m] = p[0];
+                    al[m] = p[64];
+                }
+            }
+#pragma unroll
+            for (int n = 0; n < NSUB; ++n) {
+                const uint4 b = frag(cur[n], s, h, s_g2, s_sg, s_t);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    if (m < (int)nmt) {
+                        G[n][m] = mfma(ah[m], b, G[n][m]);
+                        G[n][m] = mfma(al[m], b, G[n][m]);
+                    }
+                }
+            }
+            if (F == FMT_IQ4 && (s & 1)) {
+#pragma unroll
+                for (int n = 0; n < NSUB; ++n) {
+                    const float sc = blk_scale(cur[n], s >> 1);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[n][m][r] = fmaf(sc, G[n][m][r], acc[n][m][r]);
+                        G[n][m] = zero16();
+                    }
+                }
+            }
+        }
+        if (F != FMT_IQ4) {
+#pragma unroll
+            for (int n = 0; n < NSUB; ++n) {
+                const float sc = blk_scale(cur[n], 0);
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[n][m][r] = fmaf(sc, G[n][m][r], acc[n][m][r]);
+            }
+        }
+        if (kb + 1 < KB) {
+#pragma unroll
+            for (int n = 0; n < NSUB; ++n) cur[n] = nxt[n];
+        }
+    }
+
+    // epilogue: lane's column c, rows 8*(r/4) + 4h + r%4 of each row tile
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m >= (int)nmt) continue;
+        const uint32_t rbase = (mt0 + m) * 32 + 4 * h;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t row = rbase + 8 * (r >> 2) + (r & 3);
+            if (!g.mgroups && row >= g.nvalid) continue;
+            const float rs = g.rscale[row];
+            if (EPI == EPI_SWIGLU) {
+                float gv = acc[0][m][r] * rs, uv = acc[1][m][r] * rs;
+                gv = isfinite(gv) ? gv : 0.0f;
+                uv = isfinite(uv) ? uv : 0.0f;
+                const double sg = (double)gv / (1.0 + exp(-(double)gv));   // qx_silu, src/qx_format.c:2511-2513
+                g.out[(uint64_t)row * g.ld + c0 + col] = (float)(sg * (double)uv);
+            } else {
+#pragma unroll
+                for (int n = 0; n < NSUB; ++n) {
+                    const uint32_t c = c0 + 32 * n + col;
+                    float y = acc[n][m][r] * rs;
+                    y = isfinite(y) ? y : 0.0f;   // non-finite projection outputs -> 0 (src/qx_format.c:4284)
+                    const uint64_t o = (uint64_t)row * g.ld + c;
+                    if (EPI == EPI_RESID) {
+                        if (g.dump) g.dump[o] = y;
+                        g.out[o] = g.resid[o] + y;
+                    } else {
+                        g.out[o] = y;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ================================================================= element-wise stages
+// Q4_K embedding rows of tokens[0..T) (src/qx_format.c:3759-3793); block per token.
+extern "C" __global__ __launch_bounds__(256) void qxp_embed(const uint8_t *emb, uint64_t row_bytes,
+                                                            const uint32_t *tokens, float *x) {
+    embed_q4k_row(emb + (uint64_t)tokens[blockIdx.x] * row_bytes, x + (uint64_t)blockIdx.x * 2048);
+}
+
+// RMSNorm of each token's 2048-vector (qx_apply_f32_rmsnorm, src/qx_format.c:3358-3371);
+// wave per token.
+extern "C" __global__ __launch_bounds__(256) void qxp_norm(const float *x, const float *w, uint32_t T, float *y) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.x * 4 + wave_id();
+    if (t >= T) return;
+    float v[32], ww[32];
+    load32(x + (uint64_t)t * 2048 + 32 * lane, v);
+    load32(w + 32 * lane, ww);
+    rmsnorm32(v, ww);
+    float4 *o = reinterpret_cast<float4 *>(y + (uint64_t)t * 2048 + 32 * lane);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+
+// Packs row r of the A operand (r < nrows[1] when nrows is non-null): source row
+// map ? map[r] : r of src (K floats; rows r >= nvalid and negative map entries are
+// padding and pack zeros),
+// scaled by a power of two and split into fp16 hi/lo fragments; rscale[r] = 1/s, or 0
+// (and zeros) when the row has a non-finite value.  Block per row, 8 values per chunk.
+template <int K>
+__global__ __launch_bounds__(256) void qxp_pack(const float *src, const int32_t *map, const uint32_t *nrows,
+                                                uint32_t nvalid, uint4 *apk, float *rscale) {
+    constexpr int CH = K / 8, PER = (CH + 255) / 256, KS = K / 16;
+    const uint32_t r = blockIdx.x;
+    if (nrows && r >= nrows[1]) return;
+    __shared__ float red[4];
+    __shared__ uint32_t bad[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int32_t sr = r >= nvalid ? -1 : map ? map[r] : (int32_t)r;
+    float v[PER][8];
+    float mx = 0.0f;
+    bool fin = true;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int c = tid + 256 * i;
+        if (c < CH && sr >= 0) {
+            const float4 *p = reinterpret_cast<const float4 *>(src + (uint64_t)sr * K + 8 * c);
+            const float4 a = p[0], b = p[1];
+            v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+            v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            fin = fin && isfinite(v[i][j]);
+            mx = fmaxf(mx, fabsf(v[i][j]));
+        }
+    }
+    const uint64_t nb = __ballot(!fin);
+    if (lane == 0) bad[wave] = nb != 0;
+    mx = block_max256(mx, red);   // barriers order the bad[] writes too
+    const bool ok = !(bad[0] | bad[1] | bad[2] | bad[3]);
+    int ex = 0;
+    if (mx > 0.0f && ok) (void)frexpf(mx, &ex);   // mx = f * 2^ex, f in [0.5, 1)
+    int sh = 14 - ex;
+    sh = sh > 100 ? 100 : sh < -100 ? -100 : sh;
+    const float sc = ldexpf(1.0f, sh);
+    if (tid == 0) rscale[r] = ok ? ldexpf(1.0f, -sh) : 0.0f;
+    const uint32_t mt = r >> 5, i32 = r & 31;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int c = tid + 256 * i;
+        if (c >= CH) continue;
+        h8v hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float y = ok ? v[i][j] * sc : 0.0f;
+            const _Float16 a = (_Float16)y;
+            hi[j] = a;
+            lo[j] = (_Float16)(y - (float)a);
+        }
+        const uint64_t base = ((uint64_t)mt * KS + (c >> 1)) * 128 + i32 + 32 * (c & 1);
+        apk[base] = __builtin_bit_cast(uint4, hi);
+        apk[base + 64] = __builtin_bit_cast(uint4, lo);
+    }
+}
+
+// Per token (block): q/k head RMSNorm (src/qx_format.c:3740-3757) and RoPE at position
+// p0+t (4625-4641), INT8 quantization of K and V over all 512 values (4449-4463) into
+// the cache row [layer][p0+t]; the roped q (f32) goes to qr for attention.
+extern "C" __global__ __launch_bounds__(256) void qxp_qk(const float *qkv, const float *q_norm, const float *k_norm,
+        Tables T, int8_t *kc, int8_t *vc, float *ks, float *vs, uint32_t layer, uint32_t ctx, uint32_t p0, float *qr) {
+    __shared__ float s_k[512], s_v[512];
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const uint32_t t = blockIdx.x, pos = p0 + t;
+    const float *row = qkv + (uint64_t)t * 5120;
+    float k0 = row[4096 + 128 * wave + lane], k1 = row[4096 + 128 * wave + 64 + lane];
+    const float v0 = row[4608 + tid], v1 = row[4608 + 256 + tid];
+    const float kw0 = k_norm[lane], kw1 = k_norm[64 + lane], qw0 = q_norm[lane], qw1 = q_norm[64 + lane];
+    const double c = T.rope_cos[pos * 64 + lane], s = T.rope_sin[pos * 64 + lane];
+    head_norm_rope_wave(k0, k1, kw0, kw1, c, s);
+    s_k[128 * wave + lane] = k0;
+    s_k[128 * wave + 64 + lane] = k1;
+    s_v[tid] = v0;
+    s_v[256 + tid] = v1;
+#pragma unroll 1
+    for (int hh = 0; hh < 8; ++hh) {
+        const int qh = 8 * wave + hh;
+        float q0 = row[128 * qh + lane], q1 = row[128 * qh + 64 + lane];
+        head_norm_rope_wave(q0, q1, qw0, qw1, c, s);
+        qr[(uint64_t)t * 4096 + 128 * qh + lane] = q0;
+        qr[(uint64_t)t * 4096 + 128 * qh + 64 + lane] = q1;
+    }
+    float ka, va;
+    {
+        const float a0 = isfinite(k0) ? fabsf(k0) : 0.0f, a1 = isfinite(k1) ? fabsf(k1) : 0.0f;
+        ka = fmaxf(a0, a1);
+        const float b0 = isfinite(v0) ? fabsf(v0) : 0.0f, b1 = isfinite(v1) ? fabsf(v1) : 0.0f;
+        va = fmaxf(b0, b1);
+    }
+    ka = block_max256(ka, red);
+    va = block_max256(va, red);
+    const float kscale = ka > 0.0f ? ka / 127.0f : 1.0f, vscale = va > 0.0f ? va / 127.0f : 1.0f;
+    const uint64_t slot = (uint64_t)layer * ctx + pos;
+    for (int i = tid; i < 512; i += 256) {
+        const float kx = s_k[i], vx = s_v[i];
+        int qk = isfinite(kx) ? (int)rintf(kx / kscale) : 0;
+        int qv = isfinite(vx) ? (int)rintf(vx / vscale) : 0;
+        qk = qk < -127 ? -127 : qk > 127 ? 127 : qk;
+        qv = qv < -127 ? -127 : qv > 127 ? 127 : qv;
+        kc[slot * 512 + i] = (int8_t)qk;
+        vc[slot * 512 + i] = (int8_t)qv;
+    }
+    if (tid == 0) { ks[slot] = kscale; vs[slot] = vscale; }
+}
+
+// Causal GQA attention of token t (blockIdx.y) and q head blockIdx.x over cached
+// positions 0..p0+t (qx_rope_gqa_attention_partial, src/qx_format.c:5051-5196): double
+// scores, double softmax, f32 context per position in position order within each of
+// two position halves -- the decode kernel's order.
+extern "C" __global__ __launch_bounds__(256) void qxp_attn(const float *qr, const int8_t *kc, const int8_t *vc,
+        const float *ks, const float *vs, uint32_t layer, uint32_t ctx, uint32_t p0, double sqrt_hd, float *ctx_out) {
+    extern __shared__ double s_sc[];
+    __shared__ double s_q[128];
+    __shared__ double redd[4];
+    __shared__ float s_part[2][128];
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int qh = blockIdx.x, kvh = qh >> 3;
+    const uint32_t t = blockIdx.y, pos = p0 + t, n = pos + 1;
+    const uint64_t base = (uint64_t)layer * ctx;
+    if (tid < 128) s_q[tid] = (double)qr[(uint64_t)t * 4096 + 128 * qh + tid];
+    __syncthreads();
+    {
+        const int sub = lane >> 4, dl = lane & 15;
+        double qd[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qd[j] = s_q[8 * dl + j];
+        for (uint32_t t0 = 4 * wave; t0 < n; t0 += 16) {
+            const uint32_t tt = t0 + sub;
+            double acc = 0.0;
+            if (tt < n) {
+                const uint2 kk = *reinterpret_cast<const uint2 *>(kc + (base + tt) * 512 + kvh * 128 + 8 * dl);
+                const float ksc = ks[base + tt];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int8_t kb = (int8_t)(((j < 4 ? kk.x : kk.y) >> (8 * (j & 3))) & 255u);
+                    acc += qd[j] * (double)((float)kb * ksc);
+                }
+            }
+            acc = row16_sum_d(acc);
+            if (tt < n && dl == 0) {
+                double sc = acc / sqrt_hd;
+                if (!isfinite(sc)) sc = 0.0;
+                s_sc[tt] = sc;
+            }
+        }
+    }
+    __syncthreads();
+    double mx = -1.0e300;
+    for (uint32_t i = tid; i < n; i += 256) mx = fmax(mx, s_sc[i]);
+    mx = wave_max_d(mx);
+    if (lane == 0) redd[wave] = mx;
+    __syncthreads();
+    mx = fmax(fmax(redd[0], redd[1]), fmax(redd[2], redd[3]));
+    double den = 0.0;
+    for (uint32_t i = tid; i < n; i += 256) {
+        const double e = exp(s_sc[i] - mx);
+        s_sc[i] = e;
+        den += e;
+    }
+    den = wave_total_d(den);
+    __syncthreads();
+    if (lane == 0) redd[wave] = den;
+    __syncthreads();
+    den = (redd[0] + redd[1]) + (redd[2] + redd[3]);
+    if (!isfinite(den) || den <= 0.0) den = 1.0;
+    const int d = tid & 127, hf = tid >> 7;
+    const uint32_t ta = hf ? n / 2 : 0, tb = hf ? n : n / 2;
+    float acc = 0.0f;
+    for (uint32_t i = ta; i < tb; ++i) {
+        const double wgt = s_sc[i] / den;
+        const float vv = (float)vc[(base + i) * 512 + kvh * 128 + d] * vs[base + i];
+        acc += (float)(wgt * (double)vv);
+    }
+    s_part[hf][d] = acc;
+    __syncthreads();
+    if (tid < 128) ctx_out[(uint64_t)t * 4096 + qh * 128 + tid] = s_part[0][tid] + s_part[1][tid];
+}
+
+// Router logits of 16 tokens x 32 experts per block: logit[t][e] = sum_i
+// (double)W[e][i] * (double)xn[t][i], i ascending (src/qx_format.c:5254-5264: the same
+// products and the same order of additions as the reference).  Tiles of 256 values of
+// x and W are staged in LDS.
+extern "C" __global__ __launch_bounds__(256) void qxp_router(const float *xn, const float *router, uint32_t T,
+                                                             uint32_t experts, double *logits) {
+    __shared__ float sx[16][257], sw[32][257];
+    const int tid = threadIdx.x, ti = tid >> 4, ej = tid & 15;
+    const uint32_t t0 = blockIdx.x * 16, e0 = blockIdx.y * 32;
+    double a0 = 0.0, a1 = 0.0;
+#pragma unroll 1
+    for (int k0 = 0; k0 < 2048; k0 += 256) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int idx = tid + 256 * i, rr = idx >> 8, kk = idx & 255;
+            sx[rr][kk] = (t0 + rr < T) ? xn[(uint64_t)(t0 + rr) * 2048 + k0 + kk] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int idx = tid + 256 * i, rr = idx >> 8, kk = idx & 255;
+            sw[rr][kk] = (e0 + rr < experts) ? router[(uint64_t)(e0 + rr) * 2048 + k0 + kk] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int k = 0; k < 256; ++k) {
+            const double x = (double)sx[ti][k];
+            a0 += (double)sw[ej][k] * x;
+            a1 += (double)sw[ej + 16][k] * x;
+        }
+        __syncthreads();
+    }
+    const uint32_t t = t0 + ti;
+    if (t < T) {
+        if (e0 + ej < experts) logits[(uint64_t)t * 128 + e0 + ej] = a0;
+        if (e0 + ej + 16 < experts) logits[(uint64_t)t * 128 + e0 + ej + 16] = a1;
+    }
+}
+
+// Top-8 experts and renormalised weights per token (wave per token; the decode path's
+// selection, src/qx_format.c:5265-5285).
+extern "C" __global__ __launch_bounds__(256) void qxp_route(const double *logits, uint32_t T, uint32_t experts,
+                                                            uint32_t *ids, double *wts) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.x * 4 + wave_id();
+    if (t >= T) return;
+    const int E = (int)experts;
+    const double l0 = lane < E ? logits[(uint64_t)t * 128 + lane] : 0.0;
+    const double l1 = lane + 64 < E ? logits[(uint64_t)t * 128 + lane + 64] : 0.0;
+    uint32_t id[QXG_TOPK];
+    double w[QXG_TOPK];
+    wave_top8(l0, l1, E, id, w);
+#pragma unroll
+    for (int q = 0; q < QXG_TOPK; ++q)
+        if (lane == q) { ids[t * 8 + q] = id[q] < experts ? id[q] : 0u; wts[t * 8 + q] = w[q]; }
+}
+
+// Token -> expert grouping (one block): expert e's tokens, ascending, take slots
+// off[e] .. off[e]+n_e of an expert-major layout padded to 32 per expert; tok_slot[t][r]
+// is the slot of (token t, rank r), slot_token the inverse (-1 on padding).  m-groups of
+// up to MT row tiles per expert feed the expert GEMMs; meta = {m-groups, padded slots}.
+extern "C" __global__ __launch_bounds__(1024) void qxp_group(const uint32_t *ids, uint32_t T, uint32_t experts,
+        uint32_t mt_per_group, int32_t *slot_token, uint32_t *tok_slot, uint32_t *mgroups, uint32_t *meta) {
+    __shared__ uint32_t bm[128][QXP_MAX / 32];
+    __shared__ uint32_t cnt[128], off[129];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < 128 * (QXP_MAX / 32); i += 1024) (&bm[0][0])[i] = 0u;
+    __syncthreads();
+    for (uint32_t p = tid; p < T * 8; p += 1024) {
+        const uint32_t t = p >> 3, e = ids[p];
+        atomicOr(&bm[e][t >> 5], 1u << (t & 31));
+    }
+    __syncthreads();
+    if (tid < 128) {
+        uint32_t c = 0;
+        for (int w = 0; w < QXP_MAX / 32; ++w) c += __popc(bm[tid][w]);
+        cnt[tid] = c;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t o = 0, ng = 0;
+        for (uint32_t e = 0; e < experts; ++e) {
+            off[e] = o;
+            const uint32_t mt = (cnt[e] + 31) / 32;
+            for (uint32_t g = 0; g < mt; g += mt_per_group) {
+                const uint32_t k = mt - g < mt_per_group ? mt - g : mt_per_group;
+                mgroups[ng++] = e | ((o / 32 + g) << 8) | (k << 20);
+            }
+            o += 32 * mt;
+        }
+        off[experts] = o;
+        meta[0] = ng;
+        meta[1] = o;
+    }
+    __syncthreads();
+    for (uint32_t p = tid; p < T * 8; p += 1024) {
+        const uint32_t t = p >> 3, e = ids[p], w = t >> 5;
+        uint32_t rank = __popc(bm[e][w] & ((1u << (t & 31)) - 1u));
+        for (uint32_t i = 0; i < w; ++i) rank += __popc(bm[e][i]);
+        const uint32_t slot = off[e] + rank;
+        tok_slot[p] = slot;
+        slot_token[slot] = (int32_t)t;
+    }
+    if (tid < (int)experts)
+        for (uint32_t s = off[tid] + cnt[tid]; s < off[tid + 1]; ++s) slot_token[s] = -1;
+}
+
+// x[t][i] = x1[t][i] + sum_r (float)(w_r * (double)y[slot(t,r)][i]), ranks in order
+// (src/qx_format.c:5296-5309); block per token.
+extern "C" __global__ __launch_bounds__(256) void qxp_combine(const float *x1, const float *y, const uint32_t *tok_slot,
+                                                              const double *wts, float *x, float *moe_dump) {
+    const uint32_t t = blockIdx.x;
+    uint32_t sl[QXG_TOPK];
+    double w[QXG_TOPK];
+#pragma unroll
+    for (int r = 0; r < QXG_TOPK; ++r) { sl[r] = tok_slot[t * 8 + r]; w[r] = wts[t * 8 + r]; }
+    for (int i = threadIdx.x; i < 2048; i += 256) {
+        float m = 0.0f;
+#pragma unroll
+        for (int r = 0; r < QXG_TOPK; ++r) m += (float)(w[r] * (double)y[(uint64_t)sl[r] * 2048 + i]);
+        if (moe_dump) moe_dump[(uint64_t)t * 2048 + i] = m;
+        x[(uint64_t)t * 2048 + i] = x1[(uint64_t)t * 2048 + i] + m;
+    }
+}
+
+// ================================================================= launch wrappers
+extern "C" {
+void qxp_launch_gemm(hipStream_t s, int kind, const PfGemm &g, const PfTables &P, uint32_t grid_x, uint32_t grid_y,
+                     Timer tm) {
+    switch (kind) {
+    case 0:   // Q/K/V: IQ4_XS, 32 columns per wave
+        qx_launch(qxp_gemm<FMT_IQ4, 1, 1, EPI_STORE>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+        break;
+    case 1:   // O projection + residual: IQ4_XS, 32 columns per wave
+        qx_launch(qxp_gemm<FMT_IQ4, 1, 1, EPI_RESID>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+        break;
+    case 2:   // expert gate/up + SwiGLU: IQ2_XS
+        qx_launch(qxp_gemm<FMT_IQ2, 2, 2, EPI_SWIGLU>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+        break;
+    default:  // expert down: IQ3_XXS, 32 columns per wave
+        qx_launch(qxp_gemm<FMT_IQ3, 1, 2, EPI_STORE>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+        break;
+    }
+}
+void qxp_launch_pack(hipStream_t s, int K, const float *src, const int32_t *map, const uint32_t *nrows, uint32_t rows,
+                     uint32_t nvalid, uint4 *apk, float *rscale) {
+    switch (K) {
+    case 2048: hipLaunchKernelGGL(qxp_pack<2048>, dim3(rows), dim3(256), 0, s, src, map, nrows, nvalid, apk, rscale); break;
+    case 4096: hipLaunchKernelGGL(qxp_pack<4096>, dim3(rows), dim3(256), 0, s, src, map, nrows, nvalid, apk, rscale); break;
+    default: hipLaunchKernelGGL(qxp_pack<768>, dim3(rows), dim3(256), 0, s, src, map, nrows, nvalid, apk, rscale); break;
+    }
+}
+}

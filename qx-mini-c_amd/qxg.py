@@ -58,6 +58,8 @@ _sig(_g, "qxg_attention_layer", [vp, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_moe_layer", [vp, u32, vp, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_final_head", [vp, vp, vp, vp, u32, vp, vp, *ERR])
 _sig(_g, "qxg_set_layer_path", [vp, c_int])
+_sig(_g, "qxg_prefill", [vp, vp, u32, u32, c_int, vp, vp, u32, vp, vp, ctypes.POINTER(c_float), *ERR])
+_sig(_g, "qxg_prefill_layer", [vp, u32, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_time_kernel", [vp, c_int, u32, u32, ctypes.POINTER(c_float), *ERR])
 _sig(_g, "qxg_device_bytes", [vp], u64)
 _sig(_g, "qxg_profile_kernel", [vp, c_int])
@@ -203,6 +205,27 @@ class Context:
                                     self._err, 1024))
         return out, ms.value
 
+    def prefill(self, tokens, pos0=0, run_head=True, top_n=8, want_residual=False, want_logits=False):
+        """Batched prefill of `tokens` at positions pos0..; returns (residual [n, 2048] or
+        None, logits of the last token or None, top ids, top logits, device ms)."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        n = len(tokens)
+        res = np.zeros((n, 2048), np.float32) if want_residual else None
+        lg = np.zeros(self.info.vocab, np.float32) if want_logits and run_head else None
+        ids = np.zeros(top_n, np.uint32); tl = np.zeros(top_n, np.float64)
+        ms = c_float()
+        self._check(_g.qxg_prefill(self._c, _p(tokens), n, pos0, int(run_head), _p(res), _p(lg), top_n, _p(ids),
+                                   _p(tl), ctypes.byref(ms), self._err, 1024))
+        return res, lg, ids, tl, ms.value
+
+    def prefill_layer(self, layer, pos0, x):
+        """One prefill layer on the rows of x [n, 2048]: (ffn_inp, moe, out), each [n, 2048]."""
+        x = np.ascontiguousarray(x, np.float32)
+        n = x.shape[0]
+        fi = np.zeros((n, 2048), np.float32); moe = np.zeros((n, 2048), np.float32); out = np.zeros((n, 2048), np.float32)
+        self._check(_g.qxg_prefill_layer(self._c, layer, n, pos0, _p(x), _p(fi), _p(moe), _p(out), self._err, 1024))
+        return fi, moe, out
+
     def set_layer_path(self, persistent):
         """0: one kernel per phase (default); 1: the persistent layer kernel."""
         self._check(_g.qxg_set_layer_path(self._c, int(persistent)))
@@ -224,4 +247,5 @@ class Context:
         return int(_g.qxg_device_bytes(self._c))
 
 
-KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "oproj": 3, "head": 4, "attention": 5, "router": 6, "layers": 7}
+KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "oproj": 3, "head": 4, "attention": 5, "router": 6, "layers": 7,
+           "pf_qkv": 8, "pf_oproj": 9, "pf_gate_up": 10, "pf_down": 11}
