@@ -97,6 +97,56 @@ def copy_calibration(mib):
     print(json.dumps({"copy_bytes": n, "copies": 4}), flush=True)
 
 
+# config 5: algorithmic flops of one layer's expert GEMMs over T tokens (8 assignments each)
+def expert_flops(t):
+    return {"pf_gate_up": 2.0 * t * 8 * 2 * 768 * 2048, "pf_down": 2.0 * t * 8 * 2048 * 768}
+
+
+def prefill_leg(ctx, args):
+    """Config 5: batched prefill of T seeded ids, then greedy decode from the prefilled
+    INT8 KV.  The expert gate/up GEMM is timed in situ (event pairs around each of its
+    48 launches) for the MFMA roofline."""
+    T, G = args.prefill_tokens, args.prefill_decode
+    ids = np.random.default_rng(args.seed + 5).integers(0, VOCAB, size=T).astype(np.uint32)
+    ctx.kv_create(LAYERS, T + G + 1)
+    ctx.prefill(ids, 0, True, 1)                                      # warmup
+    ctx.kv_create(LAYERS, T + G + 1)
+    ctx.profile_kernel(qxg_kernels()["pf_gate_up"])
+    _, _, first, _, ms_prof = ctx.prefill(ids, 0, True, 1)
+    launches, kern_ms = ctx.profile_result()
+    ctx.profile_kernel(-1)
+    ctx.kv_create(LAYERS, T + G + 1)
+    t0 = time.perf_counter()
+    _, _, first2, _, ms = ctx.prefill(ids, 0, True, 1)
+    wall = time.perf_counter() - t0
+    assert int(first2[0]) == int(first[0]), "prefill result changed between identical runs"
+    toks, dec_ms = ctx.generate([int(first2[0])], G - 1, T)
+    avg = kern_ms / 1e3 / max(launches, 1)
+    fl = expert_flops(T)["pf_gate_up"]
+    expert_bytes = LAYERS * EXPERTS * (2 * 768 * 8 * 74 + 2048 * 3 * 98)
+    log(f"prefill {T} tokens: {wall * 1e3:.2f} ms wall, {ms:.2f} ms device; gate/up {launches} launches "
+        f"avg {avg * 1e6:.1f} us; decode {G - 1} tokens after it: {dec_ms:.2f} ms")
+    return {
+        "workload": f"config5: prefill of {T} seeded token ids (uniform in [0,{VOCAB})) through the same 48-layer "
+                    f"model, head on the last, then {G} greedy tokens (the first from the prefill head)",
+        "tokens": T, "ms": round(wall * 1e3, 3), "device_ms": round(ms, 3), "tok_s": round(T / wall, 1),
+        "dtype": "fp16 MFMA (codes exact; activations split hi+lo), f32 accumulation",
+        "roofline": {"bound": "mfma", "kernel": "pf_gate_up", "achieved": round(fl / avg / 1e12, 2),
+                     "peak": 2500.0, "unit": "TFLOP/s", "frac": round(fl / avg / 1e12 / 2500.0, 4),
+                     "flops_per_launch": fl, "avg_launch_us": round(avg * 1e6, 2), "launches": launches,
+                     "note": "algorithmic flops 2*M*N*K (M = 8T assignments); the split activations make the "
+                             "matrix cores execute 2x these, plus padding of each expert to 32 rows"},
+        "expert_weights_GBs": round(expert_bytes / (ms / 1e3) / 1e9, 1),
+        "decode_after": {"steps": G - 1, "tok_s": round((G - 1) / (dec_ms / 1e3), 1),
+                         "positions": f"{T}..{T + G - 2}"},
+    }
+
+
+def qxg_kernels():
+    import qxg
+    return qxg.KERNELS
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -109,6 +159,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=25.0)
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--prefill-tokens", type=int, default=512,
+                    help="config 5 leg: batched prefill of this many seeded token ids (0: skip)")
+    ap.add_argument("--prefill-decode", type=int, default=128,
+                    help="greedy tokens generated after the prefill (the first comes from the prefill's head)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-sized device buffer (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -200,6 +254,8 @@ def main():
                            "device_ms_per_token": round(dev_ms2 / args.steps, 4)},
         "first_tokens": [int(t) for t in toks[:8]],
     }
+    if args.prefill_tokens:
+        out["prefill"] = prefill_leg(ctx, args)
     ctx.close()
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, 1 thread) ...")

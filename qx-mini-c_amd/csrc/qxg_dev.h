@@ -12,19 +12,12 @@ namespace {
 // ---------------------------------------------------------------- helpers
 // reference qx_fp16_to_f32 (src/qx_format.c:1854-1876): exact, exponent 31 -> +-65504
 DEV float fp16_exact(uint32_t h) {
-    uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu, bits;
-    if (e == 0) {
-        if (m == 0) bits = sign;
-        else {
-            int sh = __builtin_clz(m) - 21;          // shifts until bit 10 is set
-            bits = sign | ((uint32_t)(113 - sh) << 23) | (((m << sh) & 0x3ffu) << 13);
-        }
-    } else if (e == 31) {
-        bits = sign | 0x477fe000u;
-    } else {
-        bits = sign | ((e + 112u) << 23) | (m << 13);
-    }
-    return __uint_as_float(bits);
+    const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu;
+    const float sub = (float)m * 5.9604644775390625e-08f;   // subnormal: m * 2^-24 (exact)
+    float v = __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+    v = e == 0 ? __uint_as_float(sign | __float_as_uint(sub)) : v;
+    v = e == 31 ? __uint_as_float(sign | 0x477fe000u) : v;   // selects, no branches
+    return v;
 }
 
 // the wave's index in its workgroup, in a scalar register (the divergence analysis
@@ -434,6 +427,96 @@ DEV void head_norm_rope_wave(float &x0, float &x1, float w0, float w1, double c,
     const float n1 = (float)((double)x1 * inv * (double)w1);
     x0 = (float)((double)n0 * c - (double)n1 * s);
     x1 = (float)((double)n0 * s + (double)n1 * c);
+}
+
+// ---- GQA attention of one q head over cached INT8 positions 0..n-1 by a block of 256
+// threads (qx_rope_gqa_attention_partial, src/qx_format.c:5051-5196).
+// Scores: one lane per position; the 128-term dot is summed in dimension order in
+// double, as the reference does: (sum_d (double)q_d * (double)((float)k8_d * ks)) /
+// sqrt(hd), non-finite -> 0.  krow(t, k[8], ks) fetches position t's 128 K bytes and
+// scale.  s_sc[t] <- score; returns the block maximum.
+template <typename KF>
+DEV double attn_scores(const float *s_q, uint32_t n, double sqrt_hd, double *s_sc, double *redd, KF krow) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    double mx = -1.0e300;
+    for (uint32_t t = tid; t < n; t += 256) {
+        uint4 k[8];
+        float ksc;
+        krow(t, k, ksc);
+        asm volatile("" ::: "memory");   // q is re-read from LDS per position (not kept in 128+ registers)
+        double acc = 0.0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint32_t w4[4] = {k[c].x, k[c].y, k[c].z, k[c].w};
+#pragma unroll
+            for (int j4 = 0; j4 < 4; ++j4) {
+                const float4 qv = *reinterpret_cast<const float4 *>(s_q + 16 * c + 4 * j4);   // LDS broadcast
+                const float q4[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int8_t kb = (int8_t)((w4[j4] >> (8 * j)) & 255u);
+                    acc += (double)q4[j] * (double)((float)kb * ksc);
+                }
+            }
+        }
+        double sc = acc / sqrt_hd;
+        if (!isfinite(sc)) sc = 0.0;
+        s_sc[t] = sc;
+        mx = fmax(mx, sc);
+    }
+    mx = wave_max_d(mx);
+    if (lane == 0) redd[wave] = mx;
+    __syncthreads();
+    mx = fmax(fmax(redd[0], redd[1]), fmax(redd[2], redd[3]));
+    __syncthreads();
+    return mx;
+}
+// s_sc[t] <- exp(s_sc[t] - mx) (double); returns the sum (1 if not finite and positive)
+DEV double attn_exp(uint32_t n, double mx, double *s_sc, double *redd) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    double den = 0.0;
+    for (uint32_t t = tid; t < n; t += 256) {
+        const double e = exp(s_sc[t] - mx);
+        s_sc[t] = e;
+        den += e;
+    }
+    den = wave_total_d(den);
+    if (lane == 0) redd[wave] = den;
+    __syncthreads();
+    den = (redd[0] + redd[1]) + (redd[2] + redd[3]);
+    if (!isfinite(den) || den <= 0.0) den = 1.0;
+    return den;
+}
+// Context: out[d] = sum_t (float)((e_t / den) * (double)((float)v8_t[d] * vs_t)).  Thread
+// (g = tid/16, dims 8*(tid%16)..+8) sums positions g, g+16, ... in f32; the 16 partial
+// sums of a dimension are then added in g order.  vrow(t, dg, v (8 bytes), vs).
+template <typename VF>
+DEV void attn_context(uint32_t n, double den, const double *s_sc, float (*s_part)[132], VF vrow, float *out) {
+    const int tid = threadIdx.x, g = tid >> 4, dg = tid & 15;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+#pragma unroll 2
+    for (uint32_t t = g; t < n; t += 16) {
+        const double wgt = s_sc[t] / den;
+        uint2 v;
+        float vsc;
+        vrow(t, dg, v, vsc);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int8_t vb = (int8_t)((((j < 4) ? v.x : v.y) >> (8 * (j & 3))) & 255u);
+            acc[j] += (float)(wgt * (double)((float)vb * vsc));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s_part[g][8 * dg + j] = acc[j];
+    __syncthreads();
+    if (tid < 128) {
+        float o = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o += s_part[i][tid];
+        out[tid] = o;
+    }
 }
 
 // order-preserving unsigned image of a double: a > b  <=>  key(a) > key(b); NaN -> 0,

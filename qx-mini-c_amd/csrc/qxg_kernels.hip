@@ -92,9 +92,9 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
 // split-half RoPE (4625-4641; cos/sin from the host-computed table) and INT8 K/V
 // quantization (4449-4463) of the current position fused in: every block derives the
 // same K/V row (the scale spans all 512 values), block 0 stores it at [layer][pos],
-// and each block uses its own copy for position pos.  Scores (double) over 0..pos,
-// double softmax, f32 context accumulation per position in position order within
-// each of two position halves (reference src/qx_format.c:5127-5172).
+// and each block uses its own copy for position pos.  Scores over 0..pos (one lane per
+// position, each dot summed in dimension order in double), double softmax, f32 context
+// sums over 16 interleaved position groups (reference src/qx_format.c:5127-5172).
 // The cached K/V rows of positions [0, min(pos, ATT_STAGE)) and their scales are
 // loaded at kernel start, together with q/k/v, and staged in LDS while the norm,
 // RoPE and quantization run; later positions are read from global memory.
@@ -108,10 +108,12 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     __shared__ uint4 s_kst[ATT_STAGE * 8], s_vst[ATT_STAGE * 8];   // staged rows of this kv head
     __shared__ float s_kss[ATT_STAGE], s_vss[ATT_STAGE];
     __shared__ float s_k[512], s_v[512];
-    __shared__ double s_q[128];
+    __shared__ __align__(16) float s_q[128];
     __shared__ float red[4];
-    __shared__ float s_part[2][128];
-    __shared__ int8_t s_k8[128], s_v8[128];
+    __shared__ double redd[4];
+    __shared__ float s_part[16][132];
+    __shared__ __align__(16) int8_t s_k8[128];
+    __shared__ __align__(16) int8_t s_v8[128];
     __shared__ float s_scale[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int qh = blockIdx.x, kvh = qh >> 3;
@@ -119,15 +121,16 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     const uint64_t base = (uint64_t)layer * ctx;
     const uint32_t nst = pos < (uint32_t)ATT_STAGE ? pos : (uint32_t)ATT_STAGE;   // staged positions
     // cached rows first: 16 bytes of row (tid>>3) + 32*i, chunk tid&7, i < 4
-    uint4 kst[4], vst[4];
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));   // register-promoted (a uint4 array is not)
+    v4u kst[4], vst[4];
     float kss = 0.0f, vss = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t t = (tid >> 3) + 32 * i;
         if (t < nst) {
             const uint64_t off = (base + t) * 512 + kvh * 128 + 16 * (tid & 7);
-            kst[i] = *reinterpret_cast<const uint4 *>(kc + off);
-            vst[i] = *reinterpret_cast<const uint4 *>(vc + off);
+            kst[i] = *reinterpret_cast<const v4u *>(kc + off);
+            vst[i] = *reinterpret_cast<const v4u *>(vc + off);
         }
     }
     if ((uint32_t)tid < nst) { kss = ks[base + tid]; vss = vs[base + tid]; }
@@ -145,8 +148,8 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     s_v[256 + tid] = v1;
     if (wave == 0) {
         head_norm_rope_wave(q0, q1, qw0, qw1, c, s);
-        s_q[lane] = (double)q0;
-        s_q[64 + lane] = (double)q1;
+        s_q[lane] = q0;
+        s_q[64 + lane] = q1;
     }
     // INT8 quantize K and V over all 512 values (scale = max|x|/127, 1 if zero)
     float ka = 0.0f, va = 0.0f;
@@ -175,81 +178,46 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t t = (tid >> 3) + 32 * i;
-        if (t < nst) { s_kst[t * 8 + (tid & 7)] = kst[i]; s_vst[t * 8 + (tid & 7)] = vst[i]; }
+        if (t < nst) {
+            reinterpret_cast<v4u *>(s_kst)[t * 8 + (tid & 7)] = kst[i];
+            reinterpret_cast<v4u *>(s_vst)[t * 8 + (tid & 7)] = vst[i];
+        }
     }
     if ((uint32_t)tid < nst) { s_kss[tid] = kss; s_vss[tid] = vss; }
     __syncthreads();
-    // scores: 16 lanes per position, 8 dims per lane
-    {
-        const int sub = lane >> 4, dl = lane & 15;
-        double qd[8];
+    // position pos from the block's own row, [0, nst) from the LDS stage, the rest from the cache
+    auto krow = [&](uint32_t t, uint4 (&k)[8], float &ksc) {
+        if (t == pos) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qd[j] = s_q[8 * dl + j];
-        for (uint32_t t0 = 4 * wave; t0 < n; t0 += 16) {
-            const uint32_t t = t0 + sub;
-            double acc = 0.0;
-            if (t < n) {
-                uint2 kk;
-                float ksc;
-                if (t == pos) {
-                    kk = *reinterpret_cast<const uint2 *>(s_k8 + 8 * dl);
-                    ksc = s_scale[0];
-                } else if (t < nst) {
-                    kk = reinterpret_cast<const uint2 *>(s_kst)[t * 16 + dl];
-                    ksc = s_kss[t];
-                } else {
-                    kk = *reinterpret_cast<const uint2 *>(kc + (base + t) * 512 + kvh * 128 + 8 * dl);
-                    ksc = ks[base + t];
-                }
+            for (int c = 0; c < 8; ++c) k[c] = reinterpret_cast<const uint4 *>(s_k8)[c];
+            ksc = s_scale[0];
+        } else if (t < nst) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int8_t kb = (int8_t)(((j < 4 ? kk.x : kk.y) >> (8 * (j & 3))) & 255u);
-                    acc += qd[j] * (double)((float)kb * ksc);
-                }
-            }
-            acc = row16_sum_d(acc);   // 16 lanes = one position
-            if (t < n && dl == 0) {
-                double sc = acc / sqrt_hd;
-                if (!isfinite(sc)) sc = 0.0;
-                s_sc[t] = sc;
-            }
+            for (int c = 0; c < 8; ++c) k[c] = s_kst[t * 8 + c];
+            ksc = s_kss[t];
+        } else {
+            const uint4 *p = reinterpret_cast<const uint4 *>(kc + (base + t) * 512 + kvh * 128);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) k[c] = p[c];
+            ksc = ks[base + t];
         }
-    }
+    };
+    auto vrow = [&](uint32_t t, int dg, uint2 &v, float &vsc) {
+        if (t == pos) {
+            v = reinterpret_cast<const uint2 *>(s_v8)[dg];
+            vsc = s_scale[1];
+        } else if (t < nst) {
+            v = reinterpret_cast<const uint2 *>(s_vst)[t * 16 + dg];
+            vsc = s_vss[t];
+        } else {
+            v = *reinterpret_cast<const uint2 *>(vc + (base + t) * 512 + kvh * 128 + 8 * dg);
+            vsc = vs[base + t];
+        }
+    };
+    const double mx = attn_scores(s_q, n, sqrt_hd, s_sc, redd, krow);
+    const double den = attn_exp(n, mx, s_sc, redd);
     __syncthreads();
-    // softmax in double
-    double mx = -1.0e300;
-    for (uint32_t t = tid; t < n; t += 256) mx = fmax(mx, s_sc[t]);
-    mx = wave_max_d(mx);
-    __shared__ double redd[4];
-    if (lane == 0) redd[wave] = mx;
-    __syncthreads();
-    mx = fmax(fmax(redd[0], redd[1]), fmax(redd[2], redd[3]));
-    double den = 0.0;
-    for (uint32_t t = tid; t < n; t += 256) {
-        const double e = exp(s_sc[t] - mx);
-        s_sc[t] = e;
-        den += e;
-    }
-    den = wave_total_d(den);
-    __syncthreads();
-    if (lane == 0) redd[wave] = den;
-    __syncthreads();
-    den = (redd[0] + redd[1]) + (redd[2] + redd[3]);
-    if (!isfinite(den) || den <= 0.0) den = 1.0;
-    // context: thread (d, half); positions of each half in order
-    const int d = tid & 127, hf = tid >> 7;
-    const uint32_t t0 = hf ? n / 2 : 0, t1 = hf ? n : n / 2;
-    float acc = 0.0f;
-    for (uint32_t t = t0; t < t1; ++t) {
-        const double wgt = s_sc[t] / den;
-        const float vv = t == pos ? (float)s_v8[d] * s_scale[1]
-                         : t < nst ? (float)reinterpret_cast<const int8_t *>(s_vst)[t * 128 + d] * s_vss[t]
-                                   : (float)vc[(base + t) * 512 + kvh * 128 + d] * vs[base + t];
-        acc += (float)(wgt * (double)vv);
-    }
-    s_part[hf][d] = acc;
-    __syncthreads();
-    if (tid < 128) ctx_out[qh * 128 + tid] = s_part[0][tid] + s_part[1][tid];
+    attn_context(n, den, s_sc, s_part, vrow, ctx_out + qh * 128);
 }
 
 // O projection IQ4_XS 4096 -> 2048 on ctx, then x[r] += o[r] (src/qx_format.c:6420-6423).

@@ -130,37 +130,104 @@ DEV f16x zero16() {
 }  // namespace
 
 // ================================================================= GEMM
-// One wave: NSUB column tiles of 32 weight rows x MT row tiles of 32 tokens/slots, over
+// One wave: NSUB column tiles of 32 weight rows x NM row tiles of 32 tokens/slots, over
 // all of K.  GU: the two column tiles are gate and up at the same rows (SwiGLU epilogue).
-// Workgroup = 4 waves on 4 consecutive column tiles of the same row tiles.
-template <int F, int NSUB, int MT, int EPI>
-__global__ __launch_bounds__(256, 2) void qxp_gemm(PfGemm g, PfTables P) {
-    constexpr bool GU = EPI == EPI_SWIGLU;
-    uint32_t e = 0, mt0, nmt;
-    if (g.mgroups) {
-        if (blockIdx.y >= g.meta[0]) return;   // whole workgroup
-        const uint32_t mg = g.mgroups[blockIdx.y];
-        e = mg & 255u; mt0 = (mg >> 8) & 0xfffu; nmt = mg >> 20;
-    } else {
-        mt0 = blockIdx.y * MT;
-        nmt = min((uint32_t)MT, g.mtiles - mt0);
-    }
-    __shared__ uint4 s_g2[F == FMT_IQ2 ? 512 : 1];
-    __shared__ uint4 s_sg[F == FMT_IQ4 ? 1 : 128];
-    __shared__ uint32_t s_t[F == FMT_IQ3 ? 512 : F == FMT_IQ4 ? 256 : 1];
-    const int tid = threadIdx.x;
-    if (F == FMT_IQ2) { s_g2[tid] = P.g2h[tid]; s_g2[tid + 256] = P.g2h[tid + 256]; }
-    if (F != FMT_IQ4 && tid < 128) s_sg[tid] = P.sgn[tid];
-    if (F == FMT_IQ3) { s_t[tid] = reinterpret_cast<const uint32_t *>(P.g3h)[tid];
-                        s_t[tid + 256] = reinterpret_cast<const uint32_t *>(P.g3h)[tid + 256]; }
-    if (F == FMT_IQ4) s_t[tid] = P.kv2[tid];
-    __syncthreads();
+// Workgroup = 4 waves on 4 consecutive column tiles of the same row tiles.  The row
+// tiles' fragments of one 256-value block (32 KiB per row tile) are copied by the whole
+// workgroup into one of two LDS stages while the previous block is multiplied, and the
+// next block's weights are loaded into registers at the same time, so each block's
+// loads have one block of matrix work to arrive.  The loop has no data-dependent
+// branches: the last iteration re-loads the last block (never used).
+struct GemmLds {
+    uint4 *g2, *sg, *a;   // a: two stages of `stage` uint4 each
+    uint32_t *t;
+    uint32_t stage;
+};
 
-    const int lane = tid & 63, wave = wave_id(), h = lane >> 5, col = lane & 31;
+// A fragments of block kb of NM row tiles: thread tid holds uint4 tid + 256*i (i < 8),
+// kept in native 4-dword vectors (register-promoted; the uint4 struct array is not)
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+template <int NM>
+DEV void a_load(v4u (&ra)[NM * 8], const uint4 *A, uint32_t KS, uint32_t kb) {
+    const v4u *a = reinterpret_cast<const v4u *>(A);
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ra[m * 8 + i] = a[((uint64_t)m * KS + kb * 16) * 128 + 256 * i];
+}
+template <int NM>
+DEV void a_store(const v4u (&ra)[NM * 8], uint4 *stage, int tid) {
+    v4u *st = reinterpret_cast<v4u *>(stage);
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st[m * 2048 + tid + 256 * i] = ra[m * 8 + i];
+}
+
+// the 16 k-steps of one block: partial sums per block (IQ2_XS, IQ3_XXS) or per group of
+// two k-steps (IQ4_XS), each scaled once into acc
+template <int F, int NSUB, int NM>
+DEV void block_mma(const Blk<F> (&bk)[NSUB], const uint4 *sa, f16x (&acc)[NSUB][NM], const GemmLds &L, int h,
+                   int lane) {
+    constexpr int NG = F == FMT_IQ4 ? 8 : 1;
+    float scl[NSUB][NG];
+#pragma unroll
+    for (int n = 0; n < NSUB; ++n)
+#pragma unroll
+        for (int q = 0; q < NG; ++q) scl[n][q] = blk_scale(bk[n], q);
+    f16x G[NSUB][NM];
+#pragma unroll
+    for (int n = 0; n < NSUB; ++n)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) G[n][m] = zero16();
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        uint4 ah[NM], al[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+            ah[m] = sa[m * 2048 + s * 128 + lane];
+            al[m] = sa[m * 2048 + s * 128 + 64 + lane];
+        }
+#pragma unroll
+        for (int n = 0; n < NSUB; ++n) {
+            const uint4 b = frag(bk[n], s, h, L.g2, L.sg, L.t);
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                G[n][m] = mfma(ah[m], b, G[n][m]);
+                G[n][m] = mfma(al[m], b, G[n][m]);
+            }
+        }
+        if (F == FMT_IQ4 && (s & 1)) {
+#pragma unroll
+            for (int n = 0; n < NSUB; ++n)
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[n][m][r] = fmaf(scl[n][s >> 1], G[n][m][r], acc[n][m][r]);
+                    G[n][m] = zero16();
+                }
+        }
+        // LDS reads of later k-steps stay behind this point: the unrolled loop would
+        // otherwise hoist all of them into registers
+        if (s & 1) asm volatile("" ::: "memory");
+    }
+    if (F != FMT_IQ4) {
+#pragma unroll
+        for (int n = 0; n < NSUB; ++n)
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[n][m][r] = fmaf(scl[n][0], G[n][m][r], acc[n][m][r]);
+    }
+}
+
+template <int F, int NSUB, int NM, int EPI>
+DEV void gemm_body(const PfGemm &g, const GemmLds &L, uint32_t e, uint32_t mt0) {
+    constexpr bool GU = EPI == EPI_SWIGLU;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), h = lane >> 5, col = lane & 31;
     const uint32_t KB = g.kb, KS = 16 * KB;
     const uint32_t nt = blockIdx.x * 4 + wave;            // column tile group of this wave
     const uint32_t c0 = GU ? 32 * nt : 32 * NSUB * nt;     // first output column
-    // matrix and row of each column tile (stacked matrices: uniform per wave)
     PfMat W[NSUB];
     uint64_t rowblk[NSUB];
 #pragma unroll
@@ -171,83 +238,56 @@ __global__ __launch_bounds__(256, 2) void qxp_gemm(PfGemm g, PfTables P) {
         const uint32_t r = (GU ? c0 : c - g.w_start[mi]) + col;
         rowblk[n] = ((uint64_t)e * g.rows + r) * KB;
     }
-    const uint4 *A = g.apk + (uint64_t)mt0 * KS * 128 + lane;
+    const uint4 *A = g.apk + (uint64_t)mt0 * KS * 128 + tid;
+    uint4 *stage0 = L.a, *stage1 = L.a + L.stage;
 
-    f16x acc[NSUB][MT], G[NSUB][MT];
+    f16x acc[NSUB][NM];
 #pragma unroll
     for (int n = 0; n < NSUB; ++n)
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[n][m] = zero16();
-    Blk<F> cur[NSUB];
+        for (int m = 0; m < NM; ++m) acc[n][m] = zero16();
+    // weights of even blocks in b0, odd blocks in b1; A of block kb in stage kb&1
+    Blk<F> b0[NSUB], b1[NSUB];
+    v4u ra[NM * 8];
+    const uint32_t k1 = KB > 1 ? 1 : 0;
 #pragma unroll
-    for (int n = 0; n < NSUB; ++n) blk_load(cur[n], W[n], rowblk[n], h);
+    for (int n = 0; n < NSUB; ++n) blk_load(b0[n], W[n], rowblk[n], h);
+    a_load<NM>(ra, A, KS, 0);
+    a_store<NM>(ra, stage0, tid);
+    a_load<NM>(ra, A, KS, k1);
+#pragma unroll
+    for (int n = 0; n < NSUB; ++n) blk_load(b1[n], W[n], rowblk[n] + k1, h);
+    __syncthreads();   // tables and stage 0
 
+    // per block: multiply, stage the next block's A (its stage was last read two blocks
+    // back, before the barrier that ended the previous block), then start the loads of
+    // the block after it (clamped to the last block: always in bounds, never used)
 #pragma unroll 1
-    for (uint32_t kb = 0; kb < KB; ++kb) {
-        Blk<F> nxt[NSUB];
-        if (kb + 1 < KB) {
+    for (uint32_t kb = 0; kb < KB; kb += 2) {
+        block_mma<F, NSUB, NM>(b0, stage0, acc, L, h, lane);
+        a_store<NM>(ra, stage1, tid);
+        {
+            const uint32_t kn = kb + 2 < KB ? kb + 2 : KB - 1;
+            a_load<NM>(ra, A, KS, kn);
 #pragma unroll
-            for (int n = 0; n < NSUB; ++n) blk_load(nxt[n], W[n], rowblk[n] + kb + 1, h);
+            for (int n = 0; n < NSUB; ++n) blk_load(b0[n], W[n], rowblk[n] + kn, h);
         }
+        __syncthreads();
+        if (kb + 1 >= KB) break;
+        block_mma<F, NSUB, NM>(b1, stage1, acc, L, h, lane);
+        a_store<NM>(ra, stage0, tid);
+        {
+            const uint32_t kn = kb + 3 < KB ? kb + 3 : KB - 1;
+            a_load<NM>(ra, A, KS, kn);
 #pragma unroll
-        for (int n = 0; n < NSUB; ++n)
-#pragma unroll
-            for (int m = 0; m < MT; ++m) G[n][m] = zero16();
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            uint4 ah[MT], al[MT];
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                if (m < (int)nmt) {
-                    const uint4 *p = A + ((uint64_t)m * KS + kb * 16 + s) * 128;
-                    ah[m] = p[0];
-                    al[m] = p[64];
-                }
-            }
-#pragma unroll
-            for (int n = 0; n < NSUB; ++n) {
-                const uint4 b = frag(cur[n], s, h, s_g2, s_sg, s_t);
-#pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    if (m < (int)nmt) {
-                        G[n][m] = mfma(ah[m], b, G[n][m]);
-                        G[n][m] = mfma(al[m], b, G[n][m]);
-                    }
-                }
-            }
-            if (F == FMT_IQ4 && (s & 1)) {
-#pragma unroll
-                for (int n = 0; n < NSUB; ++n) {
-                    const float sc = blk_scale(cur[n], s >> 1);
-#pragma unroll
-                    for (int m = 0; m < MT; ++m) {
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[n][m][r] = fmaf(sc, G[n][m][r], acc[n][m][r]);
-                        G[n][m] = zero16();
-                    }
-                }
-            }
+            for (int n = 0; n < NSUB; ++n) blk_load(b1[n], W[n], rowblk[n] + kn, h);
         }
-        if (F != FMT_IQ4) {
-#pragma unroll
-            for (int n = 0; n < NSUB; ++n) {
-                const float sc = blk_scale(cur[n], 0);
-#pragma unroll
-                for (int m = 0; m < MT; ++m)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[n][m][r] = fmaf(sc, G[n][m][r], acc[n][m][r]);
-            }
-        }
-        if (kb + 1 < KB) {
-#pragma unroll
-            for (int n = 0; n < NSUB; ++n) cur[n] = nxt[n];
-        }
+        __syncthreads();
     }
 
     // epilogue: lane's column c, rows 8*(r/4) + 4h + r%4 of each row tile
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        if (m >= (int)nmt) continue;
+    for (int m = 0; m < NM; ++m) {
         const uint32_t rbase = (mt0 + m) * 32 + 4 * h;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -277,6 +317,32 @@ __global__ __launch_bounds__(256, 2) void qxp_gemm(PfGemm g, PfTables P) {
             }
         }
     }
+}
+
+template <int F, int NSUB, int MT, int EPI>
+__global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void qxp_gemm(PfGemm g, PfTables P) {
+    uint32_t e = 0, mt0, nmt;
+    if (g.mgroups) {
+        if (blockIdx.y >= g.meta[0]) return;   // whole workgroup
+        const uint32_t mg = g.mgroups[blockIdx.y];
+        e = mg & 255u; mt0 = (mg >> 8) & 0xfffu; nmt = mg >> 20;
+    } else {
+        mt0 = blockIdx.y * MT;
+        nmt = min((uint32_t)MT, g.mtiles - mt0);
+    }
+    __shared__ uint4 s_g2[F == FMT_IQ2 ? 512 : 1];
+    __shared__ uint4 s_sg[F == FMT_IQ4 ? 1 : 128];
+    __shared__ uint32_t s_t[F == FMT_IQ3 ? 512 : F == FMT_IQ4 ? 256 : 1];
+    __shared__ uint4 s_a[2 * MT * 2048];   // [stage][row tile][(kstep*2 + piece)*64 + lane]
+    const int tid = threadIdx.x;
+    if (F == FMT_IQ2) { s_g2[tid] = P.g2h[tid]; s_g2[tid + 256] = P.g2h[tid + 256]; }
+    if (F != FMT_IQ4 && tid < 128) s_sg[tid] = P.sgn[tid];
+    if (F == FMT_IQ3) { s_t[tid] = reinterpret_cast<const uint32_t *>(P.g3h)[tid];
+                        s_t[tid + 256] = reinterpret_cast<const uint32_t *>(P.g3h)[tid + 256]; }
+    if (F == FMT_IQ4) s_t[tid] = P.kv2[tid];
+    const GemmLds L{s_g2, s_sg, s_a, s_t, MT * 2048};
+    if (MT == 2 && nmt == 2) gemm_body<F, NSUB, (MT == 2 ? 2 : 1), EPI>(g, L, e, mt0);
+    else gemm_body<F, NSUB, 1, EPI>(g, L, e, mt0);
 }
 
 // ================================================================= element-wise stages
@@ -417,114 +483,58 @@ extern "C" __global__ __launch_bounds__(256) void qxp_qk(const float *qkv, const
 }
 
 // Causal GQA attention of token t (blockIdx.y) and q head blockIdx.x over cached
-// positions 0..p0+t (qx_rope_gqa_attention_partial, src/qx_format.c:5051-5196): double
-// scores, double softmax, f32 context per position in position order within each of
-// two position halves -- the decode kernel's order.
+// positions 0..p0+t (qx_rope_gqa_attention_partial, src/qx_format.c:5051-5196), with the
+// decode kernel's score, softmax and context code.
 extern "C" __global__ __launch_bounds__(256) void qxp_attn(const float *qr, const int8_t *kc, const int8_t *vc,
         const float *ks, const float *vs, uint32_t layer, uint32_t ctx, uint32_t p0, double sqrt_hd, float *ctx_out) {
     extern __shared__ double s_sc[];
-    __shared__ double s_q[128];
+    __shared__ __align__(16) float s_q[128];
     __shared__ double redd[4];
-    __shared__ float s_part[2][128];
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    __shared__ float s_part[16][132];
+    const int tid = threadIdx.x;
     const int qh = blockIdx.x, kvh = qh >> 3;
-    const uint32_t t = blockIdx.y, pos = p0 + t, n = pos + 1;
+    const uint32_t t = blockIdx.y, n = p0 + t + 1;
     const uint64_t base = (uint64_t)layer * ctx;
-    if (tid < 128) s_q[tid] = (double)qr[(uint64_t)t * 4096 + 128 * qh + tid];
+    if (tid < 128) s_q[tid] = qr[(uint64_t)t * 4096 + 128 * qh + tid];
     __syncthreads();
-    {
-        const int sub = lane >> 4, dl = lane & 15;
-        double qd[8];
+    auto krow = [&](uint32_t p, uint4 (&k)[8], float &ksc) {
+        const uint4 *q = reinterpret_cast<const uint4 *>(kc + (base + p) * 512 + kvh * 128);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qd[j] = s_q[8 * dl + j];
-        for (uint32_t t0 = 4 * wave; t0 < n; t0 += 16) {
-            const uint32_t tt = t0 + sub;
-            double acc = 0.0;
-            if (tt < n) {
-                const uint2 kk = *reinterpret_cast<const uint2 *>(kc + (base + tt) * 512 + kvh * 128 + 8 * dl);
-                const float ksc = ks[base + tt];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int8_t kb = (int8_t)(((j < 4 ? kk.x : kk.y) >> (8 * (j & 3))) & 255u);
-                    acc += qd[j] * (double)((float)kb * ksc);
-                }
-            }
-            acc = row16_sum_d(acc);
-            if (tt < n && dl == 0) {
-                double sc = acc / sqrt_hd;
-                if (!isfinite(sc)) sc = 0.0;
-                s_sc[tt] = sc;
-            }
-        }
-    }
+        for (int c = 0; c < 8; ++c) k[c] = q[c];
+        ksc = ks[base + p];
+    };
+    auto vrow = [&](uint32_t p, int dg, uint2 &v, float &vsc) {
+        v = *reinterpret_cast<const uint2 *>(vc + (base + p) * 512 + kvh * 128 + 8 * dg);
+        vsc = vs[base + p];
+    };
+    const double mx = attn_scores(s_q, n, sqrt_hd, s_sc, redd, krow);
+    const double den = attn_exp(n, mx, s_sc, redd);
     __syncthreads();
-    double mx = -1.0e300;
-    for (uint32_t i = tid; i < n; i += 256) mx = fmax(mx, s_sc[i]);
-    mx = wave_max_d(mx);
-    if (lane == 0) redd[wave] = mx;
-    __syncthreads();
-    mx = fmax(fmax(redd[0], redd[1]), fmax(redd[2], redd[3]));
-    double den = 0.0;
-    for (uint32_t i = tid; i < n; i += 256) {
-        const double e = exp(s_sc[i] - mx);
-        s_sc[i] = e;
-        den += e;
-    }
-    den = wave_total_d(den);
-    __syncthreads();
-    if (lane == 0) redd[wave] = den;
-    __syncthreads();
-    den = (redd[0] + redd[1]) + (redd[2] + redd[3]);
-    if (!isfinite(den) || den <= 0.0) den = 1.0;
-    const int d = tid & 127, hf = tid >> 7;
-    const uint32_t ta = hf ? n / 2 : 0, tb = hf ? n : n / 2;
-    float acc = 0.0f;
-    for (uint32_t i = ta; i < tb; ++i) {
-        const double wgt = s_sc[i] / den;
-        const float vv = (float)vc[(base + i) * 512 + kvh * 128 + d] * vs[base + i];
-        acc += (float)(wgt * (double)vv);
-    }
-    s_part[hf][d] = acc;
-    __syncthreads();
-    if (tid < 128) ctx_out[(uint64_t)t * 4096 + qh * 128 + tid] = s_part[0][tid] + s_part[1][tid];
+    attn_context(n, den, s_sc, s_part, vrow, ctx_out + (uint64_t)t * 4096 + qh * 128);
 }
 
-// Router logits of 16 tokens x 32 experts per block: logit[t][e] = sum_i
-// (double)W[e][i] * (double)xn[t][i], i ascending (src/qx_format.c:5254-5264: the same
-// products and the same order of additions as the reference).  Tiles of 256 values of
-// x and W are staged in LDS.
+// Router logits: lane (token, expert) forms logit[t][e] = sum_i (double)W[e][i] *
+// (double)xn[t][i] with i ascending (src/qx_format.c:5254-5264: the same products and
+// the same order of additions as the reference).  A wave covers 8 tokens x 8 experts,
+// so each load instruction touches 8 distinct rows of x and of W.
 extern "C" __global__ __launch_bounds__(256) void qxp_router(const float *xn, const float *router, uint32_t T,
                                                              uint32_t experts, double *logits) {
-    __shared__ float sx[16][257], sw[32][257];
-    const int tid = threadIdx.x, ti = tid >> 4, ej = tid & 15;
-    const uint32_t t0 = blockIdx.x * 16, e0 = blockIdx.y * 32;
-    double a0 = 0.0, a1 = 0.0;
-#pragma unroll 1
-    for (int k0 = 0; k0 < 2048; k0 += 256) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int idx = tid + 256 * i, rr = idx >> 8, kk = idx & 255;
-            sx[rr][kk] = (t0 + rr < T) ? xn[(uint64_t)(t0 + rr) * 2048 + k0 + kk] : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const int idx = tid + 256 * i, rr = idx >> 8, kk = idx & 255;
-            sw[rr][kk] = (e0 + rr < experts) ? router[(uint64_t)(e0 + rr) * 2048 + k0 + kk] : 0.0f;
-        }
-        __syncthreads();
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const uint32_t t = blockIdx.x * 8 + (lane >> 3);
+    const uint32_t e = blockIdx.y * 32 + wave * 8 + (lane & 7);
+    const bool ok = t < T && e < experts;
+    const float4 *x = reinterpret_cast<const float4 *>(xn + (uint64_t)(ok ? t : 0) * 2048);
+    const float4 *w = reinterpret_cast<const float4 *>(router + (uint64_t)(ok ? e : 0) * 2048);
+    double acc = 0.0;
 #pragma unroll 8
-        for (int k = 0; k < 256; ++k) {
-            const double x = (double)sx[ti][k];
-            a0 += (double)sw[ej][k] * x;
-            a1 += (double)sw[ej + 16][k] * x;
-        }
-        __syncthreads();
+    for (int k = 0; k < 512; ++k) {
+        const float4 a = x[k], b = w[k];
+        acc += (double)b.x * (double)a.x;
+        acc += (double)b.y * (double)a.y;
+        acc += (double)b.z * (double)a.z;
+        acc += (double)b.w * (double)a.w;
     }
-    const uint32_t t = t0 + ti;
-    if (t < T) {
-        if (e0 + ej < experts) logits[(uint64_t)t * 128 + e0 + ej] = a0;
-        if (e0 + ej + 16 < experts) logits[(uint64_t)t * 128 + e0 + ej + 16] = a1;
-    }
+    if (ok) logits[(uint64_t)t * 128 + e] = acc;
 }
 
 // Top-8 experts and renormalised weights per token (wave per token; the decode path's
