@@ -57,6 +57,29 @@ int qxg_kv_write(qxg_ctx *ctx, uint32_t layer, uint32_t pos0, uint32_t count, co
 int qxg_kv_read(qxg_ctx *ctx, uint32_t layer, uint32_t pos0, uint32_t count, int8_t *k, int8_t *v,
                 float *kscale, float *vscale, char *err, uint64_t err_len);
 
+/* QXKVSNP1 snapshots of the INT8 KV cache (the reference's accumulated-KV files,
+ * qx_write_accumulated_kv_snapshot / qx_read_accumulated_kv_snapshot,
+ * src/qx_format.c:5860-5968, used by --kv-snapshot-out / --kv-snapshot-in,
+ * src/qx_format.c:6165-6177, 6629-6633).  File: 48-byte header ("QXKVSNP1", version 2,
+ * layers, positions, ctx_tokens, kv_heads 4, head_dim 128, format 1 = int8, row bytes
+ * 512, next_token, seed), per layer and position the K row, V row, K scale and V scale,
+ * then the SHA-256 of all preceding bytes.  ctx_tokens must equal the cache's context.
+ * qxg_kv_export writes layers [0, layers) x positions [0, positions) of the device cache;
+ * qxg_kv_import checks the header (layers, ctx_tokens, kv geometry, int8, seed) and the
+ * digest before writing positions [0, *positions_out) of every layer to the device. */
+int qxg_kv_export(qxg_ctx *ctx, const char *path, uint32_t layers, uint32_t positions, uint32_t ctx_tokens,
+                  uint32_t next_token, uint32_t seed, char *err, uint64_t err_len);
+int qxg_kv_import(qxg_ctx *ctx, const char *path, uint32_t layers, uint32_t ctx_tokens, uint32_t seed,
+                  uint32_t *positions_out, uint32_t *next_token_out, char *err, uint64_t err_len);
+/* The same file format over host caches laid out as the reference's
+ * ([layers][ctx_tokens][512] int8 rows, [layers*ctx_tokens] f32 scales); no device use. */
+int qxg_kvsnap_write(const char *path, uint32_t layers, uint32_t positions, uint32_t ctx_tokens, uint32_t next_token,
+                     uint32_t seed, const int8_t *k, const int8_t *v, const float *kscale, const float *vscale,
+                     char *err, uint64_t err_len);
+int qxg_kvsnap_read(const char *path, uint32_t layers, uint32_t ctx_tokens, uint32_t seed, int8_t *k, int8_t *v,
+                    float *kscale, float *vscale, uint32_t *positions_out, uint32_t *next_token_out, char *err,
+                    uint64_t err_len);
+
 /* One full token at `position`: Q4_K embedding, every bound layer (attention with
  * INT8 KV append, then MoE), and if run_head the output RMSNorm, Q6_K head and
  * top_n (<= 32) ids by (logit desc, index asc).  The loop body of

@@ -431,35 +431,60 @@ DEV void head_norm_rope_wave(float &x0, float &x1, float w0, float w1, double c,
 
 // ---- GQA attention of one q head over cached INT8 positions 0..n-1 by a block of 256
 // threads (qx_rope_gqa_attention_partial, src/qx_format.c:5051-5196).
-// Scores: one lane per position; the 128-term dot is summed in dimension order in
-// double, as the reference does: (sum_d (double)q_d * (double)((float)k8_d * ks)) /
-// sqrt(hd), non-finite -> 0.  krow(t, k[8], ks) fetches position t's 128 K bytes and
-// scale.  s_sc[t] <- score; returns the block maximum.
+// q (128 f32 in LDS) is written as int8 digit planes per group of 32 dimensions
+// (22 significant bits, as the projections' activations), so the score of a position is
+// exact int32 v_dot4 sums of those digits with the position's INT8 K codes:
+//     score = ks * sum_g s_g * (2^16 H_g.k + 2^8 M_g.k + L_g.k) / sqrt(hd),
+// non-finite (or a non-finite q) -> 0.  One lane per position; krow(t, k[8], ks) fetches
+// position t's 128 K bytes and scale.  s_sc[t] <- score; returns the block maximum.
 template <typename KF>
-DEV double attn_scores(const float *s_q, uint32_t n, double sqrt_hd, double *s_sc, double *redd, KF krow) {
+DEV double attn_scores(const float *s_q, uint32_t *s_qd, uint32_t n, double sqrt_hd, double *s_sc, double *redd,
+                       KF krow) {
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    bool fin = true;
+    if (tid < 16) {   // 4 groups x 4 threads of 8 values (quads: the group max is two DPP steps)
+        float y[8];
+        const float4 a = *reinterpret_cast<const float4 *>(s_q + 8 * tid), b = *reinterpret_cast<const float4 *>(s_q + 8 * tid + 4);
+        y[0] = a.x; y[1] = a.y; y[2] = a.z; y[3] = a.w; y[4] = b.x; y[5] = b.y; y[6] = b.z; y[7] = b.w;
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { fin = fin && isfinite(y[i]); mx = fmaxf(mx, fabsf(y[i])); }
+        mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
+        mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
+        uint32_t h0, h1, m0, m1, l0, l1;
+        float sc;
+        digits8(y, fin && isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
+        uint32_t *d = s_qd + (tid >> 2) * DIG_STRIDE;
+        const int q = tid & 3;
+        *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
+        *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
+        if (q == 0) d[24] = __float_as_uint(sc);
+    }
+    const bool qok = __syncthreads_or(!fin) == 0;
     double mx = -1.0e300;
     for (uint32_t t = tid; t < n; t += 256) {
         uint4 k[8];
         float ksc;
         krow(t, k, ksc);
-        asm volatile("" ::: "memory");   // q is re-read from LDS per position (not kept in 128+ registers)
+        asm volatile("" ::: "memory");   // the digits are re-read from LDS per position
         double acc = 0.0;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const uint32_t w4[4] = {k[c].x, k[c].y, k[c].z, k[c].w};
+        for (int g = 0; g < 4; ++g) {
+            Dig d;
+            load_dig(s_qd, g, d);
+            const uint32_t kw[8] = {k[2 * g].x, k[2 * g].y, k[2 * g].z, k[2 * g].w,
+                                    k[2 * g + 1].x, k[2 * g + 1].y, k[2 * g + 1].z, k[2 * g + 1].w};
+            int aH = 0, aM = 0, aL = 0;
 #pragma unroll
-            for (int j4 = 0; j4 < 4; ++j4) {
-                const float4 qv = *reinterpret_cast<const float4 *>(s_q + 16 * c + 4 * j4);   // LDS broadcast
-                const float q4[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int8_t kb = (int8_t)((w4[j4] >> (8 * j)) & 255u);
-                    acc += (double)q4[j] * (double)((float)kb * ksc);
-                }
+            for (int i = 0; i < 8; ++i) {
+                aH = sdot4(kw[i], d.h[i], aH);
+                aM = sdot4(kw[i], d.m[i], aM);
+                aL = sdot4(kw[i], d.l[i], aL);
             }
+            acc += (double)(combine(aH, aM, aL) * d.s);
         }
-        double sc = acc / sqrt_hd;
+        double sc = qok ? acc * (double)ksc / sqrt_hd : 0.0;
         if (!isfinite(sc)) sc = 0.0;
         s_sc[t] = sc;
         mx = fmax(mx, sc);
@@ -471,8 +496,11 @@ DEV double attn_scores(const float *s_q, uint32_t n, double sqrt_hd, double *s_s
     __syncthreads();
     return mx;
 }
-// s_sc[t] <- exp(s_sc[t] - mx) (double); returns the sum (1 if not finite and positive)
-DEV double attn_exp(uint32_t n, double mx, double *s_sc, double *redd) {
+// Softmax in double: e_t = exp(s_t - mx), den = sum e_t (1 if not finite and positive);
+// s_sc[t] <- (e_t / den) * vs_t, the position's weight with its V scale folded in.
+// vsc(t) returns position t's V scale.  Ends with a barrier.
+template <typename VS>
+DEV void attn_weights(uint32_t n, double mx, double *s_sc, double *redd, VS vsc) {
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     double den = 0.0;
     for (uint32_t t = tid; t < n; t += 256) {
@@ -485,27 +513,26 @@ DEV double attn_exp(uint32_t n, double mx, double *s_sc, double *redd) {
     __syncthreads();
     den = (redd[0] + redd[1]) + (redd[2] + redd[3]);
     if (!isfinite(den) || den <= 0.0) den = 1.0;
-    return den;
+    for (uint32_t t = tid; t < n; t += 256) s_sc[t] = (s_sc[t] / den) * (double)vsc(t);
+    __syncthreads();
 }
-// Context: out[d] = sum_t (float)((e_t / den) * (double)((float)v8_t[d] * vs_t)).  Thread
-// (g = tid/16, dims 8*(tid%16)..+8) sums positions g, g+16, ... in f32; the 16 partial
-// sums of a dimension are then added in g order.  vrow(t, dg, v (8 bytes), vs).
+// Context: out[d] = sum_t p_t * v8_t[d] in f32 with p_t = (float)((e_t / den) * vs_t).
+// Thread (g = tid/16, dims 8*(tid%16)..+8) sums positions g, g+16, ...; the 16 partial
+// sums of a dimension are then added in g order.  vrow(t, dg) returns the 8 V bytes.
 template <typename VF>
-DEV void attn_context(uint32_t n, double den, const double *s_sc, float (*s_part)[132], VF vrow, float *out) {
+DEV void attn_context(uint32_t n, const double *s_sc, float (*s_part)[132], VF vrow, float *out) {
     const int tid = threadIdx.x, g = tid >> 4, dg = tid & 15;
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-#pragma unroll 2
+#pragma unroll 4
     for (uint32_t t = g; t < n; t += 16) {
-        const double wgt = s_sc[t] / den;
-        uint2 v;
-        float vsc;
-        vrow(t, dg, v, vsc);
+        const float p = (float)s_sc[t];
+        const uint2 v = vrow(t, dg);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int8_t vb = (int8_t)((((j < 4) ? v.x : v.y) >> (8 * (j & 3))) & 255u);
-            acc[j] += (float)(wgt * (double)((float)vb * vsc));
+            acc[j] = fmaf(p, (float)vb, acc[j]);
         }
     }
 #pragma unroll

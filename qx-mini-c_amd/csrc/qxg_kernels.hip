@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
 // quantization (4449-4463) of the current position fused in: every block derives the
 // same K/V row (the scale spans all 512 values), block 0 stores it at [layer][pos],
 // and each block uses its own copy for position pos.  Scores over 0..pos (one lane per
-// position, each dot summed in dimension order in double), double softmax, f32 context
+// position, q as int8 digit planes against the INT8 K codes), double softmax, f32 context
 // sums over 16 interleaved position groups (reference src/qx_format.c:5127-5172).
 // The cached K/V rows of positions [0, min(pos, ATT_STAGE)) and their scales are
 // loaded at kernel start, together with q/k/v, and staged in LDS while the norm,
@@ -109,6 +109,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     __shared__ float s_kss[ATT_STAGE], s_vss[ATT_STAGE];
     __shared__ float s_k[512], s_v[512];
     __shared__ __align__(16) float s_q[128];
+    __shared__ __align__(16) uint32_t s_qd[4 * DIG_STRIDE];
     __shared__ float red[4];
     __shared__ double redd[4];
     __shared__ float s_part[16][132];
@@ -202,22 +203,15 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
             ksc = ks[base + t];
         }
     };
-    auto vrow = [&](uint32_t t, int dg, uint2 &v, float &vsc) {
-        if (t == pos) {
-            v = reinterpret_cast<const uint2 *>(s_v8)[dg];
-            vsc = s_scale[1];
-        } else if (t < nst) {
-            v = reinterpret_cast<const uint2 *>(s_vst)[t * 16 + dg];
-            vsc = s_vss[t];
-        } else {
-            v = *reinterpret_cast<const uint2 *>(vc + (base + t) * 512 + kvh * 128 + 8 * dg);
-            vsc = vs[base + t];
-        }
+    auto vrow = [&](uint32_t t, int dg) -> uint2 {
+        if (t == pos) return reinterpret_cast<const uint2 *>(s_v8)[dg];
+        if (t < nst) return reinterpret_cast<const uint2 *>(s_vst)[t * 16 + dg];
+        return *reinterpret_cast<const uint2 *>(vc + (base + t) * 512 + kvh * 128 + 8 * dg);
     };
-    const double mx = attn_scores(s_q, n, sqrt_hd, s_sc, redd, krow);
-    const double den = attn_exp(n, mx, s_sc, redd);
-    __syncthreads();
-    attn_context(n, den, s_sc, s_part, vrow, ctx_out + qh * 128);
+    auto vsc = [&](uint32_t t) -> float { return t == pos ? s_scale[1] : t < nst ? s_vss[t] : vs[base + t]; };
+    const double mx = attn_scores(s_q, s_qd, n, sqrt_hd, s_sc, redd, krow);
+    attn_weights(n, mx, s_sc, redd, vsc);
+    attn_context(n, s_sc, s_part, vrow, ctx_out + qh * 128);
 }
 
 // O projection IQ4_XS 4096 -> 2048 on ctx, then x[r] += o[r] (src/qx_format.c:6420-6423).

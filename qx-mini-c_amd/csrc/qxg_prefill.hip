@@ -489,6 +489,7 @@ extern "C" __global__ __launch_bounds__(256) void qxp_attn(const float *qr, cons
         const float *ks, const float *vs, uint32_t layer, uint32_t ctx, uint32_t p0, double sqrt_hd, float *ctx_out) {
     extern __shared__ double s_sc[];
     __shared__ __align__(16) float s_q[128];
+    __shared__ __align__(16) uint32_t s_qd[4 * DIG_STRIDE];
     __shared__ double redd[4];
     __shared__ float s_part[16][132];
     const int tid = threadIdx.x;
@@ -503,20 +504,21 @@ extern "C" __global__ __launch_bounds__(256) void qxp_attn(const float *qr, cons
         for (int c = 0; c < 8; ++c) k[c] = q[c];
         ksc = ks[base + p];
     };
-    auto vrow = [&](uint32_t p, int dg, uint2 &v, float &vsc) {
-        v = *reinterpret_cast<const uint2 *>(vc + (base + p) * 512 + kvh * 128 + 8 * dg);
-        vsc = vs[base + p];
+    auto vrow = [&](uint32_t p, int dg) -> uint2 {
+        return *reinterpret_cast<const uint2 *>(vc + (base + p) * 512 + kvh * 128 + 8 * dg);
     };
-    const double mx = attn_scores(s_q, n, sqrt_hd, s_sc, redd, krow);
-    const double den = attn_exp(n, mx, s_sc, redd);
-    __syncthreads();
-    attn_context(n, den, s_sc, s_part, vrow, ctx_out + (uint64_t)t * 4096 + qh * 128);
+    auto vsc = [&](uint32_t p) -> float { return vs[base + p]; };
+    const double mx = attn_scores(s_q, s_qd, n, sqrt_hd, s_sc, redd, krow);
+    attn_weights(n, mx, s_sc, redd, vsc);
+    attn_context(n, s_sc, s_part, vrow, ctx_out + (uint64_t)t * 4096 + qh * 128);
 }
 
 // Router logits: lane (token, expert) forms logit[t][e] = sum_i (double)W[e][i] *
-// (double)xn[t][i] with i ascending (src/qx_format.c:5254-5264: the same products and
-// the same order of additions as the reference).  A wave covers 8 tokens x 8 experts,
-// so each load instruction touches 8 distinct rows of x and of W.
+// (double)xn[t][i] (src/qx_format.c:5254-5264: the same double products) as four
+// interleaved partial sums over i = 4j+c (c < 4), each in ascending order, added as
+// (s0 + s1) + (s2 + s3): four independent chains of additions instead of one.  A wave
+// covers 8 tokens x 8 experts, so each load instruction touches 8 distinct rows of x
+// and of W.
 extern "C" __global__ __launch_bounds__(256) void qxp_router(const float *xn, const float *router, uint32_t T,
                                                              uint32_t experts, double *logits) {
     const int lane = threadIdx.x & 63, wave = wave_id();
@@ -525,16 +527,16 @@ extern "C" __global__ __launch_bounds__(256) void qxp_router(const float *xn, co
     const bool ok = t < T && e < experts;
     const float4 *x = reinterpret_cast<const float4 *>(xn + (uint64_t)(ok ? t : 0) * 2048);
     const float4 *w = reinterpret_cast<const float4 *>(router + (uint64_t)(ok ? e : 0) * 2048);
-    double acc = 0.0;
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
 #pragma unroll 8
     for (int k = 0; k < 512; ++k) {
         const float4 a = x[k], b = w[k];
-        acc += (double)b.x * (double)a.x;
-        acc += (double)b.y * (double)a.y;
-        acc += (double)b.z * (double)a.z;
-        acc += (double)b.w * (double)a.w;
+        s0 += (double)b.x * (double)a.x;
+        s1 += (double)b.y * (double)a.y;
+        s2 += (double)b.z * (double)a.z;
+        s3 += (double)b.w * (double)a.w;
     }
-    if (ok) logits[(uint64_t)t * 128 + e] = acc;
+    if (ok) logits[(uint64_t)t * 128 + e] = (s0 + s1) + (s2 + s3);
 }
 
 // Top-8 experts and renormalised weights per token (wave per token; the decode path's

@@ -58,6 +58,10 @@ _sig(_g, "qxg_attention_layer", [vp, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_moe_layer", [vp, u32, vp, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_final_head", [vp, vp, vp, vp, u32, vp, vp, *ERR])
 _sig(_g, "qxg_set_layer_path", [vp, c_int])
+_sig(_g, "qxg_kv_export", [vp, cp, u32, u32, u32, u32, u32, *ERR])
+_sig(_g, "qxg_kv_import", [vp, cp, u32, u32, u32, ctypes.POINTER(u32), ctypes.POINTER(u32), *ERR])
+_sig(_g, "qxg_kvsnap_write", [cp, u32, u32, u32, u32, u32, vp, vp, vp, vp, *ERR])
+_sig(_g, "qxg_kvsnap_read", [cp, u32, u32, u32, vp, vp, vp, vp, ctypes.POINTER(u32), ctypes.POINTER(u32), *ERR])
 _sig(_g, "qxg_prefill", [vp, vp, u32, u32, c_int, vp, vp, u32, vp, vp, ctypes.POINTER(c_float), *ERR])
 _sig(_g, "qxg_prefill_layer", [vp, u32, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_time_kernel", [vp, c_int, u32, u32, ctypes.POINTER(c_float), *ERR])
@@ -92,6 +96,29 @@ def generate_model(path, layers=1, vocab=4096, experts=128, embedding=True, head
     if not _h.qxgen_write(str(path).encode(), ctypes.byref(sp), ctypes.byref(size), err, 512):
         raise QxgError(err.value.decode())
     return size.value
+
+
+def kvsnap_write(path, next_token, seed, k, v, ks, vs, positions):
+    """QXKVSNP1 file from host caches k, v [layers, ctx, 512] int8 and ks, vs [layers, ctx] f32."""
+    k, v = np.ascontiguousarray(k, np.int8), np.ascontiguousarray(v, np.int8)
+    ks, vs = np.ascontiguousarray(ks, np.float32), np.ascontiguousarray(vs, np.float32)
+    layers, ctx = ks.shape
+    err = ctypes.create_string_buffer(512)
+    if not _g.qxg_kvsnap_write(str(path).encode(), layers, positions, ctx, next_token, seed, _p(k), _p(v), _p(ks),
+                               _p(vs), err, 512):
+        raise QxgError(err.value.decode())
+
+
+def kvsnap_read(path, layers, ctx, seed):
+    """(k, v, ks, vs, positions, next_token) of a QXKVSNP1 file; rows past `positions` are zero."""
+    k = np.zeros((layers, ctx, 512), np.int8); v = np.zeros_like(k)
+    ks = np.zeros((layers, ctx), np.float32); vs = np.zeros_like(ks)
+    pos, nt = u32(), u32()
+    err = ctypes.create_string_buffer(512)
+    if not _g.qxg_kvsnap_read(str(path).encode(), layers, ctx, seed, _p(k), _p(v), _p(ks), _p(vs), ctypes.byref(pos),
+                              ctypes.byref(nt), err, 512):
+        raise QxgError(err.value.decode())
+    return k, v, ks, vs, pos.value, nt.value
 
 
 class MemModel:
@@ -156,6 +183,17 @@ class Context:
         ks = np.zeros(count, np.float32); vs = np.zeros(count, np.float32)
         self._check(_g.qxg_kv_read(self._c, layer, pos0, count, _p(k), _p(v), _p(ks), _p(vs), self._err, 1024))
         return k, v, ks, vs
+
+    def kv_export(self, path, layers, positions, ctx_tokens, next_token, seed):
+        self._check(_g.qxg_kv_export(self._c, str(path).encode(), layers, positions, ctx_tokens, next_token, seed,
+                                     self._err, 1024))
+
+    def kv_import(self, path, layers, ctx_tokens, seed):
+        """Returns (positions, next_token) of the snapshot written into the device cache."""
+        pos, nt = u32(), u32()
+        self._check(_g.qxg_kv_import(self._c, str(path).encode(), layers, ctx_tokens, seed, ctypes.byref(pos),
+                                     ctypes.byref(nt), self._err, 1024))
+        return pos.value, nt.value
 
     def dequant(self, ggml_type, raw, nblocks):
         raw = np.ascontiguousarray(raw, np.uint8)

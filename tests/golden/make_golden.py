@@ -4,7 +4,8 @@
 Inputs are QXF1 models written by this build's seeded generator
 (qx-mini-c_amd/host/qxgen.c), so a test can regenerate identical bytes anywhere.
 Only numeric summaries are stored: FNV-1a-64 of the reference's f32 outputs,
-argmax/top tokens and a few sampled values.  Re-run here after changing the
+argmax/top tokens and a few sampled values; plus the reference's QXKVSNP1 KV
+snapshots of the state-loop runs (kvsnap_*.bin, a few KB each).  Re-run here after changing the
 generator:  python3 tests/golden/make_golden.py
 """
 import json
@@ -21,6 +22,7 @@ sys.path.insert(0, os.path.join(ROOT, "qx-mini-c_amd"))
 import qxg  # noqa: E402
 
 REF = os.path.join(ROOT, "oracle", "_ref", "qxqxf")
+GOLDEN_DIR = os.path.dirname(os.path.abspath(__file__))
 
 # model specs used by the golden checks (layers, vocab, experts, seed)
 MODELS = {
@@ -80,8 +82,14 @@ def main():
             dd = os.path.join(d, f"s{k}")
             os.mkdir(dd)
             layers = MODELS[k]["layers"]
+            snap = os.path.join(GOLDEN_DIR, f"kvsnap_{k}.bin")
             txt = run(["state-loop-probe", "--in", paths[k], "--prompt-token", "17", "--steps", str(steps),
-                       "--layers", str(layers), "--ctx", "8", "--kv", "int8", "--full-moe", "--dump-residuals", dd])
+                       "--layers", str(layers), "--ctx", "8", "--kv", "int8", "--full-moe", "--dump-residuals", dd,
+                       "--kv-snapshot-out", snap])
+            hdr = np.fromfile(snap, np.uint32, count=12)
+            out.setdefault("kv_snapshot", {})[k] = {
+                "file": os.path.basename(snap), "final_token": int(re.search(r'"final_token": (\d+)', txt).group(1)),
+                "positions": int(hdr[4]), "seed": int(hdr[11]), "bytes": os.path.getsize(snap)}
             toks = [int(t) for t in re.findall(r'"input_token": (\d+)', txt)]
             experts = [[int(e) for e in re.findall(r"\d+", m)]
                        for m in re.findall(r'"selected_experts": \[([0-9, ]*)\]', txt)]
