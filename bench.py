@@ -163,6 +163,8 @@ def main():
                     help="config 5 leg: batched prefill of this many seeded token ids (0: skip)")
     ap.add_argument("--prefill-decode", type=int, default=128,
                     help="greedy tokens generated after the prefill (the first comes from the prefill's head)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the config 5 prefill leg (profiling aid; prints that leg's JSON)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-sized device buffer (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -191,6 +193,13 @@ def main():
     t0 = time.perf_counter()
     info = ctx.load(model.path, verify=False)
     log(f"uploaded {info.tensors} tensors, {info.tensor_bytes / 1e9:.3f} GB in {time.perf_counter() - t0:.1f} s")
+
+    if args.prefill_only:
+        leg = prefill_leg(ctx, args)
+        ctx.close()
+        model.close()
+        print(json.dumps({"prefill": leg}), flush=True)
+        return
 
     def prefill():
         ctx.kv_create(LAYERS, ctx_tokens)

@@ -5,6 +5,7 @@
 #include "qx_grids.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -112,6 +113,7 @@ struct qxg_ctx {
     KernelTiming kt;
     // persistent layer kernel: per-layer pointer table, tagged exchange buffers, abort flag
     bool persist = false;            // layer path: persistent kernel (true) or one kernel per phase
+    bool eager = false;              // QXG_EAGER=1 at open: qxg_generate launches every step without a graph
     std::vector<void *> arenas;      // per-plane arenas of all layers' weights
     QxPlane planes[PL_COUNT] = {};
     uint64_t *xch = nullptr;
@@ -574,6 +576,10 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
     }
     qxg_ctx *c = new qxg_ctx();
     c->device = device;
+    {
+        const char *ev = getenv("QXG_EAGER");
+        c->eager = ev && ev[0] == '1';
+    }
     bool ok = hip_ok(hipStreamCreateWithFlags(&c->s, hipStreamNonBlocking), err, err_len, "stream");
     std::vector<uint4> g2;
     std::vector<uint2> g3, sel;
@@ -854,7 +860,9 @@ int qxg_generate(qxg_ctx *c, const uint32_t *prompt, uint32_t n_prompt, uint32_t
     (void)hipMemcpyAsync(c->tokens, prompt, (uint64_t)n_prompt * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, pos0, 0, n_prompt, 0);
     c->kt.used = 0;
-    const bool use_graph = c->kt.which < 0;   // in-situ kernel timing records events per launch: run eagerly
+    // in-situ kernel timing records events per launch, and QXG_EAGER asks for plain launches
+    // (kernel tracers): run eagerly
+    const bool use_graph = c->kt.which < 0 && !c->eager;
     if (use_graph && !c->graph_exec) {
         // every kernel reads the position/step from the device state, so one recorded
         // step serves all steps; no memset nodes are recorded
