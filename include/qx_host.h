@@ -85,6 +85,10 @@ typedef struct qxgen_spec {
     uint32_t with_head;     /* output_norm.weight + output.weight (Q6_K) */
     uint64_t seed;
     uint32_t threads;       /* 0 = all online CPUs (capped at 16) */
+    uint32_t mix;           /* 0: IQ4_XS attention, IQ2_XS gate/up, IQ3_XXS down in every layer;
+                               1: the real checkpoint's per-layer mix, layer l by l % 4:
+                               0 -> (IQ4_XS v/o, IQ2_XS gate/up, IQ3_XXS down), 1 -> (Q5_K, IQ2_S, IQ4_XS),
+                               2 -> (IQ4_XS, IQ2_XS, IQ3_S), 3 -> (Q5_K, IQ2_S, IQ3_S); q/k stay IQ4_XS */
 } qxgen_spec;
 
 /* Writes a QXF1 file at `path` (truncating).  The bytes are a pure function of

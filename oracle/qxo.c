@@ -48,6 +48,8 @@ static uint32_t rd32(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1]
 static uint8_t ksign(uint32_t i) { return (uint8_t)(i | ((uint32_t)(__builtin_popcount(i) & 1) << 7)); }
 static uint8_t iq2_grid_byte(uint32_t idx, int j) { return qx_iq2xs_levels[(qx_iq2xs_packed[idx] >> (2 * j)) & 3]; }
 static uint8_t iq3_grid_byte(uint32_t idx, int j) { return qx_iq3xxs_levels[(qx_iq3xxs_packed[idx] >> (3 * j)) & 7]; }
+static uint8_t iq2s_grid_byte(uint32_t idx, int j) { return qx_iq2xs_levels[(qx_iq2s_packed[idx] >> (2 * j)) & 3]; }
+static uint8_t iq3s_grid_byte(uint32_t idx, int j) { return qx_iq3s_levels[(qx_iq3s_packed[idx] >> (3 * j)) & 7]; }
 
 /* :1914-1933 */
 static void dec_iq2_xs(const uint8_t *b, float *y) {
@@ -84,6 +86,41 @@ static void dec_iq3_xxs(const uint8_t *b, float *y) {
     }
 }
 
+/* :1961-1984 — 10-bit grid index (qs byte + 2 bits of qh), explicit sign bytes */
+static void dec_iq2_s(const uint8_t *b, float *y) {
+    const float d = qxo_fp16_to_f32(rd16(b));
+    const uint8_t *qs = b + 2, *sg = b + 34, *qh = b + 66, *sc = b + 74;
+    for (int ib = 0; ib < 8; ++ib) {
+        const float db0 = (d * (0.5f + (float)(sc[ib] & 15))) * 0.25f;
+        const float db1 = (d * (0.5f + (float)(sc[ib] >> 4))) * 0.25f;
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t idx = (uint32_t)qs[4 * ib + l] | (((uint32_t)qh[ib] << (8 - 2 * l)) & 0x300u);
+            const float db = l < 2 ? db0 : db1;
+            for (int j = 0; j < 8; ++j)
+                y[32 * ib + 8 * l + j] = (db * (float)iq2s_grid_byte(idx, j)) * ((sg[4 * ib + l] >> j) & 1 ? -1.0f : 1.0f);
+        }
+    }
+}
+
+/* :1986-2030 — 9-bit grid index (qs byte + 1 bit of qh), explicit sign bytes,
+ * scale d*(1+2s) per 32 values */
+static void dec_iq3_s(const uint8_t *b, float *y) {
+    const float d = qxo_fp16_to_f32(rd16(b));
+    const uint8_t *qs = b + 2, *qh = b + 66, *sg = b + 74, *sc = b + 106;
+    for (int ib = 0; ib < 8; ++ib) {
+        const float db = d * (1.0f + 2.0f * (float)((sc[ib / 2] >> (4 * (ib & 1))) & 15));
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t i1 = (uint32_t)qs[8 * ib + 2 * l] | (((uint32_t)qh[ib] << (8 - 2 * l)) & 256u);
+            const uint32_t i2 = (uint32_t)qs[8 * ib + 2 * l + 1] | (((uint32_t)qh[ib] << (7 - 2 * l)) & 256u);
+            const uint8_t s8 = sg[4 * ib + l];
+            for (int j = 0; j < 4; ++j) {
+                y[32 * ib + 8 * l + j] = (db * (float)iq3s_grid_byte(i1, j)) * ((s8 >> j) & 1 ? -1.0f : 1.0f);
+                y[32 * ib + 8 * l + j + 4] = (db * (float)iq3s_grid_byte(i2, j)) * ((s8 >> (j + 4)) & 1 ? -1.0f : 1.0f);
+            }
+        }
+    }
+}
+
 /* :2032-2053 */
 static void dec_iq4_xs(const uint8_t *b, float *y) {
     const float d = qxo_fp16_to_f32(rd16(b));
@@ -103,6 +140,23 @@ static void dec_iq4_xs(const uint8_t *b, float *y) {
 static void scale_min_k4(int j, const uint8_t *q, uint8_t *d, uint8_t *m) {
     if (j < 4) { *d = q[j] & 63; *m = q[j + 4] & 63; }
     else { *d = (uint8_t)((q[j + 4] & 15) | ((q[j - 4] >> 6) << 4)); *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4)); }
+}
+
+/* :2112-2145 — 5-bit codes: nibble of qs plus bit (2j or 2j+1) of qh[l] */
+static void dec_q5_k(const uint8_t *b, float *y) {
+    const float d = qxo_fp16_to_f32(rd16(b)), dmin = qxo_fp16_to_f32(rd16(b + 2));
+    const uint8_t *sc = b + 4, *qh = b + 16, *q = b + 48;
+    for (int j = 0; j < 4; ++j) {
+        uint8_t s, m;
+        scale_min_k4(2 * j, sc, &s, &m);
+        const float d1 = d * (float)s, m1 = dmin * (float)m;
+        scale_min_k4(2 * j + 1, sc, &s, &m);
+        const float d2 = d * (float)s, m2 = dmin * (float)m;
+        for (int l = 0; l < 32; ++l)
+            y[64 * j + l] = d1 * (float)((q[32 * j + l] & 15) | (((qh[l] >> (2 * j)) & 1) << 4)) - m1;
+        for (int l = 0; l < 32; ++l)
+            y[64 * j + 32 + l] = d2 * (float)((q[32 * j + l] >> 4) | (((qh[l] >> (2 * j + 1)) & 1) << 4)) - m2;
+    }
 }
 
 static void dec_q4_k(const uint8_t *b, float *y) {
@@ -140,7 +194,10 @@ static void dec_q6_k(const uint8_t *b, float *y) {
 }
 
 static uint64_t block_bytes(uint32_t t) {
-    switch (t) { case 12: return 144; case 14: return 210; case 17: return 74; case 18: return 98; case 23: return 136; default: return 0; }
+    switch (t) {
+    case 12: return 144; case 13: return 176; case 14: return 210; case 17: return 74; case 18: return 98;
+    case 21: return 110; case 22: return 82; case 23: return 136; default: return 0;
+    }
 }
 
 /* :2195-2217 */
@@ -150,6 +207,9 @@ int qxo_decode_block(uint32_t t, const uint8_t *raw, float out[256]) {
     case 14: dec_q6_k(raw, out); return 1;
     case 17: dec_iq2_xs(raw, out); return 1;
     case 18: dec_iq3_xxs(raw, out); return 1;
+    case 13: dec_q5_k(raw, out); return 1;
+    case 21: dec_iq3_s(raw, out); return 1;
+    case 22: dec_iq2_s(raw, out); return 1;
     case 23: dec_iq4_xs(raw, out); return 1;
     default: return 0;
     }
@@ -369,10 +429,12 @@ int qxo_moe_layer(qxo_model *m, uint32_t layer, const float *x, float *out, floa
     if (!isfinite(sel) || sel <= 0.0) return 0;
     for (int r = 0; r < 8; ++r) wts[r] /= sel;
     memset(moe, 0, sizeof(moe));
-    const uint64_t gate_expert = (uint64_t)F * 8 * 74, down_expert = 2048ull * 3 * 98;
+    const uint64_t gate_expert = (uint64_t)F * 8 * block_bytes(tg), up_expert = (uint64_t)F * 8 * block_bytes(tu),
+                   down_expert = 2048ull * (F / 256) * block_bytes(td);
+    if (!gate_expert || !up_expert || !down_expert) return 0;
     for (int r = 0; r < 8; ++r) {
         qxo_matvec(tg, G + ids[r] * gate_expert, F, 2048, xn, g);
-        qxo_matvec(tu, U + ids[r] * gate_expert, F, 2048, xn, u);
+        qxo_matvec(tu, U + ids[r] * up_expert, F, 2048, xn, u);
         for (uint32_t i = 0; i < F; ++i) h[i] = (float)(silu((double)g[i]) * (double)u[i]);
         qxo_matvec(td, D + ids[r] * down_expert, 2048, F, h, y);
         for (uint32_t i = 0; i < 2048; ++i) moe[i] += (float)(wts[r] * (double)y[i]);

@@ -10,6 +10,11 @@
  *   IQ4_XS attn q/k/v/o: d = fp16(U[1e-5,3e-5]); scales_h, scales_l, qs uniform
  *   IQ2_XS gate/up    : d = fp16(U[2e-4,5e-4]); qs (9-bit grid, 7-bit sign) and scales uniform
  *   IQ3_XXS down      : d = fp16(U[1e-4,3e-4]); qs bytes and aux32 words uniform
+ * and, in the real-checkpoint mix (spec->mix = 1):
+ *   Q5_K  attn v/o    : d, dmin = fp16(U[1e-5,3e-5]); scales, qh, qs uniform bytes
+ *   IQ2_S gate/up     : d = fp16(U[2e-4,5e-4]); qs, signs, qh, scales uniform
+ *   IQ3_S down        : d = fp16(U[1e-4,3e-4]); qs, qh, signs, scales uniform
+ *   IQ4_XS down       : as the attention IQ4_XS
  *   F32 norms         : U(0.5,1.5);  router ffn_gate_inp: N(0, 0.02)
  * The fp16 ranges keep every projection output O(1) over 48 layers. */
 #ifndef _GNU_SOURCE
@@ -127,6 +132,19 @@ static void gen_block(const gen_tensor *t, uint64_t blk, uint8_t *out, uint64_t 
         put16(out, fp16_unif(&s, 1e-4, 3e-4));
         fill_bytes(out + 2, 96, &s);
         break;
+    case QXT_Q5_K:
+        put16(out, fp16_unif(&s, 1e-5, 3e-5));
+        put16(out + 2, fp16_unif(&s, 1e-5, 3e-5));
+        fill_bytes(out + 4, 172, &s);
+        break;
+    case QXT_IQ2_S:
+        put16(out, fp16_unif(&s, 2e-4, 5e-4));
+        fill_bytes(out + 2, 80, &s);
+        break;
+    case QXT_IQ3_S:
+        put16(out, fp16_unif(&s, 1e-4, 3e-4));
+        fill_bytes(out + 2, 108, &s);
+        break;
     default:
         memset(out, 0, nbytes);
     }
@@ -207,15 +225,19 @@ static uint32_t build_tensor_list(const qxgen_spec *sp, gen_tensor *v) {
         T("attn_norm.weight", QXT_F32, 1, H, 0, 0, DIST_NORM_W);
         T("attn_q.weight", QXT_IQ4_XS, 2, H, 4096, 0, 0);
         T("attn_k.weight", QXT_IQ4_XS, 2, H, 512, 0, 0);
-        T("attn_v.weight", QXT_IQ4_XS, 2, H, 512, 0, 0);
-        T("attn_output.weight", QXT_IQ4_XS, 2, 4096, H, 0, 0);
+        const uint32_t k4 = sp->mix ? l % 4 : 0;
+        const uint32_t t_vo = (k4 == 1 || k4 == 3) ? QXT_Q5_K : QXT_IQ4_XS;
+        const uint32_t t_gu = (k4 == 1 || k4 == 3) ? QXT_IQ2_S : QXT_IQ2_XS;
+        const uint32_t t_dn = k4 == 0 ? QXT_IQ3_XXS : k4 == 1 ? QXT_IQ4_XS : QXT_IQ3_S;
+        T("attn_v.weight", t_vo, 2, H, 512, 0, 0);
+        T("attn_output.weight", t_vo, 2, 4096, H, 0, 0);
         T("attn_q_norm.weight", QXT_F32, 1, 128, 0, 0, DIST_NORM_W);
         T("attn_k_norm.weight", QXT_F32, 1, 128, 0, 0, DIST_NORM_W);
         T("ffn_norm.weight", QXT_F32, 1, H, 0, 0, DIST_NORM_W);
         T("ffn_gate_inp.weight", QXT_F32, 2, H, E, 0, DIST_ROUTER);
-        T("ffn_gate_exps.weight", QXT_IQ2_XS, 3, H, F, E, 0);
-        T("ffn_up_exps.weight", QXT_IQ2_XS, 3, H, F, E, 0);
-        T("ffn_down_exps.weight", QXT_IQ3_XXS, 3, F, H, E, 0);
+        T("ffn_gate_exps.weight", t_gu, 3, H, F, E, 0);
+        T("ffn_up_exps.weight", t_gu, 3, H, F, E, 0);
+        T("ffn_down_exps.weight", t_dn, 3, F, H, E, 0);
 #undef T
     }
     return n;
@@ -224,8 +246,8 @@ static uint32_t build_tensor_list(const qxgen_spec *sp, gen_tensor *v) {
 static uint32_t dtype_for(uint32_t type) {
     switch (type) {
     case QXT_F32: return 2;
-    case QXT_IQ2_XS: return 5;
-    case QXT_IQ3_XXS: return 4;
+    case QXT_IQ2_XS: case QXT_IQ2_S: return 5;
+    case QXT_IQ3_XXS: case QXT_IQ3_S: return 4;
     default: return 3;
     }
 }

@@ -35,7 +35,7 @@ def _sig(lib, name, args, res=c_int):
 
 class GenSpec(ctypes.Structure):
     _fields_ = [("layers", u32), ("vocab", u32), ("experts", u32), ("with_embedding", u32), ("with_head", u32),
-                ("seed", u64), ("threads", u32)]
+                ("seed", u64), ("threads", u32), ("mix", u32)]
 
 
 class ModelInfo(ctypes.Structure):
@@ -88,9 +88,10 @@ def fnv1a64(a):
     return int(_h.qxf_fnv1a64(_p(a), a.nbytes))
 
 
-def generate_model(path, layers=1, vocab=4096, experts=128, embedding=True, head=True, seed=1, threads=0):
-    """Writes the seeded random-init QXF1 model; returns its size in bytes."""
-    sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads)
+def generate_model(path, layers=1, vocab=4096, experts=128, embedding=True, head=True, seed=1, threads=0, mix=0):
+    """Writes the seeded random-init QXF1 model (mix=1: the real checkpoint's per-layer
+    quant types); returns its size in bytes."""
+    sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads, mix)
     err = ctypes.create_string_buffer(512)
     size = u64()
     if not _h.qxgen_write(str(path).encode(), ctypes.byref(sp), ctypes.byref(size), err, 512):
@@ -124,8 +125,8 @@ def kvsnap_read(path, layers, ctx, seed):
 class MemModel:
     """Seeded QXF1 model in an anonymous in-memory file (path /proc/self/fd/N)."""
 
-    def __init__(self, layers=48, vocab=151936, experts=128, embedding=True, head=True, seed=1, threads=0):
-        sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads)
+    def __init__(self, layers=48, vocab=151936, experts=128, embedding=True, head=True, seed=1, threads=0, mix=0):
+        sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads, mix)
         err = ctypes.create_string_buffer(512)
         path = ctypes.create_string_buffer(128)
         fd = c_int()

@@ -28,7 +28,12 @@ GOLDEN_DIR = os.path.dirname(os.path.abspath(__file__))
 MODELS = {
     "A": dict(layers=1, vocab=1024, experts=16, seed=1234),
     "B": dict(layers=2, vocab=2048, experts=128, seed=77),
+    # the real checkpoint's per-layer quant mix: Q5_K v/o, IQ2_S gate/up, IQ4_XS and IQ3_S down
+    "C": dict(layers=4, vocab=1024, experts=16, seed=4321, mix=1),
 }
+DECODE_BLOCKS_C = [("blk.1.attn_v.weight", [0, 3, 4095]), ("blk.3.attn_output.weight", [0, 7, 32767]),
+                   ("blk.1.ffn_gate_exps.weight", [0, 5, 98303]), ("blk.3.ffn_up_exps.weight", [11]),
+                   ("blk.2.ffn_down_exps.weight", [0, 9, 98303]), ("blk.1.ffn_down_exps.weight", [4, 98303])]
 DECODE_BLOCKS = [("token_embd.weight", [0, 1, 4095]), ("output.weight", [0, 7, 8191]),
                  ("blk.0.attn_q.weight", [0, 3, 32767]), ("blk.0.attn_output.weight", [5]),
                  ("blk.0.ffn_gate_exps.weight", [0, 1, 98303]), ("blk.0.ffn_up_exps.weight", [12345]),
@@ -62,6 +67,10 @@ def main():
                 j = json.loads(run(["decode-block", "--in", paths["A"], "--name", name, "--block", str(b)]))
                 out["decode_block"][f"{name}#{b}"] = {"f32_checksum": str(j["f32_checksum"]),
                                                        "first8": j["first8"]}
+        for name, blocks in DECODE_BLOCKS_C:
+            for b in blocks:
+                j = json.loads(run(["decode-block", "--in", paths["C"], "--name", name, "--block", str(b)]))
+                out["decode_block"][f"C:{name}#{b}"] = {"f32_checksum": str(j["f32_checksum"]), "first8": j["first8"]}
         # final head probe (src/qx_format.c:5369-5411) on seeded residuals
         for k in ("A", "B"):
             for seed in (1, 2):
@@ -78,7 +87,7 @@ def main():
                     "argmax_token": j["argmax_token"], "argmax_logit": j["argmax_logit"],
                     "top8_by_float": [int(i) for i in order], "logits_sample": [float(v) for v in lg[:4]]}
         # full-MoE state loop with INT8 KV and per-layer dumps (src/qx_format.c:5970-6719)
-        for k, steps in (("A", 5), ("B", 4)):
+        for k, steps in (("A", 5), ("B", 4), ("C", 3)):
             dd = os.path.join(d, f"s{k}")
             os.mkdir(dd)
             layers = MODELS[k]["layers"]

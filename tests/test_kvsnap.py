@@ -35,7 +35,7 @@ def oracle_cache(tmp_path, k):
     return kv
 
 
-@pytest.mark.parametrize("k", ["A", "B"])
+@pytest.mark.parametrize("k", ["A", "B", "C"])
 def test_snapshot_bytes_match_reference(tmp_path, k):
     snap = GOLDEN["kv_snapshot"][k]
     ref = np.fromfile(os.path.join(GOLDEN_DIR, snap["file"]), np.uint8)

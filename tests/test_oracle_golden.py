@@ -29,9 +29,11 @@ def models(tmp_path_factory):
 
 
 def test_decode_block_matches_reference(models):
-    m = models["A"]
+    BB.update({13: 176, 21: 110, 22: 82})
     for key, want in GOLDEN["decode_block"].items():
-        name, b = key.split("#")
+        k, _, rest = key.rpartition(":")
+        m = models[k or "A"]
+        name, b = rest.split("#")
         t, dims, raw = m.tensor(name)
         v = qxo.decode_block(t, raw[int(b) * BB[t]:(int(b) + 1) * BB[t]])
         assert str(qxo.fnv1a64(v)) == want["f32_checksum"], key
@@ -49,7 +51,7 @@ def test_final_head_matches_reference(models):
         assert float(tl[0]) == pytest.approx(want["argmax_logit"], rel=0, abs=0)
 
 
-@pytest.mark.parametrize("k", ["A", "B"])
+@pytest.mark.parametrize("k", ["A", "B", "C"])
 def test_state_loop_layer_dumps_match_reference(models, k):
     """Per step and layer: input, v-cur, kqv-out, ffn-inp, ffn-moe-out, output are
     bit-identical to the reference's --dump-residuals files (INT8 KV, double

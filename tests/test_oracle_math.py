@@ -32,6 +32,23 @@ def _grid_tables():
     return g2, g3, f2, f3
 
 
+def _grid_tables_s():
+    src = open(GRIDS_H).read()
+    p2 = [int(x, 16) for x in re.search(r"qx_iq2s_packed\[1024\] = \{(.*?)\};", src, re.S).group(1).replace(",", " ").split()]
+    p3 = [int(x, 16) for x in re.search(r"qx_iq3s_packed\[512\] = \{(.*?)\};", src, re.S).group(1).replace(",", " ").split()]
+    f2 = int(re.search(r"QX_IQ2S_GRID_FNV (0x[0-9a-f]+)", src).group(1), 16)
+    f3 = int(re.search(r"QX_IQ3S_GRID_FNV (0x[0-9a-f]+)", src).group(1), 16)
+    g2 = np.array([[[8, 25, 43][(c >> (2 * j)) & 3] for j in range(8)] for c in p2], np.uint8)
+    g3 = np.array([[[1, 3, 5, 7, 9, 11, 13, 15][(c >> (3 * j)) & 7] for j in range(4)] for c in p3], np.uint8)
+    return g2, g3, f2, f3
+
+
+def test_iq2s_iq3s_grid_expansion_matches_recorded_fnv():
+    g2, g3, f2, f3 = _grid_tables_s()
+    assert qxo.fnv1a64(g2) == f2 and qxo.fnv1a64(g3) == f3
+    assert len({bytes(r) for r in g2}) == 1024 and len({bytes(r) for r in g3}) == 512
+
+
 def test_grid_expansion_matches_recorded_fnv():
     g2, g3, f2, f3 = _grid_tables()
     assert qxo.fnv1a64(g2) == f2 and qxo.fnv1a64(g3) == f3
@@ -49,6 +66,9 @@ def test_grids_equal_reference_tables():
     assert [int.from_bytes(bytes(r), "little") for r in g2] == arr("qx_iq2xs_grid")
     assert [int.from_bytes(bytes(r), "little") for r in g3] == arr("qx_iq3xxs_grid")
     assert arr("qx_ksigns_iq2xs") == [i | ((bin(i).count("1") & 1) << 7) for i in range(128)]
+    g2s, g3s, _, _ = _grid_tables_s()
+    assert [int.from_bytes(bytes(r), "little") for r in g2s] == arr("qx_iq2s_grid")
+    assert [int.from_bytes(bytes(r), "little") for r in g3s] == arr("qx_iq3s_grid")
 
 
 def _iq4_block(d16, ls, nib):
