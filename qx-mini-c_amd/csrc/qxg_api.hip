@@ -71,6 +71,9 @@ bool block_geom(uint32_t t, uint64_t &bv, uint64_t &bb) {
     case 17: bv = 256; bb = 74; return true;
     case 18: bv = 256; bb = 98; return true;
     case 23: bv = 256; bb = 136; return true;
+    case 13: bv = 256; bb = 176; return true;
+    case 21: bv = 256; bb = 110; return true;
+    case 22: bv = 256; bb = 82; return true;
     default: return false;
     }
 }
@@ -113,6 +116,7 @@ struct qxg_ctx {
     KernelTiming kt;
     // persistent layer kernel: per-layer pointer table, tagged exchange buffers, abort flag
     bool persist = false;            // layer path: persistent kernel (true) or one kernel per phase
+    bool base_mix = true;            // every layer in the benchmark mix (IQ4_XS attention, IQ2_XS/IQ3_XXS experts)
     bool eager = false;              // QXG_EAGER=1 at open: qxg_generate launches every step without a graph
     std::vector<void *> arenas;      // per-plane arenas of all layers' weights
     QxPlane planes[PL_COUNT] = {};
@@ -148,6 +152,9 @@ bool upload_planes(qxg_ctx *c, QTensor &t, const void *host, uint64_t nbytes, ch
     case 17: sz[0] = 64 * nb; sz[1] = 8 * nb; sz[3] = 2 * nb; break;
     case 18: sz[0] = 64 * nb; sz[1] = 32 * nb; sz[3] = 2 * nb; break;
     case 14: sz[0] = 128 * nb; sz[1] = 64 * nb; sz[2] = 16 * nb; sz[3] = 2 * nb; break;
+    case 13: sz[0] = 128 * nb; sz[1] = 16 * nb; sz[2] = 32 * nb; break;
+    case 22: sz[0] = 64 * nb; sz[1] = 8 * nb; sz[2] = 8 * nb; sz[3] = 2 * nb; break;
+    case 21: sz[0] = 64 * nb; sz[1] = 32 * nb; sz[2] = 16 * nb; sz[3] = 2 * nb; break;
     default: sz[0] = nbytes; break;   // F32, Q4_K: original bytes
     }
     const uint64_t total = align256(sz[0]) + align256(sz[1]) + align256(sz[2]) + align256(sz[3]);
@@ -185,6 +192,38 @@ void drop_graph(qxg_ctx *c) {
 void free_tensor(QTensor &t) {
     if (t.base) (void)hipFree(t.base);
     t.base = nullptr;
+}
+
+void build_tables_s(std::vector<uint4> &g2s, std::vector<uint2> &g3s, std::vector<uint2> &sel8) {
+    g2s.resize(1024);
+    for (int i = 0; i < 1024; ++i) {
+        uint32_t pos[2] = {0, 0}, neg[2] = {0, 0};
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t v = qx_iq2xs_levels[(qx_iq2s_packed[i] >> (2 * j)) & 3];
+            pos[j >> 2] |= v << (8 * (j & 3));
+            neg[j >> 2] |= ((256u - v) & 255u) << (8 * (j & 3));
+        }
+        g2s[i] = make_uint4(pos[0], pos[1], neg[0], neg[1]);
+    }
+    g3s.resize(512);
+    for (int i = 0; i < 512; ++i) {
+        uint32_t pos = 0, neg = 0;
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t v = qx_iq3s_levels[(qx_iq3s_packed[i] >> (3 * j)) & 7];
+            pos |= v << (8 * j);
+            neg |= ((256u - v) & 255u) << (8 * j);
+        }
+        g3s[i] = make_uint2(pos, neg);
+    }
+    sel8.resize(256);
+    for (uint32_t s = 0; s < 256; ++s) {   // explicit sign bytes (IQ2_S, IQ3_S)
+        uint32_t a = 0, b = 0;
+        for (int j = 0; j < 4; ++j) {
+            a |= (uint32_t)(j + 4 * ((s >> j) & 1)) << (8 * j);
+            b |= (uint32_t)(j + 4 * ((s >> (j + 4)) & 1)) << (8 * j);
+        }
+        sel8[s] = make_uint2(a, b);
+    }
 }
 
 void build_tables(std::vector<uint4> &g2, std::vector<uint2> &g3, std::vector<uint2> &sel) {
@@ -283,6 +322,10 @@ struct Dumps {
     float *layer = nullptr, *attn = nullptr, *moe = nullptr, *vcur = nullptr, *ctx = nullptr;
 };
 
+// The persistent kernel reads the weight arenas, built for the benchmark mix only; a model
+// with the checkpoint's other per-layer formats runs one kernel per phase.
+bool persistent(const qxg_ctx *c) { return c->persist && c->base_mix; }
+
 // Sub-layers [s0, s1) of the token in one persistent launch (2l: attention half of
 // layer l, 2l+1: its MoE half), residual x_in -> x_out (device buffers).
 void launch_layers(qxg_ctx *c, uint32_t s0, uint32_t s1, const float *x_in, float *x_out, const Dumps &d) {
@@ -313,7 +356,7 @@ void launch_step(qxg_ctx *c, uint32_t top_n, bool dump_layers) {
     hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
     Dumps d;
     if (dump_layers) d.layer = c->layer_dump;
-    if (c->persist) {
+    if (persistent(c)) {
         if (c->layers) launch_layers(c, 0, 2 * c->layers, c->x, c->x, d);
     } else {
         for (uint32_t l = 0; l < c->layers; ++l) {
@@ -449,6 +492,10 @@ uint16_t f16_int(int v) {
 }
 
 bool prefill_ready(qxg_ctx *c, char *err, uint64_t n) {
+    if (!c->base_mix) {
+        set_err(err, n, "prefill supports the IQ4_XS / IQ2_XS / IQ3_XXS mix only (decode the prompt token by token)");
+        return false;
+    }
     auto &B = c->pf;
     if (B.ready) return true;
     auto alloc = [&](void **p, uint64_t bytes) {
@@ -581,9 +628,10 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
         c->eager = ev && ev[0] == '1';
     }
     bool ok = hip_ok(hipStreamCreateWithFlags(&c->s, hipStreamNonBlocking), err, err_len, "stream");
-    std::vector<uint4> g2;
-    std::vector<uint2> g3, sel;
+    std::vector<uint4> g2, g2s;
+    std::vector<uint2> g3, sel, g3s, sel8;
     build_tables(g2, g3, sel);
+    build_tables_s(g2s, g3s, sel8);
     std::vector<double> rc((size_t)QXG_MAX_CTX * 64), rs((size_t)QXG_MAX_CTX * 64);
     // reference qx_apply_rope (src/qx_format.c:4625-4641): f = pow(theta, -(2i)/hd), angle = pos*f,
     // double cos/sin -- evaluated once here with the host libm.
@@ -598,12 +646,18 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
          hip_ok(hipMalloc(&c->T.g3, g3.size() * sizeof(uint2)), err, err_len, "tables") &&
          hip_ok(hipMalloc(&c->T.sel, sel.size() * sizeof(uint2)), err, err_len, "tables") &&
          hip_ok(hipMalloc(&c->T.rope_cos, rc.size() * sizeof(double)), err, err_len, "tables") &&
-         hip_ok(hipMalloc(&c->T.rope_sin, rs.size() * sizeof(double)), err, err_len, "tables");
+         hip_ok(hipMalloc(&c->T.rope_sin, rs.size() * sizeof(double)), err, err_len, "tables") &&
+         hip_ok(hipMalloc(&c->T.g2s, g2s.size() * sizeof(uint4)), err, err_len, "tables") &&
+         hip_ok(hipMalloc(&c->T.g3s, g3s.size() * sizeof(uint2)), err, err_len, "tables") &&
+         hip_ok(hipMalloc(&c->T.sel8, sel8.size() * sizeof(uint2)), err, err_len, "tables");
     ok = ok && hip_ok(hipMemcpy(c->T.g2, g2.data(), g2.size() * sizeof(uint4), hipMemcpyHostToDevice), err, err_len, "tables") &&
          hip_ok(hipMemcpy(c->T.g3, g3.data(), g3.size() * sizeof(uint2), hipMemcpyHostToDevice), err, err_len, "tables") &&
          hip_ok(hipMemcpy(c->T.sel, sel.data(), sel.size() * sizeof(uint2), hipMemcpyHostToDevice), err, err_len, "tables") &&
          hip_ok(hipMemcpy(c->T.rope_cos, rc.data(), rc.size() * sizeof(double), hipMemcpyHostToDevice), err, err_len, "tables") &&
-         hip_ok(hipMemcpy(c->T.rope_sin, rs.data(), rs.size() * sizeof(double), hipMemcpyHostToDevice), err, err_len, "tables");
+         hip_ok(hipMemcpy(c->T.rope_sin, rs.data(), rs.size() * sizeof(double), hipMemcpyHostToDevice), err, err_len, "tables") &&
+         hip_ok(hipMemcpy(c->T.g2s, g2s.data(), g2s.size() * sizeof(uint4), hipMemcpyHostToDevice), err, err_len, "tables") &&
+         hip_ok(hipMemcpy(c->T.g3s, g3s.data(), g3s.size() * sizeof(uint2), hipMemcpyHostToDevice), err, err_len, "tables") &&
+         hip_ok(hipMemcpy(c->T.sel8, sel8.data(), sel8.size() * sizeof(uint2), hipMemcpyHostToDevice), err, err_len, "tables");
     ok = ok && hip_ok(hipMalloc(&c->st, sizeof(DevState)), err, err_len, "state") &&
          hip_ok(hipMemset(c->st, 0, sizeof(DevState)), err, err_len, "state");
     // tagged exchange buffers start at epoch 0, which no launch uses
@@ -623,7 +677,7 @@ void qxg_close(qxg_ctx *c) {
     if (c->s) (void)hipStreamSynchronize(c->s);
     drop_graph(c);
     for (auto &kv : c->tens) free_tensor(kv.second);
-    void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->kc, c->vc, c->ks, c->vs, c->x,
+    void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->T.g2s, c->T.g3s, c->T.sel8, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
                     c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging,
                     c->xch, c->abort};
@@ -665,6 +719,7 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     c->bound = false;
     c->L.assign(layers, LayerW{});
     c->experts = 0;
+    bool base = true;
     char msg[256];
     auto bad = [&](const std::string &nm, const char *why) {
         snprintf(msg, sizeof(msg), "%s: %s", nm.c_str(), why);
@@ -673,17 +728,22 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     };
     for (uint32_t l = 0; l < layers; ++l) {
         const std::string p = "blk." + std::to_string(l) + ".";
-        struct { const char *sfx; uint32_t type; uint64_t d0, d1; const QTensor **slot; } q[] = {
-            {"attn_q.weight", 23, 2048, 4096, &c->L[l].wq}, {"attn_k.weight", 23, 2048, 512, &c->L[l].wk},
-            {"attn_v.weight", 23, 2048, 512, &c->L[l].wv}, {"attn_output.weight", 23, 4096, 2048, &c->L[l].wo},
-            {"ffn_gate_exps.weight", 17, 2048, 768, &c->L[l].gate}, {"ffn_up_exps.weight", 17, 2048, 768, &c->L[l].up},
-            {"ffn_down_exps.weight", 18, 768, 2048, &c->L[l].down}};
+        // accepted formats: the benchmark mix first, then the real checkpoint's per-layer
+        // alternatives (attention Q5_K, gate/up IQ2_S, down IQ4_XS or IQ3_S)
+        struct { const char *sfx; uint32_t type, alt1, alt2; uint64_t d0, d1; const QTensor **slot; } q[] = {
+            {"attn_q.weight", 23, 13, 13, 2048, 4096, &c->L[l].wq}, {"attn_k.weight", 23, 13, 13, 2048, 512, &c->L[l].wk},
+            {"attn_v.weight", 23, 13, 13, 2048, 512, &c->L[l].wv}, {"attn_output.weight", 23, 13, 13, 4096, 2048, &c->L[l].wo},
+            {"ffn_gate_exps.weight", 17, 22, 22, 2048, 768, &c->L[l].gate}, {"ffn_up_exps.weight", 17, 22, 22, 2048, 768, &c->L[l].up},
+            {"ffn_down_exps.weight", 18, 23, 21, 768, 2048, &c->L[l].down}};
         for (auto &e : q) {
             const QTensor *t = find(c, p + e.sfx);
             if (!t) return bad(p + e.sfx, "not uploaded");
-            if (t->type != e.type || t->dims[0] != e.d0 || t->dims[1] != e.d1) return bad(p + e.sfx, "unsupported type or shape");
+            if (t->type != e.type && t->type != e.alt1 && t->type != e.alt2) return bad(p + e.sfx, "unsupported quantization type");
+            if (t->dims[0] != e.d0 || t->dims[1] != e.d1) return bad(p + e.sfx, "unexpected shape");
+            if (t->type != e.type) base = false;
             *e.slot = t;
         }
+        if (c->L[l].gate->type != c->L[l].up->type) return bad(p + "ffn_up_exps.weight", "gate and up experts must share a type");
         const uint32_t E = (uint32_t)c->L[l].gate->dims[2];
         if (E < 8 || E > 128 || c->L[l].up->dims[2] != E || c->L[l].down->dims[2] != E) return bad(p + "ffn_*_exps.weight", "expert count");
         if (l == 0) c->experts = E;
@@ -700,6 +760,7 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
         }
     }
     c->layers = layers;
+    c->base_mix = base;
     c->emb = nullptr; c->head = nullptr; c->out_norm = nullptr; c->vocab = 0;
     if (need_embedding) {
         const QTensor *t = find(c, "token_embd.weight");
@@ -733,7 +794,7 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i)
         if (!hip_ok(hipMalloc(bufs[i], sizes[i]), err, err_len, "work buffers")) return 0;
     if (!hip_ok(hipMemset(c->tokens, 0, sizes[15]), err, err_len, "work buffers")) return 0;
-    if (layers && !build_arenas(c, err, err_len)) return 0;
+    if (layers && base && !build_arenas(c, err, err_len)) return 0;
     c->bound = true;
     return 1;
 }
@@ -817,7 +878,7 @@ int qxg_decode_token(qxg_ctx *c, uint32_t token, uint32_t position, int run_head
     hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
     Dumps d;
     if (layer_out) d.layer = c->layer_dump;
-    if (c->persist) {
+    if (persistent(c)) {
         if (c->layers) launch_layers(c, 0, 2 * c->layers, c->x, c->x, d);
     } else {
         for (uint32_t l = 0; l < c->layers; ++l) {
@@ -938,7 +999,7 @@ int qxg_attention_layer(qxg_ctx *c, uint32_t layer, uint32_t position, const flo
     (void)hipSetDevice(c->device);
     (void)hipMemcpyAsync(c->x, x_in, 2048 * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, position, 0, 1, 1);
-    if (c->persist) {
+    if (persistent(c)) {
         Dumps d;
         d.attn = c->attn; d.vcur = c->vcur; d.ctx = c->ctxv;
         launch_layers(c, 2 * layer, 2 * layer + 1, c->x, c->x, d);
@@ -959,7 +1020,7 @@ int qxg_moe_layer(qxg_ctx *c, uint32_t layer, const float *ffn_inp, float *layer
     (void)hipSetDevice(c->device);
     (void)hipMemcpyAsync(c->x, ffn_inp, 2048 * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, 0, 0, 1, 1);
-    if (c->persist) {
+    if (persistent(c)) {
         Dumps d;
         d.moe = c->moe;
         launch_layers(c, 2 * layer + 1, 2 * layer + 2, c->x, c->x, d);

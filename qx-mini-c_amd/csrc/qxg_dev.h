@@ -154,6 +154,82 @@ DEV float dot_iq3(uint2 qs, uint32_t aux, uint32_t d16, const Dig &g, const uint
     return ((fp16_exact(d16) * 0.25f) * g.s) * combine(k * aH, k * aM, k * aL);
 }
 
+// IQ2_S sub-block (32 values = 4 grid entries of 8; src/qx_format.c:1961-1984): 10-bit grid
+// index qs[l] | (2 bits of the sub-block's qh byte), explicit sign byte per entry,
+// halves scaled d*(2s+1)/8 as IQ2_XS.  G2S: 1024 entries {pos lo, pos hi, neg lo, neg hi};
+// SEL8: sign byte -> v_perm selectors.
+DEV float dot_iq2s(uint32_t qs4, uint32_t sg4, uint32_t qh, uint32_t sc, uint32_t d16, const Dig &g,
+                   const uint4 *G2S, const uint2 *SEL8) {
+    int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const uint32_t idx = ((qs4 >> (8 * l)) & 255u) | ((qh << (8 - 2 * l)) & 0x300u);
+        const uint4 gg = G2S[idx];
+        const uint2 sl = SEL8[(sg4 >> (8 * l)) & 255u];
+        const uint32_t w0 = perm(gg.z, gg.x, sl.x), w1 = perm(gg.w, gg.y, sl.y);
+        if (l < 2) {
+            h0 = sdot4(w0, g.h[2 * l], h0); h0 = sdot4(w1, g.h[2 * l + 1], h0);
+            m0 = sdot4(w0, g.m[2 * l], m0); m0 = sdot4(w1, g.m[2 * l + 1], m0);
+            l0 = sdot4(w0, g.l[2 * l], l0); l0 = sdot4(w1, g.l[2 * l + 1], l0);
+        } else {
+            h1 = sdot4(w0, g.h[2 * l], h1); h1 = sdot4(w1, g.h[2 * l + 1], h1);
+            m1 = sdot4(w0, g.m[2 * l], m1); m1 = sdot4(w1, g.m[2 * l + 1], m1);
+            l1 = sdot4(w0, g.l[2 * l], l1); l1 = sdot4(w1, g.l[2 * l + 1], l1);
+        }
+    }
+    const int k0 = 2 * (int)(sc & 15u) + 1, k1 = 2 * (int)((sc >> 4) & 15u) + 1;
+    const float v = combine(k0 * h0 + k1 * h1, k0 * m0 + k1 * m1, k0 * l0 + k1 * l1);
+    return ((fp16_exact(d16) * 0.125f) * g.s) * v;
+}
+
+// IQ3_S sub-block (src/qx_format.c:1986-2030): 8 grid indices of 9 bits (qs byte | one
+// bit of the sub-block's qh byte), 4 values each, explicit sign byte per 8 values,
+// scale d*(2s+1) (s = the sub-block's 4-bit scale).  G3S: 512 entries {pos, neg}.
+DEV float dot_iq3s(uint2 qs8, uint32_t sg4, uint32_t qh, uint32_t sc, uint32_t d16, const Dig &g,
+                   const uint2 *G3S, const uint2 *SEL8) {
+    int aH = 0, aM = 0, aL = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const uint32_t word = l < 2 ? qs8.x : qs8.y;
+        const uint32_t b1 = ((word >> (16 * (l & 1))) & 255u) | ((qh << (8 - 2 * l)) & 256u);
+        const uint32_t b2 = ((word >> (16 * (l & 1) + 8)) & 255u) | ((qh << (7 - 2 * l)) & 256u);
+        const uint2 g1 = G3S[b1], g2 = G3S[b2];
+        const uint2 sl = SEL8[(sg4 >> (8 * l)) & 255u];
+        const uint32_t w0 = perm(g1.y, g1.x, sl.x), w1 = perm(g2.y, g2.x, sl.y);
+        aH = sdot4(w0, g.h[2 * l], aH); aH = sdot4(w1, g.h[2 * l + 1], aH);
+        aM = sdot4(w0, g.m[2 * l], aM); aM = sdot4(w1, g.m[2 * l + 1], aM);
+        aL = sdot4(w0, g.l[2 * l], aL); aL = sdot4(w1, g.l[2 * l + 1], aL);
+    }
+    const int k = 2 * (int)(sc & 15u) + 1;
+    return (fp16_exact(d16) * g.s) * combine(k * aH, k * aM, k * aL);
+}
+
+// Q5_K sub-block ib (src/qx_format.c:2112-2145): values 32ib..32ib+31 have 5-bit codes
+// (nibble ib&1 of qs[32*(ib/2) + l]) | (bit ib of qh[l]) << 4 and w = d*sc*code - dmin*m
+// (6-bit sc, m of the sub-block, get_scale_min_k4 :2079-2087).  The dot is
+// d*sc * sum(code*x) - dmin*m * sum(x), both sums exact over the digits.  qa, qb: the
+// 32 qs bytes of the sub-block's 64-value group; ha, hb: the block's 32 qh bytes;
+// meta = {d, dmin, scales[12]}.
+DEV float dot_q5(uint4 qa, uint4 qb, uint4 ha, uint4 hb, uint4 meta, int ib, const Dig &g) {
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    const uint32_t hq[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+    const uint32_t nsh = 4 * (ib & 1);
+    int aH = 0, aM = 0, aL = 0, sH = 0, sM = 0, sL = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t c = ((q[k] >> nsh) & 0x0f0f0f0fu) | (((hq[k] >> ib) & 0x01010101u) << 4);
+        aH = sdot4(c, g.h[k], aH); aM = sdot4(c, g.m[k], aM); aL = sdot4(c, g.l[k], aL);
+        sH = sdot4(0x01010101u, g.h[k], sH); sM = sdot4(0x01010101u, g.m[k], sM); sL = sdot4(0x01010101u, g.l[k], sL);
+    }
+    const uint32_t s[3] = {meta.y, meta.z, meta.w};   // scales bytes 0..11
+    auto byte = [&](int i) -> uint32_t { return (s[i >> 2] >> (8 * (i & 3))) & 255u; };
+    uint32_t sc, mn;
+    if (ib < 4) { sc = byte(ib) & 63u; mn = byte(ib + 4) & 63u; }
+    else { sc = (byte(ib + 4) & 15u) | ((byte(ib - 4) >> 6) << 4); mn = (byte(ib + 4) >> 4) | ((byte(ib) >> 6) << 4); }
+    const float d1 = fp16_exact(meta.x & 0xffffu) * (float)sc, m1 = fp16_exact(meta.x >> 16) * (float)mn;
+    return (d1 * g.s) * combine(aH, aM, aL) - (m1 * g.s) * combine(sH, sM, sL);
+}
+
 // Q6_K sub-block ib: values 128h+32k+l (h=ib/4, k=ib%4), two 16-value scale segments.
 // Codes are taken unsigned (0..63); the -32 offset enters through the digit
 // sums bias[seg] = -32 * sum(digits of the segment), precomputed per lane.

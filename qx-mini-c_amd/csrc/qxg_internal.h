@@ -20,6 +20,9 @@
 //   IQ2_XS : qs[nb][64] (32 x u16), sc[nb][8], d[nb]
 //   IQ3_XXS: qs[nb][64], aux[nb][32] (8 x u32), d[nb]
 //   Q6_K   : ql[nb][128], qh[nb][64], sc[nb][16] (int8), d[nb]
+//   Q5_K   : qs[nb][128], meta[nb][16] = {d, dmin, scales[12]}, qh[nb][32]
+//   IQ2_S  : qs[nb][64] (32 grid bytes, 32 sign bytes), sc[nb][8], qh[nb][8], d[nb]
+//   IQ3_S  : qs[nb][64], signs[nb][32], {qh[8], scales[4], 0[4]}[nb], d[nb]
 //   Q4_K, F32: the original bytes
 struct QTensor {
     uint32_t type = 0;
@@ -27,8 +30,8 @@ struct QTensor {
     uint64_t nblocks = 0, bytes = 0;
     uint8_t *base = nullptr;      // device allocation
     const uint8_t *p0 = nullptr;  // qs / ql / raw
-    const uint8_t *p1 = nullptr;  // meta / sc / aux / qh
-    const uint8_t *p2 = nullptr;  // Q6_K sc
+    const uint8_t *p1 = nullptr;  // meta / sc / aux / qh / signs
+    const uint8_t *p2 = nullptr;  // Q6_K sc, Q5_K qh, IQ2_S qh, IQ3_S qh+scales
     const uint16_t *d = nullptr;  // fp16 d per block
 };
 
@@ -59,6 +62,9 @@ struct Tables {
     uint2 *g3;     // IQ3_XXS grid: 256 x {pos, neg}
     uint2 *sel;    // sign index (7 bits) -> v_perm selectors for 8 values
     double *rope_cos, *rope_sin;  // [QXG_MAX_CTX][64]
+    uint4 *g2s;    // IQ2_S grid: 1024 x {pos lo, pos hi, neg lo, neg hi}
+    uint2 *g3s;    // IQ3_S grid: 512 x {pos, neg}
+    uint2 *sel8;   // sign byte (8 bits) -> v_perm selectors for 8 values
 };
 
 // Persistent decode kernel (qxk_layers): per-layer weight pointers and launch arguments.

@@ -38,34 +38,36 @@ extern "C" __global__ __launch_bounds__(256) void qxk_embed(const uint8_t *emb, 
     embed_q4k_row(emb + (uint64_t)tokens[st->step] * row_bytes, x);
 }
 
-// attn RMSNorm + Q/K/V IQ4_XS projections (2048 -> 4096 | 512 | 512) into qkv[5120].
-// Wave per RPW consecutive rows; lane = 8*block + sub-block.  Every global load of
-// the wave is issued before the norm/digit prologue so their latencies overlap.
-template <int RPW>
-__global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm_w,
-        const uint8_t *q_qs, const uint8_t *q_meta, const uint8_t *k_qs, const uint8_t *k_meta,
-        const uint8_t *v_qs, const uint8_t *v_meta, float *qkv) {
-    __shared__ uint32_t s_dig[64 * DIG_STRIDE];
-    __shared__ double s_red[4];
-    const int lane = threadIdx.x & 63, wave = wave_id();
+// attn RMSNorm + Q/K/V projections (2048 -> 4096 | 512 | 512) into qkv[5120]; each of
+// the three matrices IQ4_XS or Q5_K (the real checkpoint's attn_v).  Wave per RPW
+// consecutive rows; lane = 8*block + sub-block.  A workgroup's 4*RPW rows lie in one
+// matrix, so its format is uniform.  Every global load of the wave is issued before the
+// norm/digit prologue so their latencies overlap.
+struct QkvW {
+    const uint8_t *qs[3], *p1[3], *p2[3];
+    uint32_t type[3];
+};
+
+template <int RPW, int FMT>
+DEV void qkv_rows(DigIn<2048, true> &din, const uint8_t *qs, const uint8_t *p1, const uint8_t *p2, int lr0, int r0,
+                  uint32_t *s_dig, double *s_red, float *qkv) {
+    const int lane = threadIdx.x & 63;
     const int b = lane >> 3, ib = lane & 7;
-    const int r0 = (blockIdx.x * 4 + wave) * RPW;   // grid covers exactly 5120 rows
-    QXG_MARK(3, 0);
-    DigIn<2048, true> din;
-    digits_load(x, norm_w, din);
-    uint4 qv[RPW];
-    uint2 mv[RPW];
+    uint4 qv[RPW], qw[RPW], ha[RPW], hb[RPW], mv[RPW];
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
-        const int r = r0 + rr;
-        const uint8_t *qs, *meta;
-        int lr;
-        if (r < 4096) { qs = q_qs; meta = q_meta; lr = r; }
-        else if (r < 4608) { qs = k_qs; meta = k_meta; lr = r - 4096; }
-        else { qs = v_qs; meta = v_meta; lr = r - 4608; }
-        const uint64_t blk = (uint64_t)lr * 8 + b;
-        qv[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[ib];
-        mv[rr] = *reinterpret_cast<const uint2 *>(meta + blk * 8);
+        const uint64_t blk = (uint64_t)(lr0 + rr) * 8 + b;
+        if constexpr (FMT == 23) {
+            qv[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[ib];
+            const uint2 m = *reinterpret_cast<const uint2 *>(p1 + blk * 8);
+            mv[rr] = make_uint4(m.x, m.y, 0u, 0u);
+        } else {
+            qv[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[2 * (ib >> 1)];
+            qw[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[2 * (ib >> 1) + 1];
+            ha[rr] = reinterpret_cast<const uint4 *>(p2 + blk * 32)[0];
+            hb[rr] = reinterpret_cast<const uint4 *>(p2 + blk * 32)[1];
+            mv[rr] = *reinterpret_cast<const uint4 *>(p1 + blk * 16);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     QXG_ANCHOR(din.v[0][7]);
@@ -76,7 +78,10 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
     load_dig(s_dig, lane, g);
     float part[RPW];
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) part[rr] = dot_iq4(qv[rr], mv[rr], ib, g);
+    for (int rr = 0; rr < RPW; ++rr) {
+        if constexpr (FMT == 23) part[rr] = dot_iq4(qv[rr], make_uint2(mv[rr].x, mv[rr].y), ib, g);
+        else part[rr] = dot_q5(qv[rr], qw[rr], ha[rr], hb[rr], mv[rr], ib, g);
+    }
     QXG_ANCHOR(part[0]); QXG_ANCHOR(part[RPW - 1]);
     QXG_MARK(3, 3);
     float out[RPW];
@@ -86,6 +91,22 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
     for (int rr = 0; rr < RPW; ++rr) if (lane == rr) mine = out[rr];
     if (lane < RPW) qkv[r0 + lane] = (ok && isfinite(mine)) ? mine : 0.0f;
     QXG_MARK(3, 4);
+}
+
+template <int RPW>
+__global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm_w, QkvW w, float *qkv) {
+    __shared__ uint32_t s_dig[64 * DIG_STRIDE];
+    __shared__ double s_red[4];
+    const int wave = wave_id();
+    const int r0 = (blockIdx.x * 4 + wave) * RPW;   // grid covers exactly 5120 rows
+    const int rb = blockIdx.x * 4 * RPW;             // the workgroup's first row: one matrix
+    const int mi = rb < 4096 ? 0 : rb < 4608 ? 1 : 2;
+    const int lr0 = r0 - (mi == 0 ? 0 : mi == 1 ? 4096 : 4608);
+    QXG_MARK(3, 0);
+    DigIn<2048, true> din;
+    digits_load(x, norm_w, din);
+    if (w.type[mi] == 13) qkv_rows<RPW, 13>(din, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv);
+    else qkv_rows<RPW, 23>(din, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv);
 }
 
 // Attention for one q head, with the per-head q/k RMSNorm (src/qx_format.c:3740-3757),
@@ -214,11 +235,12 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     attn_context(n, s_sc, s_part, vrow, ctx_out + qh * 128);
 }
 
-// O projection IQ4_XS 4096 -> 2048 on ctx, then x[r] += o[r] (src/qx_format.c:6420-6423).
-// Lane handles sub-blocks lane and lane+64 (blocks lane/8 and 8+lane/8).
-template <int RPW>
+// O projection 4096 -> 2048 on ctx (IQ4_XS, or Q5_K in the real checkpoint), then
+// x[r] += o[r] (src/qx_format.c:6420-6423).  Lane handles sub-blocks lane and lane+64
+// (blocks lane/8 and 8+lane/8).
+template <int RPW, int FMT>
 __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_t *qs, const uint8_t *meta,
-                                                  float *x, float *attn_dump) {
+                                                  const uint8_t *p2, float *x, float *attn_dump) {
     __shared__ uint32_t s_dig[128 * DIG_STRIDE];
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int ib = lane & 7, b0 = lane >> 3, b1 = 8 + (lane >> 3);
@@ -227,15 +249,28 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
     DigIn<4096, false> din;
     digits_load(ctxv, nullptr, din);
     const float xr = lane < RPW ? x[r0 + lane] : 0.0f;
-    uint4 q0[RPW], q1[RPW];
-    uint2 m0[RPW], m1[RPW];
+    uint4 q0[RPW], q1[RPW], q0b[RPW], q1b[RPW], h0a[RPW], h0b[RPW], h1a[RPW], h1b[RPW], m0[RPW], m1[RPW];
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
         const uint64_t k0 = (uint64_t)(r0 + rr) * 16 + b0, k1 = (uint64_t)(r0 + rr) * 16 + b1;
-        q0[rr] = reinterpret_cast<const uint4 *>(qs + k0 * 128)[ib];
-        q1[rr] = reinterpret_cast<const uint4 *>(qs + k1 * 128)[ib];
-        m0[rr] = *reinterpret_cast<const uint2 *>(meta + k0 * 8);
-        m1[rr] = *reinterpret_cast<const uint2 *>(meta + k1 * 8);
+        if constexpr (FMT == 23) {
+            q0[rr] = reinterpret_cast<const uint4 *>(qs + k0 * 128)[ib];
+            q1[rr] = reinterpret_cast<const uint4 *>(qs + k1 * 128)[ib];
+            const uint2 a = *reinterpret_cast<const uint2 *>(meta + k0 * 8), c = *reinterpret_cast<const uint2 *>(meta + k1 * 8);
+            m0[rr] = make_uint4(a.x, a.y, 0u, 0u);
+            m1[rr] = make_uint4(c.x, c.y, 0u, 0u);
+        } else {
+            q0[rr] = reinterpret_cast<const uint4 *>(qs + k0 * 128)[2 * (ib >> 1)];
+            q0b[rr] = reinterpret_cast<const uint4 *>(qs + k0 * 128)[2 * (ib >> 1) + 1];
+            q1[rr] = reinterpret_cast<const uint4 *>(qs + k1 * 128)[2 * (ib >> 1)];
+            q1b[rr] = reinterpret_cast<const uint4 *>(qs + k1 * 128)[2 * (ib >> 1) + 1];
+            h0a[rr] = reinterpret_cast<const uint4 *>(p2 + k0 * 32)[0];
+            h0b[rr] = reinterpret_cast<const uint4 *>(p2 + k0 * 32)[1];
+            h1a[rr] = reinterpret_cast<const uint4 *>(p2 + k1 * 32)[0];
+            h1b[rr] = reinterpret_cast<const uint4 *>(p2 + k1 * 32)[1];
+            m0[rr] = *reinterpret_cast<const uint4 *>(meta + k0 * 16);
+            m1[rr] = *reinterpret_cast<const uint4 *>(meta + k1 * 16);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     QXG_ANCHOR(din.v[1][7]);
@@ -247,7 +282,14 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
     load_dig(s_dig, lane + 64, g1);
     float part[RPW];
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) part[rr] = dot_iq4(q0[rr], m0[rr], ib, g0) + dot_iq4(q1[rr], m1[rr], ib, g1);
+    for (int rr = 0; rr < RPW; ++rr) {
+        if constexpr (FMT == 23)
+            part[rr] = dot_iq4(q0[rr], make_uint2(m0[rr].x, m0[rr].y), ib, g0) +
+                       dot_iq4(q1[rr], make_uint2(m1[rr].x, m1[rr].y), ib, g1);
+        else
+            part[rr] = dot_q5(q0[rr], q0b[rr], h0a[rr], h0b[rr], m0[rr], ib, g0) +
+                       dot_q5(q1[rr], q1b[rr], h1a[rr], h1b[rr], m1[rr], ib, g1);
+    }
     QXG_ANCHOR(part[0]); QXG_ANCHOR(part[RPW - 1]);
     QXG_MARK(0, 3);
     float out[RPW];
@@ -285,18 +327,47 @@ extern "C" __global__ __launch_bounds__(256) void qxk_router(const float *x, con
 }
 
 
-// gate/up IQ2_XS (2048 -> 768) for the 8 routed experts (ids from st) + SwiGLU
-// h[r][i] = (float)(silu((double)g) * (double)u) (src/qx_format.c:5298, 2511-2513).
-// Weight loads are issued first; the codebook tables go to LDS while they fly.
-// Units are processed in a rolled loop whose prefetch registers shift by one unit per
-// iteration (static indices keep them in VGPRs).
-template <int UPW>
-__global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *norm_w,
-        const uint8_t *g_qs, const uint8_t *g_sc, const uint16_t *g_d,
-        const uint8_t *u_qs, const uint8_t *u_sc, const uint16_t *u_d, Tables T, const double *logits,
-        uint32_t experts, DevState *st, float *h) {
-    __shared__ uint4 s_g2[512];
-    __shared__ uint2 s_sel[128];
+// gate/up (2048 -> 768; IQ2_XS, or IQ2_S in the real checkpoint) for the 8 routed experts
+// (ids from st) + SwiGLU h[r][i] = (float)(silu((double)g) * (double)u)
+// (src/qx_format.c:5298, 2511-2513).  Weight loads are issued first; the codebook tables
+// go to LDS while they fly.  Units are processed in a rolled loop whose prefetch
+// registers shift by one unit per iteration (static indices keep them in VGPRs).
+// A unit's words: IQ2_XS {qs lo, qs hi, scale byte, d}; IQ2_S {grid bytes, sign bytes,
+// qh | scale << 8, d}.
+struct GuW {
+    const uint8_t *qs, *p1, *p2;
+    const uint16_t *d;
+};
+
+typedef uint32_t gu4 __attribute__((ext_vector_type(4)));   // register-promoted (a uint4 array is not)
+
+template <int FMT>
+DEV gu4 gu_load(const GuW &w, uint64_t blk, int ib) {
+    gu4 r;
+    if constexpr (FMT == 17) {
+        const uint2 q = reinterpret_cast<const uint2 *>(w.qs + blk * 64)[ib];
+        r.x = q.x; r.y = q.y; r.z = w.p1[blk * 8 + ib]; r.w = w.d[blk];
+    } else {
+        r.x = reinterpret_cast<const uint32_t *>(w.qs + blk * 64)[ib];
+        r.y = reinterpret_cast<const uint32_t *>(w.qs + blk * 64)[8 + ib];
+        r.z = (uint32_t)w.p2[blk * 8 + ib] | ((uint32_t)w.p1[blk * 8 + ib] << 8);
+        r.w = w.d[blk];
+    }
+    return r;
+}
+
+template <int FMT>
+DEV float gu_dot(gu4 u, const Dig &g, const uint4 *G, const uint2 *SEL) {
+    if constexpr (FMT == 17) return dot_iq2(make_uint2(u.x, u.y), u.z, u.w, g, G, SEL);
+    else return dot_iq2s(u.x, u.y, u.z & 255u, u.z >> 8, u.w, g, G, SEL);
+}
+
+template <int UPW, int FMT>
+__global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *norm_w, GuW gw, GuW uw, Tables T,
+        const double *logits, uint32_t experts, DevState *st, float *h) {
+    constexpr int NG = FMT == 17 ? 512 : 1024, NS = FMT == 17 ? 128 : 256;
+    __shared__ uint4 s_g2[NG];
+    __shared__ uint2 s_sel[NS];
     __shared__ uint32_t s_dig[64 * DIG_STRIDE];
     __shared__ double s_red[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -308,8 +379,15 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     const double l0 = lane < E ? logits[lane] : 0.0, l1 = lane + 64 < E ? logits[lane + 64] : 0.0;
     DigIn<2048, true> din;
     digits_load(x, norm_w, din);
-    const uint4 t0 = T.g2[tid], t1 = T.g2[tid + 256];
-    const uint2 t2 = T.sel[tid & 127];
+    const uint4 *G = FMT == 17 ? T.g2 : T.g2s;
+    const uint2 *SL = FMT == 17 ? T.sel : T.sel8;
+    gu4 tg[NG / 256];
+#pragma unroll
+    for (int i = 0; i < NG / 256; ++i) {
+        const uint4 t = G[tid + 256 * i];
+        tg[i].x = t.x; tg[i].y = t.y; tg[i].z = t.z; tg[i].w = t.w;
+    }
+    const uint2 t2 = SL[tid & (NS - 1)];
     QXG_ANCHOR(l1);
     QXG_MARK(1, 5);
     uint32_t ids[QXG_TOPK];
@@ -327,24 +405,19 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
 #pragma unroll
     for (int q = 1; q < QXG_TOPK; ++q) if (u0 / QXG_FFN == q) e = ids[q];   // 4 | 768: one expert per wave
     e = __builtin_amdgcn_readfirstlane(e);
-    uint2 gq[UPW], uq[UPW];
-    uint32_t gs[UPW], us[UPW], gd[UPW], ud[UPW];
+    gu4 gq[UPW], uq[UPW];
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu) {
         const int i = (u0 + uu) % QXG_FFN;
         const uint64_t blk = ((uint64_t)e * QXG_FFN + i) * 8 + b;
-        gq[uu] = reinterpret_cast<const uint2 *>(g_qs + blk * 64)[ib];
-        uq[uu] = reinterpret_cast<const uint2 *>(u_qs + blk * 64)[ib];
-        gs[uu] = g_sc[blk * 8 + ib];
-        us[uu] = u_sc[blk * 8 + ib];
-        gd[uu] = g_d[blk];
-        ud[uu] = u_d[blk];
+        gq[uu] = gu_load<FMT>(gw, blk, ib);
+        uq[uu] = gu_load<FMT>(uw, blk, ib);
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     QXG_MARK(1, 7);
-    s_g2[tid] = t0;
-    s_g2[tid + 256] = t1;
-    if (tid < 128) s_sel[tid] = t2;
+#pragma unroll
+    for (int i = 0; i < NG / 256; ++i) s_g2[tid + 256 * i] = make_uint4(tg[i].x, tg[i].y, tg[i].z, tg[i].w);
+    if (tid < NS) s_sel[tid] = t2;
     QXG_ANCHOR(din.v[0][7]);
     QXG_MARK(1, 1);
     const bool ok = block_digits(din, s_dig, s_red);   // ends with a barrier
@@ -356,11 +429,11 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     float pg[UPW], pu[UPW];
 #pragma unroll 1
     for (int uu = 0; uu < UPW; ++uu) {
-        const float a = dot_iq2(gq[0], gs[0], gd[0], g, s_g2, s_sel);
-        const float c = dot_iq2(uq[0], us[0], ud[0], g, s_g2, s_sel);
+        const float a = gu_dot<FMT>(gq[0], g, s_g2, s_sel);
+        const float c = gu_dot<FMT>(uq[0], g, s_g2, s_sel);
 #pragma unroll
         for (int k = 0; k + 1 < UPW; ++k) {
-            gq[k] = gq[k + 1]; uq[k] = uq[k + 1]; gs[k] = gs[k + 1]; us[k] = us[k + 1]; gd[k] = gd[k + 1]; ud[k] = ud[k + 1];
+            gq[k] = gq[k + 1]; uq[k] = uq[k + 1];
             pg[k] = pg[k + 1]; pu[k] = pu[k + 1];
         }
         pg[UPW - 1] = a;
@@ -384,14 +457,46 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     QXG_MARK(1, 4);
 }
 
-// down IQ3_XXS (768 -> 2048) for the 8 experts, rank-ordered weighted f32 sum and
-// residual: x[i] = x[i] + sum_r (float)(w_r * (double)y_r[i]) (src/qx_format.c:5296-5309).
-// Wave per output row; lanes 8r..8r+7 hold rank r, lane 8r+k the sub-blocks k of blocks 0..2.
-template <int RPW>
-__global__ __launch_bounds__(256) void qxk_down(const float *h, const uint8_t *d_qs, const uint8_t *d_aux,
-        const uint16_t *d_d, Tables T, const DevState *st, float *x, float *moe_dump) {
-    __shared__ uint2 s_g3[256];
-    __shared__ uint2 s_sel[128];
+// down (768 -> 2048; IQ3_XXS, or IQ4_XS / IQ3_S in the real checkpoint) for the 8 experts,
+// rank-ordered weighted f32 sum and residual: x[i] = x[i] + sum_r (float)(w_r *
+// (double)y_r[i]) (src/qx_format.c:5296-5309).  Wave per output row; lanes 8r..8r+7 hold
+// rank r, lane 8r+k the sub-blocks k of blocks 0..2.  A sub-block's words: IQ3_XXS
+// {qs lo, qs hi, aux, d}; IQ3_S {qs lo, qs hi, sign bytes, qh | scale << 8 | d << 16};
+// IQ4_XS {qs (16 bytes)} + {meta (8 bytes)}.
+struct DnW {
+    const uint8_t *qs, *p1, *p2;
+    const uint16_t *d;
+};
+
+template <int FMT>
+DEV void dn_load(const DnW &w, uint64_t blk, int k, uint4 &a, uint2 &m) {
+    if constexpr (FMT == 18) {
+        const uint2 q = reinterpret_cast<const uint2 *>(w.qs + blk * 64)[k];
+        a = make_uint4(q.x, q.y, reinterpret_cast<const uint32_t *>(w.p1 + blk * 32)[k], w.d[blk]);
+    } else if constexpr (FMT == 21) {
+        const uint2 q = reinterpret_cast<const uint2 *>(w.qs + blk * 64)[k];
+        const uint32_t sg = reinterpret_cast<const uint32_t *>(w.p1 + blk * 32)[k];
+        const uint32_t qh = w.p2[blk * 16 + k], sc = (w.p2[blk * 16 + 8 + (k >> 1)] >> (4 * (k & 1))) & 15u;
+        a = make_uint4(q.x, q.y, sg, qh | (sc << 8) | ((uint32_t)w.d[blk] << 16));
+    } else {
+        a = reinterpret_cast<const uint4 *>(w.qs + blk * 128)[k];
+        m = *reinterpret_cast<const uint2 *>(w.p1 + blk * 8);
+    }
+}
+
+template <int FMT>
+DEV float dn_dot(uint4 a, uint2 m, int k, const Dig &g, const uint2 *G, const uint2 *SEL) {
+    if constexpr (FMT == 18) return dot_iq3(make_uint2(a.x, a.y), a.z, a.w, g, G, SEL);
+    else if constexpr (FMT == 21) return dot_iq3s(make_uint2(a.x, a.y), a.z, a.w & 255u, (a.w >> 8) & 255u, a.w >> 16, g, G, SEL);
+    else return dot_iq4(a, m, k, g);
+}
+
+template <int RPW, int FMT>
+__global__ __launch_bounds__(256) void qxk_down(const float *h, DnW w, Tables T, const DevState *st, float *x,
+                                                 float *moe_dump) {
+    constexpr int NG = FMT == 21 ? 512 : 256, NS = FMT == 21 ? 256 : 128;
+    __shared__ uint2 s_g3[NG];
+    __shared__ uint2 s_sel[NS];
     __shared__ uint32_t s_dig[192 * DIG_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int r = lane >> 3, k = lane & 7;
@@ -406,21 +511,26 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, const uint8_t *d
     float xr[RPW];
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) xr[rr] = x[r0 + rr];
-    const uint2 t0 = T.g3[tid], t1 = T.sel[tid & 127];
-    uint2 qv[RPW][3];
-    uint32_t aux[RPW][3], dd[RPW][3];
+    const uint2 *G = FMT == 21 ? T.g3s : T.g3;
+    const uint2 *SL = FMT == 21 ? T.sel8 : T.sel;
+    uint2 tg[NG / 256];
+    if constexpr (FMT != 23) {
+#pragma unroll
+        for (int i = 0; i < NG / 256; ++i) tg[i] = G[tid + 256 * i];
+    }
+    const uint2 t1 = FMT != 23 ? SL[tid & (NS - 1)] : make_uint2(0u, 0u);
+    uint4 qa[RPW][3];
+    uint2 qm[RPW][3];
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr)
 #pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const uint64_t blk = ((uint64_t)e * 2048 + r0 + rr) * 3 + j;
-            qv[rr][j] = reinterpret_cast<const uint2 *>(d_qs + blk * 64)[k];
-            aux[rr][j] = reinterpret_cast<const uint32_t *>(d_aux + blk * 32)[k];
-            dd[rr][j] = d_d[blk];
-        }
+        for (int j = 0; j < 3; ++j) dn_load<FMT>(w, ((uint64_t)e * 2048 + r0 + rr) * 3 + j, k, qa[rr][j], qm[rr][j]);
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
-    s_g3[tid] = t0;
-    if (tid < 128) s_sel[tid] = t1;
+    if constexpr (FMT != 23) {
+#pragma unroll
+        for (int i = 0; i < NG / 256; ++i) s_g3[tid + 256 * i] = tg[i];
+        if (tid < NS) s_sel[tid] = t1;
+    }
     QXG_ANCHOR(din.v[din.PER - 1][7]);
     QXG_MARK(2, 1);
     const bool ok = block_digits(din, s_dig, nullptr);   // ends with a barrier
@@ -432,7 +542,7 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, const uint8_t *d
     for (int rr = 0; rr < RPW; ++rr) {
         float part = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 3; ++j) part += dot_iq3(qv[rr][j], aux[rr][j], dd[rr][j], g[j], s_g3, s_sel);
+        for (int j = 0; j < 3; ++j) part += dn_dot<FMT>(qa[rr][j], qm[rr][j], k, g[j], s_g3, s_sel);
         part += dppf<DPP_XOR1>(part);
         part += dppf<DPP_XOR2>(part);
         part += dppf<DPP_HALF_MIRROR>(part);   // lanes 8q..8q+7 now hold expert rank q's row
@@ -645,6 +755,37 @@ extern "C" __global__ __launch_bounds__(256) void qxk_dequant(uint32_t type, con
         const float d1 = fp16_exact(b[0] | (b[1] << 8)) * (float)s, m1 = fp16_exact(b[2] | (b[3] << 8)) * (float)m;
         const uint8_t q = b[16 + 32 * j + l];
         y = d1 * (float)(hi ? (q >> 4) : (q & 15)) - m1;
+    } else if (type == 13) {
+        const uint8_t *meta = p1 + blk * 16, *sc = meta + 4;
+        const int j = i >> 6, hi = (i >> 5) & 1, l = i & 31;
+        const int is = 2 * j + hi;
+        uint32_t s, m;
+        if (is < 4) { s = sc[is] & 63u; m = sc[is + 4] & 63u; }
+        else { s = (sc[is + 4] & 15u) | ((uint32_t)(sc[is - 4] >> 6) << 4); m = (sc[is + 4] >> 4) | ((uint32_t)(sc[is] >> 6) << 4); }
+        const float d1 = fp16_exact(meta[0] | (meta[1] << 8)) * (float)s, m1 = fp16_exact(meta[2] | (meta[3] << 8)) * (float)m;
+        const uint8_t q = p0[blk * 128 + 32 * j + l];
+        const uint32_t code = (hi ? (q >> 4) : (q & 15u)) | (((uint32_t)(p2[blk * 32 + l] >> is) & 1u) << 4);
+        y = d1 * (float)code - m1;
+    } else if (type == 22) {
+        const int ib = i >> 5, l = (i >> 3) & 3, j = i & 7;
+        const uint8_t s = p1[blk * 8 + ib];
+        const float d = fp16_exact(dd[blk]);
+        const float db = l < 2 ? (d * (0.5f + (float)(s & 15))) * 0.25f : (d * (0.5f + (float)(s >> 4))) * 0.25f;
+        const uint32_t idx = (uint32_t)p0[blk * 64 + 4 * ib + l] | (((uint32_t)p2[blk * 8 + ib] << (8 - 2 * l)) & 0x300u);
+        const uint4 gg = T.g2s[idx];
+        const uint32_t gb = ((j < 4 ? gg.x : gg.y) >> (8 * (j & 3))) & 255u;
+        const uint32_t sgn = p0[blk * 64 + 32 + 4 * ib + l];
+        y = (db * (float)gb) * (((sgn >> j) & 1) ? -1.0f : 1.0f);
+    } else if (type == 21) {
+        const int ib = i >> 5, l = (i >> 3) & 3, j = i & 7;
+        const uint8_t *ex = p2 + blk * 16;   // qh[8], scales[4]
+        const uint32_t qh = ex[ib], sc = (ex[8 + ib / 2] >> (4 * (ib & 1))) & 15u;
+        const float db = fp16_exact(dd[blk]) * (1.0f + 2.0f * (float)sc);
+        const uint32_t gi = (j < 4) ? ((uint32_t)p0[blk * 64 + 8 * ib + 2 * l] | ((qh << (8 - 2 * l)) & 256u))
+                                    : ((uint32_t)p0[blk * 64 + 8 * ib + 2 * l + 1] | ((qh << (7 - 2 * l)) & 256u));
+        const uint32_t gb = (T.g3s[gi].x >> (8 * (j & 3))) & 255u;
+        const uint32_t sgn = p1[blk * 32 + 4 * ib + l];
+        y = (db * (float)gb) * (((sgn >> j) & 1) ? -1.0f : 1.0f);
     }
     out[blk * 256 + i] = y;
 }
@@ -674,28 +815,62 @@ extern "C" __global__ __launch_bounds__(256) void qxk_repack(uint32_t type, cons
         for (int i = 0; i < 64; ++i) p1[blk * 64 + i] = b[128 + i];
         for (int i = 0; i < 16; ++i) p2[blk * 16 + i] = b[192 + i];
         dd[blk] = (uint16_t)(b[208] | (b[209] << 8));
+    } else if (type == 13) {
+        const uint8_t *b = raw + blk * 176;
+        for (int i = 0; i < 16; ++i) p1[blk * 16 + i] = b[i];
+        for (int i = 0; i < 32; ++i) p2[blk * 32 + i] = b[16 + i];
+        for (int i = 0; i < 128; ++i) p0[blk * 128 + i] = b[48 + i];
+    } else if (type == 22) {
+        const uint8_t *b = raw + blk * 82;
+        dd[blk] = (uint16_t)(b[0] | (b[1] << 8));
+        for (int i = 0; i < 64; ++i) p0[blk * 64 + i] = b[2 + i];
+        for (int i = 0; i < 8; ++i) p2[blk * 8 + i] = b[66 + i];
+        for (int i = 0; i < 8; ++i) p1[blk * 8 + i] = b[74 + i];
+    } else if (type == 21) {
+        const uint8_t *b = raw + blk * 110;
+        dd[blk] = (uint16_t)(b[0] | (b[1] << 8));
+        for (int i = 0; i < 64; ++i) p0[blk * 64 + i] = b[2 + i];
+        for (int i = 0; i < 8; ++i) p2[blk * 16 + i] = b[66 + i];
+        for (int i = 0; i < 32; ++i) p1[blk * 32 + i] = b[74 + i];
+        for (int i = 0; i < 4; ++i) p2[blk * 16 + 8 + i] = b[106 + i];
+        for (int i = 0; i < 4; ++i) p2[blk * 16 + 12 + i] = 0;
     }
 }
 
 // ----------------------------------------------------------------- launch wrappers
 extern "C" {
+// Each wrapper picks the kernel instantiation of the tensor's format (validated at bind).
 void qxl_qkv(hipStream_t s, const float *x, const float *nw, const QTensor *q, const QTensor *k, const QTensor *v, float *qkv, Timer t) {
     constexpr int RPW = 4;
-    qx_launch(qxk_qkv<RPW>, dim3(5120 / (4 * RPW)), dim3(256), 0, s, t, x, nw, q->p0, q->p1, k->p0, k->p1, v->p0, v->p1, qkv);
+    QkvW w;
+    const QTensor *m[3] = {q, k, v};
+    for (int i = 0; i < 3; ++i) { w.qs[i] = m[i]->p0; w.p1[i] = m[i]->p1; w.p2[i] = m[i]->p2; w.type[i] = m[i]->type; }
+    qx_launch(qxk_qkv<RPW>, dim3(5120 / (4 * RPW)), dim3(256), 0, s, t, x, nw, w, qkv);
 }
 void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, float *dump, Timer t) {
     constexpr int RPW = 2;
-    qx_launch(qxk_oproj<RPW>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, t, ctxv, o->p0, o->p1, x, dump);
+    if (o->type == 13)
+        qx_launch(qxk_oproj<RPW, 13>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, t, ctxv, o->p0, o->p1, o->p2, x, dump);
+    else
+        qx_launch(qxk_oproj<RPW, 23>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, t, ctxv, o->p0, o->p1, o->p2, x, dump);
 }
 void qxl_gate_up(hipStream_t s, const float *x, const float *nw, const QTensor *g, const QTensor *u, Tables T,
                  const double *logits, uint32_t experts, DevState *st, float *h, Timer t) {
     constexpr int UPW = 4;
-    qx_launch(qxk_gate_up<UPW>, dim3(QXG_TOPK * QXG_FFN / (4 * UPW)), dim3(256), 0, s, t, x, nw,
-                       g->p0, g->p1, g->d, u->p0, u->p1, u->d, T, logits, experts, st, h);
+    const GuW gw{g->p0, g->p1, g->p2, g->d}, uw{u->p0, u->p1, u->p2, u->d};
+    const dim3 grid(QXG_TOPK * QXG_FFN / (4 * UPW));
+    if (g->type == 22)
+        qx_launch(qxk_gate_up<UPW, 22>, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h);
+    else
+        qx_launch(qxk_gate_up<UPW, 17>, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h);
 }
 void qxl_down(hipStream_t s, const float *h, const QTensor *d, Tables T, const DevState *st, float *x, float *dump, Timer t) {
     constexpr int RPW = 2;
-    qx_launch(qxk_down<RPW>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, t, h, d->p0, d->p1, d->d, T, st, x, dump);
+    const DnW w{d->p0, d->p1, d->p2, d->d};
+    const dim3 grid(2048 / (4 * RPW));
+    if (d->type == 23) qx_launch(qxk_down<RPW, 23>, grid, dim3(256), 0, s, t, h, w, T, st, x, dump);
+    else if (d->type == 21) qx_launch(qxk_down<RPW, 21>, grid, dim3(256), 0, s, t, h, w, T, st, x, dump);
+    else qx_launch(qxk_down<RPW, 18>, grid, dim3(256), 0, s, t, h, w, T, st, x, dump);
 }
 void qxl_head(hipStream_t s, const float *x, const float *nw, const QTensor *w, uint32_t vocab, DevState *st,
               float *logits, float *norm_dump, uint32_t *dig, Timer t) {

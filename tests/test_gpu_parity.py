@@ -9,8 +9,8 @@ from helpers import REL_L2, rel_l2, seeded_kv, seeded_normal, topk_consistent
 
 pytestmark = pytest.mark.gpu
 
-BLOCK_BYTES = {12: 144, 14: 210, 17: 74, 18: 98, 23: 136}
-D_OFFSET = {12: 0, 14: 208, 17: 0, 18: 0, 23: 0}
+BLOCK_BYTES = {12: 144, 13: 176, 14: 210, 17: 74, 18: 98, 21: 110, 22: 82, 23: 136}
+D_OFFSET = {12: 0, 13: 0, 14: 208, 17: 0, 18: 0, 21: 0, 22: 0, 23: 0}
 
 
 @pytest.fixture(scope="module", params=[0, 1], ids=["per_phase", "persistent"])
@@ -23,7 +23,7 @@ def ctx(request):
     c.close()
 
 
-@pytest.mark.parametrize("ggml_type", [12, 14, 17, 18, 23])
+@pytest.mark.parametrize("ggml_type", [12, 13, 14, 17, 18, 21, 22, 23])
 def test_dequant_bit_exact(ctx, ggml_type):
     """Random blocks plus every fp16 value of d (including exponent 31 -> 65504)."""
     bb = BLOCK_BYTES[ggml_type]
