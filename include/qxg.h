@@ -35,14 +35,18 @@ void qxg_close(qxg_ctx *ctx);
 /* Uploads one tensor of the QXF1 file (bytes = the tensor's mmap span) and repacks
  * quantized blocks on the device.  Replaces the per-call weight reads
  * qx_read_raw_span / qx_acquire_span (src/qx_format.c:1757-1773, 858-893).
- * ggml_type: 0 F32, 12 Q4_K, 14 Q6_K, 17 IQ2_XS, 18 IQ3_XXS, 23 IQ4_XS. */
+ * ggml_type: 0 F32, 12 Q4_K, 13 Q5_K, 14 Q6_K, 17 IQ2_XS, 18 IQ3_XXS, 21 IQ3_S,
+ * 22 IQ2_S, 23 IQ4_XS. */
 int qxg_upload_tensor(qxg_ctx *ctx, const char *name, uint32_t ggml_type, const uint64_t dims[4],
                       const void *host_bytes, uint64_t nbytes, char *err, uint64_t err_len);
 
 /* Resolves the uploaded tensors into layers [0, layers), checks every shape and
  * type (the checks of src/qx_format.c:5216-5235, 3610-3629), and sizes work
  * buffers.  need_head / need_embedding select whether output.* / token_embd.* must
- * be present. */
+ * be present.  Per layer: attn_q/k/v/output IQ4_XS or Q5_K; gate/up experts IQ2_XS
+ * or IQ2_S (both the same); down experts IQ3_XXS, IQ4_XS or IQ3_S.  A model using any
+ * format beyond IQ4_XS / IQ2_XS / IQ3_XXS decodes one kernel per phase and cannot
+ * use qxg_prefill / qxg_prefill_layer. */
 int qxg_bind_model(qxg_ctx *ctx, uint32_t layers, int need_embedding, int need_head, char *err, uint64_t err_len);
 
 /* Persistent INT8 KV cache [layers][ctx_tokens][512] for K and V plus one f32 scale
@@ -159,7 +163,8 @@ int qxg_prefill_layer(qxg_ctx *ctx, uint32_t layer, uint32_t n, uint32_t positio
  * runs one thread on the CPU).  0: one kernel per phase, six per layer; 1: one
  * persistent kernel for all layers of the token, one workgroup per CU, phases handed
  * over through epoch-tagged device words.  Both give the same results to the stated
- * tolerance; the default is 0.  Drops the recorded decode graph. */
+ * tolerance; the default is 0.  Drops the recorded decode graph.  A model bound with
+ * formats beyond IQ4_XS / IQ2_XS / IQ3_XXS keeps path 0 whatever is set here. */
 int qxg_set_layer_path(qxg_ctx *ctx, int persistent);
 
 /* ---- measurement (no reference counterpart: the reference times with clock(),
