@@ -223,6 +223,7 @@ struct qxo_model {
     uint32_t ntensors;
     const uint8_t *dir;
     uint32_t vocab, layers;
+    int q8;   /* activation mode: 0 f32, 1 q8_k_compat */
 };
 
 qxo_model *qxo_open(const char *path) {
@@ -340,6 +341,203 @@ void qxo_matvec(uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims, c
     }
 }
 
+/* ---- q8_k_compat activation mode (:3869-4205) ----
+ * Activations become Q8_K blocks (ggml's block_q8_K layout: f32 d, 256 int8, 16 int16
+ * sums); each weight type has an integer dot against them with float scaling per
+ * block, in the reference's float op order. */
+
+/* :3884-3889 — round half to even through the 1.5*2^23 bias (exact for |v| < 2^22) */
+static int32_t q8_round(float v) {
+    const float b = v + 12582912.0f;
+    uint32_t u;
+    memcpy(&u, &b, 4);
+    return (int32_t)(u & 0x7fffffu) - 0x400000;
+}
+
+/* :3891-3927 — per 256 values: the value of largest magnitude (first on ties) maps
+ * to -127; d = 1/(-127/max); codes clamp to [-128, 127]; 16 sums of 16 codes.
+ * Returns 0 for a length that is not a multiple of 256 or a non-finite value. */
+int qxo_quantize_q8k(const float *x, uint32_t n, qxo_q8k *out) {
+    if (!n || n % 256u) return 0;
+    for (uint32_t b = 0; b < n / 256u; ++b) {
+        const float *v = x + 256ull * b;
+        float amax = 0.0f, vmax = 0.0f;
+        for (int i = 0; i < 256; ++i) {
+            if (!isfinite(v[i])) return 0;
+            if (fabsf(v[i]) > amax) { amax = fabsf(v[i]); vmax = v[i]; }
+        }
+        const float inv = vmax == 0.0f ? 0.0f : -127.0f / vmax;
+        out[b].d = inv == 0.0f ? 0.0f : 1.0f / inv;
+        for (int g = 0; g < 16; ++g) {
+            int32_t sum = 0;
+            for (int i = 16 * g; i < 16 * g + 16; ++i) {
+                int32_t q = inv == 0.0f ? 0 : q8_round(inv * v[i]);
+                q = q > 127 ? 127 : q < -128 ? -128 : q;
+                out[b].qs[i] = (int8_t)q;
+                sum += q;
+            }
+            out[b].bsums[g] = (int16_t)sum;
+        }
+    }
+    return 1;
+}
+
+/* signed integer codes of the 32 values of sub-block ib (grid byte times sign) for the
+ * codebook types; the block scales are applied by the callers */
+static void iq_codes32(uint32_t t, const uint8_t *b, int ib, int32_t c[32]) {
+    for (int l = 0; l < 4; ++l) {
+        uint32_t idx[2] = {0, 0};
+        uint8_t sg = 0;
+        int per = 8;
+        if (t == 17) {
+            const uint16_t q = rd16(b + 2 + 2 * (4 * ib + l));
+            idx[0] = q & 511u; sg = ksign(q >> 9);
+        } else if (t == 22) {
+            idx[0] = (uint32_t)b[2 + 4 * ib + l] | (((uint32_t)b[66 + ib] << (8 - 2 * l)) & 0x300u);
+            sg = b[34 + 4 * ib + l];
+        } else if (t == 18) {
+            idx[0] = b[2 + 8 * ib + 2 * l]; idx[1] = b[2 + 8 * ib + 2 * l + 1];
+            sg = ksign((rd32(b + 66 + 4 * ib) >> (7 * l)) & 127u); per = 4;
+        } else {   /* 21 */
+            const uint32_t qh = b[66 + ib];
+            idx[0] = (uint32_t)b[2 + 8 * ib + 2 * l] | ((qh << (8 - 2 * l)) & 256u);
+            idx[1] = (uint32_t)b[2 + 8 * ib + 2 * l + 1] | ((qh << (7 - 2 * l)) & 256u);
+            sg = b[74 + 4 * ib + l]; per = 4;
+        }
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t id = idx[j / per];
+            const int jj = j % per;
+            const int g = t == 17 ? iq2_grid_byte(id, jj) : t == 22 ? iq2s_grid_byte(id, jj)
+                        : t == 18 ? iq3_grid_byte(id, jj) : iq3s_grid_byte(id, jj);
+            c[8 * l + j] = (sg >> j) & 1 ? -g : g;
+        }
+    }
+}
+
+/* one row of nb blocks against nb Q8_K blocks:
+ * IQ4_XS :3929-3952, Q5_K :3954-3986, Q6_K :3988-4021, IQ2_XS :4066-4099,
+ * IQ2_S :4101-4133, IQ3_XXS :4135-4166, IQ3_S :4168-4205 */
+static float dot_q8k(uint32_t t, const uint8_t *row, const qxo_q8k *a, uint32_t nb) {
+    const uint64_t bb = block_bytes(t);
+    if (t == 23) {
+        float total = 0.0f;
+        for (uint32_t k = 0; k < nb; ++k) {
+            const uint8_t *b = row + k * bb;
+            const float d = qxo_fp16_to_f32(rd16(b)) * a[k].d;
+            const uint16_t sh = rd16(b + 2);
+            for (int ib = 0; ib < 8; ++ib) {
+                const int ls = ((b[4 + ib / 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
+                int32_t dot = 0;
+                for (int j = 0; j < 16; ++j) {
+                    const uint8_t q = b[8 + 16 * ib + j];
+                    dot += (int32_t)a[k].qs[32 * ib + j] * qx_iq4nl_values[q & 15];
+                    dot += (int32_t)a[k].qs[32 * ib + 16 + j] * qx_iq4nl_values[q >> 4];
+                }
+                total += d * (float)(ls - 32) * (float)dot;
+            }
+        }
+        return total;
+    }
+    if (t == 13) {
+        float lanes[8] = {0}, sumf = 0.0f;
+        for (uint32_t k = 0; k < nb; ++k) {
+            const uint8_t *b = row + k * bb;
+            const float d = qxo_fp16_to_f32(rd16(b)), dmin = qxo_fp16_to_f32(rd16(b + 2));
+            int32_t li[8] = {0}, msum = 0;
+            for (int g = 0; g < 8; ++g) {
+                uint8_t sc, mn;
+                scale_min_k4(g, b + 4, &sc, &mn);
+                msum += ((int32_t)a[k].bsums[2 * g] + a[k].bsums[2 * g + 1]) * (int32_t)mn;
+                for (int i = 0; i < 32; ++i) {
+                    const uint8_t q = b[48 + 32 * (g / 2) + i];
+                    const int32_t code = (g & 1 ? q >> 4 : q & 15) + (b[16 + i] >> g & 1 ? 16 : 0);
+                    li[i & 7] += (int32_t)sc * code * a[k].qs[32 * g + i];
+                }
+            }
+            const float sd = d * a[k].d;
+            for (int l = 0; l < 8; ++l) lanes[l] += sd * (float)li[l];
+            sumf -= dmin * a[k].d * (float)msum;
+        }
+        for (int l = 0; l < 8; ++l) sumf += lanes[l];
+        return sumf;
+    }
+    if (t == 14) {
+        float lanes[8] = {0};
+        for (uint32_t k = 0; k < nb; ++k) {
+            const uint8_t *b = row + k * bb;
+            int32_t code[256];
+            for (int h = 0; h < 2; ++h) {
+                const uint8_t *ql = b + 64 * h, *qh = b + 128 + 32 * h;
+                for (int i = 0; i < 32; ++i) {
+                    code[128 * h + i] = ((ql[i] & 15) | ((qh[i] & 3) << 4)) - 32;
+                    code[128 * h + i + 32] = ((ql[i + 32] & 15) | (((qh[i] >> 2) & 3) << 4)) - 32;
+                    code[128 * h + i + 64] = ((ql[i] >> 4) | (((qh[i] >> 4) & 3) << 4)) - 32;
+                    code[128 * h + i + 96] = ((ql[i + 32] >> 4) | (((qh[i] >> 6) & 3) << 4)) - 32;
+                }
+            }
+            int32_t li[8] = {0};
+            for (int i = 0; i < 256; ++i) li[i & 7] += (int32_t)(int8_t)b[192 + i / 16] * a[k].qs[i] * code[i];
+            const float d = qxo_fp16_to_f32(rd16(b + 208)) * a[k].d;
+            for (int l = 0; l < 8; ++l) lanes[l] += d * (float)li[l];
+        }
+        float total = 0.0f;
+        for (int l = 0; l < 8; ++l) total += lanes[l];
+        return total;
+    }
+    /* codebook types: integer block sum, one float term per block */
+    float sumf = 0.0f;
+    for (uint32_t k = 0; k < nb; ++k) {
+        const uint8_t *b = row + k * bb;
+        int32_t bsum = 0;
+        for (int ib = 0; ib < 8; ++ib) {
+            int32_t c[32], s0 = 0, s1 = 0;
+            iq_codes32(t, b, ib, c);
+            for (int i = 0; i < 16; ++i) s0 += c[i] * a[k].qs[32 * ib + i];
+            for (int i = 16; i < 32; ++i) s1 += c[i] * a[k].qs[32 * ib + i];
+            if (t == 17 || t == 22) {
+                const uint8_t sc = t == 17 ? b[66 + ib] : b[74 + ib];
+                bsum += s0 * (2 * (sc & 15) + 1) + s1 * (2 * (sc >> 4) + 1);
+            } else if (t == 18) {
+                bsum += (s0 + s1) * (int32_t)(2u * (rd32(b + 66 + 4 * ib) >> 28) + 1u);
+            } else {
+                bsum += (s0 + s1) * (2 * ((b[106 + ib / 2] >> (4 * (ib & 1))) & 15) + 1);
+            }
+        }
+        sumf += qxo_fp16_to_f32(rd16(b)) * a[k].d * (float)bsum;
+    }
+    return t == 17 || t == 22 ? 0.125f * sumf : t == 18 ? 0.25f * sumf : sumf;
+}
+
+/* Q8_K matvec: the activation is quantized once (0 on a non-finite value, :3906).
+ * Projections (:4257-4262) store a non-finite row as 0; expert rows (:4771) fail. */
+static int matvec_q8k(uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims, const float *x, float *y,
+                      int expert) {
+    qxo_q8k a[16];
+    const uint32_t nb = in_dims / 256u;
+    if (nb > 16 || !qxo_quantize_q8k(x, in_dims, a)) return 0;
+    const uint64_t rb = nb * block_bytes(t);
+    for (uint32_t r = 0; r < rows; ++r) {
+        const float v = dot_q8k(t, w + r * rb, a, nb);
+        if (!isfinite(v) && expert) return 0;
+        y[r] = isfinite(v) ? v : 0.0f;
+    }
+    return 1;
+}
+
+void qxo_set_activation(qxo_model *m, int q8_k_compat) { m->q8 = q8_k_compat != 0; }
+
+int qxo_matvec_q8k(uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims, const float *x, float *y, int expert) {
+    return block_bytes(t) ? matvec_q8k(t, w, rows, in_dims, x, y, expert) : 0;
+}
+
+/* attention projections: Q8_K for Q5_K / Q6_K / IQ4_XS in q8_k_compat mode (:4217-4218) */
+static int project(const qxo_model *m, uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims,
+                   const float *x, float *y) {
+    if (m->q8 && (t == 13 || t == 14 || t == 23)) return matvec_q8k(t, w, rows, in_dims, x, y, 0);
+    qxo_matvec(t, w, rows, in_dims, x, y);
+    return 1;
+}
+
 typedef struct { uint32_t token; double logit; } topent;
 
 static void top_insert(topent *top, uint32_t n, uint32_t token, double logit) {
@@ -370,12 +568,18 @@ int qxo_final_head(qxo_model *m, const float *residual, float *norm_out, float *
     for (uint32_t i = 0; i < top_n; ++i) { top[i].token = 0; top[i].logit = -1.0e300; }
     const uint32_t vocab = (uint32_t)dims[1];
     float vals[256];
+    qxo_q8k a[8];
+    if (m->q8 && !qxo_quantize_q8k(xn, 2048, a)) return 0;   /* :3666, 4026-4027 */
     for (uint32_t r = 0; r < vocab; ++r) {
         const uint8_t *row = W + (uint64_t)r * 8 * 210;
         double acc = 0.0;
-        for (int b = 0; b < 8; ++b) {
-            dec_q6_k(row + 210 * b, vals);
-            for (int i = 0; i < 256; ++i) acc += (double)vals[i] * (double)xn[256 * b + i];
+        if (m->q8) {
+            acc = (double)dot_q8k(14, row, a, 8);   /* :4039-4040 */
+        } else {
+            for (int b = 0; b < 8; ++b) {
+                dec_q6_k(row + 210 * b, vals);
+                for (int i = 0; i < 256; ++i) acc += (double)vals[i] * (double)xn[256 * b + i];
+            }
         }
         if (!isfinite(acc)) return 0;
         if (logits) logits[r] = (float)acc;
@@ -432,11 +636,24 @@ int qxo_moe_layer(qxo_model *m, uint32_t layer, const float *x, float *out, floa
     const uint64_t gate_expert = (uint64_t)F * 8 * block_bytes(tg), up_expert = (uint64_t)F * 8 * block_bytes(tu),
                    down_expert = 2048ull * (F / 256) * block_bytes(td);
     if (!gate_expert || !up_expert || !down_expert) return 0;
+    /* q8_k_compat (:5286-5300): gate/up when both are IQ2_XS or both IQ2_S, down when
+       IQ3_XXS, IQ3_S or IQ4_XS */
+    const int gu_q8 = m->q8 && ((tg == 17 && tu == 17) || (tg == 22 && tu == 22));
+    const int dn_q8 = m->q8 && (td == 18 || td == 21 || td == 23);
     for (int r = 0; r < 8; ++r) {
-        qxo_matvec(tg, G + ids[r] * gate_expert, F, 2048, xn, g);
-        qxo_matvec(tu, U + ids[r] * up_expert, F, 2048, xn, u);
+        if (gu_q8) {
+            if (!matvec_q8k(tg, G + ids[r] * gate_expert, F, 2048, xn, g, 1) ||
+                !matvec_q8k(tu, U + ids[r] * up_expert, F, 2048, xn, u, 1)) return 0;
+        } else {
+            qxo_matvec(tg, G + ids[r] * gate_expert, F, 2048, xn, g);
+            qxo_matvec(tu, U + ids[r] * up_expert, F, 2048, xn, u);
+        }
         for (uint32_t i = 0; i < F; ++i) h[i] = (float)(silu((double)g[i]) * (double)u[i]);
-        qxo_matvec(td, D + ids[r] * down_expert, 2048, F, h, y);
+        if (dn_q8) {
+            if (!matvec_q8k(td, D + ids[r] * down_expert, 2048, F, h, y, 1)) return 0;
+        } else {
+            qxo_matvec(td, D + ids[r] * down_expert, 2048, F, h, y);
+        }
         for (uint32_t i = 0; i < 2048; ++i) moe[i] += (float)(wts[r] * (double)y[i]);
     }
     for (uint32_t i = 0; i < 2048; ++i) out[i] = x[i] + moe[i];
@@ -461,15 +678,14 @@ int qxo_attention_layer(qxo_model *m, uint32_t layer, uint32_t pos, uint32_t ctx
     float xn[2048], k[512], v[512];
     static float q[4096], cx[4096];
     qxo_rmsnorm(x, an, xn, 2048, NULL);
-    qxo_matvec(tk, Wk, 512, 2048, xn, k);
-    qxo_matvec(tv, Wv, 512, 2048, xn, v);
+    if (!project(m, tk, Wk, 512, 2048, xn, k) || !project(m, tv, Wv, 512, 2048, xn, v)) return 0;
     qxo_head_rmsnorm(k, kn, 4, 128);
     qxo_rope(k, 4, 128, pos, 1000000.0);
     if (vcur_out) memcpy(vcur_out, v, sizeof(v));
     const uint64_t slot = (uint64_t)layer * ctx + pos;
     ks[slot] = qxo_quantize_int8(k, kc + slot * 512, 512);
     vs[slot] = qxo_quantize_int8(v, vc + slot * 512, 512);
-    qxo_matvec(tq, Wq, 4096, 2048, xn, q);
+    if (!project(m, tq, Wq, 4096, 2048, xn, q)) return 0;
     qxo_head_rmsnorm(q, qn, 32, 128);
     qxo_rope(q, 32, 128, pos, 1000000.0);
     memset(cx, 0, sizeof(cx));
@@ -500,8 +716,7 @@ int qxo_attention_layer(qxo_model *m, uint32_t layer, uint32_t pos, uint32_t ctx
     }
     free(sc);
     if (kqv_out) memcpy(kqv_out, cx, sizeof(cx));
-    qxo_matvec(to, Wo, 2048, 4096, cx, attn_out);
-    return 1;
+    return project(m, to, Wo, 2048, 4096, cx, attn_out);
 }
 
 /* :3759-3793 — the Q4_K row of `token`, no norm on the full-MoE path */

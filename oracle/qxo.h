@@ -5,7 +5,8 @@
  * Every function cites the reference lines it restates.  Numeric contract
  * ("f32" activation mode): weights decode to f32 with the reference's op order,
  * products widen to double and accumulate in double in index order, results
- * narrow to float. */
+ * narrow to float.  "q8_k_compat" mode: integer dots against Q8_K activations with
+ * the reference's float scaling order. */
 #ifndef QXO_H
 #define QXO_H
 #include <stdint.h>
@@ -32,6 +33,19 @@ void qxo_rope(float *v, uint32_t heads, uint32_t head_dim, uint32_t pos, double 
 float qxo_quantize_int8(const float *src, int8_t *dst, uint32_t n);
 /* y[r] = (float) sum double(w) * double(x); non-finite -> 0 */
 void qxo_matvec(uint32_t ggml_type, const uint8_t *w, uint32_t rows, uint32_t in_dims, const float *x, float *y);
+
+/* q8_k_compat activation mode (reference src/qx_format.c:3869-4205): activations
+ * quantized to Q8_K blocks and integer dots per weight type.  The layout is ggml's
+ * block_q8_K (292 bytes). */
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } qxo_q8k;
+/* 0 when n is not a multiple of 256 or a value is not finite */
+int qxo_quantize_q8k(const float *x, uint32_t n, qxo_q8k *out);
+/* rows of type t against x quantized to Q8_K (in_dims <= 4096); expert != 0: a
+ * non-finite row fails (returns 0), else it is stored as 0 */
+int qxo_matvec_q8k(uint32_t ggml_type, const uint8_t *w, uint32_t rows, uint32_t in_dims, const float *x, float *y,
+                   int expert);
+/* 0: f32 (default), 1: q8_k_compat for the attention projections, experts and head */
+void qxo_set_activation(qxo_model *m, int q8_k_compat);
 
 /* Q6_K head on a residual: output_norm then 151936 (vocab) rows; top_n <= 32 ids
  * ordered by (double logit desc, index asc).  Returns 0 on a non-finite logit. */

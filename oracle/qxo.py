@@ -32,6 +32,11 @@ _sig("qxo_attention_layer", [vp, u32, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp])
 _sig("qxo_decode_token", [vp, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp, c_int, vp, u32, vp, vp])
 _sig("qxo_embed", [vp, u32, vp])
 _sig("qxo_matvec", [u32, vp, u32, u32, vp, vp], None)
+_sig("qxo_quantize_q8k", [vp, u32, vp])
+_sig("qxo_matvec_q8k", [u32, vp, u32, u32, vp, vp, c_int])
+_sig("qxo_set_activation", [vp, c_int], None)
+
+Q8K_BYTES = 292   # ggml block_q8_K: f32 d, int8 qs[256], int16 bsums[16]
 
 
 def _p(a):
@@ -55,13 +60,32 @@ def decode_block(ggml_type, raw):
     return out
 
 
-class Model:
-    """A QXF1 file opened by the oracle (mmap)."""
+def quantize_q8k(x):
+    """Q8_K blocks of x (length a multiple of 256) as raw bytes, or None when the
+    reference would fail (a non-finite value)."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(Q8K_BYTES * (len(x) // 256), np.uint8)
+    return out if _o.qxo_quantize_q8k(_p(x), len(x), _p(out)) else None
 
-    def __init__(self, path):
+
+def matvec_q8k(ggml_type, w, rows, in_dims, x, expert=False):
+    """rows of raw weight bytes w against x in q8_k_compat mode; None on failure."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(rows, np.float32)
+    return y if _o.qxo_matvec_q8k(ggml_type, _p(w), rows, in_dims, _p(x), _p(y), int(expert)) else None
+
+
+class Model:
+    """A QXF1 file opened by the oracle (mmap).  activation: "f32" or "q8_k_compat"."""
+
+    def __init__(self, path, activation="f32"):
+        if activation not in ("f32", "q8_k_compat"):
+            raise ValueError(activation)
         self._m = _o.qxo_open(str(path).encode())
         if not self._m:
             raise RuntimeError(f"oracle cannot open {path}")
+        _o.qxo_set_activation(self._m, int(activation == "q8_k_compat"))
 
     def close(self):
         if self._m:

@@ -39,6 +39,11 @@ DECODE_BLOCKS = [("token_embd.weight", [0, 1, 4095]), ("output.weight", [0, 7, 8
                  ("blk.0.ffn_gate_exps.weight", [0, 1, 98303]), ("blk.0.ffn_up_exps.weight", [12345]),
                  ("blk.0.ffn_down_exps.weight", [0, 2, 98303])]
 PHASES = ["input", "v-cur", "kqv-out", "ffn-inp", "ffn-moe-out", "output"]
+# q8_k_compat: expert rows of every expert format in model C (layer l % 4 picks the mix)
+Q8_EXPERT_DOTS = [("blk.0.ffn_gate_exps.weight", 2048), ("blk.0.ffn_down_exps.weight", 768),
+                  ("blk.1.ffn_up_exps.weight", 2048), ("blk.1.ffn_down_exps.weight", 768),
+                  ("blk.2.ffn_down_exps.weight", 768)]
+Q8_INJECT = ["none", "positive", "negative", "edge", "zero"]
 
 
 def run(args):
@@ -55,7 +60,14 @@ def fnv_file(path):
 def main():
     if not os.path.exists(REF):
         sys.exit(f"{REF} missing: run make -C oracle ref (needs /root/reference)")
-    out = {"models": MODELS, "decode_block": {}, "final_head": {}, "state_loop": {}}
+    out = {"models": MODELS, "decode_block": {}, "final_head": {}, "state_loop": {},
+           "q8k_activation": {}, "q8k_expert_dot": {}, "q8k_final_head": {}, "q8k_state_loop": {}}
+    # Q8_K activation blocks of the probe's own inputs (src/qx_format.c:4304-4345)
+    for inj in Q8_INJECT:
+        for values in (256, 512, 4096):
+            j = json.loads(run(["q8-k-activation-probe", "--values", str(values), "--inject", inj]))
+            out["q8k_activation"][f"{inj}/{values}"] = {"checksum": str(j["checksum"]), "quant_sum": j["quant_sum"],
+                                                        "first_scale": j["first_scale"]}
     with tempfile.TemporaryDirectory() as d:
         paths = {}
         for k, spec in MODELS.items():
@@ -86,6 +98,35 @@ def main():
                     "normalized_checksum": str(j["normalized_checksum"]), "logits_checksum": str(j["logits_checksum"]),
                     "argmax_token": j["argmax_token"], "argmax_logit": j["argmax_logit"],
                     "top8_by_float": [int(i) for i in order], "logits_sample": [float(v) for v in lg[:4]]}
+        # q8_k_compat: single expert rows (src/qx_format.c:5413-5470) and the Q6_K head
+        for name, n in Q8_EXPERT_DOTS:
+            ap = os.path.join(d, f"act{n}.f32")
+            np.random.default_rng(n).standard_normal(n).astype(np.float32).tofile(ap)
+            for e, r in ((0, 0), (3, 5), (15, 767 if n == 2048 else 2047)):
+                j = json.loads(run(["expert-q8-k-dot-probe", "--in", paths["C"], "--name", name, "--expert", str(e),
+                                    "--row", str(r), "--activation", ap]))
+                out["q8k_expert_dot"][f"{name}#{e}/{r}"] = {"ggml_type": j["ggml_type"], "dot": j["dot"]}
+        for k in ("A", "B"):
+            for seed in (1, 2):
+                rp = os.path.join(d, f"r{k}{seed}.f32")
+                od = os.path.join(d, f"q{k}{seed}")
+                os.mkdir(od)
+                j = json.loads(run(["final-head-probe", "--in", paths[k], "--residual", rp, "--out-dir", od,
+                                    "--activation", "q8_k_compat"]))
+                out["q8k_final_head"][f"{k}/seed{seed}"] = {
+                    "logits_checksum": str(j["logits_checksum"]), "argmax_token": j["argmax_token"],
+                    "argmax_logit": j["argmax_logit"]}
+        for k, steps in (("A", 5), ("B", 3), ("C", 3)):
+            dd = os.path.join(d, f"q{k}")
+            os.mkdir(dd)
+            layers = MODELS[k]["layers"]
+            txt = run(["state-loop-probe", "--in", paths[k], "--prompt-token", "17", "--steps", str(steps),
+                       "--layers", str(layers), "--ctx", "8", "--kv", "int8", "--full-moe", "--activation",
+                       "q8_k_compat", "--dump-residuals", dd])
+            toks = [int(t) for t in re.findall(r'"input_token": (\d+)', txt)]
+            dumps = {f"{s}/{layer}/{ph}": str(fnv_file(os.path.join(dd, f"step-{s}-layer-{layer}-{ph}.f32")))
+                     for s in range(steps) for layer in range(layers) for ph in PHASES}
+            out["q8k_state_loop"][k] = {"input_tokens": toks, "steps": steps, "ctx": 8, "dumps": dumps}
         # full-MoE state loop with INT8 KV and per-layer dumps (src/qx_format.c:5970-6719)
         for k, steps in (("A", 5), ("B", 4), ("C", 3)):
             dd = os.path.join(d, f"s{k}")
