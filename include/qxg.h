@@ -167,6 +167,23 @@ int qxg_prefill_layer(qxg_ctx *ctx, uint32_t layer, uint32_t n, uint32_t positio
  * formats beyond IQ4_XS / IQ2_XS / IQ3_XXS keeps path 0 whatever is set here. */
 int qxg_set_layer_path(qxg_ctx *ctx, int persistent);
 
+/* Activation format of the projections, experts and head: 0 "f32" (default), 1
+ * "q8_k_compat" -- the reference's activation_format argument of the state loop and
+ * stage probes (src/qx_format.c:5970-5972, 4217-4218, 5286-5288, 3565).  In
+ * q8_k_compat the matvec inputs are quantized to Q8_K blocks (256 values, one f32
+ * scale) and each weight type is dotted in integers; a non-finite activation or
+ * expert row makes the call fail with the reference's message.  Runs one kernel per
+ * phase (whatever qxg_set_layer_path says); qxg_prefill returns an error in this
+ * mode.  Drops the recorded decode graph. */
+int qxg_set_activation(qxg_ctx *ctx, uint32_t activation_format, char *err, uint64_t err_len);
+
+/* Same-input seam of the Q8_K quantizer the q8_k_compat kernels use: n values (a
+ * multiple of 256, at most 4096) -> n/256 blocks of 292 bytes in ggml's block_q8_K
+ * layout {f32 d, int8 qs[256], int16 bsums[16]}.  Replaces qx_quantize_q8_k as exposed
+ * by the reference's q8-k-activation-probe (src/qx_format.c:3891-3927, 4304-4345);
+ * fails, like it, on a non-finite value or a bad length. */
+int qxg_q8k_quantize(qxg_ctx *ctx, const float *x, uint32_t n, void *blocks_out, char *err, uint64_t err_len);
+
 /* ---- measurement (no reference counterpart: the reference times with clock(),
  *      src/qx_format.c:6245, 6642-6653) ---- */
 

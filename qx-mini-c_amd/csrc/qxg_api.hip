@@ -20,19 +20,20 @@ __global__ void qxk_router(const float *, const float *, const float *, uint32_t
 __global__ void qxk_topk(const float *, uint32_t, uint32_t, float *, uint32_t *, float *, uint32_t *, uint32_t *,
                          DevState *);
 __global__ void qxk_advance(DevState *);
+__global__ void qxk_q8k(const float *, uint32_t, uint8_t *, uint32_t *);
 __global__ void qxk_layers(QxPArgs);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
                             uint64_t, float *);
 __global__ void qxk_repack(uint32_t, const uint8_t *, uint64_t, uint8_t *, uint8_t *, uint8_t *, uint16_t *);
 void qxl_qkv(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, const QTensor *, float *,
-             Timer = Timer());
-void qxl_oproj(hipStream_t, const float *, const QTensor *, float *, float *, Timer = Timer());
+             DevState *, bool, Timer = Timer());
+void qxl_oproj(hipStream_t, const float *, const QTensor *, float *, float *, DevState *, bool, Timer = Timer());
 void qxl_gate_up(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, Tables, const double *,
-                 uint32_t, DevState *, float *, Timer = Timer());
-void qxl_down(hipStream_t, const float *, const QTensor *, Tables, const DevState *, float *, float *,
+                 uint32_t, DevState *, float *, bool, Timer = Timer());
+void qxl_down(hipStream_t, const float *, const QTensor *, Tables, DevState *, float *, float *, bool,
               Timer = Timer());
 void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32_t, DevState *, float *, float *,
-              uint32_t *, Timer = Timer());
+              uint32_t *, bool, Timer = Timer());
 __global__ void qxp_embed(const uint8_t *, uint64_t, const uint32_t *, float *);
 __global__ void qxp_norm(const float *, const float *, uint32_t, float *);
 __global__ void qxp_qk(const float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
@@ -117,6 +118,7 @@ struct qxg_ctx {
     // persistent layer kernel: per-layer pointer table, tagged exchange buffers, abort flag
     bool persist = false;            // layer path: persistent kernel (true) or one kernel per phase
     bool base_mix = true;            // every layer in the benchmark mix (IQ4_XS attention, IQ2_XS/IQ3_XXS experts)
+    bool q8 = false;                 // activation mode q8_k_compat (false: f32)
     bool eager = false;              // QXG_EAGER=1 at open: qxg_generate launches every step without a graph
     std::vector<void *> arenas;      // per-plane arenas of all layers' weights
     QxPlane planes[PL_COUNT] = {};
@@ -291,23 +293,23 @@ Timer timer_for(qxg_ctx *c, int which) {
 // ---- launch sequences (all asynchronous on c->s) ----
 void launch_attention(qxg_ctx *c, uint32_t l, float *x, float *attn_dump, float *vcur_dump) {
     const LayerW &w = c->L[l];
-    qxl_qkv(c->s, x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv, timer_for(c, 2));
+    qxl_qkv(c->s, x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv, c->st, c->q8, timer_for(c, 2));
     qx_launch(qxk_attn, dim3(32), dim3(256), (uint32_t)(c->kv_ctx * sizeof(double)), c->s, timer_for(c, 5), c->qkv,
               w.q_norm, w.k_norm, c->T, c->kc, c->vc, c->ks, c->vs, l, c->kv_ctx, std::sqrt(128.0),
               (const DevState *)c->st, c->ctxv, vcur_dump);
-    qxl_oproj(c->s, c->ctxv, w.wo, x, attn_dump, timer_for(c, 3));
+    qxl_oproj(c->s, c->ctxv, w.wo, x, attn_dump, c->st, c->q8, timer_for(c, 3));
 }
 
 void launch_moe(qxg_ctx *c, uint32_t l, float *x, float *moe_dump) {
     const LayerW &w = c->L[l];
     qx_launch(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, timer_for(c, 6), (const float *)x,
               w.ffn_norm, w.router, c->experts, c->rlog);
-    qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h, timer_for(c, 0));
-    qxl_down(c->s, c->h, w.down, c->T, c->st, x, moe_dump, timer_for(c, 1));
+    qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h, c->q8, timer_for(c, 0));
+    qxl_down(c->s, c->h, w.down, c->T, c->st, x, moe_dump, c->q8, timer_for(c, 1));
 }
 
 void launch_head(qxg_ctx *c, uint32_t top_n, float *norm_dump) {
-    qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, norm_dump, c->dig, timer_for(c, 4));
+    qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, norm_dump, c->dig, c->q8, timer_for(c, 4));
     hipLaunchKernelGGL(qxk_topk, dim3(TOPK_BLOCKS), dim3(256), 0, c->s, c->logits, c->vocab, top_n, c->cand_v,
                        c->cand_i, c->top_v, c->top_i, c->tokens, c->st);
 }
@@ -322,9 +324,9 @@ struct Dumps {
     float *layer = nullptr, *attn = nullptr, *moe = nullptr, *vcur = nullptr, *ctx = nullptr;
 };
 
-// The persistent kernel reads the weight arenas, built for the benchmark mix only; a model
-// with the checkpoint's other per-layer formats runs one kernel per phase.
-bool persistent(const qxg_ctx *c) { return c->persist && c->base_mix; }
+// The persistent kernel reads the weight arenas, built for the benchmark mix only, and
+// computes in the f32 activation mode; other models and q8_k_compat run one kernel per phase.
+bool persistent(const qxg_ctx *c) { return c->persist && c->base_mix && !c->q8; }
 
 // Sub-layers [s0, s1) of the token in one persistent launch (2l: attention half of
 // layer l, 2l+1: its MoE half), residual x_in -> x_out (device buffers).
@@ -386,9 +388,21 @@ bool check_ready(qxg_ctx *c, bool need_kv, char *err, uint64_t n) {
     return true;
 }
 
+// A q8_k_compat step that met a non-finite activation or expert row leaves a fault code
+// in the state: report it with the reference's message and clear it.
+bool check_q8(qxg_ctx *c, char *err, uint64_t n) {
+    uint32_t f = 0;
+    if (!hip_ok(hipMemcpy(&f, &c->st->q8_fault, 4, hipMemcpyDeviceToHost), err, n, "state read")) return false;
+    if (!f) return true;
+    (void)hipMemset(&c->st->q8_fault, 0, 4);
+    set_err(err, n, f == QXG_Q8_NONFINITE_EXPERT ? "non-finite packed expert Q8_K output" : "Q8_K activation contains NaN or Inf");
+    return false;
+}
+
 bool finish(qxg_ctx *c, char *err, uint64_t n) {
     if (!hip_ok(hipGetLastError(), err, n, "launch")) return false;
     if (!hip_ok(hipStreamSynchronize(c->s), err, n, "stream")) return false;
+    if (c->q8 && !check_q8(c, err, n)) return false;
     return !c->abort || check_abort(c, err, n);
 }
 
@@ -492,6 +506,10 @@ uint16_t f16_int(int v) {
 }
 
 bool prefill_ready(qxg_ctx *c, char *err, uint64_t n) {
+    if (c->q8) {
+        set_err(err, n, "prefill computes in the f32 activation mode only (decode the prompt token by token)");
+        return false;
+    }
     if (!c->base_mix) {
         set_err(err, n, "prefill supports the IQ4_XS / IQ2_XS / IQ3_XXS mix only (decode the prompt token by token)");
         return false;
@@ -980,6 +998,30 @@ int qxg_dequant_blocks(qxg_ctx *c, uint32_t type, const void *raw, uint64_t nblo
     return ok;
 }
 
+int qxg_q8k_quantize(qxg_ctx *c, const float *x, uint32_t n, void *blocks_out, char *err, uint64_t err_len) {
+    if (!c || !x || !blocks_out) { set_err(err, err_len, "invalid argument"); return 0; }
+    if (!n || n % 256u) { set_err(err, err_len, "Q8_K activation length must be a non-zero multiple of 256"); return 0; }
+    if (n > 4096u) { set_err(err, err_len, "Q8_K activation workspace is too small"); return 0; }
+    (void)hipSetDevice(c->device);
+    const uint64_t out_bytes = (uint64_t)n / 256 * 292;
+    uint8_t *buf = nullptr;
+    if (!hip_ok(hipMalloc(&buf, n * 4ull + out_bytes + 4), err, err_len, "hipMalloc")) return 0;
+    float *dx = (float *)buf;
+    uint8_t *dout = buf + n * 4ull;
+    uint32_t *dbad = (uint32_t *)(dout + out_bytes);
+    uint32_t bad = 0;
+    int ok = hip_ok(hipMemcpy(dx, x, n * 4ull, hipMemcpyHostToDevice), err, err_len, "upload") &&
+             hip_ok(hipMemset(dbad, 0, 4), err, err_len, "memset");
+    if (ok) {
+        hipLaunchKernelGGL(qxk_q8k, dim3((n / 8 + 255) / 256), dim3(256), 0, c->s, (const float *)dx, n, dout, dbad);
+        ok = finish(c, err, err_len) && hip_ok(hipMemcpy(blocks_out, dout, out_bytes, hipMemcpyDeviceToHost), err, err_len, "read") &&
+             hip_ok(hipMemcpy(&bad, dbad, 4, hipMemcpyDeviceToHost), err, err_len, "read");
+    }
+    (void)hipFree(buf);
+    if (ok && bad) { set_err(err, err_len, "Q8_K activation contains NaN or Inf"); return 0; }
+    return ok;
+}
+
 int qxg_embed_token(qxg_ctx *c, uint32_t token, float *x_out, char *err, uint64_t err_len) {
     if (!check_ready(c, false, err, err_len)) return 0;
     if (!c->emb) { set_err(err, err_len, "token_embd.weight not bound"); return 0; }
@@ -1078,11 +1120,11 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
         const uint32_t l = (layer + i) % c->layers;
         const LayerW &w = c->L[l];
         switch (which) {
-        case 0: qxl_gate_up(c->s, c->x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h); break;
-        case 1: qxl_down(c->s, c->h, w.down, c->T, c->st, c->attn, nullptr); break;
-        case 2: qxl_qkv(c->s, c->x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv); break;
-        case 3: qxl_oproj(c->s, c->ctxv, w.wo, c->attn, nullptr); break;
-        case 4: qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, nullptr, c->dig); break;
+        case 0: qxl_gate_up(c->s, c->x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h, c->q8); break;
+        case 1: qxl_down(c->s, c->h, w.down, c->T, c->st, c->attn, nullptr, c->q8); break;
+        case 2: qxl_qkv(c->s, c->x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv, c->st, c->q8); break;
+        case 3: qxl_oproj(c->s, c->ctxv, w.wo, c->attn, nullptr, c->st, c->q8); break;
+        case 4: qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, nullptr, c->dig, c->q8); break;
         case 5:
             hipLaunchKernelGGL(qxk_attn, dim3(32), dim3(256), (size_t)c->kv_ctx * sizeof(double), c->s, c->qkv,
                                w.q_norm, w.k_norm, c->T, c->kc, c->vc, c->ks, c->vs, l % c->kv_layers, c->kv_ctx,
@@ -1111,6 +1153,18 @@ int qxg_set_layer_path(qxg_ctx *c, int persistent) {
         if (c->s) (void)hipStreamSynchronize(c->s);
         drop_graph(c);
         c->persist = persistent != 0;
+    }
+    return 1;
+}
+
+int qxg_set_activation(qxg_ctx *c, uint32_t activation_format, char *err, uint64_t err_len) {
+    if (!c) { set_err(err, err_len, "invalid context"); return 0; }
+    if (activation_format > 1) { set_err(err, err_len, "unsupported activation format (0 f32, 1 q8_k_compat)"); return 0; }
+    if (c->q8 != (activation_format == 1)) {
+        (void)hipSetDevice(c->device);
+        if (c->s) (void)hipStreamSynchronize(c->s);
+        drop_graph(c);
+        c->q8 = activation_format == 1;
     }
     return 1;
 }

@@ -379,27 +379,32 @@ DEV void digits_load(const float *x, const float *w, DigIn<N, NORM> &in) {
     }
 }
 
+// RMSNorm of a 2048-vector held 8 values per thread (src/qx_format.c:3358-3371)
+template <int N>
+DEV void rms_normalise(DigIn<N, true> &in, double *s_red, float *norm_out) {
+    const int tid = threadIdx.x;
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += (double)in.v[0][i] * (double)in.v[0][i];
+    ss = wave_total_d(ss);
+    if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+    __syncthreads();
+    const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    const double inv = 1.0 / sqrt(tot / (double)N + 1.0e-6);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) in.v[0][i] = (float)((double)in.v[0][i] * inv) * in.w[i];
+    if (norm_out) {
+        reinterpret_cast<float4 *>(norm_out)[2 * tid] = make_float4(in.v[0][0], in.v[0][1], in.v[0][2], in.v[0][3]);
+        reinterpret_cast<float4 *>(norm_out)[2 * tid + 1] = make_float4(in.v[0][4], in.v[0][5], in.v[0][6], in.v[0][7]);
+    }
+}
+
 // returns true when every value is finite (block-uniform); ends with a block barrier
 template <int N, bool NORM>
 DEV bool block_digits(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float *norm_out = nullptr) {
     using D = DigIn<N, NORM>;
     const int tid = threadIdx.x;
-    if constexpr (NORM) {
-        double ss = 0.0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ss += (double)in.v[0][i] * (double)in.v[0][i];
-        ss = wave_total_d(ss);
-        if ((tid & 63) == 0) s_red[tid >> 6] = ss;
-        __syncthreads();
-        const double tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-        const double inv = 1.0 / sqrt(tot / (double)N + 1.0e-6);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) in.v[0][i] = (float)((double)in.v[0][i] * inv) * in.w[i];
-        if (norm_out) {
-            reinterpret_cast<float4 *>(norm_out)[2 * tid] = make_float4(in.v[0][0], in.v[0][1], in.v[0][2], in.v[0][3]);
-            reinterpret_cast<float4 *>(norm_out)[2 * tid + 1] = make_float4(in.v[0][4], in.v[0][5], in.v[0][6], in.v[0][7]);
-        }
-    }
+    if constexpr (NORM) rms_normalise(in, s_red, norm_out);
     bool fin = true;
 #pragma unroll
     for (int it = 0; it < D::PER; ++it) {
@@ -422,6 +427,71 @@ DEV bool block_digits(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float 
         }
     }
     return __syncthreads_or(!fin) == 0;
+}
+
+// q8_k_compat activations (src/qx_format.c:3891-3927).  A 256-value block is the 8
+// values of each of 32 consecutive lanes (half a wave): the value of largest magnitude,
+// first on ties, maps to -127: inv = -127/max, d = 1/inv, code = round-half-even(inv * v)
+// clamped to [-128, 127].  Every lane of the wave must call this (it exchanges lanes).
+// Returns d; the lane's 8 codes are packed in h0 (values 0-3) and h1 (4-7).
+DEV float q8_chunk(const float (&v)[8], uint32_t &h0, uint32_t &h1) {
+    const int half = (threadIdx.x & 63) >> 5;
+    float am = 0.0f, vm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if (fabsf(v[i]) > am) { am = fabsf(v[i]); vm = v[i]; }
+    float bm = am;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
+    const uint32_t hit = (uint32_t)(__ballot(am == bm) >> (32 * half));
+    const float vmax = __shfl(vm, 32 * half + (hit ? __ffs(hit) - 1 : 0));
+    const float inv = vmax == 0.0f ? 0.0f : -127.0f / vmax;
+    uint32_t H[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        int q = inv == 0.0f ? 0 : (int)rintf(inv * v[i]);
+        q = q > 127 ? 127 : q < -128 ? -128 : q;
+        H[i >> 2] |= (uint32_t)(q & 255) << (8 * (i & 3));
+    }
+    h0 = H[0];
+    h1 = H[1];
+    return inv == 0.0f ? 0.0f : 1.0f / inv;
+}
+
+// Q8_K activations in the digit-plane layout: codes in the h plane, m = l = 0, and every
+// 32-group of a block carries the scale d/65536, so the digit dots compute d * sum(code
+// * w).  Returns true when every value is finite (block-uniform); ends with a barrier.
+template <int N, bool NORM>
+DEV bool block_q8(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float *norm_out = nullptr) {
+    using D = DigIn<N, NORM>;
+    static_assert(D::NCH % 32 == 0, "each 256-value block is the 32 chunks of one half-wave");
+    const int tid = threadIdx.x;
+    if constexpr (NORM) rms_normalise(in, s_red, norm_out);
+    bool fin = true;
+#pragma unroll
+    for (int it = 0; it < D::PER; ++it) {
+        const int c = tid + 256 * it;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) fin = fin && isfinite(in.v[it][i]);
+        uint32_t h0, h1;
+        const float dq = q8_chunk(in.v[it], h0, h1);
+        if (c < D::NCH) {
+            uint32_t *d = s_dig + (c >> 2) * DIG_STRIDE;
+            const int q = c & 3;
+            *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(0u, 0u);
+            *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(0u, 0u);
+            if (q == 0) d[24] = __float_as_uint(dq * (1.0f / 65536.0f));
+        }
+    }
+    return __syncthreads_or(!fin) == 0;
+}
+
+// the activation mode's preparation: Q8_K codes, or the three-plane digits of f32
+template <bool Q8, int N, bool NORM>
+DEV bool block_act(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float *norm_out = nullptr) {
+    if constexpr (Q8) return block_q8(in, s_dig, s_red, norm_out);
+    else return block_digits(in, s_dig, s_red, norm_out);
 }
 
 DEV void load_dig(const uint32_t *__restrict__ s_dig, int g, Dig &d) {

@@ -54,8 +54,12 @@ struct DevState {
     uint32_t moe_ids[QXG_TOPK];
     double moe_w[QXG_TOPK];
     uint32_t epoch;         // exchange-buffer epoch of the persistent kernel (device-advanced)
-    uint32_t pad2;
+    uint32_t q8_fault;      // q8_k_compat failure of the step (QXG_Q8_*), cleared by the host
 };
+
+// q8_k_compat failures, reported as the reference reports them (src/qx_format.c:3906, 4771)
+#define QXG_Q8_NONFINITE_INPUT 1u    // "Q8_K activation contains NaN or Inf"
+#define QXG_Q8_NONFINITE_EXPERT 2u   // "non-finite packed expert Q8_K output"
 
 struct Tables {
     uint4 *g2;     // IQ2_XS grid: 512 x {pos lo, pos hi, neg lo, neg hi}

@@ -48,9 +48,9 @@ struct QkvW {
     uint32_t type[3];
 };
 
-template <int RPW, int FMT>
+template <int RPW, int FMT, bool Q8>
 DEV void qkv_rows(DigIn<2048, true> &din, const uint8_t *qs, const uint8_t *p1, const uint8_t *p2, int lr0, int r0,
-                  uint32_t *s_dig, double *s_red, float *qkv) {
+                  uint32_t *s_dig, double *s_red, float *qkv, DevState *st) {
     const int lane = threadIdx.x & 63;
     const int b = lane >> 3, ib = lane & 7;
     uint4 qv[RPW], qw[RPW], ha[RPW], hb[RPW], mv[RPW];
@@ -72,7 +72,7 @@ DEV void qkv_rows(DigIn<2048, true> &din, const uint8_t *qs, const uint8_t *p1, 
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     QXG_ANCHOR(din.v[0][7]);
     QXG_MARK(3, 1);
-    const bool ok = block_digits(din, s_dig, s_red);
+    const bool ok = block_act<Q8>(din, s_dig, s_red);
     QXG_MARK(3, 2);
     Dig g;
     load_dig(s_dig, lane, g);
@@ -90,11 +90,12 @@ DEV void qkv_rows(DigIn<2048, true> &din, const uint8_t *qs, const uint8_t *p1, 
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) if (lane == rr) mine = out[rr];
     if (lane < RPW) qkv[r0 + lane] = (ok && isfinite(mine)) ? mine : 0.0f;
+    if (Q8 && !ok && threadIdx.x == 0) st->q8_fault = QXG_Q8_NONFINITE_INPUT;
     QXG_MARK(3, 4);
 }
 
-template <int RPW>
-__global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm_w, QkvW w, float *qkv) {
+template <int RPW, bool Q8>
+__global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm_w, QkvW w, float *qkv, DevState *st) {
     __shared__ uint32_t s_dig[64 * DIG_STRIDE];
     __shared__ double s_red[4];
     const int wave = wave_id();
@@ -105,8 +106,8 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
     QXG_MARK(3, 0);
     DigIn<2048, true> din;
     digits_load(x, norm_w, din);
-    if (w.type[mi] == 13) qkv_rows<RPW, 13>(din, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv);
-    else qkv_rows<RPW, 23>(din, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv);
+    if (w.type[mi] == 13) qkv_rows<RPW, 13, Q8>(din, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv, st);
+    else qkv_rows<RPW, 23, Q8>(din, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv, st);
 }
 
 // Attention for one q head, with the per-head q/k RMSNorm (src/qx_format.c:3740-3757),
@@ -238,9 +239,9 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
 // O projection 4096 -> 2048 on ctx (IQ4_XS, or Q5_K in the real checkpoint), then
 // x[r] += o[r] (src/qx_format.c:6420-6423).  Lane handles sub-blocks lane and lane+64
 // (blocks lane/8 and 8+lane/8).
-template <int RPW, int FMT>
+template <int RPW, int FMT, bool Q8>
 __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_t *qs, const uint8_t *meta,
-                                                  const uint8_t *p2, float *x, float *attn_dump) {
+                                                  const uint8_t *p2, float *x, float *attn_dump, DevState *st) {
     __shared__ uint32_t s_dig[128 * DIG_STRIDE];
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int ib = lane & 7, b0 = lane >> 3, b1 = 8 + (lane >> 3);
@@ -275,7 +276,7 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     QXG_ANCHOR(din.v[1][7]);
     QXG_MARK(0, 1);
-    const bool ok = block_digits(din, s_dig, nullptr);
+    const bool ok = block_act<Q8>(din, s_dig, nullptr);
     QXG_MARK(0, 2);
     Dig g0, g1;
     load_dig(s_dig, lane, g0);
@@ -303,6 +304,7 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
         if (attn_dump) attn_dump[r] = o;
         x[r] = xr + o;
     }
+    if (Q8 && !ok && threadIdx.x == 0) st->q8_fault = QXG_Q8_NONFINITE_INPUT;
     QXG_MARK(0, 4);
 }
 
@@ -362,7 +364,7 @@ DEV float gu_dot(gu4 u, const Dig &g, const uint4 *G, const uint2 *SEL) {
     else return dot_iq2s(u.x, u.y, u.z & 255u, u.z >> 8, u.w, g, G, SEL);
 }
 
-template <int UPW, int FMT>
+template <int UPW, int FMT, bool Q8>
 __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *norm_w, GuW gw, GuW uw, Tables T,
         const double *logits, uint32_t experts, DevState *st, float *h) {
     constexpr int NG = FMT == 17 ? 512 : 1024, NS = FMT == 17 ? 128 : 256;
@@ -420,7 +422,7 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     if (tid < NS) s_sel[tid] = t2;
     QXG_ANCHOR(din.v[0][7]);
     QXG_MARK(1, 1);
-    const bool ok = block_digits(din, s_dig, s_red);   // ends with a barrier
+    const bool ok = block_act<Q8>(din, s_dig, s_red);   // ends with a barrier
     QXG_MARK(1, 2);
     Dig g;
     load_dig(s_dig, lane, g);
@@ -449,6 +451,9 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
 #pragma unroll
     for (int k = 0; k < UPW; ++k) if (lane == k) { gv = o[k]; uv = o[UPW + k]; }
     if (lane < UPW) {
+        // q8_k_compat fails the step on a non-finite expert row (src/qx_format.c:4771)
+        if (Q8 && (!ok || !isfinite(gv) || !isfinite(uv)))
+            st->q8_fault = ok ? QXG_Q8_NONFINITE_EXPERT : QXG_Q8_NONFINITE_INPUT;
         gv = (ok && isfinite(gv)) ? gv : 0.0f;
         uv = (ok && isfinite(uv)) ? uv : 0.0f;
         const double sg = (double)gv / (1.0 + exp(-(double)gv));
@@ -491,8 +496,8 @@ DEV float dn_dot(uint4 a, uint2 m, int k, const Dig &g, const uint2 *G, const ui
     else return dot_iq4(a, m, k, g);
 }
 
-template <int RPW, int FMT>
-__global__ __launch_bounds__(256) void qxk_down(const float *h, DnW w, Tables T, const DevState *st, float *x,
+template <int RPW, int FMT, bool Q8>
+__global__ __launch_bounds__(256) void qxk_down(const float *h, DnW w, Tables T, DevState *st, float *x,
                                                  float *moe_dump) {
     constexpr int NG = FMT == 21 ? 512 : 256, NS = FMT == 21 ? 256 : 128;
     __shared__ uint2 s_g3[NG];
@@ -533,7 +538,7 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, DnW w, Tables T,
     }
     QXG_ANCHOR(din.v[din.PER - 1][7]);
     QXG_MARK(2, 1);
-    const bool ok = block_digits(din, s_dig, nullptr);   // ends with a barrier
+    const bool ok = block_act<Q8>(din, s_dig, nullptr);   // ends with a barrier
     QXG_MARK(2, 2);
     Dig g[3];
 #pragma unroll
@@ -546,6 +551,8 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, DnW w, Tables T,
         part += dppf<DPP_XOR1>(part);
         part += dppf<DPP_XOR2>(part);
         part += dppf<DPP_HALF_MIRROR>(part);   // lanes 8q..8q+7 now hold expert rank q's row
+        if (Q8 && (!ok || !isfinite(part)) && k == 0)
+            st->q8_fault = ok ? QXG_Q8_NONFINITE_EXPERT : QXG_Q8_NONFINITE_INPUT;
         const float y = (ok && isfinite(part)) ? part : 0.0f;
         float moe = 0.0f;
 #pragma unroll
@@ -565,15 +572,46 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, DnW w, Tables T,
 // output RMSNorm + digits once per token into a global buffer (64 groups of
 // DIG_STRIDE dwords, then the all-finite flag); the head waves load their group.
 extern "C" __global__ __launch_bounds__(256) void qxk_norm_digits(const float *x, const float *norm_w, uint32_t *dig,
-                                                                   float *norm_dump, const DevState *st) {
+                                                                   float *norm_dump, DevState *st, uint32_t q8) {
     if (!st->force_head && st->step + 1 < st->n_prompt) return;
     __shared__ uint32_t s_dig[64 * DIG_STRIDE];
     __shared__ double s_red[4];
     DigIn<2048, true> din;
     digits_load(x, norm_w, din);
-    const bool ok = block_digits(din, s_dig, s_red, norm_dump);
+    // q8_k_compat: Q8_K codes of the normed residual for the Q6_K head (src/qx_format.c:4026-4027)
+    const bool ok = q8 ? block_q8(din, s_dig, s_red, norm_dump) : block_digits(din, s_dig, s_red, norm_dump);
+    if (q8 && !ok && threadIdx.x == 0) st->q8_fault = QXG_Q8_NONFINITE_INPUT;
     for (int i = threadIdx.x; i < 64 * DIG_STRIDE; i += 256) dig[i] = s_dig[i];
     if (threadIdx.x == 0) dig[64 * DIG_STRIDE] = ok ? 1u : 0u;
+}
+
+// Q8_K blocks of n values (n a multiple of 256) in ggml's block_q8_K layout: f32 d, 256
+// int8 codes, 16 int16 sums of 16 codes (src/qx_format.c:3891-3927).  Thread per 8
+// values; a 256-value block is one half-wave.  *bad is set on a non-finite value.
+extern "C" __global__ __launch_bounds__(256) void qxk_q8k(const float *x, uint32_t n, uint8_t *out, uint32_t *bad) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;   // chunk of 8 values
+    const bool live = c < n / 8;                         // whole half-waves live or not (256 | n)
+    float v[8];
+    bool fin = true;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        v[i] = live ? x[8 * c + i] : 0.0f;
+        fin = fin && isfinite(v[i]);
+    }
+    uint32_t h0, h1;
+    const float d = q8_chunk(v, h0, h1);
+    int s8 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s8 += (int8_t)(((i < 4 ? h0 : h1) >> (8 * (i & 3))) & 255u);
+    const int s16 = s8 + __shfl_xor(s8, 1);   // a 16-code sum spans the chunks 2j, 2j+1
+    if (!live) return;
+    uint8_t *blk = out + (uint64_t)(c / 32) * 292;
+    const uint32_t k = c % 32;
+    if (k == 0) *reinterpret_cast<float *>(blk) = d;
+    reinterpret_cast<uint32_t *>(blk + 4)[2 * k] = h0;   // 292-byte blocks: dword alignment only
+    reinterpret_cast<uint32_t *>(blk + 4)[2 * k + 1] = h1;
+    if (!(k & 1)) *reinterpret_cast<int16_t *>(blk + 260 + k) = (int16_t)s16;
+    if (!fin) *bad = 1u;
 }
 
 template <int RPW>
@@ -839,43 +877,47 @@ extern "C" __global__ __launch_bounds__(256) void qxk_repack(uint32_t type, cons
 
 // ----------------------------------------------------------------- launch wrappers
 extern "C" {
-// Each wrapper picks the kernel instantiation of the tensor's format (validated at bind).
-void qxl_qkv(hipStream_t s, const float *x, const float *nw, const QTensor *q, const QTensor *k, const QTensor *v, float *qkv, Timer t) {
+// Each wrapper picks the kernel instantiation of the tensor's format (validated at bind)
+// and of the activation mode (q8: q8_k_compat).
+void qxl_qkv(hipStream_t s, const float *x, const float *nw, const QTensor *q, const QTensor *k, const QTensor *v, float *qkv,
+             DevState *st, bool q8, Timer t) {
     constexpr int RPW = 4;
     QkvW w;
     const QTensor *m[3] = {q, k, v};
     for (int i = 0; i < 3; ++i) { w.qs[i] = m[i]->p0; w.p1[i] = m[i]->p1; w.p2[i] = m[i]->p2; w.type[i] = m[i]->type; }
-    qx_launch(qxk_qkv<RPW>, dim3(5120 / (4 * RPW)), dim3(256), 0, s, t, x, nw, w, qkv);
+    const dim3 grid(5120 / (4 * RPW));
+    if (q8) qx_launch(qxk_qkv<RPW, true>, grid, dim3(256), 0, s, t, x, nw, w, qkv, st);
+    else qx_launch(qxk_qkv<RPW, false>, grid, dim3(256), 0, s, t, x, nw, w, qkv, st);
 }
-void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, float *dump, Timer t) {
+void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, float *dump, DevState *st, bool q8, Timer t) {
     constexpr int RPW = 2;
-    if (o->type == 13)
-        qx_launch(qxk_oproj<RPW, 13>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, t, ctxv, o->p0, o->p1, o->p2, x, dump);
-    else
-        qx_launch(qxk_oproj<RPW, 23>, dim3(2048 / (4 * RPW)), dim3(256), 0, s, t, ctxv, o->p0, o->p1, o->p2, x, dump);
+    const dim3 grid(2048 / (4 * RPW));
+    auto go = [&](auto kernel) { qx_launch(kernel, grid, dim3(256), 0, s, t, ctxv, o->p0, o->p1, o->p2, x, dump, st); };
+    if (o->type == 13) q8 ? go(qxk_oproj<RPW, 13, true>) : go(qxk_oproj<RPW, 13, false>);
+    else q8 ? go(qxk_oproj<RPW, 23, true>) : go(qxk_oproj<RPW, 23, false>);
 }
 void qxl_gate_up(hipStream_t s, const float *x, const float *nw, const QTensor *g, const QTensor *u, Tables T,
-                 const double *logits, uint32_t experts, DevState *st, float *h, Timer t) {
+                 const double *logits, uint32_t experts, DevState *st, float *h, bool q8, Timer t) {
     constexpr int UPW = 4;
     const GuW gw{g->p0, g->p1, g->p2, g->d}, uw{u->p0, u->p1, u->p2, u->d};
     const dim3 grid(QXG_TOPK * QXG_FFN / (4 * UPW));
-    if (g->type == 22)
-        qx_launch(qxk_gate_up<UPW, 22>, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h);
-    else
-        qx_launch(qxk_gate_up<UPW, 17>, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h);
+    auto go = [&](auto kernel) { qx_launch(kernel, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h); };
+    if (g->type == 22) q8 ? go(qxk_gate_up<UPW, 22, true>) : go(qxk_gate_up<UPW, 22, false>);
+    else q8 ? go(qxk_gate_up<UPW, 17, true>) : go(qxk_gate_up<UPW, 17, false>);
 }
-void qxl_down(hipStream_t s, const float *h, const QTensor *d, Tables T, const DevState *st, float *x, float *dump, Timer t) {
+void qxl_down(hipStream_t s, const float *h, const QTensor *d, Tables T, DevState *st, float *x, float *dump, bool q8, Timer t) {
     constexpr int RPW = 2;
     const DnW w{d->p0, d->p1, d->p2, d->d};
     const dim3 grid(2048 / (4 * RPW));
-    if (d->type == 23) qx_launch(qxk_down<RPW, 23>, grid, dim3(256), 0, s, t, h, w, T, st, x, dump);
-    else if (d->type == 21) qx_launch(qxk_down<RPW, 21>, grid, dim3(256), 0, s, t, h, w, T, st, x, dump);
-    else qx_launch(qxk_down<RPW, 18>, grid, dim3(256), 0, s, t, h, w, T, st, x, dump);
+    auto go = [&](auto kernel) { qx_launch(kernel, grid, dim3(256), 0, s, t, h, w, T, st, x, dump); };
+    if (d->type == 23) q8 ? go(qxk_down<RPW, 23, true>) : go(qxk_down<RPW, 23, false>);
+    else if (d->type == 21) q8 ? go(qxk_down<RPW, 21, true>) : go(qxk_down<RPW, 21, false>);
+    else q8 ? go(qxk_down<RPW, 18, true>) : go(qxk_down<RPW, 18, false>);
 }
 void qxl_head(hipStream_t s, const float *x, const float *nw, const QTensor *w, uint32_t vocab, DevState *st,
-              float *logits, float *norm_dump, uint32_t *dig, Timer t) {
+              float *logits, float *norm_dump, uint32_t *dig, bool q8, Timer t) {
     constexpr int RPW = 4;
-    hipLaunchKernelGGL(qxk_norm_digits, dim3(1), dim3(256), 0, s, x, nw, dig, norm_dump, st);
+    hipLaunchKernelGGL(qxk_norm_digits, dim3(1), dim3(256), 0, s, x, nw, dig, norm_dump, st, (uint32_t)q8);
     const uint32_t grid = (vocab + 4 * RPW - 1) / (4 * RPW);
     qx_launch(qxk_head<RPW>, dim3(grid), dim3(256), 0, s, t, dig, w->p0, w->p1, (const int8_t *)w->p2, w->d,
                        vocab, st, logits);

@@ -58,6 +58,8 @@ _sig(_g, "qxg_attention_layer", [vp, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_moe_layer", [vp, u32, vp, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_final_head", [vp, vp, vp, vp, u32, vp, vp, *ERR])
 _sig(_g, "qxg_set_layer_path", [vp, c_int])
+_sig(_g, "qxg_set_activation", [vp, u32, vp, u64])
+_sig(_g, "qxg_q8k_quantize", [vp, vp, u32, vp, vp, u64])
 _sig(_g, "qxg_kv_export", [vp, cp, u32, u32, u32, u32, u32, *ERR])
 _sig(_g, "qxg_kv_import", [vp, cp, u32, u32, u32, ctypes.POINTER(u32), ctypes.POINTER(u32), *ERR])
 _sig(_g, "qxg_kvsnap_write", [cp, u32, u32, u32, u32, u32, vp, vp, vp, vp, *ERR])
@@ -268,6 +270,20 @@ class Context:
     def set_layer_path(self, persistent):
         """0: one kernel per phase (default); 1: the persistent layer kernel."""
         self._check(_g.qxg_set_layer_path(self._c, int(persistent)))
+
+    def set_activation(self, fmt):
+        """"f32" (default) or "q8_k_compat" (Q8_K activations, integer dots)."""
+        modes = {"f32": 0, "q8_k_compat": 1}
+        if fmt not in modes:
+            raise ValueError(f"unsupported activation format {fmt!r}")
+        self._check(_g.qxg_set_activation(self._c, modes[fmt], self._err, 1024))
+
+    def q8k_quantize(self, x):
+        """Q8_K blocks (292 bytes each) of x on the device, as raw bytes."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(292 * (len(x) // 256), np.uint8)
+        self._check(_g.qxg_q8k_quantize(self._c, x.ctypes.data_as(vp), len(x), out.ctypes.data_as(vp), self._err, 1024))
+        return out
 
     def time_kernel(self, which, layer=0, iters=20):
         ms = c_float()
