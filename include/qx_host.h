@@ -125,8 +125,13 @@ int qx_dump_decode_block_summary(const char *path, const char *name, uint64_t bl
 /* reference qx_dump_final_head_probe_summary (include/qx_format.h:163). */
 int qx_dump_final_head_probe_summary(const char *path, const char *residual_path, const char *output_dir,
         const char *activation_mode, uint32_t top_n, FILE *out, char *err, uint64_t err_len);
+/* reference qx_dump_q8_k_activation_probe_summary (include/qx_format.h:156): the
+ * probe's fixed inputs (inject: none, zero, nan, inf, positive, negative, edge)
+ * quantized to Q8_K blocks on the GPU; same JSON keys and block bytes. */
+int qx_dump_q8_k_activation_probe_gpu(uint32_t values, const char *inject, FILE *out, char *err, uint64_t err_len);
 /* reference qx_dump_state_loop_probe_summary (include/qx_format.h:157), restricted
- * to the --full-moe --rope-gqa-attention path with INT8 KV and f32 activations:
+ * to the --full-moe --rope-gqa-attention path with INT8 KV and f32 or q8_k_compat
+ * activations:
  * every other combination is rejected with an error, as the reference rejects
  * unsupported policies.  prompt_count tokens are fed, then greedy generation. */
 int qx_dump_prompt_state_loop_gpu(const char *path, const uint32_t *prompt_tokens, uint32_t prompt_count,

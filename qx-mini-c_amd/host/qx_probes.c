@@ -120,10 +120,16 @@ static void remove_f32(const char *dir, const char *name) {
     remove(p);
 }
 
+/* "f32" -> 0, "q8_k_compat" -> 1, anything else -> -1 (reference src/qx_format.c:5971-5973) */
+static int activation_code(const char *s) {
+    if (!s) return -1;
+    return !strcmp(s, "f32") ? 0 : !strcmp(s, "q8_k_compat") ? 1 : -1;
+}
+
 int qx_dump_final_head_probe_summary(const char *path, const char *residual_path, const char *output_dir,
         const char *activation_mode, uint32_t top_n, FILE *out, char *err, uint64_t err_len) {
-    if (!path || !residual_path || !output_dir || !out || top_n == 0 || top_n > 32 ||
-        !activation_mode || strcmp(activation_mode, "f32") != 0) {
+    const int act = activation_code(activation_mode);
+    if (!path || !residual_path || !output_dir || !out || top_n == 0 || top_n > 32 || act < 0) {
         set_err(err, err_len, "invalid final head probe argument or activation mode"); return 0;
     }
     float res[2048], nrm[2048];
@@ -132,6 +138,7 @@ int qx_dump_final_head_probe_summary(const char *path, const char *residual_path
     qx_gpu_model_info mi;
     if (!open_gpu(path, 1, &ctx, &mi, err, err_len)) return 0;
     if (!mi.has_head) { qxg_close(ctx); set_err(err, err_len, "final head requires Q6_K output.weight"); return 0; }
+    if (!qxg_set_activation(ctx, (uint32_t)act, err, err_len)) { qxg_close(ctx); return 0; }
     float *logits = (float *)malloc((size_t)mi.vocab * 4);
     uint32_t ids[32];
     double lg[32];
@@ -143,10 +150,11 @@ int qx_dump_final_head_probe_summary(const char *path, const char *residual_path
         double ss = 0.0, ns = 0.0;
         for (int i = 0; i < 2048; ++i) { ss += (double)res[i] * res[i]; ns += (double)nrm[i] * nrm[i]; }
         fprintf(out, "{\"probe\":\"final_head\",\"backend\":\"hip\",\"input_dims\":2048,\"vocab_size\":%u,"
-                "\"activation_mode\":\"f32\",\"lm_head_kernel\":\"q6_k_hip_dot4\",\"input_rms\":%.17g,"
+                "\"activation_mode\":\"%s\",\"lm_head_kernel\":\"%s\",\"input_rms\":%.17g,"
                 "\"normalized_l2\":%.17g,\"residual_checksum\":%llu,\"normalized_checksum\":%llu,"
                 "\"logits_checksum\":%llu,\"argmax_token\":%u,\"argmax_logit\":%.17g,\"top_tokens\":[",
-                mi.vocab, sqrt(ss / 2048.0 + 1.0e-6), sqrt(ns), (unsigned long long)qxf_fnv1a64(res, sizeof(res)),
+                mi.vocab, act ? "q8_k_compat" : "f32", act ? "q6_k_q8_k_hip_dot4" : "q6_k_hip_dot4",
+                sqrt(ss / 2048.0 + 1.0e-6), sqrt(ns), (unsigned long long)qxf_fnv1a64(res, sizeof(res)),
                 (unsigned long long)qxf_fnv1a64(nrm, sizeof(nrm)), (unsigned long long)qxf_fnv1a64(logits, (uint64_t)mi.vocab * 4),
                 ids[0], lg[0]);
         for (uint32_t i = 0; i < top_n; ++i) fprintf(out, "%s{\"token\":%u,\"logit\":%.17g}", i ? "," : "", ids[i], lg[i]);
@@ -170,13 +178,14 @@ static int dump_vec(const char *dir, uint32_t step, uint32_t layer, const char *
 }
 
 /* Full-MoE state loop on the GPU (reference src/qx_format.c:5970-6719 with
- * --full-moe [--final-head], INT8 KV, f32 activations, temperature 0). */
+ * --full-moe [--final-head], INT8 KV, f32 or q8_k_compat activations, temperature 0). */
 int qx_dump_prompt_state_loop_gpu(const char *path, const uint32_t *prompt, uint32_t n_prompt,
         uint32_t gen_steps, uint32_t ctx_tokens, const char *kv_format, const char *activation_format,
         int final_head, uint32_t top_n, const char *dump_dir, int bench, FILE *out, char *err, uint64_t err_len) {
     if (!path || !prompt || !out) { set_err(err, err_len, "invalid argument"); return 0; }
     if (!kv_format || strcmp(kv_format, "int8") != 0) { set_err(err, err_len, "the GPU state loop supports INT8 KV only"); return 0; }
-    if (!activation_format || strcmp(activation_format, "f32") != 0) { set_err(err, err_len, "unsupported activation format"); return 0; }
+    const int act = activation_code(activation_format);
+    if (act < 0) { set_err(err, err_len, "unsupported activation format"); return 0; }
     if (gen_steps == 0 || n_prompt == 0) { set_err(err, err_len, "prompt state loop requires >= 1 prompt token and >= 1 generation step"); return 0; }
     if (ctx_tokens == 0 || ctx_tokens > 4096) { set_err(err, err_len, "state loop context must be between 1 and 4096"); return 0; }
     const uint32_t steps = n_prompt + gen_steps - 1;
@@ -189,6 +198,7 @@ int qx_dump_prompt_state_loop_gpu(const char *path, const uint32_t *prompt, uint
     if (!open_gpu(path, 1, &ctx, &mi, err, err_len)) return 0;
     t_load = now_s() - t_load;
     if (!mi.has_embedding) { qxg_close(ctx); set_err(err, err_len, "token_embd.weight not found"); return 0; }
+    if (!qxg_set_activation(ctx, (uint32_t)act, err, err_len)) { qxg_close(ctx); return 0; }
     if (final_head && !mi.has_head) { qxg_close(ctx); set_err(err, err_len, "final head requires Q6_K output.weight"); return 0; }
     for (uint32_t i = 0; i < n_prompt; ++i)
         if (prompt[i] >= mi.vocab) { qxg_close(ctx); set_err(err, err_len, "prompt token out of range"); return 0; }
@@ -199,9 +209,9 @@ int qx_dump_prompt_state_loop_gpu(const char *path, const uint32_t *prompt, uint
     int ok = x && a && y && kqv && vcur && moe && logits;
     if (!ok) set_err(err, err_len, "out of memory");
     fprintf(out, "{\n  \"probe\": \"prompt_state_loop\",\n  \"backend\": \"hip-gfx950\",\n  \"layers\": %u,\n"
-            "  \"ctx_tokens\": %u,\n  \"kv_format\": \"int8\",\n  \"activation_format\": \"f32\",\n  \"full_moe\": true,\n"
+            "  \"ctx_tokens\": %u,\n  \"kv_format\": \"int8\",\n  \"activation_format\": \"%s\",\n  \"full_moe\": true,\n"
             "  \"final_head\": %s,\n  \"prompt_tokens\": %u,\n  \"generation_steps\": %u,\n  \"steps\": %u,\n  \"tokens\": [",
-            mi.layers, ctx_tokens, final_head ? "true" : "false", n_prompt, gen_steps, steps);
+            mi.layers, ctx_tokens, act ? "q8_k_compat" : "f32", final_head ? "true" : "false", n_prompt, gen_steps, steps);
     uint32_t current = prompt[0];
     double t_loop = now_s();
     for (uint32_t s = 0; ok && s < steps; ++s) {
@@ -267,5 +277,51 @@ int qx_dump_prompt_state_loop_gpu(const char *path, const uint32_t *prompt, uint
     }
     free(x); free(a); free(y); free(kqv); free(vcur); free(moe); free(logits);
     qxg_close(ctx);
+    return ok;
+}
+
+/* Q8_K blocks of the probe's fixed inputs, quantized on the GPU (reference
+ * qx_dump_q8_k_activation_probe_summary, src/qx_format.c:4304-4345: same inputs,
+ * injections, errors and JSON keys). */
+int qx_dump_q8_k_activation_probe_gpu(uint32_t values, const char *inject, FILE *out, char *err, uint64_t err_len) {
+    static const char *const kinds[] = {"none", "zero", "nan", "inf", "positive", "negative", "edge"};
+    int kind = -1;
+    for (int i = 0; inject && i < 7; ++i) if (!strcmp(inject, kinds[i])) kind = i;
+    if (!out || !inject || values == 0) { set_err(err, err_len, "invalid Q8_K activation probe size"); return 0; }
+    if (values > 4096) { set_err(err, err_len, "Q8_K activation workspace is too small"); return 0; }
+    if (kind < 0) { set_err(err, err_len, "invalid Q8_K activation injection"); return 0; }
+    float x[4096];
+    for (uint32_t i = 0; i < values; ++i) {
+        switch (kind) {
+        case 1: x[i] = 0.0f; break;
+        case 4: x[i] = (float)(i % 127u) / 127.0f; break;
+        case 5: x[i] = -(float)(i % 127u) / 127.0f; break;
+        case 6: x[i] = i % 2u ? 1.0f : -1.0f; break;
+        default: x[i] = (float)((int32_t)(i % 251u) - 125) / 127.0f; break;
+        }
+    }
+    if (kind == 2) x[values / 2] = NAN;
+    if (kind == 3) x[values / 2] = INFINITY;
+    qxg_ctx *ctx = NULL;
+    if (!qxg_open(0, &ctx, err, err_len)) return 0;
+    const uint32_t blocks = values / 256;
+    uint8_t *b = (uint8_t *)malloc((size_t)(blocks ? blocks : 1) * 292);
+    int ok = b && qxg_q8k_quantize(ctx, x, values, b, err, err_len);
+    qxg_close(ctx);
+    if (ok) {
+        int64_t qsum = 0;
+        for (uint32_t k = 0; k < blocks; ++k)
+            for (int i = 0; i < 256; ++i) qsum += (int8_t)b[292ull * k + 4 + i];
+        float d0;
+        memcpy(&d0, b, 4);
+        fprintf(out, "{\n  \"probe\": \"q8_k_activation\",\n  \"backend\": \"hip\",\n"
+                "  \"activation_format\": \"q8_k_compat\",\n  \"values\": %u,\n  \"blocks\": %u,\n"
+                "  \"block_bytes\": 292,\n  \"workspace_bytes\": %u,\n  \"first_scale\": %.9g,\n"
+                "  \"quant_sum\": %lld,\n  \"finite\": true,\n  \"block_hex\": \"",
+                values, blocks, blocks * 292u, d0, (long long)qsum);
+        for (uint32_t i = 0; i < blocks * 292u; ++i) fprintf(out, "%02x", b[i]);
+        fprintf(out, "\",\n  \"checksum\": %llu\n}\n", (unsigned long long)qxf_fnv1a64(b, (uint64_t)blocks * 292));
+    }
+    free(b);
     return ok;
 }

@@ -1,6 +1,6 @@
 /* qxqxf — CLI for the GPU path with the reference's sub-command names and flags
- * for the probes on the decode path (reference src/qx_qxf_main.c:1219-1237,
- * 1671-1697, 1726-1809).  Exit codes: 0 ok, 1 runtime failure, 2 usage. */
+ * for the probes on the decode path (reference src/qx_qxf_main.c:235-258,
+ * 1219-1237, 1671-1697, 1726-1809).  Exit codes: 0 ok, 1 runtime failure, 2 usage. */
 #include "qx_host.h"
 
 #include <errno.h>
@@ -11,11 +11,12 @@ static void usage(const char *argv0) {
     fprintf(stderr,
             "usage:\n"
             "  %s decode-block --in FILE --name TENSOR --block N\n"
-            "  %s final-head-probe --in FILE --residual R.f32 --out-dir DIR [--activation f32] [--top-n N]\n"
+            "  %s final-head-probe --in FILE --residual R.f32 --out-dir DIR [--activation f32|q8_k_compat] [--top-n N]\n"
             "  %s state-loop-probe --in FILE --prompt-token T[,T...] --steps N --ctx C --kv int8 --full-moe\n"
-            "        [--final-head] [--top-n N] [--dump-residuals DIR] [--bench] [--activation f32]\n"
-            "  %s generate-model --out FILE [--layers L] [--vocab V] [--experts E] [--seed S] [--no-embedding] [--no-head]\n",
-            argv0, argv0, argv0, argv0);
+            "        [--final-head] [--top-n N] [--dump-residuals DIR] [--bench] [--activation f32|q8_k_compat]\n"
+            "  %s q8-k-activation-probe --values N [--inject none|zero|nan|inf|positive|negative|edge]\n"
+            "  %s generate-model --out FILE [--layers L] [--vocab V] [--experts E] [--seed S] [--no-embedding] [--no-head] [--mix]\n",
+            argv0, argv0, argv0, argv0, argv0);
 }
 
 static int parse_u32(const char *s, uint32_t *out) {
@@ -95,9 +96,27 @@ int main(int argc, char **argv) {
         }
         return 0;
     }
+    if (!strcmp(cmd, "q8-k-activation-probe")) {
+        const char *inject = "none";
+        uint32_t values = 0;
+        int seen = 0;
+        for (int i = 2; i < argc; ++i) {
+            if (!strcmp(argv[i], "--values") && i + 1 < argc) {
+                if (!parse_u32(argv[++i], &values)) { fprintf(stderr, "q8-k-activation-probe failed: invalid --values\n"); return 2; }
+                seen = 1;
+            } else if (!strcmp(argv[i], "--inject") && i + 1 < argc) inject = argv[++i];
+            else { usage(argv[0]); return 2; }
+        }
+        if (!seen) { fprintf(stderr, "q8-k-activation-probe failed: invalid --values\n"); return 2; }
+        if (!qx_dump_q8_k_activation_probe_gpu(values, inject, stdout, err, sizeof(err))) {
+            fprintf(stderr, "q8-k-activation-probe failed: %s\n", err);
+            return 1;
+        }
+        return 0;
+    }
     if (!strcmp(cmd, "generate-model")) {
         const char *outp = NULL;
-        qxgen_spec sp = {48, 151936, 128, 1, 1, 1, 0};
+        qxgen_spec sp = {48, 151936, 128, 1, 1, 1, 0, 0};
         uint32_t seed = 1;
         for (int i = 2; i < argc; ++i) {
             if (!strcmp(argv[i], "--out") && i + 1 < argc) outp = argv[++i];
@@ -107,6 +126,7 @@ int main(int argc, char **argv) {
             else if (!strcmp(argv[i], "--seed") && i + 1 < argc) { if (!parse_u32(argv[++i], &seed)) { usage(argv[0]); return 2; } }
             else if (!strcmp(argv[i], "--no-embedding")) sp.with_embedding = 0;
             else if (!strcmp(argv[i], "--no-head")) sp.with_head = 0;
+            else if (!strcmp(argv[i], "--mix")) sp.mix = 1;
             else { usage(argv[0]); return 2; }
         }
         if (!outp) { usage(argv[0]); return 2; }

@@ -1,0 +1,63 @@
+"""The qxqxf CLI on the GPU: state-loop-probe with --dump-residuals in both activation
+modes, each per-layer dump checked against the oracle run on the same input tokens
+(the reference's Python tests drive its CLI the same way, through subprocess)."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import qxo
+import qxg
+from helpers import REL_L2, rel_l2
+
+pytestmark = pytest.mark.gpu
+EXE = os.path.join(os.path.dirname(qxg.__file__), "bin", "qxqxf")
+PHASES = ["input", "v-cur", "kqv-out", "ffn-inp", "ffn-moe-out", "output"]
+
+
+@pytest.mark.parametrize("act,tol", [("f32", REL_L2), ("q8_k_compat", 2e-3)])
+def test_state_loop_probe_dumps(tmp_path, act, tol):
+    """Each stage is replayed by the oracle on the CLI's own dumped input of that stage
+    (same-input chaining: the attention on "input" with a KV cache the oracle builds
+    from those inputs, the MoE on "ffn-inp"), so every stage meets its bar alone."""
+    model = tmp_path / "m.qxf"
+    qxg.generate_model(model, layers=2, vocab=1024, experts=16, seed=1234, mix=1)
+    dd = tmp_path / "dumps"
+    dd.mkdir()
+    r = subprocess.run([EXE, "state-loop-probe", "--in", str(model), "--prompt-token", "17", "--steps", "3", "--ctx", "8",
+                        "--kv", "int8", "--full-moe", "--final-head", "--top-n", "4", "--activation", act,
+                        "--dump-residuals", str(dd)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    j = json.loads(r.stdout)
+    assert j["activation_format"] == act
+    toks = [t["input_token"] for t in j["tokens"]]
+    m = qxo.Model(model, activation=act)
+    kv = qxo.KV(2, 8)
+    dump = lambda s, layer, ph: np.fromfile(dd / f"step-{s}-layer-{layer}-{ph}.f32", np.float32)
+    worst = {}
+    for s, tok in enumerate(toks):
+        assert rel_l2(dump(s, 0, "input"), m.embed(tok)) == 0.0
+        for layer in range(2):
+            x = dump(s, layer, "input")
+            a, kqv, vcur = qxo.attention_layer(m, layer, s, kv, x)
+            got = {"v-cur": (dump(s, layer, "v-cur"), vcur), "kqv-out": (dump(s, layer, "kqv-out"), kqv),
+                   "ffn-inp": (dump(s, layer, "ffn-inp"), x + a)}
+            y, moe, _, _ = m.moe_layer(layer, dump(s, layer, "ffn-inp"))
+            got["ffn-moe-out"] = (dump(s, layer, "ffn-moe-out"), moe)
+            got["output"] = (dump(s, layer, "output"), y)
+            for ph, (g, ref) in got.items():
+                e = rel_l2(g, ref)
+                worst[ph] = max(worst.get(ph, 0.0), e)
+                assert e <= tol, (act, s, layer, ph, e)
+            if layer == 0:
+                assert rel_l2(dump(s, 1, "input"), dump(s, 0, "output")) == 0.0
+        _, lg, ids, _ = m.final_head(dump(s, 1, "output"), 1024, 4)
+        e = rel_l2(np.fromfile(dd / f"step-{s}-logits.f32", np.float32), lg)
+        worst["logits"] = max(worst.get("logits", 0.0), e)
+        assert e <= REL_L2, (act, s, e)
+        if s + 1 < len(toks):
+            assert toks[s + 1] == int(ids[0]) or lg[toks[s + 1]] >= lg[ids[0]] - 1e-4
+    m.close()
+    print(act, {k: f"{v:.2e}" for k, v in worst.items()})

@@ -207,3 +207,21 @@ def test_q8k_failures_report_and_clear(ctx, models):
         assert b"unsupported activation" in err.value
     finally:
         ctx.set_activation("f32")
+
+
+def test_q8k_cli_probe_matches_reference(tmp_path):
+    """qxqxf q8-k-activation-probe prints the reference CLI's JSON for the same inputs."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(qxg.__file__), "bin", "qxqxf")
+    for key in ("none/256", "edge/512", "negative/4096"):   # one child process each, run one after another
+        want = GOLDEN["q8k_activation"][key]
+        inject, values = key.split("/")
+        r = subprocess.run([exe, "q8-k-activation-probe", "--values", values, "--inject", inject],
+                           capture_output=True, text=True, timeout=60)
+        assert r.returncode == 0, r.stderr
+        j = json.loads(r.stdout)
+        assert str(j["checksum"]) == want["checksum"] and j["quant_sum"] == want["quant_sum"], key
+        assert j["first_scale"] == want["first_scale"] and j["block_bytes"] == 292
+    r = subprocess.run([exe, "q8-k-activation-probe", "--values", "256", "--inject", "nan"], capture_output=True,
+                       text=True, timeout=60)
+    assert r.returncode == 1 and "NaN or Inf" in r.stderr

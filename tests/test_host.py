@@ -137,3 +137,17 @@ def test_cli_usage_and_failures(small, tmp_path):
                         "--out-dir", str(tmp_path)], capture_output=True, text=True)
     assert r.returncode == 1 and "non-finite" in r.stderr
     assert not os.path.exists(tmp_path / "logits.f32")
+
+
+def test_cli_q8k_probe_argument_errors():
+    """q8-k-activation-probe rejects bad arguments before any device work, with the
+    reference's messages and exit codes (src/qx_qxf_main.c:235-258, qx_format.c:4304-4314)."""
+    exe = os.path.join(PKG, "bin", "qxqxf")
+    r = subprocess.run([exe, "q8-k-activation-probe"], capture_output=True, text=True)
+    assert r.returncode == 2 and "invalid --values" in r.stderr
+    r = subprocess.run([exe, "q8-k-activation-probe", "--values", "x"], capture_output=True, text=True)
+    assert r.returncode == 2
+    r = subprocess.run([exe, "q8-k-activation-probe", "--values", "256", "--inject", "bogus"], capture_output=True, text=True)
+    assert r.returncode == 1 and "invalid Q8_K activation injection" in r.stderr
+    r = subprocess.run([exe, "q8-k-activation-probe", "--values", "8192"], capture_output=True, text=True)
+    assert r.returncode == 1 and "workspace is too small" in r.stderr
