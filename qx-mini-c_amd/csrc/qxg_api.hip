@@ -1131,8 +1131,8 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
                                std::sqrt(128.0), c->st, c->ctxv, nullptr);
             break;
         case 6:
-            hipLaunchKernelGGL(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, c->x, w.ffn_norm, w.router,
-                               c->experts, c->rlog);
+            hipLaunchKernelGGL(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, (const float *)c->x, w.ffn_norm,
+                               w.router, c->experts, c->rlog);
             break;
         }
     }

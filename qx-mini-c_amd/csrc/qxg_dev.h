@@ -764,13 +764,16 @@ DEV bool top8_rounds(K k0, K k1, MaxF wmax, uint32_t (&ids)[QXG_TOPK]) {
 // exact 64-bit keys of the doubles.  The weights p_r / sum_q p_q equal
 // e_r / sum_q e_q with e = exp(l - l_max), since the softmax denominator cancels.
 // ids[r] and w[r] are wave-uniform.
-DEV void wave_top8(double l0, double l1, int E, uint32_t (&ids)[QXG_TOPK], double (&w)[QXG_TOPK]) {
+DEV void wave_top8_ids(double l0, double l1, int E, uint32_t (&ids)[QXG_TOPK]) {
     const int lane = threadIdx.x & 63;
     const bool tie = top8_rounds<uint32_t>(lane < E ? fkey(l0) : 0u, lane + 64 < E ? fkey(l1) : 0u,
                                            [](uint32_t v) { return wave_max_u32(v); }, ids);
     if (tie)
         (void)top8_rounds<uint64_t>(lane < E ? dkey(l0) : 0ull, lane + 64 < E ? dkey(l1) : 0ull,
                                     [](uint64_t v) { return wave_max_u64(v); }, ids);
+}
+DEV void wave_top8_weights(double l0, double l1, const uint32_t (&ids)[QXG_TOPK], double (&w)[QXG_TOPK]) {
+    const int lane = threadIdx.x & 63;
     double lq = 0.0;   // lane q < 8: logit of pick q
 #pragma unroll
     for (int q = 0; q < QXG_TOPK; ++q) {
@@ -785,5 +788,9 @@ DEV void wave_top8(double l0, double l1, int E, uint32_t (&ids)[QXG_TOPK], doubl
     const double wq = eq / sel;
 #pragma unroll
     for (int q = 0; q < QXG_TOPK; ++q) w[q] = rdlaned(wq, q);
+}
+DEV void wave_top8(double l0, double l1, int E, uint32_t (&ids)[QXG_TOPK], double (&w)[QXG_TOPK]) {
+    wave_top8_ids(l0, l1, E, ids);
+    wave_top8_weights(l0, l1, ids, w);
 }
 }  // namespace

@@ -71,6 +71,17 @@ struct Tables {
     uint2 *sel8;   // sign byte (8 bits) -> v_perm selectors for 8 values
 };
 
+// Rows (units) per wave of the decode matvec kernels.  A workgroup's 4*RPW Q/K/V rows
+// must lie in one matrix (RPW | 128) and a wave's gate/up units in one expert (UPW | 768).
+#ifndef QXG_QKV_RPW
+#define QXG_QKV_RPW 2
+#endif
+#ifndef QXG_GU_UPW
+#define QXG_GU_UPW 3
+#endif
+#define QXG_OPROJ_RPW 2
+static_assert(128 % QXG_QKV_RPW == 0 && 768 % QXG_GU_UPW == 0, "row groups must not straddle a matrix or expert");
+
 // Persistent decode kernel (qxk_layers): per-layer weight pointers and launch arguments.
 #define QXG_PBLOCKS 256   // workgroups of the persistent kernel: one per CU of an MI355X
 

@@ -143,6 +143,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     const uint32_t pos = cur_pos(st), n = pos + 1;
     const uint64_t base = (uint64_t)layer * ctx;
     const uint32_t nst = pos < (uint32_t)ATT_STAGE ? pos : (uint32_t)ATT_STAGE;   // staged positions
+    QXG_MARK(4, 0);
     // cached rows first: 16 bytes of row (tid>>3) + 32*i, chunk tid&7, i < 4
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));   // register-promoted (a uint4 array is not)
     v4u kst[4], vst[4];
@@ -164,6 +165,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     const float kw0 = k_norm[lane], kw1 = k_norm[64 + lane], qw0 = q_norm[lane], qw1 = q_norm[64 + lane];
     const double c = T.rope_cos[pos * 64 + lane], s = T.rope_sin[pos * 64 + lane];
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
+    QXG_MARK(4, 1);
     head_norm_rope_wave(k0, k1, kw0, kw1, c, s);
     s_k[128 * wave + lane] = k0;
     s_k[128 * wave + 64 + lane] = k1;
@@ -182,8 +184,10 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
         const float b0 = isfinite(v0) ? fabsf(v0) : 0.0f, b1 = isfinite(v1) ? fabsf(v1) : 0.0f;
         va = fmaxf(b0, b1);
     }
+    QXG_MARK(4, 2);
     ka = block_max256(ka, red);
     va = block_max256(va, red);
+    QXG_MARK(4, 3);
     const float kscale = ka > 0.0f ? ka / 127.0f : 1.0f, vscale = va > 0.0f ? va / 127.0f : 1.0f;
     const uint64_t slot = base + pos;
     for (int i = tid; i < 512; i += 256) {
@@ -208,6 +212,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     }
     if ((uint32_t)tid < nst) { s_kss[tid] = kss; s_vss[tid] = vss; }
     __syncthreads();
+    QXG_MARK(4, 4);
     // position pos from the block's own row, [0, nst) from the LDS stage, the rest from the cache
     auto krow = [&](uint32_t t, uint4 (&k)[8], float &ksc) {
         if (t == pos) {
@@ -232,8 +237,11 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     };
     auto vsc = [&](uint32_t t) -> float { return t == pos ? s_scale[1] : t < nst ? s_vss[t] : vs[base + t]; };
     const double mx = attn_scores(s_q, s_qd, n, sqrt_hd, s_sc, redd, krow);
+    QXG_MARK(4, 5);
     attn_weights(n, mx, s_sc, redd, vsc);
+    QXG_MARK(4, 6);
     attn_context(n, s_sc, s_part, vrow, ctx_out + qh * 128);
+    QXG_MARK(4, 7);
 }
 
 // O projection 4096 -> 2048 on ctx (IQ4_XS, or Q5_K in the real checkpoint), then
@@ -316,16 +324,21 @@ extern "C" __global__ __launch_bounds__(256) void qxk_router(const float *x, con
     const int lane = threadIdx.x & 63, wave = wave_id();
     const uint32_t e = blockIdx.x * 4 + wave;
     if (e >= experts) return;
+    QXG_MARK(5, 0);
     float v[32], w[32], r[32];
     load32(router + (uint64_t)e * 2048 + 32 * lane, r);
     load32(x + 32 * lane, v);
     load32(norm_w + 32 * lane, w);
     rmsnorm32(v, w);
+    QXG_MARK(5, 1);
     double acc = 0.0;
 #pragma unroll
     for (int i = 0; i < 32; ++i) acc += (double)r[i] * (double)v[i];
+    QXG_ANCHOR(acc);
+    QXG_MARK(5, 2);
     acc = wave_total_d(acc);
     if (lane == 0) logits[e] = acc;
+    QXG_MARK(5, 3);
 }
 
 
@@ -376,9 +389,12 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     const int b = lane >> 3, ib = lane & 7;
     const int u0 = (blockIdx.x * 4 + wave) * UPW;   // grid covers exactly 8*768 units
     const int E = (int)experts;
+    __shared__ uint32_t s_ids[QXG_TOPK];
     QXG_MARK(1, 0);
-    // the router logits head the longest chain (logits -> top-8 -> weights): loaded first
-    const double l0 = lane < E ? logits[lane] : 0.0, l1 = lane + 64 < E ? logits[lane + 64] : 0.0;
+    // the router logits head the longest chain (logits -> top-8 -> weights): loaded first,
+    // by wave 0, which picks the experts for the whole workgroup
+    double l0 = 0.0, l1 = 0.0;
+    if (wave == 0) { l0 = lane < E ? logits[lane] : 0.0; l1 = lane + 64 < E ? logits[lane + 64] : 0.0; }
     DigIn<2048, true> din;
     digits_load(x, norm_w, din);
     const uint4 *G = FMT == 17 ? T.g2 : T.g2s;
@@ -390,23 +406,20 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
         tg[i].x = t.x; tg[i].y = t.y; tg[i].z = t.z; tg[i].w = t.w;
     }
     const uint2 t2 = SL[tid & (NS - 1)];
-    QXG_ANCHOR(l1);
-    QXG_MARK(1, 5);
     uint32_t ids[QXG_TOPK];
-    double wts[QXG_TOPK];
-    wave_top8(l0, l1, E, ids, wts);
-    QXG_MARK(1, 6);
+    if (wave == 0) {
+        QXG_ANCHOR(l1);
+        QXG_MARK(1, 5);
+        wave_top8_ids(l0, l1, E, ids);
 #pragma unroll
-    for (int q = 0; q < QXG_TOPK; ++q) ids[q] = ids[q] < experts ? ids[q] : 0u;   // never address past the experts
-    if (blockIdx.x == 0 && wave == 0) {   // the down kernel reads ids and renormalised weights from st
-#pragma unroll
-        for (int q = 0; q < QXG_TOPK; ++q)
-            if (lane == q) { st->moe_ids[q] = ids[q]; st->moe_w[q] = wts[q]; }
+        for (int q = 0; q < QXG_TOPK; ++q) {
+            ids[q] = ids[q] < experts ? ids[q] : 0u;   // never address past the experts
+            if (lane == q) s_ids[q] = ids[q];
+        }
+        QXG_MARK(1, 6);
     }
-    uint32_t e = ids[0];
-#pragma unroll
-    for (int q = 1; q < QXG_TOPK; ++q) if (u0 / QXG_FFN == q) e = ids[q];   // 4 | 768: one expert per wave
-    e = __builtin_amdgcn_readfirstlane(e);
+    __syncthreads();
+    const uint32_t e = __builtin_amdgcn_readfirstlane(s_ids[u0 / QXG_FFN]);   // UPW | 768: one expert per wave
     gu4 gq[UPW], uq[UPW];
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu) {
@@ -416,6 +429,13 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
         uq[uu] = gu_load<FMT>(uw, blk, ib);
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
+    if (blockIdx.x == 0 && wave == 0) {   // the down kernel reads ids and renormalised weights from st
+        double wts[QXG_TOPK];
+        wave_top8_weights(l0, l1, ids, wts);
+#pragma unroll
+        for (int q = 0; q < QXG_TOPK; ++q)
+            if (lane == q) { st->moe_ids[q] = ids[q]; st->moe_w[q] = wts[q]; }
+    }
     QXG_MARK(1, 7);
 #pragma unroll
     for (int i = 0; i < NG / 256; ++i) s_g2[tid + 256 * i] = make_uint4(tg[i].x, tg[i].y, tg[i].z, tg[i].w);
@@ -443,10 +463,13 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     }
     QXG_ANCHOR(pg[0]);
     QXG_MARK(1, 3);
-    float p[2 * UPW], o[2 * UPW];
+    constexpr int R = 2 * UPW <= 2 ? 2 : (2 * UPW + 3) / 4 * 4;   // rows_reduce takes 2 or a multiple of 4
+    float p[R], o[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) p[k] = 0.0f;
 #pragma unroll
     for (int k = 0; k < UPW; ++k) { p[k] = pg[k]; p[UPW + k] = pu[k]; }
-    rows_reduce<2 * UPW>(p, o, lane);
+    rows_reduce<R>(p, o, lane);
     float gv = 0.0f, uv = 0.0f;
 #pragma unroll
     for (int k = 0; k < UPW; ++k) if (lane == k) { gv = o[k]; uv = o[UPW + k]; }
@@ -881,7 +904,7 @@ extern "C" {
 // and of the activation mode (q8: q8_k_compat).
 void qxl_qkv(hipStream_t s, const float *x, const float *nw, const QTensor *q, const QTensor *k, const QTensor *v, float *qkv,
              DevState *st, bool q8, Timer t) {
-    constexpr int RPW = 4;
+    constexpr int RPW = QXG_QKV_RPW;
     QkvW w;
     const QTensor *m[3] = {q, k, v};
     for (int i = 0; i < 3; ++i) { w.qs[i] = m[i]->p0; w.p1[i] = m[i]->p1; w.p2[i] = m[i]->p2; w.type[i] = m[i]->type; }
@@ -890,7 +913,7 @@ void qxl_qkv(hipStream_t s, const float *x, const float *nw, const QTensor *q, c
     else qx_launch(qxk_qkv<RPW, false>, grid, dim3(256), 0, s, t, x, nw, w, qkv, st);
 }
 void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, float *dump, DevState *st, bool q8, Timer t) {
-    constexpr int RPW = 2;
+    constexpr int RPW = QXG_OPROJ_RPW;
     const dim3 grid(2048 / (4 * RPW));
     auto go = [&](auto kernel) { qx_launch(kernel, grid, dim3(256), 0, s, t, ctxv, o->p0, o->p1, o->p2, x, dump, st); };
     if (o->type == 13) q8 ? go(qxk_oproj<RPW, 13, true>) : go(qxk_oproj<RPW, 13, false>);
@@ -898,7 +921,7 @@ void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, flo
 }
 void qxl_gate_up(hipStream_t s, const float *x, const float *nw, const QTensor *g, const QTensor *u, Tables T,
                  const double *logits, uint32_t experts, DevState *st, float *h, bool q8, Timer t) {
-    constexpr int UPW = 4;
+    constexpr int UPW = QXG_GU_UPW;
     const GuW gw{g->p0, g->p1, g->p2, g->d}, uw{u->p0, u->p1, u->p2, u->d};
     const dim3 grid(QXG_TOPK * QXG_FFN / (4 * UPW));
     auto go = [&](auto kernel) { qx_launch(kernel, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h); };
