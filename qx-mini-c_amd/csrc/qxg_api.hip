@@ -590,8 +590,8 @@ void prefill_layer(qxg_ctx *c, uint32_t l, uint32_t T, uint32_t p0, float *moe_d
     qxp_launch_gemm(s, 1, g, B.P, 2048 / 128, mt, timer_for(c, 9));
     // MoE half: RMSNorm, router logits, top-8, grouping by expert, gate/up + SwiGLU, down, combine
     hipLaunchKernelGGL(qxp_norm, dim3((T + 3) / 4), dim3(256), 0, s, (const float *)B.X1, w.ffn_norm, T, B.XN);
-    hipLaunchKernelGGL(qxp_router, dim3((T + 7) / 8, (E + 31) / 32), dim3(256), 0, s, (const float *)B.XN, w.router, T,
-                       E, B.lg);
+    qx_launch(qxp_router, dim3((T + 15) / 16, (E + 15) / 16), dim3(512), 0, s, timer_for(c, 12), (const float *)B.XN,
+              w.router, T, E, B.lg);
     hipLaunchKernelGGL(qxp_route, dim3((T + 3) / 4), dim3(256), 0, s, (const double *)B.lg, T, E, B.ids, B.w);
     hipLaunchKernelGGL(qxp_group, dim3(1), dim3(1024), 0, s, (const uint32_t *)B.ids, T, E, PF_EXPERT_MT, B.slot_token,
                        B.tok_slot, B.mgroups, B.meta);

@@ -513,30 +513,44 @@ extern "C" __global__ __launch_bounds__(256) void qxp_attn(const float *qr, cons
     attn_context(n, s_sc, s_part, vrow, ctx_out + (uint64_t)t * 4096 + qh * 128);
 }
 
-// Router logits: lane (token, expert) forms logit[t][e] = sum_i (double)W[e][i] *
-// (double)xn[t][i] (src/qx_format.c:5254-5264: the same double products) as four
-// interleaved partial sums over i = 4j+c (c < 4), each in ascending order, added as
-// (s0 + s1) + (s2 + s3): four independent chains of additions instead of one.  A wave
-// covers 8 tokens x 8 experts, so each load instruction touches 8 distinct rows of x
-// and of W.
-extern "C" __global__ __launch_bounds__(256) void qxp_router(const float *xn, const float *router, uint32_t T,
+// Router logits on the FP64 matrix cores: logit[t][e] = sum_i (double)W[e][i] *
+// (double)xn[t][i] (src/qx_format.c:5254-5264: the same exact double products, summed in
+// another order, within ~1e-15 relative of the reference's sequential sum; equal router
+// rows still give equal logits).  A workgroup owns a 16 x 16 (token x expert) tile; its 8
+// waves split K = 2048 in eighths and lane group g = lane / 16 of a wave feeds k-slot g
+// of v_mfma_f64_16x16x4 with 64 consecutive k of the wave's 256.  The 8 partial tiles
+// are added in LDS in a fixed order.
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+extern "C" __global__ __launch_bounds__(512) void qxp_router(const float *xn, const float *router, uint32_t T,
                                                              uint32_t experts, double *logits) {
-    const int lane = threadIdx.x & 63, wave = wave_id();
-    const uint32_t t = blockIdx.x * 8 + (lane >> 3);
-    const uint32_t e = blockIdx.y * 32 + wave * 8 + (lane & 7);
-    const bool ok = t < T && e < experts;
-    const float4 *x = reinterpret_cast<const float4 *>(xn + (uint64_t)(ok ? t : 0) * 2048);
-    const float4 *w = reinterpret_cast<const float4 *>(router + (uint64_t)(ok ? e : 0) * 2048);
-    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-#pragma unroll 8
-    for (int k = 0; k < 512; ++k) {
-        const float4 a = x[k], b = w[k];
-        s0 += (double)b.x * (double)a.x;
-        s1 += (double)b.y * (double)a.y;
-        s2 += (double)b.z * (double)a.z;
-        s3 += (double)b.w * (double)a.w;
+    __shared__ double part[8][16][17];
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int i = lane & 15, g = lane >> 4;
+    const uint32_t t = blockIdx.x * 16 + i;   // < 512: xn holds QXP_MAX rows
+    const uint32_t e = blockIdx.y * 16 + i, er = e < experts ? e : 0u;
+    const float4 *xa = reinterpret_cast<const float4 *>(xn + (uint64_t)t * 2048 + wave * 256 + g * 64);
+    const float4 *wb = reinterpret_cast<const float4 *>(router + (uint64_t)er * 2048 + wave * 256 + g * 64);
+    f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll 4
+    for (int j = 0; j < 16; ++j) {
+        const float4 a = xa[j], b = wb[j];
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.x, (double)b.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.y, (double)b.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.z, (double)b.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.w, (double)b.w, acc, 0, 0, 0);
     }
-    if (ok) logits[(uint64_t)t * 128 + e] = (s0 + s1) + (s2 + s3);
+    // result r of lane l: token row l / 16 + 4 * r, expert column l % 16 (the f64 16x16
+    // layout, unlike the f32 ones' 4 * (l / 16) + r)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) part[wave][g + 4 * r][i] = acc[r];
+    __syncthreads();
+    if (tid < 256) {
+        const int row = tid >> 4, col = tid & 15;
+        const double v = ((part[0][row][col] + part[1][row][col]) + (part[2][row][col] + part[3][row][col])) +
+                         ((part[4][row][col] + part[5][row][col]) + (part[6][row][col] + part[7][row][col]));
+        const uint32_t tt = blockIdx.x * 16 + row, ee = blockIdx.y * 16 + col;
+        if (tt < T && ee < experts) logits[(uint64_t)tt * 128 + ee] = v;
+    }
 }
 
 // Top-8 experts and renormalised weights per token (wave per token; the decode path's
