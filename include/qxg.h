@@ -197,7 +197,7 @@ uint64_t qxg_device_bytes(const qxg_ctx *ctx);
 /* In-situ timing: while enabled, qxg_generate / qxg_decode_token record a HIP
  * event pair around every launch of kernel `which` (numbering of
  * qxg_time_kernel, plus 7 the persistent layer kernel and, for qxg_prefill, 8 Q/K/V,
- * 9 O, 10 gate/up and 11 down GEMMs, 12 router logits; -1 disables).
+ * 9 O, 10 gate/up and 11 down GEMMs, 12 router logits, 13 attention; -1 disables).
  * qxg_profile_result sums the pairs. */
 int qxg_profile_kernel(qxg_ctx *ctx, int which);
 int qxg_profile_result(qxg_ctx *ctx, uint32_t *launches, double *total_ms);

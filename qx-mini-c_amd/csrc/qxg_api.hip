@@ -39,7 +39,7 @@ __global__ void qxp_norm(const float *, const float *, uint32_t, float *);
 __global__ void qxp_qk(const float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
                        uint32_t, uint32_t, uint32_t, float *);
 __global__ void qxp_attn(const float *, const int8_t *, const int8_t *, const float *, const float *, uint32_t, uint32_t,
-                         uint32_t, double, float *);
+                         uint32_t, uint32_t, float *);
 __global__ void qxp_router(const float *, const float *, uint32_t, uint32_t, double *);
 __global__ void qxp_route(const double *, uint32_t, uint32_t, uint32_t *, double *);
 __global__ void qxp_group(const uint32_t *, uint32_t, uint32_t, uint32_t, int32_t *, uint32_t *, uint32_t *, uint32_t *);
@@ -579,9 +579,9 @@ void prefill_layer(qxg_ctx *c, uint32_t l, uint32_t T, uint32_t p0, float *moe_d
     qxp_launch_gemm(s, 0, g, B.P, 5120 / 128, mt, timer_for(c, 8));
     hipLaunchKernelGGL(qxp_qk, dim3(T), dim3(256), 0, s, (const float *)B.QKV, w.q_norm, w.k_norm, c->T, c->kc, c->vc,
                        c->ks, c->vs, l, c->kv_ctx, p0, B.QR);
-    hipLaunchKernelGGL(qxp_attn, dim3(32, T), dim3(256), (uint32_t)((p0 + T) * sizeof(double)), s, (const float *)B.QR,
-                       (const int8_t *)c->kc, (const int8_t *)c->vc, (const float *)c->ks, (const float *)c->vs, l,
-                       c->kv_ctx, p0, std::sqrt(128.0), B.CTX);
+    qx_launch(qxp_attn, dim3(4, (T + 3) / 4), dim3(256), 0, s, timer_for(c, 13), (const float *)B.QR,
+              (const int8_t *)c->kc, (const int8_t *)c->vc, (const float *)c->ks, (const float *)c->vs, l, c->kv_ctx, p0, T,
+              B.CTX);
     qxp_launch_pack(s, 4096, B.CTX, nullptr, nullptr, mt * 32, T, B.apk, B.rscale);
     g = PfGemm{};
     g.w[0] = pf_mat(w.wo); g.w_start[1] = none; g.w_start[2] = none;

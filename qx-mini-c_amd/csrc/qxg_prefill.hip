@@ -482,35 +482,232 @@ extern "C" __global__ __launch_bounds__(256) void qxp_qk(const float *qkv, const
     if (tid == 0) { ks[slot] = kscale; vs[slot] = vscale; }
 }
 
-// Causal GQA attention of token t (blockIdx.y) and q head blockIdx.x over cached
-// positions 0..p0+t (qx_rope_gqa_attention_partial, src/qx_format.c:5051-5196), with the
-// decode kernel's score, softmax and context code.
-extern "C" __global__ __launch_bounds__(256) void qxp_attn(const float *qr, const int8_t *kc, const int8_t *vc,
-        const float *ks, const float *vs, uint32_t layer, uint32_t ctx, uint32_t p0, double sqrt_hd, float *ctx_out) {
-    extern __shared__ double s_sc[];
-    __shared__ __align__(16) float s_q[128];
-    __shared__ __align__(16) uint32_t s_qd[4 * DIG_STRIDE];
-    __shared__ double redd[4];
-    __shared__ float s_part[16][132];
-    const int tid = threadIdx.x;
-    const int qh = blockIdx.x, kvh = qh >> 3;
-    const uint32_t t = blockIdx.y, n = p0 + t + 1;
-    const uint64_t base = (uint64_t)layer * ctx;
-    if (tid < 128) s_q[tid] = qr[(uint64_t)t * 4096 + 128 * qh + tid];
-    __syncthreads();
-    auto krow = [&](uint32_t p, uint4 (&k)[8], float &ksc) {
-        const uint4 *q = reinterpret_cast<const uint4 *>(kc + (base + p) * 512 + kvh * 128);
+// Causal GQA attention of the chunk on the matrix cores (qx_rope_gqa_attention_partial,
+// src/qx_format.c:5051-5196, for every token of the chunk at once).  A workgroup takes
+// one KV head and 4 consecutive tokens: the 8 q heads of the KV head x 4 tokens are the
+// 32 columns of v_mfma_f32_32x32x16_f16 (column c: head c/4, token c%4).  Its 4 waves
+// take the 32-position chunks ci = wave, wave+4, ... of positions 0..p0+t and keep, per
+// column, a running maximum, denominator and context (online softmax; the reference
+// normalises with the global maximum, the same quantity up to rounding).  Per chunk:
+//   scores  S^T[pos][col] = K8[pos][:] . q[col][:]: A = the chunk's INT8 K codes
+//           (exact in fp16), B = q split hi + lo in fp16 after a power-of-two row
+//           scale (max |q| in [2^13, 2^14)); f32 accumulation; times ks[pos] /
+//           sqrt(128) and the row scale; positions past the token masked;
+//   weights p = exp(s - m) (f32), pv = p * vs[pos], split hi + lo after a power-of-two
+//           scale per column and chunk;
+//   context C[dim][col] += V8^T[dim][pos] . pv[pos][col] (A = V codes from a transposed
+//           LDS copy of the chunk), rescaled by exp(m_old - m_new) per column.
+// The result registers of the score product are exactly the k layout the context
+// product's B operand needs (lane l: column l%32, positions 8(r/4) + 4(l/32) + r%4 of
+// register r), so the weights never leave the lane.  The waves' states are merged in
+// LDS at the end and the context is divided by the denominator.
+namespace {
+constexpr int PA_TT = 4;   // tokens per workgroup
+
+DEV uint4 i8x8_to_f16(uint2 v) {   // 8 int8 -> 8 exact fp16 (bias 0x64 trick: 1024 + (b ^ 0x80) - 1152)
+    const h2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t x = v.x ^ 0x80808080u, y = v.y ^ 0x80808080u;
+    const uint32_t c = 0x64646464u;
+    auto cv = [&](uint32_t w) { return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, w) - bias); };
+    return make_uint4(cv(perm(c, x, 0x04010400u)), cv(perm(c, x, 0x04030402u)), cv(perm(c, y, 0x04010400u)),
+                      cv(perm(c, y, 0x04030402u)));
+}
+DEV void split8(const float (&v)[8], float sc, uint4 &hi, uint4 &lo) {   // v * sc = hi + lo (+ 2^-22 rel)
+    uint32_t h[4], l[4];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) k[c] = q[c];
-        ksc = ks[base + p];
-    };
-    auto vrow = [&](uint32_t p, int dg) -> uint2 {
-        return *reinterpret_cast<const uint2 *>(vc + (base + p) * 512 + kvh * 128 + 8 * dg);
-    };
-    auto vsc = [&](uint32_t p) -> float { return vs[base + p]; };
-    const double mx = attn_scores(s_q, s_qd, n, sqrt_hd, s_sc, redd, krow);
-    attn_weights(n, mx, s_sc, redd, vsc);
-    attn_context(n, s_sc, s_part, vrow, ctx_out + (uint64_t)t * 4096 + qh * 128);
+    for (int i = 0; i < 4; ++i) {
+        const float a = v[2 * i] * sc, b = v[2 * i + 1] * sc;
+        const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+        const _Float16 la = (_Float16)(a - (float)ha), lb = (_Float16)(b - (float)hb);
+        const h2v hh = {ha, hb}, ll = {la, lb};
+        h[i] = __builtin_bit_cast(uint32_t, hh);
+        l[i] = __builtin_bit_cast(uint32_t, ll);
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+DEV float pow2_scale(float mx) {   // 2^(14-e) with mx = m * 2^e, m in [0.5, 1): mx * scale in [2^13, 2^14)
+    int e = 0;
+    if (mx > 0.0f && isfinite(mx)) (void)frexpf(mx, &e);
+    return mx > 0.0f && isfinite(mx) ? ldexpf(1.0f, 14 - e) : 1.0f;
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void qxp_attn(const float *qr, const int8_t *kc, const int8_t *vc,
+        const float *ks, const float *vs, uint32_t layer, uint32_t ctx, uint32_t p0, uint32_t T, float *ctx_out) {
+    __shared__ uint32_t s_vt[4][128 * 9];   // per wave: V^T of its chunk, rows of 36 bytes (32 positions)
+    __shared__ float s_ks[4][32], s_vs[4][32];
+    __shared__ float s_acc[2][32][129];
+    __shared__ float s_m[2][32], s_den[2][32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int col = lane & 31, h = lane >> 5;
+    const uint32_t kh = blockIdx.x, t0 = blockIdx.y * PA_TT;
+    const uint32_t tt = t0 + (col & 3), qh = kh * 8 + (col >> 2);
+    const bool tok_ok = tt < T;
+    const uint32_t limit = p0 + (tok_ok ? tt : 0);              // last position of the column's token
+    const uint32_t last_t = min(t0 + PA_TT, T) - 1;
+    const uint32_t npos = p0 + last_t + 1;                      // positions the workgroup needs
+    const uint64_t base = (uint64_t)layer * ctx;
+    // q fragments: k-step s holds dims 16s + 8h + j of the column's q row
+    float qv[8][8];
+    bool fin = true;
+    float qmx = 0.0f;
+    const float *qrow = qr + (uint64_t)(tok_ok ? tt : 0) * 4096 + qh * 128 + 8 * h;
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+        const float4 a = *reinterpret_cast<const float4 *>(qrow + 16 * s8);
+        const float4 b = *reinterpret_cast<const float4 *>(qrow + 16 * s8 + 4);
+        qv[s8][0] = a.x; qv[s8][1] = a.y; qv[s8][2] = a.z; qv[s8][3] = a.w;
+        qv[s8][4] = b.x; qv[s8][5] = b.y; qv[s8][6] = b.z; qv[s8][7] = b.w;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { fin = fin && isfinite(qv[s8][j]); qmx = fmaxf(qmx, fabsf(qv[s8][j])); }
+    }
+    fin = fin && (__shfl_xor((int)fin, 32) != 0);
+    qmx = fmaxf(qmx, __shfl_xor(qmx, 32));
+    // a non-finite q makes every score non-finite, which the reference stores as 0
+    const bool qz = !fin || !tok_ok;
+    const float qsc = pow2_scale(qz ? 0.0f : qmx);
+    uint4 qhi[8], qlo[8];
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+        if (qz) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qv[s8][j] = 0.0f;
+        }
+        split8(qv[s8], qsc, qhi[s8], qlo[s8]);
+    }
+    const float sfac = (float)(1.0 / ((double)qsc * sqrt(128.0)));   // exact power of two over sqrt(128)
+    float m_run = -INFINITY, den = 0.0f;
+    f16x acc[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) acc[d] = zero16();
+    const uint32_t nchunk = (npos + 31) / 32;
+    uint32_t *vt = s_vt[wave];
+#pragma unroll 1
+    for (uint32_t ci = wave; ci < nchunk; ci += 4) {
+        const uint32_t pb = ci * 32;
+        // K fragments of position pb + col (clamped inside the workgroup's range)
+        const uint32_t pk = min(pb + col, npos - 1);
+        const int8_t *krow = kc + (base + pk) * 512 + kh * 128 + 8 * h;
+        uint2 kq[8];
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) kq[s8] = *reinterpret_cast<const uint2 *>(krow + 16 * s8);
+        if (lane < 32) {
+            const uint32_t pp = min(pb + lane, npos - 1);
+            s_ks[wave][lane] = ks[base + pp];
+            s_vs[wave][lane] = vs[base + pp];
+        }
+        // V^T of the chunk: lane takes 4 blocks of 4 positions x 4 dims and transposes them
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int bq = lane + 64 * i, pq = bq & 7, dq = bq >> 3;
+            uint32_t w[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t pp = min(pb + 4 * pq + r, npos - 1);
+                w[r] = *reinterpret_cast<const uint32_t *>(vc + (base + pp) * 512 + kh * 128 + 4 * dq);
+            }
+            const uint32_t a0 = perm(w[1], w[0], 0x05010400u), a1 = perm(w[3], w[2], 0x05010400u);
+            const uint32_t a2 = perm(w[1], w[0], 0x07030602u), a3 = perm(w[3], w[2], 0x07030602u);
+            vt[(4 * dq + 0) * 9 + pq] = perm(a1, a0, 0x05040100u);
+            vt[(4 * dq + 1) * 9 + pq] = perm(a1, a0, 0x07060302u);
+            vt[(4 * dq + 2) * 9 + pq] = perm(a3, a2, 0x05040100u);
+            vt[(4 * dq + 3) * 9 + pq] = perm(a3, a2, 0x07060302u);
+        }
+        // scores: S^T = K8 . q
+        f16x sacc = zero16();
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) {
+            const uint4 kf = i8x8_to_f16(kq[s8]);
+            sacc = mfma(kf, qhi[s8], sacc);
+            sacc = mfma(kf, qlo[s8], sacc);
+        }
+        // register r: position pb + 8(r/4) + 4h + r%4
+        float sc[16], cmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t pr = 8 * (r >> 2) + 4 * h + (r & 3), p = pb + pr;
+            float v = sacc[r] * (s_ks[wave][pr] * sfac);
+            v = isfinite(v) ? v : 0.0f;
+            sc[r] = p <= limit ? v : -INFINITY;
+            cmax = fmaxf(cmax, sc[r]);
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float m_new = fmaxf(m_run, cmax);
+        const float alpha = m_new == -INFINITY ? 1.0f : __expf(m_run - m_new);
+        float pv[16], psum = 0.0f, pmx = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t pr = 8 * (r >> 2) + 4 * h + (r & 3);
+            const float e = sc[r] == -INFINITY ? 0.0f : __expf(sc[r] - m_new);
+            psum += e;
+            pv[r] = e * s_vs[wave][pr];
+            pmx = fmaxf(pmx, pv[r]);
+        }
+        pmx = fmaxf(pmx, __shfl_xor(pmx, 32));
+        den = den * alpha + psum;
+        m_run = m_new;
+        const float psc = pow2_scale(pmx), pinv = 1.0f / psc;   // powers of two: exact
+        uint4 phi[2], plo[2];
+        {
+            float a8[8], b8[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) { a8[j] = pv[j]; b8[j] = pv[8 + j]; }
+            split8(a8, psc, phi[0], plo[0]);
+            split8(b8, psc, phi[1], plo[1]);
+        }
+        // context: per 32-dim tile, C[dim][col] = V8^T . pv, merged into the running sums
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            f16x cacc = zero16();
+            const uint32_t *row = vt + (32 * d + col) * 9;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const uint4 vf = i8x8_to_f16(make_uint2(row[4 * s2 + h], row[4 * s2 + 2 + h]));
+                cacc = mfma(vf, phi[s2], cacc);
+                cacc = mfma(vf, plo[s2], cacc);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[d][r] = fmaf(acc[d][r], alpha, cacc[r] * pinv);
+        }
+    }
+    // merge the 4 waves' (max, denominator, context) per column: 2+3 into 0+1, then 1 into 0
+    den += __shfl_xor(den, 32);
+#pragma unroll 1
+    for (int round = 0; round < 2; ++round) {
+        const int nw = round == 0 ? 2 : 1;   // waves [nw, 2nw) hand over to [0, nw)
+        if (wave >= nw && wave < 2 * nw) {
+            const int slot = wave - nw;
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s_acc[slot][col][32 * d + 8 * (r >> 2) + 4 * h + (r & 3)] = acc[d][r];
+            if (h == 0) { s_m[slot][col] = m_run; s_den[slot][col] = den; }
+        }
+        __syncthreads();
+        if (wave < nw) {
+            const float mo = s_m[wave][col], dn = s_den[wave][col];
+            const float m_new = fmaxf(m_run, mo);
+            const float fa = m_run == -INFINITY ? 0.0f : __expf(m_run - m_new);
+            const float fb = mo == -INFINITY ? 0.0f : __expf(mo - m_new);
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    acc[d][r] = acc[d][r] * fa + s_acc[wave][col][32 * d + 8 * (r >> 2) + 4 * h + (r & 3)] * fb;
+            den = den * fa + dn * fb;
+            m_run = m_new;
+        }
+        __syncthreads();
+    }
+    if (wave == 0 && tok_ok) {
+        const float inv = 1.0f / den;
+        float *out = ctx_out + (uint64_t)tt * 4096 + qh * 128;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) out[32 * d + 8 * (r >> 2) + 4 * h + (r & 3)] = acc[d][r] * inv;
+    }
 }
 
 // Router logits on the FP64 matrix cores: logit[t][e] = sum_i (double)W[e][i] *

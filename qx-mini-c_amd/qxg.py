@@ -303,4 +303,4 @@ class Context:
 
 
 KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "oproj": 3, "head": 4, "attention": 5, "router": 6, "layers": 7,
-           "pf_qkv": 8, "pf_oproj": 9, "pf_gate_up": 10, "pf_down": 11, "pf_router": 12}
+           "pf_qkv": 8, "pf_oproj": 9, "pf_gate_up": 10, "pf_down": 11, "pf_router": 12, "pf_attn": 13}
