@@ -581,8 +581,9 @@ DEV void head_norm_rope_wave(float &x0, float &x1, float w0, float w1, double c,
 // (22 significant bits, as the projections' activations), so the score of a position is
 // exact int32 v_dot4 sums of those digits with the position's INT8 K codes:
 //     score = ks * sum_g s_g * (2^16 H_g.k + 2^8 M_g.k + L_g.k) / sqrt(hd),
-// non-finite (or a non-finite q) -> 0.  One lane per position; krow(t, k[8], ks) fetches
-// position t's 128 K bytes and scale.  s_sc[t] <- score; returns the block maximum.
+// non-finite (or a non-finite q) -> 0.  Four lanes per position; krow(t, g, k[2], ks)
+// fetches the 32 K bytes of group g of position t and the scale.  s_sc[t] <- score;
+// returns the block maximum.
 template <typename KF>
 DEV double attn_scores(const float *s_q, uint32_t *s_qd, uint32_t n, double sqrt_hd, double *s_sc, double *redd,
                        KF krow) {
@@ -608,31 +609,30 @@ DEV double attn_scores(const float *s_q, uint32_t *s_qd, uint32_t n, double sqrt
         if (q == 0) d[24] = __float_as_uint(sc);
     }
     const bool qok = __syncthreads_or(!fin) == 0;
+    // a quad per position: lane q4 of the quad takes the 32-dim group q4, the four group
+    // sums are added as (g0 + g1) + (g2 + g3) in double
+    const int q4 = tid & 3;
+    Dig d;
+    load_dig(s_qd, q4, d);
     double mx = -1.0e300;
-    for (uint32_t t = tid; t < n; t += 256) {
-        uint4 k[8];
+    for (uint32_t t = tid >> 2; t < n; t += 64) {
+        uint4 k[2];
         float ksc;
-        krow(t, k, ksc);
-        asm volatile("" ::: "memory");   // the digits are re-read from LDS per position
-        double acc = 0.0;
+        krow(t, q4, k, ksc);
+        const uint32_t kw[8] = {k[0].x, k[0].y, k[0].z, k[0].w, k[1].x, k[1].y, k[1].z, k[1].w};
+        int aH = 0, aM = 0, aL = 0;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            Dig d;
-            load_dig(s_qd, g, d);
-            const uint32_t kw[8] = {k[2 * g].x, k[2 * g].y, k[2 * g].z, k[2 * g].w,
-                                    k[2 * g + 1].x, k[2 * g + 1].y, k[2 * g + 1].z, k[2 * g + 1].w};
-            int aH = 0, aM = 0, aL = 0;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                aH = sdot4(kw[i], d.h[i], aH);
-                aM = sdot4(kw[i], d.m[i], aM);
-                aL = sdot4(kw[i], d.l[i], aL);
-            }
-            acc += (double)(combine(aH, aM, aL) * d.s);
+        for (int i = 0; i < 8; ++i) {
+            aH = sdot4(kw[i], d.h[i], aH);
+            aM = sdot4(kw[i], d.m[i], aM);
+            aL = sdot4(kw[i], d.l[i], aL);
         }
+        double acc = (double)(combine(aH, aM, aL) * d.s);
+        acc += dppd<DPP_XOR1>(acc);   // the quad shares t, so its lanes are active together
+        acc += dppd<DPP_XOR2>(acc);
         double sc = qok ? acc * (double)ksc / sqrt_hd : 0.0;
         if (!isfinite(sc)) sc = 0.0;
-        s_sc[t] = sc;
+        if (q4 == 0) s_sc[t] = sc;
         mx = fmax(mx, sc);
     }
     mx = wave_max_d(mx);

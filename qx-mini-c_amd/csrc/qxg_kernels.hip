@@ -214,19 +214,19 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     __syncthreads();
     QXG_MARK(4, 4);
     // position pos from the block's own row, [0, nst) from the LDS stage, the rest from the cache
-    auto krow = [&](uint32_t t, uint4 (&k)[8], float &ksc) {
+    auto krow = [&](uint32_t t, int g, uint4 (&k)[2], float &ksc) {
         if (t == pos) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) k[c] = reinterpret_cast<const uint4 *>(s_k8)[c];
+            k[0] = reinterpret_cast<const uint4 *>(s_k8)[2 * g];
+            k[1] = reinterpret_cast<const uint4 *>(s_k8)[2 * g + 1];
             ksc = s_scale[0];
         } else if (t < nst) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) k[c] = s_kst[t * 8 + c];
+            k[0] = s_kst[t * 8 + 2 * g];
+            k[1] = s_kst[t * 8 + 2 * g + 1];
             ksc = s_kss[t];
         } else {
             const uint4 *p = reinterpret_cast<const uint4 *>(kc + (base + t) * 512 + kvh * 128);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) k[c] = p[c];
+            k[0] = p[2 * g];
+            k[1] = p[2 * g + 1];
             ksc = ks[base + t];
         }
     };
