@@ -45,8 +45,8 @@ int qxg_upload_tensor(qxg_ctx *ctx, const char *name, uint32_t ggml_type, const 
  * buffers.  need_head / need_embedding select whether output.* / token_embd.* must
  * be present.  Per layer: attn_q/k/v/output IQ4_XS or Q5_K; gate/up experts IQ2_XS
  * or IQ2_S (both the same); down experts IQ3_XXS, IQ4_XS or IQ3_S.  A model using any
- * format beyond IQ4_XS / IQ2_XS / IQ3_XXS decodes one kernel per phase and cannot
- * use qxg_prefill / qxg_prefill_layer. */
+ * format beyond IQ4_XS / IQ2_XS / IQ3_XXS decodes one kernel per phase, and
+ * qxg_prefill / qxg_prefill_layer run it token by token through the decode kernels. */
 int qxg_bind_model(qxg_ctx *ctx, uint32_t layers, int need_embedding, int need_head, char *err, uint64_t err_len);
 
 /* Persistent INT8 KV cache [layers][ctx_tokens][512] for K and V plus one f32 scale
@@ -144,7 +144,10 @@ int qxg_final_head(qxg_ctx *ctx, const float *residual, float *norm_out, float *
  * the last token.  Stands in for the reference's prompt steps, which run one token at a
  * time through the decode step with the head only on the last prompt token
  * (src/qx_format.c:6250-6547, sampling_step at 6253).  Chunks of 512 tokens run in
- * order.  residual_out (may be NULL): n*2048 floats, each token's residual after the
+ * order.  Models with formats beyond IQ4_XS / IQ2_XS / IQ3_XXS, and the q8_k_compat
+ * mode, take those token steps on the device instead (the decode kernels, one token at
+ * a time: the result equals qxg_decode_token over the prompt).
+ * residual_out (may be NULL): n*2048 floats, each token's residual after the
  * last layer.  logits / top_* as in qxg_decode_token.  elapsed_ms: device time of the
  * whole call (HIP events on the context stream). */
 int qxg_prefill(qxg_ctx *ctx, const uint32_t *tokens, uint32_t n, uint32_t position0, int run_head,
@@ -173,8 +176,8 @@ int qxg_set_layer_path(qxg_ctx *ctx, int persistent);
  * q8_k_compat the matvec inputs are quantized to Q8_K blocks (256 values, one f32
  * scale) and each weight type is dotted in integers; a non-finite activation or
  * expert row makes the call fail with the reference's message.  Runs one kernel per
- * phase (whatever qxg_set_layer_path says); qxg_prefill returns an error in this
- * mode.  Drops the recorded decode graph. */
+ * phase (whatever qxg_set_layer_path says); qxg_prefill runs token by token through
+ * the decode kernels in this mode.  Drops the recorded decode graph. */
 int qxg_set_activation(qxg_ctx *ctx, uint32_t activation_format, char *err, uint64_t err_len);
 
 /* Same-input seam of the Q8_K quantizer the q8_k_compat kernels use: n values (a

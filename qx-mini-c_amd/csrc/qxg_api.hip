@@ -505,15 +505,12 @@ uint16_t f16_int(int v) {
     return (uint16_t)(sign | ((uint32_t)(e + 15) << 10) | mant);
 }
 
+// The batched GEMM path decodes the benchmark mix in the f32 activation mode; other
+// models and q8_k_compat prefill token by token through the decode kernels, which is
+// how the reference prefills every prompt.
+bool batched_prefill(const qxg_ctx *c) { return c->base_mix && !c->q8; }
+
 bool prefill_ready(qxg_ctx *c, char *err, uint64_t n) {
-    if (c->q8) {
-        set_err(err, n, "prefill computes in the f32 activation mode only (decode the prompt token by token)");
-        return false;
-    }
-    if (!c->base_mix) {
-        set_err(err, n, "prefill supports the IQ4_XS / IQ2_XS / IQ3_XXS mix only (decode the prompt token by token)");
-        return false;
-    }
     auto &B = c->pf;
     if (B.ready) return true;
     auto alloc = [&](void **p, uint64_t bytes) {
@@ -612,6 +609,49 @@ void prefill_layer(qxg_ctx *c, uint32_t l, uint32_t T, uint32_t p0, float *moe_d
     hipLaunchKernelGGL(qxp_combine, dim3(T), dim3(256), 0, s, (const float *)B.X1, (const float *)B.Y,
                        (const uint32_t *)B.tok_slot, (const double *)B.w, B.X, moe_dump);
 }
+// Token-step prefill: one decode step per prompt token (embedding, every layer), the head
+// on the last when run_head; residual_out row i is token i's final residual.
+int prefill_steps(qxg_ctx *c, const uint32_t *tokens, uint32_t n, uint32_t position0, int run_head,
+                  float *residual_out, uint32_t top_n, char *err, uint64_t err_len) {
+    if (!hip_ok(hipMemcpy(c->tokens, tokens, 4ull * n, hipMemcpyHostToDevice), err, err_len, "tokens")) return 0;
+    (void)hipEventRecord(c->e0, c->s);
+    for (uint32_t i = 0; i < n; ++i) {
+        write_state(c, position0, i, run_head ? n : n + 1, 0);   // steps before n_prompt - 1 skip the head
+        hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
+        for (uint32_t l = 0; l < c->layers; ++l) {
+            launch_attention(c, l, c->x, nullptr, nullptr);
+            launch_moe(c, l, c->x, nullptr);
+        }
+        if (residual_out &&
+            !hip_ok(hipMemcpyAsync(residual_out + 2048ull * i, c->x, 2048 * 4, hipMemcpyDeviceToHost, c->s), err, err_len, "read"))
+            return 0;
+        if (i + 1 == n && run_head) launch_head(c, top_n, nullptr);
+    }
+    (void)hipEventRecord(c->e1, c->s);
+    return 1;
+}
+
+// Waits for the prefill's work and reads the head's outputs of the last token.
+int prefill_finish(qxg_ctx *c, int run_head, float *logits, uint32_t top_n, uint32_t *top_ids, double *top_logits,
+                   float *elapsed_ms, char *err, uint64_t err_len) {
+    if (!finish(c, err, err_len)) return 0;
+    if (elapsed_ms) (void)hipEventElapsedTime(elapsed_ms, c->e0, c->e1);
+    if (!run_head) return 1;
+    DevState h;
+    if (!read_state(c, h, err, err_len)) return 0;
+    if (logits && !hip_ok(hipMemcpy(logits, c->logits, (uint64_t)c->vocab * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    float tv[QXG_MAX_TOPN];
+    uint32_t ti[QXG_MAX_TOPN];
+    if (!hip_ok(hipMemcpy(tv, c->top_v, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read") ||
+        !hip_ok(hipMemcpy(ti, c->top_i, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    for (uint32_t i = 0; i < top_n; ++i) {
+        if (top_ids) top_ids[i] = ti[i];
+        if (top_logits) top_logits[i] = (double)tv[i];
+    }
+    if (h.nonfinite) { write_state(c, 0, 0, 0, 0); set_err(err, err_len, "non-finite final logit"); return 0; }
+    return 1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1182,9 +1222,13 @@ int qxg_prefill(qxg_ctx *c, const uint32_t *tokens, uint32_t n, uint32_t positio
     if (top_n == 0) top_n = 1;
     if (top_n > QXG_MAX_TOPN) top_n = QXG_MAX_TOPN;
     (void)hipSetDevice(c->device);
+    c->kt.used = 0;
+    if (!batched_prefill(c)) {
+        if (!prefill_steps(c, tokens, n, position0, run_head, residual_out, top_n, err, err_len)) return 0;
+        return prefill_finish(c, run_head, logits, top_n, top_ids, top_logits, elapsed_ms, err, err_len);
+    }
     if (!prefill_ready(c, err, err_len)) return 0;
     auto &B = c->pf;
-    c->kt.used = 0;
     if (!hip_ok(hipMemcpy(B.tokens, tokens, 4ull * (n < QXP_MAX ? n : QXP_MAX), hipMemcpyHostToDevice), err, err_len, "tokens"))
         return 0;
     (void)hipEventRecord(c->e0, c->s);
@@ -1207,23 +1251,9 @@ int qxg_prefill(qxg_ctx *c, const uint32_t *tokens, uint32_t n, uint32_t positio
         }
     }
     (void)hipEventRecord(c->e1, c->s);
-    if (!finish(c, err, err_len)) return 0;
-    if (elapsed_ms) (void)hipEventElapsedTime(elapsed_ms, c->e0, c->e1);
-    if (!run_head) return 1;
-    DevState h;
-    if (!read_state(c, h, err, err_len)) return 0;
-    if (logits && !hip_ok(hipMemcpy(logits, c->logits, (uint64_t)c->vocab * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
-    float tv[QXG_MAX_TOPN];
-    uint32_t ti[QXG_MAX_TOPN];
-    if (!hip_ok(hipMemcpy(tv, c->top_v, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read") ||
-        !hip_ok(hipMemcpy(ti, c->top_i, top_n * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
-    for (uint32_t i = 0; i < top_n; ++i) {
-        if (top_ids) top_ids[i] = ti[i];
-        if (top_logits) top_logits[i] = (double)tv[i];
-    }
-    if (h.nonfinite) { write_state(c, 0, 0, 0, 0); set_err(err, err_len, "non-finite final logit"); return 0; }
-    return 1;
+    return prefill_finish(c, run_head, logits, top_n, top_ids, top_logits, elapsed_ms, err, err_len);
 }
+
 
 int qxg_prefill_layer(qxg_ctx *c, uint32_t layer, uint32_t n, uint32_t position0, const float *x_in, float *ffn_inp_out,
                       float *moe_out, float *x_out, char *err, uint64_t err_len) {
@@ -1233,9 +1263,25 @@ int qxg_prefill_layer(qxg_ctx *c, uint32_t layer, uint32_t n, uint32_t position0
         return 0;
     }
     (void)hipSetDevice(c->device);
+    c->kt.used = 0;
+    if (!batched_prefill(c)) {   // token steps of the layer's attention and MoE halves
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint64_t o = 2048ull * i;
+            if (!hip_ok(hipMemcpyAsync(c->x, x_in + o, 2048 * 4, hipMemcpyHostToDevice, c->s), err, err_len, "upload")) return 0;
+            write_state(c, position0 + i, 0, 1, 1);
+            launch_attention(c, layer, c->x, nullptr, nullptr);
+            if (ffn_inp_out && !hip_ok(hipMemcpyAsync(ffn_inp_out + o, c->x, 2048 * 4, hipMemcpyDeviceToHost, c->s), err, err_len, "read"))
+                return 0;
+            launch_moe(c, layer, c->x, c->moe);
+            if ((moe_out && !hip_ok(hipMemcpyAsync(moe_out + o, c->moe, 2048 * 4, hipMemcpyDeviceToHost, c->s), err, err_len, "read")) ||
+                (x_out && !hip_ok(hipMemcpyAsync(x_out + o, c->x, 2048 * 4, hipMemcpyDeviceToHost, c->s), err, err_len, "read")))
+                return 0;
+            if (!finish(c, err, err_len)) return 0;
+        }
+        return 1;
+    }
     if (!prefill_ready(c, err, err_len)) return 0;
     auto &B = c->pf;
-    c->kt.used = 0;
     if (!hip_ok(hipMemcpyAsync(B.X, x_in, 2048ull * 4 * n, hipMemcpyHostToDevice, c->s), err, err_len, "upload")) return 0;
     prefill_layer(c, layer, n, position0, moe_out ? B.dump : nullptr);
     if (!finish(c, err, err_len)) return 0;

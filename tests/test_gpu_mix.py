@@ -87,8 +87,25 @@ def test_mix_decode_greedy(ctx, mix_model):
         assert list(gen) == toks, rep
 
 
-def test_mix_prefill_rejected(ctx, mix_model):
+def test_mix_prefill_token_steps(ctx, mix_model):
+    """The batched GEMMs decode the benchmark mix only; this model prefills token by token
+    through the decode kernels (as the reference prefills every prompt), so the result
+    equals decoding the prompt step by step, bit for bit."""
     ctx.load(mix_model)
+    prompt = np.array([29, 4000, 7, 123, 2048], np.uint32)
     ctx.kv_create(4, 16)
-    with pytest.raises(qxg.QxgError, match="prefill supports"):
-        ctx.prefill(np.array([1, 2, 3], np.uint32))
+    res, lg, ids, tl, _ = ctx.prefill(prompt, 0, True, 4, want_residual=True, want_logits=True)
+    ctx.kv_create(4, 16)
+    for s, tok in enumerate(prompt):
+        r, _, l2, i2, _ = ctx.decode_token(int(tok), s, s == len(prompt) - 1, 4, want_logits=True)
+        assert np.array_equal(res[s], r), s
+    assert np.array_equal(lg, l2) and list(ids) == list(i2)
+    # the same-input layer seam takes the same route: each row's attention and MoE halves
+    x = np.random.default_rng(3).standard_normal((3, 2048)).astype(np.float32)
+    ctx.kv_create(4, 16)
+    fi, moe, out = ctx.prefill_layer(1, 0, x)
+    ctx.kv_create(4, 16)
+    for t in range(3):
+        a, _, _ = ctx.attention_layer(1, t, x[t])
+        y, m, _, _ = ctx.moe_layer(1, x[t] + a)
+        assert np.array_equal(fi[t], x[t] + a) and np.array_equal(moe[t], m) and np.array_equal(out[t], y), t

@@ -189,7 +189,7 @@ def test_q8k_decode_greedy_and_replay(ctx, models):
 
 def test_q8k_failures_report_and_clear(ctx, models):
     """A non-finite activation fails the call with the reference's message (f32 mode
-    zeroes it instead); the next call succeeds; prefill is refused in this mode."""
+    zeroes it instead); the next call succeeds; prefill runs as decode steps."""
     ctx.load(models["base"])
     ctx.set_activation("q8_k_compat")
     try:
@@ -199,9 +199,14 @@ def test_q8k_failures_report_and_clear(ctx, models):
             ctx.moe_layer(0, x)
         y, _, _, _ = ctx.moe_layer(0, seeded_normal(5))
         assert np.isfinite(y).all()
+        # prefill in this mode runs the decode kernels token by token: equal to decode steps
         ctx.kv_create(1, 8)
-        with pytest.raises(qxg.QxgError, match="f32 activation mode only"):
-            ctx.prefill(np.array([1, 2], np.uint32))
+        res, _, ids, _, _ = ctx.prefill(np.array([1, 2, 3], np.uint32), 0, True, 2, want_residual=True)
+        ctx.kv_create(1, 8)
+        for s, tok in enumerate((1, 2, 3)):
+            r, _, _, i2, _ = ctx.decode_token(tok, s, s == 2, 2)
+            assert np.array_equal(res[s], r)
+        assert list(ids) == list(i2)
         err = ctypes.create_string_buffer(256)
         assert not qxg._g.qxg_set_activation(ctx._c, 7, err, 256)   # the C entry point rejects unknown formats
         assert b"unsupported activation" in err.value
