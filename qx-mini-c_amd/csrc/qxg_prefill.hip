@@ -367,27 +367,25 @@ extern "C" __global__ __launch_bounds__(256) void qxp_norm(const float *x, const
     for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
 }
 
-// Packs row r of the A operand (r < nrows[1] when nrows is non-null): source row
-// map ? map[r] : r of src (K floats; rows r >= nvalid and negative map entries are
-// padding and pack zeros),
-// scaled by a power of two and split into fp16 hi/lo fragments; rscale[r] = 1/s, or 0
-// (and zeros) when the row has a non-finite value.  Block per row, 8 values per chunk.
+// Packs row r of the A operand (r < rows, and r < nrows[1] when nrows is non-null):
+// source row map ? map[r] : r of src (K floats; rows r >= nvalid and negative map
+// entries are padding and pack zeros), scaled by a power of two and split into fp16
+// hi/lo fragments; rscale[r] = 1/s, or 0 (and zeros) when the row has a non-finite
+// value.  Wave per row, 8 values per chunk, no workgroup barriers.
 template <int K>
 __global__ __launch_bounds__(256) void qxp_pack(const float *src, const int32_t *map, const uint32_t *nrows,
-                                                uint32_t nvalid, uint4 *apk, float *rscale) {
-    constexpr int CH = K / 8, PER = (CH + 255) / 256, KS = K / 16;
-    const uint32_t r = blockIdx.x;
-    if (nrows && r >= nrows[1]) return;
-    __shared__ float red[4];
-    __shared__ uint32_t bad[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+                                                uint32_t rows, uint32_t nvalid, uint4 *apk, float *rscale) {
+    constexpr int CH = K / 8, PL = (CH + 63) / 64, KS = K / 16;
+    const int lane = threadIdx.x & 63;
+    const uint32_t r = blockIdx.x * 4 + wave_id();
+    if (r >= rows || (nrows && r >= nrows[1])) return;   // whole wave
     const int32_t sr = r >= nvalid ? -1 : map ? map[r] : (int32_t)r;
-    float v[PER][8];
+    float v[PL][8];
     float mx = 0.0f;
     bool fin = true;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int c = tid + 256 * i;
+    for (int i = 0; i < PL; ++i) {
+        const int c = lane + 64 * i;
         if (c < CH && sr >= 0) {
             const float4 *p = reinterpret_cast<const float4 *>(src + (uint64_t)sr * K + 8 * c);
             const float4 a = p[0], b = p[1];
@@ -403,20 +401,20 @@ __global__ __launch_bounds__(256) void qxp_pack(const float *src, const int32_t 
             mx = fmaxf(mx, fabsf(v[i][j]));
         }
     }
-    const uint64_t nb = __ballot(!fin);
-    if (lane == 0) bad[wave] = nb != 0;
-    mx = block_max256(mx, red);   // barriers order the bad[] writes too
-    const bool ok = !(bad[0] | bad[1] | bad[2] | bad[3]);
+    const bool ok = __ballot(!fin) == 0;
+    mx = fmaxf(mx, dppf<DPP_XOR1>(mx)); mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
+    mx = fmaxf(mx, dppf<DPP_ROR4>(mx)); mx = fmaxf(mx, dppf<DPP_ROR8>(mx));
+    mx = fmaxf(fmaxf(rdlanef(mx, 0), rdlanef(mx, 16)), fmaxf(rdlanef(mx, 32), rdlanef(mx, 48)));
     int ex = 0;
     if (mx > 0.0f && ok) (void)frexpf(mx, &ex);   // mx = f * 2^ex, f in [0.5, 1)
     int sh = 14 - ex;
     sh = sh > 100 ? 100 : sh < -100 ? -100 : sh;
     const float sc = ldexpf(1.0f, sh);
-    if (tid == 0) rscale[r] = ok ? ldexpf(1.0f, -sh) : 0.0f;
+    if (lane == 0) rscale[r] = ok ? ldexpf(1.0f, -sh) : 0.0f;
     const uint32_t mt = r >> 5, i32 = r & 31;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int c = tid + 256 * i;
+    for (int i = 0; i < PL; ++i) {
+        const int c = lane + 64 * i;
         if (c >= CH) continue;
         h8v hi, lo;
 #pragma unroll
@@ -857,10 +855,11 @@ void qxp_launch_gemm(hipStream_t s, int kind, const PfGemm &g, const PfTables &P
 }
 void qxp_launch_pack(hipStream_t s, int K, const float *src, const int32_t *map, const uint32_t *nrows, uint32_t rows,
                      uint32_t nvalid, uint4 *apk, float *rscale) {
+    const dim3 grid((rows + 3) / 4);   // wave per row
     switch (K) {
-    case 2048: hipLaunchKernelGGL(qxp_pack<2048>, dim3(rows), dim3(256), 0, s, src, map, nrows, nvalid, apk, rscale); break;
-    case 4096: hipLaunchKernelGGL(qxp_pack<4096>, dim3(rows), dim3(256), 0, s, src, map, nrows, nvalid, apk, rscale); break;
-    default: hipLaunchKernelGGL(qxp_pack<768>, dim3(rows), dim3(256), 0, s, src, map, nrows, nvalid, apk, rscale); break;
+    case 2048: hipLaunchKernelGGL(qxp_pack<2048>, grid, dim3(256), 0, s, src, map, nrows, rows, nvalid, apk, rscale); break;
+    case 4096: hipLaunchKernelGGL(qxp_pack<4096>, grid, dim3(256), 0, s, src, map, nrows, rows, nvalid, apk, rscale); break;
+    default: hipLaunchKernelGGL(qxp_pack<768>, grid, dim3(256), 0, s, src, map, nrows, rows, nvalid, apk, rscale); break;
     }
 }
 }
