@@ -788,20 +788,37 @@ extern "C" __global__ __launch_bounds__(1024) void qxp_group(const uint32_t *ids
         cnt[tid] = c;
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t o = 0, ng = 0;
-        for (uint32_t e = 0; e < experts; ++e) {
-            off[e] = o;
-            const uint32_t mt = (cnt[e] + 31) / 32;
-            for (uint32_t g = 0; g < mt; g += mt_per_group) {
-                const uint32_t k = mt - g < mt_per_group ? mt - g : mt_per_group;
-                mgroups[ng++] = e | ((o / 32 + g) << 8) | (k << 20);
-            }
-            o += 32 * mt;
+    if (tid < 64) {   // wave 0: experts 2l, 2l+1 per lane; exclusive scans of row tiles and m-groups
+        uint32_t mt[2], ng[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t e = 2 * tid + j;
+            mt[j] = e < experts ? (cnt[e] + 31) / 32 : 0u;
+            ng[j] = (mt[j] + mt_per_group - 1) / mt_per_group;
         }
-        off[experts] = o;
-        meta[0] = ng;
-        meta[1] = o;
+        const uint32_t smt = mt[0] + mt[1], sng = ng[0] + ng[1];
+        uint32_t imt = smt, ing = sng;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t a = __shfl_up(imt, o), b = __shfl_up(ing, o);
+            if (tid >= o) { imt += a; ing += b; }
+        }
+        uint32_t tile = imt - smt, gi = ing - sng;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t e = 2 * tid + j;
+            if (e <= 128u) off[e] = 32 * tile;
+            for (uint32_t g = 0; g < mt[j]; g += mt_per_group) {
+                const uint32_t k = mt[j] - g < mt_per_group ? mt[j] - g : mt_per_group;
+                mgroups[gi++] = e | ((tile + g) << 8) | (k << 20);
+            }
+            tile += mt[j];
+        }
+        if (tid == 63) {   // totals (experts past `experts` hold no tiles)
+            off[experts] = 32 * imt;
+            meta[0] = ing;
+            meta[1] = 32 * imt;
+        }
     }
     __syncthreads();
     for (uint32_t p = tid; p < T * 8; p += 1024) {
