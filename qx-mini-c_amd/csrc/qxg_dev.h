@@ -24,6 +24,21 @@ DEV float fp16_exact(uint32_t h) {
 // does not know that threadIdx.x / 64 is the same in every lane of a wave)
 DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
+// Loads of weight bytes, read once per token: non-temporal (streaming), so the 1.4 GB a
+// token streams does not displace the small tensors read every layer (router rows, KV
+// rows, activations) from the caches (measured: 518 -> 539 tok/s).
+typedef uint32_t nt4 __attribute__((ext_vector_type(4)));
+typedef uint32_t nt2 __attribute__((ext_vector_type(2)));
+DEV uint4 ldw4(const void *p) {
+    const nt4 v = __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+DEV uint2 ldw2(const void *p) {
+    const nt2 v = __builtin_nontemporal_load(reinterpret_cast<const nt2 *>(p));
+    return make_uint2(v.x, v.y);
+}
+DEV uint32_t ldw1(const void *p) { return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p)); }
+
 DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 DEV uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
 

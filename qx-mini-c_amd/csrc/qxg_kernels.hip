@@ -58,15 +58,15 @@ DEV void qkv_rows(DigIn<2048, true> &din, const uint8_t *qs, const uint8_t *p1, 
     for (int rr = 0; rr < RPW; ++rr) {
         const uint64_t blk = (uint64_t)(lr0 + rr) * 8 + b;
         if constexpr (FMT == 23) {
-            qv[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[ib];
-            const uint2 m = *reinterpret_cast<const uint2 *>(p1 + blk * 8);
+            qv[rr] = ldw4(qs + blk * 128 + 16 * ib);
+            const uint2 m = ldw2(p1 + blk * 8);
             mv[rr] = make_uint4(m.x, m.y, 0u, 0u);
         } else {
-            qv[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[2 * (ib >> 1)];
-            qw[rr] = reinterpret_cast<const uint4 *>(qs + blk * 128)[2 * (ib >> 1) + 1];
-            ha[rr] = reinterpret_cast<const uint4 *>(p2 + blk * 32)[0];
-            hb[rr] = reinterpret_cast<const uint4 *>(p2 + blk * 32)[1];
-            mv[rr] = *reinterpret_cast<const uint4 *>(p1 + blk * 16);
+            qv[rr] = ldw4(qs + blk * 128 + 32 * (ib >> 1));
+            qw[rr] = ldw4(qs + blk * 128 + 32 * (ib >> 1) + 16);
+            ha[rr] = ldw4(p2 + blk * 32);
+            hb[rr] = ldw4(p2 + blk * 32 + 16);
+            mv[rr] = ldw4(p1 + blk * 16);
         }
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
@@ -263,22 +263,22 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
     for (int rr = 0; rr < RPW; ++rr) {
         const uint64_t k0 = (uint64_t)(r0 + rr) * 16 + b0, k1 = (uint64_t)(r0 + rr) * 16 + b1;
         if constexpr (FMT == 23) {
-            q0[rr] = reinterpret_cast<const uint4 *>(qs + k0 * 128)[ib];
-            q1[rr] = reinterpret_cast<const uint4 *>(qs + k1 * 128)[ib];
-            const uint2 a = *reinterpret_cast<const uint2 *>(meta + k0 * 8), c = *reinterpret_cast<const uint2 *>(meta + k1 * 8);
+            q0[rr] = ldw4(qs + k0 * 128 + 16 * ib);
+            q1[rr] = ldw4(qs + k1 * 128 + 16 * ib);
+            const uint2 a = ldw2(meta + k0 * 8), c = ldw2(meta + k1 * 8);
             m0[rr] = make_uint4(a.x, a.y, 0u, 0u);
             m1[rr] = make_uint4(c.x, c.y, 0u, 0u);
         } else {
-            q0[rr] = reinterpret_cast<const uint4 *>(qs + k0 * 128)[2 * (ib >> 1)];
-            q0b[rr] = reinterpret_cast<const uint4 *>(qs + k0 * 128)[2 * (ib >> 1) + 1];
-            q1[rr] = reinterpret_cast<const uint4 *>(qs + k1 * 128)[2 * (ib >> 1)];
-            q1b[rr] = reinterpret_cast<const uint4 *>(qs + k1 * 128)[2 * (ib >> 1) + 1];
-            h0a[rr] = reinterpret_cast<const uint4 *>(p2 + k0 * 32)[0];
-            h0b[rr] = reinterpret_cast<const uint4 *>(p2 + k0 * 32)[1];
-            h1a[rr] = reinterpret_cast<const uint4 *>(p2 + k1 * 32)[0];
-            h1b[rr] = reinterpret_cast<const uint4 *>(p2 + k1 * 32)[1];
-            m0[rr] = *reinterpret_cast<const uint4 *>(meta + k0 * 16);
-            m1[rr] = *reinterpret_cast<const uint4 *>(meta + k1 * 16);
+            q0[rr] = ldw4(qs + k0 * 128 + 32 * (ib >> 1));
+            q0b[rr] = ldw4(qs + k0 * 128 + 32 * (ib >> 1) + 16);
+            q1[rr] = ldw4(qs + k1 * 128 + 32 * (ib >> 1));
+            q1b[rr] = ldw4(qs + k1 * 128 + 32 * (ib >> 1) + 16);
+            h0a[rr] = ldw4(p2 + k0 * 32);
+            h0b[rr] = ldw4(p2 + k0 * 32 + 16);
+            h1a[rr] = ldw4(p2 + k1 * 32);
+            h1b[rr] = ldw4(p2 + k1 * 32 + 16);
+            m0[rr] = ldw4(meta + k0 * 16);
+            m1[rr] = ldw4(meta + k1 * 16);
         }
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
@@ -360,11 +360,11 @@ template <int FMT>
 DEV gu4 gu_load(const GuW &w, uint64_t blk, int ib) {
     gu4 r;
     if constexpr (FMT == 17) {
-        const uint2 q = reinterpret_cast<const uint2 *>(w.qs + blk * 64)[ib];
+        const uint2 q = ldw2(w.qs + blk * 64 + 8 * ib);
         r.x = q.x; r.y = q.y; r.z = w.p1[blk * 8 + ib]; r.w = w.d[blk];
     } else {
-        r.x = reinterpret_cast<const uint32_t *>(w.qs + blk * 64)[ib];
-        r.y = reinterpret_cast<const uint32_t *>(w.qs + blk * 64)[8 + ib];
+        r.x = ldw1(w.qs + blk * 64 + 4 * ib);
+        r.y = ldw1(w.qs + blk * 64 + 32 + 4 * ib);
         r.z = (uint32_t)w.p2[blk * 8 + ib] | ((uint32_t)w.p1[blk * 8 + ib] << 8);
         r.w = w.d[blk];
     }
@@ -499,16 +499,16 @@ struct DnW {
 template <int FMT>
 DEV void dn_load(const DnW &w, uint64_t blk, int k, uint4 &a, uint2 &m) {
     if constexpr (FMT == 18) {
-        const uint2 q = reinterpret_cast<const uint2 *>(w.qs + blk * 64)[k];
-        a = make_uint4(q.x, q.y, reinterpret_cast<const uint32_t *>(w.p1 + blk * 32)[k], w.d[blk]);
+        const uint2 q = ldw2(w.qs + blk * 64 + 8 * k);
+        a = make_uint4(q.x, q.y, ldw1(w.p1 + blk * 32 + 4 * k), w.d[blk]);
     } else if constexpr (FMT == 21) {
-        const uint2 q = reinterpret_cast<const uint2 *>(w.qs + blk * 64)[k];
-        const uint32_t sg = reinterpret_cast<const uint32_t *>(w.p1 + blk * 32)[k];
+        const uint2 q = ldw2(w.qs + blk * 64 + 8 * k);
+        const uint32_t sg = ldw1(w.p1 + blk * 32 + 4 * k);
         const uint32_t qh = w.p2[blk * 16 + k], sc = (w.p2[blk * 16 + 8 + (k >> 1)] >> (4 * (k & 1))) & 15u;
         a = make_uint4(q.x, q.y, sg, qh | (sc << 8) | ((uint32_t)w.d[blk] << 16));
     } else {
-        a = reinterpret_cast<const uint4 *>(w.qs + blk * 128)[k];
-        m = *reinterpret_cast<const uint2 *>(w.p1 + blk * 8);
+        a = ldw4(w.qs + blk * 128 + 16 * k);
+        m = ldw2(w.p1 + blk * 8);
     }
 }
 
@@ -651,9 +651,8 @@ __global__ __launch_bounds__(256) void qxk_head(const uint32_t *dig, const uint8
     for (int rr = 0; rr < RPW; ++rr) {
         const uint32_t r = min(r0 + rr, vocab - 1);   // tail rows re-read the last row; not stored
         const uint64_t blk = (uint64_t)r * 8 + b;
-        const uint4 *lp = reinterpret_cast<const uint4 *>(ql + blk * 128 + 64 * hh + 32 * (k & 1));
-        const uint4 *hp = reinterpret_cast<const uint4 *>(qh + blk * 64 + 32 * hh);
-        l0[rr] = lp[0]; l1[rr] = lp[1]; h0[rr] = hp[0]; h1[rr] = hp[1];
+        const uint8_t *lp = ql + blk * 128 + 64 * hh + 32 * (k & 1), *hp = qh + blk * 64 + 32 * hh;
+        l0[rr] = ldw4(lp); l1[rr] = ldw4(lp + 16); h0[rr] = ldw4(hp); h1[rr] = ldw4(hp + 16);
         const int8_t *sp = sc + blk * 16 + 8 * hh + 2 * k;
         s0[rr] = sp[0]; s1[rr] = sp[1];
         d16[rr] = dd[blk];
