@@ -302,7 +302,7 @@ void launch_attention(qxg_ctx *c, uint32_t l, float *x, float *attn_dump, float 
 
 void launch_moe(qxg_ctx *c, uint32_t l, float *x, float *moe_dump) {
     const LayerW &w = c->L[l];
-    qx_launch(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, timer_for(c, 6), (const float *)x,
+    qx_launch(qxk_router, dim3(c->experts), dim3(256), 0, c->s, timer_for(c, 6), (const float *)x,
               w.ffn_norm, w.router, c->experts, c->rlog);
     qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h, c->q8, timer_for(c, 0));
     qxl_down(c->s, c->h, w.down, c->T, c->st, x, moe_dump, c->q8, timer_for(c, 1));
@@ -1171,7 +1171,7 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
                                std::sqrt(128.0), c->st, c->ctxv, nullptr);
             break;
         case 6:
-            hipLaunchKernelGGL(qxk_router, dim3((c->experts + 3) / 4), dim3(256), 0, c->s, (const float *)c->x, w.ffn_norm,
+            hipLaunchKernelGGL(qxk_router, dim3(c->experts), dim3(256), 0, c->s, (const float *)c->x, w.ffn_norm,
                                w.router, c->experts, c->rlog);
             break;
         }

@@ -373,18 +373,17 @@ struct DigIn {
 template <int N, bool NORM>
 DEV void digits_load(const float *x, const float *w, DigIn<N, NORM> &in) {
     using D = DigIn<N, NORM>;
+    // every thread of the 256 loads its chunks unconditionally: straight-line loads let
+    // the compiler wait for each one separately (a load under a branch makes it wait for
+    // every load issued before the branch joins)
+    static_assert(D::NCH == 256 * D::PER, "the 256 threads cover the vector exactly");
     const int tid = threadIdx.x;
 #pragma unroll
     for (int it = 0; it < D::PER; ++it) {
         const int c = tid + 256 * it;
-        if (c < D::NCH) {
-            const float4 a = reinterpret_cast<const float4 *>(x)[2 * c], b = reinterpret_cast<const float4 *>(x)[2 * c + 1];
-            in.v[it][0] = a.x; in.v[it][1] = a.y; in.v[it][2] = a.z; in.v[it][3] = a.w;
-            in.v[it][4] = b.x; in.v[it][5] = b.y; in.v[it][6] = b.z; in.v[it][7] = b.w;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) in.v[it][i] = 0.0f;
-        }
+        const float4 a = reinterpret_cast<const float4 *>(x)[2 * c], b = reinterpret_cast<const float4 *>(x)[2 * c + 1];
+        in.v[it][0] = a.x; in.v[it][1] = a.y; in.v[it][2] = a.z; in.v[it][3] = a.w;
+        in.v[it][4] = b.x; in.v[it][5] = b.y; in.v[it][6] = b.z; in.v[it][7] = b.w;
     }
     if constexpr (NORM) {
         static_assert(D::PER == 1, "normalised vectors are 2048 long");
@@ -429,17 +428,15 @@ DEV bool block_digits(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float 
         for (int i = 0; i < 8; ++i) { fin = fin && isfinite(in.v[it][i]); mx = fmaxf(mx, fabsf(in.v[it][i])); }
         mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
         mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
-        if (c < D::NCH) {
-            uint32_t h0, h1, m0, m1, l0, l1;
-            float sc;
-            digits8(in.v[it], isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
-            uint32_t *d = s_dig + (c >> 2) * DIG_STRIDE;
-            const int q = c & 3;
-            *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
-            *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
-            *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
-            if (q == 0) d[24] = __float_as_uint(sc);
-        }
+        uint32_t h0, h1, m0, m1, l0, l1;
+        float sc;
+        digits8(in.v[it], isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
+        uint32_t *d = s_dig + (c >> 2) * DIG_STRIDE;
+        const int q = c & 3;
+        *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
+        *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
+        if (q == 0) d[24] = __float_as_uint(sc);
     }
     return __syncthreads_or(!fin) == 0;
 }
@@ -490,14 +487,12 @@ DEV bool block_q8(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float *nor
         for (int i = 0; i < 8; ++i) fin = fin && isfinite(in.v[it][i]);
         uint32_t h0, h1;
         const float dq = q8_chunk(in.v[it], h0, h1);
-        if (c < D::NCH) {
-            uint32_t *d = s_dig + (c >> 2) * DIG_STRIDE;
-            const int q = c & 3;
-            *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
-            *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(0u, 0u);
-            *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(0u, 0u);
-            if (q == 0) d[24] = __float_as_uint(dq * (1.0f / 65536.0f));
-        }
+        uint32_t *d = s_dig + (c >> 2) * DIG_STRIDE;
+        const int q = c & 3;
+        *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(0u, 0u);
+        *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(0u, 0u);
+        if (q == 0) d[24] = __float_as_uint(dq * (1.0f / 65536.0f));
     }
     return __syncthreads_or(!fin) == 0;
 }
@@ -520,6 +515,12 @@ DEV void load_dig(const uint32_t *__restrict__ s_dig, int g, Dig &d) {
 
 
 DEV uint32_t cur_pos(const DevState *st) { return st->pos0 + st->step; }
+// a prompt step whose logits nobody reads (the head kernels skip it).  The fields are
+// read together, not behind a short-circuit, so they come in one scalar load.
+DEV bool prompt_step(const DevState *st) {
+    const uint32_t fh = st->force_head, step = st->step, np = st->n_prompt;
+    return (fh == 0u) & (step + 1u < np);
+}
 
 // R per-lane partial sums (one per row, R in {1,2,4,8}) reduced over the wave:
 // up to two split rounds inside each quad (a lane keeps half of the rows and adds

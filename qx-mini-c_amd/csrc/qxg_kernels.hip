@@ -49,10 +49,15 @@ struct QkvW {
 };
 
 template <int RPW, int FMT, bool Q8>
-DEV void qkv_rows(DigIn<2048, true> &din, const uint8_t *qs, const uint8_t *p1, const uint8_t *p2, int lr0, int r0,
-                  uint32_t *s_dig, double *s_red, float *qkv, DevState *st) {
+DEV void qkv_rows(const float *x, const float *norm_w, const uint8_t *qs, const uint8_t *p1, const uint8_t *p2, int lr0,
+                  int r0, uint32_t *s_dig, double *s_red, float *qkv, DevState *st) {
     const int lane = threadIdx.x & 63;
     const int b = lane >> 3, ib = lane & 7;
+    // the activation loads come first (used first) and inside the format branch, so no
+    // norm arithmetic is hoisted above the branch, where it would wait for x before the
+    // weight loads are issued
+    DigIn<2048, true> din;
+    digits_load(x, norm_w, din);
     uint4 qv[RPW], qw[RPW], ha[RPW], hb[RPW], mv[RPW];
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
@@ -104,10 +109,8 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
     const int mi = rb < 4096 ? 0 : rb < 4608 ? 1 : 2;
     const int lr0 = r0 - (mi == 0 ? 0 : mi == 1 ? 4096 : 4608);
     QXG_MARK(3, 0);
-    DigIn<2048, true> din;
-    digits_load(x, norm_w, din);
-    if (w.type[mi] == 13) qkv_rows<RPW, 13, Q8>(din, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv, st);
-    else qkv_rows<RPW, 23, Q8>(din, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv, st);
+    if (w.type[mi] == 13) qkv_rows<RPW, 13, Q8>(x, norm_w, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv, st);
+    else qkv_rows<RPW, 23, Q8>(x, norm_w, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv, st);
 }
 
 // Attention for one q head, with the per-head q/k RMSNorm (src/qx_format.c:3740-3757),
@@ -140,29 +143,31 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     __shared__ float s_scale[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int qh = blockIdx.x, kvh = qh >> 3;
-    const uint32_t pos = cur_pos(st), n = pos + 1;
-    const uint64_t base = (uint64_t)layer * ctx;
-    const uint32_t nst = pos < (uint32_t)ATT_STAGE ? pos : (uint32_t)ATT_STAGE;   // staged positions
     QXG_MARK(4, 0);
-    // cached rows first: 16 bytes of row (tid>>3) + 32*i, chunk tid&7, i < 4
-    typedef uint32_t v4u __attribute__((ext_vector_type(4)));   // register-promoted (a uint4 array is not)
-    v4u kst[4], vst[4];
-    float kss = 0.0f, vss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t t = (tid >> 3) + 32 * i;
-        if (t < nst) {
-            const uint64_t off = (base + t) * 512 + kvh * 128 + 16 * (tid & 7);
-            kst[i] = *reinterpret_cast<const v4u *>(kc + off);
-            vst[i] = *reinterpret_cast<const v4u *>(vc + off);
-        }
-    }
-    if ((uint32_t)tid < nst) { kss = ks[base + tid]; vss = vs[base + tid]; }
-    // loads: k head `wave`, v (2 per thread), q head (wave 0 after k), norms, rope row
+    // the inputs that do not depend on the position first: the position is a load of
+    // its own (device state), and the rows, scales and RoPE entries wait for it
     float k0 = qkv[4096 + 128 * wave + lane], k1 = qkv[4096 + 128 * wave + 64 + lane];
     const float v0 = qkv[4608 + tid], v1 = qkv[4608 + 256 + tid];
     float q0 = qkv[128 * qh + lane], q1 = qkv[128 * qh + 64 + lane];
     const float kw0 = k_norm[lane], kw1 = k_norm[64 + lane], qw0 = q_norm[lane], qw1 = q_norm[64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t pos = cur_pos(st), n = pos + 1;
+    const uint64_t base = (uint64_t)layer * ctx;
+    const uint32_t nst = pos < (uint32_t)ATT_STAGE ? pos : (uint32_t)ATT_STAGE;   // staged positions
+    // cached rows first: 16 bytes of row (tid>>3) + 32*i, chunk tid&7, i < 4.  The loads
+    // are unconditional (rows past nst read the layer's row 0, which always exists), so
+    // the compiler waits for each one where it is used rather than after each branch.
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));   // register-promoted (a uint4 array is not)
+    v4u kst[4], vst[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = (tid >> 3) + 32 * i;
+        const uint64_t off = (base + (t < nst ? t : 0u)) * 512 + kvh * 128 + 16 * (tid & 7);
+        kst[i] = *reinterpret_cast<const v4u *>(kc + off);
+        vst[i] = *reinterpret_cast<const v4u *>(vc + off);
+    }
+    const uint32_t ts = (uint32_t)tid < nst ? (uint32_t)tid : 0u;
+    const float kss = ks[base + ts], vss = vs[base + ts];
     const double c = T.rope_cos[pos * 64 + lane], s = T.rope_sin[pos * 64 + lane];
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     QXG_MARK(4, 1);
@@ -317,31 +322,41 @@ __global__ __launch_bounds__(256) void qxk_oproj(const float *ctxv, const uint8_
 }
 
 // ffn RMSNorm + F32 router logits in double (reference src/qx_format.c:5254-5264);
-// wave per expert row.  The softmax and top-8 run in the prologue of the gate/up
-// kernel, where the expert ids are needed.
+// one workgroup per expert row, wave w taking values [512w, 512w + 512), 8 per lane
+// (thread t holds values 8t..8t+7, the order of the other kernels' RMSNorm).  The
+// softmax and top-8 run in the prologue of the gate/up kernel, where the ids are needed.
 extern "C" __global__ __launch_bounds__(256) void qxk_router(const float *x, const float *norm_w, const float *router,
         uint32_t experts, double *logits) {
-    const int lane = threadIdx.x & 63, wave = wave_id();
-    const uint32_t e = blockIdx.x * 4 + wave;
-    if (e >= experts) return;
+    __shared__ double s_ss[4], s_dot[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const uint32_t e = blockIdx.x;   // grid = experts
     QXG_MARK(5, 0);
-    float v[32], w[32], r[32];
-    load32(router + (uint64_t)e * 2048 + 32 * lane, r);
-    load32(x + 32 * lane, v);
-    load32(norm_w + 32 * lane, w);
-    rmsnorm32(v, w);
+    const float4 *R = reinterpret_cast<const float4 *>(router + (uint64_t)e * 2048) + 2 * tid;
+    const float4 *X = reinterpret_cast<const float4 *>(x) + 2 * tid;
+    const float4 *W = reinterpret_cast<const float4 *>(norm_w) + 2 * tid;
+    const float4 r0 = R[0], r1 = R[1], x0 = X[0], x1 = X[1], w0 = W[0], w1 = W[1];
+    float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    const float r[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+    const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += (double)v[i] * (double)v[i];
+    ss = wave_total_d(ss);
+    if (lane == 0) s_ss[wave] = ss;
+    __syncthreads();
+    const double tot = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
+    const double inv = 1.0 / sqrt(tot / 2048.0 + 1.0e-6);
     QXG_MARK(5, 1);
     double acc = 0.0;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) acc += (double)r[i] * (double)v[i];
-    QXG_ANCHOR(acc);
+    for (int i = 0; i < 8; ++i) acc += (double)r[i] * (double)((float)((double)v[i] * inv) * w[i]);
     QXG_MARK(5, 2);
     acc = wave_total_d(acc);
-    if (lane == 0) logits[e] = acc;
+    if (lane == 0) s_dot[wave] = acc;
+    __syncthreads();
+    if (tid == 0) logits[e] = (s_dot[0] + s_dot[1]) + (s_dot[2] + s_dot[3]);
     QXG_MARK(5, 3);
 }
-
-
 // gate/up (2048 -> 768; IQ2_XS, or IQ2_S in the real checkpoint) for the 8 routed experts
 // (ids from st) + SwiGLU h[r][i] = (float)(silu((double)g) * (double)u)
 // (src/qx_format.c:5298, 2511-2513).  Weight loads are issued first; the codebook tables
@@ -596,7 +611,7 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, DnW w, Tables T,
 // DIG_STRIDE dwords, then the all-finite flag); the head waves load their group.
 extern "C" __global__ __launch_bounds__(256) void qxk_norm_digits(const float *x, const float *norm_w, uint32_t *dig,
                                                                    float *norm_dump, DevState *st, uint32_t q8) {
-    if (!st->force_head && st->step + 1 < st->n_prompt) return;
+    if (prompt_step(st)) return;
     __shared__ uint32_t s_dig[64 * DIG_STRIDE];
     __shared__ double s_red[4];
     DigIn<2048, true> din;
@@ -640,7 +655,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_q8k(const float *x, uint32
 template <int RPW>
 __global__ __launch_bounds__(256) void qxk_head(const uint32_t *dig, const uint8_t *ql,
         const uint8_t *qh, const int8_t *sc, const uint16_t *dd, uint32_t vocab, DevState *st, float *logits) {
-    if (!st->force_head && st->step + 1 < st->n_prompt) return;
+    if (prompt_step(st)) return;
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int b = lane >> 3, ib = lane & 7, hh = ib >> 2, k = ib & 3;
     const uint32_t r0 = (blockIdx.x * 4 + wave) * RPW;
@@ -720,7 +735,7 @@ DEV void select_topn(const float *vals, const uint32_t *idx, uint32_t n, uint32_
 
 extern "C" __global__ __launch_bounds__(256) void qxk_topk(const float *logits, uint32_t vocab, uint32_t topn,
         float *cand_v, uint32_t *cand_i, float *top_v, uint32_t *top_i, uint32_t *tokens, DevState *st) {
-    if (!st->force_head && st->step + 1 < st->n_prompt) return;
+    if (prompt_step(st)) return;
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
     __shared__ uint32_t ticket;
