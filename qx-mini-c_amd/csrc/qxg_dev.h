@@ -333,6 +333,17 @@ DEV void rmsnorm32(float *v, const float *w) {
 }
 
 
+// Block-wide "no lane has the flag" for 256 threads, ending with the barrier the
+// caller needs anyway: each wave's ballot goes to LDS, one barrier, four reads.  One
+// use per kernel (a second call could overwrite the words before a slow wave reads them).
+DEV bool block_none256(bool flag) {
+    __shared__ uint32_t s_any[4];
+    const bool any = __ballot(flag) != 0;
+    if ((threadIdx.x & 63) == 0) s_any[threadIdx.x >> 6] = any ? 1u : 0u;
+    __syncthreads();
+    return (s_any[0] | s_any[1] | s_any[2] | s_any[3]) == 0u;
+}
+
 // ---- block-cooperative activation digits.  The digit planes of all N/32 groups of
 // a vector are computed once per block into LDS (DIG_STRIDE dwords per group: h[8],
 // m[8], l[8], scale bits), 8 consecutive values per thread; the 4 threads of a group
@@ -340,24 +351,40 @@ DEV void rmsnorm32(float *v, const float *w) {
 // is first RMS-normalised with weights w (reference src/qx_format.c:3358-3371).
 constexpr int DIG_STRIDE = 28;   // 16-byte aligned rows for ds_read_b128
 
+// X = rint(y * 2^k) with k = 22 - e (e the exponent of the group max, 2^(e-1) <= mx < 2^e),
+// so |X| <= 2^22: one fma adds 1.5 * 2^23, whose binade has unit spacing, and the
+// integer is the difference of the bit patterns.  k is capped at 126 so 2^k and the
+// scale 2^-k stay normal floats (groups below 2^-104 keep fewer than 22 bits).  A
+// non-finite group (mx passed as 0) gives p2 = 0; its values are discarded by the
+// caller's finiteness flag.  Digits: L = X mod 256 (signed), M the next byte of
+// (X - L) / 256, H = the rest.
 DEV void digits8(const float *y, float mx, uint32_t &ph0, uint32_t &ph1, uint32_t &pm0, uint32_t &pm1, uint32_t &pl0,
                  uint32_t &pl1, float &scale) {
     int e = 0;
     if (mx > 0.0f) (void)frexpf(mx, &e);
-    scale = mx > 0.0f ? ldexpf(1.0f, e - 22) : 0.0f;
-    uint32_t H[2] = {0, 0}, M[2] = {0, 0}, L[2] = {0, 0};
+    const int k = min(22 - e, 126);
+    const float p2 = mx > 0.0f ? __uint_as_float((uint32_t)(k + 127) << 23) : 0.0f;
+    scale = mx > 0.0f ? __uint_as_float((uint32_t)(127 - k) << 23) : 0.0f;
+    // per value: L = byte 0 of X; t1 = X - L has M in byte 1; X1 = t1 / 256 and
+    // t3 = X1 - sext(byte 0 of X1) has H in byte 1
+    uint32_t xl[8], xm[8], xh[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int X = mx > 0.0f ? (int)rintf(ldexpf(y[i], 22 - e)) : 0;
-        const int l = ((X + 128) & 255) - 128;
-        const int X1 = (X - l) >> 8;
-        const int m = ((X1 + 128) & 255) - 128;
-        const int hh = (X1 - m) >> 8;
-        H[i >> 2] |= (uint32_t)(hh & 255) << (8 * (i & 3));
-        M[i >> 2] |= (uint32_t)(m & 255) << (8 * (i & 3));
-        L[i >> 2] |= (uint32_t)(l & 255) << (8 * (i & 3));
+        const int X = (int)(__float_as_uint(fmaf(y[i], p2, 12582912.0f)) - 0x4B400000u);
+        const int t1 = X - (int)(int8_t)X;
+        const int X1 = t1 >> 8;
+        xl[i] = (uint32_t)X;
+        xm[i] = (uint32_t)t1;
+        xh[i] = (uint32_t)(X1 - (int)(int8_t)X1);
     }
-    ph0 = H[0]; ph1 = H[1]; pm0 = M[0]; pm1 = M[1]; pl0 = L[0]; pl1 = L[1];
+    // byte B of 4 words -> one word: two pair packs, then one merge
+    auto pack4 = [](const uint32_t *v, uint32_t sel) {
+        const uint32_t lo = perm(v[1], v[0], sel), hi = perm(v[3], v[2], sel);
+        return perm(hi, lo, 0x05040100u);
+    };
+    pl0 = pack4(xl, 0x0c0c0400u); pl1 = pack4(xl + 4, 0x0c0c0400u);
+    pm0 = pack4(xm, 0x0c0c0501u); pm1 = pack4(xm + 4, 0x0c0c0501u);
+    ph0 = pack4(xh, 0x0c0c0501u); ph1 = pack4(xh + 4, 0x0c0c0501u);
 }
 
 // The vector (and norm weights) as loaded by one thread: 8 consecutive values per
@@ -438,7 +465,7 @@ DEV bool block_digits(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float 
         *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
         if (q == 0) d[24] = __float_as_uint(sc);
     }
-    return __syncthreads_or(!fin) == 0;
+    return block_none256(!fin);
 }
 
 // q8_k_compat activations (src/qx_format.c:3891-3927).  A 256-value block is the 8
@@ -494,7 +521,7 @@ DEV bool block_q8(DigIn<N, NORM> &in, uint32_t *s_dig, double *s_red, float *nor
         *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(0u, 0u);
         if (q == 0) d[24] = __float_as_uint(dq * (1.0f / 65536.0f));
     }
-    return __syncthreads_or(!fin) == 0;
+    return block_none256(!fin);
 }
 
 // the activation mode's preparation: Q8_K codes, or the three-plane digits of f32
@@ -581,6 +608,22 @@ DEV float block_max256(float v, float *red) {
     return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+// block maxima of two values at once, one barrier; red[4] must not be in use (no
+// earlier phase of the block reads it after its last barrier)
+DEV void block_max2_256(float &a, float &b, float2 *red) {
+    a = fmaxf(a, dppf<DPP_XOR1>(a)); b = fmaxf(b, dppf<DPP_XOR1>(b));
+    a = fmaxf(a, dppf<DPP_XOR2>(a)); b = fmaxf(b, dppf<DPP_XOR2>(b));
+    a = fmaxf(a, dppf<DPP_ROR4>(a)); b = fmaxf(b, dppf<DPP_ROR4>(b));
+    a = fmaxf(a, dppf<DPP_ROR8>(a)); b = fmaxf(b, dppf<DPP_ROR8>(b));
+    a = fmaxf(fmaxf(rdlanef(a, 0), rdlanef(a, 16)), fmaxf(rdlanef(a, 32), rdlanef(a, 48)));
+    b = fmaxf(fmaxf(rdlanef(b, 0), rdlanef(b, 16)), fmaxf(rdlanef(b, 32), rdlanef(b, 48)));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = make_float2(a, b);
+    __syncthreads();
+    const float2 r0 = red[0], r1 = red[1], r2 = red[2], r3 = red[3];
+    a = fmaxf(fmaxf(r0.x, r1.x), fmaxf(r2.x, r3.x));
+    b = fmaxf(fmaxf(r0.y, r1.y), fmaxf(r2.y, r3.y));
+}
+
 // 128 values of one head held as (lane, lane+64) by a wave: per-head RMSNorm then RoPE
 DEV void head_norm_rope_wave(float &x0, float &x1, float w0, float w1, double c, double s) {
     const double ss = wave_total_d((double)x0 * (double)x0 + (double)x1 * (double)x1);
@@ -624,7 +667,7 @@ DEV double attn_scores(const float *s_q, uint32_t *s_qd, uint32_t n, double sqrt
         *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
         if (q == 0) d[24] = __float_as_uint(sc);
     }
-    const bool qok = __syncthreads_or(!fin) == 0;
+    const bool qok = block_none256(!fin);
     // a quad per position: lane q4 of the quad takes the 32-dim group q4, the four group
     // sums are added as (g0 + g1) + (g2 + g3) in double
     const int q4 = tid & 3;

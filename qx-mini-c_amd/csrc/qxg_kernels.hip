@@ -135,7 +135,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     __shared__ float s_k[512], s_v[512];
     __shared__ __align__(16) float s_q[128];
     __shared__ __align__(16) uint32_t s_qd[4 * DIG_STRIDE];
-    __shared__ float red[4];
+    __shared__ float2 red2[4];
     __shared__ double redd[4];
     __shared__ float s_part[16][132];
     __shared__ __align__(16) int8_t s_k8[128];
@@ -190,8 +190,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
         va = fmaxf(b0, b1);
     }
     QXG_MARK(4, 2);
-    ka = block_max256(ka, red);
-    va = block_max256(va, red);
+    block_max2_256(ka, va, red2);
     QXG_MARK(4, 3);
     const float kscale = ka > 0.0f ? ka / 127.0f : 1.0f, vscale = va > 0.0f ? va / 127.0f : 1.0f;
     const uint64_t slot = base + pos;
@@ -404,12 +403,10 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     const int b = lane >> 3, ib = lane & 7;
     const int u0 = (blockIdx.x * 4 + wave) * UPW;   // grid covers exactly 8*768 units
     const int E = (int)experts;
-    __shared__ uint32_t s_ids[QXG_TOPK];
     QXG_MARK(1, 0);
-    // the router logits head the longest chain (logits -> top-8 -> weights): loaded first,
-    // by wave 0, which picks the experts for the whole workgroup
-    double l0 = 0.0, l1 = 0.0;
-    if (wave == 0) { l0 = lane < E ? logits[lane] : 0.0; l1 = lane + 64 < E ? logits[lane + 64] : 0.0; }
+    // the router logits head the longest chain (logits -> top-8 -> weights): loaded first;
+    // every wave picks the experts itself (no barrier before its expert-row loads)
+    const double l0 = lane < E ? logits[lane] : 0.0, l1 = lane + 64 < E ? logits[lane + 64] : 0.0;
     DigIn<2048, true> din;
     digits_load(x, norm_w, din);
     const uint4 *G = FMT == 17 ? T.g2 : T.g2s;
@@ -422,19 +419,16 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     }
     const uint2 t2 = SL[tid & (NS - 1)];
     uint32_t ids[QXG_TOPK];
-    if (wave == 0) {
-        QXG_ANCHOR(l1);
-        QXG_MARK(1, 5);
-        wave_top8_ids(l0, l1, E, ids);
+    QXG_ANCHOR(l1);
+    QXG_MARK(1, 5);
+    wave_top8_ids(l0, l1, E, ids);
+    uint32_t e = 0u;
 #pragma unroll
-        for (int q = 0; q < QXG_TOPK; ++q) {
-            ids[q] = ids[q] < experts ? ids[q] : 0u;   // never address past the experts
-            if (lane == q) s_ids[q] = ids[q];
-        }
-        QXG_MARK(1, 6);
+    for (int q = 0; q < QXG_TOPK; ++q) {
+        ids[q] = ids[q] < experts ? ids[q] : 0u;   // never address past the experts
+        if (q == u0 / QXG_FFN) e = ids[q];           // UPW | 768: one expert per wave
     }
-    __syncthreads();
-    const uint32_t e = __builtin_amdgcn_readfirstlane(s_ids[u0 / QXG_FFN]);   // UPW | 768: one expert per wave
+    QXG_MARK(1, 6);
     gu4 gq[UPW], uq[UPW];
 #pragma unroll
     for (int uu = 0; uu < UPW; ++uu) {
