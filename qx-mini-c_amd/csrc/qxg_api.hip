@@ -15,7 +15,8 @@
 extern "C" {
 __global__ void qxk_embed(const uint8_t *, uint64_t, const uint32_t *, const DevState *, float *);
 __global__ void qxk_attn(const float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
-                         uint32_t, uint32_t, double, const DevState *, float *, float *);
+                         uint32_t, uint32_t, double, const DevState *, float *, float *, float *);
+__global__ void qxk_attn_merge(const DevState *, const float *, float *);
 __global__ void qxk_router(const float *, const float *, const float *, uint32_t, double *);
 __global__ void qxk_topk(const float *, uint32_t, uint32_t, float *, uint32_t *, float *, uint32_t *, uint32_t *,
                          DevState *);
@@ -108,6 +109,9 @@ struct qxg_ctx {
     float *x = nullptr, *qkv = nullptr, *ctxv = nullptr, *h = nullptr, *logits = nullptr;
     float *vcur = nullptr, *attn = nullptr, *moe = nullptr, *norm = nullptr, *layer_dump = nullptr;
     double *rlog = nullptr;
+    float *apart = nullptr;        // per-split attention results [32 heads][QXG_MAX_SPLITS]
+    uint32_t att_splits = 1;       // attention splits launched: covers every position the launches reach
+    uint32_t graph_splits = 0;     // the recorded step graph's
     float *cand_v = nullptr, *top_v = nullptr;
     uint32_t *cand_i = nullptr, *top_i = nullptr, *tokens = nullptr, *dig = nullptr;
     DevState *st = nullptr;
@@ -294,9 +298,12 @@ Timer timer_for(qxg_ctx *c, int which) {
 void launch_attention(qxg_ctx *c, uint32_t l, float *x, float *attn_dump, float *vcur_dump) {
     const LayerW &w = c->L[l];
     qxl_qkv(c->s, x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv, c->st, c->q8, timer_for(c, 2));
-    qx_launch(qxk_attn, dim3(32), dim3(256), (uint32_t)(c->kv_ctx * sizeof(double)), c->s, timer_for(c, 5), c->qkv,
-              w.q_norm, w.k_norm, c->T, c->kc, c->vc, c->ks, c->vs, l, c->kv_ctx, std::sqrt(128.0),
-              (const DevState *)c->st, c->ctxv, vcur_dump);
+    qx_launch(qxk_attn, dim3(32, c->att_splits), dim3(256), 0, c->s, timer_for(c, 5), c->qkv, w.q_norm, w.k_norm,
+              c->T, c->kc, c->vc, c->ks, c->vs, l, c->kv_ctx, std::sqrt(128.0), (const DevState *)c->st, c->ctxv,
+              c->apart, vcur_dump);
+    if (c->att_splits > 1)
+        hipLaunchKernelGGL(qxk_attn_merge, dim3(32), dim3(128), 0, c->s, (const DevState *)c->st, (const float *)c->apart,
+                           c->ctxv);
     qxl_oproj(c->s, c->ctxv, w.wo, x, attn_dump, c->st, c->q8, timer_for(c, 3));
 }
 
@@ -738,7 +745,7 @@ void qxg_close(qxg_ctx *c) {
     void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->T.g2s, c->T.g3s, c->T.sel8, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
                     c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging,
-                    c->xch, c->abort};
+                    c->xch, c->abort, c->apart};
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (void *p : c->arenas) (void)hipFree(p);
     for (void *p : c->pf.all) (void)hipFree(p);
@@ -842,13 +849,13 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     void **bufs[] = {(void **)&c->x, (void **)&c->qkv, (void **)&c->ctxv, (void **)&c->h, (void **)&c->logits,
                      (void **)&c->vcur, (void **)&c->attn, (void **)&c->moe, (void **)&c->norm,
                      (void **)&c->layer_dump, (void **)&c->rlog, (void **)&c->cand_v, (void **)&c->top_v,
-                     (void **)&c->cand_i, (void **)&c->top_i, (void **)&c->tokens, (void **)&c->dig};
+                     (void **)&c->cand_i, (void **)&c->top_i, (void **)&c->tokens, (void **)&c->dig, (void **)&c->apart};
     for (void **b : bufs) if (*b) { (void)hipFree(*b); *b = nullptr; }
     const uint64_t V = c->vocab ? c->vocab : 1;
     const uint64_t sizes[] = {2048 * 4, 5120 * 4, 4096 * 4, 8 * 768 * 4, V * 4, 512 * 4, 2048 * 4, 2048 * 4, 2048 * 4,
                               (uint64_t)(layers ? layers : 1) * 2048 * 4, 128 * 8, TOPK_BLOCKS * QXG_MAX_TOPN * 4,
                               QXG_MAX_TOPN * 4, TOPK_BLOCKS * QXG_MAX_TOPN * 4, QXG_MAX_TOPN * 4,
-                              (QXG_MAX_CTX + 2) * 4, (64 * 28 + 4) * 4};
+                              (QXG_MAX_CTX + 2) * 4, (64 * 28 + 4) * 4, QXG_ATT_PART_BYTES};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i)
         if (!hip_ok(hipMalloc(bufs[i], sizes[i]), err, err_len, "work buffers")) return 0;
     if (!hip_ok(hipMemset(c->tokens, 0, sizes[15]), err, err_len, "work buffers")) return 0;
@@ -863,18 +870,6 @@ int qxg_kv_create(qxg_ctx *c, uint32_t layers, uint32_t ctx_tokens, uint32_t kv_
     if (!ctx_tokens || ctx_tokens > QXG_MAX_CTX) { set_err(err, err_len, "state loop context must be between 1 and 4096"); return 0; }
     if (!layers) { set_err(err, err_len, "invalid layer count"); return 0; }
     (void)hipSetDevice(c->device);
-    {   // the attention kernel keeps one double score per position in LDS
-        hipFuncAttributes fa;
-        int max_lds = 0;
-        if (!hip_ok(hipFuncGetAttributes(&fa, (const void *)qxk_attn), err, err_len, "attention attributes") ||
-            !hip_ok(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, c->device), err, err_len,
-                    "device attributes"))
-            return 0;
-        if (fa.sharedSizeBytes + (size_t)ctx_tokens * sizeof(double) > (size_t)max_lds) {
-            set_err(err, err_len, "context too long for the attention kernel's LDS on this device");
-            return 0;
-        }
-    }
     drop_graph(c);
     void *b[] = {c->kc, c->vc, c->ks, c->vs};
     for (void *p : b) if (p) (void)hipFree(p);
@@ -888,6 +883,7 @@ int qxg_kv_create(qxg_ctx *c, uint32_t layers, uint32_t ctx_tokens, uint32_t kv_
         !hip_ok(hipMemset(c->ks, 0, slots * 4), err, err_len, "kv") || !hip_ok(hipMemset(c->vs, 0, slots * 4), err, err_len, "kv"))
         return 0;
     c->kv_layers = layers;
+    c->att_splits = (ctx_tokens + QXG_ATT_SPLIT - 1) / QXG_ATT_SPLIT;   // every position of the cache
     c->kv_ctx = ctx_tokens;
     return 1;
 }
@@ -982,7 +978,18 @@ int qxg_generate(qxg_ctx *c, const uint32_t *prompt, uint32_t n_prompt, uint32_t
     // in-situ kernel timing records events per launch, and QXG_EAGER asks for plain launches
     // (kernel tracers): run eagerly
     const bool use_graph = c->kt.which < 0 && !c->eager;
+    // attention splits for the positions this call reaches (the graph is recorded again
+    // when that count changes); restored to the whole cache's afterwards
+    const uint32_t all_splits = c->att_splits;
+    c->att_splits = (uint32_t)((pos0 + steps + QXG_ATT_SPLIT - 1) / QXG_ATT_SPLIT);
+    struct Restore {
+        qxg_ctx *c;
+        uint32_t v;
+        ~Restore() { c->att_splits = v; }
+    } restore{c, all_splits};
+    if (use_graph && c->graph_exec && c->graph_splits != c->att_splits) drop_graph(c);
     if (use_graph && !c->graph_exec) {
+        c->graph_splits = c->att_splits;
         // every kernel reads the position/step from the device state, so one recorded
         // step serves all steps; no memset nodes are recorded
         if (!hip_ok(hipStreamBeginCapture(c->s, hipStreamCaptureModeThreadLocal), err, err_len, "capture")) return 0;
@@ -1166,9 +1173,12 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
         case 3: qxl_oproj(c->s, c->ctxv, w.wo, c->attn, nullptr, c->st, c->q8); break;
         case 4: qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, nullptr, c->dig, c->q8); break;
         case 5:
-            hipLaunchKernelGGL(qxk_attn, dim3(32), dim3(256), (size_t)c->kv_ctx * sizeof(double), c->s, c->qkv,
-                               w.q_norm, w.k_norm, c->T, c->kc, c->vc, c->ks, c->vs, l % c->kv_layers, c->kv_ctx,
-                               std::sqrt(128.0), c->st, c->ctxv, nullptr);
+            hipLaunchKernelGGL(qxk_attn, dim3(32, c->att_splits), dim3(256), 0, c->s, c->qkv, w.q_norm, w.k_norm, c->T,
+                               c->kc, c->vc, c->ks, c->vs, l % c->kv_layers, c->kv_ctx, std::sqrt(128.0), c->st,
+                               c->ctxv, c->apart, nullptr);
+            if (c->att_splits > 1)
+                hipLaunchKernelGGL(qxk_attn_merge, dim3(32), dim3(128), 0, c->s, (const DevState *)c->st,
+                                   (const float *)c->apart, c->ctxv);
             break;
         case 6:
             hipLaunchKernelGGL(qxk_router, dim3(c->experts), dim3(256), 0, c->s, (const float *)c->x, w.ffn_norm,

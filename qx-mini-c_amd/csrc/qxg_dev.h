@@ -703,9 +703,10 @@ DEV double attn_scores(const float *s_q, uint32_t *s_qd, uint32_t n, double sqrt
 }
 // Softmax in double: e_t = exp(s_t - mx), den = sum e_t (1 if not finite and positive);
 // s_sc[t] <- (e_t / den) * vs_t, the position's weight with its V scale folded in.
-// vsc(t) returns position t's V scale.  Ends with a barrier.
+// Unnormalised (norm false, one split of several): s_sc[t] <- e_t * vs_t and the raw
+// den is returned.  vsc(t) returns position t's V scale.  Ends with a barrier.
 template <typename VS>
-DEV void attn_weights(uint32_t n, double mx, double *s_sc, double *redd, VS vsc) {
+DEV double attn_weights(uint32_t n, double mx, double *s_sc, double *redd, VS vsc, bool norm = true) {
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     double den = 0.0;
     for (uint32_t t = tid; t < n; t += 256) {
@@ -717,9 +718,14 @@ DEV void attn_weights(uint32_t n, double mx, double *s_sc, double *redd, VS vsc)
     if (lane == 0) redd[wave] = den;
     __syncthreads();
     den = (redd[0] + redd[1]) + (redd[2] + redd[3]);
-    if (!isfinite(den) || den <= 0.0) den = 1.0;
-    for (uint32_t t = tid; t < n; t += 256) s_sc[t] = (s_sc[t] / den) * (double)vsc(t);
+    if (norm) {
+        if (!isfinite(den) || den <= 0.0) den = 1.0;
+        for (uint32_t t = tid; t < n; t += 256) s_sc[t] = (s_sc[t] / den) * (double)vsc(t);
+    } else {
+        for (uint32_t t = tid; t < n; t += 256) s_sc[t] = s_sc[t] * (double)vsc(t);
+    }
     __syncthreads();
+    return den;
 }
 // Context: out[d] = sum_t p_t * v8_t[d] in f32 with p_t = (float)((e_t / den) * vs_t).
 // Thread (g = tid/16, dims 8*(tid%16)..+8) sums positions g, g+16, ...; the 16 partial

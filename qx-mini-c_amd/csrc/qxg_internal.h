@@ -71,6 +71,14 @@ struct Tables {
     uint2 *sel8;   // sign byte (8 bits) -> v_perm selectors for 8 values
 };
 
+// Decode attention splits: a block takes QXG_ATT_SPLIT positions of one q head; the
+// per-split results (128 context sums, then the maximum score and the exp-sum as
+// doubles) are QXG_ATT_PART floats, at [head][split].
+#define QXG_ATT_SPLIT 128
+#define QXG_MAX_SPLITS (QXG_MAX_CTX / QXG_ATT_SPLIT)
+#define QXG_ATT_PART 132
+#define QXG_ATT_PART_BYTES (32 * QXG_MAX_SPLITS * QXG_ATT_PART * 4)
+
 // Rows (units) per wave of the decode matvec kernels.  A workgroup's 4*RPW Q/K/V rows
 // must lie in one matrix (RPW | 128) and a wave's gate/up units in one expert (UPW | 768).
 #ifndef QXG_QKV_RPW

@@ -116,20 +116,23 @@ __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm
 // Attention for one q head, with the per-head q/k RMSNorm (src/qx_format.c:3740-3757),
 // split-half RoPE (4625-4641; cos/sin from the host-computed table) and INT8 K/V
 // quantization (4449-4463) of the current position fused in: every block derives the
-// same K/V row (the scale spans all 512 values), block 0 stores it at [layer][pos],
-// and each block uses its own copy for position pos.  Scores over 0..pos (one lane per
-// position, q as int8 digit planes against the INT8 K codes), double softmax, f32 context
-// sums over 16 interleaved position groups (reference src/qx_format.c:5127-5172).
-// The cached K/V rows of positions [0, min(pos, ATT_STAGE)) and their scales are
-// loaded at kernel start, together with q/k/v, and staged in LDS while the norm,
-// RoPE and quantization run; later positions are read from global memory.
+// same K/V row (the scale spans all 512 values), block (0, 0) stores it at
+// [layer][pos], and each block uses its own copy for position pos.  Scores (a quad per
+// position, q as int8 digit planes against the INT8 K codes), double softmax, f32
+// context sums over 16 interleaved position groups (reference src/qx_format.c:5127-5172).
+// Block (h, s) of the (32, S) grid takes positions [128 s, min(128 s + 128, pos + 1)):
+// their cached K/V rows and scales are loaded at kernel start, together with q/k/v, and
+// staged in LDS while the norm, RoPE and quantization run.  With one split (pos < 128)
+// the block writes the normalised context; with several, each writes its unnormalised
+// context sums, maximum score and exp-sum to part[h][s], and qxk_attn_merge combines
+// them.  Blocks past the last split return at once; the host launches S >= (pos+128)/128.
 
-constexpr int ATT_STAGE = 128;   // positions staged in LDS (4 uint4 of K and of V per thread)
+constexpr int ATT_STAGE = QXG_ATT_SPLIT;   // positions per block (4 uint4 of K and of V per thread)
 
 extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, const float *q_norm, const float *k_norm,
         Tables T, int8_t *kc, int8_t *vc, float *ks, float *vs, uint32_t layer, uint32_t ctx, double sqrt_hd,
-        const DevState *st, float *ctx_out, float *vcur_dump) {
-    extern __shared__ double s_sc[];               // ctx scores
+        const DevState *st, float *ctx_out, float *part, float *vcur_dump) {
+    __shared__ double s_sc[ATT_STAGE];             // scores, then weights
     __shared__ uint4 s_kst[ATT_STAGE * 8], s_vst[ATT_STAGE * 8];   // staged rows of this kv head
     __shared__ float s_kss[ATT_STAGE], s_vss[ATT_STAGE];
     __shared__ float s_k[512], s_v[512];
@@ -142,7 +145,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     __shared__ __align__(16) int8_t s_v8[128];
     __shared__ float s_scale[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-    const int qh = blockIdx.x, kvh = qh >> 3;
+    const int qh = blockIdx.x, kvh = qh >> 3, split = blockIdx.y;
     QXG_MARK(4, 0);
     // the inputs that do not depend on the position first: the position is a load of
     // its own (device state), and the rows, scales and RoPE entries wait for it
@@ -152,8 +155,12 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     const float kw0 = k_norm[lane], kw1 = k_norm[64 + lane], qw0 = q_norm[lane], qw1 = q_norm[64 + lane];
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t pos = cur_pos(st), n = pos + 1;
+    const uint32_t nsplit = (n + ATT_STAGE - 1) / ATT_STAGE;
+    if ((uint32_t)split >= nsplit) return;   // block-uniform
+    const uint32_t t0 = (uint32_t)split * ATT_STAGE, cnt = min(n - t0, (uint32_t)ATT_STAGE);
     const uint64_t base = (uint64_t)layer * ctx;
-    const uint32_t nst = pos < (uint32_t)ATT_STAGE ? pos : (uint32_t)ATT_STAGE;   // staged positions
+    // staged (cached) positions t0 .. t0+nst-1; the last split's last position is pos
+    const uint32_t nst = (uint32_t)split + 1 == nsplit ? cnt - 1 : cnt;
     // cached rows first: 16 bytes of row (tid>>3) + 32*i, chunk tid&7, i < 4.  The loads
     // are unconditional (rows past nst read the layer's row 0, which always exists), so
     // the compiler waits for each one where it is used rather than after each branch.
@@ -162,11 +169,11 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t t = (tid >> 3) + 32 * i;
-        const uint64_t off = (base + (t < nst ? t : 0u)) * 512 + kvh * 128 + 16 * (tid & 7);
+        const uint64_t off = (base + (t < nst ? t0 + t : 0u)) * 512 + kvh * 128 + 16 * (tid & 7);
         kst[i] = *reinterpret_cast<const v4u *>(kc + off);
         vst[i] = *reinterpret_cast<const v4u *>(vc + off);
     }
-    const uint32_t ts = (uint32_t)tid < nst ? (uint32_t)tid : 0u;
+    const uint32_t ts = (uint32_t)tid < nst ? t0 + (uint32_t)tid : 0u;
     const float kss = ks[base + ts], vss = vs[base + ts];
     const double c = T.rope_cos[pos * 64 + lane], s = T.rope_sin[pos * 64 + lane];
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
@@ -194,17 +201,18 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     QXG_MARK(4, 3);
     const float kscale = ka > 0.0f ? ka / 127.0f : 1.0f, vscale = va > 0.0f ? va / 127.0f : 1.0f;
     const uint64_t slot = base + pos;
+    const bool writer = blockIdx.x == 0 && split == 0;   // other splits never read slot pos
     for (int i = tid; i < 512; i += 256) {
         const float kx = s_k[i], vx = s_v[i];
         int qk = isfinite(kx) ? (int)rintf(kx / kscale) : 0;
         int qv = isfinite(vx) ? (int)rintf(vx / vscale) : 0;
         qk = qk < -127 ? -127 : qk > 127 ? 127 : qk;
         qv = qv < -127 ? -127 : qv > 127 ? 127 : qv;
-        if (blockIdx.x == 0) { kc[slot * 512 + i] = (int8_t)qk; vc[slot * 512 + i] = (int8_t)qv; }
+        if (writer) { kc[slot * 512 + i] = (int8_t)qk; vc[slot * 512 + i] = (int8_t)qv; }
         if ((i >> 7) == kvh) { s_k8[i & 127] = (int8_t)qk; s_v8[i & 127] = (int8_t)qv; }
     }
-    if (blockIdx.x == 0 && tid == 0) { ks[slot] = kscale; vs[slot] = vscale; }
-    if (blockIdx.x == 0 && vcur_dump) { vcur_dump[tid] = v0; vcur_dump[256 + tid] = v1; }
+    if (writer && tid == 0) { ks[slot] = kscale; vs[slot] = vscale; }
+    if (writer && vcur_dump) { vcur_dump[tid] = v0; vcur_dump[256 + tid] = v1; }
     if (tid == 0) { s_scale[0] = kscale; s_scale[1] = vscale; }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -217,35 +225,60 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     if ((uint32_t)tid < nst) { s_kss[tid] = kss; s_vss[tid] = vss; }
     __syncthreads();
     QXG_MARK(4, 4);
-    // position pos from the block's own row, [0, nst) from the LDS stage, the rest from the cache
-    auto krow = [&](uint32_t t, int g, uint4 (&k)[2], float &ksc) {
-        if (t == pos) {
+    // local position u is t0 + u: pos from the block's own row, the others from the LDS stage
+    auto krow = [&](uint32_t u, int g, uint4 (&k)[2], float &ksc) {
+        if (u >= nst) {
             k[0] = reinterpret_cast<const uint4 *>(s_k8)[2 * g];
             k[1] = reinterpret_cast<const uint4 *>(s_k8)[2 * g + 1];
             ksc = s_scale[0];
-        } else if (t < nst) {
-            k[0] = s_kst[t * 8 + 2 * g];
-            k[1] = s_kst[t * 8 + 2 * g + 1];
-            ksc = s_kss[t];
         } else {
-            const uint4 *p = reinterpret_cast<const uint4 *>(kc + (base + t) * 512 + kvh * 128);
-            k[0] = p[2 * g];
-            k[1] = p[2 * g + 1];
-            ksc = ks[base + t];
+            k[0] = s_kst[u * 8 + 2 * g];
+            k[1] = s_kst[u * 8 + 2 * g + 1];
+            ksc = s_kss[u];
         }
     };
-    auto vrow = [&](uint32_t t, int dg) -> uint2 {
-        if (t == pos) return reinterpret_cast<const uint2 *>(s_v8)[dg];
-        if (t < nst) return reinterpret_cast<const uint2 *>(s_vst)[t * 16 + dg];
-        return *reinterpret_cast<const uint2 *>(vc + (base + t) * 512 + kvh * 128 + 8 * dg);
+    auto vrow = [&](uint32_t u, int dg) -> uint2 {
+        if (u >= nst) return reinterpret_cast<const uint2 *>(s_v8)[dg];
+        return reinterpret_cast<const uint2 *>(s_vst)[u * 16 + dg];
     };
-    auto vsc = [&](uint32_t t) -> float { return t == pos ? s_scale[1] : t < nst ? s_vss[t] : vs[base + t]; };
-    const double mx = attn_scores(s_q, s_qd, n, sqrt_hd, s_sc, redd, krow);
+    auto vsc = [&](uint32_t u) -> float { return u >= nst ? s_scale[1] : s_vss[u]; };
+    const double mx = attn_scores(s_q, s_qd, cnt, sqrt_hd, s_sc, redd, krow);
     QXG_MARK(4, 5);
-    attn_weights(n, mx, s_sc, redd, vsc);
+    const bool one = nsplit == 1;
+    const double den = attn_weights(cnt, mx, s_sc, redd, vsc, one);
     QXG_MARK(4, 6);
-    attn_context(n, s_sc, s_part, vrow, ctx_out + qh * 128);
+    float *pp = part + ((uint64_t)qh * QXG_MAX_SPLITS + split) * QXG_ATT_PART;
+    attn_context(cnt, s_sc, s_part, vrow, one ? ctx_out + qh * 128 : pp);
+    if (!one && tid == 0) {
+        reinterpret_cast<double *>(pp + 128)[0] = mx;
+        reinterpret_cast<double *>(pp + 128)[1] = den;
+    }
     QXG_MARK(4, 7);
+}
+
+// The splits of qxk_attn combined for one q head (thread = dimension): M = max_s m_s,
+// w_s = exp(m_s - M), L = sum_s w_s l_s (1 if not finite and positive), ctx[d] =
+// sum_s (float)(w_s / L) * acc_s[d] in split order.  With one split the attention
+// kernel wrote the context itself and this returns.
+extern "C" __global__ __launch_bounds__(128) void qxk_attn_merge(const DevState *st, const float *part, float *ctx_out) {
+    const uint32_t n = cur_pos(st) + 1, ns = (n + ATT_STAGE - 1) / ATT_STAGE;
+    if (ns <= 1) return;
+    const int qh = blockIdx.x, d = threadIdx.x;
+    const float *p = part + (uint64_t)qh * QXG_MAX_SPLITS * QXG_ATT_PART;
+    double M = -INFINITY;
+    for (uint32_t s = 0; s < ns; ++s) M = fmax(M, reinterpret_cast<const double *>(p + s * QXG_ATT_PART + 128)[0]);
+    double L = 0.0;
+    for (uint32_t s = 0; s < ns; ++s) {
+        const double *ml = reinterpret_cast<const double *>(p + s * QXG_ATT_PART + 128);
+        L += exp(ml[0] - M) * ml[1];
+    }
+    if (!isfinite(L) || L <= 0.0) L = 1.0;
+    float o = 0.0f;
+    for (uint32_t s = 0; s < ns; ++s) {
+        const double m = reinterpret_cast<const double *>(p + s * QXG_ATT_PART + 128)[0];
+        o = fmaf((float)(exp(m - M) / L), p[s * QXG_ATT_PART + d], o);
+    }
+    ctx_out[qh * 128 + d] = o;
 }
 
 // O projection 4096 -> 2048 on ctx (IQ4_XS, or Q5_K in the real checkpoint), then

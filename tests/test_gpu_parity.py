@@ -132,7 +132,8 @@ def test_moe_router_ties(ctx, tmp_path):
                                             (2047, 2048), (4095, 4096)])
 def test_attention_block_config3(ctx, layer_model, pos, ctx_tokens):
     """Config 3: attention at `pos` with positions 0..pos-1 prefilled by seeded INT8 rows
-    (positions around the 128-row LDS staging window, and the maximum context)."""
+    (one 128-position split up to 127; from 128 on several splits and their merge, up to
+    the 32 of the maximum context)."""
     ctx.load(layer_model)
     ctx.kv_create(1, ctx_tokens)
     okv = qxo.KV(1, ctx_tokens)
