@@ -155,6 +155,42 @@ def test_attention_block_config3(ctx, layer_model, pos, ctx_tokens):
     assert abs(gks[0] / okv.ks[0, pos] - 1) < 1e-5 and abs(gvs[0] / okv.vs[0, pos] - 1) < 1e-5
 
 
+def test_generate_across_attention_splits(ctx, tmp_path):
+    """The recorded step graph launches the attention splits its positions need (two for
+    positions 118..138) while eager steps launch the whole cache's (four at 512): the
+    context depends only on the position, so both give the same tokens, and the graph
+    is recorded again when a later call needs more splits (positions 250..260)."""
+    p = tmp_path / "splits.qxf"
+    qxg.generate_model(p, layers=2, vocab=4096, experts=32, seed=45)
+    ctx.load(p)
+    ctx.kv_create(2, 512)
+    rng = np.random.default_rng(12)
+    pre = rng.integers(0, 4096, size=118).astype(np.uint32)
+    ctx.prefill(pre, 0, False, 1)
+    toks, t = [], 17
+    for s in range(118, 139):
+        _, _, _, ids, _ = ctx.decode_token(t, s, True, 1)
+        t = int(ids[0])
+        toks.append(t)
+    for rep in range(2):
+        ctx.kv_create(2, 512)
+        ctx.prefill(pre, 0, False, 1)
+        gen, _ = ctx.generate([17], 21, pos0=118)
+        assert list(gen) == toks, rep
+    pre2 = rng.integers(0, 4096, size=250).astype(np.uint32)
+    ctx.kv_create(2, 512)
+    ctx.prefill(pre2, 0, False, 1)
+    gen2, _ = ctx.generate([5], 11, pos0=250)
+    ctx.kv_create(2, 512)
+    ctx.prefill(pre2, 0, False, 1)
+    toks2, t = [], 5
+    for s in range(250, 261):
+        _, _, _, ids, _ = ctx.decode_token(t, s, True, 1)
+        t = int(ids[0])
+        toks2.append(t)
+    assert list(gen2) == toks2
+
+
 def test_decode_two_layers_greedy(ctx, tmp_path):
     """Embedding + 2 layers + head, 5 greedy steps; per-step residual and tokens."""
     p = tmp_path / "two.qxf"
