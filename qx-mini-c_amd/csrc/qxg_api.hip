@@ -37,6 +37,7 @@ void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32
               uint32_t *, bool, Timer = Timer());
 __global__ void qxp_embed(const uint8_t *, uint64_t, const uint32_t *, float *);
 __global__ void qxp_norm(const float *, const float *, uint32_t, float *);
+__global__ void qxp_norm_pack(const float *, const float *, uint32_t, uint32_t, uint4 *, float *);
 __global__ void qxp_qk(const float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
                        uint32_t, uint32_t, uint32_t, float *);
 __global__ void qxp_attn(const float *, const int8_t *, const int8_t *, const float *, const float *, uint32_t, uint32_t,
@@ -574,8 +575,8 @@ void prefill_layer(qxg_ctx *c, uint32_t l, uint32_t T, uint32_t p0, float *moe_d
     const uint32_t mt = (T + 31) / 32, E = c->experts;
     const uint32_t none = 0xffffffffu;
     // attention half: RMSNorm, Q/K/V GEMM, q/k norm + RoPE + INT8 append, attention, O GEMM + residual
-    hipLaunchKernelGGL(qxp_norm, dim3((T + 3) / 4), dim3(256), 0, s, (const float *)B.X, w.attn_norm, T, B.XN);
-    qxp_launch_pack(s, 2048, B.XN, nullptr, nullptr, mt * 32, T, B.apk, B.rscale);
+    hipLaunchKernelGGL(qxp_norm_pack, dim3(mt * 8), dim3(256), 0, s, (const float *)B.X, w.attn_norm, mt * 32, T, B.apk,
+                       B.rscale);
     PfGemm g{};
     g.w[0] = pf_mat(w.wq); g.w[1] = pf_mat(w.wk); g.w[2] = pf_mat(w.wv);
     g.w_start[0] = 0; g.w_start[1] = 4096; g.w_start[2] = 4608;

@@ -367,40 +367,22 @@ extern "C" __global__ __launch_bounds__(256) void qxp_norm(const float *x, const
     for (int i = 0; i < 8; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
 }
 
-// Packs row r of the A operand (r < rows, and r < nrows[1] when nrows is non-null):
-// source row map ? map[r] : r of src (K floats; rows r >= nvalid and negative map
-// entries are padding and pack zeros), scaled by a power of two and split into fp16
-// hi/lo fragments; rscale[r] = 1/s, or 0 (and zeros) when the row has a non-finite
-// value.  Wave per row, 8 values per chunk, no workgroup barriers.
-template <int K>
-__global__ __launch_bounds__(256) void qxp_pack(const float *src, const int32_t *map, const uint32_t *nrows,
-                                                uint32_t rows, uint32_t nvalid, uint4 *apk, float *rscale) {
-    constexpr int CH = K / 8, PL = (CH + 63) / 64, KS = K / 16;
+// Packs one row of the A operand held by a wave, NC chunks of 8 values per lane (chunk
+// index c[i]): scaled by a power of two and split into fp16 hi/lo fragments; rscale[r]
+// = 1/s, or 0 (and zeros) when the row has a non-finite value.
+template <int NC, int K>
+DEV void pack_row(const float (&v)[NC][8], const int (&c)[NC], uint32_t r, uint4 *apk, float *rscale) {
+    constexpr int CH = K / 8, KS = K / 16;
     const int lane = threadIdx.x & 63;
-    const uint32_t r = blockIdx.x * 4 + wave_id();
-    if (r >= rows || (nrows && r >= nrows[1])) return;   // whole wave
-    const int32_t sr = r >= nvalid ? -1 : map ? map[r] : (int32_t)r;
-    float v[PL][8];
     float mx = 0.0f;
     bool fin = true;
 #pragma unroll
-    for (int i = 0; i < PL; ++i) {
-        const int c = lane + 64 * i;
-        if (c < CH && sr >= 0) {
-            const float4 *p = reinterpret_cast<const float4 *>(src + (uint64_t)sr * K + 8 * c);
-            const float4 a = p[0], b = p[1];
-            v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
-            v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
-        }
+    for (int i = 0; i < NC; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             fin = fin && isfinite(v[i][j]);
             mx = fmaxf(mx, fabsf(v[i][j]));
         }
-    }
     const bool ok = __ballot(!fin) == 0;
     mx = fmaxf(mx, dppf<DPP_XOR1>(mx)); mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
     mx = fmaxf(mx, dppf<DPP_ROR4>(mx)); mx = fmaxf(mx, dppf<DPP_ROR8>(mx));
@@ -413,9 +395,8 @@ __global__ __launch_bounds__(256) void qxp_pack(const float *src, const int32_t 
     if (lane == 0) rscale[r] = ok ? ldexpf(1.0f, -sh) : 0.0f;
     const uint32_t mt = r >> 5, i32 = r & 31;
 #pragma unroll
-    for (int i = 0; i < PL; ++i) {
-        const int c = lane + 64 * i;
-        if (c >= CH) continue;
+    for (int i = 0; i < NC; ++i) {
+        if (c[i] >= CH) continue;
         h8v hi, lo;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -424,10 +405,63 @@ __global__ __launch_bounds__(256) void qxp_pack(const float *src, const int32_t 
             hi[j] = a;
             lo[j] = (_Float16)(y - (float)a);
         }
-        const uint64_t base = ((uint64_t)mt * KS + (c >> 1)) * 128 + i32 + 32 * (c & 1);
+        const uint64_t base = ((uint64_t)mt * KS + (c[i] >> 1)) * 128 + i32 + 32 * (c[i] & 1);
         apk[base] = __builtin_bit_cast(uint4, hi);
         apk[base + 64] = __builtin_bit_cast(uint4, lo);
     }
+}
+
+// Packs row r of the A operand (r < rows, and r < nrows[1] when nrows is non-null):
+// source row map ? map[r] : r of src (K floats; rows r >= nvalid and negative map
+// entries are padding and pack zeros), through pack_row.  Wave per row, chunks
+// lane + 64 i, no workgroup barriers.
+template <int K>
+__global__ __launch_bounds__(256) void qxp_pack(const float *src, const int32_t *map, const uint32_t *nrows,
+                                                uint32_t rows, uint32_t nvalid, uint4 *apk, float *rscale) {
+    constexpr int CH = K / 8, PL = (CH + 63) / 64;
+    const int lane = threadIdx.x & 63;
+    const uint32_t r = blockIdx.x * 4 + wave_id();
+    if (r >= rows || (nrows && r >= nrows[1])) return;   // whole wave
+    const int32_t sr = r >= nvalid ? -1 : map ? map[r] : (int32_t)r;
+    float v[PL][8];
+    int c[PL];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+        c[i] = lane + 64 * i;
+        if (c[i] < CH && sr >= 0) {
+            const float4 *p = reinterpret_cast<const float4 *>(src + (uint64_t)sr * K + 8 * c[i]);
+            const float4 a = p[0], b = p[1];
+            v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+            v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
+        }
+    }
+    pack_row<PL, K>(v, c, r, apk, rscale);
+}
+
+// RMSNorm of token r (qxp_norm's arithmetic: 32 consecutive values per lane) fused with
+// its packing as the Q/K/V GEMM's A operand; rows r >= nvalid pack zeros.
+extern "C" __global__ __launch_bounds__(256) void qxp_norm_pack(const float *x, const float *w, uint32_t rows,
+                                                                uint32_t nvalid, uint4 *apk, float *rscale) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t r = blockIdx.x * 4 + wave_id();
+    if (r >= rows) return;   // whole wave
+    float v[4][8];
+    const int c[4] = {4 * lane, 4 * lane + 1, 4 * lane + 2, 4 * lane + 3};
+    if (r < nvalid) {
+        float t[32], ww[32];
+        load32(x + (uint64_t)r * 2048 + 32 * lane, t);
+        load32(w + 32 * lane, ww);
+        rmsnorm32(t, ww);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i >> 3][i & 7] = t[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i >> 3][i & 7] = 0.0f;
+    }
+    pack_row<4, 2048>(v, c, r, apk, rscale);
 }
 
 // Per token (block): q/k head RMSNorm (src/qx_format.c:3740-3757) and RoPE at position
