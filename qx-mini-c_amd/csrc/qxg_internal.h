@@ -87,7 +87,12 @@ struct Tables {
 #ifndef QXG_GU_UPW
 #define QXG_GU_UPW 3
 #endif
+#ifndef QXG_OPROJ_RPW
 #define QXG_OPROJ_RPW 2
+#endif
+#ifndef QXG_DOWN_RPW
+#define QXG_DOWN_RPW 2
+#endif
 static_assert(128 % QXG_QKV_RPW == 0 && 768 % QXG_GU_UPW == 0, "row groups must not straddle a matrix or expert");
 
 // Persistent decode kernel (qxk_layers): per-layer weight pointers and launch arguments.
