@@ -79,11 +79,8 @@ struct Tables {
 #define QXG_ATT_PART 132
 #define QXG_ATT_PART_BYTES (32 * QXG_MAX_SPLITS * QXG_ATT_PART * 4)
 
-// Rows (units) per wave of the decode matvec kernels.  A workgroup's 4*RPW Q/K/V rows
-// must lie in one matrix (RPW | 128) and a wave's gate/up units in one expert (UPW | 768).
-#ifndef QXG_QKV_RPW
-#define QXG_QKV_RPW 2
-#endif
+// Rows (units) per wave of the decode matvec kernels.  A wave's gate/up units must lie
+// in one expert (UPW | 768).
 #ifndef QXG_GU_UPW
 #define QXG_GU_UPW 3
 #endif
@@ -93,7 +90,7 @@ struct Tables {
 #ifndef QXG_DOWN_RPW
 #define QXG_DOWN_RPW 2
 #endif
-static_assert(128 % QXG_QKV_RPW == 0 && 768 % QXG_GU_UPW == 0, "row groups must not straddle a matrix or expert");
+static_assert(768 % QXG_GU_UPW == 0, "a wave's units must not straddle an expert");
 
 // Persistent decode kernel (qxk_layers): per-layer weight pointers and launch arguments.
 #define QXG_PBLOCKS 256   // workgroups of the persistent kernel: one per CU of an MI355X

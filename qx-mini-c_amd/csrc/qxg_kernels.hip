@@ -99,18 +99,25 @@ DEV void qkv_rows(const float *x, const float *norm_w, const uint8_t *qs, const 
     QXG_MARK(3, 4);
 }
 
-template <int RPW, bool Q8>
+// 512 workgroups, two per CU: 0..255 take 16 Q rows each (4 per wave), 256..511 take 4 K
+// or V rows each (1 per wave), so every CU holds the same 20 rows (640 workgroups of 8
+// rows left half the CUs with a third workgroup).  The branch is workgroup-uniform.
+template <bool Q8>
 __global__ __launch_bounds__(256) void qxk_qkv(const float *x, const float *norm_w, QkvW w, float *qkv, DevState *st) {
     __shared__ uint32_t s_dig[64 * DIG_STRIDE];
     __shared__ double s_red[4];
     const int wave = wave_id();
-    const int r0 = (blockIdx.x * 4 + wave) * RPW;   // grid covers exactly 5120 rows
-    const int rb = blockIdx.x * 4 * RPW;             // the workgroup's first row: one matrix
-    const int mi = rb < 4096 ? 0 : rb < 4608 ? 1 : 2;
-    const int lr0 = r0 - (mi == 0 ? 0 : mi == 1 ? 4096 : 4608);
     QXG_MARK(3, 0);
-    if (w.type[mi] == 13) qkv_rows<RPW, 13, Q8>(x, norm_w, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv, st);
-    else qkv_rows<RPW, 23, Q8>(x, norm_w, w.qs[mi], w.p1[mi], w.p2[mi], lr0, r0, s_dig, s_red, qkv, st);
+    if (blockIdx.x < 256) {
+        const int q0 = (blockIdx.x * 4 + wave) * 4;
+        if (w.type[0] == 13) qkv_rows<4, 13, Q8>(x, norm_w, w.qs[0], w.p1[0], w.p2[0], q0, q0, s_dig, s_red, qkv, st);
+        else qkv_rows<4, 23, Q8>(x, norm_w, w.qs[0], w.p1[0], w.p2[0], q0, q0, s_dig, s_red, qkv, st);
+    } else {
+        const int g0 = 4096 + ((blockIdx.x - 256) * 4 + wave);
+        const int mi = g0 < 4608 ? 1 : 2, l0 = g0 - (mi == 1 ? 4096 : 4608);
+        if (w.type[mi] == 13) qkv_rows<1, 13, Q8>(x, norm_w, w.qs[mi], w.p1[mi], w.p2[mi], l0, g0, s_dig, s_red, qkv, st);
+        else qkv_rows<1, 23, Q8>(x, norm_w, w.qs[mi], w.p1[mi], w.p2[mi], l0, g0, s_dig, s_red, qkv, st);
+    }
 }
 
 // Attention for one q head, with the per-head q/k RMSNorm (src/qx_format.c:3740-3757),
@@ -945,13 +952,11 @@ extern "C" {
 // and of the activation mode (q8: q8_k_compat).
 void qxl_qkv(hipStream_t s, const float *x, const float *nw, const QTensor *q, const QTensor *k, const QTensor *v, float *qkv,
              DevState *st, bool q8, Timer t) {
-    constexpr int RPW = QXG_QKV_RPW;
     QkvW w;
     const QTensor *m[3] = {q, k, v};
     for (int i = 0; i < 3; ++i) { w.qs[i] = m[i]->p0; w.p1[i] = m[i]->p1; w.p2[i] = m[i]->p2; w.type[i] = m[i]->type; }
-    const dim3 grid(5120 / (4 * RPW));
-    if (q8) qx_launch(qxk_qkv<RPW, true>, grid, dim3(256), 0, s, t, x, nw, w, qkv, st);
-    else qx_launch(qxk_qkv<RPW, false>, grid, dim3(256), 0, s, t, x, nw, w, qkv, st);
+    if (q8) qx_launch(qxk_qkv<true>, dim3(512), dim3(256), 0, s, t, x, nw, w, qkv, st);
+    else qx_launch(qxk_qkv<false>, dim3(512), dim3(256), 0, s, t, x, nw, w, qkv, st);
 }
 void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, float *dump, DevState *st, bool q8, Timer t) {
     constexpr int RPW = QXG_OPROJ_RPW;
