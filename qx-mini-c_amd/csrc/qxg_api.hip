@@ -20,7 +20,7 @@ __global__ void qxk_attn_merge(const DevState *, const float *, float *);
 __global__ void qxk_router(const float *, const float *, const float *, uint32_t, double *);
 __global__ void qxk_topk(const float *, uint32_t, uint32_t, float *, uint32_t *, float *, uint32_t *, uint32_t *,
                          DevState *);
-__global__ void qxk_advance(DevState *);
+__global__ void qxk_advance(DevState *, const double *, const double *);
 __global__ void qxk_q8k(const float *, uint32_t, uint8_t *, uint32_t *);
 __global__ void qxk_layers(QxPArgs);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
@@ -270,6 +270,10 @@ void write_state(qxg_ctx *c, uint32_t pos0, uint32_t step, uint32_t n_prompt, ui
     DevState h{};
     h.pos0 = pos0; h.step = step; h.n_prompt = n_prompt; h.force_head = force_head;
     (void)hipMemcpyAsync(c->st, &h, offsetof(DevState, moe_ids), hipMemcpyHostToDevice, c->s);
+    // the position's RoPE row, read by the attention kernel without waiting for the position
+    const uint64_t p = std::min<uint64_t>((uint64_t)pos0 + step, QXG_MAX_CTX - 1);
+    (void)hipMemcpyAsync(c->st->rope_c, c->T.rope_cos + p * 64, 64 * sizeof(double), hipMemcpyDeviceToDevice, c->s);
+    (void)hipMemcpyAsync(c->st->rope_s, c->T.rope_sin + p * 64, 64 * sizeof(double), hipMemcpyDeviceToDevice, c->s);
 }
 
 const QTensor *find(qxg_ctx *c, const std::string &name) {
@@ -995,7 +999,8 @@ int qxg_generate(qxg_ctx *c, const uint32_t *prompt, uint32_t n_prompt, uint32_t
         // step serves all steps; no memset nodes are recorded
         if (!hip_ok(hipStreamBeginCapture(c->s, hipStreamCaptureModeThreadLocal), err, err_len, "capture")) return 0;
         launch_step(c, 1, false);
-        hipLaunchKernelGGL(qxk_advance, dim3(1), dim3(64), 0, c->s, c->st);
+        hipLaunchKernelGGL(qxk_advance, dim3(1), dim3(64), 0, c->s, c->st, (const double *)c->T.rope_cos,
+                           (const double *)c->T.rope_sin);
         hipGraph_t g = nullptr;
         if (!hip_ok(hipStreamEndCapture(c->s, &g), err, err_len, "capture")) return 0;
         c->graph = g;
@@ -1010,7 +1015,8 @@ int qxg_generate(qxg_ctx *c, const uint32_t *prompt, uint32_t n_prompt, uint32_t
             if (!hip_ok(hipGraphLaunch(c->graph_exec, c->s), err, err_len, "graph launch")) return 0;
         } else {
             launch_step(c, 1, false);
-            hipLaunchKernelGGL(qxk_advance, dim3(1), dim3(64), 0, c->s, c->st);
+            hipLaunchKernelGGL(qxk_advance, dim3(1), dim3(64), 0, c->s, c->st, (const double *)c->T.rope_cos,
+                           (const double *)c->T.rope_sin);
         }
     }
     (void)hipEventRecord(c->e1, c->s);

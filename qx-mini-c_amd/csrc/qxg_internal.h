@@ -55,6 +55,8 @@ struct DevState {
     double moe_w[QXG_TOPK];
     uint32_t epoch;         // exchange-buffer epoch of the persistent kernel (device-advanced)
     uint32_t q8_fault;      // q8_k_compat failure of the step (QXG_Q8_*), cleared by the host
+    double rope_c[64];      // RoPE cos/sin row of the current position (pos0 + step), written
+    double rope_s[64];      // with the position by the host and by qxk_advance
 };
 
 // q8_k_compat failures, reported as the reference reports them (src/qx_format.c:3906, 4771)

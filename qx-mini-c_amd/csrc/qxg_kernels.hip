@@ -154,35 +154,39 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int qh = blockIdx.x, kvh = qh >> 3, split = blockIdx.y;
     QXG_MARK(4, 0);
-    // the inputs that do not depend on the position first: the position is a load of
-    // its own (device state), and the rows, scales and RoPE entries wait for it
+    // the inputs that do not depend on the position first (the position is a load of its
+    // own, from the device state; the RoPE row of the position is kept there as well)
     float k0 = qkv[4096 + 128 * wave + lane], k1 = qkv[4096 + 128 * wave + 64 + lane];
     const float v0 = qkv[4608 + tid], v1 = qkv[4608 + 256 + tid];
     float q0 = qkv[128 * qh + lane], q1 = qkv[128 * qh + 64 + lane];
     const float kw0 = k_norm[lane], kw1 = k_norm[64 + lane], qw0 = q_norm[lane], qw1 = q_norm[64 + lane];
-    __builtin_amdgcn_sched_barrier(0);
-    const uint32_t pos = cur_pos(st), n = pos + 1;
-    const uint32_t nsplit = (n + ATT_STAGE - 1) / ATT_STAGE;
-    if ((uint32_t)split >= nsplit) return;   // block-uniform
-    const uint32_t t0 = (uint32_t)split * ATT_STAGE, cnt = min(n - t0, (uint32_t)ATT_STAGE);
+    const double c = st->rope_c[lane], s = st->rope_s[lane];   // the position's row, kept in st
+    // the split's cached rows: their addresses depend on the split and the cache length
+    // only, so they load before the position is known (rows past the cache read the
+    // split's first row, or row 0 for a split past the cache; rows the position does not
+    // reach are never used).  16 bytes of row t0 + (tid>>3) + 32*i, chunk tid&7, i < 4.
+    const uint32_t t0 = (uint32_t)split * ATT_STAGE;
     const uint64_t base = (uint64_t)layer * ctx;
-    // staged (cached) positions t0 .. t0+nst-1; the last split's last position is pos
-    const uint32_t nst = (uint32_t)split + 1 == nsplit ? cnt - 1 : cnt;
-    // cached rows first: 16 bytes of row (tid>>3) + 32*i, chunk tid&7, i < 4.  The loads
-    // are unconditional (rows past nst read the layer's row 0, which always exists), so
-    // the compiler waits for each one where it is used rather than after each branch.
+    const uint32_t rows = t0 < ctx ? min(ctx - t0, (uint32_t)ATT_STAGE) : 0u;
+    const uint32_t r0 = t0 < ctx ? t0 : 0u;
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));   // register-promoted (a uint4 array is not)
     v4u kst[4], vst[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t t = (tid >> 3) + 32 * i;
-        const uint64_t off = (base + (t < nst ? t0 + t : 0u)) * 512 + kvh * 128 + 16 * (tid & 7);
+        const uint64_t off = (base + r0 + (t < rows ? t : 0u)) * 512 + kvh * 128 + 16 * (tid & 7);
         kst[i] = *reinterpret_cast<const v4u *>(kc + off);
         vst[i] = *reinterpret_cast<const v4u *>(vc + off);
     }
-    const uint32_t ts = (uint32_t)tid < nst ? t0 + (uint32_t)tid : 0u;
+    const uint32_t ts = r0 + ((uint32_t)tid < rows ? (uint32_t)tid : 0u);
     const float kss = ks[base + ts], vss = vs[base + ts];
-    const double c = T.rope_cos[pos * 64 + lane], s = T.rope_sin[pos * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t pos = cur_pos(st), n = pos + 1;
+    const uint32_t nsplit = (n + ATT_STAGE - 1) / ATT_STAGE;
+    if ((uint32_t)split >= nsplit) return;   // block-uniform
+    const uint32_t cnt = min(n - t0, (uint32_t)ATT_STAGE);
+    // staged (cached) positions t0 .. t0+nst-1; the last split's last position is pos
+    const uint32_t nst = (uint32_t)split + 1 == nsplit ? cnt - 1 : cnt;
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
     QXG_MARK(4, 1);
     head_norm_rope_wave(k0, k1, kw0, kw1, c, s);
@@ -806,8 +810,13 @@ extern "C" __global__ __launch_bounds__(256) void qxk_topk(const float *logits, 
     }
 }
 
-extern "C" __global__ void qxk_advance(DevState *st) {
-    if (threadIdx.x == 0) st->step = st->step + 1;
+// Next step: step + 1, and the RoPE row of its position (64 threads)
+extern "C" __global__ void qxk_advance(DevState *st, const double *rope_cos, const double *rope_sin) {
+    const uint32_t step = st->step + 1, p = min(st->pos0 + step, (uint32_t)QXG_MAX_CTX - 1);
+    const int i = threadIdx.x;
+    st->rope_c[i] = rope_cos[p * 64 + i];
+    st->rope_s[i] = rope_sin[p * 64 + i];
+    if (i == 0) st->step = step;
 }
 
 // Bit-exact block dequant from the repacked planes (the reference's op order,
