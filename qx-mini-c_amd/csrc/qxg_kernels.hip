@@ -199,6 +199,15 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
         s_q[lane] = q0;
         s_q[64 + lane] = q1;
     }
+    // stage the split's cached rows (all 128 slots; those past nst are never read); the
+    // barrier of the K/V maxima publishes them
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = (tid >> 3) + 32 * i;
+        reinterpret_cast<v4u *>(s_kst)[t * 8 + (tid & 7)] = kst[i];
+        reinterpret_cast<v4u *>(s_vst)[t * 8 + (tid & 7)] = vst[i];
+    }
+    if (tid < ATT_STAGE) { s_kss[tid] = kss; s_vss[tid] = vss; }
     // INT8 quantize K and V over all 512 values (scale = max|x|/127, 1 if zero)
     float ka = 0.0f, va = 0.0f;
     {
@@ -211,29 +220,22 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     block_max2_256(ka, va, red2);
     QXG_MARK(4, 3);
     const float kscale = ka > 0.0f ? ka / 127.0f : 1.0f, vscale = va > 0.0f ? va / 127.0f : 1.0f;
-    const uint64_t slot = base + pos;
-    const bool writer = blockIdx.x == 0 && split == 0;   // other splits never read slot pos
-    for (int i = tid; i < 512; i += 256) {
+    // values 2 tid and 2 tid + 1 (a 2-byte store each for K and V)
+    int8_t qkb[2], qvb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = 2 * tid + j;
         const float kx = s_k[i], vx = s_v[i];
         int qk = isfinite(kx) ? (int)rintf(kx / kscale) : 0;
         int qv = isfinite(vx) ? (int)rintf(vx / vscale) : 0;
-        qk = qk < -127 ? -127 : qk > 127 ? 127 : qk;
-        qv = qv < -127 ? -127 : qv > 127 ? 127 : qv;
-        if (writer) { kc[slot * 512 + i] = (int8_t)qk; vc[slot * 512 + i] = (int8_t)qv; }
-        if ((i >> 7) == kvh) { s_k8[i & 127] = (int8_t)qk; s_v8[i & 127] = (int8_t)qv; }
+        qkb[j] = (int8_t)(qk < -127 ? -127 : qk > 127 ? 127 : qk);
+        qvb[j] = (int8_t)(qv < -127 ? -127 : qv > 127 ? 127 : qv);
     }
-    if (writer && tid == 0) { ks[slot] = kscale; vs[slot] = vscale; }
-    if (writer && vcur_dump) { vcur_dump[tid] = v0; vcur_dump[256 + tid] = v1; }
+    if ((tid >> 6) == kvh) {   // this kv head's 128 values: threads 64 kvh .. 64 kvh + 63
+        reinterpret_cast<uint16_t *>(s_k8)[tid & 63] = (uint16_t)((uint8_t)qkb[0] | ((uint32_t)(uint8_t)qkb[1] << 8));
+        reinterpret_cast<uint16_t *>(s_v8)[tid & 63] = (uint16_t)((uint8_t)qvb[0] | ((uint32_t)(uint8_t)qvb[1] << 8));
+    }
     if (tid == 0) { s_scale[0] = kscale; s_scale[1] = vscale; }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t t = (tid >> 3) + 32 * i;
-        if (t < nst) {
-            reinterpret_cast<v4u *>(s_kst)[t * 8 + (tid & 7)] = kst[i];
-            reinterpret_cast<v4u *>(s_vst)[t * 8 + (tid & 7)] = vst[i];
-        }
-    }
-    if ((uint32_t)tid < nst) { s_kss[tid] = kss; s_vss[tid] = vss; }
     __syncthreads();
     QXG_MARK(4, 4);
     // local position u is t0 + u: pos from the block's own row, the others from the LDS stage
@@ -263,6 +265,15 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     if (!one && tid == 0) {
         reinterpret_cast<double *>(pp + 128)[0] = mx;
         reinterpret_cast<double *>(pp + 128)[1] = den;
+    }
+    // the current position's K/V row into the cache, last, so that no wait for these
+    // stores precedes the block's own work (other splits never read slot pos)
+    if (blockIdx.x == 0 && split == 0) {
+        const uint64_t slot = base + pos;
+        reinterpret_cast<uint16_t *>(kc + slot * 512)[tid] = (uint16_t)((uint8_t)qkb[0] | ((uint32_t)(uint8_t)qkb[1] << 8));
+        reinterpret_cast<uint16_t *>(vc + slot * 512)[tid] = (uint16_t)((uint8_t)qvb[0] | ((uint32_t)(uint8_t)qvb[1] << 8));
+        if (tid == 0) { ks[slot] = kscale; vs[slot] = vscale; }
+        if (vcur_dump) { vcur_dump[tid] = v0; vcur_dump[256 + tid] = v1; }
     }
     QXG_MARK(4, 7);
 }
