@@ -642,7 +642,7 @@ DEV void head_norm_rope_wave(float &x0, float &x1, float w0, float w1, double c,
 //     score = ks * sum_g s_g * (2^16 H_g.k + 2^8 M_g.k + L_g.k) / sqrt(hd),
 // non-finite (or a non-finite q) -> 0.  Four lanes per position; krow(t, g, k[2], ks)
 // fetches the 32 K bytes of group g of position t and the scale.  s_sc[t] <- score;
-// returns the block maximum.
+// returns the block maximum (wave maxima in redd[0..3]; attn_weights uses redd[4..7]).
 template <typename KF>
 DEV double attn_scores(const float *s_q, uint32_t *s_qd, uint32_t n, double sqrt_hd, double *s_sc, double *redd,
                        KF krow) {
@@ -697,9 +697,7 @@ DEV double attn_scores(const float *s_q, uint32_t *s_qd, uint32_t n, double sqrt
     mx = wave_max_d(mx);
     if (lane == 0) redd[wave] = mx;
     __syncthreads();
-    mx = fmax(fmax(redd[0], redd[1]), fmax(redd[2], redd[3]));
-    __syncthreads();
-    return mx;
+    return fmax(fmax(redd[0], redd[1]), fmax(redd[2], redd[3]));   // redd[0..3] not written again
 }
 // Softmax in double: e_t = exp(s_t - mx), den = sum e_t (1 if not finite and positive);
 // s_sc[t] <- (e_t / den) * vs_t, the position's weight with its V scale folded in.
@@ -715,9 +713,9 @@ DEV double attn_weights(uint32_t n, double mx, double *s_sc, double *redd, VS vs
         den += e;
     }
     den = wave_total_d(den);
-    if (lane == 0) redd[wave] = den;
+    if (lane == 0) redd[4 + wave] = den;   // redd[0..3] may still be read by the score maximum
     __syncthreads();
-    den = (redd[0] + redd[1]) + (redd[2] + redd[3]);
+    den = (redd[4] + redd[5]) + (redd[6] + redd[7]);
     if (norm) {
         if (!isfinite(den) || den <= 0.0) den = 1.0;
         for (uint32_t t = tid; t < n; t += 256) s_sc[t] = (s_sc[t] / den) * (double)vsc(t);

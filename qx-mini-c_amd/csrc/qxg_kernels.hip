@@ -146,7 +146,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     __shared__ __align__(16) float s_q[128];
     __shared__ __align__(16) uint32_t s_qd[4 * DIG_STRIDE];
     __shared__ float2 red2[4];
-    __shared__ double redd[4];
+    __shared__ double redd[8];   // score maximum [0..3], exp-sum [4..7]
     __shared__ float s_part[16][132];
     __shared__ __align__(16) int8_t s_k8[128];
     __shared__ __align__(16) int8_t s_v8[128];
