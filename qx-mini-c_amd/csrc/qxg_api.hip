@@ -503,7 +503,7 @@ bool build_arenas(qxg_ctx *c, char *err, uint64_t n) {
 }
 
 // ---- batched prefill
-constexpr uint32_t PF_EXPERT_MT = 2;                              // row tiles per expert GEMM wave
+constexpr uint32_t PF_EXPERT_MT = QXG_PF_EXPERT_MT;               // row tiles per expert GEMM wave
 constexpr uint32_t PF_SLOTS = QXP_MAX * QXG_TOPK + 32 * 128;       // expert slots, padded per expert
 constexpr uint32_t PF_MGROUPS = QXP_MAX * QXG_TOPK / 32 + 128;     // bound on expert m-groups
 

@@ -133,6 +133,10 @@ struct QxPArgs {
 
 // ---- batched prefill (qxg_prefill.hip)
 #define QXP_MAX 512   // tokens per prefill chunk
+// 32-row tiles per wave of the expert GEMMs.  One tile keeps a workgroup at 64 KiB of
+// LDS and few enough registers for two workgroups per CU: gate/up 118 -> 102 us and
+// down 87 -> 65 us per layer at T = 512 against two tiles (one workgroup per CU).
+#define QXG_PF_EXPERT_MT 1
 
 // fp16 codebooks of the prefill GEMMs (built on the host at first use)
 struct PfTables {

@@ -897,10 +897,10 @@ void qxp_launch_gemm(hipStream_t s, int kind, const PfGemm &g, const PfTables &P
         qx_launch(qxp_gemm<FMT_IQ4, 1, 1, EPI_RESID>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
         break;
     case 2:   // expert gate/up + SwiGLU: IQ2_XS
-        qx_launch(qxp_gemm<FMT_IQ2, 2, 2, EPI_SWIGLU>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+        qx_launch(qxp_gemm<FMT_IQ2, 2, QXG_PF_EXPERT_MT, EPI_SWIGLU>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
         break;
     default:  // expert down: IQ3_XXS, 32 columns per wave
-        qx_launch(qxp_gemm<FMT_IQ3, 1, 2, EPI_STORE>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+        qx_launch(qxp_gemm<FMT_IQ3, 1, QXG_PF_EXPERT_MT, EPI_STORE>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
         break;
     }
 }
