@@ -21,6 +21,8 @@ __global__ void qxk_router(const float *, const float *, const float *, uint32_t
 __global__ void qxk_topk(const float *, uint32_t, uint32_t, float *, uint32_t *, float *, uint32_t *, uint32_t *,
                          DevState *);
 __global__ void qxk_advance(DevState *, const double *, const double *);
+__global__ void qxk_topk_merge(const float *, const uint32_t *, uint32_t, uint32_t, float *, uint32_t *, uint32_t *,
+                               DevState *);
 __global__ void qxk_q8k(const float *, uint32_t, uint8_t *, uint32_t *);
 __global__ void qxk_layers(QxPArgs);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
@@ -324,6 +326,8 @@ void launch_head(qxg_ctx *c, uint32_t top_n, float *norm_dump) {
     qxl_head(c->s, c->x, c->out_norm, c->head, c->vocab, c->st, c->logits, norm_dump, c->dig, c->q8, timer_for(c, 4));
     hipLaunchKernelGGL(qxk_topk, dim3(TOPK_BLOCKS), dim3(256), 0, c->s, c->logits, c->vocab, top_n, c->cand_v,
                        c->cand_i, c->top_v, c->top_i, c->tokens, c->st);
+    hipLaunchKernelGGL(qxk_topk_merge, dim3(1), dim3(256), 0, c->s, (const float *)c->cand_v, (const uint32_t *)c->cand_i,
+                       (uint32_t)TOPK_BLOCKS, top_n, c->top_v, c->top_i, c->tokens, c->st);
 }
 
 // Sizes of the tagged exchange buffers (per slot; two slots each, layer parity).

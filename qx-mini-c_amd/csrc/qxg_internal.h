@@ -48,7 +48,7 @@ struct DevState {
     uint32_t n_prompt;      // steps < n_prompt-1 are prompt steps (no head)
     uint32_t nonfinite;     // set by the head on a non-finite logit
     uint32_t spare;         // unused (keeps the layout of the host-written prefix)
-    uint32_t ctr_topk;      // last-block ticket of the top-N kernel (reset by that block)
+    uint32_t spare2;        // unused (keeps the layout of the host-written prefix)
     uint32_t force_head;    // run the head on every step
     uint32_t pad;
     uint32_t moe_ids[QXG_TOPK];

@@ -739,9 +739,9 @@ __global__ __launch_bounds__(256) void qxk_head(const uint32_t *dig, const uint8
     }
 }
 
-// top-N (N <= 32) over logits by (value desc, index asc): each block reduces a
-// slice to N candidates, the last block merges; writes tokens[step+1] = argmax on
-// generate steps.  Round r picks the best element strictly below pick r-1 in that
+// top-N (N <= 32) over logits by (value desc, index asc): each block of qxk_topk
+// reduces a slice to N candidates, qxk_topk_merge (one block, the next launch) merges
+// them and writes tokens[step+1] = argmax on generate steps.  Round r picks the best element strictly below pick r-1 in that
 // total order, so equal values are taken in index order.
 namespace {
 DEV bool better(float v, uint32_t i, float bv, uint32_t bi) { return v > bv || (v == bv && i < bi); }
@@ -787,7 +787,6 @@ extern "C" __global__ __launch_bounds__(256) void qxk_topk(const float *logits, 
     if (prompt_step(st)) return;
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
-    __shared__ uint32_t ticket;
     const uint32_t chunk = (vocab + gridDim.x - 1) / gridDim.x;
     const uint32_t s0 = blockIdx.x * chunk, s1 = min(vocab, s0 + chunk);
     const uint32_t n = s1 > s0 ? s1 - s0 : 0;
@@ -808,17 +807,16 @@ extern "C" __global__ __launch_bounds__(256) void qxk_topk(const float *logits, 
             pv = bv; pi = bi;
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) ticket = atomicAdd(&st->ctr_topk, 1u);
-    __syncthreads();
-    if (ticket != gridDim.x - 1) return;
-    __threadfence();
-    select_topn(cand_v, cand_i, gridDim.x * topn, topn, top_v, top_i, sv, si);
-    if (threadIdx.x == 0) {
-        st->ctr_topk = 0;
-        if (st->step + 1 >= st->n_prompt) tokens[st->step + 1] = top_i[0];
-    }
+}
+// the merge of qxk_topk's per-block candidates (one block; the kernel boundary makes
+// them visible without fences), and tokens[step+1] = argmax on generate steps
+extern "C" __global__ __launch_bounds__(256) void qxk_topk_merge(const float *cand_v, const uint32_t *cand_i,
+        uint32_t blocks, uint32_t topn, float *top_v, uint32_t *top_i, uint32_t *tokens, DevState *st) {
+    if (prompt_step(st)) return;
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    select_topn(cand_v, cand_i, blocks * topn, topn, top_v, top_i, sv, si);
+    if (threadIdx.x == 0 && st->step + 1 >= st->n_prompt) tokens[st->step + 1] = top_i[0];
 }
 
 // Next step: step + 1, and the RoPE row of its position (64 threads)
