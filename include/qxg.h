@@ -180,6 +180,12 @@ int qxg_set_layer_path(qxg_ctx *ctx, int persistent);
  * the decode kernels in this mode.  Drops the recorded decode graph. */
 int qxg_set_activation(qxg_ctx *ctx, uint32_t activation_format, char *err, uint64_t err_len);
 
+/* Routing of every layer in the last step run by qxg_decode_token (or the last step of
+ * qxg_generate): ids[l*8 + r] the expert of rank r in layer l, weights[l*8 + r] its
+ * renormalised weight, as qx_apply_real_moe_layer selects them (src/qx_format.c:5265-5290).
+ * The reference keeps no such record; this is the readback the router parity tests use. */
+int qxg_decode_routing(qxg_ctx *ctx, uint32_t layers, uint32_t *ids, double *weights, char *err, uint64_t err_len);
+
 /* Same-input seam of the Q8_K quantizer the q8_k_compat kernels use: n values (a
  * multiple of 256, at most 4096) -> n/256 blocks of 292 bytes in ggml's block_q8_K
  * layout {f32 d, int8 qs[256], int16 bsums[16]}.  Replaces qx_quantize_q8_k as exposed

@@ -666,6 +666,17 @@ int qxo_moe_layer(qxo_model *m, uint32_t layer, const float *x, float *out, floa
 int qxo_attention_layer(qxo_model *m, uint32_t layer, uint32_t pos, uint32_t ctx,
                         const float *x, int8_t *kc, int8_t *vc, float *ks, float *vs,
                         float *attn_out, float *kqv_out, float *vcur_out) {
+    return qxo_attention_layer_ex(m, layer, pos, ctx, x, kc, vc, ks, vs, attn_out, kqv_out, vcur_out, 0, NULL, NULL, NULL);
+}
+
+/* The same, with the position's own INT8 K/V row and scales also written to row_k,
+ * row_v (512 codes each) and row_scales (k, v) when given; with keep_row the cache's row
+ * at [layer][pos] is left as the caller put it and attended to instead of the computed
+ * one (a same-input replay of a device's attention on its own cache rows). */
+int qxo_attention_layer_ex(qxo_model *m, uint32_t layer, uint32_t pos, uint32_t ctx,
+                           const float *x, int8_t *kc, int8_t *vc, float *ks, float *vs,
+                           float *attn_out, float *kqv_out, float *vcur_out,
+                           int keep_row, int8_t *row_k, int8_t *row_v, float *row_scales) {
     uint32_t tq, tk, tv, to;
     const float *an = (const float *)tensor_l(m, layer, "attn_norm.weight", NULL, NULL);
     const uint8_t *Wq = tensor_l(m, layer, "attn_q.weight", &tq, NULL);
@@ -676,15 +687,24 @@ int qxo_attention_layer(qxo_model *m, uint32_t layer, uint32_t pos, uint32_t ctx
     const float *kn = (const float *)tensor_l(m, layer, "attn_k_norm.weight", NULL, NULL);
     if (!an || !Wq || !Wk || !Wv || !Wo || !qn || !kn || pos >= ctx) return 0;
     float xn[2048], k[512], v[512];
-    static float q[4096], cx[4096];
+    float q[4096], cx[4096];
     qxo_rmsnorm(x, an, xn, 2048, NULL);
     if (!project(m, tk, Wk, 512, 2048, xn, k) || !project(m, tv, Wv, 512, 2048, xn, v)) return 0;
     qxo_head_rmsnorm(k, kn, 4, 128);
     qxo_rope(k, 4, 128, pos, 1000000.0);
     if (vcur_out) memcpy(vcur_out, v, sizeof(v));
     const uint64_t slot = (uint64_t)layer * ctx + pos;
-    ks[slot] = qxo_quantize_int8(k, kc + slot * 512, 512);
-    vs[slot] = qxo_quantize_int8(v, vc + slot * 512, 512);
+    int8_t k8[512], v8[512];
+    const float ksc = qxo_quantize_int8(k, k8, 512), vsc = qxo_quantize_int8(v, v8, 512);
+    if (row_k) memcpy(row_k, k8, sizeof(k8));
+    if (row_v) memcpy(row_v, v8, sizeof(v8));
+    if (row_scales) { row_scales[0] = ksc; row_scales[1] = vsc; }
+    if (!keep_row) {
+        memcpy(kc + slot * 512, k8, sizeof(k8));
+        memcpy(vc + slot * 512, v8, sizeof(v8));
+        ks[slot] = ksc;
+        vs[slot] = vsc;
+    }
     if (!project(m, tq, Wq, 4096, 2048, xn, q)) return 0;
     qxo_head_rmsnorm(q, qn, 32, 128);
     qxo_rope(q, 32, 128, pos, 1000000.0);

@@ -64,6 +64,15 @@ int qxo_attention_layer(qxo_model *m, uint32_t layer, uint32_t pos, uint32_t ctx
                         const float *x_in, int8_t *kcache, int8_t *vcache, float *kscales, float *vscales,
                         float *attn_out, float *kqv_out, float *vcur_out);
 
+/* qxo_attention_layer plus the position's computed INT8 K/V row (row_k, row_v: 512
+ * codes each; row_scales: k and v scale; each may be NULL); keep_row != 0 leaves the
+ * cache's row at [layer][pos] unchanged and attends to it (same-input replay of a
+ * device's attention on the device's own cache rows). */
+int qxo_attention_layer_ex(qxo_model *m, uint32_t layer, uint32_t pos, uint32_t ctx,
+                           const float *x_in, int8_t *kcache, int8_t *vcache, float *kscales, float *vscales,
+                           float *attn_out, float *kqv_out, float *vcur_out,
+                           int keep_row, int8_t *row_k, int8_t *row_v, float *row_scales);
+
 /* One full token: embedding (Q4_K row), layers [0, layers), optional head.
  * layer_out (may be NULL) receives layers x 2048 floats of per-layer outputs. */
 int qxo_decode_token(qxo_model *m, uint32_t token, uint32_t pos, uint32_t ctx, uint32_t layers,

@@ -29,6 +29,7 @@ _sig("qxo_tensor", [vp, ctypes.c_char_p, ctypes.POINTER(u32), vp, ctypes.POINTER
 _sig("qxo_final_head", [vp, vp, vp, vp, u32, vp, vp])
 _sig("qxo_moe_layer", [vp, u32, vp, vp, vp, vp, vp])
 _sig("qxo_attention_layer", [vp, u32, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp])
+_sig("qxo_attention_layer_ex", [vp, u32, u32, u32, vp, vp, vp, vp, vp, vp, vp, vp, c_int, vp, vp, vp])
 _sig("qxo_decode_token", [vp, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp, c_int, vp, u32, vp, vp])
 _sig("qxo_embed", [vp, u32, vp])
 _sig("qxo_matvec", [u32, vp, u32, u32, vp, vp], None)
@@ -141,6 +142,19 @@ def attention_layer(model, layer, pos, kv, x):
                                   _p(a), _p(kqv), _p(vcur)):
         raise RuntimeError("oracle attention failed")
     return a, kqv, vcur
+
+
+def attention_layer_given_row(model, layer, pos, kv, x):
+    """Attention on the cache as given, including the row at [layer][pos] (not
+    overwritten); also returns the oracle's own INT8 row for that position:
+    (attn_out, kqv, vcur, k_row, v_row, (k_scale, v_scale))."""
+    x = np.ascontiguousarray(x, np.float32)
+    a = np.zeros(2048, np.float32); kqv = np.zeros(4096, np.float32); vcur = np.zeros(512, np.float32)
+    rk = np.zeros(512, np.int8); rv = np.zeros(512, np.int8); sc = np.zeros(2, np.float32)
+    if not _o.qxo_attention_layer_ex(model._m, layer, pos, kv.ctx, _p(x), _p(kv.k), _p(kv.v), _p(kv.ks), _p(kv.vs),
+                                     _p(a), _p(kqv), _p(vcur), 1, _p(rk), _p(rv), _p(sc)):
+        raise RuntimeError("oracle attention failed")
+    return a, kqv, vcur, rk, rv, (float(sc[0]), float(sc[1]))
 
 
 def decode_token(model, token, pos, kv, layers, run_head, vocab, top_n=8):

@@ -24,7 +24,8 @@ __global__ void qxk_advance(DevState *, const double *, const double *);
 __global__ void qxk_topk_merge(const float *, const uint32_t *, uint32_t, uint32_t, float *, uint32_t *, uint32_t *,
                                DevState *);
 __global__ void qxk_q8k(const float *, uint32_t, uint8_t *, uint32_t *);
-__global__ void qxk_layers(QxPArgs);
+__global__ void qxk_decode(QxDArgs);
+__global__ void qxk_router_fold(const float *, const float *, const float *, uint32_t, float *);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
                             uint64_t, float *);
 __global__ void qxk_repack(uint32_t, const uint8_t *, uint64_t, uint8_t *, uint8_t *, uint8_t *, uint16_t *);
@@ -32,7 +33,7 @@ void qxl_qkv(hipStream_t, const float *, const float *, const QTensor *, const Q
              DevState *, bool, Timer = Timer());
 void qxl_oproj(hipStream_t, const float *, const QTensor *, float *, float *, DevState *, bool, Timer = Timer());
 void qxl_gate_up(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, Tables, const double *,
-                 uint32_t, DevState *, float *, bool, Timer = Timer());
+                 uint32_t, DevState *, float *, uint32_t *, double *, bool, Timer = Timer());
 void qxl_down(hipStream_t, const float *, const QTensor *, Tables, DevState *, float *, float *, bool,
               Timer = Timer());
 void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32_t, DevState *, float *, float *,
@@ -112,6 +113,8 @@ struct qxg_ctx {
     float *x = nullptr, *qkv = nullptr, *ctxv = nullptr, *h = nullptr, *logits = nullptr;
     float *vcur = nullptr, *attn = nullptr, *moe = nullptr, *norm = nullptr, *layer_dump = nullptr;
     double *rlog = nullptr;
+    uint32_t *route_ids = nullptr;  // [layer][8] experts of the last step, in rank order
+    double *route_w = nullptr;      // [layer][8] their renormalised weights
     float *apart = nullptr;        // per-split attention results [32 heads][QXG_MAX_SPLITS]
     uint32_t att_splits = 1;       // attention splits launched: covers every position the launches reach
     uint32_t graph_splits = 0;     // the recorded step graph's
@@ -122,14 +125,17 @@ struct qxg_ctx {
     uint64_t staging_bytes = 0;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     KernelTiming kt;
-    // persistent layer kernel: per-layer pointer table, tagged exchange buffers, abort flag
-    bool persist = false;            // layer path: persistent kernel (true) or one kernel per phase
+    // persistent decode: weight arenas, router fold, tagged exchange buffers, abort flag
+    bool persist = false;            // layer path: persistent decode kernel (true) or one kernel per phase
     bool base_mix = true;            // every layer in the benchmark mix (IQ4_XS attention, IQ2_XS/IQ3_XXS experts)
     bool q8 = false;                 // activation mode q8_k_compat (false: f32)
     bool eager = false;              // QXG_EAGER=1 at open: qxg_generate launches every step without a graph
     std::vector<void *> arenas;      // per-plane arenas of all layers' weights
     QxPlane planes[PL_COUNT] = {};
+    uint8_t *mfold = nullptr;        // router fold M = W diag(w) O of every layer (f32)
+    uint64_t mfold_stride = 0;
     uint64_t *xch = nullptr;
+    uint32_t next_ep = 0;            // epoch base of the next persistent launch
     uint32_t *abort = nullptr;
     // one decode step (embed .. head, top-1, step advance) recorded once and replayed
     hipGraph_t graph = nullptr;
@@ -318,7 +324,8 @@ void launch_moe(qxg_ctx *c, uint32_t l, float *x, float *moe_dump) {
     const LayerW &w = c->L[l];
     qx_launch(qxk_router, dim3(c->experts), dim3(256), 0, c->s, timer_for(c, 6), (const float *)x,
               w.ffn_norm, w.router, c->experts, c->rlog);
-    qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h, c->q8, timer_for(c, 0));
+    qxl_gate_up(c->s, x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h, c->route_ids + 8 * l,
+                c->route_w + 8 * l, c->q8, timer_for(c, 0));
     qxl_down(c->s, c->h, w.down, c->T, c->st, x, moe_dump, c->q8, timer_for(c, 1));
 }
 
@@ -330,59 +337,90 @@ void launch_head(qxg_ctx *c, uint32_t top_n, float *norm_dump) {
                        (uint32_t)TOPK_BLOCKS, top_n, c->top_v, c->top_i, c->tokens, c->st);
 }
 
-// Sizes of the tagged exchange buffers (per slot; two slots each, layer parity).
-constexpr uint64_t XCH_XA = 2048, XCH_XB = 2048, XCH_QKV = 5120, XCH_CX = 4096, XCH_LG = 256,
-                   XCH_HB = QXG_TOPK * QXG_FFN;
-constexpr uint64_t XCH_TOTAL = 2 * (XCH_XA + XCH_XB + XCH_QKV + XCH_CX + XCH_LG + XCH_HB);
-constexpr uint64_t PERSIST_TIMEOUT_TICKS = 200000000ull;   // 2 s of the 100 MHz wall clock
+constexpr uint64_t DECODE_WAIT_TICKS = 100000000ull;   // 1 s of the 100 MHz wall clock per wait
 
-struct Dumps {
-    float *layer = nullptr, *attn = nullptr, *moe = nullptr, *vcur = nullptr, *ctx = nullptr;
+// The persistent decode reads the weight arenas and the router fold, built for the
+// benchmark mix only, and computes in the f32 activation mode; other models and
+// q8_k_compat run one kernel per phase.
+bool persistent(const qxg_ctx *c) { return c->persist && c->base_mix && !c->q8 && c->emb && c->head && c->mfold; }
+
+struct DecodeDumps {
+    float *layer = nullptr, *res = nullptr, *logits = nullptr;
+    uint32_t *rids = nullptr;
+    double *rw = nullptr;
 };
 
-// The persistent kernel reads the weight arenas, built for the benchmark mix only, and
-// computes in the f32 activation mode; other models and q8_k_compat run one kernel per phase.
-bool persistent(const qxg_ctx *c) { return c->persist && c->base_mix && !c->q8; }
-
-// Sub-layers [s0, s1) of the token in one persistent launch (2l: attention half of
-// layer l, 2l+1: its MoE half), residual x_in -> x_out (device buffers).
-void launch_layers(qxg_ctx *c, uint32_t s0, uint32_t s1, const float *x_in, float *x_out, const Dumps &d) {
-    QxPArgs a{};
+// One cooperative launch of the persistent decode for `steps` steps from pos0 (tokens
+// already in c->tokens).  Exchange epochs advance by the launch's phases; before they
+// could wrap, the buffers are cleared and the count restarts.
+bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0, bool force_head,
+                   const DecodeDumps &d, char *err, uint64_t n) {
+    const uint64_t phases = (uint64_t)steps * QXD_PHASES(c->layers) + 1;
+    if ((uint64_t)c->next_ep + phases >= 0x7fffffffull) {
+        if (!hip_ok(hipMemsetAsync(c->xch, 0, QXD_XCH_WORDS * 8ull, c->s), err, n, "exchange buffers")) return false;
+        c->next_ep = 0;
+    }
+    QxDArgs a{};
     for (int i = 0; i < PL_COUNT; ++i) a.P[i] = c->planes[i];
-    a.s0 = s0; a.s1 = s1;
-    a.experts = c->experts;
-    a.ctx = c->kv_ctx;
+    a.M = {c->mfold, c->mfold_stride};
+    a.emb = c->emb; a.emb_row = c->emb_row;
+    a.out_norm = c->out_norm;
+    a.h_ql = c->head->p0; a.h_qh = c->head->p1; a.h_sc = (const int8_t *)c->head->p2; a.h_d = c->head->d;
+    a.vocab = c->vocab; a.layers = c->layers; a.experts = c->experts; a.ctx = c->kv_ctx;
+    a.steps = steps; a.n_prompt = n_prompt; a.pos0 = pos0; a.force_head = force_head ? 1u : 0u;
+    a.ep0 = c->next_ep;
     a.T = c->T;
     a.kc = c->kc; a.vc = c->vc; a.ks = c->ks; a.vs = c->vs;
-    a.st_w = c->st;
-    uint64_t *p = c->xch;
-    a.xa = p; p += 2 * XCH_XA;
-    a.xb = p; p += 2 * XCH_XB;
-    a.qkv = p; p += 2 * XCH_QKV;
-    a.cx = p; p += 2 * XCH_CX;
-    a.lg = p; p += 2 * XCH_LG;
-    a.hb = p;
-    a.x_in = x_in; a.x_out = x_out;
-    a.d_layer = d.layer; a.d_attn = d.attn; a.d_moe = d.moe; a.d_vcur = d.vcur; a.d_ctx = d.ctx;
+    a.tokens = c->tokens;
+    a.st = c->st;
+    a.xch = c->xch;
+    a.logits = d.logits; a.d_layer = d.layer; a.d_rids = d.rids; a.d_rw = d.rw; a.d_res = d.res;
     a.abort = c->abort;
-    a.timeout = PERSIST_TIMEOUT_TICKS;
+    a.timeout = DECODE_WAIT_TICKS;
     a.sqrt_hd = std::sqrt(128.0);
-    qx_launch(qxk_layers, dim3(QXG_PBLOCKS), dim3(256), 0, c->s, timer_for(c, 7), a);
+    c->next_ep += (uint32_t)phases;
+    void *args[] = {&a};
+    const Timer t = timer_for(c, 7);
+    if (t.e0) (void)hipEventRecord(t.e0, c->s);
+    if (!hip_ok(hipLaunchCooperativeKernel((const void *)qxk_decode, dim3(QXG_PBLOCKS), dim3(QXD_THREADS), args, 0, c->s),
+                err, n, "persistent decode launch"))
+        return false;
+    if (t.e1) (void)hipEventRecord(t.e1, c->s);
+    return true;
+}
+
+// The router fold M = W diag(w) O of every layer (see qxg_decode.hip), from the
+// bit-exact dequantized O rows, into one arena (layer l at mfold + l * stride).
+bool build_router_fold(qxg_ctx *c, char *err, uint64_t n) {
+    if (c->mfold) { (void)hipFree(c->mfold); c->mfold = nullptr; }
+    const uint64_t E = c->experts;
+    c->mfold_stride = align256(E * 4096 * 4);
+    float *o = nullptr;
+    if (!hip_ok(hipMalloc(&c->mfold, c->mfold_stride * c->layers), err, n, "router fold") ||
+        !hip_ok(hipMalloc(&o, 2048ull * 4096 * 4), err, n, "router fold"))
+        return false;
+    bool ok = true;
+    for (uint32_t l = 0; l < c->layers && ok; ++l) {
+        const LayerW &w = c->L[l];
+        const uint64_t nb = w.wo->nblocks;   // 2048 rows x 16 blocks
+        hipLaunchKernelGGL(qxk_dequant, dim3((unsigned)nb), dim3(256), 0, c->s, 23u, w.wo->p0, w.wo->p1, w.wo->p2, w.wo->d,
+                           c->T, nb, o);
+        hipLaunchKernelGGL(qxk_router_fold, dim3(16, (unsigned)((E + 3) / 4)), dim3(256), 0, c->s, w.router, w.ffn_norm,
+                           (const float *)o, (uint32_t)E, (float *)(c->mfold + l * c->mfold_stride));
+        ok = hip_ok(hipGetLastError(), err, n, "router fold");
+    }
+    ok = ok && hip_ok(hipStreamSynchronize(c->s), err, n, "router fold");
+    (void)hipFree(o);
+    return ok;
 }
 
 void launch_step(qxg_ctx *c, uint32_t top_n, bool dump_layers) {
     hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
-    Dumps d;
-    if (dump_layers) d.layer = c->layer_dump;
-    if (persistent(c)) {
-        if (c->layers) launch_layers(c, 0, 2 * c->layers, c->x, c->x, d);
-    } else {
-        for (uint32_t l = 0; l < c->layers; ++l) {
-            launch_attention(c, l, c->x, nullptr, nullptr);
-            launch_moe(c, l, c->x, nullptr);
-            if (dump_layers)
-                (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * sizeof(float), hipMemcpyDeviceToDevice, c->s);
-        }
+    for (uint32_t l = 0; l < c->layers; ++l) {
+        launch_attention(c, l, c->x, nullptr, nullptr);
+        launch_moe(c, l, c->x, nullptr);
+        if (dump_layers)
+            (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * sizeof(float), hipMemcpyDeviceToDevice, c->s);
     }
     if (c->head) launch_head(c, top_n, nullptr);
 }
@@ -393,7 +431,7 @@ bool check_abort(qxg_ctx *c, char *err, uint64_t n) {
     if (!hip_ok(hipMemcpy(&f, c->abort, 4, hipMemcpyDeviceToHost), err, n, "abort flag")) return false;
     if (!f) return true;
     (void)hipMemset(c->abort, 0, 4);
-    set_err(err, n, "persistent layer kernel: a wait timed out (a workgroup never produced its phase output)");
+    set_err(err, n, "persistent decode: a wait timed out (a workgroup never produced its phase output)");
     return false;
 }
 
@@ -685,10 +723,12 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
         if (err && err_len) snprintf(err, (size_t)err_len, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
         return 0;
     }
-    {   // the persistent layer kernel keeps one workgroup resident on each of QXG_PBLOCKS CUs
-        int occ = 0;
+    {   // the persistent decode keeps one workgroup resident on each of QXG_PBLOCKS CUs (a
+        // cooperative launch, which fails rather than run if they cannot all be resident)
+        int occ = 0, coop = 0;
         if (prop.multiProcessorCount < QXG_PBLOCKS ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_layers, 256, 0) != hipSuccess || occ < 1) {
+            hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device) != hipSuccess || !coop ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_decode, QXD_THREADS, 0) != hipSuccess || occ < 1) {
             if (err && err_len)
                 snprintf(err, (size_t)err_len, "device %d has %d CUs; the persistent decode kernel needs %d resident workgroups",
                          device, prop.multiProcessorCount, QXG_PBLOCKS);
@@ -735,8 +775,8 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
     ok = ok && hip_ok(hipMalloc(&c->st, sizeof(DevState)), err, err_len, "state") &&
          hip_ok(hipMemset(c->st, 0, sizeof(DevState)), err, err_len, "state");
     // tagged exchange buffers start at epoch 0, which no launch uses
-    ok = ok && hip_ok(hipMalloc(&c->xch, XCH_TOTAL * 8), err, err_len, "exchange buffers") &&
-         hip_ok(hipMemset(c->xch, 0, XCH_TOTAL * 8), err, err_len, "exchange buffers") &&
+    ok = ok && hip_ok(hipMalloc(&c->xch, QXD_XCH_WORDS * 8ull), err, err_len, "exchange buffers") &&
+         hip_ok(hipMemset(c->xch, 0, QXD_XCH_WORDS * 8ull), err, err_len, "exchange buffers") &&
          hip_ok(hipMalloc(&c->abort, 4), err, err_len, "abort flag") &&
          hip_ok(hipMemset(c->abort, 0, 4), err, err_len, "abort flag");
     ok = ok && hip_ok(hipEventCreate(&c->e0), err, err_len, "event") && hip_ok(hipEventCreate(&c->e1), err, err_len, "event");
@@ -754,7 +794,7 @@ void qxg_close(qxg_ctx *c) {
     void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->T.g2s, c->T.g3s, c->T.sel8, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
                     c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging,
-                    c->xch, c->abort, c->apart};
+                    c->xch, c->abort, c->apart, c->route_ids, c->route_w, c->mfold};
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (void *p : c->arenas) (void)hipFree(p);
     for (void *p : c->pf.all) (void)hipFree(p);
@@ -858,17 +898,21 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     void **bufs[] = {(void **)&c->x, (void **)&c->qkv, (void **)&c->ctxv, (void **)&c->h, (void **)&c->logits,
                      (void **)&c->vcur, (void **)&c->attn, (void **)&c->moe, (void **)&c->norm,
                      (void **)&c->layer_dump, (void **)&c->rlog, (void **)&c->cand_v, (void **)&c->top_v,
-                     (void **)&c->cand_i, (void **)&c->top_i, (void **)&c->tokens, (void **)&c->dig, (void **)&c->apart};
+                     (void **)&c->cand_i, (void **)&c->top_i, (void **)&c->tokens, (void **)&c->dig, (void **)&c->apart,
+                     (void **)&c->route_ids, (void **)&c->route_w};
     for (void **b : bufs) if (*b) { (void)hipFree(*b); *b = nullptr; }
     const uint64_t V = c->vocab ? c->vocab : 1;
     const uint64_t sizes[] = {2048 * 4, 5120 * 4, 4096 * 4, 8 * 768 * 4, V * 4, 512 * 4, 2048 * 4, 2048 * 4, 2048 * 4,
                               (uint64_t)(layers ? layers : 1) * 2048 * 4, 128 * 8, TOPK_BLOCKS * QXG_MAX_TOPN * 4,
                               QXG_MAX_TOPN * 4, TOPK_BLOCKS * QXG_MAX_TOPN * 4, QXG_MAX_TOPN * 4,
-                              (QXG_MAX_CTX + 2) * 4, (64 * 28 + 4) * 4, QXG_ATT_PART_BYTES};
+                              (QXG_MAX_CTX + 2) * 4, (64 * 28 + 4) * 4, QXG_ATT_PART_BYTES,
+                              (uint64_t)(layers ? layers : 1) * 8 * 4, (uint64_t)(layers ? layers : 1) * 8 * 8};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i)
         if (!hip_ok(hipMalloc(bufs[i], sizes[i]), err, err_len, "work buffers")) return 0;
     if (!hip_ok(hipMemset(c->tokens, 0, sizes[15]), err, err_len, "work buffers")) return 0;
     if (layers && base && !build_arenas(c, err, err_len)) return 0;
+    if (c->mfold) { (void)hipFree(c->mfold); c->mfold = nullptr; }
+    if (layers && base && !build_router_fold(c, err, err_len)) return 0;
     c->bound = true;
     return 1;
 }
@@ -938,20 +982,29 @@ int qxg_decode_token(qxg_ctx *c, uint32_t token, uint32_t position, int run_head
     (void)hipSetDevice(c->device);
     (void)hipMemcpyAsync(c->tokens, &token, 4, hipMemcpyHostToDevice, c->s);
     write_state(c, position, 0, run_head ? 1 : 2, 0);
-    hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
-    Dumps d;
-    if (layer_out) d.layer = c->layer_dump;
-    if (persistent(c)) {
-        if (c->layers) launch_layers(c, 0, 2 * c->layers, c->x, c->x, d);
+    if (persistent(c) && c->layers) {
+        // one step of the persistent decode (its head writes every logit), then the top-N
+        // of those logits by the per-phase selection kernels
+        DecodeDumps d;
+        d.layer = c->layer_dump; d.res = c->x; d.rids = c->route_ids; d.rw = c->route_w;
+        d.logits = run_head ? c->logits : nullptr;
+        if (!launch_decode(c, 1, run_head ? 1 : 2, position, false, d, err, err_len)) return 0;
+        if (run_head) {
+            hipLaunchKernelGGL(qxk_topk, dim3(TOPK_BLOCKS), dim3(256), 0, c->s, c->logits, c->vocab, top_n, c->cand_v,
+                               c->cand_i, c->top_v, c->top_i, c->tokens, c->st);
+            hipLaunchKernelGGL(qxk_topk_merge, dim3(1), dim3(256), 0, c->s, (const float *)c->cand_v,
+                               (const uint32_t *)c->cand_i, (uint32_t)TOPK_BLOCKS, top_n, c->top_v, c->top_i, c->tokens, c->st);
+        }
     } else {
+        hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
         for (uint32_t l = 0; l < c->layers; ++l) {
             launch_attention(c, l, c->x, nullptr, nullptr);
             launch_moe(c, l, c->x, nullptr);
             if (layer_out)
                 (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * 4, hipMemcpyDeviceToDevice, c->s);
         }
+        if (run_head) launch_head(c, top_n, nullptr);
     }
-    if (run_head) launch_head(c, top_n, nullptr);
     if (!finish(c, err, err_len)) return 0;
     if (residual_out && !hip_ok(hipMemcpy(residual_out, c->x, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
     if (layer_out && !hip_ok(hipMemcpy(layer_out, c->layer_dump, 2048ull * 4 * c->layers, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
@@ -984,6 +1037,18 @@ int qxg_generate(qxg_ctx *c, const uint32_t *prompt, uint32_t n_prompt, uint32_t
     (void)hipMemcpyAsync(c->tokens, prompt, (uint64_t)n_prompt * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, pos0, 0, n_prompt, 0);
     c->kt.used = 0;
+    if (persistent(c) && c->layers) {   // every step in one cooperative launch
+        (void)hipEventRecord(c->e0, c->s);
+        if (!launch_decode(c, (uint32_t)steps, n_prompt, pos0, false, DecodeDumps(), err, err_len)) return 0;
+        (void)hipEventRecord(c->e1, c->s);
+        if (!finish(c, err, err_len)) return 0;
+        if (elapsed_ms) (void)hipEventElapsedTime(elapsed_ms, c->e0, c->e1);
+        DevState h;
+        if (!read_state(c, h, err, err_len)) return 0;
+        if (tokens_out && !hip_ok(hipMemcpy(tokens_out, c->tokens + n_prompt, (uint64_t)n_gen * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+        if (h.nonfinite) { write_state(c, 0, 0, 0, 0); set_err(err, err_len, "non-finite final logit"); return 0; }
+        return 1;
+    }
     // in-situ kernel timing records events per launch, and QXG_EAGER asks for plain launches
     // (kernel tracers): run eagerly
     const bool use_graph = c->kt.which < 0 && !c->eager;
@@ -1099,13 +1164,7 @@ int qxg_attention_layer(qxg_ctx *c, uint32_t layer, uint32_t position, const flo
     (void)hipSetDevice(c->device);
     (void)hipMemcpyAsync(c->x, x_in, 2048 * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, position, 0, 1, 1);
-    if (persistent(c)) {
-        Dumps d;
-        d.attn = c->attn; d.vcur = c->vcur; d.ctx = c->ctxv;
-        launch_layers(c, 2 * layer, 2 * layer + 1, c->x, c->x, d);
-    } else {
-        launch_attention(c, layer, c->x, c->attn, c->vcur);
-    }
+    launch_attention(c, layer, c->x, c->attn, c->vcur);
     if (!finish(c, err, err_len)) return 0;
     if (attn_out && !hip_ok(hipMemcpy(attn_out, c->attn, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
     if (kqv_out && !hip_ok(hipMemcpy(kqv_out, c->ctxv, 4096 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
@@ -1120,13 +1179,7 @@ int qxg_moe_layer(qxg_ctx *c, uint32_t layer, const float *ffn_inp, float *layer
     (void)hipSetDevice(c->device);
     (void)hipMemcpyAsync(c->x, ffn_inp, 2048 * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, 0, 0, 1, 1);
-    if (persistent(c)) {
-        Dumps d;
-        d.moe = c->moe;
-        launch_layers(c, 2 * layer + 1, 2 * layer + 2, c->x, c->x, d);
-    } else {
-        launch_moe(c, layer, c->x, c->moe);
-    }
+    launch_moe(c, layer, c->x, c->moe);
     if (!finish(c, err, err_len)) return 0;
     DevState h;
     if (!read_state(c, h, err, err_len)) return 0;
@@ -1178,7 +1231,10 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
         const uint32_t l = (layer + i) % c->layers;
         const LayerW &w = c->L[l];
         switch (which) {
-        case 0: qxl_gate_up(c->s, c->x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h, c->q8); break;
+        case 0:
+            qxl_gate_up(c->s, c->x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, c->experts, c->st, c->h, c->route_ids + 8 * l,
+                        c->route_w + 8 * l, c->q8);
+            break;
         case 1: qxl_down(c->s, c->h, w.down, c->T, c->st, c->attn, nullptr, c->q8); break;
         case 2: qxl_qkv(c->s, c->x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv, c->st, c->q8); break;
         case 3: qxl_oproj(c->s, c->ctxv, w.wo, c->attn, nullptr, c->st, c->q8); break;
@@ -1206,6 +1262,15 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
 }
 
 uint64_t qxg_device_bytes(const qxg_ctx *c) { return c ? c->dev_bytes : 0; }
+
+int qxg_decode_routing(qxg_ctx *c, uint32_t layers, uint32_t *ids, double *weights, char *err, uint64_t err_len) {
+    if (!check_ready(c, false, err, err_len)) return 0;
+    if (!layers || layers > c->layers || !ids || !weights) { set_err(err, err_len, "invalid argument"); return 0; }
+    (void)hipSetDevice(c->device);
+    return hip_ok(hipStreamSynchronize(c->s), err, err_len, "stream") &&
+           hip_ok(hipMemcpy(ids, c->route_ids, (uint64_t)layers * 8 * 4, hipMemcpyDeviceToHost), err, err_len, "read") &&
+           hip_ok(hipMemcpy(weights, c->route_w, (uint64_t)layers * 8 * 8, hipMemcpyDeviceToHost), err, err_len, "read");
+}
 
 int qxg_set_layer_path(qxg_ctx *c, int persistent) {
     if (!c) return 0;

@@ -53,7 +53,7 @@ struct DevState {
     uint32_t pad;
     uint32_t moe_ids[QXG_TOPK];
     double moe_w[QXG_TOPK];
-    uint32_t epoch;         // exchange-buffer epoch of the persistent kernel (device-advanced)
+    uint32_t epoch;         // unused (keeps the layout)
     uint32_t q8_fault;      // q8_k_compat failure of the step (QXG_Q8_*), cleared by the host
     double rope_c[64];      // RoPE cos/sin row of the current position (pos0 + step), written
     double rope_s[64];      // with the position by the host and by qxk_advance
@@ -94,8 +94,8 @@ struct Tables {
 #endif
 static_assert(768 % QXG_GU_UPW == 0, "a wave's units must not straddle an expert");
 
-// Persistent decode kernel (qxk_layers): per-layer weight pointers and launch arguments.
-#define QXG_PBLOCKS 256   // workgroups of the persistent kernel: one per CU of an MI355X
+// Persistent decode kernel (qxk_decode): per-layer weight pointers and launch arguments.
+#define QXG_PBLOCKS 256   // workgroups of the persistent decode kernel: one per CU of an MI355X
 
 // One plane of a per-layer tensor kind: the planes of all layers lie back to back in
 // one device arena, layer l's at base + l * stride, so a kernel forms every layer's
@@ -113,23 +113,41 @@ enum QxPlaneId : int {
     PL_COUNT
 };
 
-struct QxPArgs {
-    QxPlane P[PL_COUNT];        // per-layer weight planes
-    uint32_t s0, s1;            // sub-layers [s0, s1): 2l = attention half of layer l, 2l+1 = its MoE half
-    uint32_t experts, ctx;      // routed experts; KV context length
+// Arguments of the persistent decode kernel qxk_decode (qxg_decode.hip), built by the host
+// for the benchmark quant mix.
+struct QxDArgs {
+    QxPlane P[PL_COUNT];         // per-layer weight planes (layer l at base + l * stride)
+    QxPlane M;                   // router fold M = W diag(w) O, [experts][4096] f32 per layer
+    const uint8_t *emb;          // Q4_K token embedding
+    uint64_t emb_row;
+    const float *out_norm;
+    const uint8_t *h_ql, *h_qh;  // Q6_K head planes
+    const int8_t *h_sc;
+    const uint16_t *h_d;
+    uint32_t vocab, layers, experts, ctx;
+    uint32_t steps, n_prompt, pos0, force_head;
+    uint32_t ep0;                // epoch base of the launch (its phases are ep0 + 1 ...)
     Tables T;
     int8_t *kc, *vc;
     float *ks, *vs;
-    DevState *st_w;
-    // tagged exchange buffers, two slots each (layer parity)
-    uint64_t *xa, *xb, *qkv, *cx, *lg, *hb;
-    const float *x_in;          // residual entering sub-layer s0
-    float *x_out;               // residual leaving sub-layer s1-1 (may alias x_in)
-    float *d_layer, *d_attn, *d_moe, *d_vcur, *d_ctx;   // optional dumps (null: off)
-    uint32_t *abort;            // set on a timed-out wait; the host reports it
-    uint64_t timeout;           // wait deadline in 100 MHz ticks from kernel start
+    uint32_t *tokens;            // tokens[0 .. n_prompt) in; generated ids stored at [step + 1]
+    DevState *st;                // nonfinite flag
+    uint64_t *xch;               // tagged exchange buffers (QXD_XCH_WORDS words, zeroed once)
+    float *logits;               // optional: the last head step's logits
+    float *d_layer;              // optional dumps of the last step: per-layer output residuals,
+    uint32_t *d_rids;            // routed experts and renormalised weights per layer, the
+    double *d_rw;                // final residual
+    float *d_res;
+    uint32_t *abort;             // set on a timed-out wait; the host reports it
+    uint64_t timeout;            // per wait, in 100 MHz ticks
     double sqrt_hd;
 };
+#define QXD_THREADS 512
+// exchange words per launch: x, qkv, ctx, x', router logits, h, expert weights (two slots
+// each) and the per-workgroup argmax candidates
+#define QXD_XCH_WORDS (2u * (2048u + 5120u + 4096u + 2048u + 256u + 6144u + 16u + 2u * QXG_PBLOCKS))
+// phases per step (five exchanges per layer, the head input, the argmax)
+#define QXD_PHASES(layers) (5u * (layers) + 2u)
 
 // ---- batched prefill (qxg_prefill.hip)
 #define QXP_MAX 512   // tokens per prefill chunk

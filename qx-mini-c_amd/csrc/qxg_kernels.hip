@@ -448,7 +448,7 @@ DEV float gu_dot(gu4 u, const Dig &g, const uint4 *G, const uint2 *SEL) {
 
 template <int UPW, int FMT, bool Q8>
 __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *norm_w, GuW gw, GuW uw, Tables T,
-        const double *logits, uint32_t experts, DevState *st, float *h) {
+        const double *logits, uint32_t experts, DevState *st, float *h, uint32_t *route_ids, double *route_w) {
     constexpr int NG = FMT == 17 ? 512 : 1024, NS = FMT == 17 ? 128 : 256;
     __shared__ uint4 s_g2[NG];
     __shared__ uint2 s_sel[NS];
@@ -498,7 +498,12 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
         wave_top8_weights(l0, l1, ids, wts);
 #pragma unroll
         for (int q = 0; q < QXG_TOPK; ++q)
-            if (lane == q) { st->moe_ids[q] = ids[q]; st->moe_w[q] = wts[q]; }
+            if (lane == q) {
+                st->moe_ids[q] = ids[q];
+                st->moe_w[q] = wts[q];
+                route_ids[q] = ids[q];   // the layer's routing, kept for qxg_decode_routing
+                route_w[q] = wts[q];
+            }
     }
     QXG_MARK(1, 7);
 #pragma unroll
@@ -984,11 +989,14 @@ void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, flo
     else q8 ? go(qxk_oproj<RPW, 23, true>) : go(qxk_oproj<RPW, 23, false>);
 }
 void qxl_gate_up(hipStream_t s, const float *x, const float *nw, const QTensor *g, const QTensor *u, Tables T,
-                 const double *logits, uint32_t experts, DevState *st, float *h, bool q8, Timer t) {
+                 const double *logits, uint32_t experts, DevState *st, float *h, uint32_t *route_ids, double *route_w,
+                 bool q8, Timer t) {
     constexpr int UPW = QXG_GU_UPW;
     const GuW gw{g->p0, g->p1, g->p2, g->d}, uw{u->p0, u->p1, u->p2, u->d};
     const dim3 grid(QXG_TOPK * QXG_FFN / (4 * UPW));
-    auto go = [&](auto kernel) { qx_launch(kernel, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h); };
+    auto go = [&](auto kernel) {
+        qx_launch(kernel, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h, route_ids, route_w);
+    };
     if (g->type == 22) q8 ? go(qxk_gate_up<UPW, 22, true>) : go(qxk_gate_up<UPW, 22, false>);
     else q8 ? go(qxk_gate_up<UPW, 17, true>) : go(qxk_gate_up<UPW, 17, false>);
 }

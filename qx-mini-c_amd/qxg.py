@@ -67,6 +67,7 @@ _sig(_g, "qxg_kvsnap_read", [cp, u32, u32, u32, vp, vp, vp, vp, ctypes.POINTER(u
 _sig(_g, "qxg_prefill", [vp, vp, u32, u32, c_int, vp, vp, u32, vp, vp, ctypes.POINTER(c_float), *ERR])
 _sig(_g, "qxg_prefill_layer", [vp, u32, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_time_kernel", [vp, c_int, u32, u32, ctypes.POINTER(c_float), *ERR])
+_sig(_g, "qxg_decode_routing", [vp, u32, vp, vp, *ERR])
 _sig(_g, "qxg_device_bytes", [vp], u64)
 _sig(_g, "qxg_profile_kernel", [vp, c_int])
 _sig(_g, "qxg_profile_result", [vp, ctypes.POINTER(u32), ctypes.POINTER(c_double)])
@@ -237,6 +238,13 @@ class Context:
         self._check(_g.qxg_decode_token(self._c, token, pos, int(run_head), _p(res), _p(lay), _p(lg), top_n, _p(ids),
                                         _p(tl), self._err, 1024))
         return res, lay, lg, ids, tl
+
+    def routing(self, layers=None):
+        """(ids [layers, 8], weights [layers, 8]) of every layer in the last decode step."""
+        n = self.info.layers if layers is None else layers
+        ids = np.zeros((n, 8), np.uint32); w = np.zeros((n, 8), np.float64)
+        self._check(_g.qxg_decode_routing(self._c, n, _p(ids), _p(w), self._err, 1024))
+        return ids, w
 
     def generate(self, prompt, n_gen, pos0=0):
         prompt = np.ascontiguousarray(prompt, np.uint32)

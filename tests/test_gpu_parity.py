@@ -13,9 +13,19 @@ BLOCK_BYTES = {12: 144, 13: 176, 14: 210, 17: 74, 18: 98, 21: 110, 22: 82, 23: 1
 D_OFFSET = {12: 0, 13: 0, 14: 208, 17: 0, 18: 0, 21: 0, 22: 0, 23: 0}
 
 
+@pytest.fixture(scope="module")
+def ctx():
+    """The replay seams (dequant, head, MoE, attention) run the per-phase kernels on either
+    layer path."""
+    c = qxg.Context(0)
+    yield c
+    c.close()
+
+
 @pytest.fixture(scope="module", params=[0, 1], ids=["per_phase", "persistent"])
-def ctx(request):
-    """Both layer paths: one kernel per phase, and the persistent layer kernel."""
+def dctx(request):
+    """Decode steps and the greedy loop on both layer paths: one kernel per phase, and the
+    persistent decode (every step of a call in one launch)."""
     c = qxg.Context(0)
     c.set_layer_path(request.param)
     c.layer_path = request.param
@@ -155,53 +165,53 @@ def test_attention_block_config3(ctx, layer_model, pos, ctx_tokens):
     assert abs(gks[0] / okv.ks[0, pos] - 1) < 1e-5 and abs(gvs[0] / okv.vs[0, pos] - 1) < 1e-5
 
 
-def test_generate_across_attention_splits(ctx, tmp_path):
+def test_generate_across_attention_splits(dctx, tmp_path):
     """The recorded step graph launches the attention splits its positions need (two for
     positions 118..138) while eager steps launch the whole cache's (four at 512): the
     context depends only on the position, so both give the same tokens, and the graph
     is recorded again when a later call needs more splits (positions 250..260)."""
     p = tmp_path / "splits.qxf"
     qxg.generate_model(p, layers=2, vocab=4096, experts=32, seed=45)
-    ctx.load(p)
-    ctx.kv_create(2, 512)
+    dctx.load(p)
+    dctx.kv_create(2, 512)
     rng = np.random.default_rng(12)
     pre = rng.integers(0, 4096, size=118).astype(np.uint32)
-    ctx.prefill(pre, 0, False, 1)
+    dctx.prefill(pre, 0, False, 1)
     toks, t = [], 17
     for s in range(118, 139):
-        _, _, _, ids, _ = ctx.decode_token(t, s, True, 1)
+        _, _, _, ids, _ = dctx.decode_token(t, s, True, 1)
         t = int(ids[0])
         toks.append(t)
     for rep in range(2):
-        ctx.kv_create(2, 512)
-        ctx.prefill(pre, 0, False, 1)
-        gen, _ = ctx.generate([17], 21, pos0=118)
+        dctx.kv_create(2, 512)
+        dctx.prefill(pre, 0, False, 1)
+        gen, _ = dctx.generate([17], 21, pos0=118)
         assert list(gen) == toks, rep
     pre2 = rng.integers(0, 4096, size=250).astype(np.uint32)
-    ctx.kv_create(2, 512)
-    ctx.prefill(pre2, 0, False, 1)
-    gen2, _ = ctx.generate([5], 11, pos0=250)
-    ctx.kv_create(2, 512)
-    ctx.prefill(pre2, 0, False, 1)
+    dctx.kv_create(2, 512)
+    dctx.prefill(pre2, 0, False, 1)
+    gen2, _ = dctx.generate([5], 11, pos0=250)
+    dctx.kv_create(2, 512)
+    dctx.prefill(pre2, 0, False, 1)
     toks2, t = [], 5
     for s in range(250, 261):
-        _, _, _, ids, _ = ctx.decode_token(t, s, True, 1)
+        _, _, _, ids, _ = dctx.decode_token(t, s, True, 1)
         t = int(ids[0])
         toks2.append(t)
     assert list(gen2) == toks2
 
 
-def test_decode_two_layers_greedy(ctx, tmp_path):
+def test_decode_two_layers_greedy(dctx, tmp_path):
     """Embedding + 2 layers + head, 5 greedy steps; per-step residual and tokens."""
     p = tmp_path / "two.qxf"
     qxg.generate_model(p, layers=2, vocab=4096, experts=32, seed=44)
-    ctx.load(p)
-    ctx.kv_create(2, 16)
+    dctx.load(p)
+    dctx.kv_create(2, 16)
     om = qxo.Model(p)
     okv = qxo.KV(2, 16)
     tok_g = tok_o = 17
     for s in range(5):
-        res, lay, lg, ids, tl = ctx.decode_token(tok_g, s, True, 4, want_layers=True, want_logits=True)
+        res, lay, lg, ids, tl = dctx.decode_token(tok_g, s, True, 4, want_layers=True, want_logits=True)
         ores, olay, olg, oids, otl = qxo.decode_token(om, tok_o, s, okv, 2, True, 4096, 4)
         assert rel_l2(lay, olay) <= 1e-4, (s, rel_l2(lay, olay))
         assert rel_l2(lg, olg) <= 1e-4
@@ -211,26 +221,26 @@ def test_decode_two_layers_greedy(ctx, tmp_path):
     om.close()
     # the device-resident greedy loop (one recorded step replayed per token) gives the
     # same tokens as the eager step-by-step path, on every replay, interleaved with eager work
-    ctx.kv_create(2, 16)
+    dctx.kv_create(2, 16)
     toks = []
     t = 17
     for s in range(5):
-        _, _, _, ids, _ = ctx.decode_token(t, s, True, 1)
+        _, _, _, ids, _ = dctx.decode_token(t, s, True, 1)
         t = int(ids[0])
         toks.append(t)
     for rep in range(3):
-        ctx.kv_create(2, 16)
-        gen, ms = ctx.generate([17], 5)
+        dctx.kv_create(2, 16)
+        gen, ms = dctx.generate([17], 5)
         assert list(gen) == toks, rep
-        ctx.kv_create(2, 16)
-        ctx.decode_token(17, 0, True, 1)             # eager work between replays
-        gen2, _ = ctx.generate([toks[0]], 4, pos0=1)  # continue from position 1
+        dctx.kv_create(2, 16)
+        dctx.decode_token(17, 0, True, 1)             # eager work between replays
+        gen2, _ = dctx.generate([toks[0]], 4, pos0=1)  # continue from position 1
         assert list(gen2) == toks[1:], rep
     # eager (per-launch timed) loop agrees with the replayed one
-    ctx.kv_create(2, 16)
-    ctx.profile_kernel(qxg.KERNELS["layers" if ctx.layer_path else "gate_up"])
-    gen3, _ = ctx.generate([17], 5)
-    n, _ = ctx.profile_result()
-    ctx.profile_kernel(-1)
-    # one persistent launch per step, or one gate/up launch per layer and step
-    assert list(gen3) == toks and n == (5 if ctx.layer_path else 5 * 2)
+    dctx.kv_create(2, 16)
+    dctx.profile_kernel(qxg.KERNELS["layers" if dctx.layer_path else "gate_up"])
+    gen3, _ = dctx.generate([17], 5)
+    n, _ = dctx.profile_result()
+    dctx.profile_kernel(-1)
+    # one persistent launch for all steps, or one gate/up launch per layer and step
+    assert list(gen3) == toks and n == (1 if dctx.layer_path else 5 * 2)
