@@ -43,7 +43,7 @@
 // each workgroup's wave 0 stores s_memrealtime (100 MHz) into
 // qxd_trace_buf[layer][point][workgroup]; read back with qxd_trace_read.
 #ifdef QXD_TRACE
-__device__ unsigned long long qxd_trace_buf[49][16][256];
+__device__ unsigned long long qxd_trace_buf[49][24][256];
 extern "C" int qxd_trace_read(unsigned long long *out) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(qxd_trace_buf), sizeof(qxd_trace_buf)) == hipSuccess;
 }
@@ -181,7 +181,6 @@ struct DLds {
     double red[2 * NWV];
     uint32_t lgw[2 * 128];       // router logits (hi, lo words)
     float outw[32];              // the workgroup's outputs of a stage, gathered for one store
-    uint32_t ids[QXG_TOPK];      // the layer's routed experts (picked by wave 0)
     uint32_t flag[NWV];
     union {
         uint32_t vin[6144 + 16]; // polled ctx (4096), or h (6144) and the 8 expert weights
@@ -214,11 +213,27 @@ DEV bool block_any(bool f, DLds &S) {
 // only then every word is read, words not yet carrying the epoch being read again.  All
 // threads call it; the payloads are in dst (LDS) when it returns true.  sidx(j) < nsent:
 // word offsets of the sentinels; idx(i) < n: of the payload words (both from base).
-template <int K, typename IDX, typename SIDX>
+// EARLY: the words are read once first (one round trip when they are already there, as for
+// exchanges whose producers finished well before the wait); only if some are stale does
+// the sentinel phase follow.
+template <int K, bool EARLY = false, typename IDX, typename SIDX>
 DEV bool wait_xch(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, int nsent, SIDX sidx, DLds &S,
                   const Ctl &c) {
     const int tid = tix();
     bool ok = true;
+    if constexpr (EARLY) {
+        bool have = true;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int i = tid + NT * k;
+            if (i < n) {
+                const uint64_t w = xld(base + idx(i));
+                have = have && (uint32_t)(w >> 32) == ep;
+                dst[i] = (uint32_t)w;
+            }
+        }
+        if (!block_any(!have, S)) return true;
+    }
     for (int j = tid; j < nsent; j += NT) {
         const GLB uint64_t *p = base + sidx(j);
         uint64_t w = xld(p);
@@ -451,6 +466,8 @@ struct AttnPre {   // vector-typed fields: they stay in registers (arrays filled
     float ks;
     u32x2 v0, v1, v2, v3;
     float vs;          // V scale of position tid (the softmax loop's first pass)
+    double cs, sn;     // RoPE table entries of the position, dims lane and lane + 64
+    float n0, n1;      // k-norm weights (waves 0..3) or q-norm weights (wave 4), dims lane, lane + 64
 };
 DEV void attn_prefetch(const QxDArgs &a, uint32_t l, uint32_t pos, AttnPre &p) {
     const int tid = tix();
@@ -484,6 +501,12 @@ DEV void attn_prefetch(const QxDArgs &a, uint32_t l, uint32_t pos, AttnPre &p) {
         const uint32_t t = min((uint32_t)tid, pos > 0 ? pos - 1 : 0u);
         p.vs = __uint_as_float(t >= fresh ? ld_coherent(vsw + base + t) : vsw[base + t]);
     }
+    const int lane = tid & 63;
+    p.cs = gp(a.T.rope_cos)[pos * 64 + lane];
+    p.sn = gp(a.T.rope_sin)[pos * 64 + lane];
+    const GLB float *nw = (const GLB float *)plane(a, (tid >> 6) == 4 ? PL_Q_NORM : PL_K_NORM, l);
+    p.n0 = nw[lane];
+    p.n1 = nw[64 + lane];
 }
 
 // The Q/K/V words of head h's workgroup: q rows 128 h .. 128 h + 127, then the K and V rows
@@ -502,17 +525,15 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
     const int tid = tix(), lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x, kvh = h >> 3;
     const uint32_t n = pos + 1;
-    const double cs = gp(a.T.rope_cos)[pos * 64 + lane], sn = gp(a.T.rope_sin)[pos * 64 + lane];
+    const double cs = pre.cs, sn = pre.sn;
     if (wave < 4) {   // k of kv head `wave`
-        const GLB float *kn = (const GLB float *)plane(a, PL_K_NORM, l);
         float k0 = A.k[128 * wave + lane], k1 = A.k[128 * wave + 64 + lane];
-        head_norm_rope_wave(k0, k1, kn[lane], kn[64 + lane], cs, sn);
+        head_norm_rope_wave(k0, k1, pre.n0, pre.n1, cs, sn);
         A.k[128 * wave + lane] = k0;
         A.k[128 * wave + 64 + lane] = k1;
     } else if (wave == 4) {
-        const GLB float *qn = (const GLB float *)plane(a, PL_Q_NORM, l);
         float q0 = A.q[lane], q1 = A.q[64 + lane];
-        head_norm_rope_wave(q0, q1, qn[lane], qn[64 + lane], cs, sn);
+        head_norm_rope_wave(q0, q1, pre.n0, pre.n1, cs, sn);
         A.q[lane] = q0;
         A.q[64 + lane] = q1;
     }
@@ -687,9 +708,11 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
 }
 
 // ---------------------------------------------------------------- head
-// Output RMSNorm + Q6_K head (src/qx_format.c:3554-3738) over the digits in S.dig: rows
-// pair by pair, wave gw takes pairs gw, gw + 2048, ...; returns the workgroup's best
-// (logit desc, index asc) through bv/bi (uniform); non-finite logits set *nonfin.
+// Output RMSNorm + Q6_K head (src/qx_format.c:3554-3738) over the digits in S.dig: wave
+// gw takes rows R gw .. R gw + R - 1, then R (gw + 2048) .., R rows' loads in flight at a
+// time; returns the workgroup's best (logit desc, index asc) through bv/bi (uniform);
+// non-finite logits set *nonfin.
+template <int R>
 DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi, bool &nonfin) {
     const int tid = tix(), lane = tid & 63, wave = tid >> 6;
     const int b = lane >> 3, ib = lane & 7, hh = ib >> 2, k = ib & 3;
@@ -700,16 +723,16 @@ DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi,
     float best = -INFINITY;
     uint32_t besti = 0xffffffffu;
     bool nf = false;
-    const uint32_t pairs = (a.vocab + 1) / 2;
+    const uint32_t groups = (a.vocab + R - 1) / R;
     const GLB uint8_t *hql = gp(a.h_ql), *hqh = gp(a.h_qh), *hsc = gp((const uint8_t *)a.h_sc), *hd = gp((const uint8_t *)a.h_d);
     GLB float *lg = a.logits ? gpw(a.logits) : nullptr;
-    for (uint32_t p = gw; p < pairs; p += NWV * NWG) {
-        uint4 l0[2], l1[2], h0[2], h1[2];
-        int s0[2], s1[2];
-        uint32_t d16[2];
+    for (uint32_t p = gw; p < groups; p += NWV * NWG) {
+        uint4 l0[R], l1[R], h0[R], h1[R];
+        int s0[R], s1[R];
+        uint32_t d16[R];
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-            const uint32_t r = min(2 * p + rr, a.vocab - 1);
+        for (int rr = 0; rr < R; ++rr) {
+            const uint32_t r = min(R * p + rr, a.vocab - 1);
             const uint32_t blk = r * 8 + b;
             const uint32_t lo = blk * 128 + 64 * hh + 32 * (k & 1), ho = blk * 64 + 32 * hh;
             l0[rr] = gnt4(hql, lo); l1[rr] = gnt4(hql, lo + 16); h0[rr] = gnt4(hqh, ho); h1[rr] = gnt4(hqh, ho + 16);
@@ -717,13 +740,13 @@ DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi,
             s0[rr] = (int8_t)hsc[so]; s1[rr] = (int8_t)hsc[so + 1];
             d16[rr] = ld_u16(hd, blk * 2);
         }
-        float part[2], out[2];
+        float part[R], out[R];
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) part[rr] = dot_q6(l0[rr], l1[rr], h0[rr], h1[rr], s0[rr], s1[rr], d16[rr], ib, g, bias);
-        rows_reduce<2>(part, out, lane);
+        for (int rr = 0; rr < R; ++rr) part[rr] = dot_q6(l0[rr], l1[rr], h0[rr], h1[rr], s0[rr], s1[rr], d16[rr], ib, g, bias);
+        rows_reduce<R>(part, out, lane);
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-            const uint32_t r = 2 * p + rr;
+        for (int rr = 0; rr < R; ++rr) {
+            const uint32_t r = R * p + rr;
             if (r < a.vocab) {
                 const float v = out[rr];
                 if (!fin || !isfinite(v)) nf = true;
@@ -900,14 +923,15 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                              (double)wm1.z * (double)c1.z + (double)wm1.w * (double)c1.w;
                     b_part = wave_total_d(b_part);
                     if (lane == 0) S.red[wave] = b_part;
+                    __syncthreads();   // (uniform: wg < E)
+                    if (tid < 2) {   // the logit before the 1/rms(x') factor, (hi, lo) words
+                        const double bsum = ((S.red[0] + S.red[1]) + (S.red[2] + S.red[3])) + ((S.red[4] + S.red[5]) + (S.red[6] + S.red[7]));
+                        const uint64_t bits = (uint64_t)__double_as_longlong(a_part + bsum);
+                        xst(X + XO_LG + par * XN_LG + 2 * wg + tid, ep + 3, tid == 0 ? (uint32_t)(bits >> 32) : (uint32_t)bits);
+                    }
                 }
                 const bool ok = vec_digits<4096, false>(cx, nullptr, S);   // ends with barriers
                 DMARK(l, 14);
-                if ((uint32_t)wg < E && tid < 2) {   // the logit before the 1/rms(x') factor, (hi, lo) words
-                    const double bsum = ((S.red[0] + S.red[1]) + (S.red[2] + S.red[3])) + ((S.red[4] + S.red[5]) + (S.red[6] + S.red[7]));
-                    const uint64_t bits = (uint64_t)__double_as_longlong(a_part + bsum);
-                    xst(X + XO_LG + par * XN_LG + 2 * wg + tid, ep + 3, tid == 0 ? (uint32_t)(bits >> 32) : (uint32_t)bits);
-                }
                 Dig g0, g1;
                 load_dig(S.dig, lane, g0);
                 load_dig(S.dig, lane + 64, g1);
@@ -928,7 +952,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 const int gw = NWV * wg + wave;
                 // the E router logits first (hi and lo words; sentinels: the hi words): the
                 // top-8 and the routed experts' row loads then overlap the wait for x'
-                if (!wait_xch<1>(X + XO_LG + par * XN_LG, 2 * (int)E, ep + 3, S.lgw, Ident(), (int)E,
+                if (!wait_xch<1, true>(X + XO_LG + par * XN_LG, 2 * (int)E, ep + 3, S.lgw, Ident(), (int)E,
                                  [](int j) { return 2 * j; }, S, ctl))
                     return;
                 DMARK(l, 7);
@@ -936,29 +960,37 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 auto logit = [&](uint32_t e) {
                     return __longlong_as_double((long long)(((uint64_t)lgw[2 * e] << 32) | lgw[2 * e + 1]));
                 };
-                const double l0 = lane < (int)E ? logit(lane) : 0.0, l1 = lane + 64 < (int)E ? logit(lane + 64) : 0.0;
-                if (wave == 0) {   // one wave picks; the others wait at the barrier
+                // x' words read now, ahead of the expert rows in the load queue (they were
+                // published before the router logits, so they are normally all there)
+                const GLB uint64_t *xpb = X + XO_XP + par * XN_XP;
+                uint64_t xpw[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) xpw[k] = xld(xpb + tid + NT * k);
+                {   // every wave picks on its own (no barrier); ids are wave-uniform
+                    const double l0 = lane < (int)E ? logit(lane) : 0.0, l1 = lane + 64 < (int)E ? logit(lane + 64) : 0.0;
                     wave_top8_ids(l0, l1, (int)E, ids);
-                    if (lane < QXG_TOPK) {
-                        uint32_t il = 0u;
 #pragma unroll
-                        for (int q = 0; q < QXG_TOPK; ++q) if (lane == q) il = ids[q];
-                        S.ids[lane] = il < E ? il : 0u;
-                    }
+                    for (int q = 0; q < QXG_TOPK; ++q) ids[q] = ids[q] < E ? ids[q] : 0u;
                 }
-                __syncthreads();
-#pragma unroll
-                for (int q = 0; q < QXG_TOPK; ++q) ids[q] = S.ids[q];
+                DMARK(l, 16);
                 load_we(a, l, ids, we);
                 load_wd(a, l, ids, wd);
                 DMARK(l, 8);
-                if (!wait_xch<4>(X + XO_XP + par * XN_XP, 2048, ep + 3, reinterpret_cast<uint32_t *>(S.xp), Ident(), NWG,
-                                 [](int j) { return 8 * j; }, S, ctl))
+                bool have = true;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    have = have && (uint32_t)(xpw[k] >> 32) == ep + 3;
+                    reinterpret_cast<uint32_t *>(S.xp)[tid + NT * k] = (uint32_t)xpw[k];
+                }
+                if (block_any(!have, S) &&
+                    !wait_xch<4>(xpb, 2048, ep + 3, reinterpret_cast<uint32_t *>(S.xp), Ident(), NWG, [](int j) { return 8 * j; }, S, ctl))
                     return;
                 DMARK(l, 9);
                 double inv = 1.0;
                 (void)vec_digits<2048, true>(S.xp, fnw, S, &inv);   // h of a non-finite row is 0 by itself
+                DMARK(l, 17);
                 if (wg == 0 && wave == 0) {   // renormalised weights of the picks (reference :5265-5290)
+                    const double l0 = lane < (int)E ? logit(lane) : 0.0, l1 = lane + 64 < (int)E ? logit(lane + 64) : 0.0;
                     double wts[QXG_TOPK];
                     wave_top8_weights(l0 * inv, l1 * inv, ids, wts);
                     if (lane < 2 * QXG_TOPK) {   // lane 2q: hi word of weight q, lane 2q + 1: lo word
@@ -981,6 +1013,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 }
                 p[3] = p[7] = 0.0f;
                 rows_reduce<8>(p, o, lane);
+                DMARK(l, 18);
                 (void)ib;
                 (void)gw;
 #pragma unroll
@@ -1060,8 +1093,12 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             uint32_t bi;
             bool nonfin;
             DMARK(48, 2);
-            head_rows(a, S, fin, bv, bi, nonfin);
+            head_rows<4>(a, S, fin, bv, bi, nonfin);
             DMARK(48, 3);
+            // layer 0's rows again (also on the last step): they are then dead during the head
+            // rows, whose loads take their registers
+            load_wq(a, 0, wq);
+            load_wo(a, 0, wo);
             if (nonfin) gpw(a.st)->nonfinite = 1u;
             // workgroup best, then every workgroup reads all the bests
             for (int o = 32; o > 0; o >>= 1) {
