@@ -129,15 +129,47 @@ int qx_dump_final_head_probe_summary(const char *path, const char *residual_path
  * probe's fixed inputs (inject: none, zero, nan, inf, positive, negative, edge)
  * quantized to Q8_K blocks on the GPU; same JSON keys and block bytes. */
 int qx_dump_q8_k_activation_probe_gpu(uint32_t values, const char *inject, FILE *out, char *err, uint64_t err_len);
-/* reference qx_dump_state_loop_probe_summary (include/qx_format.h:157), restricted
- * to the --full-moe --rope-gqa-attention path with INT8 KV and f32 or q8_k_compat
- * activations:
- * every other combination is rejected with an error, as the reference rejects
- * unsupported policies.  prompt_count tokens are fed, then greedy generation. */
-int qx_dump_prompt_state_loop_gpu(const char *path, const uint32_t *prompt_tokens, uint32_t prompt_count,
-        uint32_t generation_steps, uint32_t ctx_tokens, const char *kv_format, const char *activation_format,
-        int final_head, uint32_t logits_top_n, const char *residual_dump_dir, int bench,
-        FILE *out, char *err, uint64_t err_len);
+/* reference qx_dump_state_loop_probe_summary and qx_dump_prompt_state_loop_probe_summary
+ * (include/qx_format.h:157-158), same prototypes: the state loop of
+ * src/qx_format.c:5970-6733 on the GPU.  The reference's argument checks run first, with
+ * its messages; the device path then requires --full-moe (full_moe, rope_gqa_attention and
+ * causal_attention set) and INT8 KV, and rejects the probe-level skeleton modes with an
+ * error.  Supported: prompt prefill then generation (1..64 steps), --layers below the
+ * manifest's, --start-layer/--residual-in replay, --kv-snapshot-out/--kv-snapshot-in
+ * (QXKVSNP1; the continuation token must be the snapshot's next token), --dump-residuals,
+ * --final-head (greedy, the device head) or, without it, the reference's token scan and
+ * sampler, --bench, f32 and q8_k_compat activations.  The JSON carries the reference's
+ * keys; thread/simd policies are validated and reported (the device ignores them). */
+int qx_dump_state_loop_probe_summary(const char *path, const char *tokens_path, uint32_t prompt_token, uint32_t steps,
+        uint32_t layers, uint32_t ctx_tokens, const char *kv_format, const char *activation_format, int real_kv,
+        int projection_matvec, int residual_vector, int residual_carry, int numeric_deltas, int delta_vectors,
+        int attention_output_vector, int causal_attention, int rope_gqa_attention, int full_moe, int final_head, int bench,
+        uint32_t residual_dims, const char *norm_name, uint32_t top_k, uint32_t scan, uint32_t logits_top_n,
+        double temperature, uint32_t seed, const char *residual_dump_dir, uint32_t start_layer,
+        const char *residual_input_path, const char *kv_snapshot_out_path, const char *kv_snapshot_in_path, FILE *out,
+        char *err, uint64_t err_len);
+int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens_path, const uint32_t *prompt_tokens,
+        uint32_t prompt_count, uint32_t generation_steps, uint32_t layers, uint32_t ctx_tokens, const char *kv_format,
+        const char *activation_format, const char *scratch_policy, const char *kernel_policy, const char *thread_policy,
+        uint32_t threads, const char *simd_policy, const char *expert_cache_policy, const char *cuda_policy,
+        const char *prefill_gemm_policy, const char *speculative_policy, const char *kv2_policy,
+        const char *sampling_policy, const char *long_context_policy, int dequant_profile, int real_kv,
+        int projection_matvec, int residual_vector, int residual_carry, int numeric_deltas, int delta_vectors,
+        int attention_output_vector, int causal_attention, int rope_gqa_attention, int full_moe, int final_head,
+        int bench, uint32_t residual_dims, const char *norm_name, uint32_t top_k, uint32_t scan,
+        uint32_t logits_top_n, double temperature, uint32_t seed, const char *residual_dump_dir, uint32_t start_layer,
+        const char *residual_input_path, const char *kv_snapshot_out_path, const char *kv_snapshot_in_path, FILE *out,
+        char *err, uint64_t err_len);
+/* reference qx_dump_attention_stage_probe_summary and qx_dump_moe_stage_probe_summary
+ * (include/qx_format.h:160-161), same prototypes: the single-token attention stage
+ * (src/qx_format.c:5478-5586) and the MoE stage (src/qx_format.c:5588-5725) of one layer
+ * on a sidecar input, writing the reference's sidecars (<dir>/<name>-<layer>.f32) and JSON;
+ * the stage arithmetic runs on the GPU (qxg_attention_stage, qxg_moe_stage). */
+int qx_dump_attention_stage_probe_summary(const char *path, uint32_t layer, const char *layer_input_path,
+        const char *output_dir, const char *activation_mode, const char *kv_format, FILE *out, char *err,
+        uint64_t err_len);
+int qx_dump_moe_stage_probe_summary(const char *path, uint32_t layer, const char *ffn_input_path,
+        const char *output_dir, const char *activation_mode, FILE *out, char *err, uint64_t err_len);
 
 #ifdef __cplusplus
 }

@@ -125,6 +125,33 @@ int qxg_dequant_blocks(qxg_ctx *ctx, uint32_t ggml_type, const void *raw, uint64
  * "kqv-out" and "v-cur"). */
 int qxg_attention_layer(qxg_ctx *ctx, uint32_t layer, uint32_t position, const float *x_in, float *attn_out,
                         float *kqv_out, float *vcur_out, char *err, uint64_t err_len);
+/* qxg_attention_layer plus, when head_weight_sums is non-NULL, each q head's sum of its
+ * normalised softmax weights (32 doubles): the reference reports their mean, minimum and
+ * maximum as softmax_sum, softmax_sum_min, softmax_sum_max (src/qx_format.c:5154-5189,
+ * printed at 6516-6523). */
+int qxg_attention_layer_ex(qxg_ctx *ctx, uint32_t layer, uint32_t position, const float *x_in, float *attn_out,
+                           float *kqv_out, float *vcur_out, double *head_weight_sums, char *err, uint64_t err_len);
+
+/* The attention stage probe's computation (qx_dump_attention_stage_probe_summary,
+ * src/qx_format.c:5478-5586): a single token attending to itself.  attn RMSNorm (norm_out,
+ * 2048), V projection (vcur_out, 512), each q head's context = its kv head's V row, after
+ * an fp16 round trip if f16_kv (kqv_out, 4096), O projection (attn_out, 2048), ffn_inp_out =
+ * x_in + attn_out.  Fails with the reference's message on a non-finite output.  Output
+ * pointers may be NULL. */
+int qxg_attention_stage(qxg_ctx *ctx, uint32_t layer, int f16_kv, const float *x_in, float *norm_out,
+                        float *vcur_out, float *kqv_out, float *attn_out, float *ffn_inp_out, char *err,
+                        uint64_t err_len);
+
+/* The MoE stage probe's computation (qx_dump_moe_stage_probe_summary, src/qx_format.c:
+ * 5588-5725) on ffn input x_in: f32 router logits, f32 softmax probabilities, 8 picks by
+ * probability, f32 renormalised weights, then per pick the gate, up, SwiGLU, down and
+ * weighted down rows.  out receives QXG_MOE_STAGE_FLOATS(experts) floats, in order:
+ * ffn_norm[2048], logits[E], probs[E], topk[8] (ids as floats), weights[8],
+ * weights_sum[1], weights_norm[8], gate[8][768], up[8][768], swiglu[8][768],
+ * down[8][2048], weighted[8][2048]; ids (may be NULL) the picks. */
+#define QXG_MOE_STAGE_FLOATS(E) (2048u + 2u * (E) + 25u + 3u * 8u * 768u + 2u * 8u * 2048u)
+int qxg_moe_stage(qxg_ctx *ctx, uint32_t layer, const float *x_in, float *out, uint32_t ids[8], char *err,
+                  uint64_t err_len);
 
 /* MoE block of `layer` on ffn_inp: replaces qx_apply_real_moe_layer
  * (src/qx_format.c:5198-5317).  layer_out = ffn_inp + moe; moe_out (may be NULL)

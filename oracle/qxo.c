@@ -327,9 +327,11 @@ float qxo_quantize_int8(const float *src, int8_t *dst, uint32_t n) {
 
 /* :4238-4291 (projections) and :4764-4784 (experts): per row, blocks in order,
  * acc += double(w_i) * double(x_i); store (float)acc, non-finite -> 0 */
-void qxo_matvec(uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims, const float *x, float *y) {
+static void matvec_f32(uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims, const float *x, float *y,
+                       double *probe) {
     const uint64_t bb = block_bytes(t), bpr = in_dims / 256u;
     float vals[256];
+    double sum = 0.0;
     for (uint32_t r = 0; r < rows; ++r) {
         const uint8_t *row = w + (uint64_t)r * bpr * bb;
         double acc = 0.0;
@@ -337,8 +339,14 @@ void qxo_matvec(uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims, c
             qxo_decode_block(t, row + b * bb, vals);
             for (int i = 0; i < 256; ++i) acc += (double)vals[i] * (double)x[256 * b + i];
         }
-        y[r] = isfinite(acc) ? (float)acc : 0.0f;
+        if (!isfinite(acc)) acc = 0.0;
+        y[r] = (float)acc;
+        sum += acc;   /* the probe: row dots before narrowing (:4276-4283) */
     }
+    if (probe) *probe = sum;
+}
+void qxo_matvec(uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims, const float *x, float *y) {
+    matvec_f32(t, w, rows, in_dims, x, y, NULL);
 }
 
 /* ---- q8_k_compat activation mode (:3869-4205) ----
@@ -530,12 +538,25 @@ int qxo_matvec_q8k(uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims
     return block_bytes(t) ? matvec_q8k(t, w, rows, in_dims, x, y, expert) : 0;
 }
 
-/* attention projections: Q8_K for Q5_K / Q6_K / IQ4_XS in q8_k_compat mode (:4217-4218) */
+/* attention projections: Q8_K for Q5_K / Q6_K / IQ4_XS in q8_k_compat mode (:4217-4218);
+ * *probe (may be NULL) receives the sum of the rows' dots (:4276-4287) */
+static int project_probe(const qxo_model *m, uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims,
+                         const float *x, float *y, double *probe) {
+    if (m->q8 && (t == 13 || t == 14 || t == 23)) {
+        if (!matvec_q8k(t, w, rows, in_dims, x, y, 0)) return 0;
+        if (probe) {
+            double sum = 0.0;
+            for (uint32_t r = 0; r < rows; ++r) sum += (double)y[r];
+            *probe = sum;
+        }
+        return 1;
+    }
+    matvec_f32(t, w, rows, in_dims, x, y, probe);
+    return 1;
+}
 static int project(const qxo_model *m, uint32_t t, const uint8_t *w, uint32_t rows, uint32_t in_dims,
                    const float *x, float *y) {
-    if (m->q8 && (t == 13 || t == 14 || t == 23)) return matvec_q8k(t, w, rows, in_dims, x, y, 0);
-    qxo_matvec(t, w, rows, in_dims, x, y);
-    return 1;
+    return project_probe(m, t, w, rows, in_dims, x, y, NULL);
 }
 
 typedef struct { uint32_t token; double logit; } topent;
@@ -768,5 +789,126 @@ int qxo_decode_token(qxo_model *m, uint32_t token, uint32_t pos, uint32_t ctx, u
     }
     if (residual_out) memcpy(residual_out, x, sizeof(x));
     if (run_head) return qxo_final_head(m, x, NULL, logits, top_n, top_ids, top_logits);
+    return 1;
+}
+
+/* :1878-1902 — f32 to IEEE binary16 with round-to-nearest-even, overflow to infinity,
+ * NaN to a quiet NaN of the same sign (restated from the IEEE rules) */
+uint16_t qxo_f32_to_fp16(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    const uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+    const uint32_t ex = (b >> 23) & 0xffu, man = b & 0x7fffffu;
+    if (ex == 0xffu) return (uint16_t)(sign | (man ? 0x7e00u : 0x7c00u));
+    const int e16 = (int)ex - 112;   /* rebias 127 -> 15 */
+    if (e16 >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e16 <= 0) {                  /* binary16 subnormal (or zero): value / 2^-24, rounded */
+        if (e16 < -10) return sign;
+        const uint32_t full = man | 0x800000u, sh = (uint32_t)(14 - e16);
+        uint32_t q = full >> sh;
+        const uint32_t rem = full & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+        return (uint16_t)(sign | q);   /* q == 0x400 carries into the smallest normal */
+    }
+    uint32_t q = ((uint32_t)e16 << 10) | (man >> 13);
+    const uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q;   /* a carry can reach infinity */
+    return (uint16_t)(sign | q);
+}
+
+/* attention stage probe (:5478-5586): one token attending to itself -- RMSNorm, V
+ * projection, each q head's context is its kv head's v (softmax weight 1; an fp16
+ * round trip with f16 KV), O projection, ffn_inp = x + O ctx.  probes: the V and O
+ * projections' row-dot sums.  Returns 0 on a non-finite output (:5560-5564). */
+int qxo_attention_stage(qxo_model *m, uint32_t layer, const float *x, int f16_kv, float *norm, float *vcur,
+                        float *kqv, float *attn_out, float *ffn_inp, double probes[2]) {
+    uint32_t tv, to;
+    const float *an = (const float *)tensor_l(m, layer, "attn_norm.weight", NULL, NULL);
+    const uint8_t *Wv = tensor_l(m, layer, "attn_v.weight", &tv, NULL);
+    const uint8_t *Wo = tensor_l(m, layer, "attn_output.weight", &to, NULL);
+    if (!an || !Wv || !Wo) return 0;
+    qxo_rmsnorm(x, an, norm, 2048, NULL);
+    if (!project_probe(m, tv, Wv, 512, 2048, norm, vcur, &probes[0])) return 0;
+    for (uint32_t qh = 0; qh < 32; ++qh)
+        for (uint32_t d = 0; d < 128; ++d) {
+            const float v = vcur[(qh / 8) * 128 + d];
+            kqv[qh * 128 + d] = f16_kv ? qxo_fp16_to_f32(qxo_f32_to_fp16(v)) : v;
+        }
+    if (!project_probe(m, to, Wo, 2048, 4096, kqv, attn_out, &probes[1])) return 0;
+    for (uint32_t i = 0; i < 2048; ++i) {
+        ffn_inp[i] = x[i] + attn_out[i];
+        if (!isfinite(attn_out[i]) || !isfinite(ffn_inp[i])) return 0;
+    }
+    return 1;
+}
+
+/* MoE stage probe (:5588-5725): router logits narrowed to f32, f32 softmax
+ * probabilities (exp of logit - max in double, normalised by their double sum), 8
+ * picks by probability (strictly larger, lower index on ties), f32 weights renormalised
+ * by their double sum, then per pick gate, up, SwiGLU, down and the weighted down
+ * rows.  out: the QXO_MOE_STAGE block (see qxo.h). */
+int qxo_moe_stage(qxo_model *m, uint32_t layer, const float *x, float *out, uint32_t ids[8]) {
+    uint32_t tg, tu, td, tr;
+    uint64_t dg[4], dr[4];
+    const float *nw = (const float *)tensor_l(m, layer, "ffn_norm.weight", NULL, NULL);
+    const float *R = (const float *)tensor_l(m, layer, "ffn_gate_inp.weight", &tr, dr);
+    const uint8_t *G = tensor_l(m, layer, "ffn_gate_exps.weight", &tg, dg);
+    const uint8_t *U = tensor_l(m, layer, "ffn_up_exps.weight", &tu, NULL);
+    const uint8_t *D = tensor_l(m, layer, "ffn_down_exps.weight", &td, NULL);
+    if (!nw || !R || !G || !U || !D || tr != 0) return 0;
+    const uint32_t E = (uint32_t)dr[1], F = (uint32_t)dg[1];
+    if (E < 8 || E > 128 || F != 768) return 0;
+    float *norm = out, *logits = norm + 2048, *probs = logits + E, *topk = probs + E, *wts = topk + 8,
+          *wsum = wts + 8, *wn = wsum + 1, *gate = wn + 8, *up = gate + 8 * 768, *sw = up + 8 * 768,
+          *down = sw + 8 * 768, *weighted = down + 8 * 2048;
+    qxo_rmsnorm(x, nw, norm, 2048, NULL);
+    double mx = -1.0e300;
+    for (uint32_t e = 0; e < E; ++e) {
+        double acc = 0.0;
+        for (uint32_t i = 0; i < 2048; ++i) acc += (double)R[(uint64_t)e * 2048 + i] * (double)norm[i];
+        if (!isfinite(acc)) return 0;
+        logits[e] = (float)acc;
+        if (acc > mx) mx = acc;
+    }
+    double den = 0.0;
+    for (uint32_t e = 0; e < E; ++e) { probs[e] = (float)exp((double)logits[e] - mx); den += probs[e]; }
+    if (!isfinite(den) || den <= 0.0) return 0;
+    for (uint32_t e = 0; e < E; ++e) probs[e] = (float)((double)probs[e] / den);
+    uint8_t picked[128] = {0};
+    double sum = 0.0;
+    for (int r = 0; r < 8; ++r) {
+        uint32_t best = 0;
+        float bp = -1.0f;
+        for (uint32_t e = 0; e < E; ++e) if (!picked[e] && probs[e] > bp) { best = e; bp = probs[e]; }
+        picked[best] = 1;
+        ids[r] = best;
+        topk[r] = (float)best;
+        wts[r] = bp;
+        sum += bp;
+    }
+    if (!isfinite(sum) || sum <= 0.0) return 0;
+    wsum[0] = (float)sum;
+    for (int r = 0; r < 8; ++r) wn[r] = (float)((double)wts[r] / sum);
+    const uint64_t gate_expert = (uint64_t)F * 8 * block_bytes(tg), up_expert = (uint64_t)F * 8 * block_bytes(tu),
+                   down_expert = 2048ull * (F / 256) * block_bytes(td);
+    const int gu_q8 = m->q8 && ((tg == 17 && tu == 17) || (tg == 22 && tu == 22));
+    const int dn_q8 = m->q8 && (td == 18 || td == 21 || td == 23);
+    for (int r = 0; r < 8; ++r) {
+        float *g = gate + r * 768, *u = up + r * 768, *h = sw + r * 768, *y = down + r * 2048;
+        if (gu_q8) {
+            if (!matvec_q8k(tg, G + ids[r] * gate_expert, F, 2048, norm, g, 1) ||
+                !matvec_q8k(tu, U + ids[r] * up_expert, F, 2048, norm, u, 1)) return 0;
+        } else {
+            qxo_matvec(tg, G + ids[r] * gate_expert, F, 2048, norm, g);
+            qxo_matvec(tu, U + ids[r] * up_expert, F, 2048, norm, u);
+        }
+        for (uint32_t i = 0; i < F; ++i) h[i] = (float)(silu((double)g[i]) * (double)u[i]);
+        if (dn_q8) {
+            if (!matvec_q8k(td, D + ids[r] * down_expert, 2048, F, h, y, 1)) return 0;
+        } else {
+            qxo_matvec(td, D + ids[r] * down_expert, 2048, F, h, y);
+        }
+        for (uint32_t i = 0; i < 2048; ++i) weighted[r * 2048 + i] = (float)((double)y[i] * (double)wn[r]);
+    }
     return 1;
 }

@@ -83,6 +83,22 @@ int qxo_decode_token(qxo_model *m, uint32_t token, uint32_t pos, uint32_t ctx, u
 /* Decodes the Q4_K embedding row of `token` (reference src/qx_format.c:3759-3793). */
 int qxo_embed(qxo_model *m, uint32_t token, float *x);
 
+/* f32 -> binary16 bits, round to nearest even (reference src/qx_format.c:1878-1902) */
+uint16_t qxo_f32_to_fp16(float f);
+
+/* attention stage probe (reference src/qx_format.c:5478-5586) of one layer input x:
+ * norm[2048], vcur[512], kqv[4096], attn_out[2048], ffn_inp[2048]; probes: the V and O
+ * row-dot sums.  f16_kv: the context takes an fp16 round trip. */
+int qxo_attention_stage(qxo_model *m, uint32_t layer, const float *x, int f16_kv, float *norm, float *vcur,
+                        float *kqv, float *attn_out, float *ffn_inp, double probes[2]);
+
+/* MoE stage probe (reference src/qx_format.c:5588-5725) of one ffn input x.  out holds,
+ * in order (E = experts, intermediate 768): ffn_norm[2048], logits[E], probs[E],
+ * topk[8] (ids as floats), weights[8], weights_sum[1], weights_norm[8], gate[8*768],
+ * up[8*768], swiglu[8*768], down[8*2048], weighted[8*2048]. */
+#define QXO_MOE_STAGE_FLOATS(E) (2048u + 2u * (E) + 25u + 3u * 8u * 768u + 2u * 8u * 2048u)
+int qxo_moe_stage(qxo_model *m, uint32_t layer, const float *x, float *out, uint32_t ids[8]);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,6 +36,9 @@ _sig("qxo_matvec", [u32, vp, u32, u32, vp, vp], None)
 _sig("qxo_quantize_q8k", [vp, u32, vp])
 _sig("qxo_matvec_q8k", [u32, vp, u32, u32, vp, vp, c_int])
 _sig("qxo_set_activation", [vp, c_int], None)
+_sig("qxo_f32_to_fp16", [ctypes.c_float], ctypes.c_uint16)
+_sig("qxo_attention_stage", [vp, u32, vp, c_int, vp, vp, vp, vp, vp, vp])
+_sig("qxo_moe_stage", [vp, u32, vp, vp, vp])
 
 Q8K_BYTES = 292   # ggml block_q8_K: f32 d, int8 qs[256], int16 bsums[16]
 
@@ -61,12 +64,43 @@ def decode_block(ggml_type, raw):
     return out
 
 
+def f32_to_fp16(v):
+    return int(_o.qxo_f32_to_fp16(float(v)))
+
+
+def moe_stage_floats(experts):
+    return 2048 + 2 * experts + 25 + 3 * 8 * 768 + 2 * 8 * 2048
+
+
+def split_moe_stage(block, experts):
+    """The named vectors of a MoE-stage output block (qxo.h / qxg.h layout)."""
+    names = [("ffn_norm", 2048), ("ffn_moe_logits", experts), ("ffn_moe_probs", experts), ("ffn_moe_topk", 8),
+             ("ffn_moe_weights", 8), ("ffn_moe_weights_sum", 1), ("ffn_moe_weights_norm", 8),
+             ("ffn_moe_gate", 8 * 768), ("ffn_moe_up", 8 * 768), ("ffn_moe_swiglu", 8 * 768),
+             ("ffn_moe_down", 8 * 2048), ("ffn_moe_weighted", 8 * 2048)]
+    out, o = {}, 0
+    for n, c in names:
+        out[n] = block[o:o + c]
+        o += c
+    assert o == len(block)
+    return out
+
+
 def quantize_q8k(x):
     """Q8_K blocks of x (length a multiple of 256) as raw bytes, or None when the
     reference would fail (a non-finite value)."""
     x = np.ascontiguousarray(x, np.float32)
     out = np.zeros(Q8K_BYTES * (len(x) // 256), np.uint8)
     return out if _o.qxo_quantize_q8k(_p(x), len(x), _p(out)) else None
+
+
+def matvec(ggml_type, w, rows, in_dims, x):
+    """rows of raw weight bytes w against f32 x (double accumulation, f32 results)."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(rows, np.float32)
+    _o.qxo_matvec(ggml_type, _p(w), rows, in_dims, _p(x), _p(y))
+    return y
 
 
 def matvec_q8k(ggml_type, w, rows, in_dims, x, expert=False):
@@ -116,6 +150,24 @@ class Model:
         if not _o.qxo_moe_layer(self._m, layer, _p(x), _p(y), _p(moe), _p(ids), _p(w)):
             raise RuntimeError("oracle MoE failed")
         return y, moe, ids, w
+
+    def attention_stage(self, layer, x, f16_kv=False):
+        """(attn_norm, Vcur, kqv_out, attn_out, ffn_inp, (v_probe, output_probe)); None when
+        the reference fails the probe (a non-finite output)."""
+        x = np.ascontiguousarray(x, np.float32)
+        nrm = np.zeros(2048, np.float32); vc = np.zeros(512, np.float32); kqv = np.zeros(4096, np.float32)
+        ao = np.zeros(2048, np.float32); fi = np.zeros(2048, np.float32); pr = np.zeros(2)
+        if not _o.qxo_attention_stage(self._m, layer, _p(x), int(f16_kv), _p(nrm), _p(vc), _p(kqv), _p(ao), _p(fi), _p(pr)):
+            return None
+        return nrm, vc, kqv, ao, fi, (float(pr[0]), float(pr[1]))
+
+    def moe_stage(self, layer, x, experts):
+        """(dict of the stage's named vectors, ids[8]); None when the reference fails."""
+        x = np.ascontiguousarray(x, np.float32)
+        blk = np.zeros(moe_stage_floats(experts), np.float32); ids = np.zeros(8, np.uint32)
+        if not _o.qxo_moe_stage(self._m, layer, _p(x), _p(blk), _p(ids)):
+            return None
+        return split_moe_stage(blk, experts), ids
 
     def embed(self, token):
         x = np.zeros(2048, np.float32)

@@ -15,8 +15,10 @@
 extern "C" {
 __global__ void qxk_embed(const uint8_t *, uint64_t, const uint32_t *, const DevState *, float *);
 __global__ void qxk_attn(const float *, const float *, const float *, Tables, int8_t *, int8_t *, float *, float *,
-                         uint32_t, uint32_t, double, const DevState *, float *, float *, float *);
-__global__ void qxk_attn_merge(const DevState *, const float *, float *);
+                         uint32_t, uint32_t, double, const DevState *, float *, float *, float *, double *);
+__global__ void qxk_attn_merge(const DevState *, const float *, float *, double *);
+__global__ void qxk_stage_route(const double *, uint32_t, float *, DevState *, uint32_t *);
+__global__ void qxk_stage_ctx(const float *, uint32_t, float *);
 __global__ void qxk_router(const float *, const float *, const float *, uint32_t, double *);
 __global__ void qxk_topk(const float *, uint32_t, uint32_t, float *, uint32_t *, float *, uint32_t *, uint32_t *,
                          DevState *);
@@ -33,9 +35,10 @@ void qxl_qkv(hipStream_t, const float *, const float *, const QTensor *, const Q
              DevState *, bool, Timer = Timer());
 void qxl_oproj(hipStream_t, const float *, const QTensor *, float *, float *, DevState *, bool, Timer = Timer());
 void qxl_gate_up(hipStream_t, const float *, const float *, const QTensor *, const QTensor *, Tables, const double *,
-                 uint32_t, DevState *, float *, uint32_t *, double *, bool, Timer = Timer());
+                 uint32_t, DevState *, float *, uint32_t *, double *, bool, Timer = Timer(), const uint32_t * = nullptr,
+                 float * = nullptr);
 void qxl_down(hipStream_t, const float *, const QTensor *, Tables, DevState *, float *, float *, bool,
-              Timer = Timer());
+              Timer = Timer(), float * = nullptr, float * = nullptr);
 void qxl_head(hipStream_t, const float *, const float *, const QTensor *, uint32_t, DevState *, float *, float *,
               uint32_t *, bool, Timer = Timer());
 __global__ void qxp_embed(const uint8_t *, uint64_t, const uint32_t *, float *);
@@ -152,6 +155,14 @@ struct qxg_ctx {
         int32_t *slot_token = nullptr;
         std::vector<void *> all;
     } pf;
+    // stage-probe outputs (allocated on first use)
+    struct Stage {
+        double *wsum = nullptr;                         // [32] per-head sums of normalised attention weights
+        float *norm = nullptr, *route = nullptr;        // [2048] RMSNorm; routing block (2 E + 25 floats)
+        float *gu = nullptr, *down = nullptr, *wdown = nullptr;   // [2][8][768] gate, up; [8][2048] down, weighted
+        uint32_t *bad = nullptr;
+        std::vector<void *> all;
+    } sg;
 };
 
 namespace {
@@ -308,15 +319,15 @@ Timer timer_for(qxg_ctx *c, int which) {
 }
 
 // ---- launch sequences (all asynchronous on c->s) ----
-void launch_attention(qxg_ctx *c, uint32_t l, float *x, float *attn_dump, float *vcur_dump) {
+void launch_attention(qxg_ctx *c, uint32_t l, float *x, float *attn_dump, float *vcur_dump, double *wsum = nullptr) {
     const LayerW &w = c->L[l];
     qxl_qkv(c->s, x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv, c->st, c->q8, timer_for(c, 2));
     qx_launch(qxk_attn, dim3(32, c->att_splits), dim3(256), 0, c->s, timer_for(c, 5), c->qkv, w.q_norm, w.k_norm,
               c->T, c->kc, c->vc, c->ks, c->vs, l, c->kv_ctx, std::sqrt(128.0), (const DevState *)c->st, c->ctxv,
-              c->apart, vcur_dump);
+              c->apart, vcur_dump, wsum);
     if (c->att_splits > 1)
         hipLaunchKernelGGL(qxk_attn_merge, dim3(32), dim3(128), 0, c->s, (const DevState *)c->st, (const float *)c->apart,
-                           c->ctxv);
+                           c->ctxv, wsum);
     qxl_oproj(c->s, c->ctxv, w.wo, x, attn_dump, c->st, c->q8, timer_for(c, 3));
 }
 
@@ -798,6 +809,7 @@ void qxg_close(qxg_ctx *c) {
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (void *p : c->arenas) (void)hipFree(p);
     for (void *p : c->pf.all) (void)hipFree(p);
+    for (void *p : c->sg.all) (void)hipFree(p);
     for (hipEvent_t e : c->kt.ev) (void)hipEventDestroy(e);
     if (c->e0) (void)hipEventDestroy(c->e0);
     if (c->e1) (void)hipEventDestroy(c->e1);
@@ -1157,15 +1169,37 @@ int qxg_embed_token(qxg_ctx *c, uint32_t token, float *x_out, char *err, uint64_
     return hip_ok(hipMemcpy(x_out, c->x, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read");
 }
 
+namespace {
+bool stage_buffers(qxg_ctx *c, char *err, uint64_t n) {
+    auto &g = c->sg;
+    if (g.bad) return true;
+    auto get = [&](void **p, uint64_t bytes) {
+        if (!hip_ok(hipMalloc(p, bytes), err, n, "stage buffer")) return false;
+        g.all.push_back(*p);
+        return true;
+    };
+    return get((void **)&g.wsum, 32 * 8) && get((void **)&g.norm, 2048 * 4) && get((void **)&g.route, (2 * 128 + 25) * 4) &&
+           get((void **)&g.gu, 2 * QXG_TOPK * QXG_FFN * 4) && get((void **)&g.down, QXG_TOPK * 2048 * 4) &&
+           get((void **)&g.wdown, QXG_TOPK * 2048 * 4) && get((void **)&g.bad, 4);
+}
+}  // namespace
+
 int qxg_attention_layer(qxg_ctx *c, uint32_t layer, uint32_t position, const float *x_in, float *attn_out,
                         float *kqv_out, float *vcur_out, char *err, uint64_t err_len) {
+    return qxg_attention_layer_ex(c, layer, position, x_in, attn_out, kqv_out, vcur_out, nullptr, err, err_len);
+}
+
+int qxg_attention_layer_ex(qxg_ctx *c, uint32_t layer, uint32_t position, const float *x_in, float *attn_out,
+                           float *kqv_out, float *vcur_out, double *head_weight_sums, char *err, uint64_t err_len) {
     if (!check_ready(c, true, err, err_len)) return 0;
     if (!x_in || layer >= c->layers || layer >= c->kv_layers || position >= c->kv_ctx) { set_err(err, err_len, "invalid attention layer argument"); return 0; }
     (void)hipSetDevice(c->device);
+    if (head_weight_sums && !stage_buffers(c, err, err_len)) return 0;
     (void)hipMemcpyAsync(c->x, x_in, 2048 * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, position, 0, 1, 1);
-    launch_attention(c, layer, c->x, c->attn, c->vcur);
+    launch_attention(c, layer, c->x, c->attn, c->vcur, head_weight_sums ? c->sg.wsum : nullptr);
     if (!finish(c, err, err_len)) return 0;
+    if (head_weight_sums && !hip_ok(hipMemcpy(head_weight_sums, c->sg.wsum, 32 * 8, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
     if (attn_out && !hip_ok(hipMemcpy(attn_out, c->attn, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
     if (kqv_out && !hip_ok(hipMemcpy(kqv_out, c->ctxv, 4096 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
     if (vcur_out && !hip_ok(hipMemcpy(vcur_out, c->vcur, 512 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
@@ -1188,6 +1222,78 @@ int qxg_moe_layer(qxg_ctx *c, uint32_t layer, const float *ffn_inp, float *layer
     for (int r = 0; r < 8; ++r) {
         if (ids) ids[r] = h.moe_ids[r];
         if (weights) weights[r] = h.moe_w[r];
+    }
+    return 1;
+}
+
+int qxg_attention_stage(qxg_ctx *c, uint32_t layer, int f16_kv, const float *x_in, float *norm_out, float *vcur_out,
+                        float *kqv_out, float *attn_out, float *ffn_inp_out, char *err, uint64_t err_len) {
+    if (!check_ready(c, false, err, err_len)) return 0;
+    if (!x_in || layer >= c->layers) { set_err(err, err_len, "invalid attention stage layer or dimensions"); return 0; }
+    (void)hipSetDevice(c->device);
+    if (!stage_buffers(c, err, err_len)) return 0;
+    const LayerW &w = c->L[layer];
+    (void)hipMemcpyAsync(c->x, x_in, 2048 * 4, hipMemcpyHostToDevice, c->s);
+    write_state(c, 0, 0, 1, 1);
+    hipLaunchKernelGGL(qxp_norm, dim3(1), dim3(256), 0, c->s, (const float *)c->x, w.attn_norm, 1u, c->sg.norm);
+    qxl_qkv(c->s, c->x, w.attn_norm, w.wq, w.wk, w.wv, c->qkv, c->st, c->q8);
+    hipLaunchKernelGGL(qxk_stage_ctx, dim3(1), dim3(256), 0, c->s, (const float *)c->qkv, (uint32_t)(f16_kv != 0), c->ctxv);
+    qxl_oproj(c->s, c->ctxv, w.wo, c->x, c->attn, c->st, c->q8);   // x becomes ffn_inp, attn the O output
+    if (!finish(c, err, err_len)) return 0;
+    std::vector<float> fi(2048), ao(2048);
+    if (!hip_ok(hipMemcpy(fi.data(), c->x, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read") ||
+        !hip_ok(hipMemcpy(ao.data(), c->attn, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    for (int i = 0; i < 2048; ++i)
+        if (!std::isfinite(ao[i]) || !std::isfinite(fi[i])) { set_err(err, err_len, "non-finite attention stage output"); return 0; }
+    if (norm_out && !hip_ok(hipMemcpy(norm_out, c->sg.norm, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (vcur_out && !hip_ok(hipMemcpy(vcur_out, c->qkv + 4608, 512 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (kqv_out && !hip_ok(hipMemcpy(kqv_out, c->ctxv, 4096 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (attn_out) memcpy(attn_out, ao.data(), 2048 * 4);
+    if (ffn_inp_out) memcpy(ffn_inp_out, fi.data(), 2048 * 4);
+    return 1;
+}
+
+int qxg_moe_stage(qxg_ctx *c, uint32_t layer, const float *x_in, float *out, uint32_t ids[8], char *err,
+                  uint64_t err_len) {
+    if (!check_ready(c, false, err, err_len)) return 0;
+    if (!x_in || !out || layer >= c->layers) { set_err(err, err_len, "invalid MoE stage layer"); return 0; }
+    if (c->experts < 8 || c->experts > 128) { set_err(err, err_len, "unsupported MoE stage tensor layout"); return 0; }
+    (void)hipSetDevice(c->device);
+    if (!stage_buffers(c, err, err_len)) return 0;
+    const LayerW &w = c->L[layer];
+    const uint32_t E = c->experts;
+    (void)hipMemcpyAsync(c->x, x_in, 2048 * 4, hipMemcpyHostToDevice, c->s);
+    write_state(c, 0, 0, 1, 1);
+    hipLaunchKernelGGL(qxp_norm, dim3(1), dim3(256), 0, c->s, (const float *)c->x, w.ffn_norm, 1u, c->sg.norm);
+    hipLaunchKernelGGL(qxk_router, dim3(E), dim3(256), 0, c->s, (const float *)c->x, w.ffn_norm, w.router, E, c->rlog);
+    hipLaunchKernelGGL(qxk_stage_route, dim3(1), dim3(64), 0, c->s, (const double *)c->rlog, E, c->sg.route, c->st, c->sg.bad);
+    qxl_gate_up(c->s, c->x, w.ffn_norm, w.gate, w.up, c->T, c->rlog, E, c->st, c->h, c->route_ids + 8 * layer,
+                c->route_w + 8 * layer, c->q8, Timer(), c->st->moe_ids, c->sg.gu);
+    qxl_down(c->s, c->h, w.down, c->T, c->st, c->x, c->moe, c->q8, Timer(), c->sg.down, c->sg.wdown);
+    if (!finish(c, err, err_len)) return 0;
+    uint32_t bad = 0;
+    if (!hip_ok(hipMemcpy(&bad, c->sg.bad, 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    if (bad) {
+        set_err(err, err_len, bad == 1 ? "non-finite MoE router logit" : bad == 2 ? "invalid MoE router softmax"
+                                                                       : "invalid selected MoE weights");
+        return 0;
+    }
+    const uint64_t F8 = QXG_TOPK * QXG_FFN;
+    float *o = out;
+    auto rd = [&](float *dst, const void *src, uint64_t nf) {
+        return hip_ok(hipMemcpy(dst, src, nf * 4, hipMemcpyDeviceToHost), err, err_len, "read");
+    };
+    if (!rd(o, c->sg.norm, 2048)) return 0;
+    o += 2048;
+    if (!rd(o, c->sg.route, 2 * E + 25)) return 0;
+    o += 2 * E + 25;
+    if (!rd(o, c->sg.gu, 2 * F8) || !rd(o + 2 * F8, c->h, F8)) return 0;
+    o += 3 * F8;
+    if (!rd(o, c->sg.down, QXG_TOPK * 2048) || !rd(o + QXG_TOPK * 2048, c->sg.wdown, QXG_TOPK * 2048)) return 0;
+    if (ids) {
+        DevState h;
+        if (!read_state(c, h, err, err_len)) return 0;
+        for (int r = 0; r < 8; ++r) ids[r] = h.moe_ids[r];
     }
     return 1;
 }
@@ -1242,10 +1348,10 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
         case 5:
             hipLaunchKernelGGL(qxk_attn, dim3(32, c->att_splits), dim3(256), 0, c->s, c->qkv, w.q_norm, w.k_norm, c->T,
                                c->kc, c->vc, c->ks, c->vs, l % c->kv_layers, c->kv_ctx, std::sqrt(128.0), c->st,
-                               c->ctxv, c->apart, nullptr);
+                               c->ctxv, c->apart, nullptr, nullptr);
             if (c->att_splits > 1)
                 hipLaunchKernelGGL(qxk_attn_merge, dim3(32), dim3(128), 0, c->s, (const DevState *)c->st,
-                                   (const float *)c->apart, c->ctxv);
+                                   (const float *)c->apart, c->ctxv, nullptr);
             break;
         case 6:
             hipLaunchKernelGGL(qxk_router, dim3(c->experts), dim3(256), 0, c->s, (const float *)c->x, w.ffn_norm,

@@ -704,7 +704,8 @@ DEV double attn_scores(const float *s_q, uint32_t *s_qd, uint32_t n, double sqrt
 // Unnormalised (norm false, one split of several): s_sc[t] <- e_t * vs_t and the raw
 // den is returned.  vsc(t) returns position t's V scale.  Ends with a barrier.
 template <typename VS>
-DEV double attn_weights(uint32_t n, double mx, double *s_sc, double *redd, VS vsc, bool norm = true) {
+DEV double attn_weights(uint32_t n, double mx, double *s_sc, double *redd, VS vsc, bool norm = true,
+                        double *wsum = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     double den = 0.0;
     for (uint32_t t = tid; t < n; t += 256) {
@@ -716,13 +717,25 @@ DEV double attn_weights(uint32_t n, double mx, double *s_sc, double *redd, VS vs
     if (lane == 0) redd[4 + wave] = den;   // redd[0..3] may still be read by the score maximum
     __syncthreads();
     den = (redd[4] + redd[5]) + (redd[6] + redd[7]);
+    double ws = 0.0;   // the head's sum of normalised weights (a diagnostic, when wsum is given)
     if (norm) {
         if (!isfinite(den) || den <= 0.0) den = 1.0;
-        for (uint32_t t = tid; t < n; t += 256) s_sc[t] = (s_sc[t] / den) * (double)vsc(t);
+        for (uint32_t t = tid; t < n; t += 256) {
+            const double w = s_sc[t] / den;
+            ws += w;
+            s_sc[t] = w * (double)vsc(t);
+        }
     } else {
         for (uint32_t t = tid; t < n; t += 256) s_sc[t] = s_sc[t] * (double)vsc(t);
     }
     __syncthreads();
+    if (wsum && norm) {   // block-uniform; redd[0..3] are free after the barrier above
+        ws = wave_total_d(ws);
+        if (lane == 0) redd[wave] = ws;
+        __syncthreads();
+        if (tid == 0) *wsum = (redd[0] + redd[1]) + (redd[2] + redd[3]);
+        __syncthreads();
+    }
     return den;
 }
 // Context: out[d] = sum_t p_t * v8_t[d] in f32 with p_t = (float)((e_t / den) * vs_t).

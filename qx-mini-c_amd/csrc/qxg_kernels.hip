@@ -138,7 +138,7 @@ constexpr int ATT_STAGE = QXG_ATT_SPLIT;   // positions per block (4 uint4 of K 
 
 extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, const float *q_norm, const float *k_norm,
         Tables T, int8_t *kc, int8_t *vc, float *ks, float *vs, uint32_t layer, uint32_t ctx, double sqrt_hd,
-        const DevState *st, float *ctx_out, float *part, float *vcur_dump) {
+        const DevState *st, float *ctx_out, float *part, float *vcur_dump, double *wsum) {
     __shared__ double s_sc[ATT_STAGE];             // scores, then weights
     __shared__ uint4 s_kst[ATT_STAGE * 8], s_vst[ATT_STAGE * 8];   // staged rows of this kv head
     __shared__ float s_kss[ATT_STAGE], s_vss[ATT_STAGE];
@@ -258,7 +258,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     const double mx = attn_scores(s_q, s_qd, cnt, sqrt_hd, s_sc, redd, krow);
     QXG_MARK(4, 5);
     const bool one = nsplit == 1;
-    const double den = attn_weights(cnt, mx, s_sc, redd, vsc, one);
+    const double den = attn_weights(cnt, mx, s_sc, redd, vsc, one, wsum ? wsum + qh : nullptr);
     QXG_MARK(4, 6);
     float *pp = part + ((uint64_t)qh * QXG_MAX_SPLITS + split) * QXG_ATT_PART;
     attn_context(cnt, s_sc, s_part, vrow, one ? ctx_out + qh * 128 : pp);
@@ -282,7 +282,9 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
 // w_s = exp(m_s - M), L = sum_s w_s l_s (1 if not finite and positive), ctx[d] =
 // sum_s (float)(w_s / L) * acc_s[d] in split order.  With one split the attention
 // kernel wrote the context itself and this returns.
-extern "C" __global__ __launch_bounds__(128) void qxk_attn_merge(const DevState *st, const float *part, float *ctx_out) {
+// wsum (may be null): the head's sum of normalised weights, sum_s w_s l_s / L.
+extern "C" __global__ __launch_bounds__(128) void qxk_attn_merge(const DevState *st, const float *part, float *ctx_out,
+                                                                  double *wsum) {
     const uint32_t n = cur_pos(st) + 1, ns = (n + ATT_STAGE - 1) / ATT_STAGE;
     if (ns <= 1) return;
     const int qh = blockIdx.x, d = threadIdx.x;
@@ -295,6 +297,14 @@ extern "C" __global__ __launch_bounds__(128) void qxk_attn_merge(const DevState 
         L += exp(ml[0] - M) * ml[1];
     }
     if (!isfinite(L) || L <= 0.0) L = 1.0;
+    if (wsum && d == 0) {
+        double t = 0.0;
+        for (uint32_t s = 0; s < ns; ++s) {
+            const double *ml = reinterpret_cast<const double *>(p + s * QXG_ATT_PART + 128);
+            t += exp(ml[0] - M) * ml[1] / L;
+        }
+        wsum[qh] = t;
+    }
     float o = 0.0f;
     for (uint32_t s = 0; s < ns; ++s) {
         const double m = reinterpret_cast<const double *>(p + s * QXG_ATT_PART + 128)[0];
@@ -448,7 +458,8 @@ DEV float gu_dot(gu4 u, const Dig &g, const uint4 *G, const uint2 *SEL) {
 
 template <int UPW, int FMT, bool Q8>
 __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *norm_w, GuW gw, GuW uw, Tables T,
-        const double *logits, uint32_t experts, DevState *st, float *h, uint32_t *route_ids, double *route_w) {
+        const double *logits, uint32_t experts, DevState *st, float *h, uint32_t *route_ids, double *route_w,
+        const uint32_t *given_ids, float *gu_dump) {
     constexpr int NG = FMT == 17 ? 512 : 1024, NS = FMT == 17 ? 128 : 256;
     __shared__ uint4 s_g2[NG];
     __shared__ uint2 s_sel[NS];
@@ -476,7 +487,12 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
     uint32_t ids[QXG_TOPK];
     QXG_ANCHOR(l1);
     QXG_MARK(1, 5);
-    wave_top8_ids(l0, l1, E, ids);
+    if (given_ids) {   // the caller routed (st->moe_ids / moe_w already hold the picks)
+#pragma unroll
+        for (int q = 0; q < QXG_TOPK; ++q) ids[q] = given_ids[q];
+    } else {
+        wave_top8_ids(l0, l1, E, ids);
+    }
     uint32_t e = 0u;
 #pragma unroll
     for (int q = 0; q < QXG_TOPK; ++q) {
@@ -493,7 +509,7 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
         uq[uu] = gu_load<FMT>(uw, blk, ib);
     }
     __builtin_amdgcn_sched_barrier(0);   // every load is issued before the first use
-    if (blockIdx.x == 0 && wave == 0) {   // the down kernel reads ids and renormalised weights from st
+    if (!given_ids && blockIdx.x == 0 && wave == 0) {   // the down kernel reads ids and renormalised weights from st
         double wts[QXG_TOPK];
         wave_top8_weights(l0, l1, ids, wts);
 #pragma unroll
@@ -548,6 +564,10 @@ __global__ __launch_bounds__(256) void qxk_gate_up(const float *x, const float *
             st->q8_fault = ok ? QXG_Q8_NONFINITE_EXPERT : QXG_Q8_NONFINITE_INPUT;
         gv = (ok && isfinite(gv)) ? gv : 0.0f;
         uv = (ok && isfinite(uv)) ? uv : 0.0f;
+        if (gu_dump) {   // gate rows, then up rows, rank-major like h
+            gu_dump[u0 + lane] = gv;
+            gu_dump[QXG_TOPK * QXG_FFN + u0 + lane] = uv;
+        }
         const double sg = (double)gv / (1.0 + exp(-(double)gv));
         h[u0 + lane] = (float)(sg * (double)uv);
     }
@@ -590,7 +610,7 @@ DEV float dn_dot(uint4 a, uint2 m, int k, const Dig &g, const uint2 *G, const ui
 
 template <int RPW, int FMT, bool Q8>
 __global__ __launch_bounds__(256) void qxk_down(const float *h, DnW w, Tables T, DevState *st, float *x,
-                                                 float *moe_dump) {
+                                                 float *moe_dump, float *down_dump, float *wdump) {
     constexpr int NG = FMT == 21 ? 512 : 256, NS = FMT == 21 ? 256 : 128;
     __shared__ uint2 s_g3[NG];
     __shared__ uint2 s_sel[NS];
@@ -646,6 +666,10 @@ __global__ __launch_bounds__(256) void qxk_down(const float *h, DnW w, Tables T,
         if (Q8 && (!ok || !isfinite(part)) && k == 0)
             st->q8_fault = ok ? QXG_Q8_NONFINITE_EXPERT : QXG_Q8_NONFINITE_INPUT;
         const float y = (ok && isfinite(part)) ? part : 0.0f;
+        if (down_dump && k == 0) {   // rank r's row and its weighted value, [rank][2048]
+            down_dump[r * 2048 + r0 + rr] = y;
+            wdump[r * 2048 + r0 + rr] = (float)(wr[r] * (double)y);
+        }
         float moe = 0.0f;
 #pragma unroll
         for (int q = 0; q < QXG_TOPK; ++q) moe += (float)(wr[q] * (double)rdlanef(y, 8 * q));
@@ -969,6 +993,62 @@ extern "C" __global__ __launch_bounds__(256) void qxk_repack(uint32_t type, cons
     }
 }
 
+// MoE stage probe routing (reference src/qx_format.c:5647-5684), one thread, index order:
+// f32 logits, f32 probabilities exp(logit - max) / sum (double max and sum), 8 picks by
+// probability (strictly larger; the lowest index among equals), f32 weights and their
+// double sum, f32 renormalised weights.  The picks and weights go to st for the expert
+// kernels; out: logits[E], probs[E], topk[8], weights[8], weights_sum[1], weights_norm[8].
+// *bad: 0, or the first of the reference's failures (1 non-finite logit, 2 invalid softmax,
+// 3 invalid selected weights).
+extern "C" __global__ void qxk_stage_route(const double *logits, uint32_t experts, float *out, DevState *st,
+                                           uint32_t *bad) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const uint32_t E = experts;
+    float *lg = out, *pr = out + E, *topk = pr + E, *wts = topk + 8, *wsum = wts + 8, *wn = wsum + 1;
+    double mx = -1.0e300;
+    uint32_t fail = 0u;
+    for (uint32_t e = 0; e < E; ++e) {
+        const double d = logits[e];
+        if (!isfinite(d) && !fail) fail = 1u;   // 1: non-finite router logit
+        lg[e] = (float)d;
+        if (d > mx) mx = d;
+    }
+    double den = 0.0;
+    for (uint32_t e = 0; e < E; ++e) { pr[e] = (float)exp((double)lg[e] - mx); den += (double)pr[e]; }
+    if ((!isfinite(den) || den <= 0.0) && !fail) fail = 2u;   // 2: invalid softmax
+    for (uint32_t e = 0; e < E; ++e) pr[e] = (float)((double)pr[e] / den);
+    uint64_t picked[2] = {0ull, 0ull};
+    double sum = 0.0;
+    for (int r = 0; r < QXG_TOPK; ++r) {
+        uint32_t best = 0u;
+        float bp = -1.0f;
+        for (uint32_t e = 0; e < E; ++e)
+            if (!((picked[e >> 6] >> (e & 63)) & 1ull) && pr[e] > bp) { best = e; bp = pr[e]; }
+        picked[best >> 6] |= 1ull << (best & 63);
+        topk[r] = (float)best;
+        wts[r] = bp;
+        sum += (double)bp;
+        st->moe_ids[r] = best;
+    }
+    if ((!isfinite(sum) || sum <= 0.0) && !fail) fail = 3u;   // 3: invalid selected weights
+    wsum[0] = (float)sum;
+    for (int r = 0; r < QXG_TOPK; ++r) {
+        wn[r] = (float)((double)wts[r] / sum);
+        st->moe_w[r] = (double)wn[r];   // the down kernel's weights: weighted = (float)(wn * down)
+    }
+    *bad = fail;
+}
+
+// The attention stage probe's context (reference src/qx_format.c:5532-5539): a single token
+// attends to itself with weight 1, so q head h's context is kv head h/8's V row (with
+// fp16 KV, after an fp16 round trip: round to nearest even, the reference's conversion).
+extern "C" __global__ __launch_bounds__(256) void qxk_stage_ctx(const float *qkv, uint32_t f16, float *ctxv) {
+    for (uint32_t i = threadIdx.x; i < 4096; i += 256) {
+        const float v = qkv[4608 + ((i >> 10) << 7) + (i & 127)];
+        ctxv[i] = f16 ? (float)(_Float16)v : v;
+    }
+}
+
 // ----------------------------------------------------------------- launch wrappers
 extern "C" {
 // Each wrapper picks the kernel instantiation of the tensor's format (validated at bind)
@@ -990,21 +1070,23 @@ void qxl_oproj(hipStream_t s, const float *ctxv, const QTensor *o, float *x, flo
 }
 void qxl_gate_up(hipStream_t s, const float *x, const float *nw, const QTensor *g, const QTensor *u, Tables T,
                  const double *logits, uint32_t experts, DevState *st, float *h, uint32_t *route_ids, double *route_w,
-                 bool q8, Timer t) {
+                 bool q8, Timer t, const uint32_t *given_ids, float *gu_dump) {
     constexpr int UPW = QXG_GU_UPW;
     const GuW gw{g->p0, g->p1, g->p2, g->d}, uw{u->p0, u->p1, u->p2, u->d};
     const dim3 grid(QXG_TOPK * QXG_FFN / (4 * UPW));
     auto go = [&](auto kernel) {
-        qx_launch(kernel, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h, route_ids, route_w);
+        qx_launch(kernel, grid, dim3(256), 0, s, t, x, nw, gw, uw, T, logits, experts, st, h, route_ids, route_w,
+                  given_ids, gu_dump);
     };
     if (g->type == 22) q8 ? go(qxk_gate_up<UPW, 22, true>) : go(qxk_gate_up<UPW, 22, false>);
     else q8 ? go(qxk_gate_up<UPW, 17, true>) : go(qxk_gate_up<UPW, 17, false>);
 }
-void qxl_down(hipStream_t s, const float *h, const QTensor *d, Tables T, DevState *st, float *x, float *dump, bool q8, Timer t) {
+void qxl_down(hipStream_t s, const float *h, const QTensor *d, Tables T, DevState *st, float *x, float *dump, bool q8, Timer t,
+              float *down_dump, float *wdump) {
     constexpr int RPW = QXG_DOWN_RPW;
     const DnW w{d->p0, d->p1, d->p2, d->d};
     const dim3 grid(2048 / (4 * RPW));
-    auto go = [&](auto kernel) { qx_launch(kernel, grid, dim3(256), 0, s, t, h, w, T, st, x, dump); };
+    auto go = [&](auto kernel) { qx_launch(kernel, grid, dim3(256), 0, s, t, h, w, T, st, x, dump, down_dump, wdump); };
     if (d->type == 23) q8 ? go(qxk_down<RPW, 23, true>) : go(qxk_down<RPW, 23, false>);
     else if (d->type == 21) q8 ? go(qxk_down<RPW, 21, true>) : go(qxk_down<RPW, 21, false>);
     else q8 ? go(qxk_down<RPW, 18, true>) : go(qxk_down<RPW, 18, false>);

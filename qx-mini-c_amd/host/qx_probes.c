@@ -1,9 +1,8 @@
-/* Host side of the GPU path: QXF1 -> device upload, and the reference's probe
- * entry points (decode-block, final-head-probe, the full-MoE state loop) driving
- * the qxg C ABI.  JSON field names follow the reference's output so existing
- * consumers of those probes keep working. */
-#include "qx_host.h"
-#include "qxg.h"
+/* Host side of the GPU path: QXF1 -> device upload, and the reference's probe entry
+ * points decode-block, final-head-probe and q8-k-activation-probe driving the qxg C
+ * ABI (the state loop and the stage probes have files of their own).  JSON field names
+ * follow the reference's output so existing consumers of those probes keep working. */
+#include "qx_util.h"
 
 #include <errno.h>
 #include <math.h>
@@ -12,9 +11,7 @@
 #include <sys/stat.h>
 #include <time.h>
 
-static void set_err(char *err, uint64_t n, const char *msg) {
-    if (err && n) snprintf(err, (size_t)n, "%s", msg);
-}
+#define set_err qxh_set_err
 
 int qx_gpu_load(struct qxg_ctx *ctx, const char *path, int verify, qx_gpu_model_info *info, char *err, uint64_t err_len) {
     qxf_file f;
@@ -47,11 +44,6 @@ int qx_gpu_load(struct qxg_ctx *ctx, const char *path, int verify, qx_gpu_model_
     return ok;
 }
 
-static int open_gpu(const char *path, int verify, qxg_ctx **ctx, qx_gpu_model_info *mi, char *err, uint64_t err_len) {
-    if (!qxg_open(0, ctx, err, err_len)) return 0;
-    if (!qx_gpu_load(*ctx, path, verify, mi, err, err_len)) { qxg_close(*ctx); *ctx = NULL; return 0; }
-    return 1;
-}
 
 int qx_dump_decode_block_summary(const char *path, const char *name, uint64_t block_index, FILE *out, char *err, uint64_t err_len) {
     qxf_file f;
@@ -88,55 +80,17 @@ int qx_dump_decode_block_summary(const char *path, const char *name, uint64_t bl
     return ok;
 }
 
-/* reference qx_read_exact_f32_sidecar (src/qx_format.c:5319-5344) */
-static int read_sidecar(const char *path, float *v, uint32_t n, char *err, uint64_t err_len) {
-    FILE *fp = fopen(path, "rb");
-    if (!fp) { set_err(err, err_len, "cannot open F32 sidecar"); return 0; }
-    struct stat st;
-    if (fstat(fileno(fp), &st) != 0 || (uint64_t)st.st_size != (uint64_t)n * 4 || fread(v, 4, n, fp) != n) {
-        fclose(fp); set_err(err, err_len, "F32 sidecar size or read mismatch"); return 0;
-    }
-    fclose(fp);
-    for (uint32_t i = 0; i < n; ++i)
-        if (!isfinite(v[i])) { set_err(err, err_len, "F32 sidecar contains non-finite value"); return 0; }
-    return 1;
-}
-
-static int write_f32(const char *dir, const char *name, const float *v, uint32_t n, char *err, uint64_t err_len) {
-    char p[1024];
-    int len = snprintf(p, sizeof(p), "%s/%s.f32", dir, name);
-    if (len < 0 || (size_t)len >= sizeof(p)) { set_err(err, err_len, "sidecar path too long"); return 0; }
-    FILE *fp = fopen(p, "wb");
-    if (!fp) { set_err(err, err_len, "cannot open sidecar for writing"); return 0; }
-    int ok = fwrite(v, 4, n, fp) == n;
-    if (fclose(fp) != 0) ok = 0;
-    if (!ok) { remove(p); set_err(err, err_len, "cannot write sidecar"); }
-    return ok;
-}
-
-static void remove_f32(const char *dir, const char *name) {
-    char p[1024];
-    snprintf(p, sizeof(p), "%s/%s.f32", dir, name);
-    remove(p);
-}
-
-/* "f32" -> 0, "q8_k_compat" -> 1, anything else -> -1 (reference src/qx_format.c:5971-5973) */
-static int activation_code(const char *s) {
-    if (!s) return -1;
-    return !strcmp(s, "f32") ? 0 : !strcmp(s, "q8_k_compat") ? 1 : -1;
-}
-
 int qx_dump_final_head_probe_summary(const char *path, const char *residual_path, const char *output_dir,
         const char *activation_mode, uint32_t top_n, FILE *out, char *err, uint64_t err_len) {
-    const int act = activation_code(activation_mode);
+    const int act = qxh_activation_code(activation_mode);
     if (!path || !residual_path || !output_dir || !out || top_n == 0 || top_n > 32 || act < 0) {
         set_err(err, err_len, "invalid final head probe argument or activation mode"); return 0;
     }
     float res[2048], nrm[2048];
-    if (!read_sidecar(residual_path, res, 2048, err, err_len)) return 0;
+    if (!qxh_read_sidecar(residual_path, res, 2048, err, err_len)) return 0;
     qxg_ctx *ctx = NULL;
     qx_gpu_model_info mi;
-    if (!open_gpu(path, 1, &ctx, &mi, err, err_len)) return 0;
+    if (!qxh_open_gpu(path, 1, &ctx, &mi, err, err_len)) return 0;
     if (!mi.has_head) { qxg_close(ctx); set_err(err, err_len, "final head requires Q6_K output.weight"); return 0; }
     if (!qxg_set_activation(ctx, (uint32_t)act, err, err_len)) { qxg_close(ctx); return 0; }
     float *logits = (float *)malloc((size_t)mi.vocab * 4);
@@ -144,8 +98,8 @@ int qx_dump_final_head_probe_summary(const char *path, const char *residual_path
     double lg[32];
     int ok = logits && qxg_final_head(ctx, res, nrm, logits, top_n, ids, lg, err, err_len);
     qxg_close(ctx);
-    if (ok && !write_f32(output_dir, "final-norm", nrm, 2048, err, err_len)) ok = 0;
-    if (ok && !write_f32(output_dir, "logits", logits, mi.vocab, err, err_len)) { remove_f32(output_dir, "final-norm"); ok = 0; }
+    if (ok && !qxh_write_f32(output_dir, "final-norm", nrm, 2048, err, err_len)) ok = 0;
+    if (ok && !qxh_write_f32(output_dir, "logits", logits, mi.vocab, err, err_len)) { qxh_remove_f32(output_dir, "final-norm"); ok = 0; }
     if (ok) {
         double ss = 0.0, ns = 0.0;
         for (int i = 0; i < 2048; ++i) { ss += (double)res[i] * res[i]; ns += (double)nrm[i] * nrm[i]; }
@@ -161,122 +115,6 @@ int qx_dump_final_head_probe_summary(const char *path, const char *residual_path
         fprintf(out, "]}\n");
     }
     free(logits);
-    return ok;
-}
-
-static double now_s(void) {
-    struct timespec ts;
-    clock_gettime(CLOCK_MONOTONIC, &ts);
-    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
-}
-
-static int dump_vec(const char *dir, uint32_t step, uint32_t layer, const char *phase, const float *v, uint32_t n,
-                    char *err, uint64_t err_len) {
-    char name[128];
-    snprintf(name, sizeof(name), "step-%u-layer-%u-%s", step, layer, phase);
-    return write_f32(dir, name, v, n, err, err_len);
-}
-
-/* Full-MoE state loop on the GPU (reference src/qx_format.c:5970-6719 with
- * --full-moe [--final-head], INT8 KV, f32 or q8_k_compat activations, temperature 0). */
-int qx_dump_prompt_state_loop_gpu(const char *path, const uint32_t *prompt, uint32_t n_prompt,
-        uint32_t gen_steps, uint32_t ctx_tokens, const char *kv_format, const char *activation_format,
-        int final_head, uint32_t top_n, const char *dump_dir, int bench, FILE *out, char *err, uint64_t err_len) {
-    if (!path || !prompt || !out) { set_err(err, err_len, "invalid argument"); return 0; }
-    if (!kv_format || strcmp(kv_format, "int8") != 0) { set_err(err, err_len, "the GPU state loop supports INT8 KV only"); return 0; }
-    const int act = activation_code(activation_format);
-    if (act < 0) { set_err(err, err_len, "unsupported activation format"); return 0; }
-    if (gen_steps == 0 || n_prompt == 0) { set_err(err, err_len, "prompt state loop requires >= 1 prompt token and >= 1 generation step"); return 0; }
-    if (ctx_tokens == 0 || ctx_tokens > 4096) { set_err(err, err_len, "state loop context must be between 1 and 4096"); return 0; }
-    const uint32_t steps = n_prompt + gen_steps - 1;
-    if (steps > ctx_tokens) { set_err(err, err_len, "steps exceed ctx"); return 0; }
-    if (top_n == 0) top_n = 1;
-    if (top_n > 32) top_n = 32;
-    qxg_ctx *ctx = NULL;
-    qx_gpu_model_info mi;
-    double t_load = now_s();
-    if (!open_gpu(path, 1, &ctx, &mi, err, err_len)) return 0;
-    t_load = now_s() - t_load;
-    if (!mi.has_embedding) { qxg_close(ctx); set_err(err, err_len, "token_embd.weight not found"); return 0; }
-    if (!qxg_set_activation(ctx, (uint32_t)act, err, err_len)) { qxg_close(ctx); return 0; }
-    if (final_head && !mi.has_head) { qxg_close(ctx); set_err(err, err_len, "final head requires Q6_K output.weight"); return 0; }
-    for (uint32_t i = 0; i < n_prompt; ++i)
-        if (prompt[i] >= mi.vocab) { qxg_close(ctx); set_err(err, err_len, "prompt token out of range"); return 0; }
-    if (!qxg_kv_create(ctx, mi.layers, ctx_tokens, 1, err, err_len)) { qxg_close(ctx); return 0; }
-    float *x = (float *)malloc(2048 * 4), *a = (float *)malloc(2048 * 4), *y = (float *)malloc(2048 * 4);
-    float *kqv = (float *)malloc(4096 * 4), *vcur = (float *)malloc(512 * 4), *moe = (float *)malloc(2048 * 4);
-    float *logits = (float *)malloc((size_t)mi.vocab * 4);
-    int ok = x && a && y && kqv && vcur && moe && logits;
-    if (!ok) set_err(err, err_len, "out of memory");
-    fprintf(out, "{\n  \"probe\": \"prompt_state_loop\",\n  \"backend\": \"hip-gfx950\",\n  \"layers\": %u,\n"
-            "  \"ctx_tokens\": %u,\n  \"kv_format\": \"int8\",\n  \"activation_format\": \"%s\",\n  \"full_moe\": true,\n"
-            "  \"final_head\": %s,\n  \"prompt_tokens\": %u,\n  \"generation_steps\": %u,\n  \"steps\": %u,\n  \"tokens\": [",
-            mi.layers, ctx_tokens, act ? "q8_k_compat" : "f32", final_head ? "true" : "false", n_prompt, gen_steps, steps);
-    uint32_t current = prompt[0];
-    double t_loop = now_s();
-    for (uint32_t s = 0; ok && s < steps; ++s) {
-        if (s < n_prompt) current = prompt[s];
-        const int sampling = s + 1 >= n_prompt;
-        const int run_head = sampling && final_head;
-        uint32_t ids[32];
-        double lg[32];
-        if (dump_dir && *dump_dir) {
-            ok = qxg_embed_token(ctx, current, x, err, err_len);
-            for (uint32_t l = 0; ok && l < mi.layers; ++l) {
-                ok = dump_vec(dump_dir, s, l, "input", x, 2048, err, err_len) &&
-                     qxg_attention_layer(ctx, l, s, x, a, kqv, vcur, err, err_len) &&
-                     dump_vec(dump_dir, s, l, "v-cur", vcur, 512, err, err_len) &&
-                     dump_vec(dump_dir, s, l, "kqv-out", kqv, 4096, err, err_len);
-                if (!ok) break;
-                for (int i = 0; i < 2048; ++i) x[i] += a[i];
-                uint32_t eid[8];
-                double ew[8];
-                ok = dump_vec(dump_dir, s, l, "ffn-inp", x, 2048, err, err_len) &&
-                     qxg_moe_layer(ctx, l, x, y, moe, eid, ew, err, err_len) &&
-                     dump_vec(dump_dir, s, l, "ffn-moe-out", moe, 2048, err, err_len) &&
-                     dump_vec(dump_dir, s, l, "output", y, 2048, err, err_len);
-                memcpy(x, y, 2048 * 4);
-            }
-            if (ok && run_head) {
-                ok = qxg_final_head(ctx, x, NULL, logits, top_n, ids, lg, err, err_len);
-                char nm[64];
-                snprintf(nm, sizeof(nm), "step-%u-logits", s);
-                if (ok) ok = write_f32(dump_dir, nm, logits, mi.vocab, err, err_len);
-            }
-        } else {
-            ok = qxg_decode_token(ctx, current, s, run_head, x, NULL, NULL, top_n, ids, lg, err, err_len);
-        }
-        if (!ok) break;
-        fprintf(out, "%s{\"step\": %u, \"position\": %u, \"phase\": \"%s\", \"input_token\": %u", s ? ", " : "", s, s,
-                sampling ? "generate" : "prefill", current);
-        if (run_head) {
-            fprintf(out, ", \"final_head\": {\"argmax_token\": %u, \"argmax_logit\": %.17g, \"top_tokens\": [", ids[0], lg[0]);
-            for (uint32_t i = 0; i < top_n; ++i) fprintf(out, "%s{\"token\": %u, \"logit\": %.17g}", i ? ", " : "", ids[i], lg[i]);
-            fprintf(out, "]}, \"selected_token\": %u}", ids[0]);
-            current = ids[0];
-        } else {
-            fprintf(out, ", \"residual_checksum_after\": %llu, \"selected_token\": null}", (unsigned long long)qxf_fnv1a64(x, 2048 * 4));
-        }
-    }
-    t_loop = now_s() - t_loop;
-    if (ok) {
-        fprintf(out, "],\n  \"final_token\": %u,\n  \"load_seconds\": %.6f,\n  \"loop_seconds\": %.6f", current, t_load, t_loop);
-        if (bench && final_head) {
-            uint32_t *gen = (uint32_t *)malloc((size_t)gen_steps * 4);
-            float ms = 0.0f;
-            if (gen && qxg_kv_create(ctx, mi.layers, ctx_tokens, 1, err, err_len) &&
-                qxg_generate(ctx, prompt, n_prompt, gen_steps, 0, gen, &ms, err, err_len)) {
-                fprintf(out, ",\n  \"bench\": {\"device_ms\": %.6f, \"steps\": %u, \"tokens_per_second\": %.3f, \"final_token\": %u}",
-                        ms, steps, steps / (ms * 1e-3), gen[gen_steps - 1]);
-            } else {
-                ok = 0;
-            }
-            free(gen);
-        }
-        fprintf(out, "\n}\n");
-    }
-    free(x); free(a); free(y); free(kqv); free(vcur); free(moe); free(logits);
-    qxg_close(ctx);
     return ok;
 }
 

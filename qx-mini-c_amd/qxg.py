@@ -26,6 +26,25 @@ u32, u64, c_int, c_float, c_double, vp, cp = (ctypes.c_uint32, ctypes.c_uint64, 
 ERR = (cp, u64)
 
 
+MOE_STAGE_NAMES = ["ffn_norm", "ffn_moe_logits", "ffn_moe_probs", "ffn_moe_topk", "ffn_moe_weights",
+                   "ffn_moe_weights_sum", "ffn_moe_weights_norm", "ffn_moe_gate", "ffn_moe_up", "ffn_moe_swiglu",
+                   "ffn_moe_down", "ffn_moe_weighted"]
+
+
+def moe_stage_floats(experts):
+    """QXG_MOE_STAGE_FLOATS of include/qxg.h"""
+    return 2048 + 2 * experts + 25 + 3 * 8 * 768 + 2 * 8 * 2048
+
+
+def split_moe_stage(block, experts):
+    sizes = [2048, experts, experts, 8, 8, 1, 8, 8 * 768, 8 * 768, 8 * 768, 8 * 2048, 8 * 2048]
+    out, o = {}, 0
+    for n, c in zip(MOE_STAGE_NAMES, sizes):
+        out[n] = block[o:o + c]
+        o += c
+    return out
+
+
 def _sig(lib, name, args, res=c_int):
     f = getattr(lib, name)
     f.argtypes = list(args)
@@ -56,6 +75,9 @@ _sig(_g, "qxg_embed_token", [vp, u32, vp, *ERR])
 _sig(_g, "qxg_dequant_blocks", [vp, u32, vp, u64, vp, *ERR])
 _sig(_g, "qxg_attention_layer", [vp, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_moe_layer", [vp, u32, vp, vp, vp, vp, vp, *ERR])
+_sig(_g, "qxg_attention_layer_ex", [vp, u32, u32, vp, vp, vp, vp, vp, *ERR])
+_sig(_g, "qxg_attention_stage", [vp, u32, c_int, vp, vp, vp, vp, vp, vp, *ERR])
+_sig(_g, "qxg_moe_stage", [vp, u32, vp, vp, vp, *ERR])
 _sig(_g, "qxg_final_head", [vp, vp, vp, vp, u32, vp, vp, *ERR])
 _sig(_g, "qxg_set_layer_path", [vp, c_int])
 _sig(_g, "qxg_set_activation", [vp, u32, vp, u64])
@@ -215,6 +237,31 @@ class Context:
         a = np.zeros(2048, np.float32); kqv = np.zeros(4096, np.float32); vcur = np.zeros(512, np.float32)
         self._check(_g.qxg_attention_layer(self._c, layer, pos, _p(x), _p(a), _p(kqv), _p(vcur), self._err, 1024))
         return a, kqv, vcur
+
+    def attention_layer_sums(self, layer, pos, x):
+        """attention_layer plus each q head's sum of normalised softmax weights (32)."""
+        x = np.ascontiguousarray(x, np.float32)
+        a = np.zeros(2048, np.float32); kqv = np.zeros(4096, np.float32); vcur = np.zeros(512, np.float32)
+        hs = np.zeros(32, np.float64)
+        self._check(_g.qxg_attention_layer_ex(self._c, layer, pos, _p(x), _p(a), _p(kqv), _p(vcur), _p(hs), self._err, 1024))
+        return a, kqv, vcur, hs
+
+    def attention_stage(self, layer, x, f16_kv=False):
+        """(attn_norm, Vcur, kqv_out, attn_out, ffn_inp) of the single-token attention stage."""
+        x = np.ascontiguousarray(x, np.float32)
+        nrm = np.zeros(2048, np.float32); vc = np.zeros(512, np.float32); kqv = np.zeros(4096, np.float32)
+        ao = np.zeros(2048, np.float32); fi = np.zeros(2048, np.float32)
+        self._check(_g.qxg_attention_stage(self._c, layer, int(f16_kv), _p(x), _p(nrm), _p(vc), _p(kqv), _p(ao), _p(fi),
+                                           self._err, 1024))
+        return nrm, vc, kqv, ao, fi
+
+    def moe_stage(self, layer, x):
+        """(dict of the MoE stage's named vectors, ids[8]); names as the reference's sidecars."""
+        x = np.ascontiguousarray(x, np.float32)
+        E = self.info.experts
+        blk = np.zeros(moe_stage_floats(E), np.float32); ids = np.zeros(8, np.uint32)
+        self._check(_g.qxg_moe_stage(self._c, layer, _p(x), _p(blk), _p(ids), self._err, 1024))
+        return split_moe_stage(blk, E), ids
 
     def moe_layer(self, layer, x):
         x = np.ascontiguousarray(x, np.float32)

@@ -44,6 +44,18 @@ Q8_EXPERT_DOTS = [("blk.0.ffn_gate_exps.weight", 2048), ("blk.0.ffn_down_exps.we
                   ("blk.1.ffn_up_exps.weight", 2048), ("blk.1.ffn_down_exps.weight", 768),
                   ("blk.2.ffn_down_exps.weight", 768)]
 Q8_INJECT = ["none", "positive", "negative", "edge", "zero"]
+# stage probes: (model, layer) pairs; model C's layer l takes quant mix l % 4
+STAGE_CASES = [("A", 0), ("B", 1), ("C", 0), ("C", 1), ("C", 2), ("C", 3)]
+ATTN_SIDECARS = ["attn_norm", "Vcur", "kqv_out", "attn_out", "ffn_inp"]
+MOE_SIDECARS = ["ffn_norm", "ffn_moe_logits", "ffn_moe_probs", "ffn_moe_topk", "ffn_moe_weights",
+                "ffn_moe_weights_sum", "ffn_moe_weights_norm", "ffn_moe_gate", "ffn_moe_up", "ffn_moe_swiglu",
+                "ffn_moe_down", "ffn_moe_weighted"]
+
+
+def stage_input(k, layer, scale):
+    """the seeded layer / ffn input of a stage-probe case"""
+    seed = 1000 * (ord(k) - ord("A")) + layer
+    return (np.random.default_rng(seed).standard_normal(2048) * scale).astype(np.float32)
 
 
 def run(args):
@@ -150,6 +162,93 @@ def main():
                         dumps[f"{s}/{layer}/{ph}"] = str(fnv_file(os.path.join(dd, f"step-{s}-layer-{layer}-{ph}.f32")))
             out["state_loop"][k] = {"input_tokens": toks, "steps": steps, "ctx": 8, "dumps": dumps,
                                     "selected_experts": experts}
+        # attention and MoE stage probes (src/qx_format.c:5478-5725) on seeded inputs
+        out["attention_stage"], out["moe_stage"] = {}, {}
+        for k, layer in STAGE_CASES:
+            x = stage_input(k, layer, 1.0)
+            xp = os.path.join(d, f"stage{k}{layer}.f32")
+            x.tofile(xp)
+            for act in ("f32", "q8_k_compat"):
+                for kv in ("f32", "f16"):
+                    od = os.path.join(d, f"as{k}{layer}{act}{kv}")
+                    os.mkdir(od)
+                    j = json.loads(run(["attention-stage-probe", "--in", paths[k], "--layer", str(layer), "--layer-in", xp,
+                                        "--out-dir", od, "--activation", act, "--kv", kv]))
+                    j["sidecars"] = {n: str(fnv_file(os.path.join(od, f"{n}-{layer}.f32"))) for n in ATTN_SIDECARS}
+                    out["attention_stage"][f"{k}/{layer}/{act}/{kv}"] = j
+                od = os.path.join(d, f"ms{k}{layer}{act}")
+                os.mkdir(od)
+                j = json.loads(run(["moe-stage-probe", "--in", paths[k], "--layer", str(layer), "--ffn-inp", xp,
+                                    "--out-dir", od, "--activation", act]))
+                j["sidecars"] = {n: str(fnv_file(os.path.join(od, f"{n}-{layer}.f32"))) for n in MOE_SIDECARS}
+                out["moe_stage"][f"{k}/{layer}/{act}"] = j
+        # state loop variants: resume from the reference's own snapshots (the continuation
+        # token must be the snapshot's next token, src/qx_format.c:6165-6177), residual
+        # replay from a layer (--start-layer/--residual-in, :6021-6025, 6260-6268), a layer
+        # prefix (--layers below the manifest's), and the reference's error messages
+        out["state_loop_resume"], out["state_loop_replay"], out["state_loop_prefix"], out["state_loop_errors"] = {}, {}, {}, {}
+        for k, steps in (("A", 2), ("B", 2), ("C", 2)):
+            layers = MODELS[k]["layers"]
+            snap = os.path.join(GOLDEN_DIR, f"kvsnap_{k}.bin")
+            nt = out["kv_snapshot"][k]["final_token"]
+            dd = os.path.join(d, f"r{k}")
+            os.mkdir(dd)
+            txt = run(["state-loop-probe", "--in", paths[k], "--prompt-token", str(nt), "--steps", str(steps),
+                       "--layers", str(layers), "--ctx", "8", "--kv", "int8", "--full-moe", "--dump-residuals", dd,
+                       "--kv-snapshot-in", snap])
+            j = json.loads(txt)
+            pb = j["position_base"]
+            dumps = {f"{s_}/{layer}/{ph}": str(fnv_file(os.path.join(dd, f"step-{pb + s_}-layer-{layer}-{ph}.f32")))
+                     for s_ in range(steps) for layer in range(layers) for ph in PHASES}
+            out["state_loop_resume"][k] = {
+                "prompt_token": nt, "steps": steps, "position_base": pb, "final_token": j["final_token"],
+                "input_tokens": [t["input_token"] for t in j["tokens"]],
+                "selected_experts": [[ly["selected_experts"] for ly in t["layers"]] for t in j["tokens"]],
+                "k_checksums": [[str(ly["k_checksum"]) for ly in t["layers"]] for t in j["tokens"]],
+                "dumps": dumps}
+        for k, start in (("B", 1), ("C", 2)):
+            layers = MODELS[k]["layers"]
+            x = stage_input(k, 100 + start, 0.5)
+            xp = os.path.join(d, f"replay{k}.f32")
+            x.tofile(xp)
+            dd = os.path.join(d, f"p{k}")
+            os.mkdir(dd)
+            j = json.loads(run(["state-loop-probe", "--in", paths[k], "--prompt-token", "17", "--steps", "1",
+                                "--layers", str(layers), "--ctx", "8", "--kv", "int8", "--full-moe", "--dump-residuals", dd,
+                                "--start-layer", str(start), "--residual-in", xp]))
+            t0 = j["tokens"][0]
+            out["state_loop_replay"][k] = {
+                "start_layer": start, "input_scale": 0.5, "residual_checksum": str(t0["residual_checksum"]),
+                "layers": [ly["layer"] for ly in t0["layers"]],
+                "selected_experts": [ly["selected_experts"] for ly in t0["layers"]],
+                "residual_output_checksums": [str(ly["residual_output_checksum"]) for ly in t0["layers"]],
+                "dumps": {f"{layer}/{ph}": str(fnv_file(os.path.join(dd, f"step-0-layer-{layer}-{ph}.f32")))
+                          for layer in range(start, layers) for ph in PHASES}}
+        dd = os.path.join(d, "prefixB")
+        os.mkdir(dd)
+        j = json.loads(run(["state-loop-probe", "--in", paths["B"], "--prompt-token", "17", "--steps", "2", "--layers", "1",
+                            "--ctx", "8", "--kv", "int8", "--full-moe", "--dump-residuals", dd]))
+        out["state_loop_prefix"]["B"] = {
+            "layers": j["layers"], "final_token": j["final_token"], "top_keys": sorted(j.keys()),
+            "step_keys": sorted(j["tokens"][0].keys()), "layer_keys": sorted(j["tokens"][0]["layers"][0].keys()),
+            "dumps": {f"{s_}/0/{ph}": str(fnv_file(os.path.join(dd, f"step-{s_}-layer-0-{ph}.f32")))
+                      for s_ in range(2) for ph in PHASES}}
+        def err_of(args):
+            r = subprocess.run([REF] + args, capture_output=True, text=True)
+            return r.returncode, r.stderr.strip()
+        base = ["state-loop-probe", "--in", paths["A"], "--steps", "1", "--layers", "1", "--ctx", "8", "--kv", "int8",
+                "--full-moe"]
+        snapA = os.path.join(GOLDEN_DIR, "kvsnap_A.bin")
+        out["state_loop_errors"] = {
+            "token_mismatch": err_of(base + ["--prompt-token", "3", "--kv-snapshot-in", snapA]),
+            "replay_two_steps": err_of(["state-loop-probe", "--in", paths["A"], "--steps", "2", "--layers", "1", "--ctx", "8",
+                                        "--kv", "int8", "--full-moe", "--prompt-token", "17", "--start-layer", "0",
+                                        "--residual-in", os.path.join(d, "replayB.f32")]),
+            "replay_start_beyond": err_of(base + ["--prompt-token", "17", "--start-layer", "1", "--residual-in",
+                                                  os.path.join(d, "replayB.f32")]),
+            "ctx_too_small": err_of(base + ["--prompt-token", str(out["kv_snapshot"]["A"]["final_token"]),
+                                            "--kv-snapshot-in", snapA, "--ctx", "4"]),
+        }
     dst = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden.json")
     with open(dst, "w") as f:
         json.dump(out, f, indent=1, sort_keys=True)

@@ -9,6 +9,8 @@ experts of every layer are compared with the reference's router on the same inpu
 (identical except where the reference's logit margin is below 1e-4).  The oracle work is
 spread over host threads (each layer replay is independent given its inputs; ctypes
 releases the GIL)."""
+import ctypes
+import json
 import os
 import threading
 import time
@@ -43,7 +45,7 @@ def big():
     om = qxo.Model(model.path)
     prompt = np.random.default_rng(1).integers(0, VOCAB, size=8).astype(np.uint32)
     say(f"model generated and uploaded in {time.time() - t0:.1f} s")
-    yield ctx, om, prompt
+    yield ctx, om, prompt, model.path
     om.close()
     ctx.close()
     model.close()
@@ -96,7 +98,7 @@ def test_config4_48_layers_same_input(big):
     for that layer and the GPU's KV rows of the earlier positions; layer outputs 1e-5,
     the position's new KV row (codes within 1, scales 1e-5), routed experts, and the
     logits on the GPU's final residual (1e-5, top-8 margin rule)."""
-    ctx, om, prompt = big
+    ctx, om, prompt, _ = big
     ctx.kv_create(LAYERS, 16)
     okv = qxo.KV(LAYERS, 16)
     tok = int(prompt[0])
@@ -142,7 +144,7 @@ def test_config4_48_layers_same_input(big):
 def test_config4_generate_matches_steps(big):
     """The device-resident greedy loop (qxg_generate) gives the same tokens as the
     step-by-step path that the same-input test checks, for 16 tokens after the prompt."""
-    ctx, om, prompt = big
+    ctx, om, prompt, _ = big
     ctx.kv_create(LAYERS, 32)
     gen, _ = ctx.generate(prompt, 16, 0)
     ctx.kv_create(LAYERS, 32)
@@ -156,12 +158,57 @@ def test_config4_generate_matches_steps(big):
     assert list(gen) == toks
 
 
+def test_config4_state_loop_final_head(big, tmp_path):
+    """qx_dump_state_loop_probe_summary (the reference's prototype) with --full-moe
+    --final-head on the full-size model, in process (the model is an in-memory file):
+    3 greedy steps; every step's head is replayed by the oracle on that step's own final
+    residual (printed to 9 digits: the exact floats), tokens chain step to step, and the
+    attention weight sums are 1 within 1e-6 as the reference's tests require."""
+    ctx, om, prompt, model_path = big
+    h = qxg._h
+    f = h.qx_dump_state_loop_probe_summary
+    c_char_p, u32, vp = ctypes.c_char_p, ctypes.c_uint32, ctypes.c_void_p
+    f.argtypes = ([c_char_p, c_char_p, u32, u32, u32, u32, c_char_p, c_char_p] + [ctypes.c_int] * 12 +
+                  [u32, c_char_p, u32, u32, u32, ctypes.c_double, u32, c_char_p, u32, c_char_p, c_char_p, c_char_p, vp,
+                   c_char_p, ctypes.c_uint64])
+    f.restype = ctypes.c_int
+    libc = ctypes.CDLL(None)
+    libc.fopen.restype = vp
+    libc.fopen.argtypes = [c_char_p, c_char_p]
+    libc.fclose.argtypes = [vp]
+    out = tmp_path / "state_loop.json"
+    fp = libc.fopen(str(out).encode(), b"w")
+    err = ctypes.create_string_buffer(512)
+    say("state loop with the final head: 3 steps x 48 layers")
+    ok = f(model_path.encode(), None, int(prompt[0]), 3, LAYERS, 16, b"int8", b"f32", 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0,
+           2048, None, 5, 64, 5, 0.0, 1, None, 0, None, None, None, fp, err, 512)
+    libc.fclose(fp)
+    assert ok == 1, err.value.decode()
+    j = json.load(open(out))
+    assert j["layers"] == LAYERS and len(j["tokens"]) == 3
+    current = int(prompt[0])
+    for t in j["tokens"]:
+        assert t["input_token"] == current
+        fh = t["final_head"]
+        x = np.array(fh["final_residual_raw"], np.float32)
+        _, lg, ids, tl = om.final_head(x, VOCAB, 5)
+        good, why = topk_consistent([r["token"] for r in fh["top_tokens"]], ids, lg)
+        assert good, why
+        assert abs(fh["argmax_logit"] - float(lg[fh["argmax_token"]])) <= 1e-5 * max(1.0, abs(float(tl[0])))
+        assert t["selected_token"] == fh["argmax_token"]
+        for ly in t["layers"]:
+            for k in ("softmax_sum", "softmax_sum_min", "softmax_sum_max"):
+                assert abs(ly[k] - 1.0) < 1e-6, k
+        current = t["selected_token"]
+    assert j["final_token"] == current
+
+
 def test_config5_prefill_layer_512_tokens(big):
     """Config 5 at size: one prefill layer over a 512-token chunk with 128 experts (about
     32 tokens per expert, the full 4096-assignment slot layout), rows scaled over six
     orders of magnitude, replayed by the oracle token by token on the GPU's own input rows
     and KV rows: ffn input and layer output of every token within 1e-5."""
-    ctx, om, _ = big
+    ctx, om, _, _ = big
     T, layer = 512, 5
     rng = np.random.default_rng(55)
     x = rng.standard_normal((T, 2048)).astype(np.float32)
@@ -204,7 +251,7 @@ def test_config5_prefill_48_layers(big):
     at a time through its decode step) are compared without replay as a report: over 48
     chained layers an INT8 code that the two sides round differently at a .5 boundary, or a
     router tie, is carried forward, so that distance is printed, not held to 1e-5."""
-    ctx, om, prompt = big
+    ctx, om, prompt, _ = big
     n = len(prompt)
     ctx.kv_create(LAYERS, 16)
     res, lg, ids, _, _ = ctx.prefill(prompt, 0, True, 8, want_residual=True, want_logits=True)

