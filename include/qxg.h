@@ -116,6 +116,19 @@ int qxg_embed_token(qxg_ctx *ctx, uint32_t token, float *x_out, char *err, uint6
 int qxg_dequant_blocks(qxg_ctx *ctx, uint32_t ggml_type, const void *raw, uint64_t nblocks, float *out,
                        char *err, uint64_t err_len);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * qxg_dequant_blocks with the raw blocks and the f32 output in device memory the caller
+ * owns (raw_dev: nblocks blocks of the type's size; out_dev: nblocks * 256 floats) and
+ * the repacked block planes in a static device workspace (one per GPU, held until the
+ * process ends) instead of per-call allocations.  At most QXG_STATIC_MAX_BLOCKS blocks
+ * per call; more fail with an error.  Allocates nothing; returns when the output is
+ * written.  Every call on one GPU shares its workspace: calls that overlap on one GPU
+ * (from several threads or contexts) race. */
+#define QXG_STATIC_MAX_BLOCKS 4096u
+int qxg_dequant_blocks_static(qxg_ctx *ctx, uint32_t ggml_type, const void *raw_dev, uint64_t nblocks, float *out_dev,
+                              char *err, uint64_t err_len);
+
 /* Attention block of `layer` for one token at `position` on residual x_in:
  * attn RMSNorm, K/V projections, k norm + RoPE, INT8 append at [layer][position],
  * Q projection/norm/RoPE, GQA softmax over 0..position, O projection.

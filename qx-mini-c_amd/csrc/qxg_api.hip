@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -140,6 +141,7 @@ struct qxg_ctx {
     uint64_t *xch = nullptr;
     uint32_t next_ep = 0;            // epoch base of the next persistent launch
     uint32_t *abort = nullptr;
+    uint8_t *scratch = nullptr;      // device address of this GPU's static workspace (qxg_dequant_blocks_static)
     // one decode step (embed .. head, top-1, step advance) recorded once and replayed
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
@@ -719,6 +721,36 @@ int prefill_finish(qxg_ctx *c, int run_head, float *logits, uint32_t top_n, uint
 
 }  // namespace
 
+// ---- the static workspace of qxg_dequant_blocks_static ----
+// The repacked block planes of an allocation-free dequant live in `scratch`, a file-scope
+// device array: each GPU the library runs on holds its own copy until the process ends.
+// On the host the array's name is only a stand-in for it, so host code never passes it
+// on: qxg_open looks up its device address once per device, with that device current
+// (hipGetSymbolAddress), and every kernel argument uses that address.  Layout for
+// QXG_STATIC_MAX_BLOCKS blocks: planes p0 (128 bytes per block), p1 (64), p2 (32) and
+// d (2) back to back - the largest of each over the supported block types.
+constexpr uint64_t SCR_P0 = 0, SCR_P1 = 128ull * QXG_STATIC_MAX_BLOCKS, SCR_P2 = 192ull * QXG_STATIC_MAX_BLOCKS,
+                   SCR_D = 224ull * QXG_STATIC_MAX_BLOCKS, SCR_BYTES = 226ull * QXG_STATIC_MAX_BLOCKS;
+static __device__ __align__(256) uint8_t scratch[SCR_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, uint8_t *> g_scratch_addr;   // device -> address of its copy of `scratch`
+
+// the calling thread's current device must be `device`
+bool scratch_address(int device, uint8_t **addr, char *err, uint64_t n) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch_addr.find(device);
+    if (it == g_scratch_addr.end()) {
+        void *p = nullptr;
+        if (!hip_ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), err, n, "hipGetSymbolAddress(scratch)")) return false;
+        it = g_scratch_addr.emplace(device, (uint8_t *)p).first;
+    }
+    *addr = it->second;
+    return true;
+}
+}  // namespace
+
 extern "C" {
 
 int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
@@ -746,8 +778,11 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
             return 0;
         }
     }
+    uint8_t *scr = nullptr;
+    if (!scratch_address(device, &scr, err, err_len)) return 0;
     qxg_ctx *c = new qxg_ctx();
     c->device = device;
+    c->scratch = scr;
     {
         const char *ev = getenv("QXG_EAGER");
         c->eager = ev && ev[0] == '1';
@@ -1131,6 +1166,34 @@ int qxg_dequant_blocks(qxg_ctx *c, uint32_t type, const void *raw, uint64_t nblo
     if (d) (void)hipFree(d);
     free_tensor(t);
     return ok;
+}
+
+int qxg_dequant_blocks_static(qxg_ctx *c, uint32_t type, const void *raw_dev, uint64_t nblocks, float *out_dev, char *err,
+                              uint64_t err_len) {
+    if (!c || !raw_dev || !out_dev || !nblocks) { set_err(err, err_len, "invalid argument"); return 0; }
+    uint64_t bv = 0, bb = 0;
+    if (!block_geom(type, bv, bb) || type == 0) { set_err(err, err_len, "unsupported GGML type for decode-block"); return 0; }
+    if (nblocks > QXG_STATIC_MAX_BLOCKS) {
+        if (err && err_len)
+            snprintf(err, (size_t)err_len, "qxg_dequant_blocks_static: %llu blocks; the static workspace holds at most %u",
+                     (unsigned long long)nblocks, QXG_STATIC_MAX_BLOCKS);
+        return 0;
+    }
+    if (!c->scratch) { set_err(err, err_len, "static workspace address not set"); return 0; }
+    (void)hipSetDevice(c->device);
+    const uint8_t *raw = (const uint8_t *)raw_dev;
+    uint8_t *p0 = c->scratch + SCR_P0, *p1 = c->scratch + SCR_P1, *p2 = c->scratch + SCR_P2;
+    uint16_t *d = (uint16_t *)(c->scratch + SCR_D);
+    if (type == 12) {   // Q4_K is read in its original layout: straight from the caller's blocks
+        hipLaunchKernelGGL(qxk_dequant, dim3((unsigned)nblocks), dim3(256), 0, c->s, type, raw, (const uint8_t *)nullptr,
+                           (const uint8_t *)nullptr, (const uint16_t *)nullptr, c->T, nblocks, out_dev);
+    } else {
+        hipLaunchKernelGGL(qxk_repack, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0, c->s, type, raw, nblocks, p0,
+                           p1, p2, d);
+        hipLaunchKernelGGL(qxk_dequant, dim3((unsigned)nblocks), dim3(256), 0, c->s, type, (const uint8_t *)p0,
+                           (const uint8_t *)p1, (const uint8_t *)p2, (const uint16_t *)d, c->T, nblocks, out_dev);
+    }
+    return finish(c, err, err_len);
 }
 
 int qxg_q8k_quantize(qxg_ctx *c, const float *x, uint32_t n, void *blocks_out, char *err, uint64_t err_len) {

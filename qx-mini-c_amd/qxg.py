@@ -73,6 +73,7 @@ _sig(_g, "qxg_decode_token", [vp, u32, u32, c_int, vp, vp, vp, u32, vp, vp, *ERR
 _sig(_g, "qxg_generate", [vp, vp, u32, u32, u32, vp, ctypes.POINTER(c_float), *ERR])
 _sig(_g, "qxg_embed_token", [vp, u32, vp, *ERR])
 _sig(_g, "qxg_dequant_blocks", [vp, u32, vp, u64, vp, *ERR])
+_sig(_g, "qxg_dequant_blocks_static", [vp, u32, vp, u64, vp, *ERR])
 _sig(_g, "qxg_attention_layer", [vp, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_moe_layer", [vp, u32, vp, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_attention_layer_ex", [vp, u32, u32, vp, vp, vp, vp, vp, *ERR])
@@ -226,6 +227,10 @@ class Context:
         out = np.zeros(nblocks * 256, np.float32)
         self._check(_g.qxg_dequant_blocks(self._c, ggml_type, _p(raw), nblocks, _p(out), self._err, 1024))
         return out
+
+    def dequant_static(self, ggml_type, raw_dev, nblocks, out_dev):
+        """qxg_dequant_blocks_static on device addresses (ints) the caller owns."""
+        self._check(_g.qxg_dequant_blocks_static(self._c, ggml_type, vp(raw_dev), nblocks, vp(out_dev), self._err, 1024))
 
     def embed(self, token):
         x = np.zeros(2048, np.float32)
