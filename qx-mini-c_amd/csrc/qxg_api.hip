@@ -28,6 +28,9 @@ __global__ void qxk_topk_merge(const float *, const uint32_t *, uint32_t, uint32
                                DevState *);
 __global__ void qxk_q8k(const float *, uint32_t, uint8_t *, uint32_t *);
 __global__ void qxk_decode(QxDArgs);
+__global__ void qxk_interleave_experts(const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *,
+                                       const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, uint32_t, uint8_t *,
+                                       uint8_t *);
 __global__ void qxk_router_fold(const float *, const float *, const float *, uint32_t, float *);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
                             uint64_t, float *);
@@ -137,6 +140,8 @@ struct qxg_ctx {
     std::vector<void *> arenas;      // per-plane arenas of all layers' weights
     QxPlane planes[PL_COUNT] = {};
     uint8_t *mfold = nullptr;        // router fold M = W diag(w) O of every layer (f32)
+    uint8_t *gu_il = nullptr, *dn_il = nullptr;   // interleaved routed-expert rows of every layer
+    uint64_t gu_stride = 0, dn_stride = 0;
     uint64_t mfold_stride = 0;
     uint64_t *xch = nullptr;
     uint32_t next_ep = 0;            // epoch base of the next persistent launch
@@ -355,7 +360,7 @@ constexpr uint64_t DECODE_WAIT_TICKS = 100000000ull;   // 1 s of the 100 MHz wal
 // The persistent decode reads the weight arenas and the router fold, built for the
 // benchmark mix only, and computes in the f32 activation mode; other models and
 // q8_k_compat run one kernel per phase.
-bool persistent(const qxg_ctx *c) { return c->persist && c->base_mix && !c->q8 && c->emb && c->head && c->mfold; }
+bool persistent(const qxg_ctx *c) { return c->persist && c->base_mix && !c->q8 && c->emb && c->head && c->mfold && c->gu_il && c->dn_il; }
 
 struct DecodeDumps {
     float *layer = nullptr, *res = nullptr, *logits = nullptr;
@@ -376,6 +381,8 @@ bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0,
     QxDArgs a{};
     for (int i = 0; i < PL_COUNT; ++i) a.P[i] = c->planes[i];
     a.M = {c->mfold, c->mfold_stride};
+    a.GU = {c->gu_il, c->gu_stride};
+    a.DN = {c->dn_il, c->dn_stride};
     a.emb = c->emb; a.emb_row = c->emb_row;
     a.out_norm = c->out_norm;
     a.h_ql = c->head->p0; a.h_qh = c->head->p1; a.h_sc = (const int8_t *)c->head->p2; a.h_d = c->head->d;
@@ -425,6 +432,29 @@ bool build_router_fold(qxg_ctx *c, char *err, uint64_t n) {
     ok = ok && hip_ok(hipStreamSynchronize(c->s), err, n, "router fold");
     (void)hipFree(o);
     return ok;
+}
+
+// The routed experts' rows of every layer in the persistent decode's interleaved layout
+// (QXD_GU_UNIT, QXD_DN_ROW in qxg_internal.h), copied from the IQ2_XS / IQ3_XXS planes.
+bool build_expert_interleave(qxg_ctx *c, char *err, uint64_t n) {
+    for (uint8_t **p : {&c->gu_il, &c->dn_il})
+        if (*p) { (void)hipFree(*p); *p = nullptr; }
+    const uint64_t E = c->experts;
+    c->gu_stride = align256(E * 768 * QXD_GU_UNIT);
+    c->dn_stride = align256(E * 2048 * QXD_DN_ROW);
+    if (!hip_ok(hipMalloc(&c->gu_il, c->gu_stride * c->layers), err, n, "expert interleave") ||
+        !hip_ok(hipMalloc(&c->dn_il, c->dn_stride * c->layers), err, n, "expert interleave"))
+        return false;
+    bool ok = true;
+    const unsigned grid = (unsigned)((E * (768 + 2048) + 255) / 256);
+    for (uint32_t l = 0; l < c->layers && ok; ++l) {
+        const LayerW &w = c->L[l];
+        hipLaunchKernelGGL(qxk_interleave_experts, dim3(grid), dim3(256), 0, c->s, w.gate->p0, w.gate->p1, (const uint8_t *)w.gate->d,
+                           w.up->p0, w.up->p1, (const uint8_t *)w.up->d, w.down->p0, w.down->p1, (const uint8_t *)w.down->d,
+                           (uint32_t)E, c->gu_il + l * c->gu_stride, c->dn_il + l * c->dn_stride);
+        ok = hip_ok(hipGetLastError(), err, n, "expert interleave");
+    }
+    return ok && hip_ok(hipStreamSynchronize(c->s), err, n, "expert interleave");
 }
 
 void launch_step(qxg_ctx *c, uint32_t top_n, bool dump_layers) {
@@ -840,7 +870,7 @@ void qxg_close(qxg_ctx *c) {
     void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->T.g2s, c->T.g3s, c->T.sel8, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
                     c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging,
-                    c->xch, c->abort, c->apart, c->route_ids, c->route_w, c->mfold};
+                    c->xch, c->abort, c->apart, c->route_ids, c->route_w, c->mfold, c->gu_il, c->dn_il};
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (void *p : c->arenas) (void)hipFree(p);
     for (void *p : c->pf.all) (void)hipFree(p);
@@ -960,6 +990,7 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     if (layers && base && !build_arenas(c, err, err_len)) return 0;
     if (c->mfold) { (void)hipFree(c->mfold); c->mfold = nullptr; }
     if (layers && base && !build_router_fold(c, err, err_len)) return 0;
+    if (layers && base && !build_expert_interleave(c, err, err_len)) return 0;
     c->bound = true;
     return 1;
 }

@@ -118,6 +118,8 @@ enum QxPlaneId : int {
 struct QxDArgs {
     QxPlane P[PL_COUNT];         // per-layer weight planes (layer l at base + l * stride)
     QxPlane M;                   // router fold M = W diag(w) O, [experts][4096] f32 per layer
+    QxPlane GU;                  // routed experts' gate/up rows, unit-interleaved (QXD_GU_UNIT bytes per unit)
+    QxPlane DN;                  // routed experts' down rows, row-interleaved (QXD_DN_ROW bytes per row)
     const uint8_t *emb;          // Q4_K token embedding
     uint64_t emb_row;
     const float *out_norm;
@@ -143,6 +145,13 @@ struct QxDArgs {
     double sqrt_hd;
 };
 #define QXD_THREADS 512
+// Interleaved expert rows of the persistent decode: unit (expert e, row r) of gate/up is
+// [gate qs 512 | sc 64 | d 16 | up qs 512 | sc 64 | d 16] at (e * 768 + r) * 1184; down row
+// (e, r) is [qs 192 | aux 96 | d 6 | 0 x 10] at (e * 2048 + r) * 304.  A wave's rows then lie
+// in one contiguous range, so each of its 16-byte load instructions touches one or two
+// pages (the cost of a scattered load instruction grows with the pages it touches).
+#define QXD_GU_UNIT 1184u
+#define QXD_DN_ROW 304u
 // exchange words per launch: x, qkv, ctx, x', router logits, h, expert weights (two slots
 // each) and the per-workgroup argmax candidates
 #define QXD_XCH_WORDS (2u * (2048u + 5120u + 4096u + 2048u + 256u + 6144u + 16u + 2u * QXG_PBLOCKS))
