@@ -43,7 +43,7 @@
 // each workgroup's wave 0 stores s_memrealtime (100 MHz) into
 // qxd_trace_buf[layer][point][workgroup]; read back with qxd_trace_read.
 #ifdef QXD_TRACE
-__device__ unsigned long long qxd_trace_buf[49][24][256];
+__device__ unsigned long long qxd_trace_buf[49][32][256];
 extern "C" int qxd_trace_read(unsigned long long *out) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(qxd_trace_buf), sizeof(qxd_trace_buf)) == hipSuccess;
 }
@@ -167,15 +167,19 @@ static_assert(NT == QXD_THREADS, "workgroup size");
 namespace {
 
 // ---------------------------------------------------------------- LDS
+struct AttnW {                   // one wave's attention scratch
+    int8_t kc[128], vc[128];     // the position's K and V codes of the workgroup's kv head
+    float p[16];                 // weights of the wave's positions in the current block
+};
 struct AttnS {
-    float q[128], k[512], v[512];
-    uint32_t qd[4 * DIG_STRIDE];
-    int8_t kq[512], vq[512];     // the position's INT8 K and V rows (all four kv heads)
-    double sc[QXG_MAX_CTX];      // scores, then weights
-    float part[32][132];         // context partial sums
-    float mx[2 * NWV];
-    double redd[2 * NWV];
-    float scale[2];
+    float q[128], k[512], v[512];   // polled q of the head, K and V rows (all four kv heads)
+    uint32_t qd[4 * DIG_STRIDE];    // q digit planes
+    float kmx[4], vmx[4];           // largest magnitudes of the K and V rows per kv head
+    uint32_t qok;
+    AttnW w[NWV];
+    int8_t kq[512], vq[512];        // the position's INT8 K and V rows (cache store)
+    float ctx[NWV][4][128];         // per wave and position subgroup: context partial sums
+    double m[NWV], l[NWV];          // per wave: running maximum and denominator
 };
 struct DLds {
     uint4 g2[512];
@@ -513,26 +517,30 @@ DEV void store_rows(const u32x4 (&v)[N], uint8_t *lds) {
 // (4625-4641, host table), INT8 K/V quantization of the position over all 512 values
 // (4449-4463; workgroup 0 stores the rows, every workgroup derives the same row), scores of
 // q as int8 digit planes against the INT8 K codes (v_dot4, exact), double softmax, f32
-// context.  Rows of positions written by this launch (>= pos0) are read with coherent
-// loads, older rows with plain loads.
+// context.
 //
-// The cached rows of the first ATT_PRE positions are fetched before the Q/K/V exchange is
-// polled (their addresses depend only on the layer and the position count): thread t
-// takes the 32 K bytes of group t%4 of position t/4 (the score loop's first pass) and the
-// 8 V bytes of dims 8(t%16).. of positions t/16 + 32 i (the context loop's).
-constexpr uint32_t ATT_PRE = 128;
+// Every wave works on its own until one barrier: it normalises and rotates the k of all four
+// kv heads (the INT8 scale is over the whole 512-value row) and its q, forms the position's
+// codes, then takes positions 128 i + 16 w .. + 15 (wave w, a quad per position) with an
+// online softmax: running maximum m, denominator l and f32 context partial sums, rescaled
+// by exp(m_old - m_new) when the maximum grows.  After the barrier thread d < 128 merges the
+// eight waves: ctx[d] = sum_w (float)(exp(m_w - M) / L) * acc_w[d], L = sum_w exp(m_w - M) l_w
+// (the same quantity as the reference's sum of exp(s - max) / den, within f32 roundings).
+//
+// The cached rows of positions 16 w + j (j < 16) are fetched before the Q/K/V exchange is
+// polled (their addresses depend only on the layer and the position count): lane q of the
+// quad of position 16 w + j takes the 32 K bytes of group q and the K and V scales, and lane
+// (p, g) (p = lane / 16, g = lane % 16) the 8 V bytes of dims 8 g .. of positions 16 w + 4 i + p.
 struct AttnPre {   // vector-typed fields: they stay in registers (arrays filled in branches did not)
     u32x4 k0, k1;
-    float ks;
+    float ks, vs;      // K and V scales of the quad's position
     u32x2 v0, v1, v2, v3;
-    float vs;          // V scale of position tid (the softmax loop's first pass)
     double cs, sn;     // RoPE table entries of the position, dims lane and lane + 64
-    float n0, n1;      // k-norm weights (waves 0..3) or q-norm weights (wave 4), dims lane, lane + 64
+    float nq0, nq1, nk0, nk1;   // q- and k-norm weights, dims lane, lane + 64
 };
 // KV cache reads: agent-coherent (sc1) buffer loads, 16/8/4 bytes per lane.  Rows written
 // earlier in this launch were stored by workgroup 0 with agent-scope stores; every row is
-// read the same way (one load instruction per piece instead of a coherent and a plain path
-// per lane: the vector-memory unit's time goes by instructions).
+// read the same way.
 constexpr int CP_SC1 = 16;
 template <typename T>
 DEV __amdgpu_buffer_rsrc_t rsrc(const T *p) { return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, 0x7fffffff, 0x00020000); }
@@ -540,138 +548,186 @@ DEV u32x4 kv_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amd
 DEV u32x2 kv_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CP_SC1); }
 DEV uint32_t kv_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CP_SC1); }
 
-DEV void attn_prefetch(const QxDArgs &a, uint32_t l, uint32_t pos, AttnPre &p) {
-    const int tid = tix();
+// the cached rows of one 128-position block (t0 = 128 i) for the calling lane, clamped to
+// positions below pos (the position itself comes from the wave's own codes)
+struct AttnRows {
+    u32x4 k0, k1;
+    float ks, vs;
+    u32x2 v[4];
+};
+DEV void attn_rows(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t t0, AttnRows &r) {
+    const int lane = tix() & 63, w = wave_id();
     const int kvh = blockIdx.x >> 3;
     const auto kr = rsrc(a.kc), vr = rsrc(a.vc), ksr = rsrc(a.ks), vsr = rsrc(a.vs);
-    const uint32_t base = l * a.ctx, last = pos > 0 ? pos - 1 : 0u;   // positions past pos - 1 are never used
-    {   // K: position tid/4, 32 bytes of group tid%4
-        const uint32_t t = min((uint32_t)tid >> 2, last);
-        const uint32_t off = ((base + t) * 128 + 32 * kvh + 8 * (tid & 3)) * 4;
-        p.k0 = kv_ld16(kr, off);
-        p.k1 = kv_ld16(kr, off + 16);
-        p.ks = __uint_as_float(kv_ld4(ksr, (base + t) * 4));
+    const uint32_t base = l * a.ctx, last = pos > 0 ? pos - 1 : 0u;
+    const uint32_t tq = min(t0 + 16u * w + (lane >> 2), last);
+    const uint32_t off = ((base + tq) * 128 + 32 * kvh + 8 * (lane & 3)) * 4;
+    r.k0 = kv_ld16(kr, off);
+    r.k1 = kv_ld16(kr, off + 16);
+    r.ks = __uint_as_float(kv_ld4(ksr, (base + tq) * 4));
+    r.vs = __uint_as_float(kv_ld4(vsr, (base + tq) * 4));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t tv = min(t0 + 16u * w + 4u * i + (lane >> 4), last);
+        r.v[i] = kv_ld8(vr, ((base + tv) * 128 + 32 * kvh + 2 * (lane & 15)) * 4);
     }
-    // V: positions tid/16 + 32 i, 8 bytes of dims 8 (tid % 16) ..
-    auto vld = [&](uint32_t i) -> u32x2 {
-        const uint32_t t = min((uint32_t)(tid >> 4) + 32u * i, last);
-        return kv_ld8(vr, ((base + t) * 128 + 32 * kvh + 2 * (tid & 15)) * 4);
-    };
-    p.v0 = vld(0); p.v1 = vld(1); p.v2 = vld(2); p.v3 = vld(3);
-    p.vs = __uint_as_float(kv_ld4(vsr, (base + min((uint32_t)tid, last)) * 4));
-    const int lane = tid & 63;
+}
+
+DEV void attn_prefetch(const QxDArgs &a, uint32_t l, uint32_t pos, AttnPre &p) {
+    AttnRows r;
+    attn_rows(a, l, pos, 0u, r);
+    p.k0 = r.k0; p.k1 = r.k1; p.ks = r.ks; p.vs = r.vs;
+    p.v0 = r.v[0]; p.v1 = r.v[1]; p.v2 = r.v[2]; p.v3 = r.v[3];
+    const int lane = tix() & 63;
     p.cs = gp(a.T.rope_cos)[pos * 64 + lane];
     p.sn = gp(a.T.rope_sin)[pos * 64 + lane];
-    const GLB float *nw = (const GLB float *)plane(a, (tid >> 6) == 4 ? PL_Q_NORM : PL_K_NORM, l);
-    p.n0 = nw[lane];
-    p.n1 = nw[64 + lane];
+    const GLB float *nq = (const GLB float *)plane(a, PL_Q_NORM, l), *nk = (const GLB float *)plane(a, PL_K_NORM, l);
+    p.nq0 = nq[lane]; p.nq1 = nq[64 + lane];
+    p.nk0 = nk[lane]; p.nk1 = nk[64 + lane];
 }
 
 // The Q/K/V words of head h's workgroup: q rows 128 h .. 128 h + 127, then the K and V rows
-// (4096 .. 5119), into A.q, A.k, A.v; sentinels: the K/V word of each producer workgroup
-// (published with its Q rows in one store)
+// (4096 .. 5119), into A.q, A.k, A.v
 DEV bool attn_wait(const QxDArgs &a, uint32_t l, uint32_t ep, DLds &S, const Ctl &c) {
     const int h = blockIdx.x;
     const GLB uint64_t *qkv = gp(a.xch) + XO_QKV + (l & 1) * XN_QKV;
     return wait_xch2<2>(qkv, 1152, ep, reinterpret_cast<uint32_t *>(S.u.att.q), [h](int i) { return i < 128 ? 128 * h + i : 3968 + i; }, S, c);
 }
 
+// wave-level LDS hand-off: the wave's own earlier LDS writes are seen by its later reads
+// (LDS instructions of a wave execute in order); this only keeps the compiler from
+// reordering them
+DEV void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+DEV float wave_max_f(float v) {
+    v = fmaxf(v, dppf<DPP_XOR1>(v)); v = fmaxf(v, dppf<DPP_XOR2>(v));
+    v = fmaxf(v, dppf<DPP_ROR4>(v)); v = fmaxf(v, dppf<DPP_ROR8>(v));
+    return fmaxf(fmaxf(rdlanef(v, 0), rdlanef(v, 16)), fmaxf(rdlanef(v, 32), rdlanef(v, 48)));
+}
+DEV int8_t int8_code(float x, float scale) {   // reference :4449-4463: rint(x / scale) clamped, non-finite -> 0
+    const int q = isfinite(x) ? (int)rintf(x / scale) : 0;
+    return (int8_t)(q < -127 ? -127 : q > 127 ? 127 : q);
+}
+
 // ep: the QKV phase (the context goes out at ep + 1)
-DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, const AttnPre &pre, DLds &S) {
+DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, const AttnPre &pre, DLds &S, bool last) {
+    (void)last;
     AttnS &A = S.u.att;
-    const int tid = tix(), lane = tid & 63, wave = tid >> 6;
+    const int tid = tix(), lane = tid & 63;
+    const int w = wave_id();
     const int h = blockIdx.x, kvh = h >> 3;
+    AttnW &W = A.w[w];
     const uint32_t n = pos + 1;
-    const double cs = pre.cs, sn = pre.sn;
-    if (wave < 4) {   // k of kv head `wave`
-        float k0 = A.k[128 * wave + lane], k1 = A.k[128 * wave + 64 + lane];
-        head_norm_rope_wave(k0, k1, pre.n0, pre.n1, cs, sn);
-        A.k[128 * wave + lane] = k0;
-        A.k[128 * wave + 64 + lane] = k1;
-    } else if (wave == 4) {
-        float q0 = A.q[lane], q1 = A.q[64 + lane];
-        head_norm_rope_wave(q0, q1, pre.n0, pre.n1, cs, sn);
-        A.q[lane] = q0;
-        A.q[64 + lane] = q1;
+    // ---- the position's rows: waves 0..3 normalise and rotate k of kv head w (in place) and
+    // take its largest magnitude; wave 4 normalises and rotates q and forms its digit planes
+    // (lanes 0..15); waves 5..7 take the largest magnitudes of the four v heads
+    if (w < 4) {
+        float k0 = A.k[128 * w + lane], k1 = A.k[128 * w + 64 + lane];
+        head_norm_rope_wave(k0, k1, pre.nk0, pre.nk1, pre.cs, pre.sn);
+        A.k[128 * w + lane] = k0;
+        A.k[128 * w + 64 + lane] = k1;
+        const float mx = wave_max_f(fmaxf(isfinite(k0) ? fabsf(k0) : 0.0f, isfinite(k1) ? fabsf(k1) : 0.0f));
+        if (lane == 0) A.kmx[w] = mx;
+    } else if (w > 4) {   // v heads 0, 1 (wave 5), 2 (wave 6), 3 (wave 7)
+        const int j0 = w == 5 ? 0 : w - 4, j1 = w == 5 ? 1 : w - 4;
+        const float v0 = A.v[128 * j0 + lane], v1 = A.v[128 * j0 + 64 + lane];
+        const float v2 = A.v[128 * j1 + lane], v3 = A.v[128 * j1 + 64 + lane];
+        const float m0 = wave_max_f(fmaxf(isfinite(v0) ? fabsf(v0) : 0.0f, isfinite(v1) ? fabsf(v1) : 0.0f));
+        const float m1 = wave_max_f(fmaxf(isfinite(v2) ? fabsf(v2) : 0.0f, isfinite(v3) ? fabsf(v3) : 0.0f));
+        if (lane == 0) { A.vmx[j0] = m0; A.vmx[j1] = m1; }
+    } else {   // wave 4
+        {
+            float q0 = A.q[lane], q1 = A.q[64 + lane];
+            head_norm_rope_wave(q0, q1, pre.nq0, pre.nq1, pre.cs, pre.sn);
+            A.q[lane] = q0;
+            A.q[64 + lane] = q1;
+            wave_lds_sync();
+            bool qfin = true;
+            if (lane < 16) {
+                float y[8];
+                const float4 a0 = reinterpret_cast<const float4 *>(A.q)[2 * lane], a1 = reinterpret_cast<const float4 *>(A.q)[2 * lane + 1];
+                y[0] = a0.x; y[1] = a0.y; y[2] = a0.z; y[3] = a0.w; y[4] = a1.x; y[5] = a1.y; y[6] = a1.z; y[7] = a1.w;
+                float mx2 = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) { qfin = qfin && isfinite(y[i]); mx2 = fmaxf(mx2, fabsf(y[i])); }
+                mx2 = fmaxf(mx2, dppf<DPP_XOR1>(mx2));
+                mx2 = fmaxf(mx2, dppf<DPP_XOR2>(mx2));
+                uint32_t h0, h1, m0, m1, l0, l1;
+                float scq;
+                digits8(y, isfinite(mx2) ? mx2 : 0.0f, h0, h1, m0, m1, l0, l1, scq);
+                uint32_t *dd = A.qd + (lane >> 2) * DIG_STRIDE;
+                const int q = lane & 3;
+                *reinterpret_cast<uint2 *>(dd + 2 * q) = make_uint2(h0, h1);
+                *reinterpret_cast<uint2 *>(dd + 8 + 2 * q) = make_uint2(m0, m1);
+                *reinterpret_cast<uint2 *>(dd + 16 + 2 * q) = make_uint2(l0, l1);
+                if (q == 0) dd[24] = __float_as_uint(scq);
+            }
+            const bool allfin = __ballot(!qfin) == 0;
+            if (lane == 0) A.qok = allfin ? 1u : 0u;
+        }
     }
+    DMARK(l, 25);
     __syncthreads();
-    // INT8 K/V rows: scale = max|x| / 127 (1 if zero), codes rint(x / scale) clamped
-    float ka = isfinite(A.k[tid]) ? fabsf(A.k[tid]) : 0.0f, va = isfinite(A.v[tid]) ? fabsf(A.v[tid]) : 0.0f;
-    ka = fmaxf(ka, dppf<DPP_XOR1>(ka)); va = fmaxf(va, dppf<DPP_XOR1>(va));
-    ka = fmaxf(ka, dppf<DPP_XOR2>(ka)); va = fmaxf(va, dppf<DPP_XOR2>(va));
-    ka = fmaxf(ka, dppf<DPP_ROR4>(ka)); va = fmaxf(va, dppf<DPP_ROR4>(va));
-    ka = fmaxf(ka, dppf<DPP_ROR8>(ka)); va = fmaxf(va, dppf<DPP_ROR8>(va));
-    ka = fmaxf(fmaxf(rdlanef(ka, 0), rdlanef(ka, 16)), fmaxf(rdlanef(ka, 32), rdlanef(ka, 48)));
-    va = fmaxf(fmaxf(rdlanef(va, 0), rdlanef(va, 16)), fmaxf(rdlanef(va, 32), rdlanef(va, 48)));
-    if (lane == 0) { A.mx[wave] = ka; A.mx[NWV + wave] = va; }
-    // q digit planes (4 groups of 32: threads 0..15, 8 values each, quads share a group)
-    bool qfin = true;
-    if (tid < 16) {
-        float y[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) { y[i] = A.q[8 * tid + i]; qfin = qfin && isfinite(y[i]); }
-        float mx = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(y[i]));
-        mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
-        mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
-        uint32_t h0, h1, m0, m1, l0, l1;
-        float scq;
-        digits8(y, isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, scq);
-        uint32_t *d = A.qd + (tid >> 2) * DIG_STRIDE;
-        const int q = tid & 3;
-        *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
-        *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
-        *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
-        if (q == 0) d[24] = __float_as_uint(scq);
-    }
-    const bool qok = !block_any(!qfin, S);   // barrier: A.mx, A.qd visible
-    float kmx = 0.0f, vmx = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NWV; ++w) { kmx = fmaxf(kmx, A.mx[w]); vmx = fmaxf(vmx, A.mx[NWV + w]); }
+    DMARK(l, 21);
+    const float kmx = fmaxf(fmaxf(A.kmx[0], A.kmx[1]), fmaxf(A.kmx[2], A.kmx[3]));
+    const float vmx = fmaxf(fmaxf(A.vmx[0], A.vmx[1]), fmaxf(A.vmx[2], A.vmx[3]));
     const float kscale = kmx > 0.0f ? kmx / 127.0f : 1.0f, vscale = vmx > 0.0f ? vmx / 127.0f : 1.0f;
-    {
-        const float kx = A.k[tid], vx = A.v[tid];
-        int qk = isfinite(kx) ? (int)rintf(kx / kscale) : 0;
-        int qv = isfinite(vx) ? (int)rintf(vx / vscale) : 0;
-        A.kq[tid] = (int8_t)(qk < -127 ? -127 : qk > 127 ? 127 : qk);
-        A.vq[tid] = (int8_t)(qv < -127 ? -127 : qv > 127 ? 127 : qv);
+    const bool qok = A.qok != 0u;
+    // the codes of the workgroup's kv head for the position, by the wave whose block holds it
+    const int wpos = (int)((pos & 127u) >> 4);
+    if (w == wpos) {
+        W.kc[lane] = int8_code(A.k[128 * kvh + lane], kscale);
+        W.kc[64 + lane] = int8_code(A.k[128 * kvh + 64 + lane], kscale);
+        W.vc[lane] = int8_code(A.v[128 * kvh + lane], vscale);
+        W.vc[64 + lane] = int8_code(A.v[128 * kvh + 64 + lane], vscale);
     }
-    __syncthreads();
-    // the cache as 32-bit words: rows of 128 words, scales at [layer * ctx + position]
-    GLB uint32_t *kc = (GLB uint32_t *)gpw(a.kc), *vc = (GLB uint32_t *)gpw(a.vc);
-    GLB uint32_t *ksw = (GLB uint32_t *)gpw(a.ks), *vsw = (GLB uint32_t *)gpw(a.vs);
-    const uint32_t base = l * a.ctx;   // slot of position 0 (layers * ctx * 512 < 2^32)
-    if (h == 0) {   // the position's rows into the cache, coherent (later steps read them)
-        const uint32_t slot = base + pos;
-        if (tid < 128) st_coherent(kc + slot * 128 + tid, reinterpret_cast<const uint32_t *>(A.kq)[tid]);
-        else if (tid < 256) st_coherent(vc + slot * 128 + (tid - 128), reinterpret_cast<const uint32_t *>(A.vq)[tid - 128]);
-        else if (tid == 256) st_coherent(ksw + slot, __float_as_uint(kscale));
-        else if (tid == 257) st_coherent(vsw + slot, __float_as_uint(vscale));
+    if (h == 0) {   // the position's rows into the cache, coherent (later steps read them): wave w
+        // stores the K row of kv head w (w < 4) or the V row of kv head w - 4
+        const int j = w & 3;
+        const float *src = w < 4 ? A.k : A.v;
+        const float sc = w < 4 ? kscale : vscale;
+        int8_t *dst = (w < 4 ? A.kq : A.vq) + 128 * j;
+        dst[lane] = int8_code(src[128 * j + lane], sc);
+        dst[64 + lane] = int8_code(src[128 * j + 64 + lane], sc);
+        wave_lds_sync();
+        const uint32_t slot = l * a.ctx + pos;   // layers * ctx * 512 < 2^32
+        GLB uint32_t *row = (GLB uint32_t *)gpw(w < 4 ? a.kc : a.vc) + slot * 128 + 32 * j;
+        if (lane < 32) st_coherent(row + lane, reinterpret_cast<const uint32_t *>(dst)[lane]);
+        if (w == 0 && lane == 0) {
+            st_coherent((GLB uint32_t *)gpw(a.ks) + slot, __float_as_uint(kscale));
+            st_coherent((GLB uint32_t *)gpw(a.vs) + slot, __float_as_uint(vscale));
+        }
     }
-    // scores: a quad per position, lane q4 the 32-dim group q4 of kv head kvh
-    const int q4 = tid & 3;
+    wave_lds_sync();
+    DMARK(l, 22);
+    // ---- positions 128 i + 16 w + j: scores (a quad per position), online softmax, context
+    const int q4 = lane & 3, jq = lane >> 2, p4 = lane >> 4, dg = lane & 15;
     Dig d;
     load_dig(A.qd, q4, d);
-    double mx = -1.0e300;
-    const auto kr = rsrc(a.kc), vr = rsrc(a.vc), ksr = rsrc(a.ks), vsr = rsrc(a.vs);
-    for (uint32_t t = tid >> 2; t < n; t += NT / 4) {
+    const double inv_sqrt_hd = 1.0 / a.sqrt_hd;
+    double m = -INFINITY, lsum = 0.0;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    AttnRows cur, nxt;
+    cur.k0 = pre.k0; cur.k1 = pre.k1; cur.ks = pre.ks; cur.vs = pre.vs;
+    cur.v[0] = pre.v0; cur.v[1] = pre.v1; cur.v[2] = pre.v2; cur.v[3] = pre.v3;
+    for (uint32_t t0 = 0; t0 < n; t0 += 128) {
+        if (t0 + 128 < n) attn_rows(a, l, pos, t0 + 128, nxt);   // the next block's rows, ahead
+        const uint32_t tq = t0 + 16u * w + (uint32_t)jq;
         uint32_t kw[8];
-        float ksc;
-        if (t == pos) {
-            const uint4 *p = reinterpret_cast<const uint4 *>(A.kq + 128 * kvh + 32 * q4);
-            const uint4 x0 = p[0], x1 = p[1];
+        float ksc = cur.ks, vsc = cur.vs;
+        kw[0] = cur.k0.x; kw[1] = cur.k0.y; kw[2] = cur.k0.z; kw[3] = cur.k0.w;
+        kw[4] = cur.k1.x; kw[5] = cur.k1.y; kw[6] = cur.k1.z; kw[7] = cur.k1.w;
+        if (tq == pos) {
+            const uint4 *pk = reinterpret_cast<const uint4 *>(W.kc + 32 * q4);
+            const uint4 x0 = pk[0], x1 = pk[1];
             kw[0] = x0.x; kw[1] = x0.y; kw[2] = x0.z; kw[3] = x0.w; kw[4] = x1.x; kw[5] = x1.y; kw[6] = x1.z; kw[7] = x1.w;
             ksc = kscale;
-        } else if (t < ATT_PRE) {   // t = tid / 4: the prefetched row
-            kw[0] = pre.k0.x; kw[1] = pre.k0.y; kw[2] = pre.k0.z; kw[3] = pre.k0.w;
-            kw[4] = pre.k1.x; kw[5] = pre.k1.y; kw[6] = pre.k1.z; kw[7] = pre.k1.w;
-            ksc = pre.ks;
-        } else {
-            const uint32_t off = ((base + t) * 128 + 32 * kvh + 8 * q4) * 4;
-            const u32x4 x0 = kv_ld16(kr, off), x1 = kv_ld16(kr, off + 16);
-            kw[0] = x0.x; kw[1] = x0.y; kw[2] = x0.z; kw[3] = x0.w; kw[4] = x1.x; kw[5] = x1.y; kw[6] = x1.z; kw[7] = x1.w;
-            ksc = __uint_as_float(kv_ld4(ksr, (base + t) * 4));
+            vsc = vscale;
         }
         int aH = 0, aM = 0, aL = 0;
 #pragma unroll
@@ -680,77 +736,64 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
             aM = sdot4(kw[i], d.m[i], aM);
             aL = sdot4(kw[i], d.l[i], aL);
         }
-        double acc = (double)(combine(aH, aM, aL) * d.s);
-        acc += dppd<DPP_XOR1>(acc);
-        acc += dppd<DPP_XOR2>(acc);
-        double sc = qok ? acc * (double)ksc / a.sqrt_hd : 0.0;
+        double sq = (double)(combine(aH, aM, aL) * d.s);
+        sq += dppd<DPP_XOR1>(sq);
+        sq += dppd<DPP_XOR2>(sq);
+        double sc = qok ? sq * (double)ksc * inv_sqrt_hd : 0.0;
         if (!isfinite(sc)) sc = 0.0;
-        if (q4 == 0) A.sc[t] = sc;
-        mx = fmax(mx, sc);
-    }
-    mx = wave_max_d(mx);
-    if (lane == 0) A.redd[wave] = mx;
-    __syncthreads();
-    mx = A.redd[0];
+        const bool valid = tq < n;
+        const double mi = wave_max_d(valid ? sc : -INFINITY);
+        if (mi != -INFINITY) {   // wave-uniform: the block holds some of the wave's positions
+            const double mn = fmax(m, mi);
+            const double f = exp(m - mn);   // 0 on the first block with positions (m = -inf)
+            const double e = valid ? exp(sc - mn) : 0.0;
+            lsum = lsum * f + wave_total_d(q4 == 0 ? e : 0.0);
+            if (q4 == 0) W.p[jq] = (float)(e * (double)vsc);
+            wave_lds_sync();
+            const float ff = (float)f;
 #pragma unroll
-    for (int w = 1; w < NWV; ++w) mx = fmax(mx, A.redd[w]);
-    // softmax in double: e_t = exp(s_t - mx), den = sum e_t (1 if not finite and positive)
-    double den = 0.0;
-    for (uint32_t t = tid; t < n; t += NT) {
-        const double e = exp(A.sc[t] - mx);
-        A.sc[t] = e;
-        den += e;
-    }
-    den = wave_total_d(den);
-    if (lane == 0) A.redd[NWV + wave] = den;
-    __syncthreads();
-    den = ((A.redd[NWV + 0] + A.redd[NWV + 1]) + (A.redd[NWV + 2] + A.redd[NWV + 3])) +
-          ((A.redd[NWV + 4] + A.redd[NWV + 5]) + (A.redd[NWV + 6] + A.redd[NWV + 7]));
-    if (!isfinite(den) || den <= 0.0) den = 1.0;
-    // weights with the V scales folded in
-    for (uint32_t t = tid; t < n; t += NT) {
-        float vsc;
-        if (t == pos) vsc = vscale;
-        else if (t < NT) vsc = pre.vs;   // t = tid: prefetched
-        else vsc = __uint_as_float(kv_ld4(vsr, (base + t) * 4));
-        A.sc[t] = (A.sc[t] / den) * (double)vsc;
-    }
-    __syncthreads();
-    // context: thread (g = tid / 16, 8 dims 8 (tid % 16) ..) sums positions g, g + 32, ...;
-    // the 32 partial sums of a dimension are added in g order
-    {
-        const int g = tid >> 4, dg = tid & 15;
-        float acc[8];
+            for (int i = 0; i < 8; ++i) acc[i] *= ff;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-        uint32_t i = 0;
-        for (uint32_t t = g; t < n; t += 32, ++i) {
-            const float p = (float)A.sc[t];
-            uint32_t v0, v1;
-            if (t == pos) {
-                const uint2 x = reinterpret_cast<const uint2 *>(A.vq + 128 * kvh)[dg];
-                v0 = x.x; v1 = x.y;
-            } else if (t < ATT_PRE) {   // t = tid / 16 + 32 i: the prefetched row
-                const u32x2 x = i == 0 ? pre.v0 : i == 1 ? pre.v1 : i == 2 ? pre.v2 : pre.v3;
-                v0 = x.x; v1 = x.y;
-            } else {
-                const u32x2 x = kv_ld8(vr, ((base + t) * 128 + 32 * kvh + 2 * dg) * 4);
-                v0 = x.x; v1 = x.y;
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t jv = 4u * i + (uint32_t)p4, tv = t0 + 16u * w + jv;
+                const float pv = W.p[jv];
+                u32x2 x = cur.v[i];
+                if (tv == pos) x = reinterpret_cast<const u32x2 *>(W.vc)[dg];
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const int8_t vb = (int8_t)((((b < 4) ? x.x : x.y) >> (8 * (b & 3))) & 255u);
+                    acc[b] = fmaf(pv, (float)vb, acc[b]);
+                }
             }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int8_t vb = (int8_t)((((j < 4) ? v0 : v1) >> (8 * (j & 3))) & 255u);
-                acc[j] = fmaf(p, (float)vb, acc[j]);
-            }
+            wave_lds_sync();   // W.p is rewritten by the next block
+            m = mn;
         }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) A.part[g][8 * dg + j] = acc[j];
+        if (t0 + 128 < n) cur = nxt;
     }
+    DMARK(l, 23);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) A.ctx[w][p4][8 * dg + i] = acc[i];
+    if (lane == 0) { A.m[w] = m; A.l[w] = lsum; }
     __syncthreads();
+    DMARK(l, 24);
     if (tid < 128) {
+        double M = A.m[0];
+#pragma unroll
+        for (int v = 1; v < NWV; ++v) M = fmax(M, A.m[v]);
+        // lane v < 8 forms wave v's factor exp(m_v - M); every lane then reads the eight
+        const double mv = A.m[lane & 7];
+        const double fl = mv == -INFINITY ? 0.0 : exp(mv - M);
+        double fw[NWV], L = 0.0;
+#pragma unroll
+        for (int v = 0; v < NWV; ++v) { fw[v] = rdlaned(fl, v); L += fw[v] * A.l[v]; }
+        if (!isfinite(L) || L <= 0.0) L = 1.0;
+        const double invL = 1.0 / L;
         float o = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) o += A.part[i][tid];
+        for (int v = 0; v < NWV; ++v) {
+            const float part = (A.ctx[v][0][tid] + A.ctx[v][1][tid]) + (A.ctx[v][2][tid] + A.ctx[v][3][tid]);
+            o = fmaf((float)(fw[v] * invL), part, o);
+        }
         xstf(gpw(a.xch) + XO_CX + (l & 1) * XN_CX + 128 * h + tid, ep + 1, o);   // the CX phase
     }
     __syncthreads();   // the union is reused by the next stage
@@ -953,7 +996,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             if (wg < QXG_HEADS) {
                 if (!attn_wait(a, l, ep + 1, S, ctl)) return;
                 DMARK(l, 3);
-                attention(a, l, pos, ep + 1, ap, S);
+                attention(a, l, pos, ep + 1, ap, S, last);
                 DMARK(l, 4);
             } else {
                 // While the attention runs, the other workgroups touch every translation page
