@@ -32,6 +32,7 @@ __global__ void qxk_interleave_experts(const uint8_t *, const uint8_t *, const u
                                        const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, uint32_t, uint8_t *,
                                        uint8_t *);
 __global__ void qxk_router_fold(const float *, const float *, const float *, uint32_t, float *);
+__global__ void qxk_interleave_head(const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, uint32_t, uint8_t *);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
                             uint64_t, float *);
 __global__ void qxk_repack(uint32_t, const uint8_t *, uint64_t, uint8_t *, uint8_t *, uint8_t *, uint16_t *);
@@ -141,6 +142,7 @@ struct qxg_ctx {
     QxPlane planes[PL_COUNT] = {};
     uint8_t *mfold = nullptr;        // router fold M = W diag(w) O of every layer (f32)
     uint8_t *gu_il = nullptr, *dn_il = nullptr;   // interleaved routed-expert rows of every layer
+    uint8_t *head_il = nullptr;                   // interleaved head rows
     uint64_t gu_stride = 0, dn_stride = 0;
     uint64_t mfold_stride = 0;
     uint64_t *xch = nullptr;
@@ -360,7 +362,9 @@ constexpr uint64_t DECODE_WAIT_TICKS = 100000000ull;   // 1 s of the 100 MHz wal
 // The persistent decode reads the weight arenas and the router fold, built for the
 // benchmark mix only, and computes in the f32 activation mode; other models and
 // q8_k_compat run one kernel per phase.
-bool persistent(const qxg_ctx *c) { return c->persist && c->base_mix && !c->q8 && c->emb && c->head && c->mfold && c->gu_il && c->dn_il; }
+bool persistent(const qxg_ctx *c) {
+    return c->persist && c->base_mix && !c->q8 && c->emb && c->head && c->mfold && c->gu_il && c->dn_il && c->head_il;
+}
 
 struct DecodeDumps {
     float *layer = nullptr, *res = nullptr, *logits = nullptr;
@@ -386,6 +390,7 @@ bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0,
     a.emb = c->emb; a.emb_row = c->emb_row;
     a.out_norm = c->out_norm;
     a.h_ql = c->head->p0; a.h_qh = c->head->p1; a.h_sc = (const int8_t *)c->head->p2; a.h_d = c->head->d;
+    a.h_il = c->head_il;
     a.vocab = c->vocab; a.layers = c->layers; a.experts = c->experts; a.ctx = c->kv_ctx;
     a.steps = steps; a.n_prompt = n_prompt; a.pos0 = pos0; a.force_head = force_head ? 1u : 0u;
     a.ep0 = c->next_ep;
@@ -453,6 +458,15 @@ bool build_expert_interleave(qxg_ctx *c, char *err, uint64_t n) {
                            w.up->p0, w.up->p1, (const uint8_t *)w.up->d, w.down->p0, w.down->p1, (const uint8_t *)w.down->d,
                            (uint32_t)E, c->gu_il + l * c->gu_stride, c->dn_il + l * c->dn_stride);
         ok = hip_ok(hipGetLastError(), err, n, "expert interleave");
+    }
+    if (ok && c->head) {
+        if (c->head_il) { (void)hipFree(c->head_il); c->head_il = nullptr; }
+        ok = hip_ok(hipMalloc(&c->head_il, (uint64_t)c->vocab * QXD_HEAD_ROW), err, n, "head interleave");
+        if (ok) {
+            hipLaunchKernelGGL(qxk_interleave_head, dim3((c->vocab + 255) / 256), dim3(256), 0, c->s, c->head->p0, c->head->p1,
+                               c->head->p2, (const uint8_t *)c->head->d, c->vocab, c->head_il);
+            ok = hip_ok(hipGetLastError(), err, n, "head interleave");
+        }
     }
     return ok && hip_ok(hipStreamSynchronize(c->s), err, n, "expert interleave");
 }
@@ -870,7 +884,7 @@ void qxg_close(qxg_ctx *c) {
     void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->T.g2s, c->T.g3s, c->T.sel8, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
                     c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging,
-                    c->xch, c->abort, c->apart, c->route_ids, c->route_w, c->mfold, c->gu_il, c->dn_il};
+                    c->xch, c->abort, c->apart, c->route_ids, c->route_w, c->mfold, c->gu_il, c->dn_il, c->head_il};
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (void *p : c->arenas) (void)hipFree(p);
     for (void *p : c->pf.all) (void)hipFree(p);

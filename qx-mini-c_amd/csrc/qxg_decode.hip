@@ -63,6 +63,8 @@ constexpr int NT = 512;            // threads per workgroup
 constexpr int NWV = NT / 64;       // waves per workgroup
 constexpr int NWG = QXG_PBLOCKS;   // workgroups, one per CU
 constexpr uint32_t GU_BYTES = 4096, DN_BYTES = 3072;   // per-wave LDS for the routed experts' rows
+constexpr int HEAD_R = 4;                                // head rows per wave and pass
+constexpr int HEAD_NI = (HEAD_R * 105 + 63) / 64;        // 16-byte load instructions per pass
 #ifndef QXD_TLB_PAGE
 #define QXD_TLB_PAGE (2ull << 20)
 #endif
@@ -209,6 +211,7 @@ struct DLds {
             float bv[NWV];
             uint32_t bi[NWV];
             uint32_t am[XN_AM];
+            alignas(16) uint8_t rows[NWV][HEAD_NI * 1024];   // each wave's staged head rows
         } hd;
     } u;
 };
@@ -800,15 +803,17 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
 }
 
 // ---------------------------------------------------------------- head
-// Output RMSNorm + Q6_K head (src/qx_format.c:3554-3738) over the digits in S.dig: wave
-// gw takes rows R gw .. R gw + R - 1, then R (gw + 2048) .., R rows' loads in flight at a
-// time; returns the workgroup's best (logit desc, index asc) through bv/bi (uniform);
-// non-finite logits set *nonfin.
-template <int R>
+// Output RMSNorm + Q6_K head (src/qx_format.c:3554-3738) over the digits in S.dig: wave gw
+// takes rows R gw .. R gw + R - 1, then R (gw + 2048) ..  A pass's R interleaved rows
+// (R * 105 16-byte chunks, contiguous) come in with HEAD_NI full-width loads and go to the
+// wave's LDS region; the next pass's loads are issued before this pass's dots.  Lane (b, ib)
+// then reads its sub-block's ql, qh, scale pair and d from LDS.  Returns the workgroup's best
+// (logit desc, index asc) through bv/bi (uniform); non-finite logits set *nonfin.
 DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi, bool &nonfin) {
-    const int tid = tix(), lane = tid & 63, wave = tid >> 6;
+    constexpr int R = HEAD_R;
+    const int lane = tix() & 63, wave = wave_id();
     const int b = lane >> 3, ib = lane & 7, hh = ib >> 2, k = ib & 3;
-    const int gw = NWV * blockIdx.x + wave;
+    const uint32_t gw = NWV * blockIdx.x + wave;
     Dig g;
     load_dig(S.dig, lane, g);
     const Q6Bias bias = q6_bias(g);
@@ -816,34 +821,47 @@ DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi,
     uint32_t besti = 0xffffffffu;
     bool nf = false;
     const uint32_t groups = (a.vocab + R - 1) / R;
-    const GLB uint8_t *hql = gp(a.h_ql), *hqh = gp(a.h_qh), *hsc = gp((const uint8_t *)a.h_sc), *hd = gp((const uint8_t *)a.h_d);
+    const uint64_t hb = uni64((uint64_t)a.h_il);
     GLB float *lg = a.logits ? gpw(a.logits) : nullptr;
-    for (uint32_t p = gw; p < groups; p += NWV * NWG) {
-        uint4 l0[R], l1[R], h0[R], h1[R];
-        int s0[R], s1[R];
-        uint32_t d16[R];
+    uint8_t *rows = S.u.hd.rows[wave];
+    u32x4 v[HEAD_NI];
+    auto issue = [&](uint32_t p) {
 #pragma unroll
-        for (int rr = 0; rr < R; ++rr) {
-            const uint32_t r = min(R * p + rr, a.vocab - 1);
-            const uint32_t blk = r * 8 + b;
-            const uint32_t lo = blk * 128 + 64 * hh + 32 * (k & 1), ho = blk * 64 + 32 * hh;
-            l0[rr] = gnt4(hql, lo); l1[rr] = gnt4(hql, lo + 16); h0[rr] = gnt4(hqh, ho); h1[rr] = gnt4(hqh, ho + 16);
-            const uint32_t so = blk * 16 + 8 * hh + 2 * k;
-            s0[rr] = (int8_t)hsc[so]; s1[rr] = (int8_t)hsc[so + 1];
-            d16[rr] = ld_u16(hd, blk * 2);
+        for (int i = 0; i < HEAD_NI; ++i) {
+            const uint32_t c = 64 * i + lane, rr = c / 105u, cc = c - 105u * rr;
+            const uint32_t row = c < (uint32_t)R * 105u ? min(R * p + rr, a.vocab - 1) : min(R * p, a.vocab - 1);
+            const uint32_t ch = c < (uint32_t)R * 105u ? cc : 0u;
+            v[i] = __builtin_nontemporal_load((const GLB u32x4 *)(hb + (uint64_t)row * QXD_HEAD_ROW + 16 * ch));
         }
+    };
+    if (gw < groups) issue(gw);
+    for (uint32_t p = gw; p < groups; p += NWV * NWG) {
+#pragma unroll
+        for (int i = 0; i < HEAD_NI; ++i) *reinterpret_cast<u32x4 *>(rows + 1024 * i + 16 * lane) = v[i];
+        wave_lds_sync();
+        if (p + NWV * NWG < groups) issue(p + NWV * NWG);   // the next pass's rows, in flight during the dots
         float part[R], out[R];
 #pragma unroll
-        for (int rr = 0; rr < R; ++rr) part[rr] = dot_q6(l0[rr], l1[rr], h0[rr], h1[rr], s0[rr], s1[rr], d16[rr], ib, g, bias);
+        for (int rr = 0; rr < R; ++rr) {
+            const uint8_t *r = rows + rr * QXD_HEAD_ROW;
+            const uint32_t lo = b * 128 + 64 * hh + 32 * (k & 1), ho = 1024 + b * 64 + 32 * hh;
+            const uint4 l0 = *reinterpret_cast<const uint4 *>(r + lo), l1 = *reinterpret_cast<const uint4 *>(r + lo + 16);
+            const uint4 h0 = *reinterpret_cast<const uint4 *>(r + ho), h1 = *reinterpret_cast<const uint4 *>(r + ho + 16);
+            const uint32_t so = 1536 + b * 16 + 8 * hh + 2 * k;
+            const int s0 = (int8_t)r[so], s1 = (int8_t)r[so + 1];
+            const uint32_t d16 = *reinterpret_cast<const uint16_t *>(r + 1664 + 2 * b);
+            part[rr] = dot_q6(l0, l1, h0, h1, s0, s1, d16, ib, g, bias);
+        }
+        wave_lds_sync();   // the rows are rewritten by the next pass
         rows_reduce<R>(part, out, lane);
 #pragma unroll
         for (int rr = 0; rr < R; ++rr) {
             const uint32_t r = R * p + rr;
             if (r < a.vocab) {
-                const float v = out[rr];
-                if (!fin || !isfinite(v)) nf = true;
-                if (lg && lane == rr) lg[r] = v;
-                if (v > best) { best = v; besti = r; }   // rows ascend: ties keep the lower index
+                const float val = out[rr];
+                if (!fin || !isfinite(val)) nf = true;
+                if (lg && lane == rr) lg[r] = val;
+                if (val > best) { best = val; besti = r; }   // rows ascend: ties keep the lower index
             }
         }
     }
@@ -1257,12 +1275,8 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             uint32_t bi;
             bool nonfin;
             DMARK(48, 2);
-            head_rows<4>(a, S, fin, bv, bi, nonfin);
+            head_rows(a, S, fin, bv, bi, nonfin);
             DMARK(48, 3);
-            // layer 0's rows again (also on the last step): they are then dead during the head
-            // rows, whose loads take their registers
-            load_wq(a, 0, wq, S.wq[wave_id()]);
-            load_wo(a, 0, wo, S.wo[wave_id()]);
             if (nonfin) gpw(a.st)->nonfinite = 1u;
             // workgroup best, then every workgroup reads all the bests
             for (int o = 32; o > 0; o >>= 1) {
@@ -1272,6 +1286,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             }
             if (lane == 0) { S.u.hd.bv[wave] = bv; S.u.hd.bi[wave] = bi; }
             __syncthreads();
+            DMARK(48, 5);
             if (tid < 2) {
                 float v = S.u.hd.bv[0];
                 uint32_t i = S.u.hd.bi[0];
@@ -1282,6 +1297,10 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             if (!wait_xch2<1>(X + XO_AM + (step & 1) * XN_AM, XN_AM, eph + 1, S.u.hd.am, Ident(), S, ctl))
                 return;
             DMARK(48, 4);
+            // layer 0's rows again (also on the last step), after the argmax exchange: issued
+            // earlier, its poll would wait behind them (loads complete in order)
+            load_wq(a, 0, wq, S.wq[wave_id()]);
+            load_wo(a, 0, wo, S.wo[wave_id()]);
             float v = __uint_as_float(S.u.hd.am[0]);
             uint32_t i = S.u.hd.am[1];
             for (int w = 1; w < NWG; ++w) {
@@ -1325,6 +1344,22 @@ extern "C" __global__ __launch_bounds__(256) void qxk_interleave_experts(const u
         const uint16_t *d16 = reinterpret_cast<const uint16_t *>(dd + r * 6);
         for (int i = 0; i < 8; ++i) o16[i] = i < 3 ? d16[i] : (uint16_t)0;
     }
+}
+
+// The Q6_K head rows in the interleaved layout (QXD_HEAD_ROW): one thread per row, from the
+// ql (128), qh (64), sc (16) and d (2) planes of its 8 blocks.
+extern "C" __global__ __launch_bounds__(256) void qxk_interleave_head(const uint8_t *ql, const uint8_t *qh, const uint8_t *sc,
+                                                                       const uint8_t *d, uint32_t vocab, uint8_t *out) {
+    const uint64_t r = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r >= vocab) return;
+    auto cp32 = [](uint8_t *dst, const uint8_t *src, int words) {
+        for (int i = 0; i < words; ++i) reinterpret_cast<uint32_t *>(dst)[i] = reinterpret_cast<const uint32_t *>(src)[i];
+    };
+    uint8_t *o = out + r * QXD_HEAD_ROW;
+    cp32(o, ql + r * 1024, 256);
+    cp32(o + 1024, qh + r * 512, 128);
+    cp32(o + 1536, sc + r * 128, 32);
+    cp32(o + 1664, d + r * 16, 4);
 }
 
 // Router fold of one layer (see the top of this file): M[e][j] = sum_i W[e][i] w[i] O[i][j]

@@ -124,6 +124,7 @@ struct QxDArgs {
     uint64_t emb_row;
     const float *out_norm;
     const uint8_t *h_ql, *h_qh;  // Q6_K head planes
+    const uint8_t *h_il;         // the head rows interleaved, QXD_HEAD_ROW bytes per row
     const int8_t *h_sc;
     const uint16_t *h_d;
     uint32_t vocab, layers, experts, ctx;
@@ -151,6 +152,9 @@ struct QxDArgs {
 // in one contiguous range, so each of its 16-byte load instructions touches one or two
 // pages (the cost of a scattered load instruction grows with the pages it touches).
 #define QXD_GU_UNIT 1184u
+// Q6_K head row r of the persistent decode: [ql 1024 | qh 512 | sc 128 | d 16] at r * 1680
+// (the 8 blocks' planes of the row back to back; 105 16-byte chunks).
+#define QXD_HEAD_ROW 1680u
 #define QXD_DN_ROW 304u
 // exchange words per launch: x, qkv, ctx, x', router logits, h, expert weights (two slots
 // each) and the per-workgroup argmax candidates
