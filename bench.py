@@ -34,8 +34,10 @@ KERNEL_BYTES = {
     "qkv": (4096 + 512 + 512) * 8 * 136 + 2048 * 4 * 2 + 5120 * 4,
     "oproj": 2048 * 16 * 136 + 4096 * 4 + 2048 * 4 * 2,
     "head": HEAD_BYTES + 2048 * 4 * 2 + VOCAB * 4,
-    # the persistent layer kernel: all 48 layers of one token (KV reads added per position)
-    "layers": LAYERS * LAYER_BYTES + 2048 * 4 * 2,
+    # the persistent decode kernel: one launch runs every step of a generate call (all 48
+    # layers and the head per token); per-launch bytes are formed in main() from the steps
+    # and the KV rows read
+    "layers": TOKEN_BYTES,
 }
 
 
@@ -48,24 +50,49 @@ def kv_bytes(p0, n):
     return sum(LAYERS * (p + 1) * 1032 for p in range(p0, p0 + n))
 
 
-def cpu_baseline(model_path, tokens, budget_s):
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(model_path, prompt_kv, first_token, p0, budget_s):
+    """The oracle (oracle/qxo.c, scalar, one thread) decoding the GPU's first timed positions:
+    its KV cache holds the prompt's rows as the GPU wrote them (positions 0..p0-1), and it
+    decodes from the GPU's first generated token at positions p0, p0 + 1, ... within budget_s.
+    Also times one FNV-1a 64 pass over the Q6_K head tensor: the reference verifies that
+    checksum on every final-head call (src/qx_format.c:3631-3632), which neither the oracle nor
+    the GPU path repeats per token; the "with_head_fnv" rate adds it to each token."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import qxo
     m = qxo.Model(model_path)
-    kv = qxo.KV(LAYERS, 16)
+    kv = qxo.KV(LAYERS, p0 + 8)
+    for l, (k, v, ks, vs) in enumerate(prompt_kv):
+        kv.k[l, :p0], kv.v[l, :p0], kv.ks[l, :p0], kv.vs[l, :p0] = k, v, ks, vs
     done, t0, c0 = 0, time.perf_counter(), time.process_time()
-    tok = tokens[0]
+    tok = first_token
     while done < 2:
-        _, _, _, ids, _ = qxo.decode_token(m, tok, done, kv, LAYERS, True, VOCAB, 1)
+        _, _, _, ids, _ = qxo.decode_token(m, tok, p0 + done, kv, LAYERS, True, VOCAB, 1)
         tok = int(ids[0])
         done += 1
         if time.perf_counter() - t0 > budget_s:
             break
     wall, cpu = time.perf_counter() - t0, time.process_time() - c0
+    _, _, head = m.tensor("output.weight")
+    t1 = time.perf_counter()
+    qxo.fnv1a64(head)
+    fnv_s = time.perf_counter() - t1
     m.close()
-    return {"value": done / wall, "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"{done} greedy decode tokens at positions 0..{done - 1} of the same model (oracle/qxo.c, "
-                      f"scalar, 1 thread); wall {wall:.2f} s, process CPU {cpu:.2f} s"}
+    return {"value": done / wall, "unit": "tok/s", "cores": 1, "kind": "port", "cpu": cpu_model(),
+            "with_head_fnv": round(done / (wall + done * fnv_s), 5), "head_fnv_s": round(fnv_s, 4),
+            "sample": f"{done} greedy decode tokens at positions {p0}..{p0 + done - 1} of the same model, the GPU's "
+                      f"first timed positions (prompt KV rows taken from the GPU; oracle/qxo.c, scalar, 1 thread); "
+                      f"wall {wall:.2f} s, process CPU {cpu:.2f} s"}
 
 
 def measured_traffic(kernel):
@@ -154,8 +181,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--roofline-kernel", default=None, choices=sorted(KERNEL_BYTES),
                     help="kernel timed in situ for the roofline (default: layers on the persistent path, else gate_up)")
-    ap.add_argument("--layer-path", type=int, default=0, choices=[0, 1],
-                    help="0: one kernel per phase; 1: the persistent layer kernel")
+    ap.add_argument("--layer-path", type=int, default=1, choices=[0, 1],
+                    help="0: one kernel per phase; 1: the persistent decode kernel (default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=25.0)
     ap.add_argument("--seed", type=int, default=1)
@@ -230,8 +257,8 @@ def main():
     tok_s = args.steps / wall2
     avg_kernel_s = kern_ms / 1e3 / max(launches, 1)
     kb = KERNEL_BYTES[args.roofline_kernel]
-    if args.roofline_kernel == "layers":   # plus the INT8 KV rows the attention reads at positions 8..8+K-1
-        kb += kv_bytes(prompt_len, args.steps) // args.steps
+    if args.roofline_kernel == "layers":   # every step of the call, plus the INT8 KV rows read at positions 8..8+K-1
+        kb = TOKEN_BYTES * args.steps + kv_bytes(prompt_len, args.steps)
     achieved = kb / avg_kernel_s / 1e9
     token_bytes = TOKEN_BYTES + kv_bytes(prompt_len, args.steps) / args.steps
     out = {
@@ -263,12 +290,16 @@ def main():
                            "device_ms_per_token": round(dev_ms2 / args.steps, 4)},
         "first_tokens": [int(t) for t in toks[:8]],
     }
+    prompt_kv = None
+    if not args.no_cpu_baseline:   # the prompt's KV rows as the GPU writes them, for the CPU baseline
+        first = prefill()
+        prompt_kv = [ctx.kv_read(l, 0, prompt_len) for l in range(LAYERS)]
     if args.prefill_tokens:
         out["prefill"] = prefill_leg(ctx, args)
     ctx.close()
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, 1 thread) ...")
-        out["cpu_baseline"] = cpu_baseline(model.path, [int(prompt[0])], args.cpu_budget)
+        out["cpu_baseline"] = cpu_baseline(model.path, prompt_kv, first, prompt_len, args.cpu_budget)
     else:
         out["cpu_baseline"] = None
     model.close()
