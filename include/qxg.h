@@ -116,6 +116,12 @@ int qxg_embed_token(qxg_ctx *ctx, uint32_t token, float *x_out, char *err, uint6
 int qxg_dequant_blocks(qxg_ctx *ctx, uint32_t ggml_type, const void *raw, uint64_t nblocks, float *out,
                        char *err, uint64_t err_len);
 
+/* INT8 KV quantization of one row of n <= 4096 f32 values on the device, with the same
+ * device functions every kernel that appends a KV row uses: scale = max|x| / 127 over the
+ * finite values (1 if zero), codes = lrintf(x / scale) clamped to +-127, non-finite -> 0.
+ * Replaces qx_quantize_int8_vector (src/qx_format.c:4449-4463) as a same-input seam. */
+int qxg_int8_quantize(qxg_ctx *ctx, const float *x, uint32_t n, int8_t *codes, float *scale, char *err, uint64_t err_len);
+
 /* No counterpart in the reference: for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * qxg_dequant_blocks with the raw blocks and the f32 output in device memory the caller

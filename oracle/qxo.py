@@ -39,6 +39,7 @@ _sig("qxo_set_activation", [vp, c_int], None)
 _sig("qxo_f32_to_fp16", [ctypes.c_float], ctypes.c_uint16)
 _sig("qxo_attention_stage", [vp, u32, vp, c_int, vp, vp, vp, vp, vp, vp])
 _sig("qxo_moe_stage", [vp, u32, vp, vp, vp])
+_sig("qxo_quantize_int8", [vp, vp, u32], ctypes.c_float)
 
 Q8K_BYTES = 292   # ggml block_q8_K: f32 d, int8 qs[256], int16 bsums[16]
 
@@ -62,6 +63,14 @@ def decode_block(ggml_type, raw):
     if not _o.qxo_decode_block(ggml_type, _p(raw), _p(out)):
         raise ValueError("unsupported type")
     return out
+
+
+def quantize_int8(x):
+    """reference qx_quantize_int8_vector (src/qx_format.c:4449-4463): (codes, scale)"""
+    x = np.ascontiguousarray(x, np.float32)
+    codes = np.zeros(len(x), np.int8)
+    sc = _o.qxo_quantize_int8(_p(x), _p(codes), len(x))
+    return codes, np.float32(sc)
 
 
 def f32_to_fp16(v):

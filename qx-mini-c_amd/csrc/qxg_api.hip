@@ -32,6 +32,7 @@ __global__ void qxk_interleave_experts(const uint8_t *, const uint8_t *, const u
                                        const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, uint32_t, uint8_t *,
                                        uint8_t *);
 __global__ void qxk_router_fold(const float *, const float *, const float *, uint32_t, float *);
+__global__ void qxk_int8_row(const float *, uint32_t, int8_t *, float *);
 __global__ void qxk_interleave_head(const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, uint32_t, uint8_t *);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
                             uint64_t, float *);
@@ -1210,6 +1211,25 @@ int qxg_dequant_blocks(qxg_ctx *c, uint32_t type, const void *raw, uint64_t nblo
     }
     if (d) (void)hipFree(d);
     free_tensor(t);
+    return ok;
+}
+
+int qxg_int8_quantize(qxg_ctx *c, const float *x, uint32_t n, int8_t *codes, float *scale, char *err, uint64_t err_len) {
+    if (!c || !x || !codes || !scale || !n || n > 4096) { set_err(err, err_len, "invalid argument"); return 0; }
+    (void)hipSetDevice(c->device);
+    float *dx = nullptr;
+    int ok = hip_ok(hipMalloc(&dx, n * 4 + 4 + n), err, err_len, "hipMalloc");
+    if (ok) {
+        float *dsc = dx + n;
+        int8_t *dc = (int8_t *)(dx + n + 1);
+        ok = hip_ok(hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, c->s), err, err_len, "copy");
+        if (ok) {
+            hipLaunchKernelGGL(qxk_int8_row, dim3(1), dim3(256), 0, c->s, dx, n, dc, dsc);
+            ok = finish(c, err, err_len) && hip_ok(hipMemcpy(codes, dc, n, hipMemcpyDeviceToHost), err, err_len, "read") &&
+                 hip_ok(hipMemcpy(scale, dsc, 4, hipMemcpyDeviceToHost), err, err_len, "read");
+        }
+    }
+    if (dx) (void)hipFree(dx);
     return ok;
 }
 

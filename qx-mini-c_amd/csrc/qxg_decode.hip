@@ -610,10 +610,6 @@ DEV float wave_max_f(float v) {
     v = fmaxf(v, dppf<DPP_ROR4>(v)); v = fmaxf(v, dppf<DPP_ROR8>(v));
     return fmaxf(fmaxf(rdlanef(v, 0), rdlanef(v, 16)), fmaxf(rdlanef(v, 32), rdlanef(v, 48)));
 }
-DEV int8_t int8_code(float x, float scale) {   // reference :4449-4463: rint(x / scale) clamped, non-finite -> 0
-    const int q = isfinite(x) ? (int)rintf(x / scale) : 0;
-    return (int8_t)(q < -127 ? -127 : q > 127 ? 127 : q);
-}
 
 // ep: the QKV phase (the context goes out at ep + 1)
 DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, const AttnPre &pre, DLds &S, bool last) {
@@ -632,14 +628,14 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
         head_norm_rope_wave(k0, k1, pre.nk0, pre.nk1, pre.cs, pre.sn);
         A.k[128 * w + lane] = k0;
         A.k[128 * w + 64 + lane] = k1;
-        const float mx = wave_max_f(fmaxf(isfinite(k0) ? fabsf(k0) : 0.0f, isfinite(k1) ? fabsf(k1) : 0.0f));
+        const float mx = wave_max_f(fmaxf(int8_mag(k0), int8_mag(k1)));
         if (lane == 0) A.kmx[w] = mx;
     } else if (w > 4) {   // v heads 0, 1 (wave 5), 2 (wave 6), 3 (wave 7)
         const int j0 = w == 5 ? 0 : w - 4, j1 = w == 5 ? 1 : w - 4;
         const float v0 = A.v[128 * j0 + lane], v1 = A.v[128 * j0 + 64 + lane];
         const float v2 = A.v[128 * j1 + lane], v3 = A.v[128 * j1 + 64 + lane];
-        const float m0 = wave_max_f(fmaxf(isfinite(v0) ? fabsf(v0) : 0.0f, isfinite(v1) ? fabsf(v1) : 0.0f));
-        const float m1 = wave_max_f(fmaxf(isfinite(v2) ? fabsf(v2) : 0.0f, isfinite(v3) ? fabsf(v3) : 0.0f));
+        const float m0 = wave_max_f(fmaxf(int8_mag(v0), int8_mag(v1)));
+        const float m1 = wave_max_f(fmaxf(int8_mag(v2), int8_mag(v3)));
         if (lane == 0) { A.vmx[j0] = m0; A.vmx[j1] = m1; }
     } else {   // wave 4
         {
@@ -677,7 +673,7 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
     DMARK(l, 21);
     const float kmx = fmaxf(fmaxf(A.kmx[0], A.kmx[1]), fmaxf(A.kmx[2], A.kmx[3]));
     const float vmx = fmaxf(fmaxf(A.vmx[0], A.vmx[1]), fmaxf(A.vmx[2], A.vmx[3]));
-    const float kscale = kmx > 0.0f ? kmx / 127.0f : 1.0f, vscale = vmx > 0.0f ? vmx / 127.0f : 1.0f;
+    const float kscale = int8_scale(kmx), vscale = int8_scale(vmx);
     const bool qok = A.qok != 0u;
     // the codes of the workgroup's kv head for the position, by the wave whose block holds it
     const int wpos = (int)((pos & 127u) >> 4);
@@ -1344,6 +1340,20 @@ extern "C" __global__ __launch_bounds__(256) void qxk_interleave_experts(const u
         const uint16_t *d16 = reinterpret_cast<const uint16_t *>(dd + r * 6);
         for (int i = 0; i < 8; ++i) o16[i] = i < 3 ? d16[i] : (uint16_t)0;
     }
+}
+
+// A given row through the KV quantizer (int8_mag, int8_scale, int8_code): one workgroup of 256
+// threads, n <= 4096 values (the same-input seam of qxg_int8_quantize).
+extern "C" __global__ __launch_bounds__(256) void qxk_int8_row(const float *x, uint32_t n, int8_t *codes, float *scale) {
+    __shared__ float red[4];
+    float mx = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, int8_mag(x[i]));
+    mx = wave_max_f(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    const float sc = int8_scale(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    for (uint32_t i = threadIdx.x; i < n; i += 256) codes[i] = int8_code(x[i], sc);
+    if (threadIdx.x == 0) *scale = sc;
 }
 
 // The Q6_K head rows in the interleaved layout (QXD_HEAD_ROW): one thread per row, from the

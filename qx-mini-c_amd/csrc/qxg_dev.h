@@ -624,6 +624,18 @@ DEV void block_max2_256(float &a, float &b, float2 *red) {
     b = fmaxf(fmaxf(r0.y, r1.y), fmaxf(r2.y, r3.y));
 }
 
+// INT8 KV quantization of one row (reference qx_quantize_int8_vector, src/qx_format.c:4449-4463):
+// scale = max |x| / 127 over the finite values (1 if that is 0), code = lrintf(x / scale) with
+// the f32 division correctly rounded (the build flag) and round-half-even, clamped to +-127,
+// non-finite -> 0.  Every kernel that appends a KV row quantizes with these two functions (the
+// maximum itself is exact in any order); qxg_int8_quantize runs them on a given row.
+DEV float int8_mag(float x) { return isfinite(x) ? fabsf(x) : 0.0f; }
+DEV float int8_scale(float max_abs) { return max_abs > 0.0f ? max_abs / 127.0f : 1.0f; }
+DEV int8_t int8_code(float x, float scale) {
+    const int q = isfinite(x) ? (int)rintf(x / scale) : 0;
+    return (int8_t)(q < -127 ? -127 : q > 127 ? 127 : q);
+}
+
 // 128 values of one head held as (lane, lane+64) by a wave: per-head RMSNorm then RoPE
 DEV void head_norm_rope_wave(float &x0, float &x1, float w0, float w1, double c, double s) {
     const double ss = wave_total_d((double)x0 * (double)x0 + (double)x1 * (double)x1);

@@ -209,27 +209,18 @@ extern "C" __global__ __launch_bounds__(256) void qxk_attn(const float *qkv, con
     }
     if (tid < ATT_STAGE) { s_kss[tid] = kss; s_vss[tid] = vss; }
     // INT8 quantize K and V over all 512 values (scale = max|x|/127, 1 if zero)
-    float ka = 0.0f, va = 0.0f;
-    {
-        const float a0 = isfinite(k0) ? fabsf(k0) : 0.0f, a1 = isfinite(k1) ? fabsf(k1) : 0.0f;
-        ka = fmaxf(a0, a1);
-        const float b0 = isfinite(v0) ? fabsf(v0) : 0.0f, b1 = isfinite(v1) ? fabsf(v1) : 0.0f;
-        va = fmaxf(b0, b1);
-    }
+    float ka = fmaxf(int8_mag(k0), int8_mag(k1)), va = fmaxf(int8_mag(v0), int8_mag(v1));
     QXG_MARK(4, 2);
     block_max2_256(ka, va, red2);
     QXG_MARK(4, 3);
-    const float kscale = ka > 0.0f ? ka / 127.0f : 1.0f, vscale = va > 0.0f ? va / 127.0f : 1.0f;
+    const float kscale = int8_scale(ka), vscale = int8_scale(va);
     // values 2 tid and 2 tid + 1 (a 2-byte store each for K and V)
     int8_t qkb[2], qvb[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int i = 2 * tid + j;
-        const float kx = s_k[i], vx = s_v[i];
-        int qk = isfinite(kx) ? (int)rintf(kx / kscale) : 0;
-        int qv = isfinite(vx) ? (int)rintf(vx / vscale) : 0;
-        qkb[j] = (int8_t)(qk < -127 ? -127 : qk > 127 ? 127 : qk);
-        qvb[j] = (int8_t)(qv < -127 ? -127 : qv > 127 ? 127 : qv);
+        qkb[j] = int8_code(s_k[i], kscale);
+        qvb[j] = int8_code(s_v[i], vscale);
     }
     if ((tid >> 6) == kvh) {   // this kv head's 128 values: threads 64 kvh .. 64 kvh + 63
         reinterpret_cast<uint16_t *>(s_k8)[tid & 63] = (uint16_t)((uint8_t)qkb[0] | ((uint32_t)(uint8_t)qkb[1] << 8));

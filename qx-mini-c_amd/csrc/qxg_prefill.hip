@@ -491,25 +491,14 @@ extern "C" __global__ __launch_bounds__(256) void qxp_qk(const float *qkv, const
         qr[(uint64_t)t * 4096 + 128 * qh + lane] = q0;
         qr[(uint64_t)t * 4096 + 128 * qh + 64 + lane] = q1;
     }
-    float ka, va;
-    {
-        const float a0 = isfinite(k0) ? fabsf(k0) : 0.0f, a1 = isfinite(k1) ? fabsf(k1) : 0.0f;
-        ka = fmaxf(a0, a1);
-        const float b0 = isfinite(v0) ? fabsf(v0) : 0.0f, b1 = isfinite(v1) ? fabsf(v1) : 0.0f;
-        va = fmaxf(b0, b1);
-    }
+    float ka = fmaxf(int8_mag(k0), int8_mag(k1)), va = fmaxf(int8_mag(v0), int8_mag(v1));
     ka = block_max256(ka, red);
     va = block_max256(va, red);
-    const float kscale = ka > 0.0f ? ka / 127.0f : 1.0f, vscale = va > 0.0f ? va / 127.0f : 1.0f;
+    const float kscale = int8_scale(ka), vscale = int8_scale(va);
     const uint64_t slot = (uint64_t)layer * ctx + pos;
     for (int i = tid; i < 512; i += 256) {
-        const float kx = s_k[i], vx = s_v[i];
-        int qk = isfinite(kx) ? (int)rintf(kx / kscale) : 0;
-        int qv = isfinite(vx) ? (int)rintf(vx / vscale) : 0;
-        qk = qk < -127 ? -127 : qk > 127 ? 127 : qk;
-        qv = qv < -127 ? -127 : qv > 127 ? 127 : qv;
-        kc[slot * 512 + i] = (int8_t)qk;
-        vc[slot * 512 + i] = (int8_t)qv;
+        kc[slot * 512 + i] = int8_code(s_k[i], kscale);
+        vc[slot * 512 + i] = int8_code(s_v[i], vscale);
     }
     if (tid == 0) { ks[slot] = kscale; vs[slot] = vscale; }
 }

@@ -74,6 +74,7 @@ _sig(_g, "qxg_generate", [vp, vp, u32, u32, u32, vp, ctypes.POINTER(c_float), *E
 _sig(_g, "qxg_embed_token", [vp, u32, vp, *ERR])
 _sig(_g, "qxg_dequant_blocks", [vp, u32, vp, u64, vp, *ERR])
 _sig(_g, "qxg_dequant_blocks_static", [vp, u32, vp, u64, vp, *ERR])
+_sig(_g, "qxg_int8_quantize", [vp, vp, u32, vp, vp, *ERR])
 _sig(_g, "qxg_attention_layer", [vp, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_moe_layer", [vp, u32, vp, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_attention_layer_ex", [vp, u32, u32, vp, vp, vp, vp, vp, *ERR])
@@ -227,6 +228,14 @@ class Context:
         out = np.zeros(nblocks * 256, np.float32)
         self._check(_g.qxg_dequant_blocks(self._c, ggml_type, _p(raw), nblocks, _p(out), self._err, 1024))
         return out
+
+    def int8_quantize(self, x):
+        """The device KV quantizer on one row: (int8 codes, f32 scale)."""
+        x = np.ascontiguousarray(x, np.float32)
+        codes = np.zeros(len(x), np.int8)
+        sc = np.zeros(1, np.float32)
+        self._check(_g.qxg_int8_quantize(self._c, _p(x), len(x), _p(codes), _p(sc), self._err, 1024))
+        return codes, sc[0]
 
     def dequant_static(self, ggml_type, raw_dev, nblocks, out_dev):
         """qxg_dequant_blocks_static on device addresses (ints) the caller owns."""

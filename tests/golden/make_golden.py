@@ -162,6 +162,19 @@ def main():
                         dumps[f"{s}/{layer}/{ph}"] = str(fnv_file(os.path.join(dd, f"step-{s}-layer-{layer}-{ph}.f32")))
             out["state_loop"][k] = {"input_tokens": toks, "steps": steps, "ctx": 8, "dumps": dumps,
                                     "selected_experts": experts}
+        # a long state loop: 64 greedy steps at ctx 64 on model A, so the reference pins the
+        # attention softmax over many positions (every step's per-layer dumps)
+        dd = os.path.join(d, "slong")
+        os.mkdir(dd)
+        txt = run(["state-loop-probe", "--in", paths["A"], "--prompt-token", "17", "--steps", "64", "--layers", "1",
+                   "--ctx", "64", "--kv", "int8", "--full-moe", "--dump-residuals", dd])
+        out["state_loop_long"] = {
+            "model": "A", "steps": 64, "ctx": 64,
+            "input_tokens": [int(t) for t in re.findall(r'"input_token": (\d+)', txt)],
+            "selected_experts": [[int(e) for e in re.findall(r"\d+", m)]
+                                 for m in re.findall(r'"selected_experts": \[([0-9, ]*)\]', txt)],
+            "dumps": {f"{s_}/0/{ph}": str(fnv_file(os.path.join(dd, f"step-{s_}-layer-0-{ph}.f32")))
+                      for s_ in range(64) for ph in PHASES}}
         # attention and MoE stage probes (src/qx_format.c:5478-5725) on seeded inputs
         out["attention_stage"], out["moe_stage"] = {}, {}
         for k, layer in STAGE_CASES:

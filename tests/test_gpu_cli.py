@@ -57,3 +57,35 @@ def test_state_loop_probe_dumps(tmp_path, act, tol):
                 assert rel_l2(dump(s, 1, "input"), dump(s, 0, "output")) == 0.0
     m.close()
     print(act, {k: f"{v:.2e}" for k, v in worst.items()})
+
+
+def test_long_state_loop_probe_vs_reference(tmp_path):
+    """The reference's 64-step loop at ctx 64 (golden state_loop_long, model A) through this
+    CLI: the same input tokens and routed experts as the reference, and every step's
+    attention and MoE replayed by the oracle on the CLI's own dumped inputs (1e-5)."""
+    GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "golden.json")))
+    g = GOLDEN["state_loop_long"]
+    model = tmp_path / "a.qxf"
+    qxg.generate_model(model, **GOLDEN["models"][g["model"]])
+    dd = tmp_path / "dumps"
+    dd.mkdir()
+    r = subprocess.run([EXE, "state-loop-probe", "--in", str(model), "--prompt-token", "17", "--steps", str(g["steps"]),
+                        "--layers", "1", "--ctx", str(g["ctx"]), "--kv", "int8", "--full-moe", "--dump-residuals", str(dd)],
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr
+    j = json.loads(r.stdout)
+    assert [t["input_token"] for t in j["tokens"]] == g["input_tokens"]
+    assert [t["layers"][0]["selected_experts"] for t in j["tokens"]] == g["selected_experts"]
+    m = qxo.Model(model)
+    kv = qxo.KV(1, g["ctx"])
+    dump = lambda s, ph: np.fromfile(dd / f"step-{s}-layer-0-{ph}.f32", np.float32)
+    worst = 0.0
+    for s in range(g["steps"]):
+        a, kqv, vcur = qxo.attention_layer(m, 0, s, kv, dump(s, "input"))
+        y, moe, _, _ = m.moe_layer(0, dump(s, "ffn-inp"))
+        for got, ref in ((dump(s, "kqv-out"), kqv), (dump(s, "ffn-inp"), dump(s, "input") + a), (dump(s, "output"), y)):
+            e = rel_l2(got, ref)
+            worst = max(worst, e)
+            assert e <= REL_L2, (s, e)
+    m.close()
+    print(f"64-step loop: worst same-input rel L2 {worst:.2e}")

@@ -244,3 +244,31 @@ def test_decode_two_layers_greedy(dctx, tmp_path):
     dctx.profile_kernel(-1)
     # one persistent launch for all steps, or one gate/up launch per layer and step
     assert list(gen3) == toks and n == (1 if dctx.layer_path else 5 * 2)
+
+
+@pytest.mark.parametrize("p0", [126, 381, 1000])
+def test_decode_long_context_vs_oracle(dctx, tmp_path, p0):
+    """Greedy steps at positions p0.. over a seeded INT8 cache of p0 positions (both sides
+    hold the same rows): the attention's 128-position blocks, their online-softmax merge
+    and the split boundaries, against the oracle's single-pass softmax; per-layer outputs
+    and logits at the multi-step bar (1e-4), tokens under the margin rule."""
+    p = tmp_path / "long.qxf"
+    qxg.generate_model(p, layers=2, vocab=4096, experts=32, seed=46)
+    dctx.load(p)
+    dctx.kv_create(2, p0 + 8)
+    om = qxo.Model(p)
+    okv = qxo.KV(2, p0 + 8)
+    for layer in range(2):
+        k, v, ks, vs = seeded_kv(300 + layer, p0)
+        dctx.kv_write(layer, 0, k, v, ks, vs)
+        okv.k[layer, :p0], okv.v[layer, :p0], okv.ks[layer, :p0], okv.vs[layer, :p0] = k, v, ks, vs
+    tok_g = tok_o = 23
+    for s in range(p0, p0 + 3):
+        res, lay, lg, ids, tl = dctx.decode_token(tok_g, s, True, 4, want_layers=True, want_logits=True)
+        ores, olay, olg, oids, otl = qxo.decode_token(om, tok_o, s, okv, 2, True, 4096, 4)
+        assert rel_l2(lay, olay) <= 1e-4, (s, rel_l2(lay, olay))
+        assert rel_l2(lg, olg) <= 1e-4, (s, rel_l2(lg, olg))
+        ok, why = topk_consistent(ids, oids, olg)
+        assert ok, why
+        tok_g, tok_o = int(ids[0]), int(oids[0])
+    om.close()

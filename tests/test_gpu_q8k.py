@@ -8,7 +8,9 @@ that re-quantize a device-computed intermediate (O projection of the attention
 context, down projection of h) may see a code one step apart where the two inputs
 straddle a rounding boundary: about 1e-5 of the values, each worth ~5e-4 of the
 output's norm, so those are held to REQ_TOL = 2e-3 (a wrong block scale, sign or
-rounding rule costs 1e-2 or more)."""
+rounding rule costs 1e-2 or more).  Those two projections are also replayed on the same
+input - the oracle's Q8_K O projection of the device's own context, its down projection of
+the device's own h per rank - and held to 1e-5."""
 import ctypes
 import json
 import os
@@ -105,15 +107,21 @@ def test_q8k_attention_layer(ctx, models, which, layer):
         om = qxo.Model(models[which], activation="q8_k_compat")
         oa, okqv, ovcur = qxo.attention_layer(om, layer, pos, okv, x)
         om.close()
+        om_o = qxo.Model(models[which], activation="q8_k_compat")
         assert rel_l2(vcur, ovcur) <= REL_L2, rel_l2(vcur, ovcur)
         assert rel_l2(kqv, okqv) <= REL_L2, rel_l2(kqv, okqv)
         assert rel_l2(a, oa) <= REQ_TOL, rel_l2(a, oa)
+        # same input: the oracle's Q8_K O projection of the device's own context
+        t, _, wo = om_o.tensor(f"blk.{layer}.attn_output.weight")
+        so = qxo.matvec_q8k(t, wo, 2048, 4096, kqv)
+        assert so is not None and rel_l2(a, so) <= REL_L2, rel_l2(a, so)
         # f32 and q8_k_compat really differ (the mode switch is live)
         ctx.set_activation("f32")
         ctx.kv_create(layers, 128)
         ctx.kv_write(layer, 0, k, v, ks, vs)
         a32, _, _ = ctx.attention_layer(layer, pos, x)
         assert rel_l2(a32, oa) > 10 * rel_l2(a, oa)
+        om_o.close()
     finally:
         ctx.set_activation("f32")
 
@@ -132,6 +140,16 @@ def test_q8k_moe_layer(ctx, models, which, layer):
             assert np.allclose(w, ow, rtol=1e-9, atol=0)
             assert rel_l2(moe, omoe) <= REQ_TOL, rel_l2(moe, omoe)
             assert rel_l2(y, oy) <= REQ_TOL
+            # same input: the oracle's Q8_K down projection of the device's own h, per rank
+            st, sids = ctx.moe_stage(layer, x)
+            t, _, wd = om.tensor(f"blk.{layer}.ffn_down_exps.weight")
+            per_expert = len(wd) // ctx.info.experts
+            for r in range(8):
+                e = int(sids[r])
+                h = st["ffn_moe_swiglu"][768 * r:768 * (r + 1)]
+                sd = qxo.matvec_q8k(t, wd[e * per_expert:(e + 1) * per_expert], 2048, 768, h, expert=True)
+                gd = st["ffn_moe_down"][2048 * r:2048 * (r + 1)]
+                assert sd is not None and rel_l2(gd, sd) <= REL_L2, (r, rel_l2(gd, sd))
         om.close()
     finally:
         ctx.set_activation("f32")

@@ -50,6 +50,9 @@ def test_final_head_matches_reference(models):
         assert str(qxo.fnv1a64(lg)) == want["logits_checksum"]
         assert int(ids[0]) == want["argmax_token"]
         assert float(tl[0]) == pytest.approx(want["argmax_logit"], rel=0, abs=0)
+        # ranks 2..8 too: the reference's logits ordered by (value desc, index asc)
+        assert [int(i) for i in ids] == want["top8_by_float"], key
+        assert [float(v) for v in lg[:4]] == want["logits_sample"], key
 
 
 @pytest.mark.parametrize("k", ["A", "B", "C"])
@@ -74,6 +77,26 @@ def test_state_loop_layer_dumps_match_reference(models, k):
             x = y
             for ph in PHASES:
                 assert str(qxo.fnv1a64(got[ph])) == g["dumps"][f"{s}/{layer}/{ph}"], (s, layer, ph)
+
+
+def test_long_state_loop_matches_reference(models):
+    """64 greedy steps at ctx 64 (softmax over up to 64 cached INT8 positions): every
+    step's dumps bit-identical to the reference's, the same tokens and routed experts."""
+    g = GOLDEN["state_loop_long"]
+    m = models[g["model"]]
+    kv = qxo.KV(1, g["ctx"])
+    for s, tok in enumerate(g["input_tokens"]):
+        x = m.embed(tok)
+        got = {"input": x.copy()}
+        a, kqv, vcur = qxo.attention_layer(m, 0, s, kv, x)
+        got["v-cur"], got["kqv-out"] = vcur, kqv
+        x = x + a
+        got["ffn-inp"] = x.copy()
+        y, moe, ids, w = m.moe_layer(0, x)
+        got["ffn-moe-out"], got["output"] = moe, y
+        assert [int(i) for i in ids] == g["selected_experts"][s], s
+        for ph in PHASES:
+            assert str(qxo.fnv1a64(got[ph])) == g["dumps"][f"{s}/0/{ph}"], (s, ph)
 
 
 def _q8_probe_input(inject, values):

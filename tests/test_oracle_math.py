@@ -148,3 +148,12 @@ def test_int8_quantize_properties():
     assert np.array_equal(q[fin], np.clip(np.rint(x[fin] / np.float32(s)), -127, 127).astype(np.int8))
     z = np.zeros(512, np.float32)
     assert qxo._o.qxo_quantize_int8(z.ctypes.data_as(qxo.vp), q.ctypes.data_as(qxo.vp), 512) == 1.0
+
+
+def test_int8_quantize_ties_round_half_even():
+    """numpy's rint is round-half-even, like lrintf in the default mode: with max 127 the
+    scale is exactly 1 and the codes of k + 0.5 are the even neighbours."""
+    x = np.float32([127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5])
+    codes, scale = qxo.quantize_int8(x)
+    assert scale == np.float32(1.0)
+    assert list(codes) == [127, 0, 2, 2, 0, -2, -2, 126, -126]
