@@ -99,14 +99,15 @@ def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a plain
     device copy of known size); None when no summary is committed for it."""
-    path = os.path.join(ROOT, "profiles", "decode_config4_traffic.md")
-    if not os.path.exists(path):
-        return None
     key = f"traffic_bytes_per_launch[{kernel}]="
-    with open(path) as f:
-        for line in f:
-            if line.startswith(key):
-                return int(line[len(key):])
+    for name in ("decode_config4_persistent_traffic.md", "decode_config4_per_phase_traffic.md"):
+        path = os.path.join(ROOT, "profiles", name)
+        if not os.path.exists(path):
+            continue
+        with open(path) as f:
+            for line in f:
+                if line.startswith(key):
+                    return int(line[len(key):])
     return None
 
 
