@@ -209,11 +209,13 @@ int qxg_prefill_layer(qxg_ctx *ctx, uint32_t layer, uint32_t n, uint32_t positio
                       float *ffn_inp_out, float *moe_out, float *x_out, char *err, uint64_t err_len);
 
 /* How the layers of a token are launched (no reference counterpart: the reference
- * runs one thread on the CPU).  0: one kernel per phase, six per layer; 1: one
- * persistent kernel for all layers of the token, one workgroup per CU, phases handed
- * over through epoch-tagged device words.  Both give the same results to the stated
- * tolerance; the default is 0.  Drops the recorded decode graph.  A model bound with
- * formats beyond IQ4_XS / IQ2_XS / IQ3_XXS keeps path 0 whatever is set here. */
+ * runs one thread on the CPU).  1 (the default): one cooperative persistent kernel per
+ * qxg_generate / qxg_decode_token call runs every step (embedding, all layers, head,
+ * argmax), one workgroup per CU, its phases handed over through epoch-tagged device
+ * words; 0: one kernel per phase, six per layer, each step replayed from a recorded
+ * graph.  Both give the same results to the stated tolerance.  Drops the recorded decode
+ * graph.  A model bound with formats beyond IQ4_XS / IQ2_XS / IQ3_XXS, and the
+ * q8_k_compat mode, run path 0 whatever is set here. */
 int qxg_set_layer_path(qxg_ctx *ctx, int persistent);
 
 /* Activation format of the projections, experts and head: 0 "f32" (default), 1

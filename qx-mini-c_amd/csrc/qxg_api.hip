@@ -135,7 +135,7 @@ struct qxg_ctx {
     hipEvent_t e0 = nullptr, e1 = nullptr;
     KernelTiming kt;
     // persistent decode: weight arenas, router fold, tagged exchange buffers, abort flag
-    bool persist = false;            // layer path: persistent decode kernel (true) or one kernel per phase
+    bool persist = true;             // layer path: persistent decode kernel (true, the default) or one kernel per phase
     bool base_mix = true;            // every layer in the benchmark mix (IQ4_XS attention, IQ2_XS/IQ3_XXS experts)
     bool q8 = false;                 // activation mode q8_k_compat (false: f32)
     bool eager = false;              // QXG_EAGER=1 at open: qxg_generate launches every step without a graph
