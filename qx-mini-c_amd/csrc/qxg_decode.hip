@@ -198,6 +198,8 @@ struct DLds {
     float ys[QXG_TOPK][8];       // down rows of each rank (stage D)
     float outw[32];              // the workgroup's outputs of a stage, gathered for one store
     uint32_t flag[NWV];
+    uint32_t sub[4];             // upper_waves_sync flags of waves 4..7
+    uint32_t fail;               // a poll of waves 4..7 timed out (stage G)
     union {
         struct {
             union {
@@ -253,14 +255,16 @@ DEV void wait_pairs(u32x4 (&w)[K2]) {
         asm volatile("s_waitcnt vmcnt(0)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]) : : "memory");
     else static_assert(K2 == 1 || K2 == 2 || K2 == 4 || K2 == 7, "pairs per thread");
 }
-template <int K2, typename IDX>
-DEV bool wait_xch2(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, DLds &S, const Ctl &c) {
-    const int tid = tix();
+// The polling of wait_xch2 by threads T0 .. T0 + P - 1 only (the caller's branch), pair
+// p = t + P k for thread T0 + t; returns this thread's success, with no barrier.
+template <int K2, int P = NT, int T0 = 0, typename IDX>
+DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, const Ctl &c) {
+    const int tid = tix() - T0;
     u32x4 w[K2];
     bool got[K2];
 #pragma unroll
     for (int k = 0; k < K2; ++k) {
-        const int i = 2 * (tid + NT * k);
+        const int i = 2 * (tid + P * k);
         got[k] = i >= n;
         w[k] = u32x4{0u, ep, 0u, ep};
     }
@@ -270,7 +274,7 @@ DEV bool wait_xch2(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, 
     for (;;) {
 #pragma unroll
         for (int k = 0; k < K2; ++k)
-            if (!got[k]) ld_pair(w[k], base + idx(2 * (tid + NT * k)));
+            if (!got[k]) ld_pair(w[k], base + idx(2 * (tid + P * k)));
         wait_pairs<K2>(w);
         bool all = true;
 #pragma unroll
@@ -283,10 +287,32 @@ DEV bool wait_xch2(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, 
     }
 #pragma unroll
     for (int k = 0; k < K2; ++k) {
-        const int i = 2 * (tid + NT * k);
+        const int i = 2 * (tid + P * k);
         if (i < n) *reinterpret_cast<uint2 *>(dst + i) = make_uint2(w[k].x, w[k].z);
     }
-    return !block_any(!ok, S);
+    return ok;
+}
+template <int K2, typename IDX>
+DEV bool wait_xch2(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, DLds &S, const Ctl &c) {
+    return !block_any(!poll_pairs<K2>(base, n, ep, dst, idx, c), S);
+}
+
+// Waves 4..7 only, all four calling it: each wave's earlier LDS writes are visible to the
+// other three afterwards (the other four waves are not involved).  Each wave posts tag in its
+// LDS flag, then spins on the four flags; tag must differ from every earlier call's (the
+// exchange epochs are).  Every wave reaches its post, so the spin ends.
+DEV void upper_waves_sync(DLds &S, uint32_t tag) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    const int wave = tix() >> 6;
+    if ((tix() & 63) == 0) __hip_atomic_store(&S.sub[wave - 4], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (;;) {
+        bool all = true;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) all = all && __hip_atomic_load(&S.sub[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == tag;
+        if (all) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
 }
 
 // Digit planes of an N-vector held in LDS (as f32 bits), 8 values per thread-chunk; with
@@ -485,14 +511,17 @@ DEV void addr_gu(const GuRef &g, uint64_t gu_base, uint64_t (&addr)[4]) {
 }
 // Down rows 8 wg .. 8 wg + 7 of the expert of rank w: 8 * QXD_DN_ROW = 2432 contiguous bytes,
 // chunks [0, 152) (3 instructions, 3 KB of LDS; lanes past 152 repeat chunk 0).  In LDS row
-// j sits at j * QXD_DN_ROW: qs +0 (3 x 64), aux +192 (3 x 32), d +288 (3 x 2).
-DEV void addr_dn(const uint32_t (&ids)[QXG_TOPK], int w, uint64_t dn_base, uint64_t (&addr)[3]) {
+// j sits at j * QXD_DN_ROW: qs +0 (3 x 64), aux +192 (3 x 32), d +288 (3 x 2).  In HBM the
+// 8-row blocks of all E experts for one row range lie together ((wg * E + e) * 8 rows), so a
+// workgroup's 8 experts' down rows lie within E * 2432 bytes (311 KB at E = 128: one or two
+// 2 MB translation pages instead of eight).
+DEV void addr_dn(const uint32_t (&ids)[QXG_TOPK], int w, uint32_t E, uint64_t dn_base, uint64_t (&addr)[3]) {
     const int lane = tix() & 63;
     uint32_t e = 0u;
 #pragma unroll
     for (int q = 0; q < QXG_TOPK; ++q)
         if (q == w) e = ids[q];
-    const uint64_t base = dn_base + (uint64_t)(e * 2048 + 8 * blockIdx.x) * QXD_DN_ROW;
+    const uint64_t base = dn_base + ((uint64_t)blockIdx.x * E + e) * (8 * QXD_DN_ROW);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const uint32_t c = 64 * i + lane;
@@ -890,6 +919,8 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
         for (int i = tid; i < 512; i += NT) S.g2[i] = a.T.g2[i];
         if (tid < 256) S.g3[tid] = a.T.g3[tid];
         if (tid < 128) S.sel[tid] = a.T.sel[tid];
+        if (tid < 4) S.sub[tid] = 0u;   // the tags start above 0
+        if (tid == 0) S.fail = 0u;
     }
     WQ wq;
     WO wo;
@@ -1081,15 +1112,11 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             {
                 const int tid = tix(), lane = tid & 63, wave = tid >> 6, ib = lane & 7;
                 const int gw = NWV * wg + wave;
-                // x', then the E router logits (hi and lo words, published early in stage O, so
-                // normally one read).  Then two halves of the workgroup in parallel: waves 0..3 (one
-                // per SIMD) take the top-8 and issue the routed experts' row copies for themselves
-                // and waves 4..7, then wait for them; waves 4..7 form the normalised x' digits.  One
-                // barrier joins them before the dots.
-                const GLB uint64_t *xpb = X + XO_XP + par * XN_XP;
-                if (!wait_xch2<2>(xpb, 2048, ep + 3, reinterpret_cast<uint32_t *>(S.xp), Ident(), S, ctl))
-                    return;
-                DMARK(l, 9);
+                // The E router logits first (hi and lo words; the router workgroups publish them in
+                // stage O before x', so they are normally in by now).  Then the halves work in
+                // parallel: waves 0..3 (one per SIMD) take the top-8, issue the routed experts' row
+                // copies for themselves and waves 4..7 and wait for them; waves 4..7 poll x' and
+                // form its normalised digits.  One barrier joins them before the dots.
                 if (!wait_xch2<1>(X + XO_LG + par * XN_LG, 2 * (int)E, ep + 3, S.lgw, Ident(), S, ctl))
                     return;
                 DMARK(l, 7);
@@ -1109,8 +1136,8 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     uint64_t ga0[4], ga1[4], da0[3], da1[3];
                     addr_gu(gu_ref(ids, wv), gub, ga0);
                     addr_gu(gu_ref(ids, wv + 4), gub, ga1);
-                    addr_dn(ids, wv, dnb, da0);
-                    addr_dn(ids, wv + 4, dnb, da1);
+                    addr_dn(ids, wv, E, dnb, da0);
+                    addr_dn(ids, wv + 4, E, dnb, da1);
                     u32x4 g0[4], g1[4], d0[3], d1[3];
                     load_rows(ga0, g0);
                     load_rows(ga1, g1);
@@ -1123,6 +1150,13 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     store_rows(d1, S.u.m.dn[wv + 4]);
                     DMARK(l, 19);
                 } else {
+                    // x', polled by these four waves alone (waves 0..3 are issuing the expert
+                    // rows meanwhile; a poll behind those loads would wait for them)
+                    const GLB uint64_t *xpb = X + XO_XP + par * XN_XP;
+                    if (!poll_pairs<4, 256, 256>(xpb, 2048, ep + 3, reinterpret_cast<uint32_t *>(S.xp), Ident(), ctl))
+                        S.fail = 1u;
+                    upper_waves_sync(S, ep + 3);
+                    DMARKT(l, 9, 256);
                     // RMSNorm of x' (reference src/qx_format.c:3358-3371, double sum of squares,
                     // each wave over all 2048 values) and the digits of values 512 (w - 4) ..
                     double ss = 0.0;
@@ -1152,6 +1186,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     DMARKT(l, 17, 256);
                 }
                 __syncthreads();
+                if (S.fail) return;   // (read by every thread after the barrier: uniform)
                 DMARK(l, 20);
                 if (wg == 0 && wv == 0) {   // renormalised weights of the picks (reference :5265-5290)
                     const double inv = S.xinv;
@@ -1172,20 +1207,33 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 load_dig(S.dig, lane, g);
                 float p[8], o[8];
                 {
+                    // six sub-blocks (gate then up of units 0..2): their index words first, then
+                    // the codebook reads of sub-block i + 1 in flight while sub-block i computes
                     const uint32_t b = lane >> 3, ib = lane & 7;
+                    const uint32_t q = b * 64 + ib * 8, sc = b * 8 + ib, d = b * 2;
+                    uint2 qs[6];
+                    uint32_t scs[6], ds[6];
 #pragma unroll
-                    for (int uu = 0; uu < 3; ++uu) {
-                        const uint8_t *u = S.u.m.gu[wv] + uu * QXD_GU_UNIT;
-                        const uint32_t q = b * 64 + ib * 8, sc = b * 8 + ib, d = b * 2;
-                        p[uu] = dot_iq2(*reinterpret_cast<const uint2 *>(u + q), u[GU_GSC + sc],
-                                        *reinterpret_cast<const uint16_t *>(u + GU_GD + d), g, S.g2, S.sel);
-                        p[4 + uu] = dot_iq2(*reinterpret_cast<const uint2 *>(u + GU_UQ + q), u[GU_USC + sc],
-                                            *reinterpret_cast<const uint16_t *>(u + GU_UD + d), g, S.g2, S.sel);
+                    for (int i = 0; i < 6; ++i) {
+                        const uint8_t *u = S.u.m.gu[wv] + (i % 3) * QXD_GU_UNIT;
+                        const uint32_t oq = i < 3 ? 0u : GU_UQ, os = i < 3 ? GU_GSC : GU_USC, od = i < 3 ? GU_GD : GU_UD;
+                        qs[i] = *reinterpret_cast<const uint2 *>(u + oq + q);
+                        scs[i] = u[os + sc];
+                        ds[i] = *reinterpret_cast<const uint16_t *>(u + od + d);
+                    }
+                    Iq2Look kl[2];
+                    iq2_look(qs[0], S.g2, S.sel, kl[0]);
+#pragma unroll
+                    for (int i = 0; i < 6; ++i) {
+                        if (i + 1 < 6) iq2_look(qs[i + 1], S.g2, S.sel, kl[(i + 1) & 1]);
+                        p[i < 3 ? i : i + 1] = iq2_dot(kl[i & 1], scs[i], ds[i], g);
                     }
                 }
                 p[3] = p[7] = 0.0f;
                 rows_reduce<8>(p, o, lane);
                 DMARK(l, 18);
+                DMARKT(l, 28, 256);
+                DMARKT(l, 30, 448);
                 (void)ib;
                 (void)gw;
                 {   // lane k < 3: unit k (selects, then one pass for the three lanes)
@@ -1202,6 +1250,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     }
                 }
                 __syncthreads();
+                DMARK(l, 29);
                 if (tid < 24) xstf(X + XO_H + par * XN_H + 24 * wg + tid, ep + 4, S.outw[tid]);
                 // attention workgroups: the next layer's Q/K/V rows, arriving during the h exchange
                 if (wg < QXG_HEADS) load_wq(a, ln, wq, S.wq[wave_id()]);
@@ -1226,19 +1275,38 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 // wave w: rank w's rows 8 wg + j (lanes 8 j .. 8 j + 7, sub-block k of each block)
                 const int j8 = lane >> 3, k = lane & 7, wv = wave_id();
                 float part = 0.0f;
-#pragma unroll
-                for (int b = 0; b < 3; ++b) {
-                    Dig g;
-                    load_dig(S.dig, 24 * wv + 8 * b + k, g);
+                {
+                    // the three blocks' index words first, then block b + 1's codebook reads
+                    // and digits in flight while block b computes
                     const uint8_t *dn = S.u.m.dn[wv] + j8 * QXD_DN_ROW;
-                    part += dot_iq3(*reinterpret_cast<const uint2 *>(dn + 64 * b + 8 * k), *reinterpret_cast<const uint32_t *>(dn + 192 + 32 * b + 4 * k),
-                                    *reinterpret_cast<const uint16_t *>(dn + 288 + 2 * b), g, S.g3, S.sel);
+                    uint2 qs[3];
+                    uint32_t aux[3], ds[3];
+#pragma unroll
+                    for (int b = 0; b < 3; ++b) {
+                        qs[b] = *reinterpret_cast<const uint2 *>(dn + 64 * b + 8 * k);
+                        aux[b] = *reinterpret_cast<const uint32_t *>(dn + 192 + 32 * b + 4 * k);
+                        ds[b] = *reinterpret_cast<const uint16_t *>(dn + 288 + 2 * b);
+                    }
+                    Iq3Look kl[2];
+                    Dig gd[2];
+                    iq3_look(qs[0], aux[0], S.g3, S.sel, kl[0]);
+                    load_dig(S.dig, 24 * wv + k, gd[0]);
+#pragma unroll
+                    for (int b = 0; b < 3; ++b) {
+                        if (b + 1 < 3) {
+                            iq3_look(qs[b + 1], aux[b + 1], S.g3, S.sel, kl[(b + 1) & 1]);
+                            load_dig(S.dig, 24 * wv + 8 * (b + 1) + k, gd[(b + 1) & 1]);
+                        }
+                        part += iq3_dot(kl[b & 1], aux[b], ds[b], gd[b & 1]);
+                    }
                 }
                 part += dppf<DPP_XOR1>(part);
                 part += dppf<DPP_XOR2>(part);
                 part += dppf<DPP_HALF_MIRROR>(part);   // lanes 8 j .. 8 j + 7 hold row j's sum
                 if (k == 0) S.ys[wv][j8] = (okh && isfinite(part)) ? part : 0.0f;
+                DMARK(l, 26);
                 __syncthreads();
+                DMARK(l, 27);
                 if (tid < 8) {
                     // reference src/qx_format.c:5296-5309: moe += (float)(w_r * (double)y_r), rank order
                     float moe = 0.0f;
@@ -1332,8 +1400,8 @@ extern "C" __global__ __launch_bounds__(256) void qxk_interleave_experts(const u
         cp32(o + 1104, us + t * 64, 16);
         cp32(o + 1168, ud + t * 16, 4);
     } else if (t < ngu + ndn) {
-        const uint64_t r = t - ngu;
-        uint8_t *o = dn + r * QXD_DN_ROW;
+        const uint64_t r = t - ngu, e = r / 2048, row = r % 2048;   // source: row-major per expert
+        uint8_t *o = dn + (((row >> 3) * E + e) * 8 + (row & 7)) * QXD_DN_ROW;
         cp32(o, dq + r * 192, 48);
         cp32(o + 192, dx + r * 96, 24);
         uint16_t *o16 = reinterpret_cast<uint16_t *>(o + 288);

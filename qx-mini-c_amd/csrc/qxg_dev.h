@@ -127,15 +127,27 @@ DEV float dot_iq4(uint4 qs, uint2 meta, int ib, const Dig &g) {
     return (dl * g.s) * combine(aH, aM, aL);
 }
 
-// IQ2_XS sub-block (32 values = 4 grid entries of 8): halves scaled d*(2s+1)/8
-DEV float dot_iq2(uint2 qs, uint32_t sc, uint32_t d16, const Dig &g, const uint4 *G2, const uint2 *SEL) {
+// IQ2_XS sub-block (32 values = 4 grid entries of 8): halves scaled d*(2s+1)/8.  Two phases:
+// iq2_look issues the sub-block's LDS codebook reads (grid entries and sign selectors),
+// iq2_dot does the arithmetic, so a caller can keep the next sub-block's reads in flight
+// while it computes this one (one dependent LDS round trip per sub-block, not one per entry).
+struct Iq2Look {
+    uint4 gg[4];
+    uint2 sl[4];
+};
+DEV void iq2_look(uint2 qs, const uint4 *G2, const uint2 *SEL, Iq2Look &k) {
     const uint32_t qv[4] = {qs.x & 0xffffu, qs.x >> 16, qs.y & 0xffffu, qs.y >> 16};
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        k.gg[l] = G2[qv[l] & 511u];
+        k.sl[l] = SEL[qv[l] >> 9];
+    }
+}
+DEV float iq2_dot(const Iq2Look &k, uint32_t sc, uint32_t d16, const Dig &g) {
     int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-        const uint4 gg = G2[qv[l] & 511u];
-        const uint2 sl = SEL[qv[l] >> 9];
-        const uint32_t w0 = perm(gg.z, gg.x, sl.x), w1 = perm(gg.w, gg.y, sl.y);
+        const uint32_t w0 = perm(k.gg[l].z, k.gg[l].x, k.sl[l].x), w1 = perm(k.gg[l].w, k.gg[l].y, k.sl[l].y);
         if (l < 2) {
             h0 = sdot4(w0, g.h[2 * l], h0); h0 = sdot4(w1, g.h[2 * l + 1], h0);
             m0 = sdot4(w0, g.m[2 * l], m0); m0 = sdot4(w1, g.m[2 * l + 1], m0);
@@ -150,23 +162,43 @@ DEV float dot_iq2(uint2 qs, uint32_t sc, uint32_t d16, const Dig &g, const uint4
     const float v = combine(k0 * h0 + k1 * h1, k0 * m0 + k1 * m1, k0 * l0 + k1 * l1);
     return ((fp16_exact(d16) * 0.125f) * g.s) * v;
 }
+DEV float dot_iq2(uint2 qs, uint32_t sc, uint32_t d16, const Dig &g, const uint4 *G2, const uint2 *SEL) {
+    Iq2Look k;
+    iq2_look(qs, G2, SEL, k);
+    return iq2_dot(k, sc, d16, g);
+}
 
-// IQ3_XXS sub-block: 8 grid indices (4 values each), scale d*(2a+1)/4
-DEV float dot_iq3(uint2 qs, uint32_t aux, uint32_t d16, const Dig &g, const uint2 *G3, const uint2 *SEL) {
-    int aH = 0, aM = 0, aL = 0;
+// IQ3_XXS sub-block: 8 grid indices (4 values each), scale d*(2a+1)/4; iq3_look / iq3_dot
+// split as for IQ2_XS.
+struct Iq3Look {
+    uint2 g[8];
+    uint2 sl[4];
+};
+DEV void iq3_look(uint2 qs, uint32_t aux, const uint2 *G3, const uint2 *SEL, Iq3Look &k) {
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
         const uint32_t word = l < 2 ? qs.x : qs.y;
-        const uint32_t b1 = (word >> (16 * (l & 1))) & 255u, b2 = (word >> (16 * (l & 1) + 8)) & 255u;
-        const uint2 g1 = G3[b1], g2 = G3[b2];
-        const uint2 sl = SEL[(aux >> (7 * l)) & 127u];
-        const uint32_t w0 = perm(g1.y, g1.x, sl.x), w1 = perm(g2.y, g2.x, sl.y);
+        k.g[2 * l] = G3[(word >> (16 * (l & 1))) & 255u];
+        k.g[2 * l + 1] = G3[(word >> (16 * (l & 1) + 8)) & 255u];
+        k.sl[l] = SEL[(aux >> (7 * l)) & 127u];
+    }
+}
+DEV float iq3_dot(const Iq3Look &k, uint32_t aux, uint32_t d16, const Dig &g) {
+    int aH = 0, aM = 0, aL = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+        const uint32_t w0 = perm(k.g[2 * l].y, k.g[2 * l].x, k.sl[l].x), w1 = perm(k.g[2 * l + 1].y, k.g[2 * l + 1].x, k.sl[l].y);
         aH = sdot4(w0, g.h[2 * l], aH); aH = sdot4(w1, g.h[2 * l + 1], aH);
         aM = sdot4(w0, g.m[2 * l], aM); aM = sdot4(w1, g.m[2 * l + 1], aM);
         aL = sdot4(w0, g.l[2 * l], aL); aL = sdot4(w1, g.l[2 * l + 1], aL);
     }
-    const int k = 2 * (int)(aux >> 28) + 1;
-    return ((fp16_exact(d16) * 0.25f) * g.s) * combine(k * aH, k * aM, k * aL);
+    const int k3 = 2 * (int)(aux >> 28) + 1;
+    return ((fp16_exact(d16) * 0.25f) * g.s) * combine(k3 * aH, k3 * aM, k3 * aL);
+}
+DEV float dot_iq3(uint2 qs, uint32_t aux, uint32_t d16, const Dig &g, const uint2 *G3, const uint2 *SEL) {
+    Iq3Look k;
+    iq3_look(qs, aux, G3, SEL, k);
+    return iq3_dot(k, aux, d16, g);
 }
 
 // IQ2_S sub-block (32 values = 4 grid entries of 8; src/qx_format.c:1961-1984): 10-bit grid
@@ -841,19 +873,83 @@ DEV bool top8_rounds(K k0, K k1, MaxF wmax, uint32_t (&ids)[QXG_TOPK]) {
     return tie;
 }
 
+// The top 8 of the 128 keys by merging sorted lists across lanes, in a short dependency chain
+// (about 30 dependent steps against about 120 for eight rounds of wave maxima; measured 0.71
+// against 1.22 us per call).  Keys are packed as the f32 key's top 25 bits over the expert
+// index (127 - e, so a lower index wins between equal prefixes), unique, so the list merges
+// need no tie handling.  Each lane starts with its two keys as a sorted list; xor-1 and xor-2
+// lane exchanges merge the lists to 4 and 8 entries, then four merges keep the top 8 of two
+// 8-lists (row rotations by 4 and 8, row broadcasts 15 and 31); lane 63 ends with the wave's
+// top 8 in order.  Returns true when the packed order may differ from the order by
+// (f32 key, index): two keys of the top 8, or the 8th and a key outside, share a 25-bit
+// prefix; the caller then redoes the selection exactly.
+#define QXG_CE(x, y) { const uint32_t hi_ = max(x, y), lo_ = min(x, y); x = hi_; y = lo_; }
+template <int CTRL, int ROWS>
+DEV uint32_t lane_pull(uint32_t v) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xf, false); }
+template <int CTRL, int ROWS>
+DEV void merge_top8(uint32_t (&v)[8]) {
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = lane_pull<CTRL, ROWS>(v[i]);   // rows outside ROWS pull 0
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = max(v[i], b[7 - i]);   // the top 8 of both lists, bitonic
+    QXG_CE(v[0], v[4]) QXG_CE(v[1], v[5]) QXG_CE(v[2], v[6]) QXG_CE(v[3], v[7])
+    QXG_CE(v[0], v[2]) QXG_CE(v[1], v[3]) QXG_CE(v[4], v[6]) QXG_CE(v[5], v[7])
+    QXG_CE(v[0], v[1]) QXG_CE(v[2], v[3]) QXG_CE(v[4], v[5]) QXG_CE(v[6], v[7])
+}
+DEV bool top8_lists(double l0, double l1, int E, uint32_t (&ids)[QXG_TOPK]) {
+    static_assert(QXG_TOPK == 8, "eight picks");
+    const int lane = threadIdx.x & 63;
+    const uint32_t f0 = lane < E ? fkey(l0) : 0u, f1 = lane + 64 < E ? fkey(l1) : 0u;
+    const uint32_t k0 = f0 ? (f0 & ~127u) | (127u - (uint32_t)lane) : 0u;
+    const uint32_t k1 = f1 ? (f1 & ~127u) | (63u - (uint32_t)lane) : 0u;
+    uint32_t v[8] = {max(k0, k1), min(k0, k1), 0u, 0u, 0u, 0u, 0u, 0u};
+    {   // 2 + 2 -> 4 (lane xor 1): a0 a1 b1 b0 is bitonic
+        const uint32_t b0 = lane_pull<0xb1, 0xf>(v[0]), b1 = lane_pull<0xb1, 0xf>(v[1]);
+        v[2] = b1; v[3] = b0;
+        QXG_CE(v[0], v[2]) QXG_CE(v[1], v[3]) QXG_CE(v[0], v[1]) QXG_CE(v[2], v[3])
+    }
+    {   // 4 + 4 -> 8 (lane xor 2)
+        uint32_t b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b[i] = lane_pull<0x4e, 0xf>(v[i]);
+        v[4] = b[3]; v[5] = b[2]; v[6] = b[1]; v[7] = b[0];
+        QXG_CE(v[0], v[4]) QXG_CE(v[1], v[5]) QXG_CE(v[2], v[6]) QXG_CE(v[3], v[7])
+        QXG_CE(v[0], v[2]) QXG_CE(v[1], v[3]) QXG_CE(v[4], v[6]) QXG_CE(v[5], v[7])
+        QXG_CE(v[0], v[1]) QXG_CE(v[2], v[3]) QXG_CE(v[4], v[5]) QXG_CE(v[6], v[7])
+    }
+    merge_top8<0x124, 0xf>(v);   // row_ror:4
+    merge_top8<0x128, 0xf>(v);   // row_ror:8: every lane holds its row's top 8
+    merge_top8<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+    merge_top8<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3: lane 63 holds the wave's
+    uint32_t m[8];
+    bool tie = false;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        m[q] = (uint32_t)__builtin_amdgcn_readlane((int)v[q], 63);
+        ids[q] = m[q] ? 127u - (m[q] & 127u) : 0u;   // no key left (non-finite logits): expert 0
+        if (q > 0) tie = tie || (m[q] != 0u && (m[q] & ~127u) == (m[q - 1] & ~127u));
+    }
+    const uint32_t p7 = m[7] & ~127u;
+    return tie || __ballot(p7 != 0u && ((k0 < m[7] && (k0 & ~127u) == p7) || (k1 < m[7] && (k1 & ~127u) == p7))) != 0;
+}
+#undef QXG_CE
+
 // Router top-8 and renormalised weights (src/qx_format.c:5265-5285), by every wave on
 // its own (no block barrier).  Lane l holds the logits of experts l and l+64 (double).
 // The reference picks by softmax probability with repeated strict-> scans (larger
 // first, lower index on ties); the probability is a non-decreasing function of the
 // logit, so picking by logit gives the same experts except where two probabilities
 // round to the same double (a zero margin).  The picks use 32-bit keys of the logits
-// rounded to f32: a unique maximal f32 key is also the maximal double.  Only when a
-// round sees several experts at the maximal f32 key are the picks redone with the
-// exact 64-bit keys of the doubles.  The weights p_r / sum_q p_q equal
+// rounded to f32: a unique maximal f32 key is also the maximal double.  The list merge
+// above picks first; where its packed keys may misorder, eight rounds of wave maxima over
+// the full f32 keys pick, and only when a round sees several experts at the maximal f32
+// key are the picks redone with the exact 64-bit keys of the doubles.  The weights p_r / sum_q p_q equal
 // e_r / sum_q e_q with e = exp(l - l_max), since the softmax denominator cancels.
 // ids[r] and w[r] are wave-uniform.
 DEV void wave_top8_ids(double l0, double l1, int E, uint32_t (&ids)[QXG_TOPK]) {
     const int lane = threadIdx.x & 63;
+    if (!top8_lists(l0, l1, E, ids)) return;
     const bool tie = top8_rounds<uint32_t>(lane < E ? fkey(l0) : 0u, lane + 64 < E ? fkey(l1) : 0u,
                                            [](uint32_t v) { return wave_max_u32(v); }, ids);
     if (tie)

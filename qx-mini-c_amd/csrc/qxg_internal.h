@@ -119,7 +119,7 @@ struct QxDArgs {
     QxPlane P[PL_COUNT];         // per-layer weight planes (layer l at base + l * stride)
     QxPlane M;                   // router fold M = W diag(w) O, [experts][4096] f32 per layer
     QxPlane GU;                  // routed experts' gate/up rows, unit-interleaved (QXD_GU_UNIT bytes per unit)
-    QxPlane DN;                  // routed experts' down rows, row-interleaved (QXD_DN_ROW bytes per row)
+    QxPlane DN;                  // routed experts' down rows (QXD_DN_ROW bytes per row), 8-row blocks of all experts together
     const uint8_t *emb;          // Q4_K token embedding
     uint64_t emb_row;
     const float *out_norm;
