@@ -198,6 +198,8 @@ struct DLds {
     float ys[QXG_TOPK][8];       // down rows of each rank (stage D)
     float outw[32];              // the workgroup's outputs of a stage, gathered for one store
     uint32_t flag[NWV];
+    uint32_t bflag[2][NWV];      // block_any flags, two sets by call parity
+    uint32_t bpar[NWV];          // block_any call parity of each wave
     uint32_t sub[4];             // upper_waves_sync flags of waves 4..7
     uint32_t fail;               // a poll of waves 4..7 timed out (stage G)
     union {
@@ -219,16 +221,22 @@ struct DLds {
 };
 
 // block-wide OR of a per-thread flag (every thread of the workgroup calls it); includes
-// the barrier that publishes the caller's earlier LDS writes
+// the barrier that publishes the caller's earlier LDS writes.  One barrier: the flags
+// alternate between two sets by call parity (each wave keeps its own parity bit), and a
+// wave can only write a set again two calls later, after the barrier of the call between,
+// which every wave reaches after reading this call's set.
 DEV bool block_any(bool f, DLds &S) {
     const bool any = __ballot(f) != 0;
     const int wave = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) S.flag[wave] = any ? 1u : 0u;
+    const uint32_t p = S.bpar[wave];   // (only this wave touches its bit)
+    if ((threadIdx.x & 63) == 0) {
+        S.bflag[p][wave] = any ? 1u : 0u;
+        S.bpar[wave] = p ^ 1u;
+    }
     __syncthreads();
     uint32_t r = 0;
 #pragma unroll
-    for (int w = 0; w < NWV; ++w) r |= S.flag[w];
+    for (int w = 0; w < NWV; ++w) r |= S.bflag[p][w];
     return r != 0;
 }
 
@@ -920,6 +928,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
         if (tid < 256) S.g3[tid] = a.T.g3[tid];
         if (tid < 128) S.sel[tid] = a.T.sel[tid];
         if (tid < 4) S.sub[tid] = 0u;   // the tags start above 0
+        if (tid < NWV) S.bpar[tid] = 0u;
         if (tid == 0) S.fail = 0u;
     }
     WQ wq;

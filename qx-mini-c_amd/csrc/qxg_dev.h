@@ -89,6 +89,11 @@ struct Dig {
     float s;
 };
 
+// a * b for |a|, |b| < 2^23 (a full-rate 24-bit multiply; the 32-bit integer multiply runs
+// at a quarter of the rate).  The dot epilogues' scale factors (< 2^8) and digit-plane sums
+// (< 2^18) are in range.
+DEV int mul24(int a, int b) { return __mul24(a, b); }
+
 DEV float combine(int aH, int aM, int aL) {
     return fmaf((float)aH, 65536.0f, fmaf((float)aM, 256.0f, (float)aL));
 }
@@ -159,7 +164,7 @@ DEV float iq2_dot(const Iq2Look &k, uint32_t sc, uint32_t d16, const Dig &g) {
         }
     }
     const int k0 = 2 * (int)(sc & 15u) + 1, k1 = 2 * (int)(sc >> 4) + 1;
-    const float v = combine(k0 * h0 + k1 * h1, k0 * m0 + k1 * m1, k0 * l0 + k1 * l1);
+    const float v = combine(mul24(k0, h0) + mul24(k1, h1), mul24(k0, m0) + mul24(k1, m1), mul24(k0, l0) + mul24(k1, l1));
     return ((fp16_exact(d16) * 0.125f) * g.s) * v;
 }
 DEV float dot_iq2(uint2 qs, uint32_t sc, uint32_t d16, const Dig &g, const uint4 *G2, const uint2 *SEL) {
@@ -193,7 +198,7 @@ DEV float iq3_dot(const Iq3Look &k, uint32_t aux, uint32_t d16, const Dig &g) {
         aL = sdot4(w0, g.l[2 * l], aL); aL = sdot4(w1, g.l[2 * l + 1], aL);
     }
     const int k3 = 2 * (int)(aux >> 28) + 1;
-    return ((fp16_exact(d16) * 0.25f) * g.s) * combine(k3 * aH, k3 * aM, k3 * aL);
+    return ((fp16_exact(d16) * 0.25f) * g.s) * combine(mul24(k3, aH), mul24(k3, aM), mul24(k3, aL));
 }
 DEV float dot_iq3(uint2 qs, uint32_t aux, uint32_t d16, const Dig &g, const uint2 *G3, const uint2 *SEL) {
     Iq3Look k;
@@ -225,7 +230,7 @@ DEV float dot_iq2s(uint32_t qs4, uint32_t sg4, uint32_t qh, uint32_t sc, uint32_
         }
     }
     const int k0 = 2 * (int)(sc & 15u) + 1, k1 = 2 * (int)((sc >> 4) & 15u) + 1;
-    const float v = combine(k0 * h0 + k1 * h1, k0 * m0 + k1 * m1, k0 * l0 + k1 * l1);
+    const float v = combine(mul24(k0, h0) + mul24(k1, h1), mul24(k0, m0) + mul24(k1, m1), mul24(k0, l0) + mul24(k1, l1));
     return ((fp16_exact(d16) * 0.125f) * g.s) * v;
 }
 
@@ -248,7 +253,7 @@ DEV float dot_iq3s(uint2 qs8, uint32_t sg4, uint32_t qh, uint32_t sc, uint32_t d
         aL = sdot4(w0, g.l[2 * l], aL); aL = sdot4(w1, g.l[2 * l + 1], aL);
     }
     const int k = 2 * (int)(sc & 15u) + 1;
-    return (fp16_exact(d16) * g.s) * combine(k * aH, k * aM, k * aL);
+    return (fp16_exact(d16) * g.s) * combine(mul24(k, aH), mul24(k, aM), mul24(k, aL));
 }
 
 // Q5_K sub-block ib (src/qx_format.c:2112-2145): values 32ib..32ib+31 have 5-bit codes
@@ -313,7 +318,8 @@ DEV float dot_q6(uint4 ql0, uint4 ql1, uint4 qh0, uint4 qh1, int sc0, int sc1, u
         aM[s] = sdot4(u, g.m[j], aM[s]);
         aL[s] = sdot4(u, g.l[j], aL[s]);
     }
-    const float v = combine(sc0 * aH[0] + sc1 * aH[1], sc0 * aM[0] + sc1 * aM[1], sc0 * aL[0] + sc1 * aL[1]);
+    const float v = combine(mul24(sc0, aH[0]) + mul24(sc1, aH[1]), mul24(sc0, aM[0]) + mul24(sc1, aM[1]),
+                            mul24(sc0, aL[0]) + mul24(sc1, aL[1]));
     return (fp16_exact(d16) * g.s) * v;
 }
 
