@@ -148,9 +148,10 @@ struct QxDArgs {
 #define QXD_THREADS 512
 // Interleaved expert rows of the persistent decode: unit (expert e, row r) of gate/up is
 // [gate qs 512 | sc 64 | d 16 | up qs 512 | sc 64 | d 16] at (e * 768 + r) * 1184; down row
-// (e, r) is [qs 192 | aux 96 | d 6 | 0 x 10] at (e * 2048 + r) * 304.  A wave's rows then lie
-// in one contiguous range, so each of its 16-byte load instructions touches one or two
-// pages (the cost of a scattered load instruction grows with the pages it touches).
+// (e, r) is [qs 192 | aux 96 | d 6 | 0 x 10] at (((r / 8) * E + e) * 8 + r % 8) * 304 (the
+// 8-row blocks of all E experts for one row range together).  A wave's rows then lie in one
+// contiguous range, so each of its 16-byte load instructions touches one or two pages (the
+// cost of a scattered load instruction grows with the pages it touches).
 #define QXD_GU_UNIT 1184u
 // Q6_K head row r of the persistent decode: [ql 1024 | qh 512 | sc 128 | d 16] at r * 1680
 // (the 8 blocks' planes of the row back to back; 105 16-byte chunks).
@@ -200,6 +201,7 @@ struct PfGemm {
     uint32_t ld;
     const float *resid;        // residual added by the O projection epilogue
     float *dump;               // O projection output without the residual (optional)
+    uint32_t xcd_rows;         // row-tile classes across the 8 XCDs (1, 2, 4 or 8; the launcher sets it)
 };
 
 // Optional start/stop events recorded around one launch on its stream.  Created with

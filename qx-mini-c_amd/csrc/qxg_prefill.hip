@@ -222,11 +222,11 @@ DEV void block_mma(const Blk<F> (&bk)[NSUB], const uint4 *sa, f16x (&acc)[NSUB][
 }
 
 template <int F, int NSUB, int NM, int EPI>
-DEV void gemm_body(const PfGemm &g, const GemmLds &L, uint32_t e, uint32_t mt0) {
+DEV void gemm_body(const PfGemm &g, const GemmLds &L, uint32_t e, uint32_t mt0, uint32_t bx) {
     constexpr bool GU = EPI == EPI_SWIGLU;
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), h = lane >> 5, col = lane & 31;
     const uint32_t KB = g.kb, KS = 16 * KB;
-    const uint32_t nt = blockIdx.x * 4 + wave;            // column tile group of this wave
+    const uint32_t nt = bx * 4 + wave;                    // column tile group of this wave
     const uint32_t c0 = GU ? 32 * nt : 32 * NSUB * nt;     // first output column
     PfMat W[NSUB];
     uint64_t rowblk[NSUB];
@@ -319,15 +319,31 @@ DEV void gemm_body(const PfGemm &g, const GemmLds &L, uint32_t e, uint32_t mt0) 
     }
 }
 
+// XCD-aware tile order.  Workgroups go to the 8 XCDs round-robin by linear index, and each
+// XCD has its own L2, so a row tile's packed activations are fetched once into every L2
+// whose XCD runs one of its column workgroups, and a weight column group once into every
+// L2 that runs one of its row tiles.  Workgroup L (on XCD r = L % 8) takes the tile
+// (x, y) with y % a == r / b and x % b == r % b, a = xcd_rows row classes, b = 8 / a column
+// classes: each XCD then reads 1/a of the activations and 1/b of the weights.  The
+// launcher makes gridDim.x a multiple of b and gridDim.y of a (extra rows return).
+DEV void xcd_tile(uint32_t a, uint32_t &bx, uint32_t &by) {
+    const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y, r = L & 7u, j = L >> 3;
+    const uint32_t b = 8u / a, nxb = gridDim.x / b;
+    bx = (j % nxb) * b + r % b;
+    by = (j / nxb) * a + r / b;
+}
+
 template <int F, int NSUB, int MT, int EPI>
 __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void qxp_gemm(PfGemm g, PfTables P) {
-    uint32_t e = 0, mt0, nmt;
+    uint32_t e = 0, mt0, nmt, bx, by;
+    xcd_tile(g.xcd_rows, bx, by);
     if (g.mgroups) {
-        if (blockIdx.y >= g.meta[0]) return;   // whole workgroup
-        const uint32_t mg = g.mgroups[blockIdx.y];
+        if (by >= g.meta[0]) return;   // whole workgroup
+        const uint32_t mg = g.mgroups[by];
         e = mg & 255u; mt0 = (mg >> 8) & 0xfffu; nmt = mg >> 20;
     } else {
-        mt0 = blockIdx.y * MT;
+        mt0 = by * MT;
+        if (mt0 >= g.mtiles) return;   // whole workgroup: a padding row
         nmt = min((uint32_t)MT, g.mtiles - mt0);
     }
     __shared__ uint4 s_g2[F == FMT_IQ2 ? 512 : 1];
@@ -341,8 +357,8 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void qxp_gemm(PfGemm g, PfTab
                         s_t[tid + 256] = reinterpret_cast<const uint32_t *>(P.g3h)[tid + 256]; }
     if (F == FMT_IQ4) s_t[tid] = P.kv2[tid];
     const GemmLds L{s_g2, s_sg, s_a, s_t, MT * 2048};
-    if (MT == 2 && nmt == 2) gemm_body<F, NSUB, (MT == 2 ? 2 : 1), EPI>(g, L, e, mt0);
-    else gemm_body<F, NSUB, 1, EPI>(g, L, e, mt0);
+    if (MT == 2 && nmt == 2) gemm_body<F, NSUB, (MT == 2 ? 2 : 1), EPI>(g, L, e, mt0, bx);
+    else gemm_body<F, NSUB, 1, EPI>(g, L, e, mt0, bx);
 }
 
 // ================================================================= element-wise stages
@@ -876,8 +892,16 @@ extern "C" __global__ __launch_bounds__(256) void qxp_combine(const float *x1, c
 
 // ================================================================= launch wrappers
 extern "C" {
-void qxp_launch_gemm(hipStream_t s, int kind, const PfGemm &g, const PfTables &P, uint32_t grid_x, uint32_t grid_y,
+void qxp_launch_gemm(hipStream_t s, int kind, const PfGemm &g0, const PfTables &P, uint32_t grid_x, uint32_t grid_y,
                      Timer tm) {
+    // row classes per kind (xcd_tile): Q/K/V 2 (4 MB of activations, 5.6 MB of weights),
+    // O 4 (8 MB, 4.5 MB), experts 8 (an expert tile's activations in one L2; its weights
+    // are read by that tile only)
+    PfGemm g = g0;
+    g.xcd_rows = kind == 0 ? 2u : kind == 1 ? 4u : 8u;
+    const uint32_t b = 8u / g.xcd_rows;
+    if (grid_x % b) g.xcd_rows = 8u;   // (the column counts here are multiples of 8 workgroups)
+    grid_y = (grid_y + g.xcd_rows - 1) / g.xcd_rows * g.xcd_rows;
     switch (kind) {
     case 0:   // Q/K/V: IQ4_XS, 32 columns per wave
         qx_launch(qxp_gemm<FMT_IQ4, 1, 1, EPI_STORE>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
