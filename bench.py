@@ -193,6 +193,9 @@ def main():
                     help="greedy tokens generated after the prefill (the first comes from the prefill's head)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the config 5 prefill leg (profiling aid; prints that leg's JSON)")
+    ap.add_argument("--real-mix", action="store_true",
+                    help="with --prefill-only: the model in the real checkpoint's per-layer formats (layer l %% 4: "
+                         "Q5_K or IQ4_XS attention V/O, IQ2_S or IQ2_XS gate/up, IQ3_XXS, IQ4_XS or IQ3_S down)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-sized device buffer (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -203,6 +206,8 @@ def main():
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
+    if args.real_mix and not args.prefill_only:
+        sys.exit("--real-mix measures the prefill leg only (use it with --prefill-only)")
     import qxg
 
     prompt_len = 8
@@ -212,7 +217,7 @@ def main():
     prompt = np.random.default_rng(args.seed).integers(0, VOCAB, size=prompt_len).astype(np.uint32)
 
     t0 = time.perf_counter()
-    model = qxg.MemModel(LAYERS, VOCAB, EXPERTS, True, True, seed=args.seed)
+    model = qxg.MemModel(LAYERS, VOCAB, EXPERTS, True, True, seed=args.seed, mix=1 if args.real_mix else 0)
     log(f"generated the {LAYERS}-layer model in memory in {time.perf_counter() - t0:.1f} s ({model.path})")
     ctx = qxg.Context(0)
     ctx.set_layer_path(args.layer_path)
@@ -224,6 +229,9 @@ def main():
 
     if args.prefill_only:
         leg = prefill_leg(ctx, args)
+        if args.real_mix:
+            leg["quant_mix"] = ("real checkpoint per-layer formats: Q5_K/IQ4_XS attn V/O, IQ2_S/IQ2_XS gate/up, "
+                                "IQ3_XXS/IQ4_XS/IQ3_S down (layer l % 4)")
         ctx.close()
         model.close()
         print(json.dumps({"prefill": leg}), flush=True)

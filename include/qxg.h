@@ -190,9 +190,10 @@ int qxg_final_head(qxg_ctx *ctx, const float *residual, float *norm_out, float *
  * the last token.  Stands in for the reference's prompt steps, which run one token at a
  * time through the decode step with the head only on the last prompt token
  * (src/qx_format.c:6250-6547, sampling_step at 6253).  Chunks of 512 tokens run in
- * order.  Models with formats beyond IQ4_XS / IQ2_XS / IQ3_XXS, and the q8_k_compat
- * mode, take those token steps on the device instead (the decode kernels, one token at
- * a time: the result equals qxg_decode_token over the prompt).
+ * order; every per-layer format of the real checkpoint (IQ4_XS / Q5_K attention,
+ * IQ2_XS / IQ2_S gate/up, IQ3_XXS / IQ3_S / IQ4_XS down) runs batched.  The q8_k_compat
+ * mode takes those token steps on the device instead (the decode kernels, one token at a
+ * time: the result equals qxg_decode_token over the prompt).
  * residual_out (may be NULL): n*2048 floats, each token's residual after the
  * last layer.  logits / top_* as in qxg_decode_token.  elapsed_ms: device time of the
  * whole call (HIP events on the context stream). */

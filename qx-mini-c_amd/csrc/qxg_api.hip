@@ -620,7 +620,7 @@ uint16_t f16_int(int v) {
 // The batched GEMM path decodes the benchmark mix in the f32 activation mode; other
 // models and q8_k_compat prefill token by token through the decode kernels, which is
 // how the reference prefills every prompt.
-bool batched_prefill(const qxg_ctx *c) { return c->base_mix && !c->q8; }
+bool batched_prefill(const qxg_ctx *c) { return !c->q8; }
 
 bool prefill_ready(qxg_ctx *c, char *err, uint64_t n) {
     auto &B = c->pf;
@@ -653,12 +653,25 @@ bool prefill_ready(qxg_ctx *c, char *err, uint64_t n) {
     }
     for (uint32_t b = 0; b < 256; ++b)
         kv2[b] = (uint32_t)f16_int(qx_iq4nl_values[b & 15]) | ((uint32_t)f16_int(qx_iq4nl_values[b >> 4]) << 16);
+    // the real checkpoint's IQ2_S / IQ3_S grids as fp16, and sign masks of an explicit sign byte
+    std::vector<uint16_t> g2s(1024 * 8), g3s(512 * 4), sg8(256 * 8);
+    for (int i = 0; i < 1024; ++i)
+        for (int j = 0; j < 8; ++j) g2s[i * 8 + j] = f16_int(qx_iq2xs_levels[(qx_iq2s_packed[i] >> (2 * j)) & 3]);
+    for (int i = 0; i < 512; ++i)
+        for (int j = 0; j < 4; ++j) g3s[i * 4 + j] = f16_int(qx_iq3s_levels[(qx_iq3s_packed[i] >> (3 * j)) & 7]);
+    for (uint32_t i = 0; i < 256; ++i)
+        for (int j = 0; j < 8; ++j) sg8[i * 8 + j] = ((i >> j) & 1) ? 0x8000 : 0;
     ok = ok && alloc((void **)&B.P.g2h, g2.size() * 2) && alloc((void **)&B.P.g3h, g3.size() * 2) &&
-         alloc((void **)&B.P.sgn, sg.size() * 2) && alloc((void **)&B.P.kv2, kv2.size() * 4);
+         alloc((void **)&B.P.sgn, sg.size() * 2) && alloc((void **)&B.P.kv2, kv2.size() * 4) &&
+         alloc((void **)&B.P.g2sh, g2s.size() * 2) && alloc((void **)&B.P.g3sh, g3s.size() * 2) &&
+         alloc((void **)&B.P.sgn8, sg8.size() * 2);
     ok = ok && hip_ok(hipMemcpy(B.P.g2h, g2.data(), g2.size() * 2, hipMemcpyHostToDevice), err, n, "prefill tables") &&
          hip_ok(hipMemcpy(B.P.g3h, g3.data(), g3.size() * 2, hipMemcpyHostToDevice), err, n, "prefill tables") &&
          hip_ok(hipMemcpy(B.P.sgn, sg.data(), sg.size() * 2, hipMemcpyHostToDevice), err, n, "prefill tables") &&
-         hip_ok(hipMemcpy(B.P.kv2, kv2.data(), kv2.size() * 4, hipMemcpyHostToDevice), err, n, "prefill tables");
+         hip_ok(hipMemcpy(B.P.kv2, kv2.data(), kv2.size() * 4, hipMemcpyHostToDevice), err, n, "prefill tables") &&
+         hip_ok(hipMemcpy(B.P.g2sh, g2s.data(), g2s.size() * 2, hipMemcpyHostToDevice), err, n, "prefill tables") &&
+         hip_ok(hipMemcpy(B.P.g3sh, g3s.data(), g3s.size() * 2, hipMemcpyHostToDevice), err, n, "prefill tables") &&
+         hip_ok(hipMemcpy(B.P.sgn8, sg8.data(), sg8.size() * 2, hipMemcpyHostToDevice), err, n, "prefill tables");
     if (!ok) {
         for (void *p : B.all) (void)hipFree(p);
         B.all.clear();
@@ -668,7 +681,7 @@ bool prefill_ready(qxg_ctx *c, char *err, uint64_t n) {
     return true;
 }
 
-PfMat pf_mat(const QTensor *t) { return PfMat{t->p0, t->p1, t->d}; }
+PfMat pf_mat(const QTensor *t) { return PfMat{t->p0, t->p1, t->p2, t->d}; }
 
 // One layer over the T tokens of a chunk at positions p0..p0+T-1: pf.X -> pf.X (pf.X1
 // holds the attention half's result, the MoE input).  Asynchronous on c->s.
@@ -681,11 +694,20 @@ void prefill_layer(qxg_ctx *c, uint32_t l, uint32_t T, uint32_t p0, float *moe_d
     // attention half: RMSNorm, Q/K/V GEMM, q/k norm + RoPE + INT8 append, attention, O GEMM + residual
     hipLaunchKernelGGL(qxp_norm_pack, dim3(mt * 8), dim3(256), 0, s, (const float *)B.X, w.attn_norm, mt * 32, T, B.apk,
                        B.rscale);
+    // per-layer formats of the real checkpoint: V and O in Q5_K or IQ4_XS, gate/up in IQ2_S or
+    // IQ2_XS, down in IQ3_XXS, IQ3_S or IQ4_XS (type ids of the QXF1 manifest)
+    const bool vo_q5 = w.wv->type == 13, gu_s = w.gate->type == 22;
+    const int dn_kind = w.down->type == 21 ? QXP_DOWN_IQ3S : w.down->type == 23 ? QXP_DOWN_IQ4 : QXP_DOWN;
     PfGemm g{};
     g.w[0] = pf_mat(w.wq); g.w[1] = pf_mat(w.wk); g.w[2] = pf_mat(w.wv);
-    g.w_start[0] = 0; g.w_start[1] = 4096; g.w_start[2] = 4608;
+    g.w_start[0] = 0; g.w_start[1] = 4096; g.w_start[2] = vo_q5 ? none : 4608;
     g.kb = 8; g.apk = B.apk; g.rscale = B.rscale; g.mtiles = mt; g.nvalid = T; g.out = B.QKV; g.ld = 5120;
-    qxp_launch_gemm(s, 0, g, B.P, 5120 / 128, mt, timer_for(c, 8));
+    qxp_launch_gemm(s, QXP_QKV, g, B.P, (vo_q5 ? 4608 : 5120) / 128, mt, timer_for(c, 8));
+    if (vo_q5) {   // V (Q5_K) into columns 4608..5119
+        PfGemm gv = g;
+        gv.w[0] = pf_mat(w.wv); gv.w_start[1] = none; gv.w_start[2] = none; gv.out = B.QKV + 4608;
+        qxp_launch_gemm(s, QXP_V_Q5, gv, B.P, 512 / 128, mt, Timer{});
+    }
     hipLaunchKernelGGL(qxp_qk, dim3(T), dim3(256), 0, s, (const float *)B.QKV, w.q_norm, w.k_norm, c->T, c->kc, c->vc,
                        c->ks, c->vs, l, c->kv_ctx, p0, B.QR);
     qx_launch(qxp_attn, dim3(4, (T + 3) / 4), dim3(256), 0, s, timer_for(c, 13), (const float *)B.QR,
@@ -696,7 +718,7 @@ void prefill_layer(qxg_ctx *c, uint32_t l, uint32_t T, uint32_t p0, float *moe_d
     g.w[0] = pf_mat(w.wo); g.w_start[1] = none; g.w_start[2] = none;
     g.kb = 16; g.apk = B.apk; g.rscale = B.rscale; g.mtiles = mt; g.nvalid = T; g.out = B.X1; g.ld = 2048;
     g.resid = B.X;
-    qxp_launch_gemm(s, 1, g, B.P, 2048 / 128, mt, timer_for(c, 9));
+    qxp_launch_gemm(s, vo_q5 ? QXP_O_Q5 : QXP_O, g, B.P, 2048 / 128, mt, timer_for(c, 9));
     // MoE half: RMSNorm, router logits, top-8, grouping by expert, gate/up + SwiGLU, down, combine
     hipLaunchKernelGGL(qxp_norm, dim3((T + 3) / 4), dim3(256), 0, s, (const float *)B.X1, w.ffn_norm, T, B.XN);
     qx_launch(qxp_router, dim3((T + 15) / 16, (E + 15) / 16), dim3(512), 0, s, timer_for(c, 12), (const float *)B.XN,
@@ -711,13 +733,13 @@ void prefill_layer(qxg_ctx *c, uint32_t l, uint32_t T, uint32_t p0, float *moe_d
     g.w[0] = pf_mat(w.gate); g.w[1] = pf_mat(w.up); g.w_start[1] = none; g.w_start[2] = none;
     g.rows = QXG_FFN; g.kb = 8; g.apk = B.apk; g.rscale = B.rscale; g.mgroups = B.mgroups; g.meta = B.meta;
     g.out = B.H; g.ld = QXG_FFN;
-    qxp_launch_gemm(s, 2, g, B.P, QXG_FFN / 128, mg_ub, timer_for(c, 10));
+    qxp_launch_gemm(s, gu_s ? QXP_GU_IQ2S : QXP_GU, g, B.P, QXG_FFN / 128, mg_ub, timer_for(c, 10));
     qxp_launch_pack(s, 768, B.H, nullptr, B.meta, slots_ub, none, B.apk, B.rscale);
     g = PfGemm{};
     g.w[0] = pf_mat(w.down); g.w_start[1] = none; g.w_start[2] = none;
     g.rows = 2048; g.kb = 3; g.apk = B.apk; g.rscale = B.rscale; g.mgroups = B.mgroups; g.meta = B.meta;
     g.out = B.Y; g.ld = 2048;
-    qxp_launch_gemm(s, 3, g, B.P, 2048 / 128, mg_ub, timer_for(c, 11));
+    qxp_launch_gemm(s, dn_kind, g, B.P, 2048 / 128, mg_ub, timer_for(c, 11));
     hipLaunchKernelGGL(qxp_combine, dim3(T), dim3(256), 0, s, (const float *)B.X1, (const float *)B.Y,
                        (const uint32_t *)B.tok_slot, (const double *)B.w, B.X, moe_dump);
 }

@@ -176,12 +176,16 @@ struct PfTables {
     uint2 *g3h;      // IQ3_XXS grid: 256 x 4 fp16 values
     uint4 *sgn;      // 7-bit sign index -> 8 fp16 sign masks (0x8000 where negative)
     uint32_t *kv2;   // IQ4_XS byte -> {fp16 kvalue[low nibble], fp16 kvalue[high nibble]}
+    uint4 *g2sh;     // IQ2_S grid: 1024 x 8 fp16 values
+    uint2 *g3sh;     // IQ3_S grid: 512 x 4 fp16 values
+    uint4 *sgn8;     // sign byte -> 8 fp16 sign masks (IQ2_S, IQ3_S)
 };
 
 // One quantized matrix [rows x K] in the repacked layout (expert e's rows follow e*rows).
 struct PfMat {
-    const uint8_t *qs, *p1;   // qs plane; IQ4_XS meta / IQ2_XS scales / IQ3_XXS aux
-    const uint16_t *d;        // fp16 d per block (IQ2_XS, IQ3_XXS)
+    const uint8_t *qs, *p1;   // qs plane; IQ4_XS / Q5_K meta, IQ2_XS / IQ2_S scales, IQ3_XXS aux, IQ3_S signs
+    const uint8_t *p2;        // Q5_K qh, IQ2_S qh, IQ3_S {qh, scales}
+    const uint16_t *d;        // fp16 d per block (IQ2_XS, IQ3_XXS, IQ2_S, IQ3_S)
 };
 
 // Arguments of one prefill GEMM launch: Y[row][col] = sum_k A[row][k] * W[col][k], A the
@@ -202,6 +206,11 @@ struct PfGemm {
     const float *resid;        // residual added by the O projection epilogue
     float *dump;               // O projection output without the residual (optional)
     uint32_t xcd_rows;         // row-tile classes across the 8 XCDs (1, 2, 4 or 8; the launcher sets it)
+};
+// GEMM kinds of qxp_launch_gemm (format and epilogue of the weight matrix)
+enum QxpGemmKind : int {
+    QXP_QKV = 0, QXP_O = 1, QXP_GU = 2, QXP_DOWN = 3,              // the benchmark mix
+    QXP_V_Q5 = 4, QXP_O_Q5 = 5, QXP_GU_IQ2S = 6, QXP_DOWN_IQ3S = 7, QXP_DOWN_IQ4 = 8   // real-checkpoint layers
 };
 
 // Optional start/stop events recorded around one launch on its stream.  Created with

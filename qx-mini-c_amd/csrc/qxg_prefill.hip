@@ -30,7 +30,7 @@ typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 
-enum { FMT_IQ4 = 0, FMT_IQ2 = 1, FMT_IQ3 = 2 };
+enum { FMT_IQ4 = 0, FMT_IQ2 = 1, FMT_IQ3 = 2, FMT_Q5 = 3, FMT_IQ2S = 4, FMT_IQ3S = 5 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 
 DEV f16x mfma(uint4 a, uint4 b, f16x c) {
@@ -52,6 +52,9 @@ template <int F> struct Blk;
 template <> struct Blk<FMT_IQ2> { uint4 q[4]; uint2 sc; uint32_t d; };    // qs (32 x u16), scales, d
 template <> struct Blk<FMT_IQ3> { uint4 q[4]; uint4 a[2]; uint32_t d; };  // qs (64 x u8), aux (8 x u32), d
 template <> struct Blk<FMT_IQ4> { uint2 q[8]; uint2 m; };                 // qs bytes 16ib+8h..+8, meta
+template <> struct Blk<FMT_Q5> { uint2 q[8]; uint2 qh[2]; uint4 m; };     // qs 32p+16t+8h..+8, qh 16t+8h..+8, meta
+template <> struct Blk<FMT_IQ2S> { uint4 g[2], sg[2]; uint2 qh, sc; uint32_t d; };   // grid, sign, qh, scale bytes
+template <> struct Blk<FMT_IQ3S> { uint4 q[4], sg[2], hs; uint32_t d; };  // grid, sign bytes, {qh[8], scales[4]}
 
 DEV void blk_load(Blk<FMT_IQ2> &b, const PfMat &w, uint64_t bi, int) {
     const uint4 *p = reinterpret_cast<const uint4 *>(w.qs + bi * 64);
@@ -72,6 +75,32 @@ DEV void blk_load(Blk<FMT_IQ4> &b, const PfMat &w, uint64_t bi, int h) {
     for (int ib = 0; ib < 8; ++ib) b.q[ib] = *reinterpret_cast<const uint2 *>(q + 16 * ib);
     b.m = *reinterpret_cast<const uint2 *>(w.p1 + bi * 8);
 }
+
+DEV void blk_load(Blk<FMT_Q5> &b, const PfMat &w, uint64_t bi, int h) {
+    const uint8_t *q = w.qs + bi * 128 + 8 * h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b.q[i] = *reinterpret_cast<const uint2 *>(q + 32 * (i >> 1) + 16 * (i & 1));
+    b.qh[0] = *reinterpret_cast<const uint2 *>(w.p2 + bi * 32 + 8 * h);
+    b.qh[1] = *reinterpret_cast<const uint2 *>(w.p2 + bi * 32 + 16 + 8 * h);
+    b.m = *reinterpret_cast<const uint4 *>(w.p1 + bi * 16);
+}
+DEV void blk_load(Blk<FMT_IQ2S> &b, const PfMat &w, uint64_t bi, int) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(w.qs + bi * 64);
+    b.g[0] = p[0]; b.g[1] = p[1]; b.sg[0] = p[2]; b.sg[1] = p[3];
+    b.qh = *reinterpret_cast<const uint2 *>(w.p2 + bi * 8);
+    b.sc = *reinterpret_cast<const uint2 *>(w.p1 + bi * 8);
+    b.d = w.d[bi];
+}
+DEV void blk_load(Blk<FMT_IQ3S> &b, const PfMat &w, uint64_t bi, int) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(w.qs + bi * 64);
+    b.q[0] = p[0]; b.q[1] = p[1]; b.q[2] = p[2]; b.q[3] = p[3];
+    const uint4 *g = reinterpret_cast<const uint4 *>(w.p1 + bi * 32);
+    b.sg[0] = g[0]; b.sg[1] = g[1];
+    b.hs = *reinterpret_cast<const uint4 *>(w.p2 + bi * 16);
+    b.d = w.d[bi];
+}
+DEV uint32_t byte_of(const uint4 (&v)[2], uint32_t i) { return (comp(v[i >> 4], (i >> 2) & 3) >> (8 * (i & 3))) & 255u; }
+DEV uint32_t byte_of4(const uint4 (&v)[4], uint32_t i) { return (comp(v[i >> 4], (i >> 2) & 3) >> (8 * (i & 3))) & 255u; }
 
 // B fragment of k-step s (8 fp16 codes).  IQ2_XS (src/qx_format.c:1914-1933): element
 // 32ib+8l+j = db(l<2 ? lo : hi nibble of scales[ib]) * grid[q&511][j] * sign, q = qs[4ib+l];
@@ -112,6 +141,53 @@ DEV uint4 frag(const Blk<FMT_IQ4> &b, int s, int, const uint4 *, const uint4 *, 
     const uint32_t sel = (s & 1) ? 0x07060302u : 0x05040100u;
     return make_uint4(perm(p[1], p[0], sel), perm(p[3], p[2], sel), perm(p[5], p[4], sel), perm(p[7], p[6], sel));
 }
+// Q5_K (src/qx_format.c:2112-2145): element 32ib+l has the 5-bit code (nibble ib&1 of
+// qs[32(ib/2)+l]) | (bit ib of qh[l]) << 4 and w = d*sc*code - dmin*m; k-step s = 2ib + t
+// takes l = 16t + 8h + j.  Codes 0..31 go to fp16 exactly as bits(1024 + c) - 1024.
+DEV uint32_t u8pair_h2(uint32_t w4, bool hi) {
+    const h2v v = __builtin_bit_cast(h2v, perm(0u, w4, hi ? 0x0c030c02u : 0x0c010c00u) | 0x64006400u);
+    const h2v k = {(_Float16)1024.0f, (_Float16)1024.0f};
+    return __builtin_bit_cast(uint32_t, v - k);
+}
+DEV uint4 frag(const Blk<FMT_Q5> &b, int s, int, const uint4 *, const uint4 *, const uint32_t *) {
+    const int ib = s >> 1, t = s & 1;
+    const uint2 q = b.q[2 * (ib >> 1) + t], qh = b.qh[t];
+    const uint32_t nsh = 4 * (ib & 1);
+    const uint32_t c0 = ((q.x >> nsh) & 0x0f0f0f0fu) | (((qh.x >> ib) & 0x01010101u) << 4);
+    const uint32_t c1 = ((q.y >> nsh) & 0x0f0f0f0fu) | (((qh.y >> ib) & 0x01010101u) << 4);
+    return make_uint4(u8pair_h2(c0, false), u8pair_h2(c0, true), u8pair_h2(c1, false), u8pair_h2(c1, true));
+}
+// IQ2_S (src/qx_format.c:1961-1984): entry e = 4ib + l (l = 2t + h) of the block: grid
+// index qs[e] | ((qh[ib] >> 2l) & 3) << 8, explicit sign byte qs[32 + e], halves scaled by
+// the nibble t of scales[ib] as IQ2_XS.
+DEV uint4 frag(const Blk<FMT_IQ2S> &b, int s, int h, const uint4 *G2S, const uint4 *SG8, const uint32_t *) {
+    const int ib = s >> 1, t = s & 1, l = 2 * t + h;
+    const uint32_t e = 4 * ib + l;
+    const uint32_t qh = ((ib < 4 ? b.qh.x : b.qh.y) >> (8 * (ib & 3))) & 255u;
+    const uint32_t idx = byte_of(b.g, e) | (((qh >> (2 * l)) & 3u) << 8);
+    uint4 g = G2S[idx];
+    const uint4 m = SG8[byte_of(b.sg, e)];
+    g.x ^= m.x; g.y ^= m.y; g.z ^= m.z; g.w ^= m.w;
+    const uint32_t scb = ((ib < 4 ? b.sc.x : b.sc.y) >> (8 * (ib & 3))) & 255u;
+    return hmul8(g, 2u * ((scb >> (4 * t)) & 15u) + 1u);
+}
+// IQ3_S (src/qx_format.c:1986-2030): k-step s = 2ib + t, lane half h: grid entries
+// e = 8ib + 4t + 2h + {0, 1} (4 values each), index qs[e] | (bit e%8 of qh[ib]) << 8, sign
+// byte signs[4ib + 2t + h], scale d*(2 sc + 1), sc the nibble ib&1 of scales[ib/2].
+DEV uint4 frag(const Blk<FMT_IQ3S> &b, int s, int h, const uint4 *, const uint4 *SG8, const uint32_t *G3S) {
+    const int ib = s >> 1, t = s & 1;
+    const uint32_t e = 8 * ib + 4 * t + 2 * h;
+    const uint32_t qh = (comp(b.hs, ib >> 2) >> (8 * (ib & 3))) & 255u;
+    const uint32_t i1 = byte_of4(b.q, e) | (((qh >> (e & 7)) & 1u) << 8);
+    const uint32_t i2 = byte_of4(b.q, e + 1) | (((qh >> ((e + 1) & 7)) & 1u) << 8);
+    const uint2 g1 = reinterpret_cast<const uint2 *>(G3S)[i1];
+    const uint2 g2 = reinterpret_cast<const uint2 *>(G3S)[i2];
+    const uint4 m = SG8[byte_of(b.sg, 4 * ib + 2 * t + h)];
+    const uint4 g = make_uint4(g1.x ^ m.x, g1.y ^ m.y, g2.x ^ m.z, g2.y ^ m.w);
+    const uint32_t scw = (b.hs.z >> (8 * (ib >> 1))) & 255u;
+    return hmul8(g, 2u * ((scw >> (4 * (ib & 1))) & 15u) + 1u);
+}
+
 // f32 scale of the partial sums: the block's d/8 or d/4; IQ4_XS: group ib's d*(ls-32)
 DEV float blk_scale(const Blk<FMT_IQ2> &b, int) { return fp16_exact(b.d) * 0.125f; }
 DEV float blk_scale(const Blk<FMT_IQ3> &b, int) { return fp16_exact(b.d) * 0.25f; }
@@ -119,6 +195,31 @@ DEV float blk_scale(const Blk<FMT_IQ4> &b, int ib) {
     const uint32_t sh = b.m.x >> 16, sl = (b.m.y >> (8 * (ib >> 1))) & 255u;
     const int ls = (int)(((sl >> (4 * (ib & 1))) & 15u) | (((sh >> (2 * ib)) & 3u) << 4));
     return fp16_exact(b.m.x & 0xffffu) * (float)(ls - 32);
+}
+DEV float blk_scale(const Blk<FMT_IQ2S> &b, int) { return fp16_exact(b.d) * 0.125f; }
+DEV float blk_scale(const Blk<FMT_IQ3S> &b, int) { return fp16_exact(b.d); }
+// Q5_K sub-block ib: scale d*sc and offset dmin*m (6-bit sc, m: get_scale_min_k4,
+// src/qx_format.c:2079-2087); meta = {d, dmin, scales[12]}
+DEV uint32_t q5_scale_byte(const uint4 &m, int i) { return (comp(m, 1 + (i >> 2)) >> (8 * (i & 3))) & 255u; }
+DEV void q5_sc_m(const Blk<FMT_Q5> &b, int ib, uint32_t &sc, uint32_t &mn) {
+    if (ib < 4) {
+        sc = q5_scale_byte(b.m, ib) & 63u;
+        mn = q5_scale_byte(b.m, ib + 4) & 63u;
+    } else {
+        sc = (q5_scale_byte(b.m, ib + 4) & 15u) | ((q5_scale_byte(b.m, ib - 4) >> 6) << 4);
+        mn = (q5_scale_byte(b.m, ib + 4) >> 4) | ((q5_scale_byte(b.m, ib) >> 6) << 4);
+    }
+}
+DEV float blk_scale(const Blk<FMT_Q5> &b, int ib) {
+    uint32_t sc, mn;
+    q5_sc_m(b, ib, sc, mn);
+    return fp16_exact(b.m.x & 0xffffu) * (float)sc;
+}
+template <int F> DEV float blk_offset(const Blk<F> &, int) { return 0.0f; }
+DEV float blk_offset(const Blk<FMT_Q5> &b, int ib) {
+    uint32_t sc, mn;
+    q5_sc_m(b, ib, sc, mn);
+    return fp16_exact(b.m.x >> 16) * (float)mn;
 }
 
 DEV f16x zero16() {
@@ -169,17 +270,24 @@ DEV void a_store(const v4u (&ra)[NM * 8], uint4 *stage, int tid) {
 template <int F, int NSUB, int NM>
 DEV void block_mma(const Blk<F> (&bk)[NSUB], const uint4 *sa, f16x (&acc)[NSUB][NM], const GemmLds &L, int h,
                    int lane) {
-    constexpr int NG = F == FMT_IQ4 ? 8 : 1;
-    float scl[NSUB][NG];
+    constexpr bool PER32 = F == FMT_IQ4 || F == FMT_Q5;   // a scale per 32-value group
+    constexpr int NG = PER32 ? 8 : 1;
+    float scl[NSUB][NG], ofs[NSUB][NG];
 #pragma unroll
     for (int n = 0; n < NSUB; ++n)
 #pragma unroll
-        for (int q = 0; q < NG; ++q) scl[n][q] = blk_scale(bk[n], q);
+        for (int q = 0; q < NG; ++q) {
+            scl[n][q] = blk_scale(bk[n], q);
+            ofs[n][q] = F == FMT_Q5 ? blk_offset(bk[n], q) : 0.0f;
+        }
     f16x G[NSUB][NM];
+    f16x S[NM];   // Q5_K: sums of the activations over the group (B = all ones), for the dmin term
 #pragma unroll
     for (int n = 0; n < NSUB; ++n)
 #pragma unroll
         for (int m = 0; m < NM; ++m) G[n][m] = zero16();
+#pragma unroll
+    for (int m = 0; m < NM; ++m) S[m] = zero16();
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
         uint4 ah[NM], al[NM];
@@ -187,6 +295,14 @@ DEV void block_mma(const Blk<F> (&bk)[NSUB], const uint4 *sa, f16x (&acc)[NSUB][
         for (int m = 0; m < NM; ++m) {
             ah[m] = sa[m * 2048 + s * 128 + lane];
             al[m] = sa[m * 2048 + s * 128 + 64 + lane];
+        }
+        if (F == FMT_Q5) {
+            const uint4 ones = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);   // fp16 1.0
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                S[m] = mfma(ah[m], ones, S[m]);
+                S[m] = mfma(al[m], ones, S[m]);
+            }
         }
 #pragma unroll
         for (int n = 0; n < NSUB; ++n) {
@@ -197,21 +313,27 @@ DEV void block_mma(const Blk<F> (&bk)[NSUB], const uint4 *sa, f16x (&acc)[NSUB][
                 G[n][m] = mfma(al[m], b, G[n][m]);
             }
         }
-        if (F == FMT_IQ4 && (s & 1)) {
+        if (PER32 && (s & 1)) {
 #pragma unroll
             for (int n = 0; n < NSUB; ++n)
 #pragma unroll
                 for (int m = 0; m < NM; ++m) {
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[n][m][r] = fmaf(scl[n][s >> 1], G[n][m][r], acc[n][m][r]);
+                    for (int r = 0; r < 16; ++r) {
+                        acc[n][m][r] = fmaf(scl[n][s >> 1], G[n][m][r], acc[n][m][r]);
+                        if (F == FMT_Q5) acc[n][m][r] = fmaf(-ofs[n][s >> 1], S[m][r], acc[n][m][r]);
+                    }
                     G[n][m] = zero16();
                 }
+            if (F == FMT_Q5)
+#pragma unroll
+                for (int m = 0; m < NM; ++m) S[m] = zero16();
         }
         // LDS reads of later k-steps stay behind this point: the unrolled loop would
         // otherwise hoist all of them into registers
         if (s & 1) asm volatile("" ::: "memory");
     }
-    if (F != FMT_IQ4) {
+    if (!PER32) {
 #pragma unroll
         for (int n = 0; n < NSUB; ++n)
 #pragma unroll
@@ -346,16 +468,23 @@ __global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void qxp_gemm(PfGemm g, PfTab
         if (mt0 >= g.mtiles) return;   // whole workgroup: a padding row
         nmt = min((uint32_t)MT, g.mtiles - mt0);
     }
-    __shared__ uint4 s_g2[F == FMT_IQ2 ? 512 : 1];
-    __shared__ uint4 s_sg[F == FMT_IQ4 ? 1 : 128];
-    __shared__ uint32_t s_t[F == FMT_IQ3 ? 512 : F == FMT_IQ4 ? 256 : 1];
+    constexpr int NG2 = F == FMT_IQ2 ? 512 : F == FMT_IQ2S ? 1024 : 1;        // fp16 grid entries of 8
+    constexpr int NSG = F == FMT_IQ2 || F == FMT_IQ3 ? 128 : F == FMT_IQ2S || F == FMT_IQ3S ? 256 : 1;   // sign masks
+    constexpr int NT4 = F == FMT_IQ3 ? 512 : F == FMT_IQ3S ? 1024 : F == FMT_IQ4 ? 256 : 1;   // words
+    __shared__ uint4 s_g2[NG2];
+    __shared__ uint4 s_sg[NSG];
+    __shared__ uint32_t s_t[NT4];
     __shared__ uint4 s_a[2 * MT * 2048];   // [stage][row tile][(kstep*2 + piece)*64 + lane]
     const int tid = threadIdx.x;
-    if (F == FMT_IQ2) { s_g2[tid] = P.g2h[tid]; s_g2[tid + 256] = P.g2h[tid + 256]; }
-    if (F != FMT_IQ4 && tid < 128) s_sg[tid] = P.sgn[tid];
-    if (F == FMT_IQ3) { s_t[tid] = reinterpret_cast<const uint32_t *>(P.g3h)[tid];
-                        s_t[tid + 256] = reinterpret_cast<const uint32_t *>(P.g3h)[tid + 256]; }
-    if (F == FMT_IQ4) s_t[tid] = P.kv2[tid];
+    {
+        const uint4 *g2 = F == FMT_IQ2S ? P.g2sh : P.g2h;
+        const uint4 *sg = F == FMT_IQ2S || F == FMT_IQ3S ? P.sgn8 : P.sgn;
+        const uint32_t *t4 = F == FMT_IQ3 ? reinterpret_cast<const uint32_t *>(P.g3h)
+                           : F == FMT_IQ3S ? reinterpret_cast<const uint32_t *>(P.g3sh) : P.kv2;
+        if (NG2 > 1) for (int i = tid; i < NG2; i += 256) s_g2[i] = g2[i];
+        if (NSG > 1) for (int i = tid; i < NSG; i += 256) s_sg[i] = sg[i];
+        if (NT4 > 1) for (int i = tid; i < NT4; i += 256) s_t[i] = t4[i];
+    }
     const GemmLds L{s_g2, s_sg, s_a, s_t, MT * 2048};
     if (MT == 2 && nmt == 2) gemm_body<F, NSUB, (MT == 2 ? 2 : 1), EPI>(g, L, e, mt0, bx);
     else gemm_body<F, NSUB, 1, EPI>(g, L, e, mt0, bx);
@@ -898,22 +1027,36 @@ void qxp_launch_gemm(hipStream_t s, int kind, const PfGemm &g0, const PfTables &
     // O 4 (8 MB, 4.5 MB), experts 8 (an expert tile's activations in one L2; its weights
     // are read by that tile only)
     PfGemm g = g0;
-    g.xcd_rows = kind == 0 ? 2u : kind == 1 ? 4u : 8u;
+    g.xcd_rows = kind == QXP_QKV || kind == QXP_V_Q5 ? 2u : kind == QXP_O || kind == QXP_O_Q5 ? 4u : 8u;
     const uint32_t b = 8u / g.xcd_rows;
     if (grid_x % b) g.xcd_rows = 8u;   // (the column counts here are multiples of 8 workgroups)
     grid_y = (grid_y + g.xcd_rows - 1) / g.xcd_rows * g.xcd_rows;
+    const dim3 grid(grid_x, grid_y);
     switch (kind) {
-    case 0:   // Q/K/V: IQ4_XS, 32 columns per wave
-        qx_launch(qxp_gemm<FMT_IQ4, 1, 1, EPI_STORE>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+    case QXP_QKV:       // Q/K/V (or Q/K): IQ4_XS, 32 columns per wave
+    case QXP_DOWN_IQ4:  // expert down, IQ4_XS (the kernel reads the expert groups from g)
+        qx_launch(qxp_gemm<FMT_IQ4, 1, 1, EPI_STORE>, grid, dim3(256), 0, s, tm, g, P);
         break;
-    case 1:   // O projection + residual: IQ4_XS, 32 columns per wave
-        qx_launch(qxp_gemm<FMT_IQ4, 1, 1, EPI_RESID>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+    case QXP_O:         // O projection + residual: IQ4_XS
+        qx_launch(qxp_gemm<FMT_IQ4, 1, 1, EPI_RESID>, grid, dim3(256), 0, s, tm, g, P);
         break;
-    case 2:   // expert gate/up + SwiGLU: IQ2_XS
-        qx_launch(qxp_gemm<FMT_IQ2, 2, QXG_PF_EXPERT_MT, EPI_SWIGLU>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+    case QXP_GU:        // expert gate/up + SwiGLU: IQ2_XS
+        qx_launch(qxp_gemm<FMT_IQ2, 2, QXG_PF_EXPERT_MT, EPI_SWIGLU>, grid, dim3(256), 0, s, tm, g, P);
         break;
-    default:  // expert down: IQ3_XXS, 32 columns per wave
-        qx_launch(qxp_gemm<FMT_IQ3, 1, QXG_PF_EXPERT_MT, EPI_STORE>, dim3(grid_x, grid_y), dim3(256), 0, s, tm, g, P);
+    case QXP_DOWN:      // expert down: IQ3_XXS
+        qx_launch(qxp_gemm<FMT_IQ3, 1, QXG_PF_EXPERT_MT, EPI_STORE>, grid, dim3(256), 0, s, tm, g, P);
+        break;
+    case QXP_V_Q5:      // V alone: Q5_K
+        qx_launch(qxp_gemm<FMT_Q5, 1, 1, EPI_STORE>, grid, dim3(256), 0, s, tm, g, P);
+        break;
+    case QXP_O_Q5:      // O projection + residual: Q5_K
+        qx_launch(qxp_gemm<FMT_Q5, 1, 1, EPI_RESID>, grid, dim3(256), 0, s, tm, g, P);
+        break;
+    case QXP_GU_IQ2S:   // expert gate/up + SwiGLU: IQ2_S
+        qx_launch(qxp_gemm<FMT_IQ2S, 2, QXG_PF_EXPERT_MT, EPI_SWIGLU>, grid, dim3(256), 0, s, tm, g, P);
+        break;
+    default:            // expert down: IQ3_S
+        qx_launch(qxp_gemm<FMT_IQ3S, 1, QXG_PF_EXPERT_MT, EPI_STORE>, grid, dim3(256), 0, s, tm, g, P);
         break;
     }
 }

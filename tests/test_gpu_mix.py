@@ -88,25 +88,78 @@ def test_mix_decode_greedy(ctx, mix_model):
         assert list(gen) == toks, rep
 
 
-def test_mix_prefill_token_steps(ctx, mix_model):
-    """The batched GEMMs decode the benchmark mix only; this model prefills token by token
-    through the decode kernels (as the reference prefills every prompt), so the result
-    equals decoding the prompt step by step, bit for bit."""
+@pytest.mark.parametrize("layer", [0, 1, 2, 3])
+def test_mix_prefill_layer_replay(ctx, mix_model, layer):
+    """The batched prefill GEMMs on every per-layer format combination: Q5_K V and O (the
+    dmin term through a pass over an all-ones operand), IQ2_S gate/up, IQ4_XS or IQ3_S down.
+    40 tokens through the layer at positions 20..59 (earlier positions hold seeded INT8
+    rows), rows 1000x apart in magnitude; each token's attention recomputed by the oracle
+    over the GPU's own cache rows (its own row included), the MoE half replayed by the
+    oracle on the GPU's own ffn input (1e-5 per row)."""
     ctx.load(mix_model)
-    prompt = np.array([29, 4000, 7, 123, 2048], np.uint32)
-    ctx.kv_create(4, 16)
-    res, lg, ids, tl, _ = ctx.prefill(prompt, 0, True, 4, want_residual=True, want_logits=True)
-    ctx.kv_create(4, 16)
-    for s, tok in enumerate(prompt):
-        r, _, l2, i2, _ = ctx.decode_token(int(tok), s, s == len(prompt) - 1, 4, want_logits=True)
-        assert np.array_equal(res[s], r), s
-    assert np.array_equal(lg, l2) and list(ids) == list(i2)
-    # the same-input layer seam takes the same route: each row's attention and MoE halves
-    x = np.random.default_rng(3).standard_normal((3, 2048)).astype(np.float32)
-    ctx.kv_create(4, 16)
-    fi, moe, out = ctx.prefill_layer(1, 0, x)
-    ctx.kv_create(4, 16)
-    for t in range(3):
-        a, _, _ = ctx.attention_layer(1, t, x[t])
-        y, m, _, _ = ctx.moe_layer(1, x[t] + a)
-        assert np.array_equal(fi[t], x[t] + a) and np.array_equal(moe[t], m) and np.array_equal(out[t], y), t
+    n, p0 = 40, 20
+    ctx.kv_create(4, 128)
+    okv = qxo.KV(4, 128)
+    k, v, ks, vs = seeded_kv(90 + layer, p0)
+    ctx.kv_write(layer, 0, k, v, ks, vs)
+    okv.k[layer, :p0], okv.v[layer, :p0], okv.ks[layer, :p0], okv.vs[layer, :p0] = k, v, ks, vs
+    x = np.random.default_rng(300 + layer).standard_normal((n, 2048)).astype(np.float32)
+    x[3] *= 1e-3
+    x[5] *= 300.0
+    fi, moe, out = ctx.prefill_layer(layer, p0, x)
+    gk, gv, gks, gvs = ctx.kv_read(layer, p0, n)
+    okv.k[layer, p0:p0 + n], okv.v[layer, p0:p0 + n], okv.ks[layer, p0:p0 + n], okv.vs[layer, p0:p0 + n] = gk, gv, gks, gvs
+    om = qxo.Model(mix_model)
+    for t in range(n):
+        # token t's attention by the oracle over the GPU's own cache rows, its own included;
+        # the oracle's row for the token: codes within 1 (inputs within 1e-7), scales 1e-5
+        a, _, _, rk, rv, (sk, sv) = qxo.attention_layer_given_row(om, layer, p0 + t, okv, x[t])
+        assert rel_l2(fi[t], x[t] + a) <= REL_L2, (layer, t, rel_l2(fi[t], x[t] + a))
+        assert np.abs(gk[t].astype(int) - rk.astype(int)).max() <= 1, (layer, t)
+        assert np.abs(gv[t].astype(int) - rv.astype(int)).max() <= 1, (layer, t)
+        assert abs(gks[t] / sk - 1) < 1e-5 and abs(gvs[t] / sv - 1) < 1e-5, (layer, t)
+    for t in range(n):
+        y, m, _, _ = om.moe_layer(layer, fi[t])
+        assert rel_l2(moe[t], m) <= REL_L2, (layer, t, rel_l2(moe[t], m))
+        assert rel_l2(out[t], y) <= REL_L2, (layer, t)
+    om.close()
+
+
+def test_mix_prefill_vs_token_steps(ctx, mix_model):
+    """A 29-token prompt batched through the four mixed layers and the head, against the
+    oracle's token-by-token steps (residuals and logits 1e-4, top-k by the margin rule)."""
+    ctx.load(mix_model)
+    prompt = np.random.default_rng(12).integers(0, 4096, size=29).astype(np.uint32)
+    n = len(prompt)
+    ctx.kv_create(4, 64)
+    res, lg, ids, tl, _ = ctx.prefill(prompt, 0, True, 8, want_residual=True, want_logits=True)
+    om = qxo.Model(mix_model)
+    okv = qxo.KV(4, 64)
+    ores = np.zeros((n, 2048), np.float32)
+    for t in range(n):
+        r, _, olg, oids, _ = qxo.decode_token(om, int(prompt[t]), t, okv, 4, t == n - 1, 4096, 8)
+        ores[t] = r
+    om.close()
+    assert rel_l2(res, ores) <= 1e-4, rel_l2(res, ores)
+    assert rel_l2(lg, olg) <= 1e-4, rel_l2(lg, olg)
+    ok, why = topk_consistent(ids, oids, olg)
+    assert ok, why
+
+
+def test_mix_prefill_q8k_token_steps(mix_model):
+    """In the q8_k_compat mode the prompt still runs as device token steps (the batched GEMMs
+    compute in the f32 scheme), bit-identical to stepping it with decode_token."""
+    c = qxg.Context(0)
+    try:
+        c.set_activation("q8_k_compat")
+        c.load(mix_model)
+        prompt = np.array([29, 4000, 7, 123, 2048], np.uint32)
+        c.kv_create(4, 16)
+        res, lg, ids, tl, _ = c.prefill(prompt, 0, True, 4, want_residual=True, want_logits=True)
+        c.kv_create(4, 16)
+        for s, tok in enumerate(prompt):
+            r, _, l2, i2, _ = c.decode_token(int(tok), s, s == len(prompt) - 1, 4, want_logits=True)
+            assert np.array_equal(res[s], r), s
+        assert np.array_equal(lg, l2) and list(ids) == list(i2)
+    finally:
+        c.close()
