@@ -83,13 +83,11 @@ constexpr uint32_t XO_AM = XO_WT + 2 * XN_WT;
 constexpr uint32_t XO_END = XO_AM + 2 * XN_AM;
 
 #define GLB __attribute__((address_space(1)))
-DEV uint64_t xld(const GLB uint64_t *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 DEV void xst(GLB uint64_t *p, uint32_t ep, uint32_t bits) {
     __hip_atomic_store(p, ((uint64_t)ep << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 DEV void xstf(GLB uint64_t *p, uint32_t ep, float v) { xst(p, ep, __float_as_uint(v)); }
 DEV void st_coherent(GLB uint32_t *p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-DEV uint32_t ld_coherent(const GLB uint32_t *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 // The thread index as a value the compiler cannot hoist: each stage derives its lane
 // indices from its own copy, so they are recomputed where used (a few ALU ops) instead of
@@ -115,41 +113,6 @@ DEV bool keep_waiting(uint32_t &it, uint64_t deadline, const Ctl &c) {
     return true;
 }
 
-// Waits until words idx(i), i < n, all carry epoch ep and stores their payloads to dst[i];
-// threads 0 .. P-1 take words tid, tid + P, ... (K >= n / P each).  Reloads only stale
-// words.  Returns false on timeout/abort; the caller makes that block-uniform.
-template <int K, int P = 512, typename IDX>
-DEV bool poll(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, const Ctl &c) {
-    const int tid = tix();
-    constexpr int NT = P;
-    uint64_t w[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int i = tid + NT * k;
-        w[k] = i < n ? xld(base + idx(i)) : ((uint64_t)ep << 32);
-    }
-    const uint64_t deadline = wall_clock64() + c.timeout;
-    uint32_t it = 0;
-    bool ok = true;
-    for (;;) {
-        bool all = true;
-#pragma unroll
-        for (int k = 0; k < K; ++k) all = all && (uint32_t)(w[k] >> 32) == ep;
-        if (all) break;
-        if (!keep_waiting(it, deadline, c)) { ok = false; break; }
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-            const int i = tid + NT * k;
-            if (i < n && (uint32_t)(w[k] >> 32) != ep) w[k] = xld(base + idx(i));
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-        const int i = tid + NT * k;
-        if (i < n) dst[i] = (uint32_t)w[k];
-    }
-    return ok;
-}
 struct Ident {
     DEV int operator()(int i) const { return i; }
 };
@@ -382,15 +345,10 @@ template <typename T>
 DEV const GLB T *gp(const T *p) { return (const GLB T *)uni64((uint64_t)p); }
 template <typename T>
 DEV GLB T *gpw(T *p) { return (GLB T *)uni64((uint64_t)p); }
-DEV uint4 gnt4(const GLB uint8_t *b, uint32_t off) {
-    const u32x4 v = __builtin_nontemporal_load((const GLB u32x4 *)(b + off));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
 DEV uint2 gnt2(const GLB uint8_t *b, uint32_t off) {
     const u32x2 v = __builtin_nontemporal_load((const GLB u32x2 *)(b + off));
     return make_uint2(v.x, v.y);
 }
-DEV uint32_t gnt1(const GLB uint8_t *b, uint32_t off) { return __builtin_nontemporal_load((const GLB uint32_t *)(b + off)); }
 DEV float4 ldf4(const GLB uint8_t *b, uint32_t off) {
     const f32x4 v = *(const GLB f32x4 *)(b + off);
     return make_float4(v.x, v.y, v.z, v.w);
@@ -487,11 +445,6 @@ DEV void load_w8(const GLB uint8_t *p, float (&w)[8]) {
 // the 3 blocks)
 // Routed experts' rows, staged in LDS as whole 16-byte chunks.  A CU's vector-memory unit
 // spends about the same time per load instruction whatever its width, so the rows are
-// fetched with as few instructions as possible: every lane of a global_load_lds_dwordx4
-// takes one 16-byte chunk of a list of byte ranges (each range widened to 16-byte
-// alignment), and chunk c of the list lands at lds + 16 c.  A wave's lanes then read
-// their sub-blocks from LDS.
-DEV uint32_t ld_u16(const GLB uint8_t *b, uint32_t off) { return *(const GLB uint16_t *)(b + off); }
 // Gate/up of wave w's 3 units (3 consecutive rows r0.. of expert e): 3 * QXD_GU_UNIT =
 // 3552 contiguous bytes, chunks [0, 222) (4 instructions, 4 KB of LDS; lanes past 222 repeat
 // chunk 0).  In LDS unit uu sits at uu * QXD_GU_UNIT: gate qs +0, sc +512, d +576, up qs
@@ -1267,7 +1220,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             }
             // ---------------------------------------------------------- stage D
             {
-                const int tid = tix(), lane = tid & 63, wave = tid >> 6;
+                const int tid = tix(), lane = tid & 63;
                 // h and the 8 expert weights (hi, lo words)
                 if (!wait_xch2<7>(X, 6144 + 16, ep + 4, S.u.m.vin,
                                    [par](int i) { return i < 6144 ? (int)(XO_H + par * XN_H) + i : (int)(XO_WT + par * XN_WT) + i - 6144; }, S, ctl))

@@ -456,7 +456,7 @@ DEV void xcd_tile(uint32_t a, uint32_t &bx, uint32_t &by) {
 }
 
 template <int F, int NSUB, int MT, int EPI>
-__global__ __launch_bounds__(256, MT == 1 ? 2 : 1) void qxp_gemm(PfGemm g, PfTables P) {
+__global__ __launch_bounds__(256, MT == 1 && F != FMT_IQ2S ? 2 : 1) void qxp_gemm(PfGemm g, PfTables P) {   // (IQ2_S: 86 KB of LDS, one per CU)
     uint32_t e = 0, mt0, nmt, bx, by;
     xcd_tile(g.xcd_rows, bx, by);
     if (g.mgroups) {
