@@ -272,3 +272,35 @@ def test_decode_long_context_vs_oracle(dctx, tmp_path, p0):
         assert ok, why
         tok_g, tok_o = int(ids[0]), int(oids[0])
     om.close()
+
+
+@pytest.mark.parametrize("layers", [1, 3])
+def test_first_launch_of_fresh_context(tmp_path, layers):
+    """The persistent decode's exchange buffers start in a state of their own (no layer has
+    written them): the very first launch of a fresh context must read only what its own
+    layers wrote.  With 3 layers, layer 2 reads x's slot 0 in the first step, which layer
+    0 never writes.  Its residuals match the oracle's token steps and a later launch of the
+    same steps, bit for bit."""
+    p = tmp_path / f"fresh{layers}.qxf"
+    qxg.generate_model(p, layers=layers, vocab=1024, experts=16, seed=57 + layers)
+    prompt = [11, 500, 77]
+    c = qxg.Context(0)
+    try:
+        c.set_layer_path(1)
+        c.load(p)
+        c.kv_create(layers, 16)
+        first = [c.decode_token(t, s, s == 2, 4, want_layers=True) for s, t in enumerate(prompt)]
+        c.kv_create(layers, 16)
+        again = [c.decode_token(t, s, s == 2, 4, want_layers=True) for s, t in enumerate(prompt)]
+    finally:
+        c.close()
+    for s in range(3):
+        assert np.array_equal(first[s][0], again[s][0]) and np.array_equal(first[s][1], again[s][1]), s
+    om = qxo.Model(p)
+    okv = qxo.KV(layers, 16)
+    for s, t in enumerate(prompt):
+        r, lay, _, _, _ = qxo.decode_token(om, t, s, okv, layers, False, 1024, 4)
+        assert rel_l2(first[s][0], r) <= 1e-4, (s, rel_l2(first[s][0], r))
+        for l in range(layers):
+            assert rel_l2(first[s][1][l], lay[l]) <= 1e-4, (s, l)
+    om.close()
