@@ -39,17 +39,21 @@
 // gate/up and down rows right after the top-8.
 #include "qxg_dev.h"
 
-// Stage timestamps for development builds only (-DQXD_TRACE): on the last step, lane 0 of
-// each workgroup's wave 0 stores s_memrealtime (100 MHz) into
-// qxd_trace_buf[layer][point][workgroup]; read back with qxd_trace_read.
+// Stage timestamps for development builds only (-DQXD_TRACE): on the last step, one lane
+// per workgroup records s_memrealtime (100 MHz) for layers 20..23 and the head into LDS
+// (a global store would count in the wave's vmcnt and delay the next poll); after the step
+// loop the workgroup copies them to qxd_trace_buf[layer][point][workgroup], read back with
+// qxd_trace_read.
 #ifdef QXD_TRACE
 __device__ unsigned long long qxd_trace_buf[49][32][256];
 extern "C" int qxd_trace_read(unsigned long long *out) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(qxd_trace_buf), sizeof(qxd_trace_buf)) == hipSuccess;
 }
+#define QXD_TL_SLOT(layer) ((layer) >= 20 && (layer) < 24 ? (int)(layer) - 20 : (layer) == 48 ? 4 : -1)
 #define DMARKT(layer, point, thread)                                                                           \
     do {                                                                                                      \
-        if (last && (threadIdx.x == (thread))) qxd_trace_buf[layer][point][blockIdx.x] = __builtin_amdgcn_s_memrealtime(); \
+        const int sl_ = QXD_TL_SLOT(layer);                                                                   \
+        if (last && sl_ >= 0 && (threadIdx.x == (thread))) qxd_tl[sl_][point] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #define DMARK(layer, point) DMARKT(layer, point, 0)
 #else
@@ -864,6 +868,10 @@ DEV bool better(float v, uint32_t i, float bv, uint32_t bi) { return v > bv || (
 // ================================================================= kernel
 extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
     __shared__ DLds S;
+#ifdef QXD_TRACE
+    __shared__ unsigned long long qxd_tl[5][32];
+    if (threadIdx.x < 5 * 32) qxd_tl[threadIdx.x >> 5][threadIdx.x & 31] = 0ull;
+#endif
     // the arguments are read from an LDS copy where used (LDS reads are not hoisted across
     // the stage barriers, so the ~70 argument dwords are not all held in scalar registers)
     __shared__ QxDArgs a;
@@ -1339,6 +1347,13 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             __syncthreads();
         }
     }
+#ifdef QXD_TRACE
+    __syncthreads();
+    if (threadIdx.x < 5 * 32) {
+        const int sl = threadIdx.x >> 5, pt = threadIdx.x & 31;
+        qxd_trace_buf[sl < 4 ? 20 + sl : 48][pt][blockIdx.x] = qxd_tl[sl][pt];
+    }
+#endif
 }
 
 // The routed experts' rows of one layer in the interleaved layout (QXD_GU_UNIT, QXD_DN_ROW),
