@@ -45,7 +45,8 @@
 // loop the workgroup copies them to qxd_trace_buf[layer][point][workgroup], read back with
 // qxd_trace_read.
 #ifdef QXD_TRACE
-__device__ unsigned long long qxd_trace_buf[49][32][256];
+__device__ unsigned long long qxd_trace_buf[49][40][256];
+__shared__ unsigned long long qxd_tl[5][40];
 extern "C" int qxd_trace_read(unsigned long long *out) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(qxd_trace_buf), sizeof(qxd_trace_buf)) == hipSuccess;
 }
@@ -367,7 +368,11 @@ DEV void dma16(const GLB uint8_t *base, uint32_t off, const void *lds) {
     const uint32_t l = (uint32_t)(uintptr_t)lds;   // low half of the flat address = LDS offset
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" : : "v"(off), "s"(base), "s"(l) : "memory", "m0");
 }
-DEV void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); }
+// s_waitcnt vmcnt(0) as the builtin (0x0F70: vmcnt 0, expcnt and lgkmcnt unconstrained), which
+// the compiler's wait insertion takes into account (after an opaque asm wait it still assumed
+// older loads pending and waited again behind loads issued later); the fence keeps LDS reads
+// of the copied rows below it.
+DEV void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
 
 // layer l's plane `id` (scalar arithmetic on the argument copy)
 DEV const GLB uint8_t *plane(const QxDArgs &a, int id, uint32_t l) {
@@ -537,10 +542,14 @@ struct AttnPre {   // vector-typed fields: they stay in registers (arrays filled
 };
 // KV cache reads: agent-coherent (sc1) buffer loads, 16/8/4 bytes per lane.  Rows written
 // earlier in this launch were stored by workgroup 0 with agent-scope stores; every row is
-// read the same way.
+// read the same way.  The base goes through readfirstlane: a descriptor the compiler cannot
+// prove uniform (the argument copy is read from LDS) gets a loop around each load that
+// copies the result out afterwards, which waits for the load right after issuing it.
 constexpr int CP_SC1 = 16;
 template <typename T>
-DEV __amdgpu_buffer_rsrc_t rsrc(const T *p) { return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, 0x7fffffff, 0x00020000); }
+DEV __amdgpu_buffer_rsrc_t rsrc(const T *p) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)uni64((uint64_t)p), (short)0, 0x7fffffff, 0x00020000);
+}
 DEV u32x4 kv_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP_SC1); }
 DEV u32x2 kv_ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CP_SC1); }
 DEV uint32_t kv_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CP_SC1); }
@@ -869,8 +878,7 @@ DEV bool better(float v, uint32_t i, float bv, uint32_t bi) { return v > bv || (
 extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
     __shared__ DLds S;
 #ifdef QXD_TRACE
-    __shared__ unsigned long long qxd_tl[5][32];
-    if (threadIdx.x < 5 * 32) qxd_tl[threadIdx.x >> 5][threadIdx.x & 31] = 0ull;
+    if (threadIdx.x < 5 * 40) qxd_tl[threadIdx.x / 40][threadIdx.x % 40] = 0ull;
 #endif
     // the arguments are read from an LDS copy where used (LDS reads are not hoisted across
     // the stage barriers, so the ~70 argument dwords are not all held in scalar registers)
@@ -925,9 +933,10 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     return;
                 DMARK(l, 1);
                 wait_loads();   // the Q/K/V rows in LDS (issued a stage or more ago; nothing later is outstanding)
-                // attention workgroups: the cached K/V rows they attend to, issued now so they
-                // have arrived before the Q/K/V words are polled (loads complete in order)
-                if (wg < QXG_HEADS) attn_prefetch(a, l, pos, ap);
+                // attention workgroups: the cached K/V rows they attend to (layers after the
+                // first: issued at the end of the layer before, behind the x exchange)
+                if (wg < QXG_HEADS && l == 0) attn_prefetch(a, l, pos, ap);
+                DMARK(l, 32);
                 // the normalised input's digits; the attn-norm weights came with the Q/K/V rows
                 double inv = 1.0;
                 bool fin = true;
@@ -946,6 +955,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                                  (double)wo.wr.z * (double)wo.fw.z * (double)x4.z + (double)wo.wr.w * (double)wo.fw.w * (double)x4.w;
                     }
                     __syncthreads();
+                    DMARK(l, 33);
                     const double tot = (S.red[0] + S.red[1]) + (S.red[2] + S.red[3]);
                     inv = 1.0 / sqrt(tot / 2048.0 + 1.0e-6);
                 }
@@ -973,6 +983,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     a_part = wave_total_d(a_part);
                     if (lane == 0) S.red[NWV + wave] = a_part;
                 }
+                DMARK(l, 34);
                 const bool ok = !block_any(!fin, S);
                 DMARK(l, 13);
                 if ((uint32_t)wg < E)
@@ -1222,6 +1233,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 __syncthreads();
                 DMARK(l, 29);
                 if (tid < 24) xstf(X + XO_H + par * XN_H + 24 * wg + tid, ep + 4, S.outw[tid]);
+                DMARK(l, 31);
                 // attention workgroups: the next layer's Q/K/V rows, arriving during the h exchange
                 if (wg < QXG_HEADS) load_wq(a, ln, wq, S.wq[wave_id()]);
                 DMARK(l, 10);
@@ -1289,6 +1301,9 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     xstf(X + XO_X + ((l + 1) & 1) * XN_X + r, ep + 5, xn);
                 }
                 DMARK(l, 12);
+                // attention workgroups: the next layer's cached K/V rows (positions below pos,
+                // all written in earlier steps), issued while x is exchanged
+                if (wg < QXG_HEADS && l + 1 < L) attn_prefetch(a, l + 1, pos, ap);
             }
         }
         // ---------------------------------------------------------------- head
@@ -1349,8 +1364,8 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
     }
 #ifdef QXD_TRACE
     __syncthreads();
-    if (threadIdx.x < 5 * 32) {
-        const int sl = threadIdx.x >> 5, pt = threadIdx.x & 31;
+    if (threadIdx.x < 5 * 40) {
+        const int sl = threadIdx.x / 40, pt = threadIdx.x % 40;
         qxd_trace_buf[sl < 4 ? 20 + sl : 48][pt][blockIdx.x] = qxd_tl[sl][pt];
     }
 #endif
