@@ -34,6 +34,9 @@ __global__ void qxk_interleave_experts(const uint8_t *, const uint8_t *, const u
 __global__ void qxk_router_fold(const float *, const float *, const float *, uint32_t, float *);
 __global__ void qxk_int8_row(const float *, uint32_t, int8_t *, float *);
 __global__ void qxk_interleave_head(const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, uint32_t, uint8_t *);
+__global__ void qxk_pack_decode(const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *,
+                                const uint8_t *, const uint8_t *, const uint8_t *, const float *, const float *, uint32_t,
+                                uint8_t *);
 __global__ void qxk_dequant(uint32_t, const uint8_t *, const uint8_t *, const uint8_t *, const uint16_t *, Tables,
                             uint64_t, float *);
 __global__ void qxk_repack(uint32_t, const uint8_t *, uint64_t, uint8_t *, uint8_t *, uint8_t *, uint16_t *);
@@ -144,6 +147,7 @@ struct qxg_ctx {
     uint8_t *mfold = nullptr;        // router fold M = W diag(w) O of every layer (f32)
     uint8_t *gu_il = nullptr, *dn_il = nullptr;   // interleaved routed-expert rows of every layer
     uint8_t *head_il = nullptr;                   // interleaved head rows
+    uint8_t *dpack = nullptr;                     // decode packs of every layer (QXD_PK_*)
     uint64_t gu_stride = 0, dn_stride = 0;
     uint64_t mfold_stride = 0;
     uint64_t *xch = nullptr;
@@ -364,7 +368,8 @@ constexpr uint64_t DECODE_WAIT_TICKS = 100000000ull;   // 1 s of the 100 MHz wal
 // benchmark mix only, and computes in the f32 activation mode; other models and
 // q8_k_compat run one kernel per phase.
 bool persistent(const qxg_ctx *c) {
-    return c->persist && c->base_mix && !c->q8 && c->emb && c->head && c->mfold && c->gu_il && c->dn_il && c->head_il;
+    return c->persist && c->base_mix && !c->q8 && c->emb && c->head && c->mfold && c->gu_il && c->dn_il && c->head_il &&
+           c->dpack;
 }
 
 struct DecodeDumps {
@@ -385,9 +390,9 @@ bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0,
     }
     QxDArgs a{};
     for (int i = 0; i < PL_COUNT; ++i) a.P[i] = c->planes[i];
-    a.M = {c->mfold, c->mfold_stride};
     a.GU = {c->gu_il, c->gu_stride};
     a.DN = {c->dn_il, c->dn_stride};
+    a.PK = {c->dpack, (uint64_t)QXG_PBLOCKS * QXD_PK_BYTES};
     a.emb = c->emb; a.emb_row = c->emb_row;
     a.out_norm = c->out_norm;
     a.h_ql = c->head->p0; a.h_qh = c->head->p1; a.h_sc = (const int8_t *)c->head->p2; a.h_d = c->head->d;
@@ -470,6 +475,25 @@ bool build_expert_interleave(qxg_ctx *c, char *err, uint64_t n) {
         }
     }
     return ok && hip_ok(hipStreamSynchronize(c->s), err, n, "expert interleave");
+}
+
+// The persistent decode's packs (QXD_PK_* in qxg_internal.h): per layer, each workgroup's
+// Q/K/V/O rows with their metas, router row and router-fold row, contiguous.  After the
+// arenas and the router fold.
+bool build_decode_pack(qxg_ctx *c, char *err, uint64_t n) {
+    if (c->dpack) { (void)hipFree(c->dpack); c->dpack = nullptr; }
+    if (c->experts < 1 || c->experts > QXG_PBLOCKS || !c->mfold) return true;   // no persistent decode for this model
+    const uint64_t stride = (uint64_t)QXG_PBLOCKS * QXD_PK_BYTES;
+    if (!hip_ok(hipMalloc(&c->dpack, stride * c->layers), err, n, "decode pack")) return false;
+    bool ok = true;
+    for (uint32_t l = 0; l < c->layers && ok; ++l) {
+        const LayerW &w = c->L[l];
+        hipLaunchKernelGGL(qxk_pack_decode, dim3(QXG_PBLOCKS), dim3(256), 0, c->s, w.wq->p0, w.wq->p1, w.wk->p0, w.wk->p1,
+                           w.wv->p0, w.wv->p1, w.wo->p0, w.wo->p1, w.router,
+                           (const float *)(c->mfold + l * c->mfold_stride), (uint32_t)c->experts, c->dpack + l * stride);
+        ok = hip_ok(hipGetLastError(), err, n, "decode pack");
+    }
+    return ok && hip_ok(hipStreamSynchronize(c->s), err, n, "decode pack");
 }
 
 void launch_step(qxg_ctx *c, uint32_t top_n, bool dump_layers) {
@@ -560,11 +584,24 @@ bool build_arenas(qxg_ctx *c, char *err, uint64_t n) {
         default: return {(const uint8_t *)w.down->d, w.down->nblocks * 2};
         }
     };
+    // the four norm vectors of a layer together (QXD_NORM_STRIDE): one translation page
+    // holds every layer's
+    uint8_t *norms = nullptr;
+    if (!hip_ok(hipMalloc(&norms, (uint64_t)QXD_NORM_STRIDE * L), err, n, "weight arena")) return false;
+    c->arenas.push_back(norms);
+    const uint64_t norm_off[4] = {0, 16384, 16896, 8192};   // PL_ATTN_NORM, PL_Q_NORM, PL_K_NORM, PL_FFN_NORM
+    static_assert(PL_ATTN_NORM == 0 && PL_Q_NORM == 1 && PL_K_NORM == 2 && PL_FFN_NORM == 3, "norm planes first");
     for (int id = 0; id < PL_COUNT; ++id) {
-        const uint64_t stride = align256(src(id, 0).bytes);
         uint8_t *ar = nullptr;
-        if (!hip_ok(hipMalloc(&ar, stride * L), err, n, "weight arena")) return false;
-        c->arenas.push_back(ar);
+        uint64_t stride;
+        if (id <= PL_FFN_NORM) {
+            ar = norms + norm_off[id];
+            stride = QXD_NORM_STRIDE;
+        } else {
+            stride = align256(src(id, 0).bytes);
+            if (!hip_ok(hipMalloc(&ar, stride * L), err, n, "weight arena")) return false;
+            c->arenas.push_back(ar);
+        }
         for (uint32_t l = 0; l < L; ++l) {
             const Src sp = src(id, l);
             if (!hip_ok(hipMemcpyAsync(ar + l * stride, sp.p, sp.bytes, hipMemcpyDeviceToDevice, c->s), err, n, "weight arena"))
@@ -869,11 +906,18 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
             rc[p * 64 + i] = cos(a);
             rs[p * 64 + i] = sin(a);
         }
+    std::vector<double> rcs((size_t)QXG_MAX_CTX * 128);   // per position: 64 cos, then 64 sin (one page)
+    for (uint32_t p = 0; p < QXG_MAX_CTX; ++p)
+        for (uint32_t i = 0; i < 64; ++i) {
+            rcs[p * 128 + i] = rc[p * 64 + i];
+            rcs[p * 128 + 64 + i] = rs[p * 64 + i];
+        }
     ok = ok && hip_ok(hipMalloc(&c->T.g2, g2.size() * sizeof(uint4)), err, err_len, "tables") &&
          hip_ok(hipMalloc(&c->T.g3, g3.size() * sizeof(uint2)), err, err_len, "tables") &&
          hip_ok(hipMalloc(&c->T.sel, sel.size() * sizeof(uint2)), err, err_len, "tables") &&
          hip_ok(hipMalloc(&c->T.rope_cos, rc.size() * sizeof(double)), err, err_len, "tables") &&
          hip_ok(hipMalloc(&c->T.rope_sin, rs.size() * sizeof(double)), err, err_len, "tables") &&
+         hip_ok(hipMalloc(&c->T.rope_cs, rcs.size() * sizeof(double)), err, err_len, "tables") &&
          hip_ok(hipMalloc(&c->T.g2s, g2s.size() * sizeof(uint4)), err, err_len, "tables") &&
          hip_ok(hipMalloc(&c->T.g3s, g3s.size() * sizeof(uint2)), err, err_len, "tables") &&
          hip_ok(hipMalloc(&c->T.sel8, sel8.size() * sizeof(uint2)), err, err_len, "tables");
@@ -882,6 +926,7 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
          hip_ok(hipMemcpy(c->T.sel, sel.data(), sel.size() * sizeof(uint2), hipMemcpyHostToDevice), err, err_len, "tables") &&
          hip_ok(hipMemcpy(c->T.rope_cos, rc.data(), rc.size() * sizeof(double), hipMemcpyHostToDevice), err, err_len, "tables") &&
          hip_ok(hipMemcpy(c->T.rope_sin, rs.data(), rs.size() * sizeof(double), hipMemcpyHostToDevice), err, err_len, "tables") &&
+         hip_ok(hipMemcpy(c->T.rope_cs, rcs.data(), rcs.size() * sizeof(double), hipMemcpyHostToDevice), err, err_len, "tables") &&
          hip_ok(hipMemcpy(c->T.g2s, g2s.data(), g2s.size() * sizeof(uint4), hipMemcpyHostToDevice), err, err_len, "tables") &&
          hip_ok(hipMemcpy(c->T.g3s, g3s.data(), g3s.size() * sizeof(uint2), hipMemcpyHostToDevice), err, err_len, "tables") &&
          hip_ok(hipMemcpy(c->T.sel8, sel8.data(), sel8.size() * sizeof(uint2), hipMemcpyHostToDevice), err, err_len, "tables");
@@ -907,7 +952,8 @@ void qxg_close(qxg_ctx *c) {
     void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->T.g2s, c->T.g3s, c->T.sel8, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
                     c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging,
-                    c->xch, c->abort, c->apart, c->route_ids, c->route_w, c->mfold, c->gu_il, c->dn_il, c->head_il};
+                    c->xch, c->abort, c->apart, c->route_ids, c->route_w, c->mfold, c->gu_il, c->dn_il, c->head_il, c->dpack,
+                    c->T.rope_cs};
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (void *p : c->arenas) (void)hipFree(p);
     for (void *p : c->pf.all) (void)hipFree(p);
@@ -1028,6 +1074,7 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     if (c->mfold) { (void)hipFree(c->mfold); c->mfold = nullptr; }
     if (layers && base && !build_router_fold(c, err, err_len)) return 0;
     if (layers && base && !build_expert_interleave(c, err, err_len)) return 0;
+    if (layers && base && !build_decode_pack(c, err, err_len)) return 0;
     c->bound = true;
     return 1;
 }

@@ -67,6 +67,7 @@ namespace {
 constexpr int NT = 512;            // threads per workgroup
 constexpr int NWV = NT / 64;       // waves per workgroup
 constexpr int NWG = QXG_PBLOCKS;   // workgroups, one per CU
+static_assert((NWG - QXG_HEADS) * 24 >= 5120, "the non-attention workgroups' 24 slots cover the Q/K/V rows");
 constexpr uint32_t GU_BYTES = 4096, DN_BYTES = 3072;   // per-wave LDS for the routed experts' rows
 constexpr int HEAD_R = 4;                                // head rows per wave and pass
 constexpr int HEAD_NI = (HEAD_R * 105 + 63) / 64;        // 16-byte load instructions per pass
@@ -378,12 +379,16 @@ DEV void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); __builtin_amdgcn_fen
 DEV const GLB uint8_t *plane(const QxDArgs &a, int id, uint32_t l) {
     return (const GLB uint8_t *)(uni64((uint64_t)a.P[id].base) + (uint64_t)l * uni64(a.P[id].stride));
 }
+// the calling workgroup's decode pack of layer l
+DEV const GLB uint8_t *wg_pack(const QxDArgs &a, uint32_t l) {
+    return (const GLB uint8_t *)(uni64((uint64_t)a.PK.base) + (uint64_t)l * uni64(a.PK.stride) +
+                                 (uint64_t)blockIdx.x * QXD_PK_BYTES);
+}
 
 // ---------------------------------------------------------------- weight sets
-// Q/K/V rows of a wave: Q rows 16 wg + 2 w + {0, 1}; waves 0..3 also K/V row 4096 + 4 wg + w
-// (waves 4..7 load their partner's, unused), and the attn-norm weights of the thread's 8
-// values.  Every load is unconditional: a register set reloaded on every path is not kept
-// live across the stages in between.
+// Q/K/V rows of a wave of workgroup wg >= QXG_HEADS (the attention workgroups make none):
+// stacked rows [Q 4096 | K 512 | V 512] 24 (wg - 32) + 3 w + {0, 1, 2} (pack slots past row
+// 5119 are zero), and the attn-norm weights of the thread's 8 values.
 // The 16-byte qs chunks go to LDS (lq[wave][r][lane], DMA); meta and norm weights stay in
 // registers.
 struct WQ {
@@ -391,22 +396,16 @@ struct WQ {
     float4 nw0, nw1;
 };
 DEV void load_wq(const QxDArgs &a, uint32_t l, WQ &w, uint4 (*lq)[64]) {
-    const int tid = tix(), lane = tid & 63, wg = blockIdx.x;
+    const int tid = tix(), lane = tid & 63;
     const int wave = wave_id();
     const uint32_t b = lane >> 3, ib = lane & 7;
-    const GLB uint8_t *qq = plane(a, PL_Q_QS, l), *qm = plane(a, PL_Q_META, l);
+    const GLB uint8_t *pk = wg_pack(a, l);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const uint32_t blk = (uint32_t)(16 * wg + 2 * wave + r) * 8 + b;
-        dma16(qq, blk * 128 + 16 * ib, lq[r]);
-        w.m[r] = gnt2(qm, blk * 8);
+    for (int r = 0; r < 3; ++r) {
+        const uint32_t blk = (uint32_t)(3 * wave + r) * 8 + b;
+        dma16(pk, QXD_PK_QQ + blk * 128 + 16 * ib, lq[r]);
+        w.m[r] = gnt2(pk, QXD_PK_QM + blk * 8);
     }
-    const uint32_t kv = 4 * wg + (wave & 3);   // 0..1023: K rows 0..511, then V rows
-    const GLB uint8_t *kq = kv < 512 ? plane(a, PL_K_QS, l) : plane(a, PL_V_QS, l);
-    const GLB uint8_t *km = kv < 512 ? plane(a, PL_K_META, l) : plane(a, PL_V_META, l);
-    const uint32_t blk = (kv & 511) * 8 + b;
-    dma16(kq, blk * 128 + 16 * ib, lq[2]);
-    w.m[2] = gnt2(km, blk * 8);
     const GLB uint8_t *nw = plane(a, PL_ATTN_NORM, l);
     w.nw0 = ldf4(nw, 32 * (tid & 255));
     w.nw1 = ldf4(nw, 32 * (tid & 255) + 16);
@@ -419,27 +418,25 @@ struct WO {
     float4 wr, fw;
 };
 DEV void load_wo(const QxDArgs &a, uint32_t l, WO &w, uint4 (*lo)[64]) {
-    const int tid = tix(), lane = tid & 63, wg = blockIdx.x;
+    const int tid = tix(), lane = tid & 63;
     const int wave = wave_id();
     const uint32_t ib = lane & 7;
-    const GLB uint8_t *oq = plane(a, PL_O_QS, l), *om = plane(a, PL_O_META, l);
-    const uint32_t r = (uint32_t)(8 * wg + wave) * 16;
+    const GLB uint8_t *pk = wg_pack(a, l);   // O rows 8 wg .., router row min(wg, experts - 1)
+    const uint32_t r = (uint32_t)wave * 16;
     const uint32_t k0 = r + (lane >> 3), k1 = r + 8 + (lane >> 3);
-    dma16(oq, k0 * 128 + 16 * ib, lo[0]);
-    dma16(oq, k1 * 128 + 16 * ib, lo[1]);
-    w.m0 = gnt2(om, k0 * 8);
-    w.m1 = gnt2(om, k1 * 8);
-    const uint32_t e = min((uint32_t)wg, a.experts - 1);
-    w.wr = ldf4(plane(a, PL_ROUTER, l), e * 8192 + 16 * tid);
+    dma16(pk, QXD_PK_OQ + k0 * 128 + 16 * ib, lo[0]);
+    dma16(pk, QXD_PK_OQ + k1 * 128 + 16 * ib, lo[1]);
+    w.m0 = gnt2(pk, QXD_PK_OM + k0 * 8);
+    w.m1 = gnt2(pk, QXD_PK_OM + k1 * 8);
+    w.wr = ldf4(pk, QXD_PK_RT + 16 * tid);
     w.fw = ldf4(plane(a, PL_FFN_NORM, l), 16 * tid);
 }
 // router fold row M[e], values 8 tid .. 8 tid + 7 (the router's ctx-part)
 DEV void load_wm(const QxDArgs &a, uint32_t l, float4 &m0, float4 &m1) {
-    const int tid = tix(), wg = blockIdx.x;
-    const uint32_t e = min((uint32_t)wg, a.experts - 1);
-    const GLB uint8_t *mm = (const GLB uint8_t *)(uni64((uint64_t)a.M.base) + (uint64_t)l * uni64(a.M.stride));
-    m0 = ldf4(mm, e * 16384 + 32 * tid);
-    m1 = ldf4(mm, e * 16384 + 32 * tid + 16);
+    const int tid = tix();
+    const GLB uint8_t *pk = wg_pack(a, l);
+    m0 = ldf4(pk, QXD_PK_MF + 32 * tid);
+    m1 = ldf4(pk, QXD_PK_MF + 32 * tid + 16);
 }
 // norm weights of the thread's 8 values 8 tid .. 8 tid + 7 (used by threads < 256; the
 // others load a copy)
@@ -585,8 +582,8 @@ DEV void attn_prefetch(const QxDArgs &a, uint32_t l, uint32_t pos, AttnPre &p) {
     p.k0 = r.k0; p.k1 = r.k1; p.ks = r.ks; p.vs = r.vs;
     p.v0 = r.v[0]; p.v1 = r.v[1]; p.v2 = r.v[2]; p.v3 = r.v[3];
     const int lane = tix() & 63;
-    p.cs = gp(a.T.rope_cos)[pos * 64 + lane];
-    p.sn = gp(a.T.rope_sin)[pos * 64 + lane];
+    p.cs = gp(a.T.rope_cs)[pos * 128 + lane];
+    p.sn = gp(a.T.rope_cs)[pos * 128 + 64 + lane];
     const GLB float *nq = (const GLB float *)plane(a, PL_Q_NORM, l), *nk = (const GLB float *)plane(a, PL_K_NORM, l);
     p.nq0 = nq[lane]; p.nq1 = nq[64 + lane];
     p.nk0 = nk[lane]; p.nk1 = nk[64 + lane];
@@ -905,7 +902,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
     AttnPre ap;
     float4 wm0 = make_float4(0.f, 0.f, 0.f, 0.f), wm1 = wm0;
     float fnw[8];
-    load_wq(a, 0, wq, S.wq[wave_id()]);
+    if (wg >= QXG_HEADS) load_wq(a, 0, wq, S.wq[wave_id()]);
     load_wo(a, 0, wo, S.wo[wave_id()]);
     uint32_t token = 0;
     __syncthreads();
@@ -933,16 +930,17 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     return;
                 DMARK(l, 1);
                 wait_loads();   // the Q/K/V rows in LDS (issued a stage or more ago; nothing later is outstanding)
-                // attention workgroups: the cached K/V rows they attend to (layers after the
-                // first: issued at the end of the layer before, behind the x exchange)
-                if (wg < QXG_HEADS && l == 0) attn_prefetch(a, l, pos, ap);
+                // attention workgroups (no Q/K/V rows of their own): the cached K/V rows they
+                // attend to, arriving while the other workgroups make the Q/K/V rows
+                const bool mk = wg >= QXG_HEADS;
+                if (!mk) attn_prefetch(a, l, pos, ap);
                 DMARK(l, 32);
                 // the normalised input's digits; the attn-norm weights came with the Q/K/V rows
                 double inv = 1.0;
                 bool fin = true;
                 {
                     double ss = 0.0;
-                    if (tid < 256) {
+                    if (mk && tid < 256) {
 #pragma unroll
                         for (int i = 0; i < 8; ++i) ss += (double)S.xs[8 * tid + i] * (double)S.xs[8 * tid + i];
                     }
@@ -959,7 +957,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     const double tot = (S.red[0] + S.red[1]) + (S.red[2] + S.red[3]);
                     inv = 1.0 / sqrt(tot / 2048.0 + 1.0e-6);
                 }
-                if (tid < 256) {
+                if (mk && tid < 256) {
                     float y[8];
                     const float nw8[8] = {wq.nw0.x, wq.nw0.y, wq.nw0.z, wq.nw0.w, wq.nw1.x, wq.nw1.y, wq.nw1.z, wq.nw1.w};
 #pragma unroll
@@ -989,33 +987,32 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 if ((uint32_t)wg < E)
                     a_part = ((S.red[NWV + 0] + S.red[NWV + 1]) + (S.red[NWV + 2] + S.red[NWV + 3])) +
                              ((S.red[NWV + 4] + S.red[NWV + 5]) + (S.red[NWV + 6] + S.red[NWV + 7]));
-                Dig g;
-                load_dig(S.dig, lane, g);
-                float part[4], out[4];
-                {
-                    const uint4(*lq)[64] = S.wq[wave_id()];
-                    part[0] = dot_iq4(lq[0][lane], wq.m[0], ib, g);
-                    part[1] = dot_iq4(lq[1][lane], wq.m[1], ib, g);
-                    part[2] = wave < 4 ? dot_iq4(lq[2][lane], wq.m[2], ib, g) : 0.0f;
-                }
-                part[3] = 0.0f;
-                rows_reduce<4>(part, out, lane);
-                // gather the workgroup's 20 rows, then one store: Q rows 16 wg .., K/V rows 4096 + 4 wg ..
-#pragma unroll
-                for (int r = 0; r < 3; ++r)
-                    if (lane == r && (r < 2 || wave < 4)) {
-                        const float v = (ok && isfinite(out[r])) ? out[r] : 0.0f;
-                        S.outw[r < 2 ? 2 * wave + r : 16 + wave] = v;
+                if (mk) {
+                    Dig g;
+                    load_dig(S.dig, lane, g);
+                    float part[4], out[4];
+                    {
+                        const uint4(*lq)[64] = S.wq[wave_id()];
+                        part[0] = dot_iq4(lq[0][lane], wq.m[0], ib, g);
+                        part[1] = dot_iq4(lq[1][lane], wq.m[1], ib, g);
+                        part[2] = dot_iq4(lq[2][lane], wq.m[2], ib, g);
                     }
+                    part[3] = 0.0f;
+                    rows_reduce<4>(part, out, lane);
+                    // gather the workgroup's 24 rows, then one store: stacked rows 24 (wg - 32) ..
+#pragma unroll
+                    for (int r = 0; r < 3; ++r)
+                        if (lane == r) S.outw[3 * wave + r] = (ok && isfinite(out[r])) ? out[r] : 0.0f;
+                }
                 __syncthreads();
-                if (tid < 20) {
-                    GLB uint64_t *qkv = X + XO_QKV + par * XN_QKV;
-                    xstf(qkv + (tid < 16 ? 16 * wg + tid : 4096 + 4 * wg + (tid - 16)), ep + 1, S.outw[tid]);
+                if (mk && tid < 24) {
+                    const uint32_t row = 24u * (uint32_t)(wg - QXG_HEADS) + (uint32_t)tid;
+                    if (row < 5120u) xstf(X + XO_QKV + par * XN_QKV + row, ep + 1, S.outw[tid]);
                 }
                 DMARK(l, 2);
             }
-            // prefetch: the router fold rows (stage O); workgroups without attention work the
-            // next layer's Q/K/V rows
+            // prefetch: the router fold rows (stage O); workgroups that make Q/K/V rows the
+            // next layer's
             load_wm(a, l, wm0, wm1);
             if (wg >= QXG_HEADS) load_wq(a, ln, wq, S.wq[wave_id()]);
             // ---------------------------------------------------------- stage A
@@ -1234,8 +1231,6 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 DMARK(l, 29);
                 if (tid < 24) xstf(X + XO_H + par * XN_H + 24 * wg + tid, ep + 4, S.outw[tid]);
                 DMARK(l, 31);
-                // attention workgroups: the next layer's Q/K/V rows, arriving during the h exchange
-                if (wg < QXG_HEADS) load_wq(a, ln, wq, S.wq[wave_id()]);
                 DMARK(l, 10);
             }
             // ---------------------------------------------------------- stage D
@@ -1301,9 +1296,6 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     xstf(X + XO_X + ((l + 1) & 1) * XN_X + r, ep + 5, xn);
                 }
                 DMARK(l, 12);
-                // attention workgroups: the next layer's cached K/V rows (positions below pos,
-                // all written in earlier steps), issued while x is exchanged
-                if (wg < QXG_HEADS && l + 1 < L) attn_prefetch(a, l + 1, pos, ap);
             }
         }
         // ---------------------------------------------------------------- head
@@ -1348,7 +1340,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             DMARK(48, 4);
             // layer 0's rows again (also on the last step), after the argmax exchange: issued
             // earlier, its poll would wait behind them (loads complete in order)
-            load_wq(a, 0, wq, S.wq[wave_id()]);
+            if (wg >= QXG_HEADS) load_wq(a, 0, wq, S.wq[wave_id()]);
             load_wo(a, 0, wo, S.wo[wave_id()]);
             float v = __uint_as_float(S.u.hd.am[0]);
             uint32_t i = S.u.hd.am[1];
@@ -1430,6 +1422,46 @@ extern "C" __global__ __launch_bounds__(256) void qxk_interleave_head(const uint
     cp32(o + 1024, qh + r * 512, 128);
     cp32(o + 1536, sc + r * 128, 32);
     cp32(o + 1664, d + r * 16, 4);
+}
+
+// The decode packs of one layer (QXD_PK_*): workgroup w of the grid (256) copies pack w:
+// for w >= 32 its 24 Q/K/V row slots (stacked rows [Q 4096 | K 512 | V 512] 24 (w - 32) ..,
+// zero past row 5119) with their 8-byte block metas; for every w its O rows 8 w .. 8 w + 7
+// and metas, router row and router-fold row (expert min(w, experts - 1)).
+extern "C" __global__ __launch_bounds__(256) void qxk_pack_decode(const uint8_t *qq, const uint8_t *qm, const uint8_t *kq,
+                                                                   const uint8_t *km, const uint8_t *vq, const uint8_t *vm,
+                                                                   const uint8_t *oq, const uint8_t *om, const float *router,
+                                                                   const float *mfold, uint32_t experts, uint8_t *out) {
+    const uint32_t w = blockIdx.x, e = min(w, experts - 1u);
+    uint8_t *o = out + (uint64_t)w * QXD_PK_BYTES;
+    auto cp = [](uint8_t *dst, const uint8_t *src, uint32_t bytes) {
+        for (uint32_t i = threadIdx.x; i < bytes / 16; i += 256)
+            reinterpret_cast<uint4 *>(dst)[i] = reinterpret_cast<const uint4 *>(src)[i];
+    };
+    // one Q/K/V row slot: 1024 qs bytes (64 chunks) or 64 meta bytes (4 chunks) of row `row`
+    auto slot = [&](uint32_t s, bool meta) -> const uint4 * {
+        const uint32_t row = 24u * (w - QXG_HEADS) + s;
+        if (row >= 5120u) return nullptr;
+        const uint32_t rb = meta ? 64u : 1024u;
+        const uint8_t *p = row < 4096u ? (meta ? qm : qq) + (uint64_t)row * rb
+                         : row < 4608u ? (meta ? km : kq) + (uint64_t)(row - 4096u) * rb
+                                       : (meta ? vm : vq) + (uint64_t)(row - 4608u) * rb;
+        return reinterpret_cast<const uint4 *>(p);
+    };
+    if (w >= QXG_HEADS) {
+        for (uint32_t i = threadIdx.x; i < 24u * 64u; i += 256) {
+            const uint4 *src = slot(i / 64u, false);
+            reinterpret_cast<uint4 *>(o + QXD_PK_QQ)[i] = src ? src[i % 64u] : make_uint4(0u, 0u, 0u, 0u);
+        }
+        for (uint32_t i = threadIdx.x; i < 24u * 4u; i += 256) {
+            const uint4 *src = slot(i / 4u, true);
+            reinterpret_cast<uint4 *>(o + QXD_PK_QM)[i] = src ? src[i % 4u] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    cp(o + QXD_PK_OQ, oq + (uint64_t)w * 8 * 2048, 16384);
+    cp(o + QXD_PK_OM, om + (uint64_t)w * 8 * 128, 1024);
+    cp(o + QXD_PK_RT, reinterpret_cast<const uint8_t *>(router + (uint64_t)e * 2048), 8192);
+    cp(o + QXD_PK_MF, reinterpret_cast<const uint8_t *>(mfold + (uint64_t)e * 4096), 16384);
 }
 
 // Router fold of one layer (see the top of this file): M[e][j] = sum_i W[e][i] w[i] O[i][j]

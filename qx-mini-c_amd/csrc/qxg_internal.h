@@ -68,6 +68,7 @@ struct Tables {
     uint2 *g3;     // IQ3_XXS grid: 256 x {pos, neg}
     uint2 *sel;    // sign index (7 bits) -> v_perm selectors for 8 values
     double *rope_cos, *rope_sin;  // [QXG_MAX_CTX][64]
+    double *rope_cs;              // [QXG_MAX_CTX][128]: the position's 64 cos, then its 64 sin
     uint4 *g2s;    // IQ2_S grid: 1024 x {pos lo, pos hi, neg lo, neg hi}
     uint2 *g3s;    // IQ3_S grid: 512 x {pos, neg}
     uint2 *sel8;   // sign byte (8 bits) -> v_perm selectors for 8 values
@@ -117,9 +118,9 @@ enum QxPlaneId : int {
 // for the benchmark quant mix.
 struct QxDArgs {
     QxPlane P[PL_COUNT];         // per-layer weight planes (layer l at base + l * stride)
-    QxPlane M;                   // router fold M = W diag(w) O, [experts][4096] f32 per layer
     QxPlane GU;                  // routed experts' gate/up rows, unit-interleaved (QXD_GU_UNIT bytes per unit)
     QxPlane DN;                  // routed experts' down rows (QXD_DN_ROW bytes per row), 8-row blocks of all experts together
+    QxPlane PK;                  // each workgroup's dense rows of the layer (QXD_PK_*), 256 packs of QXD_PK_BYTES
     const uint8_t *emb;          // Q4_K token embedding
     uint64_t emb_row;
     const float *out_norm;
@@ -157,6 +158,21 @@ struct QxDArgs {
 // (the 8 blocks' planes of the row back to back; 105 16-byte chunks).
 #define QXD_HEAD_ROW 1680u
 #define QXD_DN_ROW 304u
+// Decode pack of workgroup w (0..255) for one layer: the dense rows it reads, copied
+// contiguously so that its loads of a layer touch one or two translation pages instead of
+// one per plane (Q/K/V, O, their metas, router, router fold).  Workgroups w >= 32 make the
+// Q/K/V rows: 24 slots, slot 3 v + r = stacked row [Q 4096 | K 512 | V 512] 24 (w - 32) +
+// 3 v + r (224 x 24 >= 5120; the slots past row 5119 are zero).  Byte offsets in the pack:
+#define QXD_PK_QQ 0u        // the 24 Q/K/V slots' IQ4_XS qs (8 blocks x 128 B a row)
+#define QXD_PK_OQ 24576u    // O rows 8 w .. 8 w + 7, qs (16 blocks x 128 B a row)
+#define QXD_PK_QM 40960u    // the Q/K/V slots' 8-byte block metas
+#define QXD_PK_OM 42496u    // the O rows' metas
+#define QXD_PK_RT 43520u    // router row W[e], e = min(w, experts - 1), 2048 f32
+#define QXD_PK_MF 51712u    // router fold row M[e], 4096 f32
+#define QXD_PK_BYTES 68096u
+// The four per-layer norm vectors share one arena: layer l's at l * QXD_NORM_STRIDE, attn
+// norm (2048 f32) at 0, ffn norm at 8192, q norm (128 f32) at 16384, k norm at 16896.
+#define QXD_NORM_STRIDE 17408u
 // exchange words per launch: x, qkv, ctx, x', router logits, h, expert weights (two slots
 // each) and the per-workgroup argmax candidates
 #define QXD_XCH_WORDS (2u * (2048u + 5120u + 4096u + 2048u + 256u + 6144u + 16u + 2u * QXG_PBLOCKS))
