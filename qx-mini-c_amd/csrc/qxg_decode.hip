@@ -417,18 +417,25 @@ struct WO {
     uint2 m0, m1;
     float4 wr, fw;
 };
-DEV void load_wo(const QxDArgs &a, uint32_t l, WO &w, uint4 (*lo)[64]) {
-    const int tid = tix(), lane = tid & 63;
+// The O rows (load-to-LDS copies, which issue slowly: issued where the workgroup waits
+// anyway, after its Q/K/V rows) ...
+DEV void load_o(const QxDArgs &a, uint32_t l, WO &w, uint4 (*lo)[64]) {
+    const int lane = tix() & 63;
     const int wave = wave_id();
     const uint32_t ib = lane & 7;
-    const GLB uint8_t *pk = wg_pack(a, l);   // O rows 8 wg .., router row min(wg, experts - 1)
+    const GLB uint8_t *pk = wg_pack(a, l);   // O rows 8 wg ..
     const uint32_t r = (uint32_t)wave * 16;
     const uint32_t k0 = r + (lane >> 3), k1 = r + 8 + (lane >> 3);
     dma16(pk, QXD_PK_OQ + k0 * 128 + 16 * ib, lo[0]);
     dma16(pk, QXD_PK_OQ + k1 * 128 + 16 * ib, lo[1]);
     w.m0 = gnt2(pk, QXD_PK_OM + k0 * 8);
     w.m1 = gnt2(pk, QXD_PK_OM + k1 * 8);
-    w.wr = ldf4(pk, QXD_PK_RT + 16 * tid);
+}
+// ... and the router row min(wg, experts - 1) with the ffn-norm weights (register loads,
+// needed from stage Q on)
+DEV void load_wr(const QxDArgs &a, uint32_t l, WO &w) {
+    const int tid = tix();
+    w.wr = ldf4(wg_pack(a, l), QXD_PK_RT + 16 * tid);
     w.fw = ldf4(plane(a, PL_FFN_NORM, l), 16 * tid);
 }
 // router fold row M[e], values 8 tid .. 8 tid + 7 (the router's ctx-part)
@@ -903,7 +910,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
     float4 wm0 = make_float4(0.f, 0.f, 0.f, 0.f), wm1 = wm0;
     float fnw[8];
     if (wg >= QXG_HEADS) load_wq(a, 0, wq, S.wq[wave_id()]);
-    load_wo(a, 0, wo, S.wo[wave_id()]);
+    load_wr(a, 0, wo);
     uint32_t token = 0;
     __syncthreads();
     GLB uint64_t *const X = gpw(a.xch);
@@ -933,7 +940,10 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 // attention workgroups (no Q/K/V rows of their own): the cached K/V rows they
                 // attend to, arriving while the other workgroups make the Q/K/V rows
                 const bool mk = wg >= QXG_HEADS;
-                if (!mk) attn_prefetch(a, l, pos, ap);
+                if (!mk) {
+                    attn_prefetch(a, l, pos, ap);
+                    load_o(a, l, wo, S.wo[wave_id()]);   // (the others load them after their rows)
+                }
                 DMARK(l, 32);
                 // the normalised input's digits; the attn-norm weights came with the Q/K/V rows
                 double inv = 1.0;
@@ -1011,10 +1021,14 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 }
                 DMARK(l, 2);
             }
-            // prefetch: the router fold rows (stage O); workgroups that make Q/K/V rows the
-            // next layer's
+            // prefetch, where the workgroup waits: the router fold rows (stage O); workgroups
+            // that make Q/K/V rows (idle until the context arrives) the O rows and the next
+            // layer's Q/K/V rows
             load_wm(a, l, wm0, wm1);
-            if (wg >= QXG_HEADS) load_wq(a, ln, wq, S.wq[wave_id()]);
+            if (wg >= QXG_HEADS) {
+                load_o(a, l, wo, S.wo[wave_id()]);
+                load_wq(a, ln, wq, S.wq[wave_id()]);
+            }
             // ---------------------------------------------------------- stage A
             if (wg < QXG_HEADS) {
                 if (!attn_wait(a, l, ep + 1, S, ctl)) return;
@@ -1241,7 +1255,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                                    [par](int i) { return i < 6144 ? (int)(XO_H + par * XN_H) + i : (int)(XO_WT + par * XN_WT) + i - 6144; }, S, ctl))
                     return;
                 DMARK(l, 11);
-                load_wo(a, ln, wo, S.wo[wave_id()]);   // the next layer's O rows and router rows
+                load_wr(a, ln, wo);   // the next layer's router row
                 const uint32_t *wtw = S.u.m.vin + 6144;
                 double wr[QXG_TOPK];
 #pragma unroll
@@ -1341,7 +1355,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             // layer 0's rows again (also on the last step), after the argmax exchange: issued
             // earlier, its poll would wait behind them (loads complete in order)
             if (wg >= QXG_HEADS) load_wq(a, 0, wq, S.wq[wave_id()]);
-            load_wo(a, 0, wo, S.wo[wave_id()]);
+            load_wr(a, 0, wo);
             float v = __uint_as_float(S.u.hd.am[0]);
             uint32_t i = S.u.hd.am[1];
             for (int w = 1; w < NWG; ++w) {
