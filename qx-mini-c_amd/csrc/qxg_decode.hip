@@ -171,6 +171,7 @@ struct DLds {
     uint32_t bpar[NWV];          // block_any call parity of each wave
     uint32_t sub[4];             // upper_waves_sync flags of waves 4..7
     uint32_t fail;               // a poll of waves 4..7 timed out (stage G)
+    uint32_t dne[QXG_TOPK];      // the picked experts by rank (stage G, for stage D's down rows)
     union {
         struct {
             union {
@@ -489,17 +490,14 @@ DEV void addr_gu(const GuRef &g, uint64_t gu_base, uint64_t (&addr)[4]) {
 // 8-row blocks of all E experts for one row range lie together ((wg * E + e) * 8 rows), so a
 // workgroup's 8 experts' down rows lie within E * 2432 bytes (311 KB at E = 128: one or two
 // 2 MB translation pages instead of eight).
-DEV void addr_dn(const uint32_t (&ids)[QXG_TOPK], int w, uint32_t E, uint64_t dn_base, uint64_t (&addr)[3]) {
+DEV void dma_dn(const QxDArgs &a, uint32_t l, uint32_t e, uint32_t E, uint8_t *lds) {
     const int lane = tix() & 63;
-    uint32_t e = 0u;
-#pragma unroll
-    for (int q = 0; q < QXG_TOPK; ++q)
-        if (q == w) e = ids[q];
-    const uint64_t base = dn_base + ((uint64_t)blockIdx.x * E + e) * (8 * QXD_DN_ROW);
+    const GLB uint8_t *base = (const GLB uint8_t *)uni64(uni64((uint64_t)a.DN.base) + (uint64_t)l * uni64(a.DN.stride) +
+                                                          ((uint64_t)blockIdx.x * E + e) * (8 * QXD_DN_ROW));
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const uint32_t c = 64 * i + lane;
-        addr[i] = base + (c < 8 * QXD_DN_ROW / 16 ? 16 * c : 0u);
+        dma16(base, c < 8 * QXD_DN_ROW / 16 ? 16 * c : 0u, lds + 1024 * i);
     }
 }
 // The rows go through registers: 16-byte non-temporal loads, then one LDS store per chunk
@@ -1123,23 +1121,24 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
 #pragma unroll
                     for (int q = 0; q < QXG_TOPK; ++q) ids[q] = ids[q] < E ? ids[q] : 0u;
                     DMARK(l, 16);
+                    if (wv == 0 && lane < QXG_TOPK) {   // the picks for every wave's down rows (stage D)
+                        uint32_t e = 0u;
+#pragma unroll
+                        for (int q = 0; q < QXG_TOPK; ++q)
+                            if (q == lane) e = ids[q];
+                        S.dne[lane] = e;
+                    }
                     const uint64_t gub = uni64((uint64_t)a.GU.base) + (uint64_t)l * uni64(a.GU.stride);
-                    const uint64_t dnb = uni64((uint64_t)a.DN.base) + (uint64_t)l * uni64(a.DN.stride);
-                    uint64_t ga0[4], ga1[4], da0[3], da1[3];
+                    uint64_t ga0[4], ga1[4];
                     addr_gu(gu_ref(ids, wv), gub, ga0);
                     addr_gu(gu_ref(ids, wv + 4), gub, ga1);
-                    addr_dn(ids, wv, E, dnb, da0);
-                    addr_dn(ids, wv + 4, E, dnb, da1);
-                    u32x4 g0[4], g1[4], d0[3], d1[3];
+                    DMARK(l, 35);
+                    u32x4 g0[4], g1[4];
                     load_rows(ga0, g0);
                     load_rows(ga1, g1);
-                    load_rows(da0, d0);
-                    load_rows(da1, d1);
                     DMARK(l, 8);
                     store_rows(g0, S.u.m.gu[wv]);   // (the barrier below publishes them)
                     store_rows(g1, S.u.m.gu[wv + 4]);
-                    store_rows(d0, S.u.m.dn[wv]);
-                    store_rows(d1, S.u.m.dn[wv + 4]);
                     DMARK(l, 19);
                 } else {
                     // x', polled by these four waves alone (waves 0..3 are issuing the expert
@@ -1245,6 +1244,9 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 DMARK(l, 29);
                 if (tid < 24) xstf(X + XO_H + par * XN_H + 24 * wg + tid, ep + 4, S.outw[tid]);
                 DMARK(l, 31);
+                // each wave's down rows (rank w), copied to LDS behind the gate/up dots: the h
+                // poll waits behind these copies, which arrive within the exchange
+                dma_dn(a, l, S.dne[wave_id()], E, S.u.m.dn[wave_id()]);
                 DMARK(l, 10);
             }
             // ---------------------------------------------------------- stage D
@@ -1255,6 +1257,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                                    [par](int i) { return i < 6144 ? (int)(XO_H + par * XN_H) + i : (int)(XO_WT + par * XN_WT) + i - 6144; }, S, ctl))
                     return;
                 DMARK(l, 11);
+                wait_loads();   // the down rows (copied before the poll's loads, so already in)
                 load_wr(a, ln, wo);   // the next layer's router row
                 const uint32_t *wtw = S.u.m.vin + 6144;
                 double wr[QXG_TOPK];
