@@ -380,11 +380,13 @@ DEV void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); __builtin_amdgcn_fen
 DEV const GLB uint8_t *plane(const QxDArgs &a, int id, uint32_t l) {
     return (const GLB uint8_t *)(uni64((uint64_t)a.P[id].base) + (uint64_t)l * uni64(a.P[id].stride));
 }
-// the calling workgroup's decode pack of layer l
-DEV const GLB uint8_t *wg_pack(const QxDArgs &a, uint32_t l) {
-    return (const GLB uint8_t *)(uni64((uint64_t)a.PK.base) + (uint64_t)l * uni64(a.PK.stride) +
-                                 (uint64_t)blockIdx.x * QXD_PK_BYTES);
+// decode pack w of layer l (the calling workgroup's by default)
+DEV const GLB uint8_t *wg_pack(const QxDArgs &a, uint32_t l, uint32_t w = blockIdx.x) {
+    return (const GLB uint8_t *)(uni64((uint64_t)a.PK.base) + (uint64_t)l * uni64(a.PK.stride) + (uint64_t)w * QXD_PK_BYTES);
 }
+// the pack holding the router and router-fold rows the workgroup reads: workgroups past the
+// experts read expert E - 1's (unused) from one pack, so the copies stay in L2
+DEV const GLB uint8_t *router_pack(const QxDArgs &a, uint32_t l) { return wg_pack(a, l, min((uint32_t)blockIdx.x, a.experts - 1u)); }
 
 // ---------------------------------------------------------------- weight sets
 // Q/K/V rows of a wave of workgroup wg >= QXG_HEADS (the attention workgroups make none):
@@ -436,13 +438,13 @@ DEV void load_o(const QxDArgs &a, uint32_t l, WO &w, uint4 (*lo)[64]) {
 // needed from stage Q on)
 DEV void load_wr(const QxDArgs &a, uint32_t l, WO &w) {
     const int tid = tix();
-    w.wr = ldf4(wg_pack(a, l), QXD_PK_RT + 16 * tid);
+    w.wr = ldf4(router_pack(a, l), QXD_PK_RT + 16 * tid);
     w.fw = ldf4(plane(a, PL_FFN_NORM, l), 16 * tid);
 }
 // router fold row M[e], values 8 tid .. 8 tid + 7 (the router's ctx-part)
 DEV void load_wm(const QxDArgs &a, uint32_t l, float4 &m0, float4 &m1) {
     const int tid = tix();
-    const GLB uint8_t *pk = wg_pack(a, l);
+    const GLB uint8_t *pk = router_pack(a, l);
     m0 = ldf4(pk, QXD_PK_MF + 32 * tid);
     m1 = ldf4(pk, QXD_PK_MF + 32 * tid + 16);
 }
@@ -1444,12 +1446,12 @@ extern "C" __global__ __launch_bounds__(256) void qxk_interleave_head(const uint
 // The decode packs of one layer (QXD_PK_*): workgroup w of the grid (256) copies pack w:
 // for w >= 32 its 24 Q/K/V row slots (stacked rows [Q 4096 | K 512 | V 512] 24 (w - 32) ..,
 // zero past row 5119) with their 8-byte block metas; for every w its O rows 8 w .. 8 w + 7
-// and metas, router row and router-fold row (expert min(w, experts - 1)).
+// and metas; for w < experts the router row and router-fold row of expert w.
 extern "C" __global__ __launch_bounds__(256) void qxk_pack_decode(const uint8_t *qq, const uint8_t *qm, const uint8_t *kq,
                                                                    const uint8_t *km, const uint8_t *vq, const uint8_t *vm,
                                                                    const uint8_t *oq, const uint8_t *om, const float *router,
                                                                    const float *mfold, uint32_t experts, uint8_t *out) {
-    const uint32_t w = blockIdx.x, e = min(w, experts - 1u);
+    const uint32_t w = blockIdx.x;
     uint8_t *o = out + (uint64_t)w * QXD_PK_BYTES;
     auto cp = [](uint8_t *dst, const uint8_t *src, uint32_t bytes) {
         for (uint32_t i = threadIdx.x; i < bytes / 16; i += 256)
@@ -1477,8 +1479,10 @@ extern "C" __global__ __launch_bounds__(256) void qxk_pack_decode(const uint8_t 
     }
     cp(o + QXD_PK_OQ, oq + (uint64_t)w * 8 * 2048, 16384);
     cp(o + QXD_PK_OM, om + (uint64_t)w * 8 * 128, 1024);
-    cp(o + QXD_PK_RT, reinterpret_cast<const uint8_t *>(router + (uint64_t)e * 2048), 8192);
-    cp(o + QXD_PK_MF, reinterpret_cast<const uint8_t *>(mfold + (uint64_t)e * 4096), 16384);
+    if (w < experts) {   // (workgroups past the experts read pack experts - 1's)
+        cp(o + QXD_PK_RT, reinterpret_cast<const uint8_t *>(router + (uint64_t)w * 2048), 8192);
+        cp(o + QXD_PK_MF, reinterpret_cast<const uint8_t *>(mfold + (uint64_t)w * 4096), 16384);
+    }
 }
 
 // Router fold of one layer (see the top of this file): M[e][j] = sum_i W[e][i] w[i] O[i][j]

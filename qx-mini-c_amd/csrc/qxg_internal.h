@@ -167,8 +167,8 @@ struct QxDArgs {
 #define QXD_PK_OQ 24576u    // O rows 8 w .. 8 w + 7, qs (16 blocks x 128 B a row)
 #define QXD_PK_QM 40960u    // the Q/K/V slots' 8-byte block metas
 #define QXD_PK_OM 42496u    // the O rows' metas
-#define QXD_PK_RT 43520u    // router row W[e], e = min(w, experts - 1), 2048 f32
-#define QXD_PK_MF 51712u    // router fold row M[e], 4096 f32
+#define QXD_PK_RT 43520u    // w < experts: router row W[w], 2048 f32
+#define QXD_PK_MF 51712u    // w < experts: router fold row M[w], 4096 f32
 #define QXD_PK_BYTES 68096u
 // The four per-layer norm vectors share one arena: layer l's at l * QXD_NORM_STRIDE, attn
 // norm (2048 f32) at 0, ffn norm at 8192, q norm (128 f32) at 16384, k norm at 16896.
