@@ -171,6 +171,7 @@ struct DLds {
     uint32_t bpar[NWV];          // block_any call parity of each wave
     uint32_t sub[4];             // upper_waves_sync flags of waves 4..7
     uint32_t fail;               // a poll of waves 4..7 timed out (stage G)
+    double ssp[4];               // x' sums of squares of waves 4..7 (stage G)
     uint32_t dne[QXG_TOPK];      // the picked experts by rank (stage G, for stage D's down rows)
     union {
         struct {
@@ -1148,15 +1149,29 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     const GLB uint64_t *xpb = X + XO_XP + par * XN_XP;
                     if (!poll_pairs<4, 256, 256>(xpb, 2048, ep + 3, reinterpret_cast<uint32_t *>(S.xp), Ident(), ctl))
                         S.fail = 1u;
+                    DMARKT(l, 38, 256);
+                    // RMSNorm of x' (reference src/qx_format.c:3358-3371, a double sum of squares):
+                    // each thread over the 8 values it polled (pairs t + 256 k), then its wave;
+                    // the four waves' sums are added after the sync below, in the same order in
+                    // every workgroup
+                    {
+                        const int t = tid - 256;
+                        double s8 = 0.0;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const float2 v = *reinterpret_cast<const float2 *>(S.xp + 2 * (t + 256 * k));
+                            s8 += (double)v.x * (double)v.x;
+                            s8 += (double)v.y * (double)v.y;
+                        }
+                        s8 = wave_total_d(s8);
+                        if (lane == 0) S.ssp[wv - 4] = s8;
+                    }
                     upper_waves_sync(S, ep + 3);
                     DMARKT(l, 9, 256);
-                    // RMSNorm of x' (reference src/qx_format.c:3358-3371, double sum of squares,
-                    // each wave over all 2048 values) and the digits of values 512 (w - 4) ..
-                    double ss = 0.0;
-#pragma unroll 8
-                    for (int k = 0; k < 32; ++k) { const double v = (double)S.xp[lane + 64 * k]; ss += v * v; }
-                    ss = wave_total_d(ss);
+                    // ... and the digits of values 512 (w - 4) ..
+                    const double ss = (S.ssp[0] + S.ssp[1]) + (S.ssp[2] + S.ssp[3]);
                     const double inv = 1.0 / sqrt(ss / 2048.0 + 1.0e-6);
+                    DMARKT(l, 37, 256);
                     if (wv == 4 && lane == 0) S.xinv = inv;
                     const int c = 64 * (wv - 4) + lane;   // chunk of 8 values; fnw holds their weights
                     float y[8];
