@@ -185,6 +185,7 @@ struct DLds {
         struct {
             float bv[NWV];
             uint32_t bi[NWV];
+            uint32_t next;           // the head's group counter (head_rows)
             uint32_t am[XN_AM];
             alignas(16) uint8_t rows[NWV][HEAD_NI * 1024];   // each wave's staged head rows
         } hd;
@@ -807,8 +808,9 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
 }
 
 // ---------------------------------------------------------------- head
-// Output RMSNorm + Q6_K head (src/qx_format.c:3554-3738) over the digits in S.dig: wave gw
-// takes rows R gw .. R gw + R - 1, then R (gw + 2048) ..  A pass's R interleaved rows
+// Output RMSNorm + Q6_K head (src/qx_format.c:3554-3738) over the digits in S.dig: group g
+// is rows R g .. R g + R - 1; workgroup w's groups are w + 256 j, its waves taking them in
+// turn (S.u.hd.next, zeroed before the call).  A pass's R interleaved rows
 // (R * 105 16-byte chunks, contiguous) come in with HEAD_NI full-width loads and go to the
 // wave's LDS region; the next pass's loads are issued before this pass's dots.  Lane (b, ib)
 // then reads its sub-block's ql, qh, scale pair and d from LDS.  Returns the workgroup's best
@@ -817,7 +819,6 @@ DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi,
     constexpr int R = HEAD_R;
     const int lane = tix() & 63, wave = wave_id();
     const int b = lane >> 3, ib = lane & 7, hh = ib >> 2, k = ib & 3;
-    const uint32_t gw = NWV * blockIdx.x + wave;
     Dig g;
     load_dig(S.dig, lane, g);
     const Q6Bias bias = q6_bias(g);
@@ -838,12 +839,23 @@ DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi,
             v[i] = __builtin_nontemporal_load((const GLB u32x4 *)(hb + (uint64_t)row * QXD_HEAD_ROW + 16 * ch));
         }
     };
-    if (gw < groups) issue(gw);
-    for (uint32_t p = gw; p < groups; p += NWV * NWG) {
+    // the workgroup's groups blockIdx.x + NWG j, j taken in turn from an LDS counter: the two
+    // waves of a SIMD are not served equally (the older one issues first), so with fixed
+    // shares waves 4..7 finished 13 us after waves 0..3, alone and with half the loads in
+    // flight.  Each wave's groups still ascend.
+    auto take = [&]() -> uint32_t {
+        uint32_t j = 0u;
+        if (lane == 0) j = __hip_atomic_fetch_add(&S.u.hd.next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return blockIdx.x + NWG * (uint32_t)__builtin_amdgcn_readfirstlane((int)j);
+    };
+    uint32_t p = take();
+    if (p < groups) issue(p);
+    while (p < groups) {
 #pragma unroll
         for (int i = 0; i < HEAD_NI; ++i) *reinterpret_cast<u32x4 *>(rows + 1024 * i + 16 * lane) = v[i];
         wave_lds_sync();
-        if (p + NWV * NWG < groups) issue(p + NWV * NWG);   // the next pass's rows, in flight during the dots
+        const uint32_t pn = take();
+        if (pn < groups) issue(pn);   // the next pass's rows, in flight during the dots
         float part[R], out[R];
 #pragma unroll
         for (int rr = 0; rr < R; ++rr) {
@@ -868,6 +880,7 @@ DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi,
                 if (val > best) { best = val; besti = r; }   // rows ascend: ties keep the lower index
             }
         }
+        p = pn;
     }
     bv = best;
     bi = besti;
@@ -1345,6 +1358,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             if (!wait_xch2<2>(X + XO_X + (L & 1) * XN_X, 2048, eph, reinterpret_cast<uint32_t *>(S.xs), Ident(), S, ctl))
                 return;
             DMARK(48, 1);
+            if (tid == 0) S.u.hd.next = 0u;   // (published by the barrier in vec_digits)
             const bool fin = vec_digits<2048, true>(S.xs, onw, S);
             float bv;
             uint32_t bi;
@@ -1352,6 +1366,10 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             DMARK(48, 2);
             head_rows(a, S, fin, bv, bi, nonfin);
             DMARK(48, 3);
+            DMARKT(48, 6, 64);
+            DMARKT(48, 7, 192);
+            DMARKT(48, 8, 256);
+            DMARKT(48, 9, 448);
             if (nonfin) gpw(a.st)->nonfinite = 1u;
             // workgroup best, then every workgroup reads all the bests
             for (int o = 32; o > 0; o >>= 1) {
