@@ -458,34 +458,56 @@ DEV void load_w8(const GLB uint8_t *p, float (&w)[8]) {
     w[0] = x0.x; w[1] = x0.y; w[2] = x0.z; w[3] = x0.w;
     w[4] = x1.x; w[5] = x1.y; w[6] = x1.z; w[7] = x1.w;
 }
-// routed experts' rows of a wave: gate/up units 3 gw .. 3 gw + 2 (one expert per wave:
-// 768 = 256 * 3); down row 8 wg + w of all 8 ranks (lane 8 r + k: rank r, sub-block k of
-// the 3 blocks)
-// Routed experts' rows, staged in LDS as whole 16-byte chunks.  A CU's vector-memory unit
-// spends about the same time per load instruction whatever its width, so the rows are
-// Gate/up of wave w's 3 units (3 consecutive rows r0.. of expert e): 3 * QXD_GU_UNIT =
-// 3552 contiguous bytes, chunks [0, 222) (4 instructions, 4 KB of LDS; lanes past 222 repeat
-// chunk 0).  In LDS unit uu sits at uu * QXD_GU_UNIT: gate qs +0, sc +512, d +576, up qs
-// +592, sc +1104, d +1168.
+// Routed experts' rows, staged in LDS as whole 16-byte chunks (a CU's vector-memory unit
+// spends about the same time per load instruction whatever its width).  A gate/up unit sits
+// at uu * QXD_GU_UNIT: gate qs +0, sc +512, d +576, up qs +592, sc +1104, d +1168.
 constexpr uint32_t GU_GSC = 512, GU_GD = 576, GU_UQ = 592, GU_USC = 1104, GU_UD = 1168;
-struct GuRef {
-    uint32_t e, r0;   // expert, first row
-};
-DEV GuRef gu_ref(const uint32_t (&ids)[QXG_TOPK], int w) {
-    const int u0 = 3 * (NWV * (int)blockIdx.x + w);
+// Gate/up dots of NU units at ub (LDS, QXD_GU_UNIT apart) for lane (b, ib) of each 32-value
+// sub-block: p[k] gate and p[4 + k] up of unit k (the rest 0).  Sub-blocks in the order gate,
+// up of unit 0, 1, ..; a sub-block's index words are read two ahead and its codebook entries
+// one ahead of its dot.
+template <int NU>
+DEV void gu_dots(const uint8_t *ub, uint32_t q, uint32_t sc, uint32_t d, const DLds &S, const Dig &g, float (&p)[8]) {
+    constexpr int NS = 2 * NU;
+    uint2 qs[3];
+    uint32_t scs[3], ds[3];
+    auto ld = [&](int s2) {
+        const uint8_t *u = ub + (s2 >> 1) * QXD_GU_UNIT;
+        const bool up = s2 & 1;
+        const uint32_t oq = up ? GU_UQ : 0u, os = up ? GU_USC : GU_GSC, od = up ? GU_UD : GU_GD;
+        qs[s2 % 3] = *reinterpret_cast<const uint2 *>(u + oq + q);
+        scs[s2 % 3] = u[os + sc];
+        ds[s2 % 3] = *reinterpret_cast<const uint16_t *>(u + od + d);
+    };
+    ld(0);
+    ld(1);
+    Iq2Look kl[2];
+    iq2_look(qs[0], S.g2, S.sel, kl[0]);
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) {
+        if (s2 + 2 < NS) ld(s2 + 2);
+        if (s2 + 1 < NS) iq2_look(qs[(s2 + 1) % 3], S.g2, S.sel, kl[(s2 + 1) & 1]);
+        p[(s2 & 1) ? 4 + (s2 >> 1) : (s2 >> 1)] = iq2_dot(kl[s2 & 1], scs[s2 % 3], ds[s2 % 3], g);
+    }
+#pragma unroll
+    for (int k = NU; k < 4; ++k) p[k] = p[4 + k] = 0.0f;
+}
+// The workgroup's 24 units (24 wg .. 24 wg + 23 of the stacked 8 x 768, one rank: 24 | 768)
+// lie contiguously in HBM (28,416 bytes, 1776 chunks); wave w < 4 loads chunks 448 w ..
+// 448 w + 447 (7 instructions, chunks past 1775 repeat the last one) to LDS byte 16 chunk.
+DEV void addr_gu_wg(const uint32_t (&ids)[QXG_TOPK], int w, uint64_t gu_base, uint64_t (&addr)[7], uint32_t (&lds_off)[7]) {
+    const int lane = tix() & 63;
+    const uint32_t u0 = 24u * blockIdx.x, rank = u0 / QXG_FFN;
     uint32_t e = 0u;
 #pragma unroll
     for (int q = 0; q < QXG_TOPK; ++q)
-        if (q == u0 / QXG_FFN) e = ids[q];
-    return GuRef{e, (uint32_t)(u0 % QXG_FFN)};
-}
-DEV void addr_gu(const GuRef &g, uint64_t gu_base, uint64_t (&addr)[4]) {
-    const int lane = tix() & 63;
-    const uint64_t base = gu_base + (uint64_t)(g.e * QXG_FFN + g.r0) * QXD_GU_UNIT;
+        if ((uint32_t)q == rank) e = ids[q];
+    const uint64_t base = gu_base + (uint64_t)(e * QXG_FFN + u0 % QXG_FFN) * QXD_GU_UNIT;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t c = 64 * i + lane;
-        addr[i] = base + (c < 3 * QXD_GU_UNIT / 16 ? 16 * c : 0u);
+    for (int i = 0; i < 7; ++i) {
+        const uint32_t c = min(448u * w + 64u * i + lane, 24u * QXD_GU_UNIT / 16 - 1u);
+        addr[i] = base + 16 * c;
+        lds_off[i] = 16 * c;
     }
 }
 // Down rows 8 wg .. 8 wg + 7 of the expert of rank w: 8 * QXD_DN_ROW = 2432 contiguous bytes,
@@ -1145,16 +1167,16 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                         S.dne[lane] = e;
                     }
                     const uint64_t gub = uni64((uint64_t)a.GU.base) + (uint64_t)l * uni64(a.GU.stride);
-                    uint64_t ga0[4], ga1[4];
-                    addr_gu(gu_ref(ids, wv), gub, ga0);
-                    addr_gu(gu_ref(ids, wv + 4), gub, ga1);
+                    uint64_t ga[7];
+                    uint32_t go[7];
+                    addr_gu_wg(ids, wv, gub, ga, go);
                     DMARK(l, 35);
-                    u32x4 g0[4], g1[4];
-                    load_rows(ga0, g0);
-                    load_rows(ga1, g1);
+                    u32x4 g[7];
+                    load_rows(ga, g);
                     DMARK(l, 8);
-                    store_rows(g0, S.u.m.gu[wv]);   // (the barrier below publishes them)
-                    store_rows(g1, S.u.m.gu[wv + 4]);
+#pragma unroll
+                    for (int i = 0; i < 7; ++i)   // (the barrier below publishes them)
+                        *reinterpret_cast<u32x4 *>(S.u.m.gu[0] + go[i]) = g[i];
                     DMARK(l, 19);
                 } else {
                     // x', polled by these four waves alone (waves 0..3 are issuing the expert
@@ -1228,46 +1250,31 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 load_dig(S.dig, lane, g);
                 float p[8], o[8];
                 {
-                    // six sub-blocks (gate then up of units 0..2): their index words first, then
-                    // the codebook reads of sub-block i + 1 in flight while sub-block i computes
+                    // waves 0..3 take 4 of the workgroup's 24 units, waves 4..7 two (the older
+                    // wave of a SIMD issues first: with 3 each, waves 4..7 finished 1 us later)
                     const uint32_t b = lane >> 3, ib = lane & 7;
                     const uint32_t q = b * 64 + ib * 8, sc = b * 8 + ib, d = b * 2;
-                    uint2 qs[6];
-                    uint32_t scs[6], ds[6];
-#pragma unroll
-                    for (int i = 0; i < 6; ++i) {
-                        const uint8_t *u = S.u.m.gu[wv] + (i % 3) * QXD_GU_UNIT;
-                        const uint32_t oq = i < 3 ? 0u : GU_UQ, os = i < 3 ? GU_GSC : GU_USC, od = i < 3 ? GU_GD : GU_UD;
-                        qs[i] = *reinterpret_cast<const uint2 *>(u + oq + q);
-                        scs[i] = u[os + sc];
-                        ds[i] = *reinterpret_cast<const uint16_t *>(u + od + d);
-                    }
-                    Iq2Look kl[2];
-                    iq2_look(qs[0], S.g2, S.sel, kl[0]);
-#pragma unroll
-                    for (int i = 0; i < 6; ++i) {
-                        if (i + 1 < 6) iq2_look(qs[i + 1], S.g2, S.sel, kl[(i + 1) & 1]);
-                        p[i < 3 ? i : i + 1] = iq2_dot(kl[i & 1], scs[i], ds[i], g);
-                    }
+                    const uint8_t *ub = S.u.m.gu[0] + (wv < 4 ? 4 * wv : 16 + 2 * (wv - 4)) * QXD_GU_UNIT;
+                    if (wv < 4) gu_dots<4>(ub, q, sc, d, S, g, p);
+                    else gu_dots<2>(ub, q, sc, d, S, g, p);
                 }
-                p[3] = p[7] = 0.0f;
                 rows_reduce<8>(p, o, lane);
                 DMARK(l, 18);
                 DMARKT(l, 28, 256);
                 DMARKT(l, 30, 448);
                 (void)ib;
                 (void)gw;
-                {   // lane k < 3: unit k (selects, then one pass for the three lanes)
+                {   // lane k < units: unit k (selects, then one pass for the lanes)
                     float gv = o[0], uv = o[4];
 #pragma unroll
-                    for (int k = 1; k < 3; ++k)
+                    for (int k = 1; k < 4; ++k)
                         if (lane == k) { gv = o[k]; uv = o[4 + k]; }
                     gv = isfinite(gv) ? gv : 0.0f;
                     uv = isfinite(uv) ? uv : 0.0f;
-                    if (lane < 3) {
+                    if (lane < (wave < 4 ? 4 : 2)) {
                         // reference src/qx_format.c:5298, 2511-2513: h = (float)(silu((double)g) * (double)u)
                         const double sg = (double)gv / (1.0 + exp(-(double)gv));
-                        S.outw[3 * wave + lane] = (float)(sg * (double)uv);
+                        S.outw[(wave < 4 ? 4 * wave : 16 + 2 * (wave - 4)) + lane] = (float)(sg * (double)uv);
                     }
                 }
                 __syncthreads();
