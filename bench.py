@@ -95,11 +95,14 @@ def cpu_baseline(model_path, prompt_kv, first_token, p0, budget_s):
                       f"wall {wall:.2f} s, process CPU {cpu:.2f} s"}
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a plain
-    device copy of known size); None when no summary is committed for it."""
-    key = f"traffic_bytes_per_launch[{kernel}]="
+def measured_traffic_ratio(kernel):
+    """HBM bytes over algorithmic bytes of `kernel` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a plain device
+    copy of known size, divided by the profiled launch's algorithmic bytes): (ratio, file), or
+    (None, None) when no summary is committed for it.  The ratio carries over to a launch of
+    another step count (the counted excess is per token), so `traffic` is this run's
+    algorithmic bytes times it."""
+    key = f"traffic_ratio[{kernel}]="
     for name in ("decode_config4_persistent_traffic.md", "decode_config4_per_phase_traffic.md"):
         path = os.path.join(ROOT, "profiles", name)
         if not os.path.exists(path):
@@ -107,8 +110,8 @@ def measured_traffic(kernel):
         with open(path) as f:
             for line in f:
                 if line.startswith(key):
-                    return int(line[len(key):])
-    return None
+                    return float(line[len(key):]), f"profiles/{name}"
+    return None, None
 
 
 def copy_calibration(mib):
@@ -175,6 +178,63 @@ def qxg_kernels():
     return qxg.KERNELS
 
 
+def long_context_leg(ctx, args):
+    """Decode at the end of the 4096-long context (config 5's "4096-long INT8 KV"): the
+    cache holds seeded INT8 rows at positions 0..p0-1 of every layer, then one persistent
+    launch generates n greedy tokens at positions p0..4095; the KV rows read per token grow
+    to 203 MB at position 4095, counted in the roofline."""
+    n = args.long_steps
+    p0 = 4096 - n
+    rng = np.random.default_rng(args.seed + 9)
+    ctx.kv_create(LAYERS, 4096)
+    t0 = time.perf_counter()
+    for layer in range(LAYERS):
+        k = rng.integers(-127, 128, size=(p0, 512), dtype=np.int8)
+        v = rng.integers(-127, 128, size=(p0, 512), dtype=np.int8)
+        ks = (rng.uniform(0.5, 2.0, size=p0) / 127.0).astype(np.float32)
+        vs = (rng.uniform(0.5, 2.0, size=p0) / 127.0).astype(np.float32)
+        ctx.kv_write(layer, 0, k, v, ks, vs)
+    log(f"long context: seeded {p0} INT8 rows x {LAYERS} layers in {time.perf_counter() - t0:.1f} s")
+    ctx.generate([11], n, p0)                      # warmup (rewrites rows p0.. itself)
+    t0 = time.perf_counter()
+    toks, dev_ms = ctx.generate([11], n, p0)
+    wall = time.perf_counter() - t0
+    tok_s = n / wall
+    token_bytes = TOKEN_BYTES + kv_bytes(p0, n) / n
+    log(f"long context: {n} tokens at positions {p0}..4095: {wall * 1e3:.2f} ms wall ({tok_s:.1f} tok/s)")
+    return {"workload": f"{n} greedy tokens at positions {p0}..4095 over a seeded INT8 KV cache of the same model "
+                        f"(4096-long context)", "positions": f"{p0}..4095", "steps": n,
+            "tok_s": round(tok_s, 1), "ms_per_token": round(wall * 1e3 / n, 4),
+            "algorithmic_bytes_per_token": int(token_bytes),
+            "frac": round(token_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def mix_decode_leg(args):
+    """Decode on the real checkpoint's per-layer quant mix (layer l % 4: Q5_K or IQ4_XS V/O,
+    IQ2_S or IQ2_XS gate/up, IQ3_XXS / IQ4_XS / IQ3_S down): these layers decode one kernel per
+    phase (replayed step graph)."""
+    import qxg
+    model = qxg.MemModel(LAYERS, VOCAB, EXPERTS, True, True, seed=args.seed, mix=1)
+    ctx = qxg.Context(0)
+    ctx.load(model.path, verify=False)
+    prompt = np.random.default_rng(args.seed).integers(0, VOCAB, size=8).astype(np.uint32)
+    n = args.mix_steps
+    ctx.kv_create(LAYERS, 8 + 2 * n + 1)
+    first, _ = ctx.generate(prompt, 1, 0)
+    ctx.generate([int(first[0])], n, 8)            # warmup (records the step graph)
+    ctx.kv_create(LAYERS, 8 + 2 * n + 1)
+    first, _ = ctx.generate(prompt, 1, 0)
+    t0 = time.perf_counter()
+    ctx.generate([int(first[0])], n, 8)
+    wall = time.perf_counter() - t0
+    ctx.close()
+    model.close()
+    log(f"real-mix decode: {n} tokens in {wall * 1e3:.2f} ms ({n / wall:.1f} tok/s)")
+    return {"workload": f"{n} greedy tokens at positions 8..{7 + n} after an 8-token prompt, the 48-layer model in "
+                        "the real checkpoint's per-layer formats", "steps": n, "tok_s": round(n / wall, 1),
+            "ms_per_token": round(wall * 1e3 / n, 4), "layer_path": "per_phase (graph replay)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -196,6 +256,13 @@ def main():
     ap.add_argument("--real-mix", action="store_true",
                     help="with --prefill-only: the model in the real checkpoint's per-layer formats (layer l %% 4: "
                          "Q5_K or IQ4_XS attention V/O, IQ2_S or IQ2_XS gate/up, IQ3_XXS, IQ4_XS or IQ3_S down)")
+    ap.add_argument("--long-steps", type=int, default=128,
+                    help="long-context leg: greedy tokens at positions 4096-N..4095 over a seeded KV (0: skip)")
+    ap.add_argument("--mix-steps", type=int, default=32,
+                    help="real-mix decode leg: greedy tokens on the real checkpoint's per-layer formats (0: skip)")
+    ap.add_argument("--attention-chunks", type=int, default=0, metavar="N",
+                    help="persistent decode: attend by kv head and chunk from N = pos + 1 positions on "
+                         "(0: the library default; 1: always; 4097: never)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-sized device buffer (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -221,6 +288,8 @@ def main():
     log(f"generated the {LAYERS}-layer model in memory in {time.perf_counter() - t0:.1f} s ({model.path})")
     ctx = qxg.Context(0)
     ctx.set_layer_path(args.layer_path)
+    if args.attention_chunks:
+        ctx.set_attention_chunks(args.attention_chunks)
     if args.roofline_kernel is None:
         args.roofline_kernel = "layers" if args.layer_path else "gate_up"
     t0 = time.perf_counter()
@@ -269,6 +338,7 @@ def main():
     if args.roofline_kernel == "layers":   # every step of the call, plus the INT8 KV rows read at positions 8..8+K-1
         kb = TOKEN_BYTES * args.steps + kv_bytes(prompt_len, args.steps)
     achieved = kb / avg_kernel_s / 1e9
+    ratio, ratio_src = measured_traffic_ratio(args.roofline_kernel)
     token_bytes = TOKEN_BYTES + kv_bytes(prompt_len, args.steps) / args.steps
     out = {
         "metric": "batch-1 decode tok/s (48 layers + Q6_K head)",
@@ -281,7 +351,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32 result; activations as 22-bit block-fixed-point int8 digit planes x exact integer weight "
+                 "codes (int32 v_dot4 sums), f32/f64 combination and softmax",
         "data": "synthetic: seeded random-init QXF1 (generator qxgen.c), seeded 8-token prompt",
         "config": {"workload": "config4: Qwen3-30B-A3B-shaped decode, 48 layers + Q6_K head 2048x151936, "
                                "greedy tokens after an 8-token prompt, INT8 KV",
@@ -291,8 +362,10 @@ def main():
                    "layer_path": "persistent" if args.layer_path else "per_phase"},
         "roofline": {"bound": "hbm", "kernel": args.roofline_kernel, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(args.roofline_kernel), "bytes_per_launch": kb, "avg_launch_us": round(avg_kernel_s * 1e6, 3),
-                     "launches": launches},
+                     "traffic": round(ratio * kb) if ratio else None, "traffic_ratio": ratio,
+                     "traffic_note": (f"HBM bytes of this launch = its algorithmic bytes x the FETCH_SIZE+WRITE_SIZE "
+                                      f"ratio measured in {ratio_src}") if ratio else None,
+                     "bytes_per_launch": kb, "avg_launch_us": round(avg_kernel_s * 1e6, 3), "launches": launches},
         "token_roofline": {"algorithmic_bytes_per_token": int(token_bytes),
                            "achieved_GBs": round(token_bytes * tok_s / 1e9, 1),
                            "frac": round(token_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
@@ -305,7 +378,11 @@ def main():
         prompt_kv = [ctx.kv_read(l, 0, prompt_len) for l in range(LAYERS)]
     if args.prefill_tokens:
         out["prefill"] = prefill_leg(ctx, args)
+    if args.long_steps and args.layer_path:
+        out["long_context"] = long_context_leg(ctx, args)
     ctx.close()
+    if args.mix_steps:
+        out["real_mix_decode"] = mix_decode_leg(args)
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle, 1 thread) ...")
         out["cpu_baseline"] = cpu_baseline(model.path, prompt_kv, first, prompt_len, args.cpu_budget)

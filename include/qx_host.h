@@ -89,6 +89,14 @@ typedef struct qxgen_spec {
                                1: the real checkpoint's per-layer mix, layer l by l % 4:
                                0 -> (IQ4_XS v/o, IQ2_XS gate/up, IQ3_XXS down), 1 -> (Q5_K, IQ2_S, IQ4_XS),
                                2 -> (IQ4_XS, IQ2_XS, IQ3_S), 3 -> (Q5_K, IQ2_S, IQ3_S); q/k stay IQ4_XS */
+    uint32_t outliers;      /* planted outlier channels (a test input, not a model distribution).
+                               0: none.  1: single x1000 channels - channel 128 k + 5 of every
+                               2048-long norm and channel 5 of the q/k norms, fp16 d x1000 in V row
+                               128 k + 3 (the context) and O row 11 (the residual stream).  2: a
+                               compound stress pattern - as 1, plus x1e6 in channel 1001 of the
+                               attention and output norms and fp16 d x1000 in gate row 7 and down
+                               row 13 of every expert (h groups spanning ~1e4-1e5, and expert
+                               outputs that cancel in channel 13) */
 } qxgen_spec;
 
 /* Writes a QXF1 file at `path` (truncating).  The bytes are a pure function of

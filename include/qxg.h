@@ -235,6 +235,20 @@ int qxg_set_activation(qxg_ctx *ctx, uint32_t activation_format, char *err, uint
  * The reference keeps no such record; this is the readback the router parity tests use. */
 int qxg_decode_routing(qxg_ctx *ctx, uint32_t layers, uint32_t *ids, double *weights, char *err, uint64_t err_len);
 
+/* The two halves of every layer in the last step run by qxg_decode_token, before their
+ * residual adds: attn_out[l*2048 ..] the attention output (the O projection of the
+ * context; the reference's "attn-out" dump phase, src/qx_format.c:6420-6423) and
+ * moe_out[l*2048 ..] the weighted expert sum ("ffn-moe-out", :5296-5309).  Either may be
+ * NULL.  Same-input replay of each half on its own: the residual stream can be many orders
+ * of magnitude larger than a half, so a layer output alone would hide an error in it. */
+int qxg_decode_halves(qxg_ctx *ctx, uint32_t layers, float *attn_out, float *moe_out, char *err, uint64_t err_len);
+
+/* Persistent decode only (no reference counterpart): from n = position + 1 >=
+ * min_positions on, stage A attends by (kv head, 64-position chunk) over every workgroup
+ * and merges the chunks' partial softmax results; below it the 32 q-head workgroups walk
+ * the cache themselves.  Default 257; 1 chunks every position, 4097 never. */
+int qxg_set_attention_chunks(qxg_ctx *ctx, uint32_t min_positions);
+
 /* Same-input seam of the Q8_K quantizer the q8_k_compat kernels use: n values (a
  * multiple of 256, at most 4096) -> n/256 blocks of 292 bytes in ggml's block_q8_K
  * layout {f32 d, int8 qs[256], int16 bsums[16]}.  Replaces qx_quantize_q8_k as exposed

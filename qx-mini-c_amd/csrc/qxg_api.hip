@@ -124,6 +124,8 @@ struct qxg_ctx {
     // work buffers
     float *x = nullptr, *qkv = nullptr, *ctxv = nullptr, *h = nullptr, *logits = nullptr;
     float *vcur = nullptr, *attn = nullptr, *moe = nullptr, *norm = nullptr, *layer_dump = nullptr;
+    float *half_dump = nullptr;    // [layer][attention 2048 | MoE 2048] of the last qxg_decode_token step
+    uint32_t att_split_min = QXD_SPLIT_MIN_DEFAULT;   // persistent decode: chunked stage A from n = pos + 1 on
     double *rlog = nullptr;
     uint32_t *route_ids = nullptr;  // [layer][8] experts of the last step, in rank order
     double *route_w = nullptr;      // [layer][8] their renormalised weights
@@ -151,6 +153,7 @@ struct qxg_ctx {
     uint64_t gu_stride = 0, dn_stride = 0;
     uint64_t mfold_stride = 0;
     uint64_t *xch = nullptr;
+    uint64_t *xpart = nullptr;       // partial results of the chunked attention (2 x QXD_PART_WORDS)
     uint32_t next_ep = 0;            // epoch base of the next persistent launch
     uint32_t *abort = nullptr;
     uint8_t *scratch = nullptr;      // device address of this GPU's static workspace (qxg_dequant_blocks_static)
@@ -373,7 +376,7 @@ bool persistent(const qxg_ctx *c) {
 }
 
 struct DecodeDumps {
-    float *layer = nullptr, *res = nullptr, *logits = nullptr;
+    float *layer = nullptr, *res = nullptr, *logits = nullptr, *half = nullptr;
     uint32_t *rids = nullptr;
     double *rw = nullptr;
 };
@@ -385,7 +388,9 @@ bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0,
                    const DecodeDumps &d, char *err, uint64_t n) {
     const uint64_t phases = (uint64_t)steps * QXD_PHASES(c->layers) + 1;
     if ((uint64_t)c->next_ep + phases >= 0x7fffffffull) {
-        if (!hip_ok(hipMemsetAsync(c->xch, 0, QXD_XCH_WORDS * 8ull, c->s), err, n, "exchange buffers")) return false;
+        if (!hip_ok(hipMemsetAsync(c->xch, 0, QXD_XCH_WORDS * 8ull, c->s), err, n, "exchange buffers") ||
+            !hip_ok(hipMemsetAsync(c->xpart, 0, 2ull * QXD_PART_WORDS * 8, c->s), err, n, "exchange buffers"))
+            return false;
         c->next_ep = 0;
     }
     QxDArgs a{};
@@ -405,7 +410,9 @@ bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0,
     a.tokens = c->tokens;
     a.st = c->st;
     a.xch = c->xch;
-    a.logits = d.logits; a.d_layer = d.layer; a.d_rids = d.rids; a.d_rw = d.rw; a.d_res = d.res;
+    a.xpart = c->xpart;
+    a.logits = d.logits; a.d_layer = d.layer; a.d_rids = d.rids; a.d_rw = d.rw; a.d_res = d.res; a.d_half = d.half;
+    a.att_split_min = c->att_split_min;
     a.abort = c->abort;
     a.timeout = DECODE_WAIT_TICKS;
     a.sqrt_hd = std::sqrt(128.0);
@@ -935,6 +942,8 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
     // tagged exchange buffers start at epoch 0, which no launch uses
     ok = ok && hip_ok(hipMalloc(&c->xch, QXD_XCH_WORDS * 8ull), err, err_len, "exchange buffers") &&
          hip_ok(hipMemset(c->xch, 0, QXD_XCH_WORDS * 8ull), err, err_len, "exchange buffers") &&
+         hip_ok(hipMalloc(&c->xpart, 2ull * QXD_PART_WORDS * 8), err, err_len, "exchange buffers") &&
+         hip_ok(hipMemset(c->xpart, 0, 2ull * QXD_PART_WORDS * 8), err, err_len, "exchange buffers") &&
          hip_ok(hipMalloc(&c->abort, 4), err, err_len, "abort flag") &&
          hip_ok(hipMemset(c->abort, 0, 4), err, err_len, "abort flag");
     ok = ok && hip_ok(hipEventCreate(&c->e0), err, err_len, "event") && hip_ok(hipEventCreate(&c->e1), err, err_len, "event");
@@ -952,8 +961,8 @@ void qxg_close(qxg_ctx *c) {
     void *bufs[] = {c->T.g2, c->T.g3, c->T.sel, c->T.rope_cos, c->T.rope_sin, c->T.g2s, c->T.g3s, c->T.sel8, c->kc, c->vc, c->ks, c->vs, c->x,
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
                     c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging,
-                    c->xch, c->abort, c->apart, c->route_ids, c->route_w, c->mfold, c->gu_il, c->dn_il, c->head_il, c->dpack,
-                    c->T.rope_cs};
+                    c->xch, c->xpart, c->abort, c->apart, c->route_ids, c->route_w, c->mfold, c->gu_il, c->dn_il, c->head_il, c->dpack,
+                    c->T.rope_cs, c->half_dump};
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (void *p : c->arenas) (void)hipFree(p);
     for (void *p : c->pf.all) (void)hipFree(p);
@@ -1059,14 +1068,15 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
                      (void **)&c->vcur, (void **)&c->attn, (void **)&c->moe, (void **)&c->norm,
                      (void **)&c->layer_dump, (void **)&c->rlog, (void **)&c->cand_v, (void **)&c->top_v,
                      (void **)&c->cand_i, (void **)&c->top_i, (void **)&c->tokens, (void **)&c->dig, (void **)&c->apart,
-                     (void **)&c->route_ids, (void **)&c->route_w};
+                     (void **)&c->route_ids, (void **)&c->route_w, (void **)&c->half_dump};
     for (void **b : bufs) if (*b) { (void)hipFree(*b); *b = nullptr; }
     const uint64_t V = c->vocab ? c->vocab : 1;
     const uint64_t sizes[] = {2048 * 4, 5120 * 4, 4096 * 4, 8 * 768 * 4, V * 4, 512 * 4, 2048 * 4, 2048 * 4, 2048 * 4,
                               (uint64_t)(layers ? layers : 1) * 2048 * 4, 128 * 8, TOPK_BLOCKS * QXG_MAX_TOPN * 4,
                               QXG_MAX_TOPN * 4, TOPK_BLOCKS * QXG_MAX_TOPN * 4, QXG_MAX_TOPN * 4,
                               (QXG_MAX_CTX + 2) * 4, (64 * 28 + 4) * 4, QXG_ATT_PART_BYTES,
-                              (uint64_t)(layers ? layers : 1) * 8 * 4, (uint64_t)(layers ? layers : 1) * 8 * 8};
+                              (uint64_t)(layers ? layers : 1) * 8 * 4, (uint64_t)(layers ? layers : 1) * 8 * 8,
+                              (uint64_t)(layers ? layers : 1) * 4096 * 4};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i)
         if (!hip_ok(hipMalloc(bufs[i], sizes[i]), err, err_len, "work buffers")) return 0;
     if (!hip_ok(hipMemset(c->tokens, 0, sizes[15]), err, err_len, "work buffers")) return 0;
@@ -1148,7 +1158,7 @@ int qxg_decode_token(qxg_ctx *c, uint32_t token, uint32_t position, int run_head
         // one step of the persistent decode (its head writes every logit), then the top-N
         // of those logits by the per-phase selection kernels
         DecodeDumps d;
-        d.layer = c->layer_dump; d.res = c->x; d.rids = c->route_ids; d.rw = c->route_w;
+        d.layer = c->layer_dump; d.res = c->x; d.rids = c->route_ids; d.rw = c->route_w; d.half = c->half_dump;
         d.logits = run_head ? c->logits : nullptr;
         if (!launch_decode(c, 1, run_head ? 1 : 2, position, false, d, err, err_len)) return 0;
         if (run_head) {
@@ -1160,8 +1170,8 @@ int qxg_decode_token(qxg_ctx *c, uint32_t token, uint32_t position, int run_head
     } else {
         hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
         for (uint32_t l = 0; l < c->layers; ++l) {
-            launch_attention(c, l, c->x, nullptr, nullptr);
-            launch_moe(c, l, c->x, nullptr);
+            launch_attention(c, l, c->x, c->half_dump + 4096ull * l, nullptr);
+            launch_moe(c, l, c->x, c->half_dump + 4096ull * l + 2048);
             if (layer_out)
                 (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * 4, hipMemcpyDeviceToDevice, c->s);
         }
@@ -1573,6 +1583,24 @@ int qxg_decode_routing(qxg_ctx *c, uint32_t layers, uint32_t *ids, double *weigh
     return hip_ok(hipStreamSynchronize(c->s), err, err_len, "stream") &&
            hip_ok(hipMemcpy(ids, c->route_ids, (uint64_t)layers * 8 * 4, hipMemcpyDeviceToHost), err, err_len, "read") &&
            hip_ok(hipMemcpy(weights, c->route_w, (uint64_t)layers * 8 * 8, hipMemcpyDeviceToHost), err, err_len, "read");
+}
+
+int qxg_decode_halves(qxg_ctx *c, uint32_t layers, float *attn_out, float *moe_out, char *err, uint64_t err_len) {
+    if (!check_ready(c, false, err, err_len)) return 0;
+    if (!layers || layers > c->layers) { set_err(err, err_len, "invalid argument"); return 0; }
+    (void)hipSetDevice(c->device);
+    if (!hip_ok(hipStreamSynchronize(c->s), err, err_len, "stream")) return 0;
+    for (uint32_t l = 0; l < layers; ++l) {
+        if (attn_out && !hip_ok(hipMemcpy(attn_out + 2048ull * l, c->half_dump + 4096ull * l, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+        if (moe_out && !hip_ok(hipMemcpy(moe_out + 2048ull * l, c->half_dump + 4096ull * l + 2048, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    }
+    return 1;
+}
+
+int qxg_set_attention_chunks(qxg_ctx *c, uint32_t min_positions) {
+    if (!c) return 0;
+    c->att_split_min = min_positions ? min_positions : 1u;
+    return 1;
 }
 
 int qxg_set_layer_path(qxg_ctx *c, int persistent) {

@@ -77,7 +77,7 @@ constexpr int HEAD_NI = (HEAD_R * 105 + 63) / 64;        // 16-byte load instruc
 
 // exchange buffers: word offsets of slot 0 (slot 1 follows at + size)
 constexpr uint32_t XN_X = 2048, XN_QKV = 5120, XN_CX = 4096, XN_XP = 2048, XN_LG = 256, XN_H = 6144, XN_WT = 16,
-                   XN_AM = 2 * NWG;
+                   XN_AM = 2 * NWG, XN_PT = QXD_PART_WORDS;   // (partial results: their own buffer)
 constexpr uint32_t XO_X = 0;
 constexpr uint32_t XO_QKV = XO_X + 2 * XN_X;
 constexpr uint32_t XO_CX = XO_QKV + 2 * XN_QKV;
@@ -152,6 +152,19 @@ struct AttnS {
     float ctx[NWV][4][128];         // per wave and position subgroup: context partial sums
     double m[NWV], l[NWV];          // per wave: running maximum and denominator
 };
+struct AttnK {                      // stage A by kv head and position chunk (attention_chunk_part)
+    float q[NWV][128];              // polled q of heads 8 g .. 8 g + 7, normalised and rotated in place
+    float k[512], v[512];           // the position's K and V rows (all four kv heads); follow q for the poll
+    uint32_t qd[NWV][4 * DIG_STRIDE];   // each head's q digit planes
+    float kmx[4], vmx[4];           // largest magnitudes of the K and V rows per kv head
+    uint32_t qok[NWV];
+    float p[NWV][QXD_CHUNK];        // per wave: weights of the chunk's positions (0 past the position)
+};
+struct ChunkRows {                  // the chunk's cached K and V rows of kv head g and their scales,
+    alignas(16) int8_t k[QXD_CHUNK][128];   // copied to LDS in stage Q (dma_chunk); rows past the
+    alignas(16) int8_t v[QXD_CHUNK][128];   // position repeat its predecessor's and are masked
+    float ks[QXD_CHUNK], vs[QXD_CHUNK];
+};
 struct DLds {
     uint4 g2[512];
     uint2 g3[256];
@@ -182,6 +195,7 @@ struct DLds {
             alignas(16) uint8_t dn[NWV][DN_BYTES];      // down rows of each wave (DMA in stage G, dots in stage D)
         } m;
         AttnS att;
+        AttnK atk;
         struct {
             float bv[NWV];
             uint32_t bi[NWV];
@@ -377,6 +391,17 @@ DEV void dma16(const GLB uint8_t *base, uint32_t off, const void *lds) {
 // older loads pending and waited again behind loads issued later); the fence keeps LDS reads
 // of the copied rows below it.
 DEV void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
+// The same copies with agent-coherent (sc1) loads, for KV-cache rows and scales, which
+// workgroups of this launch store with agent-scope stores (every KV-cache read is
+// agent-coherent): 16 bytes a lane, or 4 (lane i's at lds + 4 i).
+DEV void dma16_kv(const GLB uint8_t *base, uint32_t off, const void *lds) {
+    const uint32_t l = (uint32_t)(uintptr_t)lds;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc1" : : "v"(off), "s"(base), "s"(l) : "memory", "m0");
+}
+DEV void dma4_kv(const GLB uint8_t *base, uint32_t off, const void *lds) {
+    const uint32_t l = (uint32_t)(uintptr_t)lds;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1 sc1" : : "v"(off), "s"(base), "s"(l) : "memory", "m0");
+}
 
 // layer l's plane `id` (scalar arithmetic on the argument copy)
 DEV const GLB uint8_t *plane(const QxDArgs &a, int id, uint32_t l) {
@@ -829,6 +854,262 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
     __syncthreads();   // the union is reused by the next stage
 }
 
+// ---------------------------------------------------------------- attention by chunk (stage A, long context)
+// The same attention (reference src/qx_format.c:5051-5196) spread over every workgroup once
+// the cache is long: with n = pos + 1 positions in QXD_CHUNK-position chunks (nch of them),
+// workgroup w < 4 nch takes kv head g = w % 4 and chunk c = w / 4 for all eight q heads that
+// share g (wave v: q head 8 g + v), so each chunk's K and V rows are read once, into LDS in
+// stage Q (dma_chunk), for eight heads.  A wave scores the chunk's 64 positions (a quad per
+// position, four rounds of 16), takes one maximum and one exponential per lane, and sums the
+// weighted V codes (lane: 4 dimensions, odd or even positions).  Its partial result - the
+// chunk's maximum score m_c, its sum of exp(s - m_c) and the f32 context sums - is published
+// as 8 records of 16 dimensions.  Then workgroup w merges q head w / 8, dimensions
+// 16 (w % 8) .. over the chunks: ctx[d] = sum_c (float)(exp(m_c - M) / L) acc_c[d],
+// L = sum_c exp(m_c - M) l_c, the formula of the per-wave merge in attention().
+// The chunk holding the position (c = nch - 1) quantizes its kv head's K and V rows of the
+// position (scales over all 512 values of the row) and stores them in the cache.
+DEV uint32_t pack_codes4(const float *v, float sc) {
+    return (uint32_t)(uint8_t)int8_code(v[0], sc) | ((uint32_t)(uint8_t)int8_code(v[1], sc) << 8) |
+           ((uint32_t)(uint8_t)int8_code(v[2], sc) << 16) | ((uint32_t)(uint8_t)int8_code(v[3], sc) << 24);
+}
+DEV double dbl_words(uint32_t hi, uint32_t lo) { return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo)); }
+DEV uint32_t chunk_count(uint32_t pos) { return (pos + QXD_CHUNK) / QXD_CHUNK; }   // ceil((pos + 1) / QXD_CHUNK)
+DEV ChunkRows &chunk_rows(DLds &S) {
+    static_assert(sizeof(ChunkRows) <= sizeof(S.u.m.dn), "a chunk's rows fit the down-row area");
+    static_assert(sizeof(AttnK) <= offsetof(decltype(S.u.m), dn), "the chunk workgroup's scratch stays clear of its rows");
+    return *reinterpret_cast<ChunkRows *>(&S.u.m.dn[0][0]);
+}
+
+// Stage Q of a chunk workgroup (w < 4 nch): its chunk's cached rows (positions c0 .. c0 + 63,
+// clamped below pos) and scales to LDS; wave v copies rows 8 v .. 8 v + 7 of K and of V.
+DEV void dma_chunk(const QxDArgs &a, uint32_t l, uint32_t pos, DLds &S) {
+    const int lane = tix() & 63, w = wave_id();
+    const uint32_t g = blockIdx.x & 3u, c0 = (blockIdx.x >> 2) * QXD_CHUNK;
+    const uint32_t lastc = pos > 0 ? pos - 1 : 0u, base = l * a.ctx;
+    ChunkRows &C = chunk_rows(S);
+    const uint32_t t = min(c0 + 8u * w + (uint32_t)(lane >> 3), lastc);
+    const uint32_t off = (base + t) * 512 + 128 * g + 16 * (lane & 7);   // layers * ctx * 512 < 2^32
+    dma16_kv(gp(reinterpret_cast<const uint8_t *>(a.kc)), off, C.k[8 * w]);
+    dma16_kv(gp(reinterpret_cast<const uint8_t *>(a.vc)), off, C.v[8 * w]);
+    if (w < 2) {
+        const uint32_t ts = min(c0 + (uint32_t)lane, lastc);
+        dma4_kv(gp(reinterpret_cast<const uint8_t *>(w == 0 ? a.ks : a.vs)), (base + ts) * 4, w == 0 ? C.ks : C.vs);
+    }
+}
+
+// ep: the QKV phase (the partial results go out at ep + 1).  The chunk's rows are in LDS once
+// the Q/K/V poll has returned (its loads complete after the earlier copies).
+__device__ __attribute__((noinline)) bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, DLds &S, const Ctl &ctl, bool last) {
+    (void)last;
+    constexpr uint32_t MAXCH = QXG_MAX_CTX / QXD_CHUNK;
+    GLB uint64_t *const X = gpw(a.xch);
+    const uint32_t n = pos + 1, nch = chunk_count(pos), par = l & 1;
+    AttnK &A = S.u.atk;
+    ChunkRows &C = chunk_rows(S);
+    const int g = blockIdx.x & 3;
+    const uint32_t ch = blockIdx.x >> 2, c0 = ch * QXD_CHUNK;
+    const bool own = ch + 1 == nch;   // the chunk holding the position (workgroup-uniform)
+    const int tid = tix(), lane = tid & 63, w = wave_id();
+    const double cs = gp(a.T.rope_cs)[pos * 128 + lane], sn = gp(a.T.rope_cs)[pos * 128 + 64 + lane];
+    const GLB float *nqp = (const GLB float *)plane(a, PL_Q_NORM, l), *nkp = (const GLB float *)plane(a, PL_K_NORM, l);
+    const float nq0 = nqp[lane], nq1 = nqp[64 + lane], nk0 = nkp[lane], nk1 = nkp[64 + lane];
+    // q of heads 8 g .. 8 g + 7 (words 1024 g ..), then the K and V rows (4096 .. 5119)
+    const GLB uint64_t *qkv = X + XO_QKV + par * XN_QKV;
+    if (!wait_xch2<2>(qkv, 2048, ep, reinterpret_cast<uint32_t *>(A.q[0]), [g](int i) { return i < 1024 ? 1024 * g + i : 3072 + i; },
+                      S, ctl))
+        return false;
+    DMARK(l, 3);
+    // ---- wave v: q head 8 g + v normalised, rotated, as digit planes; the position's chunk
+    // also the K heads (waves 0..3, in place) and the V maxima (waves 4..7)
+    {
+        float q0 = A.q[w][lane], q1 = A.q[w][64 + lane];
+        head_norm_rope_wave(q0, q1, nq0, nq1, cs, sn);
+        A.q[w][lane] = q0;
+        A.q[w][64 + lane] = q1;
+        wave_lds_sync();
+        bool qfin = true;
+        if (lane < 16) {
+            float y[8];
+            const float4 a0 = reinterpret_cast<const float4 *>(A.q[w])[2 * lane], a1 = reinterpret_cast<const float4 *>(A.q[w])[2 * lane + 1];
+            y[0] = a0.x; y[1] = a0.y; y[2] = a0.z; y[3] = a0.w; y[4] = a1.x; y[5] = a1.y; y[6] = a1.z; y[7] = a1.w;
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { qfin = qfin && isfinite(y[i]); mx = fmaxf(mx, fabsf(y[i])); }
+            mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
+            mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
+            uint32_t h0, h1, m0, m1, l0, l1;
+            float scq;
+            digits8(y, isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, scq);
+            uint32_t *dd = A.qd[w] + (lane >> 2) * DIG_STRIDE;
+            const int q = lane & 3;
+            *reinterpret_cast<uint2 *>(dd + 2 * q) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2 *>(dd + 8 + 2 * q) = make_uint2(m0, m1);
+            *reinterpret_cast<uint2 *>(dd + 16 + 2 * q) = make_uint2(l0, l1);
+            if (q == 0) dd[24] = __float_as_uint(scq);
+        }
+        const bool allfin = __ballot(!qfin) == 0;
+        if (lane == 0) A.qok[w] = allfin ? 1u : 0u;
+    }
+    if (own) {
+        if (w < 4) {
+            float k0 = A.k[128 * w + lane], k1 = A.k[128 * w + 64 + lane];
+            head_norm_rope_wave(k0, k1, nk0, nk1, cs, sn);
+            A.k[128 * w + lane] = k0;
+            A.k[128 * w + 64 + lane] = k1;
+            const float mx = wave_max_f(fmaxf(int8_mag(k0), int8_mag(k1)));
+            if (lane == 0) A.kmx[w] = mx;
+        } else {
+            const int j = w - 4;
+            const float mx = wave_max_f(fmaxf(int8_mag(A.v[128 * j + lane]), int8_mag(A.v[128 * j + 64 + lane])));
+            if (lane == 0) A.vmx[j] = mx;
+        }
+    }
+    __syncthreads();
+    DMARK(l, 21);
+    if (own) {
+        // the position's codes of kv head g (wave 0 K, wave 1 V, 4 per lane) replace the copied
+        // row in its chunk slot (pos - c0; the copy held position pos - 1 there), and go to the
+        // cache, coherent (later steps read them)
+        const float kscale = int8_scale(fmaxf(fmaxf(A.kmx[0], A.kmx[1]), fmaxf(A.kmx[2], A.kmx[3])));
+        const float vscale = int8_scale(fmaxf(fmaxf(A.vmx[0], A.vmx[1]), fmaxf(A.vmx[2], A.vmx[3])));
+        const uint32_t up = pos - c0;
+        if (w < 2 && lane < 32) {
+            const uint32_t word = pack_codes4((w == 0 ? A.k : A.v) + 128 * g + 4 * lane, w == 0 ? kscale : vscale);
+            reinterpret_cast<uint32_t *>(w == 0 ? C.k[up] : C.v[up])[lane] = word;
+            const uint32_t slot = l * a.ctx + pos;   // layers * ctx * 512 < 2^32
+            GLB uint32_t *row = (GLB uint32_t *)gpw(w == 0 ? a.kc : a.vc) + slot * 128 + 32 * g;
+            st_coherent(row + lane, word);
+            if (lane == 0) {
+                (w == 0 ? C.ks : C.vs)[up] = w == 0 ? kscale : vscale;
+                if (g == 0) st_coherent((GLB uint32_t *)gpw(w == 0 ? a.ks : a.vs) + slot, __float_as_uint(w == 0 ? kscale : vscale));
+            }
+        }
+        __syncthreads();
+    }
+    DMARK(l, 22);
+    // ---- scores of positions c0 + 16 i + jq (a quad per position; lane q4 takes dims 32 q4 ..)
+    const int q4 = lane & 3, jq = lane >> 2;
+    Dig d;
+    load_dig(A.qd[w], q4, d);
+    const bool qok = A.qok[w] != 0u;
+    const double inv_sqrt_hd = 1.0 / a.sqrt_hd;
+    double sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t u = 16u * i + (uint32_t)jq, t = c0 + u;
+        const uint4 x0 = *reinterpret_cast<const uint4 *>(C.k[u] + 32 * q4), x1 = *reinterpret_cast<const uint4 *>(C.k[u] + 32 * q4 + 16);
+        const uint32_t kw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const float ksc = C.ks[u];
+        int aH = 0, aM = 0, aL = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            aH = sdot4(kw[k], d.h[k], aH);
+            aM = sdot4(kw[k], d.m[k], aM);
+            aL = sdot4(kw[k], d.l[k], aL);
+        }
+        double sq = (double)(combine(aH, aM, aL) * d.s);
+        sq += dppd<DPP_XOR1>(sq);
+        sq += dppd<DPP_XOR2>(sq);
+        double v = qok ? sq * (double)ksc * inv_sqrt_hd : 0.0;
+        if (!isfinite(v)) v = 0.0;
+        sc[i] = t < n ? v : -INFINITY;
+    }
+    const double m = wave_max_d(fmax(fmax(sc[0], sc[1]), fmax(sc[2], sc[3])));
+    // one exponential per lane: lane (jq, q4) weighs position c0 + 16 q4 + jq
+    double ss = sc[0];
+    if (q4 == 1) ss = sc[1];
+    if (q4 == 2) ss = sc[2];
+    if (q4 == 3) ss = sc[3];
+    const uint32_t u = 16u * q4 + (uint32_t)jq;
+    const bool uvalid = c0 + u < n;
+    const float vsel = C.vs[u];
+    const double e = uvalid ? exp(ss - m) : 0.0;
+    const double lsum = wave_total_d(e);
+    A.p[w][u] = uvalid ? (float)(e * (double)vsel) : 0.0f;   // (a clamped row's scale may be unset)
+    wave_lds_sync();
+    DMARK(l, 23);
+    // ---- context sums: lane (p4 = lane / 16, dims 8 dg ..) over positions 4 j + p4, then the
+    // four position groups added (xor 16, then xor 32: the same order in every lane)
+    const int p4 = lane >> 4, dg = lane & 15;
+    float acc[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] = 0.0f;
+#pragma unroll 4
+    for (int j = 0; j < (int)QXD_CHUNK / 4; ++j) {
+        const uint32_t uu = 4u * j + (uint32_t)p4;
+        const float pv = A.p[w][uu];
+        const uint2 x = *reinterpret_cast<const uint2 *>(C.v[uu] + 8 * dg);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[b] = fmaf(pv, (float)(int8_t)((((b < 4) ? x.x : x.y) >> (8 * (b & 3))) & 255u), acc[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] += __shfl_xor(acc[b], 16);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) acc[b] += __shfl_xor(acc[b], 32);
+    // ---- the wave's partial result, 8 records of 16 dimensions: lanes 0..31 the context sums
+    // (lane (p4 < 2, dg): dims 8 dg + 4 p4 .. of record dg / 2), lanes 32..63 the maximum and
+    // the denominator
+    {
+        const uint32_t hq = 8u * g + (uint32_t)w;
+        GLB uint64_t *pt = gpw(a.xpart) + par * XN_PT;
+        if (lane < 32) {
+            GLB uint64_t *rec = pt + ((hq * 8u + (uint32_t)(dg >> 1)) * MAXCH + ch) * QXD_PREC + 8 * (dg & 1) + 4 * p4;
+            const uint32_t hi = p4 ? 0xffffffffu : 0u;   // (a bit select: a lane-dependent index would go through scratch)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                xst(rec + b, ep + 1, (__float_as_uint(acc[4 + b]) & hi) | (__float_as_uint(acc[b]) & ~hi));
+        } else {
+            const int r = (lane - 32) >> 2, k = lane & 3;   // record r, word 16 + k
+            const uint64_t bits = (uint64_t)__double_as_longlong(k < 2 ? m : lsum);
+            GLB uint64_t *rec = pt + ((hq * 8u + (uint32_t)r) * MAXCH + ch) * QXD_PREC + 16 + k;
+            xst(rec, ep + 1, (k & 1) ? (uint32_t)bits : (uint32_t)(bits >> 32));
+        }
+    }
+    DMARK(l, 24);
+    __syncthreads();   // the union is reused by the merge
+    return true;
+}
+
+// Every workgroup: q head wgi / 8, dimensions 16 (wgi % 8) .. merged over the chunks, published
+// as its context words.  ep: the partial results' phase (the context goes out with it too).
+__device__ __attribute__((noinline)) bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, DLds &S, const Ctl &ctl, bool last) {
+    (void)last;
+    constexpr uint32_t MAXCH = QXG_MAX_CTX / QXD_CHUNK;
+    static_assert(4 * MAXCH <= NWG && 32 * 8 == NWG, "one workgroup per (kv head, chunk) and per (q head, 16 dims)");
+    GLB uint64_t *const X = gpw(a.xch);
+    const uint32_t nch = chunk_count(pos), par = l & 1;
+    const int lane = tix() & 63, w = wave_id();
+    const uint32_t h = blockIdx.x >> 3, dgm = blockIdx.x & 7u;
+    uint32_t *rw = S.u.m.vin;                                           // nch records of QXD_PREC words
+    float *wt = reinterpret_cast<float *>(S.u.m.vin) + 2048;            // per chunk: (float)(exp(m_c - M) / L)
+    const GLB uint64_t *src = gpw(a.xpart) + par * XN_PT + (h * 8u + dgm) * MAXCH * QXD_PREC;
+    if (!wait_xch2<2>(src, (int)(QXD_PREC * nch), ep, rw, Ident(), S, ctl)) return false;
+    DMARK(l, 25);
+    if (w == 0) {   // wave 0 alone: lane c forms chunk c's factor, then lane (cg, d) sums chunks cg + 4 k
+        double mc = -INFINITY, lc = 0.0;
+        if ((uint32_t)lane < nch) {
+            mc = dbl_words(rw[QXD_PREC * lane + 16], rw[QXD_PREC * lane + 17]);
+            lc = dbl_words(rw[QXD_PREC * lane + 18], rw[QXD_PREC * lane + 19]);
+        }
+        const double M = wave_max_d(mc);
+        const double f = mc == -INFINITY ? 0.0 : exp(mc - M);
+        double L = wave_total_d(f * lc);
+        if (!isfinite(L) || L <= 0.0) L = 1.0;
+        const double invL = 1.0 / L;
+        wt[lane] = (float)(f * invL);
+        wave_lds_sync();
+        const int dd = lane & 15, cg = lane >> 4;
+        float o = 0.0f;
+        for (uint32_t cc = (uint32_t)cg; cc < nch; cc += 4) o = fmaf(wt[cc], __uint_as_float(rw[QXD_PREC * cc + dd]), o);
+        o += __shfl_xor(o, 16);
+        o += __shfl_xor(o, 32);
+        if (lane < 16) xstf(X + XO_CX + par * XN_CX + 128 * h + 16 * dgm + lane, ep, o);   // the CX phase
+    }
+    DMARK(l, 39);
+    __syncthreads();   // the union is reused by the next stage
+    return true;
+}
+
 // ---------------------------------------------------------------- head
 // Output RMSNorm + Q6_K head (src/qx_format.c:3554-3738) over the digits in S.dig: group g
 // is rows R g .. R g + R - 1; workgroup w's groups are w + 256 j, its waves taking them in
@@ -942,9 +1223,6 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
     }
     WQ wq;
     WO wo;
-    AttnPre ap;
-    float4 wm0 = make_float4(0.f, 0.f, 0.f, 0.f), wm1 = wm0;
-    float fnw[8];
     if (wg >= QXG_HEADS) load_wq(a, 0, wq, S.wq[wave_id()]);
     load_wr(a, 0, wo);
     uint32_t token = 0;
@@ -955,12 +1233,17 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
         const uint32_t ep_step = a.ep0 + step * phases + 1;
         const bool head_step = a.force_head || step + 1 >= a.n_prompt;
         const bool last = step + 1 == a.steps;
+        const bool chunked = pos + 1 >= a.att_split_min;   // stage A by kv head and chunk (uniform)
         if (step < a.n_prompt) token = gp(a.tokens)[step];
         // embedding row of the token (reference src/qx_format.c:3759-3793), decoded by every
         // workgroup into its copy of x
         if (tix() < 256) embed_q4k_row((const uint8_t *)(gp(a.emb) + (uint64_t)token * a.emb_row), S.xs);
         __syncthreads();
         for (uint32_t l = 0; l < L; ++l) {
+            // values loaded and used within one layer (declared here, they are not carried)
+            AttnPre ap;
+            float4 wm0, wm1;
+            float fnw[8];
             const uint32_t ep = ep_step + 5 * l;   // + 0 X, + 1 QKV, + 2 CX, + 3 XP/LG, + 4 H/WT
             const uint32_t par = l & 1;
             const uint32_t ln = l + 1 < L ? l + 1 : 0u;   // after the last layer: layer 0 of the next step
@@ -977,9 +1260,10 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 // attend to, arriving while the other workgroups make the Q/K/V rows
                 const bool mk = wg >= QXG_HEADS;
                 if (!mk) {
-                    attn_prefetch(a, l, pos, ap);
+                    if (!chunked) attn_prefetch(a, l, pos, ap);
                     load_o(a, l, wo, S.wo[wave_id()]);   // (the others load them after their rows)
                 }
+                if (chunked && (uint32_t)wg < 4u * chunk_count(pos)) dma_chunk(a, l, pos, S);
                 DMARK(l, 32);
                 // the normalised input's digits; the attn-norm weights came with the Q/K/V rows
                 double inv = 1.0;
@@ -1061,12 +1345,23 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
             // that make Q/K/V rows (idle until the context arrives) the O rows and the next
             // layer's Q/K/V rows
             load_wm(a, l, wm0, wm1);
-            if (wg >= QXG_HEADS) {
+            if (wg >= QXG_HEADS && !chunked) {
                 load_o(a, l, wo, S.wo[wave_id()]);
                 load_wq(a, ln, wq, S.wq[wave_id()]);
             }
             // ---------------------------------------------------------- stage A
-            if (wg < QXG_HEADS) {
+            if (chunked) {
+                // the chunk workgroups' partial results, every workgroup's merge, then the O
+                // rows and next layer's Q/K/V rows of the workgroups that make Q/K/V rows (loads
+                // complete in order: issued before a poll, they would delay it)
+                if ((uint32_t)wg < 4u * chunk_count(pos) && !attention_chunk_part(a, l, pos, ep + 1, S, ctl, last)) return;
+                DMARK(l, 4);
+                if (!attention_merge(a, l, pos, ep + 2, S, ctl, last)) return;
+                if (wg >= QXG_HEADS) {   // (the context exchange hides them)
+                    load_o(a, l, wo, S.wo[wave_id()]);
+                    load_wq(a, ln, wq, S.wq[wave_id()]);
+                }
+            } else if (wg < QXG_HEADS) {
                 if (!attn_wait(a, l, ep + 1, S, ctl)) return;
                 DMARK(l, 3);
                 attention(a, l, pos, ep + 1, ap, S, last);
@@ -1131,6 +1426,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 const int r = 8 * wg + wave;
                 const float o = (ok && isfinite(out[0])) ? out[0] : 0.0f;
                 if (lane == 0) S.outw[wave] = S.xs[r] + o;
+                if (last && a.d_half && lane == 0) gpw(a.d_half)[l * 4096 + r] = o;
                 __syncthreads();
                 if (tid < 8) xstf(X + XO_XP + par * XN_XP + 8 * wg + tid, ep + 3, S.outw[tid]);
                 DMARK(l, 6);
@@ -1346,6 +1642,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     const int r = 8 * wg + tid;
                     const float xn = S.xp[r] + moe;
                     if (last && a.d_layer) gpw(a.d_layer)[l * 2048 + r] = xn;
+                    if (last && a.d_half) gpw(a.d_half)[l * 4096 + 2048 + r] = moe;
                     if (last && a.d_res && l + 1 == L) gpw(a.d_res)[r] = xn;
                     xstf(X + XO_X + ((l + 1) & 1) * XN_X + r, ep + 5, xn);
                 }

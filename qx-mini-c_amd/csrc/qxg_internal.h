@@ -137,14 +137,18 @@ struct QxDArgs {
     uint32_t *tokens;            // tokens[0 .. n_prompt) in; generated ids stored at [step + 1]
     DevState *st;                // nonfinite flag
     uint64_t *xch;               // tagged exchange buffers (QXD_XCH_WORDS words, zeroed once)
+    uint64_t *xpart;             // tagged partial results of the chunked attention (2 QXD_PART_WORDS)
     float *logits;               // optional: the last head step's logits
     float *d_layer;              // optional dumps of the last step: per-layer output residuals,
     uint32_t *d_rids;            // routed experts and renormalised weights per layer, the
-    double *d_rw;                // final residual
-    float *d_res;
+    double *d_rw;                // final residual, and each layer's two halves before their
+    float *d_res;                // residual adds ([layer][attention 2048 | MoE 2048])
+    float *d_half;
     uint32_t *abort;             // set on a timed-out wait; the host reports it
     uint64_t timeout;            // per wait, in 100 MHz ticks
     double sqrt_hd;
+    uint32_t att_split_min;      // positions n = pos + 1 from which stage A runs by kv head and chunk
+    uint32_t pad_;
 };
 #define QXD_THREADS 512
 // Interleaved expert rows of the persistent decode: unit (expert e, row r) of gate/up is
@@ -173,8 +177,20 @@ struct QxDArgs {
 // The four per-layer norm vectors share one arena: layer l's at l * QXD_NORM_STRIDE, attn
 // norm (2048 f32) at 0, ffn norm at 8192, q norm (128 f32) at 16384, k norm at 16896.
 #define QXD_NORM_STRIDE 17408u
+// Long-context attention of the persistent decode: stage A by (kv head g, chunk c) of
+// QXD_CHUNK positions, one workgroup each, then a merge by (q head, 16 dimensions).  A
+// chunk's partial result for one q head and 16 dimensions is a record of QXD_PREC words
+// {context sums 16, running maximum (hi, lo), denominator (hi, lo)} at
+// [head][dimension group][chunk].
+#define QXD_CHUNK 64u
+#define QXD_PREC 20u
+#define QXD_PART_WORDS (32u * 8u * (QXG_MAX_CTX / QXD_CHUNK) * QXD_PREC)
+// Default positions (n = pos + 1) from which the persistent decode attends by chunk: below
+// it the 32 q-head workgroups walk the cache themselves (no merge exchange).
+#define QXD_SPLIT_MIN_DEFAULT 257u
 // exchange words per launch: x, qkv, ctx, x', router logits, h, expert weights (two slots
-// each) and the per-workgroup argmax candidates
+// each) and the per-workgroup argmax candidates; the chunked attention's partial results
+// (two slots of QXD_PART_WORDS) have a buffer of their own
 #define QXD_XCH_WORDS (2u * (2048u + 5120u + 4096u + 2048u + 256u + 6144u + 16u + 2u * QXG_PBLOCKS))
 // phases per step (five exchanges per layer, the head input, the argmax)
 #define QXD_PHASES(layers) (5u * (layers) + 2u)

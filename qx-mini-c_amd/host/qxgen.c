@@ -88,12 +88,24 @@ typedef struct gen_tensor {
     uint64_t dims[4];
     uint64_t offset, bytes, blocks, block_bytes;
     uint64_t key;
+    /* planted outliers (spec->outliers): F32 norms by channel (1: x1000 at channel 5 mod 128,
+       2: also x1e6 at channel 1001); quantized rows: blocks of row out_row mod out_rows get
+       their fp16 d range x1000 (0: none), bpr blocks per row */
+    uint32_t out_norm;
+    uint64_t out_rows, out_row, bpr;
 } gen_tensor;
+
+/* fp16 d range factor of block blk: x1000 in a planted outlier row */
+static double d_scale(const gen_tensor *t, uint64_t blk) {
+    if (!t->out_rows) return 1.0;
+    return (blk / t->bpr) % t->out_rows == t->out_row ? 1000.0 : 1.0;
+}
 
 /* one 256-value block (or 256 floats for F32) */
 static void gen_block(const gen_tensor *t, uint64_t blk, uint8_t *out, uint64_t nbytes) {
     uint64_t s = t->key ^ (blk * 0xd1342543de82ef95ull);
     splitmix(&s);
+    const double ds = d_scale(t, blk);
     switch (t->type) {
     case QXT_F32: {
         uint64_t n = nbytes / 4;
@@ -105,6 +117,9 @@ static void gen_block(const gen_tensor *t, uint64_t blk, uint8_t *out, uint64_t 
                 v = (float)(0.02 * sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
             } else {
                 v = (float)(0.5 + unif(&s));
+                const uint64_t ch = blk * 256 + i;
+                if (t->out_norm && ch % 128 == 5) v *= 1000.0f;
+                if (t->out_norm == 2 && ch == 1001) v *= 1.0e6f;
             }
             memcpy(out + 4 * i, &v, 4);
         }
@@ -121,28 +136,28 @@ static void gen_block(const gen_tensor *t, uint64_t blk, uint8_t *out, uint64_t 
         put16(out + 208, fp16_unif(&s, 1e-4, 1e-3));
         break;
     case QXT_IQ4_XS:
-        put16(out, fp16_unif(&s, 1e-5, 3e-5));
+        put16(out, fp16_unif(&s, 1e-5 * ds, 3e-5 * ds));
         fill_bytes(out + 2, 134, &s);
         break;
     case QXT_IQ2_XS:
-        put16(out, fp16_unif(&s, 2e-4, 5e-4));
+        put16(out, fp16_unif(&s, 2e-4 * ds, 5e-4 * ds));
         fill_bytes(out + 2, 72, &s);
         break;
     case QXT_IQ3_XXS:
-        put16(out, fp16_unif(&s, 1e-4, 3e-4));
+        put16(out, fp16_unif(&s, 1e-4 * ds, 3e-4 * ds));
         fill_bytes(out + 2, 96, &s);
         break;
     case QXT_Q5_K:
-        put16(out, fp16_unif(&s, 1e-5, 3e-5));
+        put16(out, fp16_unif(&s, 1e-5 * ds, 3e-5 * ds));
         put16(out + 2, fp16_unif(&s, 1e-5, 3e-5));
         fill_bytes(out + 4, 172, &s);
         break;
     case QXT_IQ2_S:
-        put16(out, fp16_unif(&s, 2e-4, 5e-4));
+        put16(out, fp16_unif(&s, 2e-4 * ds, 5e-4 * ds));
         fill_bytes(out + 2, 80, &s);
         break;
     case QXT_IQ3_S:
-        put16(out, fp16_unif(&s, 1e-4, 3e-4));
+        put16(out, fp16_unif(&s, 1e-4 * ds, 3e-4 * ds));
         fill_bytes(out + 2, 108, &s);
         break;
     default:
@@ -211,18 +226,29 @@ static void add_tensor(gen_tensor *v, uint32_t *n, const char *name, uint32_t ty
     t->key = k;
 }
 
+/* planted outliers of the last tensor added (spec->outliers) */
+static void mark_norm(gen_tensor *t, uint32_t kind) { t->out_norm = kind; }
+static void mark_rows(gen_tensor *t, uint64_t rows, uint64_t row) {
+    t->out_rows = rows;
+    t->out_row = row;
+    t->bpr = t->dims[0] / 256;
+}
+
 static uint32_t build_tensor_list(const qxgen_spec *sp, gen_tensor *v) {
     uint32_t n = 0;
     char nm[QXF_NAME_MAX];
+    const int ol = sp->outliers != 0, ol2 = sp->outliers == 2;
     const uint64_t H = 2048, V = sp->vocab, E = sp->experts, F = 768;
     if (sp->with_embedding) add_tensor(v, &n, "token_embd.weight", QXT_Q4_K, 2, H, V, 0, 0, sp->seed);
     if (sp->with_head) {
         add_tensor(v, &n, "output_norm.weight", QXT_F32, 1, H, 0, 0, DIST_NORM_W, sp->seed);
+        if (ol) mark_norm(&v[n - 1], ol2 ? 2 : 1);
         add_tensor(v, &n, "output.weight", QXT_Q6_K, 2, H, V, 0, 0, sp->seed);
     }
     for (uint32_t l = 0; l < sp->layers; ++l) {
 #define T(suffix, ...) do { snprintf(nm, sizeof(nm), "blk.%u." suffix, l); add_tensor(v, &n, nm, __VA_ARGS__, sp->seed); } while (0)
         T("attn_norm.weight", QXT_F32, 1, H, 0, 0, DIST_NORM_W);
+        if (ol) mark_norm(&v[n - 1], ol2 ? 2 : 1);
         T("attn_q.weight", QXT_IQ4_XS, 2, H, 4096, 0, 0);
         T("attn_k.weight", QXT_IQ4_XS, 2, H, 512, 0, 0);
         const uint32_t k4 = sp->mix ? l % 4 : 0;
@@ -230,14 +256,21 @@ static uint32_t build_tensor_list(const qxgen_spec *sp, gen_tensor *v) {
         const uint32_t t_gu = (k4 == 1 || k4 == 3) ? QXT_IQ2_S : QXT_IQ2_XS;
         const uint32_t t_dn = k4 == 0 ? QXT_IQ3_XXS : k4 == 1 ? QXT_IQ4_XS : QXT_IQ3_S;
         T("attn_v.weight", t_vo, 2, H, 512, 0, 0);
+        if (ol) mark_rows(&v[n - 1], 128, 3);
         T("attn_output.weight", t_vo, 2, 4096, H, 0, 0);
+        if (ol) mark_rows(&v[n - 1], H, 11);
         T("attn_q_norm.weight", QXT_F32, 1, 128, 0, 0, DIST_NORM_W);
+        if (ol) mark_norm(&v[n - 1], 1);
         T("attn_k_norm.weight", QXT_F32, 1, 128, 0, 0, DIST_NORM_W);
+        if (ol) mark_norm(&v[n - 1], 1);
         T("ffn_norm.weight", QXT_F32, 1, H, 0, 0, DIST_NORM_W);
+        if (ol) mark_norm(&v[n - 1], 1);
         T("ffn_gate_inp.weight", QXT_F32, 2, H, E, 0, DIST_ROUTER);
         T("ffn_gate_exps.weight", t_gu, 3, H, F, E, 0);
+        if (ol2) mark_rows(&v[n - 1], F, 7);
         T("ffn_up_exps.weight", t_gu, 3, H, F, E, 0);
         T("ffn_down_exps.weight", t_dn, 3, F, H, E, 0);
+        if (ol2) mark_rows(&v[n - 1], H, 13);
 #undef T
     }
     return n;

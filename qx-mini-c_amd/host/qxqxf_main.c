@@ -242,7 +242,7 @@ int main(int argc, char **argv) {
     }
     if (!strcmp(cmd, "generate-model")) {
         const char *outp = NULL;
-        qxgen_spec sp = {48, 151936, 128, 1, 1, 1, 0, 0};
+        qxgen_spec sp = {48, 151936, 128, 1, 1, 1, 0, 0, 0};
         uint32_t seed = 1;
         for (int i = 2; i < argc; ++i) {
             if (!strcmp(argv[i], "--out") && i + 1 < argc) outp = argv[++i];

@@ -54,7 +54,7 @@ def _sig(lib, name, args, res=c_int):
 
 class GenSpec(ctypes.Structure):
     _fields_ = [("layers", u32), ("vocab", u32), ("experts", u32), ("with_embedding", u32), ("with_head", u32),
-                ("seed", u64), ("threads", u32), ("mix", u32)]
+                ("seed", u64), ("threads", u32), ("mix", u32), ("outliers", u32)]
 
 
 class ModelInfo(ctypes.Structure):
@@ -92,6 +92,8 @@ _sig(_g, "qxg_prefill", [vp, vp, u32, u32, c_int, vp, vp, u32, vp, vp, ctypes.PO
 _sig(_g, "qxg_prefill_layer", [vp, u32, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_time_kernel", [vp, c_int, u32, u32, ctypes.POINTER(c_float), *ERR])
 _sig(_g, "qxg_decode_routing", [vp, u32, vp, vp, *ERR])
+_sig(_g, "qxg_decode_halves", [vp, u32, vp, vp, *ERR])
+_sig(_g, "qxg_set_attention_chunks", [vp, u32])
 _sig(_g, "qxg_device_bytes", [vp], u64)
 _sig(_g, "qxg_profile_kernel", [vp, c_int])
 _sig(_g, "qxg_profile_result", [vp, ctypes.POINTER(u32), ctypes.POINTER(c_double)])
@@ -115,10 +117,12 @@ def fnv1a64(a):
     return int(_h.qxf_fnv1a64(_p(a), a.nbytes))
 
 
-def generate_model(path, layers=1, vocab=4096, experts=128, embedding=True, head=True, seed=1, threads=0, mix=0):
+def generate_model(path, layers=1, vocab=4096, experts=128, embedding=True, head=True, seed=1, threads=0, mix=0,
+                   outliers=0):
     """Writes the seeded random-init QXF1 model (mix=1: the real checkpoint's per-layer
-    quant types); returns its size in bytes."""
-    sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads, mix)
+    quant types; outliers=1: planted outlier channels, see qx_host.h); returns its size in
+    bytes."""
+    sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads, mix, outliers)
     err = ctypes.create_string_buffer(512)
     size = u64()
     if not _h.qxgen_write(str(path).encode(), ctypes.byref(sp), ctypes.byref(size), err, 512):
@@ -152,8 +156,9 @@ def kvsnap_read(path, layers, ctx, seed):
 class MemModel:
     """Seeded QXF1 model in an anonymous in-memory file (path /proc/self/fd/N)."""
 
-    def __init__(self, layers=48, vocab=151936, experts=128, embedding=True, head=True, seed=1, threads=0, mix=0):
-        sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads, mix)
+    def __init__(self, layers=48, vocab=151936, experts=128, embedding=True, head=True, seed=1, threads=0, mix=0,
+                 outliers=0):
+        sp = GenSpec(layers, vocab, experts, int(embedding), int(head), seed, threads, mix, outliers)
         err = ctypes.create_string_buffer(512)
         path = ctypes.create_string_buffer(128)
         fd = c_int()
@@ -335,6 +340,19 @@ class Context:
         fi = np.zeros((n, 2048), np.float32); moe = np.zeros((n, 2048), np.float32); out = np.zeros((n, 2048), np.float32)
         self._check(_g.qxg_prefill_layer(self._c, layer, n, pos0, _p(x), _p(fi), _p(moe), _p(out), self._err, 1024))
         return fi, moe, out
+
+    def halves(self, layers=None):
+        """(attention outputs, MoE outputs) [layers, 2048] of the last decode_token step,
+        each before its residual add."""
+        n = self.info.layers if layers is None else layers
+        a = np.zeros((n, 2048), np.float32)
+        m = np.zeros((n, 2048), np.float32)
+        self._check(_g.qxg_decode_halves(self._c, n, _p(a), _p(m), self._err, 1024))
+        return a, m
+
+    def set_attention_chunks(self, min_positions):
+        """Persistent decode: stage A by kv head and chunk from n = pos + 1 >= min_positions."""
+        _g.qxg_set_attention_chunks(self._c, int(min_positions))
 
     def set_layer_path(self, persistent):
         """0: one kernel per phase (default); 1: the persistent layer kernel."""
