@@ -28,6 +28,7 @@ __global__ void qxk_topk_merge(const float *, const uint32_t *, uint32_t, uint32
                                DevState *);
 __global__ void qxk_q8k(const float *, uint32_t, uint8_t *, uint32_t *);
 __global__ void qxk_decode(QxDArgs);
+__global__ void qxk_decode_chunked(QxDArgs);
 __global__ void qxk_interleave_experts(const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *,
                                        const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, uint32_t, uint8_t *,
                                        uint8_t *);
@@ -382,10 +383,11 @@ struct DecodeDumps {
 };
 
 // One cooperative launch of the persistent decode for `steps` steps from pos0 (tokens
-// already in c->tokens).  Exchange epochs advance by the launch's phases; before they
-// could wrap, the buffers are cleared and the count restarts.
-bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0, bool force_head,
-                   const DecodeDumps &d, char *err, uint64_t n) {
+// already in c->tokens from index s0: the launch reads tokens[s0 ..] as its own tokens[0 ..]).
+// Exchange epochs advance by the launch's phases; before they could wrap, the buffers are
+// cleared and the count restarts.
+bool launch_decode_part(qxg_ctx *c, bool chunked, uint32_t s0, uint32_t steps, uint32_t n_prompt, uint32_t pos0,
+                        bool force_head, const DecodeDumps &d, char *err, uint64_t n) {
     const uint64_t phases = (uint64_t)steps * QXD_PHASES(c->layers) + 1;
     if ((uint64_t)c->next_ep + phases >= 0x7fffffffull) {
         if (!hip_ok(hipMemsetAsync(c->xch, 0, QXD_XCH_WORDS * 8ull, c->s), err, n, "exchange buffers") ||
@@ -404,15 +406,14 @@ bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0,
     a.h_il = c->head_il;
     a.vocab = c->vocab; a.layers = c->layers; a.experts = c->experts; a.ctx = c->kv_ctx;
     a.steps = steps; a.n_prompt = n_prompt; a.pos0 = pos0; a.force_head = force_head ? 1u : 0u;
+    a.tokens = c->tokens + s0;
     a.ep0 = c->next_ep;
     a.T = c->T;
     a.kc = c->kc; a.vc = c->vc; a.ks = c->ks; a.vs = c->vs;
-    a.tokens = c->tokens;
     a.st = c->st;
     a.xch = c->xch;
     a.xpart = c->xpart;
     a.logits = d.logits; a.d_layer = d.layer; a.d_rids = d.rids; a.d_rw = d.rw; a.d_res = d.res; a.d_half = d.half;
-    a.att_split_min = c->att_split_min;
     a.abort = c->abort;
     a.timeout = DECODE_WAIT_TICKS;
     a.sqrt_hd = std::sqrt(128.0);
@@ -420,10 +421,27 @@ bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0,
     void *args[] = {&a};
     const Timer t = timer_for(c, 7);
     if (t.e0) (void)hipEventRecord(t.e0, c->s);
-    if (!hip_ok(hipLaunchCooperativeKernel((const void *)qxk_decode, dim3(QXG_PBLOCKS), dim3(QXD_THREADS), args, 0, c->s),
+    if (!hip_ok(hipLaunchCooperativeKernel(chunked ? (const void *)qxk_decode_chunked : (const void *)qxk_decode,
+                                           dim3(QXG_PBLOCKS), dim3(QXD_THREADS), args, 0, c->s),
                 err, n, "persistent decode launch"))
         return false;
     if (t.e1) (void)hipEventRecord(t.e1, c->s);
+    return true;
+}
+
+// The persistent decode of steps 0 .. steps-1 at positions pos0 ..: the steps whose cache
+// reaches n = pos + 1 >= att_split_min run in the chunked kernel, those before in the walk
+// kernel (two launches where the call crosses the threshold; the second reads its first
+// token from where the first left it, and its prompt is what remains of the call's).  Each
+// launch writes the dumps of its own last step, so the call's last step wins.
+bool launch_decode(qxg_ctx *c, uint32_t steps, uint32_t n_prompt, uint32_t pos0, bool force_head,
+                   const DecodeDumps &d, char *err, uint64_t n) {
+    const uint64_t first_chunked = c->att_split_min > (uint64_t)pos0 + 1 ? (uint64_t)c->att_split_min - 1 - pos0 : 0;
+    const uint32_t s1 = (uint32_t)std::min<uint64_t>(first_chunked, steps);
+    if (s1 > 0 && !launch_decode_part(c, false, 0, s1, n_prompt, pos0, force_head, d, err, n)) return false;
+    if (s1 < steps &&
+        !launch_decode_part(c, true, s1, steps - s1, n_prompt > s1 ? n_prompt - s1 : 1u, pos0 + s1, force_head, d, err, n))
+        return false;
     return true;
 }
 
@@ -882,7 +900,8 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
         int occ = 0, coop = 0;
         if (prop.multiProcessorCount < QXG_PBLOCKS ||
             hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device) != hipSuccess || !coop ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_decode, QXD_THREADS, 0) != hipSuccess || occ < 1) {
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_decode, QXD_THREADS, 0) != hipSuccess || occ < 1 ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_decode_chunked, QXD_THREADS, 0) != hipSuccess || occ < 1) {
             if (err && err_len)
                 snprintf(err, (size_t)err_len, "device %d has %d CUs; the persistent decode kernel needs %d resident workgroups",
                          device, prop.multiProcessorCount, QXG_PBLOCKS);

@@ -179,6 +179,7 @@ struct DLds {
     double xinv;                 // 1 / rms(x') (stage G)
     float ys[QXG_TOPK][8];       // down rows of each rank (stage D)
     float outw[32];              // the workgroup's outputs of a stage, gathered for one store
+    float oatt[NWV];             // the workgroup's O-projection outputs (stage O, for the last step's dumps)
     uint32_t flag[NWV];
     uint32_t bflag[2][NWV];      // block_any flags, two sets by call parity
     uint32_t bpar[NWV];          // block_any call parity of each wave
@@ -899,7 +900,7 @@ DEV void dma_chunk(const QxDArgs &a, uint32_t l, uint32_t pos, DLds &S) {
 
 // ep: the QKV phase (the partial results go out at ep + 1).  The chunk's rows are in LDS once
 // the Q/K/V poll has returned (its loads complete after the earlier copies).
-__device__ __attribute__((noinline)) bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, DLds &S, const Ctl &ctl, bool last) {
+DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, DLds &S, const Ctl &ctl, bool last) {
     (void)last;
     constexpr uint32_t MAXCH = QXG_MAX_CTX / QXD_CHUNK;
     GLB uint64_t *const X = gpw(a.xch);
@@ -1072,7 +1073,7 @@ __device__ __attribute__((noinline)) bool attention_chunk_part(const QxDArgs &a,
 
 // Every workgroup: q head wgi / 8, dimensions 16 (wgi % 8) .. merged over the chunks, published
 // as its context words.  ep: the partial results' phase (the context goes out with it too).
-__device__ __attribute__((noinline)) bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, DLds &S, const Ctl &ctl, bool last) {
+DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, DLds &S, const Ctl &ctl, bool last) {
     (void)last;
     constexpr uint32_t MAXCH = QXG_MAX_CTX / QXD_CHUNK;
     static_assert(4 * MAXCH <= NWG && 32 * 8 == NWG, "one workgroup per (kv head, chunk) and per (q head, 16 dims)");
@@ -1196,7 +1197,11 @@ DEV bool better(float v, uint32_t i, float bv, uint32_t bi) { return v > bv || (
 }  // namespace
 
 // ================================================================= kernel
-extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
+// The decode steps; CHUNKED: stage A by kv head and chunk (every step of the launch at
+// n = pos + 1 >= att_split_min), else the 32 q-head workgroups' walk.  Two kernels, so neither
+// carries the other's stage A code in its layer loop (the host splits a launch at the threshold).
+template <bool CHUNKED>
+DEV void decode_steps(const QxDArgs &args) {
     __shared__ DLds S;
 #ifdef QXD_TRACE
     if (threadIdx.x < 5 * 40) qxd_tl[threadIdx.x / 40][threadIdx.x % 40] = 0ull;
@@ -1233,7 +1238,7 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
         const uint32_t ep_step = a.ep0 + step * phases + 1;
         const bool head_step = a.force_head || step + 1 >= a.n_prompt;
         const bool last = step + 1 == a.steps;
-        const bool chunked = pos + 1 >= a.att_split_min;   // stage A by kv head and chunk (uniform)
+        constexpr bool chunked = CHUNKED;
         if (step < a.n_prompt) token = gp(a.tokens)[step];
         // embedding row of the token (reference src/qx_format.c:3759-3793), decoded by every
         // workgroup into its copy of x
@@ -1425,8 +1430,10 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                 rows_reduce<1>(part, out, lane);
                 const int r = 8 * wg + wave;
                 const float o = (ok && isfinite(out[0])) ? out[0] : 0.0f;
-                if (lane == 0) S.outw[wave] = S.xs[r] + o;
-                if (last && a.d_half && lane == 0) gpw(a.d_half)[l * 4096 + r] = o;
+                if (lane == 0) {
+                    S.outw[wave] = S.xs[r] + o;
+                    S.oatt[wave] = o;   // (dumped in stage D, after the x publish)
+                }
                 __syncthreads();
                 if (tid < 8) xstf(X + XO_XP + par * XN_XP + 8 * wg + tid, ep + 3, S.outw[tid]);
                 DMARK(l, 6);
@@ -1531,12 +1538,15 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     const double inv = S.xinv;
                     const double l0 = lane < (int)E ? logit(lane) : 0.0, l1 = lane + 64 < (int)E ? logit(lane + 64) : 0.0;
                     double wts[QXG_TOPK];
-                    wave_top8_weights(l0 * inv, l1 * inv, ids, wts);
+                    uint32_t pk[QXG_TOPK];   // the picks again, from LDS (the registers of ids are free after the row loads)
+#pragma unroll
+                    for (int q = 0; q < QXG_TOPK; ++q) pk[q] = S.dne[q];
+                    wave_top8_weights(l0 * inv, l1 * inv, pk, wts);
                     if (lane < 2 * QXG_TOPK) {   // lane 2q: hi word of weight q, lane 2q + 1: lo word
                         double wl = 0.0;
                         uint32_t il = 0u;
 #pragma unroll
-                        for (int q = 0; q < QXG_TOPK; ++q) if ((lane >> 1) == q) { wl = wts[q]; il = ids[q]; }
+                        for (int q = 0; q < QXG_TOPK; ++q) if ((lane >> 1) == q) { wl = wts[q]; il = pk[q]; }
                         const uint64_t bits = (uint64_t)__double_as_longlong(wl);
                         xst(X + XO_WT + par * XN_WT + lane, ep + 4, (lane & 1) ? (uint32_t)bits : (uint32_t)(bits >> 32));
                         if (last && a.d_rids && !(lane & 1)) { gpw(a.d_rids)[8 * l + (lane >> 1)] = il; gpw(a.d_rw)[8 * l + (lane >> 1)] = wl; }
@@ -1641,10 +1651,15 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
                     for (int q = 0; q < QXG_TOPK; ++q) moe += (float)(wr[q] * (double)S.ys[q][tid]);
                     const int r = 8 * wg + tid;
                     const float xn = S.xp[r] + moe;
-                    if (last && a.d_layer) gpw(a.d_layer)[l * 2048 + r] = xn;
-                    if (last && a.d_half) gpw(a.d_half)[l * 4096 + 2048 + r] = moe;
-                    if (last && a.d_res && l + 1 == L) gpw(a.d_res)[r] = xn;
                     xstf(X + XO_X + ((l + 1) & 1) * XN_X + r, ep + 5, xn);
+                    if (last) {   // the last step's dumps, after the publish (off the layer's critical path)
+                        if (a.d_layer) gpw(a.d_layer)[l * 2048 + r] = xn;
+                        if (a.d_half) {
+                            gpw(a.d_half)[l * 4096 + r] = S.oatt[tid];
+                            gpw(a.d_half)[l * 4096 + 2048 + r] = moe;
+                        }
+                        if (a.d_res && l + 1 == L) gpw(a.d_res)[r] = xn;
+                    }
                 }
                 DMARK(l, 12);
             }
@@ -1718,6 +1733,9 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) {
     }
 #endif
 }
+
+extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) { decode_steps<false>(args); }
+extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode_chunked(QxDArgs args) { decode_steps<true>(args); }
 
 // The routed experts' rows of one layer in the interleaved layout (QXD_GU_UNIT, QXD_DN_ROW),
 // from the IQ2_XS gate/up planes (qs 64, sc 8, d 2 bytes per block, 8 blocks per row) and

@@ -147,8 +147,6 @@ struct QxDArgs {
     uint32_t *abort;             // set on a timed-out wait; the host reports it
     uint64_t timeout;            // per wait, in 100 MHz ticks
     double sqrt_hd;
-    uint32_t att_split_min;      // positions n = pos + 1 from which stage A runs by kv head and chunk
-    uint32_t pad_;
 };
 #define QXD_THREADS 512
 // Interleaved expert rows of the persistent decode: unit (expert e, row r) of gate/up is
