@@ -133,10 +133,11 @@ int qx_dump_decode_block_summary(const char *path, const char *name, uint64_t bl
 /* reference qx_dump_final_head_probe_summary (include/qx_format.h:163). */
 int qx_dump_final_head_probe_summary(const char *path, const char *residual_path, const char *output_dir,
         const char *activation_mode, uint32_t top_n, FILE *out, char *err, uint64_t err_len);
-/* reference qx_dump_q8_k_activation_probe_summary (include/qx_format.h:156): the
- * probe's fixed inputs (inject: none, zero, nan, inf, positive, negative, edge)
- * quantized to Q8_K blocks on the GPU; same JSON keys and block bytes. */
-int qx_dump_q8_k_activation_probe_gpu(uint32_t values, const char *inject, FILE *out, char *err, uint64_t err_len);
+/* reference qx_dump_q8_k_activation_probe_summary (include/qx_format.h:156), same name
+ * and prototype: the probe's fixed inputs (inject: none, zero, nan, inf, positive,
+ * negative, edge) quantized to Q8_K blocks on the GPU; the reference's JSON keys, block
+ * bytes and error messages. */
+int qx_dump_q8_k_activation_probe_summary(uint32_t values, const char *inject, FILE *out, char *err, uint64_t err_len);
 /* reference qx_dump_state_loop_probe_summary and qx_dump_prompt_state_loop_probe_summary
  * (include/qx_format.h:157-158), same prototypes: the state loop of
  * src/qx_format.c:5970-6733 on the GPU.  The reference's argument checks run first, with

@@ -130,7 +130,8 @@ int qxg_int8_quantize(qxg_ctx *ctx, const float *x, uint32_t n, int8_t *codes, f
  * process ends) instead of per-call allocations.  At most QXG_STATIC_MAX_BLOCKS blocks
  * per call; more fail with an error.  Allocates nothing; returns when the output is
  * written.  Every call on one GPU shares its workspace: calls that overlap on one GPU
- * (from several threads or contexts) race. */
+ * (from several threads or contexts) are serialised by a per-GPU lock held from the
+ * repack until the call has finished. */
 #define QXG_STATIC_MAX_BLOCKS 4096u
 int qxg_dequant_blocks_static(qxg_ctx *ctx, uint32_t ggml_type, const void *raw_dev, uint64_t nblocks, float *out_dev,
                               char *err, uint64_t err_len);

@@ -865,6 +865,12 @@ static __device__ __align__(256) uint8_t scratch[SCR_BYTES];
 namespace {
 std::mutex g_scratch_mu;
 std::map<int, uint8_t *> g_scratch_addr;   // device -> address of its copy of `scratch`
+std::map<int, std::mutex> g_scratch_use;   // device -> held by a call using its copy (repack through finish)
+
+std::mutex &scratch_use(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_scratch_use[device];   // (map nodes do not move)
+}
 
 // the calling thread's current device must be `device`
 bool scratch_address(int device, uint8_t **addr, char *err, uint64_t n) {
@@ -1343,6 +1349,9 @@ int qxg_dequant_blocks_static(qxg_ctx *c, uint32_t type, const void *raw_dev, ui
         return 0;
     }
     if (!c->scratch) { set_err(err, err_len, "static workspace address not set"); return 0; }
+    // calls on one GPU share its workspace: held from the repack until the call has finished,
+    // so overlapping calls (other contexts, other threads) run one after another
+    std::lock_guard<std::mutex> use(scratch_use(c->device));
     (void)hipSetDevice(c->device);
     const uint8_t *raw = (const uint8_t *)raw_dev;
     uint8_t *p0 = c->scratch + SCR_P0, *p1 = c->scratch + SCR_P1, *p2 = c->scratch + SCR_P2;

@@ -1252,6 +1252,9 @@ DEV void decode_steps(const QxDArgs &args) {
             const uint32_t ep = ep_step + 5 * l;   // + 0 X, + 1 QKV, + 2 CX, + 3 XP/LG, + 4 H/WT
             const uint32_t par = l & 1;
             const uint32_t ln = l + 1 < L ? l + 1 : 0u;   // after the last layer: layer 0 of the next step
+            // the next layer's rows are prefetched in this layer, except after the last layer of
+            // a head step (layer 0's come in after the argmax exchange) or of the launch's last step
+            const bool pre = l + 1 < L || !(head_step || last);
             // ---------------------------------------------------------- stage Q
             double a_part = 0.0;   // router x-part of expert wg (workgroups < E)
             {
@@ -1352,7 +1355,7 @@ DEV void decode_steps(const QxDArgs &args) {
             load_wm(a, l, wm0, wm1);
             if (wg >= QXG_HEADS && !chunked) {
                 load_o(a, l, wo, S.wo[wave_id()]);
-                load_wq(a, ln, wq, S.wq[wave_id()]);
+                if (pre) load_wq(a, ln, wq, S.wq[wave_id()]);
             }
             // ---------------------------------------------------------- stage A
             if (chunked) {
@@ -1364,7 +1367,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 if (!attention_merge(a, l, pos, ep + 2, S, ctl, last)) return;
                 if (wg >= QXG_HEADS) {   // (the context exchange hides them)
                     load_o(a, l, wo, S.wo[wave_id()]);
-                    load_wq(a, ln, wq, S.wq[wave_id()]);
+                    if (pre) load_wq(a, ln, wq, S.wq[wave_id()]);
                 }
             } else if (wg < QXG_HEADS) {
                 if (!attn_wait(a, l, ep + 1, S, ctl)) return;
@@ -1601,7 +1604,7 @@ DEV void decode_steps(const QxDArgs &args) {
                     return;
                 DMARK(l, 11);
                 wait_loads();   // the down rows (copied before the poll's loads, so already in)
-                load_wr(a, ln, wo);   // the next layer's router row
+                if (pre) load_wr(a, ln, wo);   // the next layer's router row
                 const uint32_t *wtw = S.u.m.vin + 6144;
                 double wr[QXG_TOPK];
 #pragma unroll
@@ -1709,10 +1712,12 @@ DEV void decode_steps(const QxDArgs &args) {
             if (!wait_xch2<1>(X + XO_AM + (step & 1) * XN_AM, XN_AM, eph + 1, S.u.hd.am, Ident(), S, ctl))
                 return;
             DMARK(48, 4);
-            // layer 0's rows again (also on the last step), after the argmax exchange: issued
-            // earlier, its poll would wait behind them (loads complete in order)
-            if (wg >= QXG_HEADS) load_wq(a, 0, wq, S.wq[wave_id()]);
-            load_wr(a, 0, wo);
+            // layer 0's rows for the next step, after the argmax exchange: issued earlier, its
+            // poll would wait behind them (loads complete in order); none after the last step
+            if (!last) {
+                if (wg >= QXG_HEADS) load_wq(a, 0, wq, S.wq[wave_id()]);
+                load_wr(a, 0, wo);
+            }
             float v = __uint_as_float(S.u.hd.am[0]);
             uint32_t i = S.u.hd.am[1];
             for (int w = 1; w < NWG; ++w) {

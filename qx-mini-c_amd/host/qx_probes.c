@@ -121,7 +121,7 @@ int qx_dump_final_head_probe_summary(const char *path, const char *residual_path
 /* Q8_K blocks of the probe's fixed inputs, quantized on the GPU (reference
  * qx_dump_q8_k_activation_probe_summary, src/qx_format.c:4304-4345: same inputs,
  * injections, errors and JSON keys). */
-int qx_dump_q8_k_activation_probe_gpu(uint32_t values, const char *inject, FILE *out, char *err, uint64_t err_len) {
+int qx_dump_q8_k_activation_probe_summary(uint32_t values, const char *inject, FILE *out, char *err, uint64_t err_len) {
     static const char *const kinds[] = {"none", "zero", "nan", "inf", "positive", "negative", "edge"};
     int kind = -1;
     for (int i = 0; inject && i < 7; ++i) if (!strcmp(inject, kinds[i])) kind = i;
@@ -152,7 +152,7 @@ int qx_dump_q8_k_activation_probe_gpu(uint32_t values, const char *inject, FILE 
             for (int i = 0; i < 256; ++i) qsum += (int8_t)b[292ull * k + 4 + i];
         float d0;
         memcpy(&d0, b, 4);
-        fprintf(out, "{\n  \"probe\": \"q8_k_activation\",\n  \"backend\": \"hip\",\n"
+        fprintf(out, "{\n  \"probe\": \"q8_k_activation\",\n"
                 "  \"activation_format\": \"q8_k_compat\",\n  \"values\": %u,\n  \"blocks\": %u,\n"
                 "  \"block_bytes\": 292,\n  \"workspace_bytes\": %u,\n  \"first_scale\": %.9g,\n"
                 "  \"quant_sum\": %lld,\n  \"finite\": true,\n  \"block_hex\": \"",

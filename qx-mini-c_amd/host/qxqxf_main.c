@@ -234,7 +234,7 @@ int main(int argc, char **argv) {
             else { usage(argv[0]); return 2; }
         }
         if (!seen) { fprintf(stderr, "q8-k-activation-probe failed: invalid --values\n"); return 2; }
-        if (!qx_dump_q8_k_activation_probe_gpu(values, inject, stdout, err, sizeof(err))) {
+        if (!qx_dump_q8_k_activation_probe_summary(values, inject, stdout, err, sizeof(err))) {
             fprintf(stderr, "q8-k-activation-probe failed: %s\n", err);
             return 1;
         }

@@ -245,6 +245,9 @@ def test_q8k_cli_probe_matches_reference(tmp_path):
         j = json.loads(r.stdout)
         assert str(j["checksum"]) == want["checksum"] and j["quant_sum"] == want["quant_sum"], key
         assert j["first_scale"] == want["first_scale"] and j["block_bytes"] == 292
+        # the reference's keys, in its order (src/qx_format.c:4331-4343)
+        assert list(j) == ["probe", "activation_format", "values", "blocks", "block_bytes", "workspace_bytes",
+                           "first_scale", "quant_sum", "finite", "block_hex", "checksum"], list(j)
     r = subprocess.run([exe, "q8-k-activation-probe", "--values", "256", "--inject", "nan"], capture_output=True,
                        text=True, timeout=60)
     assert r.returncode == 1 and "NaN or Inf" in r.stderr

@@ -107,6 +107,24 @@ def test_abi_library_exports_every_declared_symbol():
             assert hasattr(lib, n), f"{n} declared in {header} but not exported"
 
 
+def test_reference_prototypes_compile_and_link(tmp_path):
+    """A C caller written against the reference's declarations of the replaced entry points
+    (tests/abi/reference_prototypes.c holds them verbatim beside include/qx_host.h) compiles
+    without conflicting types, links against libqxhost.so by those names, and runs (it only
+    takes their addresses)."""
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    lib = os.path.join(ROOT, "qx-mini-c_amd", "lib")
+    exe = tmp_path / "abi_check"
+    r = subprocess.run([gcc, "-std=c17", "-Wall", "-Wextra", "-Werror", "-I" + os.path.join(ROOT, "include"),
+                        os.path.join(ROOT, "tests", "abi", "reference_prototypes.c"), "-o", str(exe), "-L" + lib,
+                        "-lqxhost", "-lqxg", "-Wl,-rpath," + lib], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip() == "7", (r.returncode, r.stdout, r.stderr)
+
+
 def _have_gpu():
     try:
         c = qxg.Context(0)
