@@ -104,6 +104,36 @@ int qxg_decode_token(qxg_ctx *ctx, uint32_t token, uint32_t position, int run_he
 int qxg_generate(qxg_ctx *ctx, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_gen, uint32_t pos0,
                  uint32_t *tokens_out, float *elapsed_ms, char *err, uint64_t err_len);
 
+/* 1 when qxg_generate / qxg_decode_token run the persistent decode on this context (the
+ * layer path set to 1, the f32 activation mode, every bound format one it decodes), else 0.
+ * No reference counterpart. */
+int qxg_persistent_path(const qxg_ctx *ctx);
+
+/* qxg_generate with every step's records, for the reference's prompt state loop
+ * (qx_dump_prompt_state_loop_probe_summary, src/qx_format.c:6250-6627, which prints them per
+ * step and layer): one persistent launch over the S = n_prompt + n_gen - 1 steps, then the
+ * top_n (<= 32) tokens of each head step ranked on the device and everything copied back in
+ * bulk.  Persistent path only (qxg_persistent_path); the records live in device buffers
+ * allocated for the call.  Outputs, any of which may be NULL, with L = the bound layers:
+ *   tokens_out[S + 1]      the prompt, then each generated id at [step + 1];
+ *   layer_out[S][L][2048]  each layer's output residual;
+ *   attn_out, moe_out      [S][L][2048] each layer's attention output and MoE sum (before
+ *                          their residual adds, as qxg_decode_halves);
+ *   ids_out, weights_out   [S][L][8] the routing (as qxg_decode_routing);
+ *   head_sums_out[S][L][32] each q head's sum of normalised attention weights;
+ *   norm_out[S][2048], logits_out[S][vocab]   each head step's output-RMSNorm vector and
+ *                          logits (steps before the last prompt token hold no head);
+ *   top_ids, top_logits    [S][top_n] each head step's best tokens, highest first;
+ *   step_ms[S + 1]         the device clock at each step's start and at the end, in ms from
+ *                          the first step's start;
+ *   elapsed_ms             the device time of the launch (HIP events).
+ * Returns 0 on a non-finite final logit (src/qx_format.c:3715) or a bad argument. */
+int qxg_generate_recorded(qxg_ctx *ctx, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_gen, uint32_t pos0,
+                          uint32_t top_n, uint32_t *tokens_out, float *layer_out, float *attn_out, float *moe_out,
+                          uint32_t *ids_out, double *weights_out, double *head_sums_out, float *norm_out, float *logits_out,
+                          uint32_t *top_ids, double *top_logits, double *step_ms, float *elapsed_ms, char *err,
+                          uint64_t err_len);
+
 /* ---- same-input replay seams (host pointers in and out, synchronous) ---- */
 
 /* Q4_K embedding row of `token` as 2048 floats, no norm on the full-MoE path:
@@ -249,6 +279,22 @@ int qxg_decode_halves(qxg_ctx *ctx, uint32_t layers, float *attn_out, float *moe
  * and merges the chunks' partial softmax results; below it the 32 q-head workgroups walk
  * the cache themselves.  Default 257; 1 chunks every position, 4097 never. */
 int qxg_set_attention_chunks(qxg_ctx *ctx, uint32_t min_positions);
+
+/* The output-RMSNorm vector (2048 floats) of the last head step run by qxg_decode_token:
+ * the normalised final residual the head consumed (src/qx_format.c:3655, the state loop's
+ * final_norm_raw). */
+int qxg_decode_final_norm(qxg_ctx *ctx, float *norm_out, char *err, uint64_t err_len);
+
+/* Each q head's sum of its normalised attention weights in every layer of the last step run
+ * by qxg_decode_token: sums[l*32 + h].  The state loop's per-layer softmax_sum fields
+ * (src/qx_format.c:5183-5190, printed at :6494-6529); the reference keeps no other record. */
+int qxg_decode_head_sums(qxg_ctx *ctx, uint32_t layers, double *sums, char *err, uint64_t err_len);
+
+/* The cache rows of one position in layers [0, layers): k, v layers*512 int8 and the
+ * scales, one strided copy each (qxg_kv_read per layer, batched for the state loop's
+ * per-step K/V checksums, src/qx_format.c:6494-6529). */
+int qxg_kv_read_position(qxg_ctx *ctx, uint32_t position, uint32_t layers, int8_t *k, int8_t *v, float *ks, float *vs,
+                         char *err, uint64_t err_len);
 
 /* Same-input seam of the Q8_K quantizer the q8_k_compat kernels use: n values (a
  * multiple of 256, at most 4096) -> n/256 blocks of 292 bytes in ggml's block_q8_K

@@ -126,6 +126,7 @@ struct qxg_ctx {
     float *x = nullptr, *qkv = nullptr, *ctxv = nullptr, *h = nullptr, *logits = nullptr;
     float *vcur = nullptr, *attn = nullptr, *moe = nullptr, *norm = nullptr, *layer_dump = nullptr;
     float *half_dump = nullptr;    // [layer][attention 2048 | MoE 2048] of the last qxg_decode_token step
+    double *wsum_dump = nullptr;   // [layer][32] each head's sum of normalised attention weights (same step)
     uint32_t att_split_min = QXD_SPLIT_MIN_DEFAULT;   // persistent decode: chunked stage A from n = pos + 1 on
     double *rlog = nullptr;
     uint32_t *route_ids = nullptr;  // [layer][8] experts of the last step, in rank order
@@ -156,6 +157,7 @@ struct qxg_ctx {
     uint64_t *xch = nullptr;
     uint64_t *xpart = nullptr;       // partial results of the chunked attention (2 x QXD_PART_WORDS)
     uint32_t next_ep = 0;            // epoch base of the next persistent launch
+    bool coop_held = false;          // another process holds the GPU's cooperative launches: launch plainly
     uint32_t *abort = nullptr;
     uint8_t *scratch = nullptr;      // device address of this GPU's static workspace (qxg_dequant_blocks_static)
     // one decode step (embed .. head, top-1, step advance) recorded once and replayed
@@ -378,8 +380,12 @@ bool persistent(const qxg_ctx *c) {
 
 struct DecodeDumps {
     float *layer = nullptr, *res = nullptr, *logits = nullptr, *half = nullptr;
+    double *wsum = nullptr;
+    float *norm = nullptr;
     uint32_t *rids = nullptr;
+    bool rec_all = false;   // every step's dumps, one slot per step of the call
     double *rw = nullptr;
+    uint64_t *time = nullptr;   // with rec_all: each step's start and the end, 100 MHz ticks
 };
 
 // One cooperative launch of the persistent decode for `steps` steps from pos0 (tokens
@@ -414,6 +420,11 @@ bool launch_decode_part(qxg_ctx *c, bool chunked, uint32_t s0, uint32_t steps, u
     a.xch = c->xch;
     a.xpart = c->xpart;
     a.logits = d.logits; a.d_layer = d.layer; a.d_rids = d.rids; a.d_rw = d.rw; a.d_res = d.res; a.d_half = d.half;
+    a.d_wsum = d.wsum;
+    a.d_norm = d.norm;
+    a.rec_all = d.rec_all ? 1u : 0u;
+    a.rec_base = s0;
+    a.d_time = d.rec_all ? d.time : nullptr;
     a.abort = c->abort;
     a.timeout = DECODE_WAIT_TICKS;
     a.sqrt_hd = std::sqrt(128.0);
@@ -421,10 +432,23 @@ bool launch_decode_part(qxg_ctx *c, bool chunked, uint32_t s0, uint32_t steps, u
     void *args[] = {&a};
     const Timer t = timer_for(c, 7);
     if (t.e0) (void)hipEventRecord(t.e0, c->s);
-    if (!hip_ok(hipLaunchCooperativeKernel(chunked ? (const void *)qxk_decode_chunked : (const void *)qxk_decode,
-                                           dim3(QXG_PBLOCKS), dim3(QXD_THREADS), args, 0, c->s),
-                err, n, "persistent decode launch"))
-        return false;
+    // A cooperative launch fails rather than run unless every workgroup can be resident.  The
+    // runtime grants cooperative launches on a GPU to one process at a time: once another
+    // process has made one, ours are refused (hipErrorIllegalState) while it lives.  Then the
+    // kernel is launched plainly: one workgroup per CU fits (checked at open), so on a GPU not
+    // saturated by other work all of them are resident, and every wait is bounded
+    // (DECODE_WAIT_TICKS; a timed-out launch exits and the call reports it).
+    const void *fn = chunked ? (const void *)qxk_decode_chunked : (const void *)qxk_decode;
+    hipError_t e = hipErrorIllegalState;
+    if (!c->coop_held) {
+        e = hipLaunchCooperativeKernel(fn, dim3(QXG_PBLOCKS), dim3(QXD_THREADS), args, 0, c->s);
+        if (e == hipErrorIllegalState) {
+            (void)hipGetLastError();   // the refusal is not an error of the call
+            c->coop_held = true;
+        }
+    }
+    if (c->coop_held) e = hipLaunchKernel(fn, dim3(QXG_PBLOCKS), dim3(QXD_THREADS), args, 0, c->s);
+    if (!hip_ok(e, err, n, "persistent decode launch")) return false;
     if (t.e1) (void)hipEventRecord(t.e1, c->s);
     return true;
 }
@@ -902,7 +926,7 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
         return 0;
     }
     {   // the persistent decode keeps one workgroup resident on each of QXG_PBLOCKS CUs (a
-        // cooperative launch, which fails rather than run if they cannot all be resident)
+        // cooperative launch where the runtime grants one, see launch_decode_part)
         int occ = 0, coop = 0;
         if (prop.multiProcessorCount < QXG_PBLOCKS ||
             hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device) != hipSuccess || !coop ||
@@ -987,7 +1011,7 @@ void qxg_close(qxg_ctx *c) {
                     c->qkv, c->ctxv, c->h, c->logits, c->vcur, c->attn, c->moe, c->norm, c->layer_dump, c->rlog,
                     c->cand_v, c->top_v, c->cand_i, c->top_i, c->tokens, c->dig, c->st, c->staging,
                     c->xch, c->xpart, c->abort, c->apart, c->route_ids, c->route_w, c->mfold, c->gu_il, c->dn_il, c->head_il, c->dpack,
-                    c->T.rope_cs, c->half_dump};
+                    c->T.rope_cs, c->half_dump, c->wsum_dump};
     for (void *p : bufs) if (p) (void)hipFree(p);
     for (void *p : c->arenas) (void)hipFree(p);
     for (void *p : c->pf.all) (void)hipFree(p);
@@ -1093,7 +1117,7 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
                      (void **)&c->vcur, (void **)&c->attn, (void **)&c->moe, (void **)&c->norm,
                      (void **)&c->layer_dump, (void **)&c->rlog, (void **)&c->cand_v, (void **)&c->top_v,
                      (void **)&c->cand_i, (void **)&c->top_i, (void **)&c->tokens, (void **)&c->dig, (void **)&c->apart,
-                     (void **)&c->route_ids, (void **)&c->route_w, (void **)&c->half_dump};
+                     (void **)&c->route_ids, (void **)&c->route_w, (void **)&c->half_dump, (void **)&c->wsum_dump};
     for (void **b : bufs) if (*b) { (void)hipFree(*b); *b = nullptr; }
     const uint64_t V = c->vocab ? c->vocab : 1;
     const uint64_t sizes[] = {2048 * 4, 5120 * 4, 4096 * 4, 8 * 768 * 4, V * 4, 512 * 4, 2048 * 4, 2048 * 4, 2048 * 4,
@@ -1101,7 +1125,7 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
                               QXG_MAX_TOPN * 4, TOPK_BLOCKS * QXG_MAX_TOPN * 4, QXG_MAX_TOPN * 4,
                               (QXG_MAX_CTX + 2) * 4, (64 * 28 + 4) * 4, QXG_ATT_PART_BYTES,
                               (uint64_t)(layers ? layers : 1) * 8 * 4, (uint64_t)(layers ? layers : 1) * 8 * 8,
-                              (uint64_t)(layers ? layers : 1) * 4096 * 4};
+                              (uint64_t)(layers ? layers : 1) * 4096 * 4, (uint64_t)(layers ? layers : 1) * 32 * 8};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); ++i)
         if (!hip_ok(hipMalloc(bufs[i], sizes[i]), err, err_len, "work buffers")) return 0;
     if (!hip_ok(hipMemset(c->tokens, 0, sizes[15]), err, err_len, "work buffers")) return 0;
@@ -1184,6 +1208,8 @@ int qxg_decode_token(qxg_ctx *c, uint32_t token, uint32_t position, int run_head
         // of those logits by the per-phase selection kernels
         DecodeDumps d;
         d.layer = c->layer_dump; d.res = c->x; d.rids = c->route_ids; d.rw = c->route_w; d.half = c->half_dump;
+        d.wsum = c->wsum_dump;
+        d.norm = run_head ? c->norm : nullptr;
         d.logits = run_head ? c->logits : nullptr;
         if (!launch_decode(c, 1, run_head ? 1 : 2, position, false, d, err, err_len)) return 0;
         if (run_head) {
@@ -1195,12 +1221,12 @@ int qxg_decode_token(qxg_ctx *c, uint32_t token, uint32_t position, int run_head
     } else {
         hipLaunchKernelGGL(qxk_embed, dim3(1), dim3(256), 0, c->s, c->emb, c->emb_row, c->tokens, c->st, c->x);
         for (uint32_t l = 0; l < c->layers; ++l) {
-            launch_attention(c, l, c->x, c->half_dump + 4096ull * l, nullptr);
+            launch_attention(c, l, c->x, c->half_dump + 4096ull * l, nullptr, c->wsum_dump + 32ull * l);
             launch_moe(c, l, c->x, c->half_dump + 4096ull * l + 2048);
             if (layer_out)
                 (void)hipMemcpyAsync(c->layer_dump + 2048ull * l, c->x, 2048 * 4, hipMemcpyDeviceToDevice, c->s);
         }
-        if (run_head) launch_head(c, top_n, nullptr);
+        if (run_head) launch_head(c, top_n, c->norm);
     }
     if (!finish(c, err, err_len)) return 0;
     if (residual_out && !hip_ok(hipMemcpy(residual_out, c->x, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
@@ -1604,6 +1630,102 @@ int qxg_time_kernel(qxg_ctx *c, int which, uint32_t layer, uint32_t iters, float
 
 uint64_t qxg_device_bytes(const qxg_ctx *c) { return c ? c->dev_bytes : 0; }
 
+int qxg_persistent_path(const qxg_ctx *c) { return c && c->bound && c->layers && persistent(c) ? 1 : 0; }
+
+int qxg_generate_recorded(qxg_ctx *c, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_gen, uint32_t pos0,
+                          uint32_t top_n, uint32_t *tokens_out, float *layer_out, float *attn_out, float *moe_out,
+                          uint32_t *ids_out, double *weights_out, double *head_sums_out, float *norm_out, float *logits_out,
+                          uint32_t *top_ids, double *top_logits, double *step_ms, float *elapsed_ms, char *err,
+                          uint64_t err_len) {
+    if (!check_ready(c, true, err, err_len)) return 0;
+    if (!persistent(c) || !c->layers) { set_err(err, err_len, "recorded generation runs the persistent decode only"); return 0; }
+    if (!prompt || !n_prompt || !n_gen) { set_err(err, err_len, "generation needs >= 1 prompt token and >= 1 generated token"); return 0; }
+    const uint64_t steps = (uint64_t)n_prompt + n_gen - 1, L = c->layers, V = c->vocab;
+    if (pos0 + steps > c->kv_ctx || c->layers > c->kv_layers) { set_err(err, err_len, "prompt plus generation exceeds the KV context"); return 0; }
+    for (uint32_t i = 0; i < n_prompt; ++i)
+        if (prompt[i] >= c->vocab) { set_err(err, err_len, "prompt token out of range"); return 0; }
+    if (top_n == 0) top_n = 1;
+    if (top_n > QXG_MAX_TOPN) top_n = QXG_MAX_TOPN;
+    (void)hipSetDevice(c->device);
+    // one slot per step of every record (device), freed at the end of the call
+    const uint64_t n_lay = steps * L * 2048, n_half = steps * L * 4096, n_ids = steps * L * 8, n_ws = steps * L * 32;
+    const uint64_t n_res = steps * 2048, n_lg = steps * V, n_top = steps * QXG_MAX_TOPN;
+    float *d_lay = nullptr, *d_half = nullptr, *d_res = nullptr, *d_norm = nullptr, *d_lg = nullptr, *d_tv = nullptr;
+    uint32_t *d_ids = nullptr, *d_ti = nullptr, *d_tok = nullptr;
+    double *d_w = nullptr, *d_ws = nullptr;
+    uint64_t *d_time = nullptr;
+    DevState *d_post = nullptr;
+    struct Frees {
+        std::vector<void *> p;
+        ~Frees() { for (void *q : p) if (q) (void)hipFree(q); }
+    } frees;
+    auto get = [&](void **q, uint64_t bytes) {
+        if (!hip_ok(hipMalloc(q, bytes), err, err_len, "record buffers")) return false;
+        frees.p.push_back(*q);
+        return true;
+    };
+    if (!get((void **)&d_lay, n_lay * 4) || !get((void **)&d_half, n_half * 4) || !get((void **)&d_res, n_res * 4) ||
+        !get((void **)&d_norm, n_res * 4) || !get((void **)&d_lg, n_lg * 4) || !get((void **)&d_tv, n_top * 4) ||
+        !get((void **)&d_ids, n_ids * 4) || !get((void **)&d_ti, n_top * 4) || !get((void **)&d_tok, 8) ||
+        !get((void **)&d_w, n_ids * 8) || !get((void **)&d_ws, n_ws * 8) || !get((void **)&d_post, sizeof(DevState)) ||
+        !get((void **)&d_time, (steps + 1) * 8))
+        return 0;
+    (void)hipMemcpyAsync(c->tokens, prompt, (uint64_t)n_prompt * 4, hipMemcpyHostToDevice, c->s);
+    write_state(c, pos0, 0, n_prompt, 0);
+    DecodeDumps d;
+    d.layer = d_lay; d.res = d_res; d.rids = d_ids; d.rw = d_w; d.half = d_half; d.wsum = d_ws; d.norm = d_norm; d.logits = d_lg;
+    d.rec_all = true;
+    d.time = d_time;
+    (void)hipEventRecord(c->e0, c->s);
+    if (!launch_decode(c, (uint32_t)steps, n_prompt, pos0, false, d, err, err_len)) return 0;
+    (void)hipEventRecord(c->e1, c->s);
+    // each head step's top-N from its recorded logits (the per-phase selection kernels, on a
+    // scratch state that marks a generate step and a scratch token pair)
+    DevState post{};
+    post.n_prompt = 1;
+    (void)hipMemcpyAsync(d_post, &post, sizeof(post), hipMemcpyHostToDevice, c->s);
+    for (uint64_t s = (n_prompt > 0 ? n_prompt - 1 : 0); s < steps; ++s) {
+        hipLaunchKernelGGL(qxk_topk, dim3(TOPK_BLOCKS), dim3(256), 0, c->s, (const float *)(d_lg + s * V), c->vocab, top_n,
+                           c->cand_v, c->cand_i, d_tv + s * QXG_MAX_TOPN, d_ti + s * QXG_MAX_TOPN, d_tok, d_post);
+        hipLaunchKernelGGL(qxk_topk_merge, dim3(1), dim3(256), 0, c->s, (const float *)c->cand_v, (const uint32_t *)c->cand_i,
+                           (uint32_t)TOPK_BLOCKS, top_n, d_tv + s * QXG_MAX_TOPN, d_ti + s * QXG_MAX_TOPN, d_tok, d_post);
+    }
+    if (!finish(c, err, err_len)) return 0;
+    if (elapsed_ms) (void)hipEventElapsedTime(elapsed_ms, c->e0, c->e1);
+    DevState h;
+    if (!read_state(c, h, err, err_len)) return 0;
+    if (h.nonfinite) { write_state(c, 0, 0, 0, 0); set_err(err, err_len, "non-finite final logit"); return 0; }
+    auto rd = [&](void *dst, const void *src, uint64_t bytes) {
+        return !dst || hip_ok(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), err, err_len, "read");
+    };
+    if (!rd(tokens_out, c->tokens, (steps + 1) * 4) || !rd(layer_out, d_lay, n_lay * 4) || !rd(ids_out, d_ids, n_ids * 4) ||
+        !rd(weights_out, d_w, n_ids * 8) || !rd(head_sums_out, d_ws, n_ws * 8) || !rd(norm_out, d_norm, n_res * 4) ||
+        !rd(logits_out, d_lg, n_lg * 4))
+        return 0;
+    if (attn_out && !hip_ok(hipMemcpy2D(attn_out, 2048 * 4, d_half, 4096 * 4, 2048 * 4, steps * L, hipMemcpyDeviceToHost),
+                            err, err_len, "read"))
+        return 0;
+    if (moe_out && !hip_ok(hipMemcpy2D(moe_out, 2048 * 4, d_half + 2048, 4096 * 4, 2048 * 4, steps * L, hipMemcpyDeviceToHost),
+                           err, err_len, "read"))
+        return 0;
+    if (step_ms) {   // the device clock (100 MHz) of each step's start and the end, from the first start
+        std::vector<uint64_t> t(steps + 1);
+        if (!rd(t.data(), d_time, (steps + 1) * 8)) return 0;
+        for (uint64_t s = 0; s <= steps; ++s) step_ms[s] = (double)(int64_t)(t[s] - t[0]) * 1e-5;
+    }
+    if (top_ids || top_logits) {
+        std::vector<float> tv(n_top);
+        std::vector<uint32_t> ti(n_top);
+        if (!rd(tv.data(), d_tv, n_top * 4) || !rd(ti.data(), d_ti, n_top * 4)) return 0;
+        for (uint64_t s = 0; s < steps; ++s)
+            for (uint32_t i = 0; i < top_n; ++i) {
+                if (top_ids) top_ids[s * top_n + i] = ti[s * QXG_MAX_TOPN + i];
+                if (top_logits) top_logits[s * top_n + i] = (double)tv[s * QXG_MAX_TOPN + i];
+            }
+    }
+    return 1;
+}
+
 int qxg_decode_routing(qxg_ctx *c, uint32_t layers, uint32_t *ids, double *weights, char *err, uint64_t err_len) {
     if (!check_ready(c, false, err, err_len)) return 0;
     if (!layers || layers > c->layers || !ids || !weights) { set_err(err, err_len, "invalid argument"); return 0; }
@@ -1618,11 +1740,43 @@ int qxg_decode_halves(qxg_ctx *c, uint32_t layers, float *attn_out, float *moe_o
     if (!layers || layers > c->layers) { set_err(err, err_len, "invalid argument"); return 0; }
     (void)hipSetDevice(c->device);
     if (!hip_ok(hipStreamSynchronize(c->s), err, err_len, "stream")) return 0;
-    for (uint32_t l = 0; l < layers; ++l) {
-        if (attn_out && !hip_ok(hipMemcpy(attn_out + 2048ull * l, c->half_dump + 4096ull * l, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
-        if (moe_out && !hip_ok(hipMemcpy(moe_out + 2048ull * l, c->half_dump + 4096ull * l + 2048, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read")) return 0;
+    // one strided copy per half ([layer][attention | MoE] on the device)
+    return (!attn_out || hip_ok(hipMemcpy2D(attn_out, 2048 * 4, c->half_dump, 4096 * 4, 2048 * 4, layers, hipMemcpyDeviceToHost),
+                                err, err_len, "read")) &&
+           (!moe_out || hip_ok(hipMemcpy2D(moe_out, 2048 * 4, c->half_dump + 2048, 4096 * 4, 2048 * 4, layers,
+                                           hipMemcpyDeviceToHost), err, err_len, "read"));
+}
+
+int qxg_decode_final_norm(qxg_ctx *c, float *norm_out, char *err, uint64_t err_len) {
+    if (!check_ready(c, false, err, err_len)) return 0;
+    if (!norm_out) { set_err(err, err_len, "invalid argument"); return 0; }
+    (void)hipSetDevice(c->device);
+    return hip_ok(hipStreamSynchronize(c->s), err, err_len, "stream") &&
+           hip_ok(hipMemcpy(norm_out, c->norm, 2048 * 4, hipMemcpyDeviceToHost), err, err_len, "read");
+}
+
+int qxg_decode_head_sums(qxg_ctx *c, uint32_t layers, double *sums, char *err, uint64_t err_len) {
+    if (!check_ready(c, false, err, err_len)) return 0;
+    if (!layers || layers > c->layers || !sums) { set_err(err, err_len, "invalid argument"); return 0; }
+    (void)hipSetDevice(c->device);
+    return hip_ok(hipStreamSynchronize(c->s), err, err_len, "stream") &&
+           hip_ok(hipMemcpy(sums, c->wsum_dump, (uint64_t)layers * 32 * 8, hipMemcpyDeviceToHost), err, err_len, "read");
+}
+
+int qxg_kv_read_position(qxg_ctx *c, uint32_t position, uint32_t layers, int8_t *k, int8_t *v, float *ks, float *vs,
+                         char *err, uint64_t err_len) {
+    if (!check_ready(c, true, err, err_len)) return 0;
+    if (!layers || layers > c->kv_layers || position >= c->kv_ctx || !k || !v || !ks || !vs) {
+        set_err(err, err_len, "invalid argument");
+        return 0;
     }
-    return 1;
+    (void)hipSetDevice(c->device);
+    const uint64_t pitch = (uint64_t)c->kv_ctx * 512, spitch = (uint64_t)c->kv_ctx * 4;
+    return hip_ok(hipStreamSynchronize(c->s), err, err_len, "stream") &&
+           hip_ok(hipMemcpy2D(k, 512, c->kc + (uint64_t)position * 512, pitch, 512, layers, hipMemcpyDeviceToHost), err, err_len, "read") &&
+           hip_ok(hipMemcpy2D(v, 512, c->vc + (uint64_t)position * 512, pitch, 512, layers, hipMemcpyDeviceToHost), err, err_len, "read") &&
+           hip_ok(hipMemcpy2D(ks, 4, c->ks + position, spitch, 4, layers, hipMemcpyDeviceToHost), err, err_len, "read") &&
+           hip_ok(hipMemcpy2D(vs, 4, c->vs + position, spitch, 4, layers, hipMemcpyDeviceToHost), err, err_len, "read");
 }
 
 int qxg_set_attention_chunks(qxg_ctx *c, uint32_t min_positions) {

@@ -315,7 +315,7 @@ DEV void upper_waves_sync(DLds &S, uint32_t tag) {
 // weights of the thread's 8 values (threads < 256).
 // The inverse RMS goes to *inv_out.  Returns true when every value is finite.
 template <int N, bool NORM>
-DEV bool vec_digits(const float *v, const float *w8, DLds &S, double *inv_out = nullptr) {
+DEV bool vec_digits(const float *v, const float *w8, DLds &S, double *inv_out = nullptr, GLB float *norm_out = nullptr) {
     constexpr int NCH = N / 8;
     const int tid = tix(), lane = tid & 63, wave = tid >> 6;
     double inv = 1.0;
@@ -341,6 +341,10 @@ DEV bool vec_digits(const float *v, const float *w8, DLds &S, double *inv_out = 
         if constexpr (NORM) {   // c == tid: w8 holds the thread's 8 weights
 #pragma unroll
             for (int i = 0; i < 8; ++i) y[i] = (float)((double)y[i] * inv) * w8[i];
+            if (norm_out) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) norm_out[8 * c + i] = y[i];
+            }
         }
         float mx = 0.0f;
 #pragma unroll
@@ -669,8 +673,8 @@ DEV float wave_max_f(float v) {
 }
 
 // ep: the QKV phase (the context goes out at ep + 1)
-DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, const AttnPre &pre, DLds &S, bool last) {
-    (void)last;
+// rrow: the record row (slot * layers + l) of this layer's dumps, or -1
+DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, const AttnPre &pre, DLds &S, bool last, int rrow) {
     AttnS &A = S.u.att;
     const int tid = tix(), lane = tid & 63;
     const int w = wave_id();
@@ -851,6 +855,12 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
             o = fmaf((float)(fw[v] * invL), part, o);
         }
         xstf(gpw(a.xch) + XO_CX + (l & 1) * XN_CX + 128 * h + tid, ep + 1, o);   // the CX phase
+        if (rrow >= 0 && a.d_wsum && tid == 0) {   // the head's sum of normalised weights (the state loop's softmax_sum)
+            double ws = 0.0;
+#pragma unroll
+            for (int v = 0; v < NWV; ++v) ws += (fw[v] * invL) * A.l[v];
+            gpw(a.d_wsum)[(uint32_t)rrow * 32 + h] = ws;
+        }
     }
     __syncthreads();   // the union is reused by the next stage
 }
@@ -1073,7 +1083,7 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
 
 // Every workgroup: q head wgi / 8, dimensions 16 (wgi % 8) .. merged over the chunks, published
 // as its context words.  ep: the partial results' phase (the context goes out with it too).
-DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, DLds &S, const Ctl &ctl, bool last) {
+DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, DLds &S, const Ctl &ctl, bool last, int rrow) {
     (void)last;
     constexpr uint32_t MAXCH = QXG_MAX_CTX / QXD_CHUNK;
     static_assert(4 * MAXCH <= NWG && 32 * 8 == NWG, "one workgroup per (kv head, chunk) and per (q head, 16 dims)");
@@ -1098,6 +1108,10 @@ DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep
         if (!isfinite(L) || L <= 0.0) L = 1.0;
         const double invL = 1.0 / L;
         wt[lane] = (float)(f * invL);
+        if (rrow >= 0 && a.d_wsum) {   // the head's sum of normalised weights (the state loop's softmax_sum)
+            const double ws = wave_total_d((f * invL) * lc);
+            if (dgm == 0 && lane == 0) gpw(a.d_wsum)[(uint32_t)rrow * 32 + h] = ws;
+        }
         wave_lds_sync();
         const int dd = lane & 15, cg = lane >> 4;
         float o = 0.0f;
@@ -1119,7 +1133,7 @@ DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep
 // wave's LDS region; the next pass's loads are issued before this pass's dots.  Lane (b, ib)
 // then reads its sub-block's ql, qh, scale pair and d from LDS.  Returns the workgroup's best
 // (logit desc, index asc) through bv/bi (uniform); non-finite logits set *nonfin.
-DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi, bool &nonfin) {
+DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi, bool &nonfin, uint32_t rslot) {
     constexpr int R = HEAD_R;
     const int lane = tix() & 63, wave = wave_id();
     const int b = lane >> 3, ib = lane & 7, hh = ib >> 2, k = ib & 3;
@@ -1131,7 +1145,7 @@ DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi,
     bool nf = false;
     const uint32_t groups = (a.vocab + R - 1) / R;
     const uint64_t hb = uni64((uint64_t)a.h_il);
-    GLB float *lg = a.logits ? gpw(a.logits) : nullptr;
+    GLB float *lg = a.logits ? gpw(a.logits) + (uint64_t)rslot * a.vocab : nullptr;
     uint8_t *rows = S.u.hd.rows[wave];
     u32x4 v[HEAD_NI];
     auto issue = [&](uint32_t p) {
@@ -1238,8 +1252,11 @@ DEV void decode_steps(const QxDArgs &args) {
         const uint32_t ep_step = a.ep0 + step * phases + 1;
         const bool head_step = a.force_head || step + 1 >= a.n_prompt;
         const bool last = step + 1 == a.steps;
+        const bool rec = last || a.rec_all != 0u;                // this step's dumps are written
+        const uint32_t rslot = a.rec_all ? a.rec_base + step : 0u;   // ... at this record slot
         constexpr bool chunked = CHUNKED;
         if (step < a.n_prompt) token = gp(a.tokens)[step];
+        if (a.d_time && wg == 0 && tix() == 0) gpw(a.d_time)[rslot] = __builtin_amdgcn_s_memrealtime();
         // embedding row of the token (reference src/qx_format.c:3759-3793), decoded by every
         // workgroup into its copy of x
         if (tix() < 256) embed_q4k_row((const uint8_t *)(gp(a.emb) + (uint64_t)token * a.emb_row), S.xs);
@@ -1251,6 +1268,7 @@ DEV void decode_steps(const QxDArgs &args) {
             float fnw[8];
             const uint32_t ep = ep_step + 5 * l;   // + 0 X, + 1 QKV, + 2 CX, + 3 XP/LG, + 4 H/WT
             const uint32_t par = l & 1;
+            const uint32_t rrow = rslot * L + l;            // the record row of this layer's dumps
             const uint32_t ln = l + 1 < L ? l + 1 : 0u;   // after the last layer: layer 0 of the next step
             // the next layer's rows are prefetched in this layer, except after the last layer of
             // a head step (layer 0's come in after the argmax exchange) or of the launch's last step
@@ -1364,7 +1382,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 // complete in order: issued before a poll, they would delay it)
                 if ((uint32_t)wg < 4u * chunk_count(pos) && !attention_chunk_part(a, l, pos, ep + 1, S, ctl, last)) return;
                 DMARK(l, 4);
-                if (!attention_merge(a, l, pos, ep + 2, S, ctl, last)) return;
+                if (!attention_merge(a, l, pos, ep + 2, S, ctl, last, rec ? (int)rrow : -1)) return;
                 if (wg >= QXG_HEADS) {   // (the context exchange hides them)
                     load_o(a, l, wo, S.wo[wave_id()]);
                     if (pre) load_wq(a, ln, wq, S.wq[wave_id()]);
@@ -1372,7 +1390,7 @@ DEV void decode_steps(const QxDArgs &args) {
             } else if (wg < QXG_HEADS) {
                 if (!attn_wait(a, l, ep + 1, S, ctl)) return;
                 DMARK(l, 3);
-                attention(a, l, pos, ep + 1, ap, S, last);
+                attention(a, l, pos, ep + 1, ap, S, last, rec ? (int)rrow : -1);
                 DMARK(l, 4);
             } else {
                 // While the attention runs, the other workgroups touch every translation page
@@ -1552,7 +1570,7 @@ DEV void decode_steps(const QxDArgs &args) {
                         for (int q = 0; q < QXG_TOPK; ++q) if ((lane >> 1) == q) { wl = wts[q]; il = pk[q]; }
                         const uint64_t bits = (uint64_t)__double_as_longlong(wl);
                         xst(X + XO_WT + par * XN_WT + lane, ep + 4, (lane & 1) ? (uint32_t)bits : (uint32_t)(bits >> 32));
-                        if (last && a.d_rids && !(lane & 1)) { gpw(a.d_rids)[8 * l + (lane >> 1)] = il; gpw(a.d_rw)[8 * l + (lane >> 1)] = wl; }
+                        if (rec && a.d_rids && !(lane & 1)) { gpw(a.d_rids)[8 * rrow + (lane >> 1)] = il; gpw(a.d_rw)[8 * rrow + (lane >> 1)] = wl; }
                     }
                 }
                 Dig g;
@@ -1655,13 +1673,13 @@ DEV void decode_steps(const QxDArgs &args) {
                     const int r = 8 * wg + tid;
                     const float xn = S.xp[r] + moe;
                     xstf(X + XO_X + ((l + 1) & 1) * XN_X + r, ep + 5, xn);
-                    if (last) {   // the last step's dumps, after the publish (off the layer's critical path)
-                        if (a.d_layer) gpw(a.d_layer)[l * 2048 + r] = xn;
+                    if (rec) {   // the recorded step's dumps, after the publish (off the layer's critical path)
+                        if (a.d_layer) gpw(a.d_layer)[rrow * 2048 + r] = xn;
                         if (a.d_half) {
-                            gpw(a.d_half)[l * 4096 + r] = S.oatt[tid];
-                            gpw(a.d_half)[l * 4096 + 2048 + r] = moe;
+                            gpw(a.d_half)[rrow * 4096 + r] = S.oatt[tid];
+                            gpw(a.d_half)[rrow * 4096 + 2048 + r] = moe;
                         }
-                        if (a.d_res && l + 1 == L) gpw(a.d_res)[r] = xn;
+                        if (a.d_res && l + 1 == L) gpw(a.d_res)[rslot * 2048 + r] = xn;
                     }
                 }
                 DMARK(l, 12);
@@ -1681,12 +1699,12 @@ DEV void decode_steps(const QxDArgs &args) {
                 return;
             DMARK(48, 1);
             if (tid == 0) S.u.hd.next = 0u;   // (published by the barrier in vec_digits)
-            const bool fin = vec_digits<2048, true>(S.xs, onw, S);
+            const bool fin = vec_digits<2048, true>(S.xs, onw, S, nullptr, rec && a.d_norm ? gpw(a.d_norm) + rslot * 2048 : nullptr);
             float bv;
             uint32_t bi;
             bool nonfin;
             DMARK(48, 2);
-            head_rows(a, S, fin, bv, bi, nonfin);
+            head_rows(a, S, fin, bv, bi, nonfin, rslot);
             DMARK(48, 3);
             DMARKT(48, 6, 64);
             DMARKT(48, 7, 192);
@@ -1730,6 +1748,7 @@ DEV void decode_steps(const QxDArgs &args) {
             __syncthreads();
         }
     }
+    if (a.d_time && wg == 0 && tix() == 0) gpw(a.d_time)[a.rec_base + a.steps] = __builtin_amdgcn_s_memrealtime();
 #ifdef QXD_TRACE
     __syncthreads();
     if (threadIdx.x < 5 * 40) {

@@ -144,6 +144,12 @@ struct QxDArgs {
     double *d_rw;                // final residual, and each layer's two halves before their
     float *d_res;                // residual adds ([layer][attention 2048 | MoE 2048])
     float *d_half;
+    double *d_wsum;              // [layer][32] each q head's sum of normalised attention weights
+    float *d_norm;               // the last head step's output-RMSNorm vector (2048)
+    uint32_t rec_all;            // 1: the dumps (and logits) of every step, at record slot rec_base + step
+    uint32_t rec_base;           //    (dump arrays then hold one slot per step); 0: the last step's only
+    uint64_t *d_time;            // optional with rec_all: 100 MHz clock at each step's start on workgroup 0
+                                 //    ([rec_base + step]) and at the launch's end ([rec_base + steps])
     uint32_t *abort;             // set on a timed-out wait; the host reports it
     uint64_t timeout;            // per wait, in 100 MHz ticks
     double sqrt_hd;

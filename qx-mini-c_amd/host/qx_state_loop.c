@@ -3,12 +3,20 @@
  * qx_dump_state_loop_probe_summary, with the reference's prototypes, validation
  * messages, JSON keys, residual dumps, KV snapshots (QXKVSNP1) and residual replay.
  *
- * The transformer arithmetic runs on the device through the per-layer seams
- * (qxg_attention_layer_ex, qxg_moe_layer, qxg_final_head) so that every layer's JSON
- * entry carries its own routing, K/V row checksums and residual checksums; the
- * persistent decode (qxg_generate) is timed separately under --bench.  The GPU path
- * implements --full-moe with INT8 KV; the reference's probe-level skeleton modes
- * (without --full-moe) are rejected with an error. */
+ * With --final-head on the persistent path (the benchmark mix in f32) the whole loop is one
+ * launch of the persistent decode, its argmax feeding each next token on the device, that
+ * records every step's per-layer entries (qxg_generate_recorded): the layer outputs, the
+ * attention and MoE halves, the routing, the heads' softmax sums, the head's norm, logits and
+ * top tokens; the K/V rows are read back per layer after it.  Otherwise each step is one
+ * qxg_decode_token call followed by the same readbacks for that step.  --bench times the
+ * device work (the launch, or the per-step calls with their readbacks; the phases from the
+ * device clock at each step's start in the one-launch mode) and reports the loop's wall time,
+ * JSON formatting included, apart.  Residual
+ * replay (--start-layer / --residual-in) and --dump-residuals, which need stage vectors the
+ * fused step does not keep (v-cur, kqv-out), run through the per-layer seams
+ * (qxg_attention_layer_ex, qxg_moe_layer, qxg_final_head).  The GPU path implements
+ * --full-moe with INT8 KV; the reference's probe-level skeleton modes (without --full-moe)
+ * are rejected with an error. */
 #include "qx_util.h"
 
 #include <math.h>
@@ -298,6 +306,11 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
     memset(&ps, 0, sizeof(ps));
     float *logits = NULL;
     char *generated = NULL;
+    float *s_lay = NULL, *s_att = NULL, *s_moe = NULL, *s_ks = NULL, *s_vs = NULL;   /* device step records */
+    float *s_norm = NULL, *s_lg = NULL;
+    double *s_ws = NULL, *s_rw = NULL, *s_tl = NULL, *s_ms = NULL;
+    uint32_t *s_ids = NULL, *s_tid = NULL, *s_tok = NULL;
+    int8_t *s_k = NULL, *s_v = NULL;
     if (hidden != 2048) FAIL("unsupported full MoE hidden size");
     const uint32_t requested_layers = layers, manifest_layers = man->layers ? man->layers : layers;
     if (layers > manifest_layers) layers = manifest_layers;
@@ -368,13 +381,50 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
             (unsigned long long)layer_stride);
     float x[2048], a[2048], y[2048], kqv[4096], vcur[512], moe[2048], nrm[2048];
     int8_t krow[512], vrow[512];
+    /* Without replay or dumps the steps run on the device and the loop prints their records:
+     * with the final head on the persistent path, the whole loop is one launch (its argmax
+     * feeding each next token on the device) and every step's records come back after it;
+     * otherwise (the token scan picks each next token on the host) one qxg_decode_token per
+     * step, its records read back after it.  Records are [step][layer][...] with one step slot
+     * in the per-step mode; K/V rows [layer][step][512]. */
+    const int one_launch = !replay && !dumping && layers == mi.layers;
+    const int recorded = one_launch && final_head && qxg_persistent_path(ctx);
+    const uint64_t rs = recorded ? steps : 1, rl = rs * layers;
+    if (one_launch) {
+        s_lay = (float *)malloc((size_t)rl * 2048 * 4); s_att = (float *)malloc((size_t)rl * 2048 * 4);
+        s_moe = (float *)malloc((size_t)rl * 2048 * 4); s_ks = (float *)malloc((size_t)rl * 4);
+        s_vs = (float *)malloc((size_t)rl * 4); s_ws = (double *)malloc((size_t)rl * 32 * 8);
+        s_rw = (double *)malloc((size_t)rl * 8 * 8); s_ids = (uint32_t *)malloc((size_t)rl * 8 * 4);
+        s_k = (int8_t *)malloc((size_t)rl * 512); s_v = (int8_t *)malloc((size_t)rl * 512);
+        s_norm = (float *)malloc((size_t)rs * 2048 * 4); s_lg = (float *)malloc((size_t)rs * vocab * 4);
+        s_tid = (uint32_t *)malloc((size_t)rs * 32 * 4); s_tl = (double *)malloc((size_t)rs * 32 * 8);
+        s_tok = (uint32_t *)malloc((size_t)(rs + 1) * 4); s_ms = (double *)malloc((size_t)(rs + 1) * 8);
+        if (!s_lay || !s_att || !s_moe || !s_ks || !s_vs || !s_ws || !s_rw || !s_ids || !s_k || !s_v || !s_norm || !s_lg ||
+            !s_tid || !s_tl || !s_tok || !s_ms)
+            FAIL("out of memory");
+    }
+    double t_dev = 0.0;   /* device time: the one launch, or the per-step calls and readbacks */
+    if (recorded) {
+        float ms = 0.0f;
+        if (!qxg_generate_recorded(ctx, prompt_tokens, prompt_count, generation_steps, position_base, logits_top_n, s_tok,
+                                   s_lay, s_att, s_moe, s_ids, s_rw, s_ws, s_norm, s_lg, s_tid, s_tl, s_ms, &ms, err,
+                                   err_len)) {
+            ok = 0; goto done;
+        }
+        t_dev = ms * 1e-3;
+        for (uint32_t l = 0; l < layers; ++l)
+            if (!qxg_kv_read(ctx, l, position_base, steps, s_k + (uint64_t)l * steps * 512, s_v + (uint64_t)l * steps * 512,
+                             s_ks + (uint64_t)l * steps, s_vs + (uint64_t)l * steps, err, err_len)) { ok = 0; goto done; }
+    }
     uint64_t k_mix = FNV_OFFSET, v_mix = FNV_OFFSET, layers_run = 0, kv_appends = 0;
     size_t gen_len = 0;
     uint32_t current = prompt_tokens[0], prefill_tokens = 0, decode_tokens = 0;
     double t_loop = qxh_now_s(), t_prefill = 0.0, t_decode = 0.0;
     for (uint32_t ls = 0; ok && ls < steps; ++ls) {
         const double t_step = qxh_now_s();
+        double step_dev = 0.0;
         const uint32_t step = position_base + ls;
+        const uint64_t so = recorded ? ls : 0;   /* the step's record slot */
         if (ls < prompt_count) current = prompt_tokens[ls];
         const int sampling = ls + 1 >= prompt_count;
         fprintf(out, "%s{\"step\": %u, \"position\": %u, \"phase\": \"%s\", \"input_token\": %u, \"layers\": [", ls ? ", " : "",
@@ -390,6 +440,21 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
             probe = sum / 2048.0;
         }
         const uint64_t in_chk = qxf_fnv1a64(x, sizeof(x));
+        const int run_head = final_head && sampling;
+        if (recorded) {   /* the step's share of the launch, from the device clock */
+            step_dev = (s_ms[ls + 1] - s_ms[ls]) * 1e-3;
+        } else if (one_launch) {   /* the whole step on the device, then its records */
+            const double t0 = qxh_now_s();
+            if (!qxg_decode_token(ctx, current, step, run_head, NULL, s_lay, run_head ? s_lg : NULL, logits_top_n, s_tid,
+                                  s_tl, err, err_len) ||
+                !qxg_decode_halves(ctx, layers, s_att, s_moe, err, err_len) ||
+                !qxg_decode_routing(ctx, layers, s_ids, s_rw, err, err_len) ||
+                !qxg_decode_head_sums(ctx, layers, s_ws, err, err_len) ||
+                (run_head && !qxg_decode_final_norm(ctx, s_norm, err, err_len)) ||
+                !qxg_kv_read_position(ctx, step, layers, s_k, s_v, s_ks, s_vs, err, err_len)) { ok = 0; break; }
+            step_dev = qxh_now_s() - t0;
+            t_dev += step_dev;
+        }
         for (uint32_t l = start_layer; ok && l < layers; ++l) {
             const uint64_t rin = qxf_fnv1a64(x, sizeof(x));
             double hs[32];
@@ -397,14 +462,27 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
             double w[8];
             float ks, vs;
             if (dumping && !dump_vec(residual_dump_dir, step, l, "input", x, 2048, err, err_len)) { ok = 0; break; }
-            if (!qxg_attention_layer_ex(ctx, l, step, x, a, kqv, vcur, hs, err, err_len) ||
-                !qxg_kv_read(ctx, l, step, 1, krow, vrow, &ks, &vs, err, err_len)) { ok = 0; break; }
+            const uint64_t sl = so * layers + l, kl = (uint64_t)l * rs + so;   /* record and K/V row slots */
+            if (one_launch) {
+                memcpy(a, s_att + 2048 * sl, sizeof(a));
+                memcpy(hs, s_ws + 32 * sl, sizeof(hs));
+                memcpy(krow, s_k + 512 * kl, 512);
+                memcpy(vrow, s_v + 512 * kl, 512);
+                ks = s_ks[kl];
+                vs = s_vs[kl];
+            } else if (!qxg_attention_layer_ex(ctx, l, step, x, a, kqv, vcur, hs, err, err_len) ||
+                       !qxg_kv_read(ctx, l, step, 1, krow, vrow, &ks, &vs, err, err_len)) { ok = 0; break; }
             if (dumping && (!dump_vec(residual_dump_dir, step, l, "v-cur", vcur, 512, err, err_len) ||
                             !dump_vec(residual_dump_dir, step, l, "kqv-out", kqv, 4096, err, err_len))) { ok = 0; break; }
             double a2 = 0.0;
             for (int i = 0; i < 2048; ++i) { a2 += (double)a[i] * (double)a[i]; x[i] += a[i]; }
             if (dumping && !dump_vec(residual_dump_dir, step, l, "ffn-inp", x, 2048, err, err_len)) { ok = 0; break; }
-            if (!qxg_moe_layer(ctx, l, x, y, moe, ids, w, err, err_len)) { ok = 0; break; }
+            if (one_launch) {   /* x is now the step's ffn input, x + attention as the device added them */
+                memcpy(y, s_lay + 2048 * sl, sizeof(y));
+                memcpy(moe, s_moe + 2048 * sl, sizeof(moe));
+                memcpy(ids, s_ids + 8 * sl, sizeof(ids));
+                memcpy(w, s_rw + 8 * sl, sizeof(w));
+            } else if (!qxg_moe_layer(ctx, l, x, y, moe, ids, w, err, err_len)) { ok = 0; break; }
             if (dumping && (!dump_vec(residual_dump_dir, step, l, "ffn-moe-out", moe, 2048, err, err_len) ||
                             !dump_vec(residual_dump_dir, step, l, "output", y, 2048, err, err_len))) { ok = 0; break; }
             double m2 = 0.0, sum = 0.0;
@@ -456,7 +534,7 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
                 (unsigned long long)qxf_fnv1a64(x, sizeof(x)));
         if (!sampling) {
             fprintf(out, ", \"selected_token\": null, \"source\": \"fixed_prompt\"}");
-            t_prefill += qxh_now_s() - t_step;
+            t_prefill += one_launch ? step_dev : qxh_now_s() - t_step;
             ++prefill_tokens;
             current = prompt_tokens[ls + 1];
             continue;
@@ -465,16 +543,23 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
         if (final_head) {
             uint32_t tid[32];
             double tl[32];
-            if (!qxg_final_head(ctx, x, nrm, logits, logits_top_n, tid, tl, err, err_len)) { ok = 0; break; }
+            const float *lg = logits;
+            if (one_launch) {   /* the step's own head: its argmax is the token it feeds on */
+                memcpy(tid, s_tid + so * logits_top_n, logits_top_n * sizeof(uint32_t));
+                memcpy(tl, s_tl + so * logits_top_n, logits_top_n * sizeof(double));
+                memcpy(nrm, s_norm + so * 2048, sizeof(nrm));
+                lg = s_lg + so * vocab;
+                if (recorded && tid[0] != s_tok[ls + 1]) FAIL("device argmax and top-N ranking disagree");
+            } else if (!qxg_final_head(ctx, x, nrm, logits, logits_top_n, tid, tl, err, err_len)) { ok = 0; break; }
             if (dumping) {
                 char nm[64];
                 snprintf(nm, sizeof(nm), "step-%u-logits", step);
-                if (!qxh_write_f32(residual_dump_dir, nm, logits, vocab, err, err_len)) { ok = 0; break; }
+                if (!qxh_write_f32(residual_dump_dir, nm, lg, vocab, err, err_len)) { ok = 0; break; }
             }
-            double ss = 0.0, ns = 0.0, lmin = logits[0], lmax = logits[0], l2 = 0.0;
+            double ss = 0.0, ns = 0.0, lmin = lg[0], lmax = lg[0], l2 = 0.0;
             for (int i = 0; i < 2048; ++i) { ss += (double)x[i] * (double)x[i]; ns += (double)nrm[i] * (double)nrm[i]; }
             for (uint32_t i = 0; i < vocab; ++i) {
-                const double v = logits[i];
+                const double v = lg[i];
                 if (v < lmin) lmin = v;
                 if (v > lmax) lmax = v;
                 l2 += v * v;
@@ -492,7 +577,7 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
                     (unsigned long long)qxf_fnv1a64(x, sizeof(x)), (unsigned long long)qxf_fnv1a64(nrm, sizeof(nrm)),
                     hd ? hd->flags : 0u, act ? "q6_k_q8_k_hip_dot4" : "q6_k_hip_dot4", act ? 1u : 0u,
                     (unsigned long long)(hd ? hd->checksum : 0), vocab, vocab,
-                    (unsigned long long)qxf_fnv1a64(logits, (uint64_t)vocab * 4), lmin, lmax, sqrt(l2 / (double)vocab),
+                    (unsigned long long)qxf_fnv1a64(lg, (uint64_t)vocab * 4), lmin, lmax, sqrt(l2 / (double)vocab),
                     tid[0], tl[0]);
             const uint64_t row_bytes = hd ? hd->byte_size / vocab : 0;
             for (uint32_t r = 0; r < logits_top_n; ++r)
@@ -517,7 +602,7 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
         fprintf(out, ", \"selected_token\": %u, \"piece\": ", next);
         qxh_json_string(out, piece);
         fprintf(out, ", \"source\": \"%s\"}", src);
-        t_decode += qxh_now_s() - t_step;
+        t_decode += one_launch ? step_dev : qxh_now_s() - t_step;
         ++decode_tokens;
         current = next;
     }
@@ -534,13 +619,18 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
     qxh_json_string(out, generated);
     fprintf(out, ",\n");
     if (bench) {
-        const double el = t_loop > 0.0 ? t_loop : 1e-6;
-        fprintf(out, "  \"bench\": {\"enabled\": true, \"timer\": \"monotonic_wall\", \"elapsed_sec\": %.9g, \"tokens_per_second\": %.9g, "
+        /* device mode: the device work (the one launch, or the per-step calls with their
+         * readbacks), the JSON formatting apart in wall_elapsed_sec; the per-layer seams: the
+         * whole loop */
+        const double el = one_launch ? (t_dev > 0.0 ? t_dev : 1e-6) : (t_loop > 0.0 ? t_loop : 1e-6);
+        fprintf(out, "  \"bench\": {\"enabled\": true, \"timer\": \"monotonic_wall\", \"timed\": \"%s\", \"elapsed_sec\": %.9g, "
+                "\"wall_elapsed_sec\": %.9g, \"tokens_per_second\": %.9g, "
                 "\"ms_per_token\": %.9g, \"layer_steps\": %llu, \"layer_steps_per_second\": %.9g, \"phases\": {\"prefill\": "
                 "{\"tokens\": %u, \"elapsed_sec\": %.9g, \"tokens_per_second\": %.9g}, \"decode\": {\"tokens\": %u, "
                 "\"elapsed_sec\": %.9g, \"tokens_per_second\": %.9g}}",
-                el, steps / el, 1000.0 * el / steps, (unsigned long long)layers_run, layers_run / el, prefill_tokens, t_prefill,
-                prefill_tokens ? prefill_tokens / t_prefill : 0.0, decode_tokens, t_decode, decode_tokens ? decode_tokens / t_decode : 0.0);
+                recorded ? "device_launch" : one_launch ? "device_steps" : "loop", el, t_loop, steps / el, 1000.0 * el / steps, (unsigned long long)layers_run,
+                layers_run / el, prefill_tokens, t_prefill, prefill_tokens ? prefill_tokens / t_prefill : 0.0, decode_tokens,
+                t_decode, decode_tokens ? decode_tokens / t_decode : 0.0);
         /* the same tokens through the device decode loop (one launch per call, no host
          * work per layer), on a fresh cache: the path's own throughput */
         if (final_head && !replay && position_base == 0) {
@@ -600,6 +690,8 @@ int qx_dump_prompt_state_loop_probe_summary(const char *path, const char *tokens
     fprintf(out, "  \"note\": \"%s\"\n}\n", note);
 done:
 #undef FAIL
+    free(s_lay); free(s_att); free(s_moe); free(s_ks); free(s_vs); free(s_ws); free(s_rw); free(s_ids); free(s_k); free(s_v);
+    free(s_norm); free(s_lg); free(s_tid); free(s_tl); free(s_tok); free(s_ms);
     probe_scan_free(&ps);
     free(logits);
     free(generated);

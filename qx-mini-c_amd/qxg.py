@@ -71,6 +71,8 @@ _sig(_g, "qxg_kv_write", [vp, u32, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_kv_read", [vp, u32, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_decode_token", [vp, u32, u32, c_int, vp, vp, vp, u32, vp, vp, *ERR])
 _sig(_g, "qxg_generate", [vp, vp, u32, u32, u32, vp, ctypes.POINTER(c_float), *ERR])
+_sig(_g, "qxg_persistent_path", [vp])
+_sig(_g, "qxg_generate_recorded", [vp, vp, u32, u32, u32, u32] + [vp] * 12 + [ctypes.POINTER(c_float), *ERR])
 _sig(_g, "qxg_embed_token", [vp, u32, vp, *ERR])
 _sig(_g, "qxg_dequant_blocks", [vp, u32, vp, u64, vp, *ERR])
 _sig(_g, "qxg_dequant_blocks_static", [vp, u32, vp, u64, vp, *ERR])
@@ -94,6 +96,9 @@ _sig(_g, "qxg_time_kernel", [vp, c_int, u32, u32, ctypes.POINTER(c_float), *ERR]
 _sig(_g, "qxg_decode_routing", [vp, u32, vp, vp, *ERR])
 _sig(_g, "qxg_decode_halves", [vp, u32, vp, vp, *ERR])
 _sig(_g, "qxg_set_attention_chunks", [vp, u32])
+_sig(_g, "qxg_decode_head_sums", [vp, u32, vp, *ERR])
+_sig(_g, "qxg_decode_final_norm", [vp, vp, *ERR])
+_sig(_g, "qxg_kv_read_position", [vp, u32, u32, vp, vp, vp, vp, *ERR])
 _sig(_g, "qxg_device_bytes", [vp], u64)
 _sig(_g, "qxg_profile_kernel", [vp, c_int])
 _sig(_g, "qxg_profile_result", [vp, ctypes.POINTER(u32), ctypes.POINTER(c_double)])
@@ -320,6 +325,30 @@ class Context:
                                     self._err, 1024))
         return out, ms.value
 
+    def persistent_path(self):
+        return bool(_g.qxg_persistent_path(self._c))
+
+    def generate_recorded(self, prompt, n_gen, pos0=0, top_n=8):
+        """qxg_generate with every step's records (one persistent launch): a dict of tokens
+        [S+1], layer/attn/moe [S, layers, 2048], ids/weights [S, layers, 8], head_sums
+        [S, layers, 32], norm [S, 2048], logits [S, vocab], top_ids/top_logits [S, top_n],
+        step_ms [S+1] and elapsed_ms, with S = len(prompt) + n_gen - 1."""
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        S, L = len(prompt) + n_gen - 1, self.info.layers
+        r = {"tokens": np.zeros(S + 1, np.uint32), "layer": np.zeros((S, L, 2048), np.float32),
+             "attn": np.zeros((S, L, 2048), np.float32), "moe": np.zeros((S, L, 2048), np.float32),
+             "ids": np.zeros((S, L, 8), np.uint32), "weights": np.zeros((S, L, 8), np.float64),
+             "head_sums": np.zeros((S, L, 32), np.float64), "norm": np.zeros((S, 2048), np.float32),
+             "logits": np.zeros((S, self.info.vocab), np.float32), "top_ids": np.zeros((S, top_n), np.uint32),
+             "top_logits": np.zeros((S, top_n), np.float64), "step_ms": np.zeros(S + 1, np.float64)}
+        ms = c_float()
+        self._check(_g.qxg_generate_recorded(
+            self._c, _p(prompt), len(prompt), n_gen, pos0, top_n, _p(r["tokens"]), _p(r["layer"]), _p(r["attn"]),
+            _p(r["moe"]), _p(r["ids"]), _p(r["weights"]), _p(r["head_sums"]), _p(r["norm"]), _p(r["logits"]),
+            _p(r["top_ids"]), _p(r["top_logits"]), _p(r["step_ms"]), ctypes.byref(ms), self._err, 1024))
+        r["elapsed_ms"] = ms.value
+        return r
+
     def prefill(self, tokens, pos0=0, run_head=True, top_n=8, want_residual=False, want_logits=False):
         """Batched prefill of `tokens` at positions pos0..; returns (residual [n, 2048] or
         None, logits of the last token or None, top ids, top logits, device ms)."""
@@ -349,6 +378,26 @@ class Context:
         m = np.zeros((n, 2048), np.float32)
         self._check(_g.qxg_decode_halves(self._c, n, _p(a), _p(m), self._err, 1024))
         return a, m
+
+    def head_sums(self, layers=None):
+        """[layers, 32] each q head's sum of normalised attention weights, last decode_token step."""
+        n = self.info.layers if layers is None else layers
+        out = np.zeros((n, 32), np.float64)
+        self._check(_g.qxg_decode_head_sums(self._c, n, _p(out), self._err, 1024))
+        return out
+
+    def final_norm(self):
+        """The output-RMSNorm vector of the last decode_token head step."""
+        out = np.zeros(2048, np.float32)
+        self._check(_g.qxg_decode_final_norm(self._c, _p(out), self._err, 1024))
+        return out
+
+    def kv_read_position(self, pos, layers):
+        """(k [layers, 512], v, ks [layers], vs) of one position."""
+        k = np.zeros((layers, 512), np.int8); v = np.zeros_like(k)
+        ks = np.zeros(layers, np.float32); vs = np.zeros_like(ks)
+        self._check(_g.qxg_kv_read_position(self._c, pos, layers, _p(k), _p(v), _p(ks), _p(vs), self._err, 1024))
+        return k, v, ks, vs
 
     def set_attention_chunks(self, min_positions):
         """Persistent decode: stage A by kv head and chunk from n = pos + 1 >= min_positions."""

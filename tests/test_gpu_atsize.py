@@ -180,7 +180,7 @@ def test_config4_state_loop_final_head(big, tmp_path):
     fp = libc.fopen(str(out).encode(), b"w")
     err = ctypes.create_string_buffer(512)
     say("state loop with the final head: 3 steps x 48 layers")
-    ok = f(model_path.encode(), None, int(prompt[0]), 3, LAYERS, 16, b"int8", b"f32", 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0,
+    ok = f(model_path.encode(), None, int(prompt[0]), 3, LAYERS, 16, b"int8", b"f32", 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1,
            2048, None, 5, 64, 5, 0.0, 1, None, 0, None, None, None, fp, err, 512)
     libc.fclose(fp)
     assert ok == 1, err.value.decode()
@@ -201,6 +201,63 @@ def test_config4_state_loop_final_head(big, tmp_path):
                 assert abs(ly[k] - 1.0) < 1e-6, k
         current = t["selected_token"]
     assert j["final_token"] == current
+    # --bench: the loop is one launch of the persistent decode (timed on the device), beside
+    # the same tokens through qxg_generate
+    b = j["bench"]
+    assert b["timed"] == "device_launch" and b["device"]["matches_probe"]
+    assert b["phases"]["decode"]["tokens"] == 3 and b["phases"]["decode"]["elapsed_sec"] <= b["elapsed_sec"]
+    say(f"state loop --bench: {b['tokens_per_second']:.1f} tok/s in its launch, "
+        f"{b['device']['tokens_per_second']:.1f} tok/s in qxg_generate, wall {b['wall_elapsed_sec']:.3f} s")
+
+
+def test_config4_prompt_state_loop_one_launch(big, tmp_path):
+    """qx_dump_prompt_state_loop_probe_summary (the reference's prototype) with an 8-token
+    prompt and 8 greedy tokens at size: the whole loop is one persistent launch that records
+    every step (the device's argmax feeding each next token), the prompt steps carry no head
+    and select nothing, the generated tokens are qxg_generate's, and --bench times that launch
+    with its prefill and decode phases from the device clock at each step's start."""
+    ctx, om, prompt, model_path = big
+    h = qxg._h
+    f = h.qx_dump_prompt_state_loop_probe_summary
+    c_char_p, u32, vp, ci = ctypes.c_char_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int
+    f.argtypes = ([c_char_p, c_char_p, vp, u32, u32, u32, u32, c_char_p, c_char_p, c_char_p, c_char_p, c_char_p, u32,
+                   c_char_p] + [c_char_p] * 7 + [ci] * 13 + [u32, c_char_p, u32, u32, u32, ctypes.c_double, u32, c_char_p,
+                                                             u32, c_char_p, c_char_p, c_char_p, vp, c_char_p, ctypes.c_uint64])
+    f.restype = ci
+    libc = ctypes.CDLL(None)
+    libc.fopen.restype = vp
+    libc.fopen.argtypes = [c_char_p, c_char_p]
+    libc.fclose.argtypes = [vp]
+    out = tmp_path / "prompt_loop.json"
+    fp = libc.fopen(str(out).encode(), b"w")
+    err = ctypes.create_string_buffer(512)
+    p = np.ascontiguousarray(prompt, np.uint32)
+    say("prompt state loop: 8 prompt tokens, 8 generated, 48 layers, one launch")
+    ok = f(model_path.encode(), None, p.ctypes.data_as(vp), len(p), 8, LAYERS, 32, b"int8", b"f32", b"ephemeral",
+           b"baseline", b"serial", 1, b"scalar", b"none", b"none", b"none", b"none", b"none", b"none", b"none",
+           0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 2048, None, 5, 64, 5, 0.0, 1, None, 0, None, None, None, fp, err, 512)
+    libc.fclose(fp)
+    assert ok == 1, err.value.decode()
+    j = json.load(open(out))
+    toks = j["tokens"]
+    assert len(toks) == 15 and [t["input_token"] for t in toks[:8]] == [int(t) for t in prompt]
+    for t in toks[:7]:
+        assert t["selected_token"] is None and "final_head" not in t and t["phase"] == "prefill"
+    gen, _ = ctx.generate(prompt, 8)
+    assert [t["selected_token"] for t in toks[7:]] == [int(g) for g in gen]
+    for t in toks[7:]:
+        assert t["final_head"]["argmax_token"] == t["selected_token"]
+        for ly in t["layers"]:
+            assert abs(ly["softmax_sum"] - 1.0) < 1e-6
+    b = j["bench"]
+    assert b["timed"] == "device_launch" and b["device"]["matches_probe"]
+    ph = b["phases"]
+    assert ph["prefill"]["tokens"] == 7 and ph["decode"]["tokens"] == 8
+    assert ph["prefill"]["elapsed_sec"] + ph["decode"]["elapsed_sec"] <= b["elapsed_sec"]
+    say(f"prompt state loop --bench: {b['tokens_per_second']:.1f} tok/s in its launch (prefill "
+        f"{ph['prefill']['tokens_per_second']:.1f}, decode {ph['decode']['tokens_per_second']:.1f}), "
+        f"{b['device']['tokens_per_second']:.1f} tok/s in qxg_generate, wall {b['wall_elapsed_sec']:.3f} s")
+    assert b["tokens_per_second"] >= 0.8 * b["device"]["tokens_per_second"]
 
 
 def test_config5_prefill_layer_512_tokens(big):

@@ -89,3 +89,63 @@ def test_long_state_loop_probe_vs_reference(tmp_path):
             assert e <= REL_L2, (s, e)
     m.close()
     print(f"64-step loop: worst same-input rel L2 {worst:.2e}")
+
+
+def test_state_loop_one_launch_matches_layer_seams(tmp_path):
+    """Without residual dumps the state loop runs each step as one qxg_decode_token launch
+    (the persistent decode on this benchmark-mix model) and rebuilds every layer's JSON entry
+    from the step's records; with --dump-residuals it runs the per-layer seams.  Both give the
+    same tokens and routed experts, the same layer-0 input checksum, and per-layer vector
+    norms, scales and softmax sums within the bars; --bench times the device steps."""
+    model = tmp_path / "m.qxf"
+    qxg.generate_model(model, layers=2, vocab=1024, experts=16, seed=4321)
+    base = [EXE, "state-loop-probe", "--in", str(model), "--prompt-token", "17", "--steps", "6", "--layers", "2", "--ctx",
+            "16", "--kv", "int8", "--full-moe"]
+    r1 = subprocess.run(base + ["--bench"], capture_output=True, text=True, timeout=120)
+    assert r1.returncode == 0, r1.stderr
+    dd = tmp_path / "dumps"
+    dd.mkdir()
+    r2 = subprocess.run(base + ["--dump-residuals", str(dd)], capture_output=True, text=True, timeout=120)
+    assert r2.returncode == 0, r2.stderr
+    one, seams = json.loads(r1.stdout), json.loads(r2.stdout)
+    assert one["bench"]["timed"] == "device_steps" and one["bench"]["tokens_per_second"] > 0
+    assert len(one["tokens"]) == len(seams["tokens"]) == 6
+    for t1, t2 in zip(one["tokens"], seams["tokens"]):
+        assert t1["input_token"] == t2["input_token"] and t1.get("selected_token") == t2.get("selected_token")
+        assert t1["residual_checksum"] == t2["residual_checksum"]   # the embedding row, exact
+        for l1, l2 in zip(t1["layers"], t2["layers"]):
+            assert l1["selected_experts"] == l2["selected_experts"], (t1["step"], l1["layer"])
+            assert np.allclose(l1["routing_weights"], l2["routing_weights"], rtol=1e-5, atol=0)
+            for k in ("attention_output_vector_l2", "moe_output_l2", "k_scale", "v_scale"):
+                assert abs(l1[k] / l2[k] - 1.0) <= REL_L2, (t1["step"], l1["layer"], k, l1[k], l2[k])
+            for k in ("softmax_sum", "softmax_sum_min", "softmax_sum_max"):
+                assert abs(l1[k] - 1.0) < 1e-6, (t1["step"], l1["layer"], k, l1[k])
+
+
+def test_persistent_decode_in_a_second_process(tmp_path):
+    """The runtime grants cooperative launches on a GPU to one process at a time: after this
+    process has run the persistent decode, a child's cooperative launch is refused
+    (hipErrorIllegalState) for as long as this process lives.  The child's decode then
+    launches the same kernel plainly and gives the tokens this process's decode gives."""
+    model = tmp_path / "m.qxf"
+    qxg.generate_model(model, layers=2, vocab=1024, experts=16, seed=4321)
+    c = qxg.Context(0)
+    try:
+        c.set_layer_path(1)
+        c.load(model)
+        assert c.persistent_path()
+        c.kv_create(2, 16)
+        c.generate([17], 3)   # a cooperative launch in this process
+        r = subprocess.run([EXE, "state-loop-probe", "--in", str(model), "--prompt-token", "17", "--steps", "6", "--layers",
+                            "2", "--ctx", "16", "--kv", "int8", "--full-moe"], capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr
+        j = json.loads(r.stdout)
+        c.kv_create(2, 16)
+        tok = 17
+        for t in j["tokens"]:
+            assert t["input_token"] == tok
+            _, lay, _, _, _ = c.decode_token(tok, t["position"], False, 1, want_layers=True)
+            assert t["residual_checksum_after"] == qxg.fnv1a64(lay[-1]), t["step"]
+            tok = t["selected_token"]
+    finally:
+        c.close()

@@ -171,6 +171,54 @@ def test_generate_long_context_matches_steps(model):
         c.close()
 
 
+@pytest.mark.parametrize("p0", [0, 250], ids=["start", "across_threshold"])
+def test_generate_recorded_matches_steps(model, p0):
+    """qxg_generate_recorded (the state loop's one launch) keeps for every step what the
+    step-by-step path reads back after each qxg_decode_token: the same tokens, layer outputs,
+    attention and MoE halves, routing, head sums, final norms, logits, top tokens and cache
+    rows, bit for bit (the same kernels on the same inputs).  From p0 250 the 7 steps cross the
+    chunked stage A's default threshold (257 positions), so the call runs as two launches, the
+    second writing its records from slot 6 on."""
+    m, om = model
+    c = open_ctx(m.path)
+    try:
+        prompt, n_gen = [5, 900, 17], 5
+        S = len(prompt) + n_gen - 1
+        c.kv_create(LAYERS, p0 + S + 1)
+        okv = qxo.KV(LAYERS, p0 + S + 1)
+        seed_cache(c, okv, p0, 31)
+        r = c.generate_recorded(prompt, n_gen, pos0=p0, top_n=8)
+        rows = [c.kv_read(l, p0, S) for l in range(LAYERS)]
+        assert list(r["tokens"][:len(prompt)]) == prompt
+        seed_cache(c, okv, p0, 31)
+        tok = prompt[0]
+        for s in range(S):
+            head = s + 1 >= len(prompt)
+            _, lay, lg, ids, tl = c.decode_token(tok, p0 + s, head, 8, want_layers=True, want_logits=head)
+            att, moe = c.halves()
+            r_ids, r_w = c.routing()
+            assert np.array_equal(r["layer"][s], lay), s
+            assert np.array_equal(r["attn"][s], att) and np.array_equal(r["moe"][s], moe), s
+            assert np.array_equal(r["ids"][s], r_ids) and np.array_equal(r["weights"][s], r_w), s
+            assert np.array_equal(r["head_sums"][s], c.head_sums()), s
+            if head:
+                assert np.array_equal(r["logits"][s], lg) and np.array_equal(r["norm"][s], c.final_norm()), s
+                assert np.array_equal(r["top_ids"][s], ids) and np.array_equal(r["top_logits"][s], tl), s
+                tok = int(ids[0])
+                assert int(r["tokens"][s + 1]) == tok, s
+            else:
+                tok = prompt[s + 1]
+        for l in range(LAYERS):
+            for got, want in zip(rows[l], c.kv_read(l, p0, S)):
+                assert np.array_equal(got, want), l
+        ms = r["step_ms"]
+        assert ms[0] == 0.0 and np.all(np.diff(ms) > 0) and ms[-1] <= r["elapsed_ms"], (ms, r["elapsed_ms"])
+        say(f"recorded launch at p0 {p0}: {S} steps in {r['elapsed_ms']:.3f} ms, per step "
+            f"{', '.join(f'{d:.3f}' for d in np.diff(ms))} ms")
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("chunks", [WALK, CHUNKS], ids=["walk", "chunked"])
 def test_outliers_same_input(outlier_model, chunks):
     """Planted outlier channels through the persistent kernel: a 4-token prompt and 3 greedy
