@@ -867,11 +867,12 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
 
 // ---------------------------------------------------------------- attention by chunk (stage A, long context)
 // The same attention (reference src/qx_format.c:5051-5196) spread over every workgroup once
-// the cache is long: with n = pos + 1 positions in QXD_CHUNK-position chunks (nch of them),
-// workgroup w < 4 nch takes kv head g = w % 4 and chunk c = w / 4 for all eight q heads that
-// share g (wave v: q head 8 g + v), so each chunk's K and V rows are read once, into LDS in
-// stage Q (dma_chunk), for eight heads.  A wave scores the chunk's 64 positions (a quad per
-// position, four rounds of 16), takes one maximum and one exponential per lane, and sums the
+// the cache is long: with n = pos + 1 positions in chunks of cs = 32 positions (n <= 2048) or
+// 64 (nch <= 64 chunks either way), workgroup w < 4 nch takes kv head g = w % 4 and chunk
+// c = w / 4 for all eight q heads that share g (wave v: q head 8 g + v), so each chunk's K and V
+// rows are read once, into LDS in stage Q (dma_chunk), for eight heads.  A wave scores the
+// chunk's positions (a quad per position, rounds of 16), takes one maximum and one
+// exponential per lane, and sums the
 // weighted V codes (lane: 4 dimensions, odd or even positions).  Its partial result - the
 // chunk's maximum score m_c, its sum of exp(s - m_c) and the f32 context sums - is published
 // as 8 records of 16 dimensions.  Then workgroup w merges q head w / 8, dimensions
@@ -884,25 +885,32 @@ DEV uint32_t pack_codes4(const float *v, float sc) {
            ((uint32_t)(uint8_t)int8_code(v[2], sc) << 16) | ((uint32_t)(uint8_t)int8_code(v[3], sc) << 24);
 }
 DEV double dbl_words(uint32_t hi, uint32_t lo) { return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo)); }
-DEV uint32_t chunk_count(uint32_t pos) { return (pos + QXD_CHUNK) / QXD_CHUNK; }   // ceil((pos + 1) / QXD_CHUNK)
+// positions per chunk: QXD_CHUNK_S up to QXD_CHUNK_S_MAXN cached positions, QXD_CHUNK beyond
+// (at most QXG_MAX_CTX / QXD_CHUNK = 64 chunks either way)
+DEV uint32_t chunk_size(uint32_t pos) { return pos + 1 <= QXD_CHUNK_S_MAXN ? QXD_CHUNK_S : QXD_CHUNK; }
+DEV uint32_t chunk_count(uint32_t pos) { const uint32_t cs = chunk_size(pos); return (pos + cs) / cs; }   // ceil((pos + 1) / cs)
 DEV ChunkRows &chunk_rows(DLds &S) {
     static_assert(sizeof(ChunkRows) <= sizeof(S.u.m.dn), "a chunk's rows fit the down-row area");
     static_assert(sizeof(AttnK) <= offsetof(decltype(S.u.m), dn), "the chunk workgroup's scratch stays clear of its rows");
     return *reinterpret_cast<ChunkRows *>(&S.u.m.dn[0][0]);
 }
 
-// Stage Q of a chunk workgroup (w < 4 nch): its chunk's cached rows (positions c0 .. c0 + 63,
-// clamped below pos) and scales to LDS; wave v copies rows 8 v .. 8 v + 7 of K and of V.
+// Stage Q of a chunk workgroup (w < 4 nch): its chunk's cached rows (positions c0 .. c0 + cs - 1,
+// clamped below pos) and scales to LDS; wave v copies rows rpw v .. rpw v + rpw - 1 of K and of
+// V (rpw = cs / 8 rows, 8 lanes a row; the other lanes idle).
 DEV void dma_chunk(const QxDArgs &a, uint32_t l, uint32_t pos, DLds &S) {
     const int lane = tix() & 63, w = wave_id();
-    const uint32_t g = blockIdx.x & 3u, c0 = (blockIdx.x >> 2) * QXD_CHUNK;
+    const uint32_t cs = chunk_size(pos), rpw = cs / 8u;
+    const uint32_t g = blockIdx.x & 3u, c0 = (blockIdx.x >> 2) * cs;
     const uint32_t lastc = pos > 0 ? pos - 1 : 0u, base = l * a.ctx;
     ChunkRows &C = chunk_rows(S);
-    const uint32_t t = min(c0 + 8u * w + (uint32_t)(lane >> 3), lastc);
-    const uint32_t off = (base + t) * 512 + 128 * g + 16 * (lane & 7);   // layers * ctx * 512 < 2^32
-    dma16_kv(gp(reinterpret_cast<const uint8_t *>(a.kc)), off, C.k[8 * w]);
-    dma16_kv(gp(reinterpret_cast<const uint8_t *>(a.vc)), off, C.v[8 * w]);
-    if (w < 2) {
+    if ((uint32_t)(lane >> 3) < rpw) {
+        const uint32_t t = min(c0 + rpw * w + (uint32_t)(lane >> 3), lastc);
+        const uint32_t off = (base + t) * 512 + 128 * g + 16 * (lane & 7);   // layers * ctx * 512 < 2^32
+        dma16_kv(gp(reinterpret_cast<const uint8_t *>(a.kc)), off, C.k[rpw * w]);
+        dma16_kv(gp(reinterpret_cast<const uint8_t *>(a.vc)), off, C.v[rpw * w]);
+    }
+    if (w < 2 && (uint32_t)lane < cs) {
         const uint32_t ts = min(c0 + (uint32_t)lane, lastc);
         dma4_kv(gp(reinterpret_cast<const uint8_t *>(w == 0 ? a.ks : a.vs)), (base + ts) * 4, w == 0 ? C.ks : C.vs);
     }
@@ -914,11 +922,11 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
     (void)last;
     constexpr uint32_t MAXCH = QXG_MAX_CTX / QXD_CHUNK;
     GLB uint64_t *const X = gpw(a.xch);
-    const uint32_t n = pos + 1, nch = chunk_count(pos), par = l & 1;
+    const uint32_t n = pos + 1, nch = chunk_count(pos), csz = chunk_size(pos), par = l & 1;
     AttnK &A = S.u.atk;
     ChunkRows &C = chunk_rows(S);
     const int g = blockIdx.x & 3;
-    const uint32_t ch = blockIdx.x >> 2, c0 = ch * QXD_CHUNK;
+    const uint32_t ch = blockIdx.x >> 2, c0 = ch * csz;
     const bool own = ch + 1 == nch;   // the chunk holding the position (workgroup-uniform)
     const int tid = tix(), lane = tid & 63, w = wave_id();
     const double cs = gp(a.T.rope_cs)[pos * 128 + lane], sn = gp(a.T.rope_cs)[pos * 128 + 64 + lane];
@@ -1023,7 +1031,7 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
         sq += dppd<DPP_XOR2>(sq);
         double v = qok ? sq * (double)ksc * inv_sqrt_hd : 0.0;
         if (!isfinite(v)) v = 0.0;
-        sc[i] = t < n ? v : -INFINITY;
+        sc[i] = u < csz && t < n ? v : -INFINITY;   // (rows past a 32-position chunk are stale LDS)
     }
     const double m = wave_max_d(fmax(fmax(sc[0], sc[1]), fmax(sc[2], sc[3])));
     // one exponential per lane: lane (jq, q4) weighs position c0 + 16 q4 + jq
@@ -1032,7 +1040,7 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
     if (q4 == 2) ss = sc[2];
     if (q4 == 3) ss = sc[3];
     const uint32_t u = 16u * q4 + (uint32_t)jq;
-    const bool uvalid = c0 + u < n;
+    const bool uvalid = u < csz && c0 + u < n;
     const float vsel = C.vs[u];
     const double e = uvalid ? exp(ss - m) : 0.0;
     const double lsum = wave_total_d(e);
@@ -1046,7 +1054,7 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
 #pragma unroll
     for (int b = 0; b < 8; ++b) acc[b] = 0.0f;
 #pragma unroll 4
-    for (int j = 0; j < (int)QXD_CHUNK / 4; ++j) {
+    for (int j = 0; j < (int)(csz / 4u); ++j) {
         const uint32_t uu = 4u * j + (uint32_t)p4;
         const float pv = A.p[w][uu];
         const uint2 x = *reinterpret_cast<const uint2 *>(C.v[uu] + 8 * dg);

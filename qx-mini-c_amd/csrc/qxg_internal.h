@@ -187,6 +187,8 @@ struct QxDArgs {
 // {context sums 16, running maximum (hi, lo), denominator (hi, lo)} at
 // [head][dimension group][chunk].
 #define QXD_CHUNK 64u
+#define QXD_CHUNK_S 32u          // ... of QXD_CHUNK_S positions while the cache has at most
+#define QXD_CHUNK_S_MAXN 2048u   //     QXD_CHUNK_S_MAXN (more workgroups, each with less to do)
 #define QXD_PREC 20u
 #define QXD_PART_WORDS (32u * 8u * (QXG_MAX_CTX / QXD_CHUNK) * QXD_PREC)
 // Default positions (n = pos + 1) from which the persistent decode attends by chunk: below

@@ -108,10 +108,12 @@ def seed_cache(ctx, okv, p0, seed):
         okv.k[layer, :p0], okv.v[layer, :p0], okv.ks[layer, :p0], okv.vs[layer, :p0] = k, v, ks, vs
 
 
-@pytest.mark.parametrize("p0", [0, 1, 63, 64, 65, 127, 300, 1000])
+@pytest.mark.parametrize("p0", [0, 1, 31, 32, 33, 63, 64, 65, 127, 300, 1000])
 def test_chunked_short_positions(model, p0):
     """The chunked stage A at every chunk count boundary it can meet (one chunk, the
-    position alone in its chunk, a full last chunk) forced at short positions."""
+    position alone in its chunk, a full last chunk; chunks of 32 positions up to 2048
+    cached positions, of 64 beyond: the switch is met at 2047/2048 below) forced at short
+    positions."""
     m, om = model
     c = open_ctx(m.path, CHUNKS)
     try:
