@@ -1042,7 +1042,9 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
     const uint32_t u = 16u * q4 + (uint32_t)jq;
     const bool uvalid = u < csz && c0 + u < n;
     const float vsel = C.vs[u];
-    const double e = uvalid ? exp(ss - m) : 0.0;
+    // the exponentials of the chunked path in f32 (arguments <= 0, relative error ~1e-7: far
+    // inside the 1e-5 bar; a double exp is a long dependent chain)
+    const double e = uvalid ? (double)expf((float)(ss - m)) : 0.0;
     const double lsum = wave_total_d(e);
     A.p[w][u] = uvalid ? (float)(e * (double)vsel) : 0.0f;   // (a clamped row's scale may be unset)
     wave_lds_sync();
@@ -1111,7 +1113,7 @@ DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep
             lc = dbl_words(rw[QXD_PREC * lane + 18], rw[QXD_PREC * lane + 19]);
         }
         const double M = wave_max_d(mc);
-        const double f = mc == -INFINITY ? 0.0 : exp(mc - M);
+        const double f = mc == -INFINITY ? 0.0 : (double)expf((float)(mc - M));
         double L = wave_total_d(f * lc);
         if (!isfinite(L) || L <= 0.0) L = 1.0;
         const double invL = 1.0 / L;
@@ -1607,9 +1609,10 @@ DEV void decode_steps(const QxDArgs &args) {
                     gv = isfinite(gv) ? gv : 0.0f;
                     uv = isfinite(uv) ? uv : 0.0f;
                     if (lane < (wave < 4 ? 4 : 2)) {
-                        // reference src/qx_format.c:5298, 2511-2513: h = (float)(silu((double)g) * (double)u)
-                        const double sg = (double)gv / (1.0 + exp(-(double)gv));
-                        S.outw[(wave < 4 ? 4 * wave : 16 + 2 * (wave - 4)) + lane] = (float)(sg * (double)uv);
+                        // reference src/qx_format.c:5298, 2511-2513: h = silu(g) * u, here in f32
+                        // (relative error ~1e-7 against the reference's double)
+                        const float sg = gv / (1.0f + expf(-gv));
+                        S.outw[(wave < 4 ? 4 * wave : 16 + 2 * (wave - 4)) + lane] = sg * uv;
                     }
                 }
                 __syncthreads();
