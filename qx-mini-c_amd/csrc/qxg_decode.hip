@@ -1759,6 +1759,7 @@ DEV void decode_steps(const QxDArgs &args) {
             __syncthreads();
         }
     }
+    wait_loads();   // no copy into LDS outstanding at exit (a launch of no steps has the prologue's)
     if (a.d_time && wg == 0 && tix() == 0) gpw(a.d_time)[a.rec_base + a.steps] = __builtin_amdgcn_s_memrealtime();
 #ifdef QXD_TRACE
     __syncthreads();

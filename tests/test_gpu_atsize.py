@@ -243,6 +243,7 @@ def test_config4_prompt_state_loop_one_launch(big, tmp_path):
     assert len(toks) == 15 and [t["input_token"] for t in toks[:8]] == [int(t) for t in prompt]
     for t in toks[:7]:
         assert t["selected_token"] is None and "final_head" not in t and t["phase"] == "prefill"
+    ctx.kv_create(LAYERS, 32)
     gen, _ = ctx.generate(prompt, 8)
     assert [t["selected_token"] for t in toks[7:]] == [int(g) for g in gen]
     for t in toks[7:]:
@@ -258,6 +259,53 @@ def test_config4_prompt_state_loop_one_launch(big, tmp_path):
         f"{ph['prefill']['tokens_per_second']:.1f}, decode {ph['decode']['tokens_per_second']:.1f}), "
         f"{b['device']['tokens_per_second']:.1f} tok/s in qxg_generate, wall {b['wall_elapsed_sec']:.3f} s")
     assert b["tokens_per_second"] >= 0.8 * b["device"]["tokens_per_second"]
+
+
+def _prompt_loop(model_path, prompt, n_gen, out, snap_out=None, snap_in=None, ctx_tokens=32):
+    """qx_dump_prompt_state_loop_probe_summary with --full-moe --final-head --bench (the
+    reference's prototype), optionally writing or resuming a QXKVSNP1 snapshot."""
+    f = qxg._h.qx_dump_prompt_state_loop_probe_summary
+    c_char_p, u32, vp, ci = ctypes.c_char_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_int
+    f.argtypes = ([c_char_p, c_char_p, vp, u32, u32, u32, u32, c_char_p, c_char_p, c_char_p, c_char_p, c_char_p, u32,
+                   c_char_p] + [c_char_p] * 7 + [ci] * 13 + [u32, c_char_p, u32, u32, u32, ctypes.c_double, u32, c_char_p,
+                                                             u32, c_char_p, c_char_p, c_char_p, vp, c_char_p, ctypes.c_uint64])
+    f.restype = ci
+    libc = ctypes.CDLL(None)
+    libc.fopen.restype = vp
+    libc.fopen.argtypes = [c_char_p, c_char_p]
+    libc.fclose.argtypes = [vp]
+    fp = libc.fopen(str(out).encode(), b"w")
+    err = ctypes.create_string_buffer(512)
+    p = np.ascontiguousarray(prompt, np.uint32)
+    enc = lambda x: None if x is None else str(x).encode()
+    ok = f(model_path.encode(), None, p.ctypes.data_as(vp), len(p), n_gen, LAYERS, ctx_tokens, b"int8", b"f32", b"ephemeral",
+           b"baseline", b"serial", 1, b"scalar", b"none", b"none", b"none", b"none", b"none", b"none", b"none",
+           0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 2048, None, 5, 64, 5, 0.0, 7, None, 0, None, enc(snap_out), enc(snap_in),
+           fp, err, 512)
+    libc.fclose(fp)
+    assert ok == 1, err.value.decode()
+    return json.load(open(out))
+
+
+def test_config4_state_loop_snapshot_resume(big, tmp_path):
+    """The state loop's one recorded launch from a resumed cache (position_base > 0): a
+    3-token prompt and 2 greedy tokens written to a QXKVSNP1 snapshot, then the snapshot's
+    next token resumed for 3 more steps at positions 4..6 (the reference's resume rule,
+    src/qx_format.c:6165-6177), give the tokens of one uninterrupted qxg_generate."""
+    ctx, om, prompt, model_path = big
+    p3 = [int(t) for t in prompt[:3]]
+    snap = tmp_path / "kv.qxkv"
+    j1 = _prompt_loop(model_path, p3, 2, tmp_path / "a.json", snap_out=snap)
+    first = [t["selected_token"] for t in j1["tokens"] if t["selected_token"] is not None]
+    assert len(first) == 2 and j1["bench"]["timed"] == "device_launch"
+    j2 = _prompt_loop(model_path, [first[-1]], 3, tmp_path / "b.json", snap_in=snap)
+    assert j2["position_base"] == 4 and [t["position"] for t in j2["tokens"]] == [4, 5, 6]
+    resumed = [t["selected_token"] for t in j2["tokens"]]
+    ctx.kv_create(LAYERS, 32)
+    gen, _ = ctx.generate(p3, 5)
+    assert first + resumed == [int(g) for g in gen], (first, resumed, list(gen))
+    say(f"snapshot resume: {first} + {resumed} = qxg_generate; resumed launch "
+        f"{j2['bench']['tokens_per_second']:.1f} tok/s")
 
 
 def test_config5_prefill_layer_512_tokens(big):
