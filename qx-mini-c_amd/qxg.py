@@ -404,7 +404,7 @@ class Context:
         _g.qxg_set_attention_chunks(self._c, int(min_positions))
 
     def set_layer_path(self, persistent):
-        """0: one kernel per phase (default); 1: the persistent layer kernel."""
+        """1: the persistent layer kernel (the default); 0: one kernel per phase."""
         self._check(_g.qxg_set_layer_path(self._c, int(persistent)))
 
     def set_activation(self, fmt):

@@ -221,6 +221,30 @@ def test_generate_recorded_matches_steps(model, p0):
         c.close()
 
 
+def test_generate_recorded_rejects_bad_arguments(model):
+    """qxg_generate_recorded fails with a message, before any launch, on an empty prompt or
+    no generated token, a prompt token past the vocabulary, a loop past the KV context, and
+    on a context whose decode is not the persistent kernel; the context stays usable."""
+    m, om = model
+    c = open_ctx(m.path)
+    try:
+        c.kv_create(LAYERS, 8)
+        for prompt, n_gen, pos0, msg in (([], 2, 0, "prompt"), ([5], 0, 0, "generated"),
+                                         ([VOCAB], 1, 0, "out of range"), ([5, 6], 8, 0, "KV context"),
+                                         ([5], 2, 7, "KV context")):
+            with pytest.raises(qxg.QxgError, match=msg):
+                c.generate_recorded(prompt, n_gen, pos0=pos0)
+        r = c.generate_recorded([5, 6], 3)
+        gen, _ = c.generate([5, 6], 3)
+        assert list(r["tokens"][2:]) == list(gen)
+        c.set_layer_path(0)
+        assert not c.persistent_path()
+        with pytest.raises(qxg.QxgError, match="persistent"):
+            c.generate_recorded([5], 1)
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("chunks", [WALK, CHUNKS], ids=["walk", "chunked"])
 def test_outliers_same_input(outlier_model, chunks):
     """Planted outlier channels through the persistent kernel: a 4-token prompt and 3 greedy
