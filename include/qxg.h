@@ -45,8 +45,8 @@ int qxg_upload_tensor(qxg_ctx *ctx, const char *name, uint32_t ggml_type, const 
  * buffers.  need_head / need_embedding select whether output.* / token_embd.* must
  * be present.  Per layer: attn_q/k/v/output IQ4_XS or Q5_K; gate/up experts IQ2_XS
  * or IQ2_S (both the same); down experts IQ3_XXS, IQ4_XS or IQ3_S.  A model using any
- * format beyond IQ4_XS / IQ2_XS / IQ3_XXS decodes one kernel per phase, and
- * qxg_prefill / qxg_prefill_layer run it token by token through the decode kernels. */
+ * format beyond IQ4_XS / IQ2_XS / IQ3_XXS decodes one kernel per phase; its prefill
+ * (qxg_prefill / qxg_prefill_layer) stays batched on the matrix cores. */
 int qxg_bind_model(qxg_ctx *ctx, uint32_t layers, int need_embedding, int need_head, char *err, uint64_t err_len);
 
 /* Persistent INT8 KV cache [layers][ctx_tokens][512] for K and V plus one f32 scale
@@ -277,7 +277,8 @@ int qxg_decode_halves(qxg_ctx *ctx, uint32_t layers, float *attn_out, float *moe
 /* Persistent decode only (no reference counterpart): from n = position + 1 >=
  * min_positions on, stage A attends by (kv head, 64-position chunk) over every workgroup
  * and merges the chunks' partial softmax results; below it the 32 q-head workgroups walk
- * the cache themselves.  Default 257; 1 chunks every position, 4097 never. */
+ * the cache themselves.  Default 481 (measured crossover of the two); 1 chunks every position,
+ * 4097 never. */
 int qxg_set_attention_chunks(qxg_ctx *ctx, uint32_t min_positions);
 
 /* The output-RMSNorm vector (2048 floats) of the last head step run by qxg_decode_token:

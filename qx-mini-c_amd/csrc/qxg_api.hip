@@ -703,9 +703,9 @@ uint16_t f16_int(int v) {
     return (uint16_t)(sign | ((uint32_t)(e + 15) << 10) | mant);
 }
 
-// The batched GEMM path decodes the benchmark mix in the f32 activation mode; other
-// models and q8_k_compat prefill token by token through the decode kernels, which is
-// how the reference prefills every prompt.
+// The batched GEMM path takes every bound format in the f32 activation mode; q8_k_compat
+// prefills token by token through the decode kernels, which is how the reference
+// prefills every prompt.
 bool batched_prefill(const qxg_ctx *c) { return !c->q8; }
 
 bool prefill_ready(qxg_ctx *c, char *err, uint64_t n) {
