@@ -122,8 +122,9 @@ int qxg_persistent_path(const qxg_ctx *ctx);
  *   ids_out, weights_out   [S][L][8] the routing (as qxg_decode_routing);
  *   head_sums_out[S][L][32] each q head's sum of normalised attention weights;
  *   norm_out[S][2048], logits_out[S][vocab]   each head step's output-RMSNorm vector and
- *                          logits (steps before the last prompt token hold no head);
- *   top_ids, top_logits    [S][top_n] each head step's best tokens, highest first;
+ *                          logits (steps before the last prompt token run no head: zeros);
+ *   top_ids, top_logits    [S][top_n] each head step's best tokens, highest first (zeros
+ *                          before the last prompt token);
  *   step_ms[S + 1]         the device clock at each step's start and at the end, in ms from
  *                          the first step's start;
  *   elapsed_ms             the device time of the launch (HIP events).

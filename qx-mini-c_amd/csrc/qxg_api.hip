@@ -1679,6 +1679,12 @@ int qxg_generate_recorded(qxg_ctx *c, const uint32_t *prompt, uint32_t n_prompt,
         !get((void **)&d_w, n_ids * 8) || !get((void **)&d_ws, n_ws * 8) || !get((void **)&d_post, sizeof(DevState)) ||
         !get((void **)&d_time, (steps + 1) * 8))
         return 0;
+    // the prompt steps before the last write no head records: their slots read back as zeros
+    if (!hip_ok(hipMemsetAsync(d_norm, 0, n_res * 4, c->s), err, err_len, "record buffers") ||
+        !hip_ok(hipMemsetAsync(d_lg, 0, n_lg * 4, c->s), err, err_len, "record buffers") ||
+        !hip_ok(hipMemsetAsync(d_tv, 0, n_top * 4, c->s), err, err_len, "record buffers") ||
+        !hip_ok(hipMemsetAsync(d_ti, 0, n_top * 4, c->s), err, err_len, "record buffers"))
+        return 0;
     (void)hipMemcpyAsync(c->tokens, prompt, (uint64_t)n_prompt * 4, hipMemcpyHostToDevice, c->s);
     write_state(c, pos0, 0, n_prompt, 0);
     DecodeDumps d;

@@ -210,6 +210,7 @@ def test_generate_recorded_matches_steps(model, p0):
                 assert int(r["tokens"][s + 1]) == tok, s
             else:
                 tok = prompt[s + 1]
+                assert not r["logits"][s].any() and not r["top_ids"][s].any(), s   # no head: zeros
         for l in range(LAYERS):
             for got, want in zip(rows[l], c.kv_read(l, p0, S)):
                 assert np.array_equal(got, want), l
