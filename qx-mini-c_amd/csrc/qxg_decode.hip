@@ -767,6 +767,9 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
     const int q4 = lane & 3, jq = lane >> 2, p4 = lane >> 4, dg = lane & 15;
     Dig d;
     load_dig(A.qd, q4, d);
+    // scores and the running maximum in double (planted x1e6 channels make scores large
+    // enough that an f32 difference s - m loses the 1e-5 bar); the exponentials in f32 of
+    // that double difference (a double exp's polynomial constants spill the layer loop)
     const double inv_sqrt_hd = 1.0 / a.sqrt_hd;
     double m = -INFINITY, lsum = 0.0;
     float acc[8];
@@ -805,12 +808,12 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
         const double mi = wave_max_d(valid ? sc : -INFINITY);
         if (mi != -INFINITY) {   // wave-uniform: the block holds some of the wave's positions
             const double mn = fmax(m, mi);
-            const double f = exp(m - mn);   // 0 on the first block with positions (m = -inf)
-            const double e = valid ? exp(sc - mn) : 0.0;
-            lsum = lsum * f + wave_total_d(q4 == 0 ? e : 0.0);
-            if (q4 == 0) W.p[jq] = (float)(e * (double)vsc);
+            const float f = expf((float)(m - mn));   // 0 on the first block with positions (m = -inf)
+            const float e = valid ? expf((float)(sc - mn)) : 0.0f;
+            lsum = lsum * (double)f + wave_total_f(q4 == 0 ? e : 0.0f);
+            if (q4 == 0) W.p[jq] = e * vsc;
             wave_lds_sync();
-            const float ff = (float)f;
+            const float ff = f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[i] *= ff;
 #pragma unroll
@@ -842,7 +845,7 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
         for (int v = 1; v < NWV; ++v) M = fmax(M, A.m[v]);
         // lane v < 8 forms wave v's factor exp(m_v - M); every lane then reads the eight
         const double mv = A.m[lane & 7];
-        const double fl = mv == -INFINITY ? 0.0 : exp(mv - M);
+        const double fl = mv == -INFINITY ? 0.0 : (double)expf((float)(mv - M));   // (f32, as the block loop)
         double fw[NWV], L = 0.0;
 #pragma unroll
         for (int v = 0; v < NWV; ++v) { fw[v] = rdlaned(fl, v); L += fw[v] * A.l[v]; }
@@ -1572,7 +1575,7 @@ DEV void decode_steps(const QxDArgs &args) {
                     uint32_t pk[QXG_TOPK];   // the picks again, from LDS (the registers of ids are free after the row loads)
 #pragma unroll
                     for (int q = 0; q < QXG_TOPK; ++q) pk[q] = S.dne[q];
-                    wave_top8_weights(l0 * inv, l1 * inv, pk, wts);
+                    wave_top8_weights<true>(l0 * inv, l1 * inv, pk, wts);
                     if (lane < 2 * QXG_TOPK) {   // lane 2q: hi word of weight q, lane 2q + 1: lo word
                         double wl = 0.0;
                         uint32_t il = 0u;

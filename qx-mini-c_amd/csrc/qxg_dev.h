@@ -77,6 +77,10 @@ DEV double wave_total_d(double v) {
     v = row16_sum_d(v);
     return (rdlaned(v, 0) + rdlaned(v, 16)) + (rdlaned(v, 32) + rdlaned(v, 48));
 }
+DEV float wave_total_f(float v) {
+    v += dppf<DPP_XOR1>(v); v += dppf<DPP_XOR2>(v); v += dppf<DPP_ROR4>(v); v += dppf<DPP_ROR8>(v);
+    return (rdlanef(v, 0) + rdlanef(v, 16)) + (rdlanef(v, 32) + rdlanef(v, 48));
+}
 DEV double wave_max_d(double v) {
     v = fmax(v, dppd<DPP_XOR1>(v)); v = fmax(v, dppd<DPP_XOR2>(v));
     v = fmax(v, dppd<DPP_ROR4>(v)); v = fmax(v, dppd<DPP_ROR8>(v));
@@ -962,6 +966,10 @@ DEV void wave_top8_ids(double l0, double l1, int E, uint32_t (&ids)[QXG_TOPK]) {
         (void)top8_rounds<uint64_t>(lane < E ? dkey(l0) : 0ull, lane + 64 < E ? dkey(l1) : 0ull,
                                     [](uint64_t v) { return wave_max_u64(v); }, ids);
 }
+// F32EXP: e = exp(x) as (double)expf(hi) * (1 + lo), x = hi + lo with hi = (float)x (relative
+// error ~1 f32 ulp, 6e-8, against the double exp; the persistent decode, where a double exp's
+// polynomial constants would be held in registers across its layer loop)
+template <bool F32EXP = false>
 DEV void wave_top8_weights(double l0, double l1, const uint32_t (&ids)[QXG_TOPK], double (&w)[QXG_TOPK]) {
     const int lane = threadIdx.x & 63;
     double lq = 0.0;   // lane q < 8: logit of pick q
@@ -971,7 +979,16 @@ DEV void wave_top8_weights(double l0, double l1, const uint32_t (&ids)[QXG_TOPK]
         if (lane == q) lq = v;
     }
     const double lmax = rdlaned(lq, 0);
-    const double eq = lane < QXG_TOPK ? exp(lq - lmax) : 0.0;
+    double eq = 0.0;
+    if (lane < QXG_TOPK) {
+        const double x = lq - lmax;
+        if constexpr (F32EXP) {
+            const float hi = (float)x;
+            eq = (double)expf(hi) * (1.0 + (x - (double)hi));
+        } else {
+            eq = exp(x);
+        }
+    }
     double sel = 0.0;
 #pragma unroll
     for (int q = 0; q < QXG_TOPK; ++q) sel += rdlaned(eq, q);   // rank order, as the reference
