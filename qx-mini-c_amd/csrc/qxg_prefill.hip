@@ -420,8 +420,11 @@ DEV void gemm_body(const PfGemm &g, const GemmLds &L, uint32_t e, uint32_t mt0, 
                 float gv = acc[0][m][r] * rs, uv = acc[1][m][r] * rs;
                 gv = isfinite(gv) ? gv : 0.0f;
                 uv = isfinite(uv) ? uv : 0.0f;
-                const double sg = (double)gv / (1.0 + exp(-(double)gv));   // qx_silu, src/qx_format.c:2511-2513
-                g.out[(uint64_t)row * g.ld + c0 + col] = (float)(sg * (double)uv);
+                // qx_silu (src/qx_format.c:2511-2513) in f32: relative error ~1e-7 against the
+                // reference's double, far inside the 1e-5 bar; a double exp per output was a
+                // large share of the epilogue
+                const float sg = gv / (1.0f + expf(-gv));
+                g.out[(uint64_t)row * g.ld + c0 + col] = sg * uv;
             } else {
 #pragma unroll
                 for (int n = 0; n < NSUB; ++n) {
