@@ -110,11 +110,11 @@ def seed_cache(ctx, okv, p0, seed):
 
 @pytest.mark.parametrize("p0", [0, 1, 31, 32, 33, 63, 64, 65, 127, 300, 1000, 2016, 4032])
 def test_chunked_short_positions(model, p0):
-    """The chunked stage A at every chunk count boundary it can meet (no cached chunk, a
-    ragged or full last cached chunk; chunks of 32 positions up to 2048 positions, of 64
-    beyond: the switch is met at 2047/2048 below), forced at short positions.  2016/2017 and
-    4032/4033 step from 63 to 64 cached chunks, where the position's own workgroups no longer
-    fit the grid and the last chunk holds the position."""
+    """The chunked stage A at every chunk count boundary it can meet (one chunk, the
+    position alone in its chunk, a full last chunk; chunks of 32 positions up to 2048
+    positions, of 64 beyond: the switch is met at 2047/2048 below), forced at short
+    positions, and at 2016/2017 and 4032/4033, where the last chunk is full and then the
+    position opens the 64th."""
     m, om = model
     c = open_ctx(m.path, CHUNKS)
     try:
