@@ -224,8 +224,9 @@ int qxg_final_head(qxg_ctx *ctx, const float *residual, float *norm_out, float *
  * (src/qx_format.c:6250-6547, sampling_step at 6253).  Chunks of 512 tokens run in
  * order; every per-layer format of the real checkpoint (IQ4_XS / Q5_K attention,
  * IQ2_XS / IQ2_S gate/up, IQ3_XXS / IQ3_S / IQ4_XS down) runs batched.  The q8_k_compat
- * mode takes those token steps on the device instead (the decode kernels, one token at a
- * time: the result equals qxg_decode_token over the prompt).
+ * mode takes those token steps on the device instead (the one-kernel-per-phase decode
+ * kernels, one token at a time: the result equals qxg_decode_token over the prompt on
+ * layer path 0, and the persistent path's within the decode tolerance).
  * residual_out (may be NULL): n*2048 floats, each token's residual after the
  * last layer.  logits / top_* as in qxg_decode_token.  elapsed_ms: device time of the
  * whole call (HIP events on the context stream). */
@@ -247,8 +248,9 @@ int qxg_prefill_layer(qxg_ctx *ctx, uint32_t layer, uint32_t n, uint32_t positio
  * argmax), one workgroup per CU, its phases handed over through epoch-tagged device
  * words; 0: one kernel per phase, six per layer, each step replayed from a recorded
  * graph.  Both give the same results to the stated tolerance.  Drops the recorded decode
- * graph.  A model bound with formats beyond IQ4_XS / IQ2_XS / IQ3_XXS, and the
- * q8_k_compat mode, run path 0 whatever is set here. */
+ * graph.  A model bound with formats beyond IQ4_XS / IQ2_XS / IQ3_XXS runs path 0
+ * whatever is set here; the q8_k_compat mode runs either path (the persistent kernel has
+ * a Q8_K instantiation). */
 int qxg_set_layer_path(qxg_ctx *ctx, int persistent);
 
 /* Activation format of the projections, experts and head: 0 "f32" (default), 1
@@ -256,9 +258,10 @@ int qxg_set_layer_path(qxg_ctx *ctx, int persistent);
  * stage probes (src/qx_format.c:5970-5972, 4217-4218, 5286-5288, 3565).  In
  * q8_k_compat the matvec inputs are quantized to Q8_K blocks (256 values, one f32
  * scale) and each weight type is dotted in integers; a non-finite activation or
- * expert row makes the call fail with the reference's message.  Runs one kernel per
- * phase (whatever qxg_set_layer_path says); qxg_prefill runs token by token through
- * the decode kernels in this mode.  Drops the recorded decode graph. */
+ * expert row makes the call fail with the reference's message.  Decode follows
+ * qxg_set_layer_path (the persistent kernel's Q8_K instantiation by default);
+ * qxg_prefill runs token by token through the one-kernel-per-phase decode kernels in
+ * this mode.  Drops the recorded decode graph. */
 int qxg_set_activation(qxg_ctx *ctx, uint32_t activation_format, char *err, uint64_t err_len);
 
 /* Routing of every layer in the last step run by qxg_decode_token (or the last step of

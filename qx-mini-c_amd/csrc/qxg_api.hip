@@ -29,6 +29,8 @@ __global__ void qxk_topk_merge(const float *, const uint32_t *, uint32_t, uint32
 __global__ void qxk_q8k(const float *, uint32_t, uint8_t *, uint32_t *);
 __global__ void qxk_decode(QxDArgs);
 __global__ void qxk_decode_chunked(QxDArgs);
+__global__ void qxk_decode_q8(QxDArgs);
+__global__ void qxk_decode_chunked_q8(QxDArgs);
 __global__ void qxk_interleave_experts(const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *,
                                        const uint8_t *, const uint8_t *, const uint8_t *, const uint8_t *, uint32_t, uint8_t *,
                                        uint8_t *);
@@ -374,8 +376,7 @@ constexpr uint64_t DECODE_WAIT_TICKS = 100000000ull;   // 1 s of the 100 MHz wal
 // benchmark mix only, and computes in the f32 activation mode; other models and
 // q8_k_compat run one kernel per phase.
 bool persistent(const qxg_ctx *c) {
-    return c->persist && c->base_mix && !c->q8 && c->emb && c->head && c->mfold && c->gu_il && c->dn_il && c->head_il &&
-           c->dpack;
+    return c->persist && c->base_mix && c->emb && c->head && c->mfold && c->gu_il && c->dn_il && c->head_il && c->dpack;
 }
 
 struct DecodeDumps {
@@ -438,7 +439,8 @@ bool launch_decode_part(qxg_ctx *c, bool chunked, uint32_t s0, uint32_t steps, u
     // kernel is launched plainly: one workgroup per CU fits (checked at open), so on a GPU not
     // saturated by other work all of them are resident, and every wait is bounded
     // (DECODE_WAIT_TICKS; a timed-out launch exits and the call reports it).
-    const void *fn = chunked ? (const void *)qxk_decode_chunked : (const void *)qxk_decode;
+    const void *fn = chunked ? (c->q8 ? (const void *)qxk_decode_chunked_q8 : (const void *)qxk_decode_chunked)
+                             : (c->q8 ? (const void *)qxk_decode_q8 : (const void *)qxk_decode);
     hipError_t e = hipErrorIllegalState;
     if (!c->coop_held) {
         e = hipLaunchCooperativeKernel(fn, dim3(QXG_PBLOCKS), dim3(QXD_THREADS), args, 0, c->s);
@@ -931,7 +933,9 @@ int qxg_open(int device, qxg_ctx **out, char *err, uint64_t err_len) {
         if (prop.multiProcessorCount < QXG_PBLOCKS ||
             hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device) != hipSuccess || !coop ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_decode, QXD_THREADS, 0) != hipSuccess || occ < 1 ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_decode_chunked, QXD_THREADS, 0) != hipSuccess || occ < 1) {
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_decode_chunked, QXD_THREADS, 0) != hipSuccess || occ < 1 ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_decode_q8, QXD_THREADS, 0) != hipSuccess || occ < 1 ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void *)qxk_decode_chunked_q8, QXD_THREADS, 0) != hipSuccess || occ < 1) {
             if (err && err_len)
                 snprintf(err, (size_t)err_len, "device %d has %d CUs; the persistent decode kernel needs %d resident workgroups",
                          device, prop.multiProcessorCount, QXG_PBLOCKS);
@@ -1135,14 +1139,21 @@ int qxg_bind_model(qxg_ctx *c, uint32_t layers, int need_embedding, int need_hea
     if (layers && base && !build_expert_interleave(c, err, err_len)) return 0;
     if (layers && base && !build_decode_pack(c, err, err_len)) return 0;
     c->bound = true;
-    // one launch of each persistent kernel with no steps (prologue only): the runtime loads a
-    // kernel's code and sets up its first cooperative launch at that launch (≈12 ms measured),
-    // which would otherwise fall in the first timed call
+    // one launch of each persistent kernel (both activation modes: the mode may change after
+    // binding) with no steps (prologue only): the runtime loads a kernel's code and sets up its
+    // first cooperative launch at that launch (≈12 ms measured), which would otherwise fall in
+    // the first timed call
     if (persistent(c)) {
         DecodeDumps none;
-        for (bool chunked : {false, true})
-            if (!launch_decode_part(c, chunked, 0, 0, 1, 0, false, none, err, err_len)) return 0;
-        if (!finish(c, err, err_len)) return 0;
+        const bool q8 = c->q8;
+        bool ok = true;
+        for (bool mode : {false, true}) {
+            c->q8 = mode;
+            for (bool chunked : {false, true})
+                ok = ok && launch_decode_part(c, chunked, 0, 0, 1, 0, false, none, err, err_len);
+        }
+        c->q8 = q8;
+        if (!ok || !finish(c, err, err_len)) return 0;
     }
     return 1;
 }

@@ -310,11 +310,28 @@ DEV void upper_waves_sync(DLds &S, uint32_t tag) {
     asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
 }
 
+// Chunk c (values 8 c .. 8 c + 7, in y) of a q8_k_compat activation into the digit planes:
+// its Q8_K codes (q8_chunk: every lane of the wave calls it, 32 lanes a 256-value block) in
+// the h plane, m = l = 0, and the block's d / 65536 as the 32-group scale, so the digit dots
+// compute d * sum(code * w) (the per-phase kernels' block_q8).
+DEV void store_q8(const float (&y)[8], int c, uint32_t *dig) {
+    uint32_t h0, h1;
+    const float dq = q8_chunk(y, h0, h1);
+    uint32_t *d = dig + (c >> 2) * DIG_STRIDE;
+    const int q = c & 3;
+    *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+    *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(0u, 0u);
+    *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(0u, 0u);
+    if (q == 0) d[24] = __float_as_uint(dq * (1.0f / 65536.0f));
+}
+
 // Digit planes of an N-vector held in LDS (as f32 bits), 8 values per thread-chunk; with
 // NORM it is first RMS-normalised (reference src/qx_format.c:3358-3371), w8 the norm
 // weights of the thread's 8 values (threads < 256).
-// The inverse RMS goes to *inv_out.  Returns true when every value is finite.
-template <int N, bool NORM>
+// The inverse RMS goes to *inv_out.  Returns true when every value is finite.  Q8: the
+// q8_k_compat activations instead (Q8_K codes in the h plane, m = l = 0, each 32-group
+// scale d / 65536; q8_chunk): the 256-value blocks are the chunks of 32 consecutive lanes.
+template <int N, bool NORM, bool Q8 = false>
 DEV bool vec_digits(const float *v, const float *w8, DLds &S, double *inv_out = nullptr, GLB float *norm_out = nullptr) {
     constexpr int NCH = N / 8;
     const int tid = tix(), lane = tid & 63, wave = tid >> 6;
@@ -346,20 +363,26 @@ DEV bool vec_digits(const float *v, const float *w8, DLds &S, double *inv_out = 
                 for (int i = 0; i < 8; ++i) norm_out[8 * c + i] = y[i];
             }
         }
-        float mx = 0.0f;
+        if constexpr (Q8) {   // (whole waves take each pass: NCH and NT are multiples of 64)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { fin = fin && isfinite(y[i]); mx = fmaxf(mx, fabsf(y[i])); }
-        mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
-        mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
-        uint32_t h0, h1, m0, m1, l0, l1;
-        float sc;
-        digits8(y, isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
-        uint32_t *d = S.dig + (c >> 2) * DIG_STRIDE;
-        const int q = c & 3;
-        *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
-        *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
-        *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
-        if (q == 0) d[24] = __float_as_uint(sc);
+            for (int i = 0; i < 8; ++i) fin = fin && isfinite(y[i]);
+            store_q8(y, c, S.dig);
+        } else {
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { fin = fin && isfinite(y[i]); mx = fmaxf(mx, fabsf(y[i])); }
+            mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
+            mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
+            uint32_t h0, h1, m0, m1, l0, l1;
+            float sc;
+            digits8(y, isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
+            uint32_t *d = S.dig + (c >> 2) * DIG_STRIDE;
+            const int q = c & 3;
+            *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
+            *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
+            if (q == 0) d[24] = __float_as_uint(sc);
+        }
     }
     return !block_any(!fin, S);
 }
@@ -1227,7 +1250,7 @@ DEV bool better(float v, uint32_t i, float bv, uint32_t bi) { return v > bv || (
 // The decode steps; CHUNKED: stage A by kv head and chunk (every step of the launch at
 // n = pos + 1 >= att_split_min), else the 32 q-head workgroups' walk.  Two kernels, so neither
 // carries the other's stage A code in its layer loop (the host splits a launch at the threshold).
-template <bool CHUNKED>
+template <bool CHUNKED, bool Q8>
 DEV void decode_steps(const QxDArgs &args) {
     __shared__ DLds S;
 #ifdef QXD_TRACE
@@ -1331,20 +1354,26 @@ DEV void decode_steps(const QxDArgs &args) {
                     const float nw8[8] = {wq.nw0.x, wq.nw0.y, wq.nw0.z, wq.nw0.w, wq.nw1.x, wq.nw1.y, wq.nw1.z, wq.nw1.w};
 #pragma unroll
                     for (int i = 0; i < 8; ++i) y[i] = (float)((double)S.xs[8 * tid + i] * inv) * nw8[i];
-                    float mx = 0.0f;
+                    if constexpr (Q8) {   // (waves 0..3 whole)
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) { fin = fin && isfinite(y[i]); mx = fmaxf(mx, fabsf(y[i])); }
-                    mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
-                    mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
-                    uint32_t h0, h1, m0, m1, l0, l1;
-                    float sc;
-                    digits8(y, isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
-                    uint32_t *d = S.dig + (tid >> 2) * DIG_STRIDE;
-                    const int q = tid & 3;
-                    *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
-                    *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
-                    *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
-                    if (q == 0) d[24] = __float_as_uint(sc);
+                        for (int i = 0; i < 8; ++i) fin = fin && isfinite(y[i]);
+                        store_q8(y, tid, S.dig);
+                    } else {
+                        float mx = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) { fin = fin && isfinite(y[i]); mx = fmaxf(mx, fabsf(y[i])); }
+                        mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
+                        mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
+                        uint32_t h0, h1, m0, m1, l0, l1;
+                        float sc;
+                        digits8(y, isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
+                        uint32_t *d = S.dig + (tid >> 2) * DIG_STRIDE;
+                        const int q = tid & 3;
+                        *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+                        *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
+                        *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
+                        if (q == 0) d[24] = __float_as_uint(sc);
+                    }
                 }
                 if ((uint32_t)wg < E) {
                     a_part = wave_total_d(a_part);
@@ -1352,6 +1381,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 }
                 DMARK(l, 34);
                 const bool ok = !block_any(!fin, S);
+                if (Q8 && !ok && tid == 0) gpw(a.st)->q8_fault = QXG_Q8_NONFINITE_INPUT;   // (src/qx_format.c:3906)
                 DMARK(l, 13);
                 if ((uint32_t)wg < E)
                     a_part = ((S.red[NWV + 0] + S.red[NWV + 1]) + (S.red[NWV + 2] + S.red[NWV + 3])) +
@@ -1439,19 +1469,33 @@ DEV void decode_steps(const QxDArgs &args) {
                 double b_part = 0.0;
                 if ((uint32_t)wg < E) {   // router ctx-part: sum_j M[e,j] ctx_j over values 8 tid ..
                     const float4 c0 = reinterpret_cast<const float4 *>(cx)[2 * tid], c1 = reinterpret_cast<const float4 *>(cx)[2 * tid + 1];
-                    b_part = (double)wm0.x * (double)c0.x + (double)wm0.y * (double)c0.y + (double)wm0.z * (double)c0.z +
-                             (double)wm0.w * (double)c0.w + (double)wm1.x * (double)c1.x + (double)wm1.y * (double)c1.y +
-                             (double)wm1.z * (double)c1.z + (double)wm1.w * (double)c1.w;
+                    double cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                    if constexpr (Q8) {
+                        // the O projection sees the context as Q8_K blocks (d * code), and the
+                        // fold M = W diag(w) O must see what it sees: the codes of chunk tid,
+                        // as vec_digits forms them below (whole waves: wg < E is uniform)
+                        const float c8[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                        uint32_t h0, h1;
+                        const double dq = q8_chunk(c8, h0, h1);
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) cv[i] = dq * (double)(int8_t)(((i < 4 ? h0 : h1) >> (8 * (i & 3))) & 255u);
+                    }
+                    b_part = (double)wm0.x * cv[0] + (double)wm0.y * cv[1] + (double)wm0.z * cv[2] + (double)wm0.w * cv[3] +
+                             (double)wm1.x * cv[4] + (double)wm1.y * cv[5] + (double)wm1.z * cv[6] + (double)wm1.w * cv[7];
                     b_part = wave_total_d(b_part);
                     if (lane == 0) S.red[wave] = b_part;
                     __syncthreads();   // (uniform: wg < E)
                     if (tid < 2) {   // the logit before the 1/rms(x') factor, (hi, lo) words
-                        const double bsum = ((S.red[0] + S.red[1]) + (S.red[2] + S.red[3])) + ((S.red[4] + S.red[5]) + (S.red[6] + S.red[7]));
+                        double bsum = ((S.red[0] + S.red[1]) + (S.red[2] + S.red[3])) + ((S.red[4] + S.red[5]) + (S.red[6] + S.red[7]));
+                        // a non-finite context makes every O output 0 (below, the reference's
+                        // non-finite rule), so x' = x and the context adds nothing to the logit
+                        if (!isfinite(bsum)) bsum = 0.0;
                         const uint64_t bits = (uint64_t)__double_as_longlong(a_part + bsum);
                         xst(X + XO_LG + par * XN_LG + 2 * wg + tid, ep + 3, tid == 0 ? (uint32_t)(bits >> 32) : (uint32_t)bits);
                     }
                 }
-                const bool ok = vec_digits<4096, false>(cx, nullptr, S);   // ends with barriers
+                const bool ok = vec_digits<4096, false, Q8>(cx, nullptr, S);   // ends with barriers
+                if (Q8 && !ok && tid == 0) gpw(a.st)->q8_fault = QXG_Q8_NONFINITE_INPUT;
                 DMARK(l, 14);
                 Dig g0, g1;
                 load_dig(S.dig, lane, g0);
@@ -1549,20 +1593,28 @@ DEV void decode_steps(const QxDArgs &args) {
                     float y[8];
 #pragma unroll
                     for (int k = 0; k < 8; ++k) y[k] = (float)((double)S.xp[8 * c + k] * inv) * fnw[k];
-                    float mx = 0.0f;
+                    if constexpr (Q8) {   // (waves 4..7 whole; a non-finite x' fails the step)
+                        bool fq = true;
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(y[k]));   // h of a non-finite row is 0 by itself
-                    mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
-                    mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
-                    uint32_t h0, h1, m0, m1, l0, l1;
-                    float sc;
-                    digits8(y, isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
-                    uint32_t *d = S.dig + (c >> 2) * DIG_STRIDE;
-                    const int q = c & 3;
-                    *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
-                    *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
-                    *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
-                    if (q == 0) d[24] = __float_as_uint(sc);
+                        for (int k = 0; k < 8; ++k) fq = fq && isfinite(y[k]);
+                        if (__ballot(!fq) != 0 && lane == 0) gpw(a.st)->q8_fault = QXG_Q8_NONFINITE_INPUT;
+                        store_q8(y, c, S.dig);
+                    } else {
+                        float mx = 0.0f;
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(y[k]));   // h of a non-finite row is 0 by itself
+                        mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
+                        mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
+                        uint32_t h0, h1, m0, m1, l0, l1;
+                        float sc;
+                        digits8(y, isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
+                        uint32_t *d = S.dig + (c >> 2) * DIG_STRIDE;
+                        const int q = c & 3;
+                        *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+                        *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
+                        *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
+                        if (q == 0) d[24] = __float_as_uint(sc);
+                    }
                     DMARKT(l, 17, 256);
                 }
                 __syncthreads();
@@ -1609,6 +1661,8 @@ DEV void decode_steps(const QxDArgs &args) {
 #pragma unroll
                     for (int k = 1; k < 4; ++k)
                         if (lane == k) { gv = o[k]; uv = o[4 + k]; }
+                    // q8_k_compat fails the step on a non-finite expert row (src/qx_format.c:4771)
+                    if (Q8 && lane < (wave < 4 ? 4 : 2) && (!isfinite(gv) || !isfinite(uv))) gpw(a.st)->q8_fault = QXG_Q8_NONFINITE_EXPERT;
                     gv = isfinite(gv) ? gv : 0.0f;
                     uv = isfinite(uv) ? uv : 0.0f;
                     if (lane < (wave < 4 ? 4 : 2)) {
@@ -1642,7 +1696,8 @@ DEV void decode_steps(const QxDArgs &args) {
 #pragma unroll
                 for (int q = 0; q < QXG_TOPK; ++q)
                     wr[q] = __longlong_as_double((long long)(((uint64_t)wtw[2 * q] << 32) | wtw[2 * q + 1]));
-                const bool okh = vec_digits<6144, false>(reinterpret_cast<const float *>(S.u.m.vin), nullptr, S);
+                const bool okh = vec_digits<6144, false, Q8>(reinterpret_cast<const float *>(S.u.m.vin), nullptr, S);
+                if (Q8 && !okh && tid == 0) gpw(a.st)->q8_fault = QXG_Q8_NONFINITE_INPUT;
                 DMARK(l, 15);
                 // wave w: rank w's rows 8 wg + j (lanes 8 j .. 8 j + 7, sub-block k of each block)
                 const int j8 = lane >> 3, k = lane & 7, wv = wave_id();
@@ -1675,6 +1730,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 part += dppf<DPP_XOR1>(part);
                 part += dppf<DPP_XOR2>(part);
                 part += dppf<DPP_HALF_MIRROR>(part);   // lanes 8 j .. 8 j + 7 hold row j's sum
+                if (Q8 && okh && k == 0 && !isfinite(part)) gpw(a.st)->q8_fault = QXG_Q8_NONFINITE_EXPERT;
                 if (k == 0) S.ys[wv][j8] = (okh && isfinite(part)) ? part : 0.0f;
                 DMARK(l, 26);
                 __syncthreads();
@@ -1713,7 +1769,8 @@ DEV void decode_steps(const QxDArgs &args) {
                 return;
             DMARK(48, 1);
             if (tid == 0) S.u.hd.next = 0u;   // (published by the barrier in vec_digits)
-            const bool fin = vec_digits<2048, true>(S.xs, onw, S, nullptr, rec && a.d_norm ? gpw(a.d_norm) + rslot * 2048 : nullptr);
+            const bool fin = vec_digits<2048, true, Q8>(S.xs, onw, S, nullptr, rec && a.d_norm ? gpw(a.d_norm) + rslot * 2048 : nullptr);
+            if (Q8 && !fin && tid == 0) gpw(a.st)->q8_fault = QXG_Q8_NONFINITE_INPUT;   // (src/qx_format.c:4026-4027)
             float bv;
             uint32_t bi;
             bool nonfin;
@@ -1773,8 +1830,11 @@ DEV void decode_steps(const QxDArgs &args) {
 #endif
 }
 
-extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) { decode_steps<false>(args); }
-extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode_chunked(QxDArgs args) { decode_steps<true>(args); }
+extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode(QxDArgs args) { decode_steps<false, false>(args); }
+extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode_chunked(QxDArgs args) { decode_steps<true, false>(args); }
+// the same in the q8_k_compat activation mode (every matvec input as Q8_K blocks)
+extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode_q8(QxDArgs args) { decode_steps<false, true>(args); }
+extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode_chunked_q8(QxDArgs args) { decode_steps<true, true>(args); }
 
 // The routed experts' rows of one layer in the interleaved layout (QXD_GU_UNIT, QXD_DN_ROW),
 // from the IQ2_XS gate/up planes (qs 64, sc 8, d 2 bytes per block, 8 blocks per row) and

@@ -217,7 +217,9 @@ def test_q8k_failures_report_and_clear(ctx, models):
             ctx.moe_layer(0, x)
         y, _, _, _ = ctx.moe_layer(0, seeded_normal(5))
         assert np.isfinite(y).all()
-        # prefill in this mode runs the decode kernels token by token: equal to decode steps
+        # prefill in this mode runs the one-kernel-per-phase decode kernels token by token:
+        # equal to the decode steps of that path
+        ctx.set_layer_path(0)
         ctx.kv_create(1, 8)
         res, _, ids, _, _ = ctx.prefill(np.array([1, 2, 3], np.uint32), 0, True, 2, want_residual=True)
         ctx.kv_create(1, 8)
@@ -229,6 +231,7 @@ def test_q8k_failures_report_and_clear(ctx, models):
         assert not qxg._g.qxg_set_activation(ctx._c, 7, err, 256)   # the C entry point rejects unknown formats
         assert b"unsupported activation" in err.value
     finally:
+        ctx.set_layer_path(1)
         ctx.set_activation("f32")
 
 
