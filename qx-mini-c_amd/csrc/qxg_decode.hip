@@ -519,7 +519,7 @@ constexpr uint32_t GU_GSC = 512, GU_GD = 576, GU_UQ = 592, GU_USC = 1104, GU_UD 
 // sub-block: p[k] gate and p[4 + k] up of unit k (the rest 0).  Sub-blocks in the order gate,
 // up of unit 0, 1, ..; a sub-block's index words are read two ahead and its codebook entries
 // one ahead of its dot.
-template <int NU>
+template <int NU, bool H1 = false>
 DEV void gu_dots(const uint8_t *ub, uint32_t q, uint32_t sc, uint32_t d, const DLds &S, const Dig &g, float (&p)[8]) {
     constexpr int NS = 2 * NU;
     uint2 qs[3];
@@ -540,7 +540,7 @@ DEV void gu_dots(const uint8_t *ub, uint32_t q, uint32_t sc, uint32_t d, const D
     for (int s2 = 0; s2 < NS; ++s2) {
         if (s2 + 2 < NS) ld(s2 + 2);
         if (s2 + 1 < NS) iq2_look(qs[(s2 + 1) % 3], S.g2, S.sel, kl[(s2 + 1) & 1]);
-        p[(s2 & 1) ? 4 + (s2 >> 1) : (s2 >> 1)] = iq2_dot(kl[s2 & 1], scs[s2 % 3], ds[s2 % 3], g);
+        p[(s2 & 1) ? 4 + (s2 >> 1) : (s2 >> 1)] = iq2_dot<H1>(kl[s2 & 1], scs[s2 % 3], ds[s2 % 3], g);
     }
 #pragma unroll
     for (int k = NU; k < 4; ++k) p[k] = p[4 + k] = 0.0f;
@@ -1169,6 +1169,7 @@ DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep
 // wave's LDS region; the next pass's loads are issued before this pass's dots.  Lane (b, ib)
 // then reads its sub-block's ql, qh, scale pair and d from LDS.  Returns the workgroup's best
 // (logit desc, index asc) through bv/bi (uniform); non-finite logits set *nonfin.
+template <bool H1>
 DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi, bool &nonfin, uint32_t rslot) {
     constexpr int R = HEAD_R;
     const int lane = tix() & 63, wave = wave_id();
@@ -1220,7 +1221,7 @@ DEV void head_rows(const QxDArgs &a, DLds &S, bool fin, float &bv, uint32_t &bi,
             const uint32_t so = 1536 + b * 16 + 8 * hh + 2 * k;
             const int s0 = (int8_t)r[so], s1 = (int8_t)r[so + 1];
             const uint32_t d16 = *reinterpret_cast<const uint16_t *>(r + 1664 + 2 * b);
-            part[rr] = dot_q6(l0, l1, h0, h1, s0, s1, d16, ib, g, bias);
+            part[rr] = dot_q6<H1>(l0, l1, h0, h1, s0, s1, d16, ib, g, bias);
         }
         wave_lds_sync();   // the rows are rewritten by the next pass
         rows_reduce<R>(part, out, lane);
@@ -1392,9 +1393,9 @@ DEV void decode_steps(const QxDArgs &args) {
                     float part[4], out[4];
                     {
                         const uint4(*lq)[64] = S.wq[wave_id()];
-                        part[0] = dot_iq4(lq[0][lane], wq.m[0], ib, g);
-                        part[1] = dot_iq4(lq[1][lane], wq.m[1], ib, g);
-                        part[2] = dot_iq4(lq[2][lane], wq.m[2], ib, g);
+                        part[0] = dot_iq4<Q8>(lq[0][lane], wq.m[0], ib, g);
+                        part[1] = dot_iq4<Q8>(lq[1][lane], wq.m[1], ib, g);
+                        part[2] = dot_iq4<Q8>(lq[2][lane], wq.m[2], ib, g);
                     }
                     part[3] = 0.0f;
                     rows_reduce<4>(part, out, lane);
@@ -1503,7 +1504,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 float part[1], out[1];
                 {
                     const uint4(*lo)[64] = S.wo[wave_id()];
-                    part[0] = dot_iq4(lo[0][lane], wo.m0, ib, g0) + dot_iq4(lo[1][lane], wo.m1, ib, g1);
+                    part[0] = dot_iq4<Q8>(lo[0][lane], wo.m0, ib, g0) + dot_iq4<Q8>(lo[1][lane], wo.m1, ib, g1);
                 }
                 rows_reduce<1>(part, out, lane);
                 const int r = 8 * wg + wave;
@@ -1647,8 +1648,8 @@ DEV void decode_steps(const QxDArgs &args) {
                     const uint32_t b = lane >> 3, ib = lane & 7;
                     const uint32_t q = b * 64 + ib * 8, sc = b * 8 + ib, d = b * 2;
                     const uint8_t *ub = S.u.m.gu[0] + (wv < 4 ? 4 * wv : 16 + 2 * (wv - 4)) * QXD_GU_UNIT;
-                    if (wv < 4) gu_dots<4>(ub, q, sc, d, S, g, p);
-                    else gu_dots<2>(ub, q, sc, d, S, g, p);
+                    if (wv < 4) gu_dots<4, Q8>(ub, q, sc, d, S, g, p);
+                    else gu_dots<2, Q8>(ub, q, sc, d, S, g, p);
                 }
                 rows_reduce<8>(p, o, lane);
                 DMARK(l, 18);
@@ -1724,7 +1725,7 @@ DEV void decode_steps(const QxDArgs &args) {
                             iq3_look(qs[b + 1], aux[b + 1], S.g3, S.sel, kl[(b + 1) & 1]);
                             load_dig(S.dig, 24 * wv + 8 * (b + 1) + k, gd[(b + 1) & 1]);
                         }
-                        part += iq3_dot(kl[b & 1], aux[b], ds[b], gd[b & 1]);
+                        part += iq3_dot<Q8>(kl[b & 1], aux[b], ds[b], gd[b & 1]);
                     }
                 }
                 part += dppf<DPP_XOR1>(part);
@@ -1775,7 +1776,7 @@ DEV void decode_steps(const QxDArgs &args) {
             uint32_t bi;
             bool nonfin;
             DMARK(48, 2);
-            head_rows(a, S, fin, bv, bi, nonfin, rslot);
+            head_rows<Q8>(a, S, fin, bv, bi, nonfin, rslot);
             DMARK(48, 3);
             DMARKT(48, 6, 64);
             DMARKT(48, 7, 192);

@@ -119,6 +119,8 @@ DEV uint32_t kv_lookup(uint32_t n) {
 
 // ---------------------------------------------------------------- per-format sub-block dots
 // IQ4_XS sub-block ib (32 values): codes kvalue[nibble], scale d*(ls-32)
+// H1 (q8_k_compat activations): the m and l planes are zero, their dots are skipped.
+template <bool H1 = false>
 DEV float dot_iq4(uint4 qs, uint2 meta, int ib, const Dig &g) {
     const uint32_t sh = meta.x >> 16, sl = meta.y;
     const int ls = ((sl >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
@@ -129,8 +131,10 @@ DEV float dot_iq4(uint4 qs, uint2 meta, int ib, const Dig &g) {
         const uint32_t wlo = kv_lookup(q[k] & 0x0f0f0f0fu);
         const uint32_t whi = kv_lookup((q[k] >> 4) & 0x0f0f0f0fu);
         aH = sdot4(wlo, g.h[k], aH); aH = sdot4(whi, g.h[4 + k], aH);
-        aM = sdot4(wlo, g.m[k], aM); aM = sdot4(whi, g.m[4 + k], aM);
-        aL = sdot4(wlo, g.l[k], aL); aL = sdot4(whi, g.l[4 + k], aL);
+        if constexpr (!H1) {
+            aM = sdot4(wlo, g.m[k], aM); aM = sdot4(whi, g.m[4 + k], aM);
+            aL = sdot4(wlo, g.l[k], aL); aL = sdot4(whi, g.l[4 + k], aL);
+        }
     }
     const float dl = fp16_exact(meta.x & 0xffffu) * (float)(ls - 32);
     return (dl * g.s) * combine(aH, aM, aL);
@@ -152,6 +156,7 @@ DEV void iq2_look(uint2 qs, const uint4 *G2, const uint2 *SEL, Iq2Look &k) {
         k.sl[l] = SEL[qv[l] >> 9];
     }
 }
+template <bool H1 = false>
 DEV float iq2_dot(const Iq2Look &k, uint32_t sc, uint32_t d16, const Dig &g) {
     int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
 #pragma unroll
@@ -159,12 +164,16 @@ DEV float iq2_dot(const Iq2Look &k, uint32_t sc, uint32_t d16, const Dig &g) {
         const uint32_t w0 = perm(k.gg[l].z, k.gg[l].x, k.sl[l].x), w1 = perm(k.gg[l].w, k.gg[l].y, k.sl[l].y);
         if (l < 2) {
             h0 = sdot4(w0, g.h[2 * l], h0); h0 = sdot4(w1, g.h[2 * l + 1], h0);
-            m0 = sdot4(w0, g.m[2 * l], m0); m0 = sdot4(w1, g.m[2 * l + 1], m0);
-            l0 = sdot4(w0, g.l[2 * l], l0); l0 = sdot4(w1, g.l[2 * l + 1], l0);
+            if constexpr (!H1) {
+                m0 = sdot4(w0, g.m[2 * l], m0); m0 = sdot4(w1, g.m[2 * l + 1], m0);
+                l0 = sdot4(w0, g.l[2 * l], l0); l0 = sdot4(w1, g.l[2 * l + 1], l0);
+            }
         } else {
             h1 = sdot4(w0, g.h[2 * l], h1); h1 = sdot4(w1, g.h[2 * l + 1], h1);
-            m1 = sdot4(w0, g.m[2 * l], m1); m1 = sdot4(w1, g.m[2 * l + 1], m1);
-            l1 = sdot4(w0, g.l[2 * l], l1); l1 = sdot4(w1, g.l[2 * l + 1], l1);
+            if constexpr (!H1) {
+                m1 = sdot4(w0, g.m[2 * l], m1); m1 = sdot4(w1, g.m[2 * l + 1], m1);
+                l1 = sdot4(w0, g.l[2 * l], l1); l1 = sdot4(w1, g.l[2 * l + 1], l1);
+            }
         }
     }
     const int k0 = 2 * (int)(sc & 15u) + 1, k1 = 2 * (int)(sc >> 4) + 1;
@@ -192,14 +201,17 @@ DEV void iq3_look(uint2 qs, uint32_t aux, const uint2 *G3, const uint2 *SEL, Iq3
         k.sl[l] = SEL[(aux >> (7 * l)) & 127u];
     }
 }
+template <bool H1 = false>
 DEV float iq3_dot(const Iq3Look &k, uint32_t aux, uint32_t d16, const Dig &g) {
     int aH = 0, aM = 0, aL = 0;
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
         const uint32_t w0 = perm(k.g[2 * l].y, k.g[2 * l].x, k.sl[l].x), w1 = perm(k.g[2 * l + 1].y, k.g[2 * l + 1].x, k.sl[l].y);
         aH = sdot4(w0, g.h[2 * l], aH); aH = sdot4(w1, g.h[2 * l + 1], aH);
-        aM = sdot4(w0, g.m[2 * l], aM); aM = sdot4(w1, g.m[2 * l + 1], aM);
-        aL = sdot4(w0, g.l[2 * l], aL); aL = sdot4(w1, g.l[2 * l + 1], aL);
+        if constexpr (!H1) {
+            aM = sdot4(w0, g.m[2 * l], aM); aM = sdot4(w1, g.m[2 * l + 1], aM);
+            aL = sdot4(w0, g.l[2 * l], aL); aL = sdot4(w1, g.l[2 * l + 1], aL);
+        }
     }
     const int k3 = 2 * (int)(aux >> 28) + 1;
     return ((fp16_exact(d16) * 0.25f) * g.s) * combine(mul24(k3, aH), mul24(k3, aM), mul24(k3, aL));
@@ -307,6 +319,7 @@ DEV Q6Bias q6_bias(const Dig &g) {
     return b;
 }
 
+template <bool H1 = false>
 DEV float dot_q6(uint4 ql0, uint4 ql1, uint4 qh0, uint4 qh1, int sc0, int sc1, uint32_t d16, int ib,
                  const Dig &g, const Q6Bias &bias) {
     const int k = ib & 3;
@@ -319,8 +332,10 @@ DEV float dot_q6(uint4 ql0, uint4 ql1, uint4 qh0, uint4 qh1, int sc0, int sc1, u
         const uint32_t u = ((ql[j] >> shl) & 0x0f0f0f0fu) | (((qh[j] >> shh) & 0x03030303u) << 4);
         const int s = j >> 2;
         aH[s] = sdot4(u, g.h[j], aH[s]);
-        aM[s] = sdot4(u, g.m[j], aM[s]);
-        aL[s] = sdot4(u, g.l[j], aL[s]);
+        if constexpr (!H1) {
+            aM[s] = sdot4(u, g.m[j], aM[s]);
+            aL[s] = sdot4(u, g.l[j], aL[s]);
+        }
     }
     const float v = combine(mul24(sc0, aH[0]) + mul24(sc1, aH[1]), mul24(sc0, aM[0]) + mul24(sc1, aM[1]),
                             mul24(sc0, aL[0]) + mul24(sc1, aL[1]));
@@ -521,11 +536,18 @@ DEV float q8_chunk(const float (&v)[8], uint32_t &h0, uint32_t &h1) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
         if (fabsf(v[i]) > am) { am = fabsf(v[i]); vm = v[i]; }
-    float bm = am;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) bm = fmaxf(bm, __shfl_xor(bm, o));
-    const uint32_t hit = (uint32_t)(__ballot(am == bm) >> (32 * half));
-    const float vmax = __shfl(vm, 32 * half + (hit ? __ffs(hit) - 1 : 0));
+    // the half-wave's largest magnitude: each 16-lane row's by DPP, then the two rows' read
+    // out (no LDS round trip); the first lane holding it, per half, from one ballot
+    float bm = fmaxf(am, dppf<DPP_XOR1>(am));
+    bm = fmaxf(bm, dppf<DPP_XOR2>(bm));
+    bm = fmaxf(bm, dppf<DPP_ROR4>(bm));
+    bm = fmaxf(bm, dppf<DPP_ROR8>(bm));
+    const float b0 = fmaxf(rdlanef(bm, 0), rdlanef(bm, 16)), b1 = fmaxf(rdlanef(bm, 32), rdlanef(bm, 48));
+    bm = half ? b1 : b0;
+    const uint64_t hits = __ballot(am == bm);
+    const uint32_t lo = (uint32_t)hits, hi = (uint32_t)(hits >> 32);
+    const float v0 = rdlanef(vm, lo ? __ffs(lo) - 1 : 0), v1 = rdlanef(vm, hi ? 31 + __ffs(hi) : 32);
+    const float vmax = half ? v1 : v0;
     const float inv = vmax == 0.0f ? 0.0f : -127.0f / vmax;
     uint32_t H[2] = {0u, 0u};
 #pragma unroll
