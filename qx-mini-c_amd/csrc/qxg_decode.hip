@@ -251,9 +251,11 @@ DEV void wait_pairs(u32x4 (&w)[K2]) {
     else static_assert(K2 == 1 || K2 == 2 || K2 == 4 || K2 == 7, "pairs per thread");
 }
 // The polling of wait_xch2 by threads T0 .. T0 + P - 1 only (the caller's branch), pair
-// p = t + P k for thread T0 + t; returns this thread's success, with no barrier.
+// p = t + P k for thread T0 + t; returns this thread's success, with no barrier.  ssq (may
+// be null) gets the sum of squares of the thread's payloads as f32 values, in double.
 template <int K2, int P = NT, int T0 = 0, typename IDX>
-DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, const Ctl &c) {
+DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, const Ctl &c,
+                    double *ssq = nullptr) {
     const int tid = tix() - T0;
     u32x4 w[K2];
     bool got[K2];
@@ -283,7 +285,13 @@ DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst,
 #pragma unroll
     for (int k = 0; k < K2; ++k) {
         const int i = 2 * (tid + P * k);
-        if (i < n) *reinterpret_cast<uint2 *>(dst + i) = make_uint2(w[k].x, w[k].z);
+        if (i < n) {
+            *reinterpret_cast<uint2 *>(dst + i) = make_uint2(w[k].x, w[k].z);
+            if (ssq) {
+                const double u = (double)__uint_as_float(w[k].x), v = (double)__uint_as_float(w[k].z);
+                *ssq += u * u + v * v;
+            }
+        }
     }
     return ok;
 }
@@ -1315,8 +1323,23 @@ DEV void decode_steps(const QxDArgs &args) {
             {
                 const int tid = tix(), lane = tid & 63, wave = tid >> 6, ib = lane & 7;
                 DMARK(l, 0);
-                if (l > 0 && !wait_xch2<2>(X + XO_X + par * XN_X, 2048, ep, reinterpret_cast<uint32_t *>(S.xs), Ident(), S, ctl))
-                    return;
+                // x, and its sum of squares for the attention RMSNorm (reference
+                // src/qx_format.c:3358-3371, a double sum) from each thread's 4 polled values:
+                // the poll's barrier publishes the waves' sums with x (layer 0: the embedding,
+                // already in LDS)
+                {
+                    double ssq = 0.0;
+                    bool okx = true;
+                    if (l > 0) {
+                        okx = poll_pairs<2>(X + XO_X + par * XN_X, 2048, ep, reinterpret_cast<uint32_t *>(S.xs), Ident(), ctl, &ssq);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) ssq += (double)S.xs[4 * tid + i] * (double)S.xs[4 * tid + i];
+                    }
+                    ssq = wave_total_d(ssq);
+                    if (lane == 0) S.red[wave] = ssq;
+                    if (block_any(!okx, S)) return;
+                }
                 DMARK(l, 1);
                 wait_loads();   // the Q/K/V rows in LDS (issued a stage or more ago; nothing later is outstanding)
                 // attention workgroups (no Q/K/V rows of their own): the cached K/V rows they
@@ -1332,22 +1355,14 @@ DEV void decode_steps(const QxDArgs &args) {
                 double inv = 1.0;
                 bool fin = true;
                 {
-                    double ss = 0.0;
-                    if (mk && tid < 256) {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) ss += (double)S.xs[8 * tid + i] * (double)S.xs[8 * tid + i];
-                    }
-                    ss = wave_total_d(ss);
-                    if (lane == 0) S.red[wave] = ss;
                     // router x-part: sum_i W[e,i] w_i x_i over values 4 tid .. 4 tid + 3
                     if ((uint32_t)wg < E) {
                         const float4 x4 = reinterpret_cast<const float4 *>(S.xs)[tid];
                         a_part = (double)wo.wr.x * (double)wo.fw.x * (double)x4.x + (double)wo.wr.y * (double)wo.fw.y * (double)x4.y +
                                  (double)wo.wr.z * (double)wo.fw.z * (double)x4.z + (double)wo.wr.w * (double)wo.fw.w * (double)x4.w;
                     }
-                    __syncthreads();
                     DMARK(l, 33);
-                    const double tot = (S.red[0] + S.red[1]) + (S.red[2] + S.red[3]);
+                    const double tot = ((S.red[0] + S.red[1]) + (S.red[2] + S.red[3])) + ((S.red[4] + S.red[5]) + (S.red[6] + S.red[7]));
                     inv = 1.0 / sqrt(tot / 2048.0 + 1.0e-6);
                 }
                 if (mk && tid < 256) {
