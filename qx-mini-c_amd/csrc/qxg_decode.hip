@@ -1712,11 +1712,63 @@ DEV void decode_steps(const QxDArgs &args) {
 #pragma unroll
                 for (int q = 0; q < QXG_TOPK; ++q)
                     wr[q] = __longlong_as_double((long long)(((uint64_t)wtw[2 * q] << 32) | wtw[2 * q + 1]));
-                const bool okh = vec_digits<6144, false, Q8>(reinterpret_cast<const float *>(S.u.m.vin), nullptr, S);
-                if (Q8 && !okh && tid == 0) gpw(a.st)->q8_fault = QXG_Q8_NONFINITE_INPUT;
+                // wave w: the digits of rank w's h (values 768 w .., digit groups 24 w ..), which
+                // only its own dots read: no workgroup barrier (the h poll's barrier ordered
+                // them after every wave's stage G reads of the digit area).  A non-finite h
+                // zeroes that rank's rows only, as the reference's per-row rule does.
+                const int j8 = lane >> 3, k = lane & 7, wv = wave_id();
+                bool fh = true;
+                {
+                    const float *hv = reinterpret_cast<const float *>(S.u.m.vin) + 768 * wv;
+#pragma unroll
+                    for (int rd = 0; rd < 2; ++rd) {   // chunk lane, then chunk 64 + lane (lanes < 32)
+                        const int c = 64 * rd + lane;
+                        if (!Q8 && c >= 96) break;   // (whole quads: lanes 32.. of the second round)
+                        float y[8];
+                        if (c < 96) {
+                            const float4 a0 = reinterpret_cast<const float4 *>(hv)[2 * c], a1 = reinterpret_cast<const float4 *>(hv)[2 * c + 1];
+                            y[0] = a0.x; y[1] = a0.y; y[2] = a0.z; y[3] = a0.w; y[4] = a1.x; y[5] = a1.y; y[6] = a1.z; y[7] = a1.w;
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 8; ++i) y[i] = 0.0f;
+                        }
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) fh = fh && isfinite(y[i]);
+                        const int cg = 96 * wv + c;   // chunk of the 6144
+                        if constexpr (Q8) {   // (whole wave: a 256-value block is 32 lanes)
+                            uint32_t h0, h1;
+                            const float dq = q8_chunk(y, h0, h1);
+                            if (c < 96) {
+                                uint32_t *d = S.dig + (cg >> 2) * DIG_STRIDE;
+                                const int q = cg & 3;
+                                *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+                                *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(0u, 0u);
+                                *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(0u, 0u);
+                                if (q == 0) d[24] = __float_as_uint(dq * (1.0f / 65536.0f));
+                            }
+                        } else {
+                            float mx = 0.0f;
+#pragma unroll
+                            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(y[i]));
+                            mx = fmaxf(mx, dppf<DPP_XOR1>(mx));
+                            mx = fmaxf(mx, dppf<DPP_XOR2>(mx));
+                            uint32_t h0, h1, m0, m1, l0, l1;
+                            float sc;
+                            digits8(y, isfinite(mx) ? mx : 0.0f, h0, h1, m0, m1, l0, l1, sc);
+                            uint32_t *d = S.dig + (cg >> 2) * DIG_STRIDE;
+                            const int q = cg & 3;
+                            *reinterpret_cast<uint2 *>(d + 2 * q) = make_uint2(h0, h1);
+                            *reinterpret_cast<uint2 *>(d + 8 + 2 * q) = make_uint2(m0, m1);
+                            *reinterpret_cast<uint2 *>(d + 16 + 2 * q) = make_uint2(l0, l1);
+                            if (q == 0) d[24] = __float_as_uint(sc);
+                        }
+                    }
+                }
+                const bool okh = __ballot(!fh) == 0;
+                if (Q8 && !okh && lane == 0) gpw(a.st)->q8_fault = QXG_Q8_NONFINITE_INPUT;
+                wave_lds_sync();   // the wave's digits, read by its own lanes below
                 DMARK(l, 15);
                 // wave w: rank w's rows 8 wg + j (lanes 8 j .. 8 j + 7, sub-block k of each block)
-                const int j8 = lane >> 3, k = lane & 7, wv = wave_id();
                 float part = 0.0f;
                 {
                     // the three blocks' index words first, then block b + 1's codebook reads
