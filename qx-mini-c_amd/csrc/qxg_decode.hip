@@ -62,6 +62,36 @@ extern "C" int qxd_trace_read(unsigned long long *out) {
 #define DMARKT(layer, point, thread) ((void)0)
 #endif
 
+// First-round delays of the exchange polls, in units of 64 cycles (s_sleep): a workgroup
+// reaches a poll right after storing its own outputs, ahead of most producers, and poll
+// rounds issued while the words are still in flight only load the memory system the
+// producers' stores and the weight copies go through.
+#ifndef QXD_SLEEP_X
+#define QXD_SLEEP_X 16
+#endif
+#ifndef QXD_SLEEP_QKV
+#define QXD_SLEEP_QKV 0
+#endif
+#ifndef QXD_SLEEP_CX
+#define QXD_SLEEP_CX 0
+#endif
+#ifndef QXD_SLEEP_LG
+#define QXD_SLEEP_LG 0
+#endif
+#ifndef QXD_SLEEP_H
+#define QXD_SLEEP_H 16
+#endif
+#ifndef QXD_SLEEP_CQ
+#define QXD_SLEEP_CQ 0
+#endif
+#ifndef QXD_SLEEP_MG
+#define QXD_SLEEP_MG 0
+#endif
+#define QXD_SLEEP(n) \
+    do { \
+        if ((n) > 0) __builtin_amdgcn_s_sleep((n) > 0 ? (n) : 1); \
+    } while (0)
+
 namespace {
 
 constexpr int NT = 512;            // threads per workgroup
@@ -968,6 +998,7 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
     const float nq0 = nqp[lane], nq1 = nqp[64 + lane], nk0 = nkp[lane], nk1 = nkp[64 + lane];
     // q of heads 8 g .. 8 g + 7 (words 1024 g ..), then the K and V rows (4096 .. 5119)
     const GLB uint64_t *qkv = X + XO_QKV + par * XN_QKV;
+    QXD_SLEEP(QXD_SLEEP_CQ);
     if (!wait_xch2<2>(qkv, 2048, ep, reinterpret_cast<uint32_t *>(A.q[0]), [g](int i) { return i < 1024 ? 1024 * g + i : 3072 + i; },
                       S, ctl))
         return false;
@@ -1138,6 +1169,7 @@ DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep
     uint32_t *rw = S.u.m.vin;                                           // nch records of QXD_PREC words
     float *wt = reinterpret_cast<float *>(S.u.m.vin) + 2048;            // per chunk: (float)(exp(m_c - M) / L)
     const GLB uint64_t *src = gpw(a.xpart) + par * XN_PT + (h * 8u + dgm) * MAXCH * QXD_PREC;
+    QXD_SLEEP(QXD_SLEEP_MG);
     if (!wait_xch2<2>(src, (int)(QXD_PREC * nch), ep, rw, Ident(), S, ctl)) return false;
     DMARK(l, 25);
     if (w == 0) {   // wave 0 alone: lane c forms chunk c's factor, then lane (cg, d) sums chunks cg + 4 k
@@ -1331,6 +1363,7 @@ DEV void decode_steps(const QxDArgs &args) {
                     double ssq = 0.0;
                     bool okx = true;
                     if (l > 0) {
+                        QXD_SLEEP(QXD_SLEEP_X);
                         okx = poll_pairs<2>(X + XO_X + par * XN_X, 2048, ep, reinterpret_cast<uint32_t *>(S.xs), Ident(), ctl, &ssq);
                     } else {
 #pragma unroll
@@ -1447,6 +1480,7 @@ DEV void decode_steps(const QxDArgs &args) {
                     if (pre) load_wq(a, ln, wq, S.wq[wave_id()]);
                 }
             } else if (wg < QXG_HEADS) {
+                QXD_SLEEP(QXD_SLEEP_QKV);
                 if (!attn_wait(a, l, ep + 1, S, ctl)) return;
                 DMARK(l, 3);
                 attention(a, l, pos, ep + 1, ap, S, last, rec ? (int)rrow : -1);
@@ -1476,6 +1510,7 @@ DEV void decode_steps(const QxDArgs &args) {
             {
                 const int tid = tix(), lane = tid & 63, wave = tid >> 6, ib = lane & 7;
                 // sentinels: words 128 h and 128 h + 64 (the two store instructions of head h)
+                QXD_SLEEP(QXD_SLEEP_CX);
                 if (!wait_xch2<4>(X + XO_CX + par * XN_CX, 4096, ep + 2, S.u.m.vin, Ident(), S, ctl))
                     return;
                 DMARK(l, 5);
@@ -1542,6 +1577,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 // parallel: waves 0..3 (one per SIMD) take the top-8, issue the routed experts' row
                 // copies for themselves and waves 4..7 and wait for them; waves 4..7 poll x' and
                 // form its normalised digits.  One barrier joins them before the dots.
+                QXD_SLEEP(QXD_SLEEP_LG);
                 if (!wait_xch2<1>(X + XO_LG + par * XN_LG, 2 * (int)E, ep + 3, S.lgw, Ident(), S, ctl))
                     return;
                 DMARK(l, 7);
@@ -1701,6 +1737,7 @@ DEV void decode_steps(const QxDArgs &args) {
             {
                 const int tid = tix(), lane = tid & 63;
                 // h and the 8 expert weights (hi, lo words)
+                QXD_SLEEP(QXD_SLEEP_H);
                 if (!wait_xch2<7>(X, 6144 + 16, ep + 4, S.u.m.vin,
                                    [par](int i) { return i < 6144 ? (int)(XO_H + par * XN_H) + i : (int)(XO_WT + par * XN_WT) + i - 6144; }, S, ctl))
                     return;
