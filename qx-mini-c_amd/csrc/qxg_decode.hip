@@ -81,6 +81,18 @@ extern "C" int qxd_trace_read(unsigned long long *out) {
 #ifndef QXD_SLEEP_H
 #define QXD_SLEEP_H 16
 #endif
+#ifndef QXD_SLEEP_XR
+#define QXD_SLEEP_XR 0
+#endif
+#ifndef QXD_SLEEP_HR
+#define QXD_SLEEP_HR 0
+#endif
+#ifndef QXD_SLEEP_XP
+#define QXD_SLEEP_XP 16
+#endif
+#ifndef QXD_SLEEP_HX
+#define QXD_SLEEP_HX 0
+#endif
 #ifndef QXD_SLEEP_CQ
 #define QXD_SLEEP_CQ 0
 #endif
@@ -283,7 +295,7 @@ DEV void wait_pairs(u32x4 (&w)[K2]) {
 // The polling of wait_xch2 by threads T0 .. T0 + P - 1 only (the caller's branch), pair
 // p = t + P k for thread T0 + t; returns this thread's success, with no barrier.  ssq (may
 // be null) gets the sum of squares of the thread's payloads as f32 values, in double.
-template <int K2, int P = NT, int T0 = 0, typename IDX>
+template <int K2, int P = NT, int T0 = 0, int SR = 0, typename IDX>
 DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, const Ctl &c,
                     double *ssq = nullptr) {
     const int tid = tix() - T0;
@@ -311,6 +323,7 @@ DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst,
         }
         if (all) break;
         if (!keep_waiting(it, deadline, c)) { ok = false; break; }
+        QXD_SLEEP(SR);   // (between rounds)
     }
 #pragma unroll
     for (int k = 0; k < K2; ++k) {
@@ -325,9 +338,9 @@ DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst,
     }
     return ok;
 }
-template <int K2, typename IDX>
+template <int K2, int SR = 0, typename IDX>
 DEV bool wait_xch2(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, DLds &S, const Ctl &c) {
-    return !block_any(!poll_pairs<K2>(base, n, ep, dst, idx, c), S);
+    return !block_any(!poll_pairs<K2, NT, 0, SR>(base, n, ep, dst, idx, c), S);
 }
 
 // Waves 4..7 only, all four calling it: each wave's earlier LDS writes are visible to the
@@ -1364,7 +1377,7 @@ DEV void decode_steps(const QxDArgs &args) {
                     bool okx = true;
                     if (l > 0) {
                         QXD_SLEEP(QXD_SLEEP_X);
-                        okx = poll_pairs<2>(X + XO_X + par * XN_X, 2048, ep, reinterpret_cast<uint32_t *>(S.xs), Ident(), ctl, &ssq);
+                        okx = poll_pairs<2, NT, 0, QXD_SLEEP_XR>(X + XO_X + par * XN_X, 2048, ep, reinterpret_cast<uint32_t *>(S.xs), Ident(), ctl, &ssq);
                     } else {
 #pragma unroll
                         for (int i = 0; i < 4; ++i) ssq += (double)S.xs[4 * tid + i] * (double)S.xs[4 * tid + i];
@@ -1615,6 +1628,7 @@ DEV void decode_steps(const QxDArgs &args) {
                     // x', polled by these four waves alone (waves 0..3 are issuing the expert
                     // rows meanwhile; a poll behind those loads would wait for them)
                     const GLB uint64_t *xpb = X + XO_XP + par * XN_XP;
+                    QXD_SLEEP(QXD_SLEEP_XP);
                     if (!poll_pairs<4, 256, 256>(xpb, 2048, ep + 3, reinterpret_cast<uint32_t *>(S.xp), Ident(), ctl))
                         S.fail = 1u;
                     DMARKT(l, 38, 256);
@@ -1738,7 +1752,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 const int tid = tix(), lane = tid & 63;
                 // h and the 8 expert weights (hi, lo words)
                 QXD_SLEEP(QXD_SLEEP_H);
-                if (!wait_xch2<7>(X, 6144 + 16, ep + 4, S.u.m.vin,
+                if (!wait_xch2<7, QXD_SLEEP_HR>(X, 6144 + 16, ep + 4, S.u.m.vin,
                                    [par](int i) { return i < 6144 ? (int)(XO_H + par * XN_H) + i : (int)(XO_WT + par * XN_WT) + i - 6144; }, S, ctl))
                     return;
                 DMARK(l, 11);
@@ -1870,6 +1884,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 onw[0] = x0.x; onw[1] = x0.y; onw[2] = x0.z; onw[3] = x0.w; onw[4] = x1.x; onw[5] = x1.y; onw[6] = x1.z; onw[7] = x1.w;
             }
             DMARK(48, 0);
+            QXD_SLEEP(QXD_SLEEP_HX);
             if (!wait_xch2<2>(X + XO_X + (L & 1) * XN_X, 2048, eph, reinterpret_cast<uint32_t *>(S.xs), Ident(), S, ctl))
                 return;
             DMARK(48, 1);
