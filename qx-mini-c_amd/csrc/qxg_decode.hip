@@ -62,42 +62,20 @@ extern "C" int qxd_trace_read(unsigned long long *out) {
 #define DMARKT(layer, point, thread) ((void)0)
 #endif
 
-// First-round delays of the exchange polls, in units of 64 cycles (s_sleep): a workgroup
-// reaches a poll right after storing its own outputs, ahead of most producers, and poll
-// rounds issued while the words are still in flight only load the memory system the
-// producers' stores and the weight copies go through.
+// First-round delays of three exchange polls (x in stage Q, x' in stage G, h in stage D), in
+// units of 64 cycles (s_sleep).  A workgroup reaches a poll right after storing its own
+// outputs, ahead of most producers, and poll rounds issued while the words are still in
+// flight only load the memory system that the producers' stores and the weight copies go
+// through.  Measured on the benchmark: 16 (~0.43 us) each; longer or shorter was slower, a
+// sleep between rounds was slower, and delaying the other polls gave nothing.
 #ifndef QXD_SLEEP_X
 #define QXD_SLEEP_X 16
-#endif
-#ifndef QXD_SLEEP_QKV
-#define QXD_SLEEP_QKV 0
-#endif
-#ifndef QXD_SLEEP_CX
-#define QXD_SLEEP_CX 0
-#endif
-#ifndef QXD_SLEEP_LG
-#define QXD_SLEEP_LG 0
-#endif
-#ifndef QXD_SLEEP_H
-#define QXD_SLEEP_H 16
-#endif
-#ifndef QXD_SLEEP_XR
-#define QXD_SLEEP_XR 0
-#endif
-#ifndef QXD_SLEEP_HR
-#define QXD_SLEEP_HR 0
 #endif
 #ifndef QXD_SLEEP_XP
 #define QXD_SLEEP_XP 16
 #endif
-#ifndef QXD_SLEEP_HX
-#define QXD_SLEEP_HX 0
-#endif
-#ifndef QXD_SLEEP_CQ
-#define QXD_SLEEP_CQ 0
-#endif
-#ifndef QXD_SLEEP_MG
-#define QXD_SLEEP_MG 0
+#ifndef QXD_SLEEP_H
+#define QXD_SLEEP_H 16
 #endif
 #define QXD_SLEEP(n) \
     do { \
@@ -295,7 +273,7 @@ DEV void wait_pairs(u32x4 (&w)[K2]) {
 // The polling of wait_xch2 by threads T0 .. T0 + P - 1 only (the caller's branch), pair
 // p = t + P k for thread T0 + t; returns this thread's success, with no barrier.  ssq (may
 // be null) gets the sum of squares of the thread's payloads as f32 values, in double.
-template <int K2, int P = NT, int T0 = 0, int SR = 0, typename IDX>
+template <int K2, int P = NT, int T0 = 0, typename IDX>
 DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, const Ctl &c,
                     double *ssq = nullptr) {
     const int tid = tix() - T0;
@@ -323,7 +301,6 @@ DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst,
         }
         if (all) break;
         if (!keep_waiting(it, deadline, c)) { ok = false; break; }
-        QXD_SLEEP(SR);   // (between rounds)
     }
 #pragma unroll
     for (int k = 0; k < K2; ++k) {
@@ -338,9 +315,9 @@ DEV bool poll_pairs(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst,
     }
     return ok;
 }
-template <int K2, int SR = 0, typename IDX>
+template <int K2, typename IDX>
 DEV bool wait_xch2(const GLB uint64_t *base, int n, uint32_t ep, uint32_t *dst, IDX idx, DLds &S, const Ctl &c) {
-    return !block_any(!poll_pairs<K2, NT, 0, SR>(base, n, ep, dst, idx, c), S);
+    return !block_any(!poll_pairs<K2>(base, n, ep, dst, idx, c), S);
 }
 
 // Waves 4..7 only, all four calling it: each wave's earlier LDS writes are visible to the
@@ -1011,7 +988,6 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
     const float nq0 = nqp[lane], nq1 = nqp[64 + lane], nk0 = nkp[lane], nk1 = nkp[64 + lane];
     // q of heads 8 g .. 8 g + 7 (words 1024 g ..), then the K and V rows (4096 .. 5119)
     const GLB uint64_t *qkv = X + XO_QKV + par * XN_QKV;
-    QXD_SLEEP(QXD_SLEEP_CQ);
     if (!wait_xch2<2>(qkv, 2048, ep, reinterpret_cast<uint32_t *>(A.q[0]), [g](int i) { return i < 1024 ? 1024 * g + i : 3072 + i; },
                       S, ctl))
         return false;
@@ -1182,7 +1158,6 @@ DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep
     uint32_t *rw = S.u.m.vin;                                           // nch records of QXD_PREC words
     float *wt = reinterpret_cast<float *>(S.u.m.vin) + 2048;            // per chunk: (float)(exp(m_c - M) / L)
     const GLB uint64_t *src = gpw(a.xpart) + par * XN_PT + (h * 8u + dgm) * MAXCH * QXD_PREC;
-    QXD_SLEEP(QXD_SLEEP_MG);
     if (!wait_xch2<2>(src, (int)(QXD_PREC * nch), ep, rw, Ident(), S, ctl)) return false;
     DMARK(l, 25);
     if (w == 0) {   // wave 0 alone: lane c forms chunk c's factor, then lane (cg, d) sums chunks cg + 4 k
@@ -1377,7 +1352,7 @@ DEV void decode_steps(const QxDArgs &args) {
                     bool okx = true;
                     if (l > 0) {
                         QXD_SLEEP(QXD_SLEEP_X);
-                        okx = poll_pairs<2, NT, 0, QXD_SLEEP_XR>(X + XO_X + par * XN_X, 2048, ep, reinterpret_cast<uint32_t *>(S.xs), Ident(), ctl, &ssq);
+                        okx = poll_pairs<2>(X + XO_X + par * XN_X, 2048, ep, reinterpret_cast<uint32_t *>(S.xs), Ident(), ctl, &ssq);
                     } else {
 #pragma unroll
                         for (int i = 0; i < 4; ++i) ssq += (double)S.xs[4 * tid + i] * (double)S.xs[4 * tid + i];
@@ -1493,7 +1468,6 @@ DEV void decode_steps(const QxDArgs &args) {
                     if (pre) load_wq(a, ln, wq, S.wq[wave_id()]);
                 }
             } else if (wg < QXG_HEADS) {
-                QXD_SLEEP(QXD_SLEEP_QKV);
                 if (!attn_wait(a, l, ep + 1, S, ctl)) return;
                 DMARK(l, 3);
                 attention(a, l, pos, ep + 1, ap, S, last, rec ? (int)rrow : -1);
@@ -1523,7 +1497,6 @@ DEV void decode_steps(const QxDArgs &args) {
             {
                 const int tid = tix(), lane = tid & 63, wave = tid >> 6, ib = lane & 7;
                 // sentinels: words 128 h and 128 h + 64 (the two store instructions of head h)
-                QXD_SLEEP(QXD_SLEEP_CX);
                 if (!wait_xch2<4>(X + XO_CX + par * XN_CX, 4096, ep + 2, S.u.m.vin, Ident(), S, ctl))
                     return;
                 DMARK(l, 5);
@@ -1590,7 +1563,6 @@ DEV void decode_steps(const QxDArgs &args) {
                 // parallel: waves 0..3 (one per SIMD) take the top-8, issue the routed experts' row
                 // copies for themselves and waves 4..7 and wait for them; waves 4..7 poll x' and
                 // form its normalised digits.  One barrier joins them before the dots.
-                QXD_SLEEP(QXD_SLEEP_LG);
                 if (!wait_xch2<1>(X + XO_LG + par * XN_LG, 2 * (int)E, ep + 3, S.lgw, Ident(), S, ctl))
                     return;
                 DMARK(l, 7);
@@ -1752,7 +1724,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 const int tid = tix(), lane = tid & 63;
                 // h and the 8 expert weights (hi, lo words)
                 QXD_SLEEP(QXD_SLEEP_H);
-                if (!wait_xch2<7, QXD_SLEEP_HR>(X, 6144 + 16, ep + 4, S.u.m.vin,
+                if (!wait_xch2<7>(X, 6144 + 16, ep + 4, S.u.m.vin,
                                    [par](int i) { return i < 6144 ? (int)(XO_H + par * XN_H) + i : (int)(XO_WT + par * XN_WT) + i - 6144; }, S, ctl))
                     return;
                 DMARK(l, 11);
@@ -1884,7 +1856,6 @@ DEV void decode_steps(const QxDArgs &args) {
                 onw[0] = x0.x; onw[1] = x0.y; onw[2] = x0.z; onw[3] = x0.w; onw[4] = x1.x; onw[5] = x1.y; onw[6] = x1.z; onw[7] = x1.w;
             }
             DMARK(48, 0);
-            QXD_SLEEP(QXD_SLEEP_HX);
             if (!wait_xch2<2>(X + XO_X + (L & 1) * XN_X, 2048, eph, reinterpret_cast<uint32_t *>(S.xs), Ident(), S, ctl))
                 return;
             DMARK(48, 1);
