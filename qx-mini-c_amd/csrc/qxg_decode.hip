@@ -204,6 +204,7 @@ struct DLds {
     uint32_t bflag[2][NWV];      // block_any flags, two sets by call parity
     uint32_t bpar[NWV];          // block_any call parity of each wave
     uint32_t sub[4];             // upper_waves_sync flags of waves 4..7
+    uint32_t sublo[4];           // lower_waves_sync flags of waves 0..3
     uint32_t fail;               // a poll of waves 4..7 timed out (stage G)
     double ssp[4];               // x' sums of squares of waves 4..7 (stage G)
     uint32_t dne[QXG_TOPK];      // the picked experts by rank (stage G, for stage D's down rows)
@@ -332,6 +333,21 @@ DEV void upper_waves_sync(DLds &S, uint32_t tag) {
         bool all = true;
 #pragma unroll
         for (int w = 0; w < 4; ++w) all = all && __hip_atomic_load(&S.sub[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == tag;
+        if (all) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+}
+
+// The same for waves 0..3 (the other four not involved).
+DEV void lower_waves_sync(DLds &S, uint32_t tag) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    const int wave = tix() >> 6;
+    if ((tix() & 63) == 0) __hip_atomic_store(&S.sublo[wave], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (;;) {
+        bool all = true;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) all = all && __hip_atomic_load(&S.sublo[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == tag;
         if (all) break;
         __builtin_amdgcn_s_sleep(1);
     }
@@ -1301,7 +1317,7 @@ DEV void decode_steps(const QxDArgs &args) {
         for (int i = tid; i < 512; i += NT) S.g2[i] = a.T.g2[i];
         if (tid < 256) S.g3[tid] = a.T.g3[tid];
         if (tid < 128) S.sel[tid] = a.T.sel[tid];
-        if (tid < 4) S.sub[tid] = 0u;   // the tags start above 0
+        if (tid < 4) { S.sub[tid] = 0u; S.sublo[tid] = 0u; }   // the tags start above 0
         if (tid < NWV) S.bpar[tid] = 0u;
         if (tid == 0) S.fail = 0u;
     }
@@ -1563,15 +1579,18 @@ DEV void decode_steps(const QxDArgs &args) {
                 // parallel: waves 0..3 (one per SIMD) take the top-8, issue the routed experts' row
                 // copies for themselves and waves 4..7 and wait for them; waves 4..7 poll x' and
                 // form its normalised digits.  One barrier joins them before the dots.
-                if (!wait_xch2<1>(X + XO_LG + par * XN_LG, 2 * (int)E, ep + 3, S.lgw, Ident(), S, ctl))
-                    return;
-                DMARK(l, 7);
                 const uint32_t *lgw = S.lgw;
                 auto logit = [&](uint32_t e) {
                     return __longlong_as_double((long long)(((uint64_t)lgw[2 * e] << 32) | lgw[2 * e + 1]));
                 };
                 const int wv = wave_id();
                 if (wv < 4) {
+                    // the logits, polled by these four waves alone (threads 0 .. 127, a pair
+                    // each), so waves 4..7 poll x' meanwhile; a failed poll is seen after the
+                    // barrier below
+                    if (!poll_pairs<1, 256, 0>(X + XO_LG + par * XN_LG, 2 * (int)E, ep + 3, S.lgw, Ident(), ctl)) S.fail = 1u;
+                    lower_waves_sync(S, ep + 3);
+                    DMARK(l, 7);
                     const double l0 = lane < (int)E ? logit(lane) : 0.0, l1 = lane + 64 < (int)E ? logit(lane + 64) : 0.0;
                     wave_top8_ids(l0, l1, (int)E, ids);
 #pragma unroll
