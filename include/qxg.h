@@ -281,7 +281,7 @@ int qxg_decode_halves(qxg_ctx *ctx, uint32_t layers, float *attn_out, float *moe
 /* Persistent decode only (no reference counterpart): from n = position + 1 >=
  * min_positions on, stage A attends by (kv head, 64-position chunk) over every workgroup
  * and merges the chunks' partial softmax results; below it the 32 q-head workgroups walk
- * the cache themselves.  Default 481 (measured crossover of the two); 1 chunks every position,
+ * the cache themselves.  Default 577 (measured crossover of the two); 1 chunks every position,
  * 4097 never. */
 int qxg_set_attention_chunks(qxg_ctx *ctx, uint32_t min_positions);
 

@@ -193,7 +193,7 @@ struct QxDArgs {
 #define QXD_PART_WORDS (32u * 8u * (QXG_MAX_CTX / QXD_CHUNK) * QXD_PREC)
 // Default positions (n = pos + 1) from which the persistent decode attends by chunk: below
 // it the 32 q-head workgroups walk the cache themselves (no merge exchange).
-#define QXD_SPLIT_MIN_DEFAULT 481u
+#define QXD_SPLIT_MIN_DEFAULT 577u
 // exchange words per launch: x, qkv, ctx, x', router logits, h, expert weights (two slots
 // each) and the per-workgroup argmax candidates; the chunked attention's partial results
 // (two slots of QXD_PART_WORDS) have a buffer of their own

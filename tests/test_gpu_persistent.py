@@ -135,7 +135,7 @@ def test_chunked_short_positions(model, p0):
 def test_long_position_same_input(model, p0, chunks):
     """Config 3's position 2047 and the last position of the 4096 context, over seeded INT8
     caches, on the persistent path with stage A walked by the 32 q-head workgroups and
-    chunked over every workgroup (the default from 481 positions on)."""
+    chunked over every workgroup (the default from 577 positions on)."""
     m, om = model
     ctx_len = min(p0 + 2, 4096)
     c = open_ctx(m.path, chunks)
@@ -175,13 +175,13 @@ def test_generate_long_context_matches_steps(model):
         c.close()
 
 
-@pytest.mark.parametrize("p0", [0, 475], ids=["start", "across_threshold"])
+@pytest.mark.parametrize("p0", [0, 571], ids=["start", "across_threshold"])
 def test_generate_recorded_matches_steps(model, p0):
     """qxg_generate_recorded (the state loop's one launch) keeps for every step what the
     step-by-step path reads back after each qxg_decode_token: the same tokens, layer outputs,
     attention and MoE halves, routing, head sums, final norms, logits, top tokens and cache
-    rows, bit for bit (the same kernels on the same inputs).  From p0 475 the 7 steps cross the
-    chunked stage A's default threshold (481 positions), so the call runs as two launches, the
+    rows, bit for bit (the same kernels on the same inputs).  From p0 571 the 7 steps cross the
+    chunked stage A's default threshold (577 positions), so the call runs as two launches, the
     second writing its records from slot 5 on."""
     m, om = model
     c = open_ctx(m.path)
