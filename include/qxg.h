@@ -224,9 +224,10 @@ int qxg_final_head(qxg_ctx *ctx, const float *residual, float *norm_out, float *
  * (src/qx_format.c:6250-6547, sampling_step at 6253).  Chunks of 512 tokens run in
  * order; every per-layer format of the real checkpoint (IQ4_XS / Q5_K attention,
  * IQ2_XS / IQ2_S gate/up, IQ3_XXS / IQ3_S / IQ4_XS down) runs batched.  The q8_k_compat
- * mode takes those token steps on the device instead (the one-kernel-per-phase decode
- * kernels, one token at a time: the result equals qxg_decode_token over the prompt on
- * layer path 0, and the persistent path's within the decode tolerance).
+ * mode takes those token steps on the device instead: one persistent launch over the
+ * prompt where the persistent path serves the model and residual_out is NULL, else the
+ * one-kernel-per-phase decode kernels one token at a time; either way the result equals
+ * qxg_decode_token over the prompt on the same layer path.
  * residual_out (may be NULL): n*2048 floats, each token's residual after the
  * last layer.  logits / top_* as in qxg_decode_token.  elapsed_ms: device time of the
  * whole call (HIP events on the context stream). */

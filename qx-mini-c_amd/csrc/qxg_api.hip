@@ -373,8 +373,7 @@ void launch_head(qxg_ctx *c, uint32_t top_n, float *norm_dump) {
 constexpr uint64_t DECODE_WAIT_TICKS = 100000000ull;   // 1 s of the 100 MHz wall clock per wait
 
 // The persistent decode reads the weight arenas and the router fold, built for the
-// benchmark mix only, and computes in the f32 activation mode; other models and
-// q8_k_compat run one kernel per phase.
+// benchmark mix only (in either activation mode); other models run one kernel per phase.
 bool persistent(const qxg_ctx *c) {
     return c->persist && c->base_mix && c->emb && c->head && c->mfold && c->gu_il && c->dn_il && c->head_il && c->dpack;
 }
@@ -1849,7 +1848,26 @@ int qxg_prefill(qxg_ctx *c, const uint32_t *tokens, uint32_t n, uint32_t positio
     (void)hipSetDevice(c->device);
     c->kt.used = 0;
     if (!batched_prefill(c)) {
-        if (!prefill_steps(c, tokens, n, position0, run_head, residual_out, top_n, err, err_len)) return 0;
+        if (persistent(c) && c->layers && !residual_out) {
+            // the token steps in one persistent launch (the head on the last token only:
+            // n_prompt one past the steps keeps it off), then the top-N of its logits
+            if (!hip_ok(hipMemcpy(c->tokens, tokens, 4ull * n, hipMemcpyHostToDevice), err, err_len, "tokens")) return 0;
+            write_state(c, position0, 0, n, run_head ? 1u : 0u);   // (force_head: the top-N kernels run after it)
+            DecodeDumps d;
+            d.logits = run_head ? c->logits : nullptr;
+            d.norm = run_head ? c->norm : nullptr;
+            (void)hipEventRecord(c->e0, c->s);
+            if (!launch_decode(c, n, run_head ? n : n + 1, position0, false, d, err, err_len)) return 0;
+            if (run_head) {
+                hipLaunchKernelGGL(qxk_topk, dim3(TOPK_BLOCKS), dim3(256), 0, c->s, c->logits, c->vocab, top_n, c->cand_v,
+                                   c->cand_i, c->top_v, c->top_i, c->tokens, c->st);
+                hipLaunchKernelGGL(qxk_topk_merge, dim3(1), dim3(256), 0, c->s, (const float *)c->cand_v,
+                                   (const uint32_t *)c->cand_i, (uint32_t)TOPK_BLOCKS, top_n, c->top_v, c->top_i, c->tokens, c->st);
+            }
+            (void)hipEventRecord(c->e1, c->s);
+        } else if (!prefill_steps(c, tokens, n, position0, run_head, residual_out, top_n, err, err_len)) {
+            return 0;
+        }
         return prefill_finish(c, run_head, logits, top_n, top_ids, top_logits, elapsed_ms, err, err_len);
     }
     if (!prefill_ready(c, err, err_len)) return 0;

@@ -370,3 +370,28 @@ def test_q8k_nonfinite_fails_and_clears(model):
         assert np.isfinite(res).all()
     finally:
         c.close()
+
+
+def test_q8k_prefill_one_launch_matches_steps(model):
+    """q8_k_compat: qxg_prefill (the reference's token steps) runs as one persistent launch
+    when no per-token residual is asked for; its head outputs and the cache rows it leaves
+    equal the persistent decode_token steps over the same prompt, bit for bit (the same
+    kernel on the same inputs)."""
+    m, _ = model
+    c = open_ctx(m.path)
+    c.set_activation("q8_k_compat")
+    try:
+        prompt = np.array([31, 7, 2048, 900, 5], np.uint32)
+        c.kv_create(LAYERS, 16)
+        _, lg, ids, tl, _ = c.prefill(prompt, 0, True, 8, want_logits=True)
+        rows = [c.kv_read(l, 0, len(prompt)) for l in range(LAYERS)]
+        c.kv_create(LAYERS, 16)
+        for pos, t in enumerate(prompt):
+            _, _, lg2, ids2, tl2 = c.decode_token(int(t), pos, pos == len(prompt) - 1, 8, want_logits=pos == len(prompt) - 1)
+        assert np.array_equal(lg, lg2)
+        assert list(ids) == list(ids2) and np.array_equal(tl, tl2)
+        for l in range(LAYERS):
+            for a, b in zip(rows[l], c.kv_read(l, 0, len(prompt))):
+                assert np.array_equal(a, b), l
+    finally:
+        c.close()
