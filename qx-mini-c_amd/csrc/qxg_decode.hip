@@ -62,12 +62,13 @@ extern "C" int qxd_trace_read(unsigned long long *out) {
 #define DMARKT(layer, point, thread) ((void)0)
 #endif
 
-// First-round delays of three exchange polls (x in stage Q, x' in stage G, h in stage D), in
-// units of 64 cycles (s_sleep).  A workgroup reaches a poll right after storing its own
+// First-round delays of four exchange polls (x in stage Q, x' in stage G, h in stage D, the
+// chunk records of the chunked stage A's merge), in units of 64 cycles (s_sleep).  A workgroup reaches a poll right after storing its own
 // outputs, ahead of most producers, and poll rounds issued while the words are still in
 // flight only load the memory system that the producers' stores and the weight copies go
-// through.  Measured on the benchmark: 16 (~0.43 us) each; longer or shorter was slower, a
-// sleep between rounds was slower, and delaying the other polls gave nothing.
+// through.  Measured on the benchmark: 16 (~0.43 us) each and 24 for the merge; longer or
+// shorter was slower, a sleep between rounds was slower, and delaying the other polls gave
+// nothing.
 #ifndef QXD_SLEEP_X
 #define QXD_SLEEP_X 16
 #endif
@@ -76,6 +77,9 @@ extern "C" int qxd_trace_read(unsigned long long *out) {
 #endif
 #ifndef QXD_SLEEP_H
 #define QXD_SLEEP_H 16
+#endif
+#ifndef QXD_SLEEP_MG
+#define QXD_SLEEP_MG 24
 #endif
 #define QXD_SLEEP(n) \
     do { \
@@ -1174,6 +1178,7 @@ DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep
     uint32_t *rw = S.u.m.vin;                                           // nch records of QXD_PREC words
     float *wt = reinterpret_cast<float *>(S.u.m.vin) + 2048;            // per chunk: (float)(exp(m_c - M) / L)
     const GLB uint64_t *src = gpw(a.xpart) + par * XN_PT + (h * 8u + dgm) * MAXCH * QXD_PREC;
+    QXD_SLEEP(QXD_SLEEP_MG);
     if (!wait_xch2<2>(src, (int)(QXD_PREC * nch), ep, rw, Ident(), S, ctl)) return false;
     DMARK(l, 25);
     if (w == 0) {   // wave 0 alone: lane c forms chunk c's factor, then lane (cg, d) sums chunks cg + 4 k
