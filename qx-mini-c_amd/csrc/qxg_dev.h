@@ -10,14 +10,14 @@
 namespace {
 
 // ---------------------------------------------------------------- helpers
-// reference qx_fp16_to_f32 (src/qx_format.c:1854-1876): exact, exponent 31 -> +-65504
+// reference qx_fp16_to_f32 (src/qx_format.c:1854-1876): exact, exponent 31 -> +-65504.
+// The hardware conversion is exact for every finite half, subnormals included (half
+// denormals are kept in the kernels' default float mode); it yields an infinity or a NaN
+// exactly when the exponent is 31, and those take +-65504 with the sign of the input bits
+// (not of the converted NaN, whose sign the conversion need not keep).
 DEV float fp16_exact(uint32_t h) {
-    const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu;
-    const float sub = (float)m * 5.9604644775390625e-08f;   // subnormal: m * 2^-24 (exact)
-    float v = __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
-    v = e == 0 ? __uint_as_float(sign | __float_as_uint(sub)) : v;
-    v = e == 31 ? __uint_as_float(sign | 0x477fe000u) : v;   // selects, no branches
-    return v;
+    const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    return __builtin_isfinite(v) ? v : copysignf(65504.0f, __uint_as_float(h << 16));
 }
 
 // the wave's index in its workgroup, in a scalar register (the divergence analysis
@@ -40,6 +40,15 @@ DEV uint2 ldw2(const void *p) {
 DEV uint32_t ldw1(const void *p) { return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p)); }
 
 DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+// a . b with a zero accumulator, the first of a chain: the three-operand form takes the 0
+// inline, where the accumulating form the compiler picks needs a register copy of 0 first.
+// sdot4s: the chain's first link when z (a constant at each unrolled call site), else sdot4.
+DEV int sdot4z(uint32_t a, uint32_t b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+DEV int sdot4s(uint32_t a, uint32_t b, int c, bool z) { return z ? sdot4z(a, b) : sdot4(a, b, c); }
 DEV uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
 
 // ---- DPP lane exchanges (VALU latency; __shfl_xor lowers to ds_bpermute through LDS).
@@ -130,10 +139,10 @@ DEV float dot_iq4(uint4 qs, uint2 meta, int ib, const Dig &g) {
     for (int k = 0; k < 4; ++k) {
         const uint32_t wlo = kv_lookup(q[k] & 0x0f0f0f0fu);
         const uint32_t whi = kv_lookup((q[k] >> 4) & 0x0f0f0f0fu);
-        aH = sdot4(wlo, g.h[k], aH); aH = sdot4(whi, g.h[4 + k], aH);
+        aH = sdot4s(wlo, g.h[k], aH, k == 0); aH = sdot4(whi, g.h[4 + k], aH);
         if constexpr (!H1) {
-            aM = sdot4(wlo, g.m[k], aM); aM = sdot4(whi, g.m[4 + k], aM);
-            aL = sdot4(wlo, g.l[k], aL); aL = sdot4(whi, g.l[4 + k], aL);
+            aM = sdot4s(wlo, g.m[k], aM, k == 0); aM = sdot4(whi, g.m[4 + k], aM);
+            aL = sdot4s(wlo, g.l[k], aL, k == 0); aL = sdot4(whi, g.l[4 + k], aL);
         }
     }
     const float dl = fp16_exact(meta.x & 0xffffu) * (float)(ls - 32);
@@ -163,16 +172,16 @@ DEV float iq2_dot(const Iq2Look &k, uint32_t sc, uint32_t d16, const Dig &g) {
     for (int l = 0; l < 4; ++l) {
         const uint32_t w0 = perm(k.gg[l].z, k.gg[l].x, k.sl[l].x), w1 = perm(k.gg[l].w, k.gg[l].y, k.sl[l].y);
         if (l < 2) {
-            h0 = sdot4(w0, g.h[2 * l], h0); h0 = sdot4(w1, g.h[2 * l + 1], h0);
+            h0 = sdot4s(w0, g.h[2 * l], h0, l == 0); h0 = sdot4(w1, g.h[2 * l + 1], h0);
             if constexpr (!H1) {
-                m0 = sdot4(w0, g.m[2 * l], m0); m0 = sdot4(w1, g.m[2 * l + 1], m0);
-                l0 = sdot4(w0, g.l[2 * l], l0); l0 = sdot4(w1, g.l[2 * l + 1], l0);
+                m0 = sdot4s(w0, g.m[2 * l], m0, l == 0); m0 = sdot4(w1, g.m[2 * l + 1], m0);
+                l0 = sdot4s(w0, g.l[2 * l], l0, l == 0); l0 = sdot4(w1, g.l[2 * l + 1], l0);
             }
         } else {
-            h1 = sdot4(w0, g.h[2 * l], h1); h1 = sdot4(w1, g.h[2 * l + 1], h1);
+            h1 = sdot4s(w0, g.h[2 * l], h1, l == 2); h1 = sdot4(w1, g.h[2 * l + 1], h1);
             if constexpr (!H1) {
-                m1 = sdot4(w0, g.m[2 * l], m1); m1 = sdot4(w1, g.m[2 * l + 1], m1);
-                l1 = sdot4(w0, g.l[2 * l], l1); l1 = sdot4(w1, g.l[2 * l + 1], l1);
+                m1 = sdot4s(w0, g.m[2 * l], m1, l == 2); m1 = sdot4(w1, g.m[2 * l + 1], m1);
+                l1 = sdot4s(w0, g.l[2 * l], l1, l == 2); l1 = sdot4(w1, g.l[2 * l + 1], l1);
             }
         }
     }
@@ -207,10 +216,10 @@ DEV float iq3_dot(const Iq3Look &k, uint32_t aux, uint32_t d16, const Dig &g) {
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
         const uint32_t w0 = perm(k.g[2 * l].y, k.g[2 * l].x, k.sl[l].x), w1 = perm(k.g[2 * l + 1].y, k.g[2 * l + 1].x, k.sl[l].y);
-        aH = sdot4(w0, g.h[2 * l], aH); aH = sdot4(w1, g.h[2 * l + 1], aH);
+        aH = sdot4s(w0, g.h[2 * l], aH, l == 0); aH = sdot4(w1, g.h[2 * l + 1], aH);
         if constexpr (!H1) {
-            aM = sdot4(w0, g.m[2 * l], aM); aM = sdot4(w1, g.m[2 * l + 1], aM);
-            aL = sdot4(w0, g.l[2 * l], aL); aL = sdot4(w1, g.l[2 * l + 1], aL);
+            aM = sdot4s(w0, g.m[2 * l], aM, l == 0); aM = sdot4(w1, g.m[2 * l + 1], aM);
+            aL = sdot4s(w0, g.l[2 * l], aL, l == 0); aL = sdot4(w1, g.l[2 * l + 1], aL);
         }
     }
     const int k3 = 2 * (int)(aux >> 28) + 1;
