@@ -866,9 +866,9 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
         int aH = 0, aM = 0, aL = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            aH = sdot4(kw[i], d.h[i], aH);
-            aM = sdot4(kw[i], d.m[i], aM);
-            aL = sdot4(kw[i], d.l[i], aL);
+            aH = sdot4s(kw[i], d.h[i], aH, i == 0);
+            aM = sdot4s(kw[i], d.m[i], aM, i == 0);
+            aL = sdot4s(kw[i], d.l[i], aL, i == 0);
         }
         double sq = (double)(combine(aH, aM, aL) * d.s);
         sq += dppd<DPP_XOR1>(sq);
@@ -1096,9 +1096,9 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
         int aH = 0, aM = 0, aL = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            aH = sdot4(kw[k], d.h[k], aH);
-            aM = sdot4(kw[k], d.m[k], aM);
-            aL = sdot4(kw[k], d.l[k], aL);
+            aH = sdot4s(kw[k], d.h[k], aH, k == 0);
+            aM = sdot4s(kw[k], d.m[k], aM, k == 0);
+            aL = sdot4s(kw[k], d.l[k], aL, k == 0);
         }
         double sq = (double)(combine(aH, aM, aL) * d.s);
         sq += dppd<DPP_XOR1>(sq);

@@ -107,7 +107,15 @@ struct Dig {
 // (< 2^18) are in range.
 DEV int mul24(int a, int b) { return __mul24(a, b); }
 
+// aH * 65536 + aM * 256 + aL in f32 for digit-plane sums below 2^24 in magnitude.  The
+// m and l sums join in integer first: every caller but dot_q6 bounds |aM * 256 + aL|
+// below 2^31 (the largest, IQ3_XXS: 32 values x 62 x 128 x 31 x 256 + the l sum, about
+// 2.02e9), so the join is exact and its one rounding to f32 is that of the fma
+// fmaf(aM, 256, aL).  combine_wide converts each sum (dot_q6's scaled segments reach 2^24).
 DEV float combine(int aH, int aM, int aL) {
+    return fmaf((float)aH, 65536.0f, (float)(aM * 256 + aL));
+}
+DEV float combine_wide(int aH, int aM, int aL) {
     return fmaf((float)aH, 65536.0f, fmaf((float)aM, 256.0f, (float)aL));
 }
 
@@ -245,13 +253,13 @@ DEV float dot_iq2s(uint32_t qs4, uint32_t sg4, uint32_t qh, uint32_t sc, uint32_
         const uint2 sl = SEL8[(sg4 >> (8 * l)) & 255u];
         const uint32_t w0 = perm(gg.z, gg.x, sl.x), w1 = perm(gg.w, gg.y, sl.y);
         if (l < 2) {
-            h0 = sdot4(w0, g.h[2 * l], h0); h0 = sdot4(w1, g.h[2 * l + 1], h0);
-            m0 = sdot4(w0, g.m[2 * l], m0); m0 = sdot4(w1, g.m[2 * l + 1], m0);
-            l0 = sdot4(w0, g.l[2 * l], l0); l0 = sdot4(w1, g.l[2 * l + 1], l0);
+            h0 = sdot4s(w0, g.h[2 * l], h0, l == 0); h0 = sdot4(w1, g.h[2 * l + 1], h0);
+            m0 = sdot4s(w0, g.m[2 * l], m0, l == 0); m0 = sdot4(w1, g.m[2 * l + 1], m0);
+            l0 = sdot4s(w0, g.l[2 * l], l0, l == 0); l0 = sdot4(w1, g.l[2 * l + 1], l0);
         } else {
-            h1 = sdot4(w0, g.h[2 * l], h1); h1 = sdot4(w1, g.h[2 * l + 1], h1);
-            m1 = sdot4(w0, g.m[2 * l], m1); m1 = sdot4(w1, g.m[2 * l + 1], m1);
-            l1 = sdot4(w0, g.l[2 * l], l1); l1 = sdot4(w1, g.l[2 * l + 1], l1);
+            h1 = sdot4s(w0, g.h[2 * l], h1, l == 2); h1 = sdot4(w1, g.h[2 * l + 1], h1);
+            m1 = sdot4s(w0, g.m[2 * l], m1, l == 2); m1 = sdot4(w1, g.m[2 * l + 1], m1);
+            l1 = sdot4s(w0, g.l[2 * l], l1, l == 2); l1 = sdot4(w1, g.l[2 * l + 1], l1);
         }
     }
     const int k0 = 2 * (int)(sc & 15u) + 1, k1 = 2 * (int)((sc >> 4) & 15u) + 1;
@@ -273,9 +281,9 @@ DEV float dot_iq3s(uint2 qs8, uint32_t sg4, uint32_t qh, uint32_t sc, uint32_t d
         const uint2 g1 = G3S[b1], g2 = G3S[b2];
         const uint2 sl = SEL8[(sg4 >> (8 * l)) & 255u];
         const uint32_t w0 = perm(g1.y, g1.x, sl.x), w1 = perm(g2.y, g2.x, sl.y);
-        aH = sdot4(w0, g.h[2 * l], aH); aH = sdot4(w1, g.h[2 * l + 1], aH);
-        aM = sdot4(w0, g.m[2 * l], aM); aM = sdot4(w1, g.m[2 * l + 1], aM);
-        aL = sdot4(w0, g.l[2 * l], aL); aL = sdot4(w1, g.l[2 * l + 1], aL);
+        aH = sdot4s(w0, g.h[2 * l], aH, l == 0); aH = sdot4(w1, g.h[2 * l + 1], aH);
+        aM = sdot4s(w0, g.m[2 * l], aM, l == 0); aM = sdot4(w1, g.m[2 * l + 1], aM);
+        aL = sdot4s(w0, g.l[2 * l], aL, l == 0); aL = sdot4(w1, g.l[2 * l + 1], aL);
     }
     const int k = 2 * (int)(sc & 15u) + 1;
     return (fp16_exact(d16) * g.s) * combine(mul24(k, aH), mul24(k, aM), mul24(k, aL));
@@ -295,8 +303,9 @@ DEV float dot_q5(uint4 qa, uint4 qb, uint4 ha, uint4 hb, uint4 meta, int ib, con
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const uint32_t c = ((q[k] >> nsh) & 0x0f0f0f0fu) | (((hq[k] >> ib) & 0x01010101u) << 4);
-        aH = sdot4(c, g.h[k], aH); aM = sdot4(c, g.m[k], aM); aL = sdot4(c, g.l[k], aL);
-        sH = sdot4(0x01010101u, g.h[k], sH); sM = sdot4(0x01010101u, g.m[k], sM); sL = sdot4(0x01010101u, g.l[k], sL);
+        aH = sdot4s(c, g.h[k], aH, k == 0); aM = sdot4s(c, g.m[k], aM, k == 0); aL = sdot4s(c, g.l[k], aL, k == 0);
+        sH = sdot4s(0x01010101u, g.h[k], sH, k == 0); sM = sdot4s(0x01010101u, g.m[k], sM, k == 0);
+        sL = sdot4s(0x01010101u, g.l[k], sL, k == 0);
     }
     const uint32_t s[3] = {meta.y, meta.z, meta.w};   // scales bytes 0..11
     auto byte = [&](int i) -> uint32_t { return (s[i >> 2] >> (8 * (i & 3))) & 255u; };
@@ -346,8 +355,8 @@ DEV float dot_q6(uint4 ql0, uint4 ql1, uint4 qh0, uint4 qh1, int sc0, int sc1, u
             aL[s] = sdot4(u, g.l[j], aL[s]);
         }
     }
-    const float v = combine(mul24(sc0, aH[0]) + mul24(sc1, aH[1]), mul24(sc0, aM[0]) + mul24(sc1, aM[1]),
-                            mul24(sc0, aL[0]) + mul24(sc1, aL[1]));
+    const float v = combine_wide(mul24(sc0, aH[0]) + mul24(sc1, aH[1]), mul24(sc0, aM[0]) + mul24(sc1, aM[1]),
+                                 mul24(sc0, aL[0]) + mul24(sc1, aL[1]));
     return (fp16_exact(d16) * g.s) * v;
 }
 
@@ -767,9 +776,9 @@ DEV double attn_scores(const float *s_q, uint32_t *s_qd, uint32_t n, double sqrt
         int aH = 0, aM = 0, aL = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            aH = sdot4(kw[i], d.h[i], aH);
-            aM = sdot4(kw[i], d.m[i], aM);
-            aL = sdot4(kw[i], d.l[i], aL);
+            aH = sdot4s(kw[i], d.h[i], aH, i == 0);
+            aM = sdot4s(kw[i], d.m[i], aM, i == 0);
+            aL = sdot4s(kw[i], d.l[i], aL, i == 0);
         }
         double acc = (double)(combine(aH, aM, aL) * d.s);
         acc += dppd<DPP_XOR1>(acc);   // the quad shares t, so its lanes are active together
