@@ -631,10 +631,21 @@ DEV bool prompt_step(const DevState *st) {
     return (fh == 0u) & (step + 1u < np);
 }
 
+// The sum of v over the wave's four 16-lane rows, in every lane: v_permlane32_swap
+// exchanges the upper half of one register with the lower half of another (each lane then
+// adds the value 32 lanes away), v_permlane16_swap the odd rows with the even ones.  Every
+// lane forms the same two sums in the same order, so the result is uniform.
+DEV float rows4_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), true, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), true, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // R per-lane partial sums (one per row, R in {1,2,4,8}) reduced over the wave:
 // up to two split rounds inside each quad (a lane keeps half of the rows and adds
-// its partner's half), then row16 sums, then the four rows of the wave through
-// readlane.  out[r] is the total of row r, wave-uniform.
+// its partner's half), then row16 sums, then the four 16-lane rows (rows4_sum) and
+// one readlane per row.  out[r] is the total of row r, wave-uniform.
 template <int R>
 DEV void rows_reduce(float (&v)[R], float (&out)[R], int lane) {
     constexpr int S = R >= 4 ? 2 : (R == 2 ? 1 : 0);   // quad split rounds
@@ -664,6 +675,7 @@ DEV void rows_reduce(float (&v)[R], float (&out)[R], int lane) {
         if constexpr (S <= 1) { v[i] += dppf<DPP_XOR2>(v[i]); }
         v[i] += dppf<DPP_ROR4>(v[i]);
         v[i] += dppf<DPP_ROR8>(v[i]);
+        v[i] = rows4_sum(v[i]);
     }
     // lane L (low bits b0,b1) holds rows base..base+K-1 with base = K*(2^(S-1)*b0 + ...)
 #pragma unroll
@@ -675,7 +687,7 @@ DEV void rows_reduce(float (&v)[R], float (&out)[R], int lane) {
         float t = 0.0f;
 #pragma unroll
         for (int i = 0; i < K; ++i) if (i == j) t = v[i];
-        out[r] = (rdlanef(t, l0) + rdlanef(t, l0 + 16)) + (rdlanef(t, l0 + 32) + rdlanef(t, l0 + 48));
+        out[r] = rdlanef(t, l0);
     }
 }
 
