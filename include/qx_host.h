@@ -96,7 +96,11 @@ typedef struct qxgen_spec {
                                compound stress pattern - as 1, plus x1e6 in channel 1001 of the
                                attention and output norms and fp16 d x1000 in gate row 7 and down
                                row 13 of every expert (h groups spanning ~1e4-1e5, and expert
-                               outputs that cancel in channel 13) */
+                               outputs that cancel in channel 13).  3: exponent-31 fp16 block
+                               scales (+inf, -inf, NaN, -NaN by block, which the reference reads
+                               as +-65504) in every block of Q row 100, K row 7, V row 3, O row 11
+                               and gate row 7, up row 9, down row 13 of every expert; no norm
+                               outliers */
 } qxgen_spec;
 
 /* Writes a QXF1 file at `path` (truncating).  The bytes are a pure function of

@@ -588,7 +588,7 @@ DEV void gu_dots(const uint8_t *ub, uint32_t q, uint32_t sc, uint32_t d, const D
     for (int s2 = 0; s2 < NS; ++s2) {
         if (s2 + 2 < NS) ld(s2 + 2);
         if (s2 + 1 < NS) iq2_look(qs[(s2 + 1) % 3], S.g2, S.sel, kl[(s2 + 1) & 1]);
-        p[(s2 & 1) ? 4 + (s2 >> 1) : (s2 >> 1)] = iq2_dot<H1>(kl[s2 & 1], scs[s2 % 3], ds[s2 % 3], g);
+        p[(s2 & 1) ? 4 + (s2 >> 1) : (s2 >> 1)] = iq2_dot<H1, true>(kl[s2 & 1], scs[s2 % 3], ds[s2 % 3], g);
     }
 #pragma unroll
     for (int k = NU; k < 4; ++k) p[k] = p[4 + k] = 0.0f;
@@ -1450,9 +1450,9 @@ DEV void decode_steps(const QxDArgs &args) {
                     float part[4], out[4];
                     {
                         const uint4(*lq)[64] = S.wq[wave_id()];
-                        part[0] = dot_iq4<Q8>(lq[0][lane], wq.m[0], ib, g);
-                        part[1] = dot_iq4<Q8>(lq[1][lane], wq.m[1], ib, g);
-                        part[2] = dot_iq4<Q8>(lq[2][lane], wq.m[2], ib, g);
+                        part[0] = dot_iq4<Q8, true>(lq[0][lane], wq.m[0], ib, g);
+                        part[1] = dot_iq4<Q8, true>(lq[1][lane], wq.m[1], ib, g);
+                        part[2] = dot_iq4<Q8, true>(lq[2][lane], wq.m[2], ib, g);
                     }
                     part[3] = 0.0f;
                     rows_reduce<4>(part, out, lane);
@@ -1561,7 +1561,7 @@ DEV void decode_steps(const QxDArgs &args) {
                 float part[1], out[1];
                 {
                     const uint4(*lo)[64] = S.wo[wave_id()];
-                    part[0] = dot_iq4<Q8>(lo[0][lane], wo.m0, ib, g0) + dot_iq4<Q8>(lo[1][lane], wo.m1, ib, g1);
+                    part[0] = dot_iq4<Q8, true>(lo[0][lane], wo.m0, ib, g0) + dot_iq4<Q8, true>(lo[1][lane], wo.m1, ib, g1);
                 }
                 rows_reduce<1>(part, out, lane);
                 const int r = 8 * wg + wave;
@@ -1839,7 +1839,7 @@ DEV void decode_steps(const QxDArgs &args) {
                             iq3_look(qs[b + 1], aux[b + 1], S.g3, S.sel, kl[(b + 1) & 1]);
                             load_dig(S.dig, 24 * wv + 8 * (b + 1) + k, gd[(b + 1) & 1]);
                         }
-                        part += iq3_dot<Q8>(kl[b & 1], aux[b], ds[b], gd[b & 1]);
+                        part += iq3_dot<Q8, true>(kl[b & 1], aux[b], ds[b], gd[b & 1]);
                     }
                 }
                 part += dppf<DPP_XOR1>(part);
@@ -1954,7 +1954,8 @@ extern "C" __global__ __launch_bounds__(NT, 1) void qxk_decode_chunked_q8(QxDArg
 // The routed experts' rows of one layer in the interleaved layout (QXD_GU_UNIT, QXD_DN_ROW),
 // from the IQ2_XS gate/up planes (qs 64, sc 8, d 2 bytes per block, 8 blocks per row) and
 // the IQ3_XXS down planes (qs 64, aux 32, d 2 per block, 3 blocks per row): one thread per
-// gate/up unit or down row.
+// gate/up unit or down row.  The block scales d are stored saturated (fp16_sat), so the
+// decode's dots convert them with the plain hardware conversion.
 extern "C" __global__ __launch_bounds__(256) void qxk_interleave_experts(const uint8_t *gq, const uint8_t *gs, const uint8_t *gd,
                                                                           const uint8_t *uq, const uint8_t *us, const uint8_t *ud,
                                                                           const uint8_t *dq, const uint8_t *dx, const uint8_t *dd,
@@ -1963,14 +1964,18 @@ extern "C" __global__ __launch_bounds__(256) void qxk_interleave_experts(const u
     auto cp32 = [](uint8_t *dst, const uint8_t *src, int words) {
         for (int i = 0; i < words; ++i) reinterpret_cast<uint32_t *>(dst)[i] = reinterpret_cast<const uint32_t *>(src)[i];
     };
+    auto cp_d16 = [](uint8_t *dst, const uint8_t *src, int n) {   // block scales, saturated
+        for (int i = 0; i < n; ++i)
+            reinterpret_cast<uint16_t *>(dst)[i] = (uint16_t)fp16_sat(reinterpret_cast<const uint16_t *>(src)[i]);
+    };
     if (t < ngu) {
         uint8_t *o = gu + t * QXD_GU_UNIT;
         cp32(o, gq + t * 512, 128);
         cp32(o + 512, gs + t * 64, 16);
-        cp32(o + 576, gd + t * 16, 4);
+        cp_d16(o + 576, gd + t * 16, 8);
         cp32(o + 592, uq + t * 512, 128);
         cp32(o + 1104, us + t * 64, 16);
-        cp32(o + 1168, ud + t * 16, 4);
+        cp_d16(o + 1168, ud + t * 16, 8);
     } else if (t < ngu + ndn) {
         const uint64_t r = t - ngu, e = r / 2048, row = r % 2048;   // source: row-major per expert
         uint8_t *o = dn + (((row >> 3) * E + e) * 8 + (row & 7)) * QXD_DN_ROW;
@@ -1978,7 +1983,7 @@ extern "C" __global__ __launch_bounds__(256) void qxk_interleave_experts(const u
         cp32(o + 192, dx + r * 96, 24);
         uint16_t *o16 = reinterpret_cast<uint16_t *>(o + 288);
         const uint16_t *d16 = reinterpret_cast<const uint16_t *>(dd + r * 6);
-        for (int i = 0; i < 8; ++i) o16[i] = i < 3 ? d16[i] : (uint16_t)0;
+        for (int i = 0; i < 8; ++i) o16[i] = i < 3 ? (uint16_t)fp16_sat(d16[i]) : (uint16_t)0;
     }
 }
 
@@ -2015,7 +2020,8 @@ extern "C" __global__ __launch_bounds__(256) void qxk_interleave_head(const uint
 // The decode packs of one layer (QXD_PK_*): workgroup w of the grid (256) copies pack w:
 // for w >= 32 its 24 Q/K/V row slots (stacked rows [Q 4096 | K 512 | V 512] 24 (w - 32) ..,
 // zero past row 5119) with their 8-byte block metas; for every w its O rows 8 w .. 8 w + 7
-// and metas; for w < experts the router row and router-fold row of expert w.
+// and metas; for w < experts the router row and router-fold row of expert w.  The metas'
+// scale halves are stored saturated (fp16_sat), as are the expert layouts' below.
 extern "C" __global__ __launch_bounds__(256) void qxk_pack_decode(const uint8_t *qq, const uint8_t *qm, const uint8_t *kq,
                                                                    const uint8_t *km, const uint8_t *vq, const uint8_t *vm,
                                                                    const uint8_t *oq, const uint8_t *om, const float *router,
@@ -2025,6 +2031,12 @@ extern "C" __global__ __launch_bounds__(256) void qxk_pack_decode(const uint8_t 
     auto cp = [](uint8_t *dst, const uint8_t *src, uint32_t bytes) {
         for (uint32_t i = threadIdx.x; i < bytes / 16; i += 256)
             reinterpret_cast<uint4 *>(dst)[i] = reinterpret_cast<const uint4 *>(src)[i];
+    };
+    // two IQ4_XS block metas {d | scales_h << 16, scales_l}, their scale halves saturated
+    auto sat_meta = [](uint4 m) {
+        m.x = (m.x & 0xffff0000u) | fp16_sat(m.x & 0xffffu);
+        m.z = (m.z & 0xffff0000u) | fp16_sat(m.z & 0xffffu);
+        return m;
     };
     // one Q/K/V row slot: 1024 qs bytes (64 chunks) or 64 meta bytes (4 chunks) of row `row`
     auto slot = [&](uint32_t s, bool meta) -> const uint4 * {
@@ -2043,11 +2055,12 @@ extern "C" __global__ __launch_bounds__(256) void qxk_pack_decode(const uint8_t 
         }
         for (uint32_t i = threadIdx.x; i < 24u * 4u; i += 256) {
             const uint4 *src = slot(i / 4u, true);
-            reinterpret_cast<uint4 *>(o + QXD_PK_QM)[i] = src ? src[i % 4u] : make_uint4(0u, 0u, 0u, 0u);
+            reinterpret_cast<uint4 *>(o + QXD_PK_QM)[i] = src ? sat_meta(src[i % 4u]) : make_uint4(0u, 0u, 0u, 0u);
         }
     }
     cp(o + QXD_PK_OQ, oq + (uint64_t)w * 8 * 2048, 16384);
-    cp(o + QXD_PK_OM, om + (uint64_t)w * 8 * 128, 1024);
+    for (uint32_t i = threadIdx.x; i < 1024u / 16u; i += 256)
+        reinterpret_cast<uint4 *>(o + QXD_PK_OM)[i] = sat_meta(reinterpret_cast<const uint4 *>(om + (uint64_t)w * 8 * 128)[i]);
     if (w < experts) {   // (workgroups past the experts read pack experts - 1's)
         cp(o + QXD_PK_RT, reinterpret_cast<const uint8_t *>(router + (uint64_t)w * 2048), 8192);
         cp(o + QXD_PK_MF, reinterpret_cast<const uint8_t *>(mfold + (uint64_t)w * 4096), 16384);

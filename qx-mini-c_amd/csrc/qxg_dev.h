@@ -19,6 +19,17 @@ DEV float fp16_exact(uint32_t h) {
     const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
     return __builtin_isfinite(v) ? v : copysignf(65504.0f, __uint_as_float(h << 16));
 }
+// A half with exponent 31 replaced by +-65504 (0x7bff with its sign), so the plain hardware
+// conversion of the result equals fp16_exact of the input for every bit pattern.  The
+// persistent decode's row layouts hold their block scales this way (fp16_d<true>).
+DEV uint32_t fp16_sat(uint32_t h) {
+    return (h & 0x7c00u) == 0x7c00u ? (h & 0x8000u) | 0x7bffu : h;
+}
+template <bool SAT>
+DEV float fp16_d(uint32_t h) {
+    if constexpr (SAT) return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    else return fp16_exact(h);
+}
 
 // the wave's index in its workgroup, in a scalar register (the divergence analysis
 // does not know that threadIdx.x / 64 is the same in every lane of a wave)
@@ -137,7 +148,8 @@ DEV uint32_t kv_lookup(uint32_t n) {
 // ---------------------------------------------------------------- per-format sub-block dots
 // IQ4_XS sub-block ib (32 values): codes kvalue[nibble], scale d*(ls-32)
 // H1 (q8_k_compat activations): the m and l planes are zero, their dots are skipped.
-template <bool H1 = false>
+// SAT: the scale half is stored saturated (fp16_sat), as in the persistent decode's packs.
+template <bool H1 = false, bool SAT = false>
 DEV float dot_iq4(uint4 qs, uint2 meta, int ib, const Dig &g) {
     const uint32_t sh = meta.x >> 16, sl = meta.y;
     const int ls = ((sl >> (8 * (ib >> 1) + 4 * (ib & 1))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
@@ -153,7 +165,7 @@ DEV float dot_iq4(uint4 qs, uint2 meta, int ib, const Dig &g) {
             aL = sdot4s(wlo, g.l[k], aL, k == 0); aL = sdot4(whi, g.l[4 + k], aL);
         }
     }
-    const float dl = fp16_exact(meta.x & 0xffffu) * (float)(ls - 32);
+    const float dl = fp16_d<SAT>(meta.x & 0xffffu) * (float)(ls - 32);
     return (dl * g.s) * combine(aH, aM, aL);
 }
 
@@ -173,7 +185,7 @@ DEV void iq2_look(uint2 qs, const uint4 *G2, const uint2 *SEL, Iq2Look &k) {
         k.sl[l] = SEL[qv[l] >> 9];
     }
 }
-template <bool H1 = false>
+template <bool H1 = false, bool SAT = false>
 DEV float iq2_dot(const Iq2Look &k, uint32_t sc, uint32_t d16, const Dig &g) {
     int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
 #pragma unroll
@@ -195,7 +207,7 @@ DEV float iq2_dot(const Iq2Look &k, uint32_t sc, uint32_t d16, const Dig &g) {
     }
     const int k0 = 2 * (int)(sc & 15u) + 1, k1 = 2 * (int)(sc >> 4) + 1;
     const float v = combine(mul24(k0, h0) + mul24(k1, h1), mul24(k0, m0) + mul24(k1, m1), mul24(k0, l0) + mul24(k1, l1));
-    return ((fp16_exact(d16) * 0.125f) * g.s) * v;
+    return ((fp16_d<SAT>(d16) * 0.125f) * g.s) * v;
 }
 DEV float dot_iq2(uint2 qs, uint32_t sc, uint32_t d16, const Dig &g, const uint4 *G2, const uint2 *SEL) {
     Iq2Look k;
@@ -218,7 +230,7 @@ DEV void iq3_look(uint2 qs, uint32_t aux, const uint2 *G3, const uint2 *SEL, Iq3
         k.sl[l] = SEL[(aux >> (7 * l)) & 127u];
     }
 }
-template <bool H1 = false>
+template <bool H1 = false, bool SAT = false>
 DEV float iq3_dot(const Iq3Look &k, uint32_t aux, uint32_t d16, const Dig &g) {
     int aH = 0, aM = 0, aL = 0;
 #pragma unroll
@@ -231,7 +243,7 @@ DEV float iq3_dot(const Iq3Look &k, uint32_t aux, uint32_t d16, const Dig &g) {
         }
     }
     const int k3 = 2 * (int)(aux >> 28) + 1;
-    return ((fp16_exact(d16) * 0.25f) * g.s) * combine(mul24(k3, aH), mul24(k3, aM), mul24(k3, aL));
+    return ((fp16_d<SAT>(d16) * 0.25f) * g.s) * combine(mul24(k3, aH), mul24(k3, aM), mul24(k3, aL));
 }
 DEV float dot_iq3(uint2 qs, uint32_t aux, uint32_t d16, const Dig &g, const uint2 *G3, const uint2 *SEL) {
     Iq3Look k;

@@ -93,13 +93,21 @@ typedef struct gen_tensor {
        their fp16 d range x1000 (0: none), bpr blocks per row */
     uint32_t out_norm;
     uint64_t out_rows, out_row, bpr;
+    /* spec->outliers 3: the marked row's blocks get an exponent-31 fp16 d instead of x1000 */
+    uint32_t sat;
 } gen_tensor;
+
+static int in_marked_row(const gen_tensor *t, uint64_t blk) {
+    return t->out_rows && (blk / t->bpr) % t->out_rows == t->out_row;
+}
 
 /* fp16 d range factor of block blk: x1000 in a planted outlier row */
 static double d_scale(const gen_tensor *t, uint64_t blk) {
-    if (!t->out_rows) return 1.0;
-    return (blk / t->bpr) % t->out_rows == t->out_row ? 1000.0 : 1.0;
+    return !t->sat && in_marked_row(t, blk) ? 1000.0 : 1.0;
 }
+
+/* exponent-31 halves (+inf, -inf, NaN, NaN with the sign bit), taken in turn by block */
+static const uint16_t SAT_D[4] = {0x7c00u, 0xfc00u, 0x7e00u, 0xfe01u};
 
 /* one 256-value block (or 256 floats for F32) */
 static void gen_block(const gen_tensor *t, uint64_t blk, uint8_t *out, uint64_t nbytes) {
@@ -163,6 +171,9 @@ static void gen_block(const gen_tensor *t, uint64_t blk, uint8_t *out, uint64_t 
     default:
         memset(out, 0, nbytes);
     }
+    /* every quantized type but Q4_K / Q6_K leads with its fp16 d */
+    if (t->sat && in_marked_row(t, blk) && t->type != QXT_F32 && t->type != QXT_Q4_K && t->type != QXT_Q6_K)
+        put16(out, SAT_D[blk % 4]);
 }
 
 typedef struct gen_job {
@@ -233,11 +244,15 @@ static void mark_rows(gen_tensor *t, uint64_t rows, uint64_t row) {
     t->out_row = row;
     t->bpr = t->dims[0] / 256;
 }
+static void mark_sat(gen_tensor *t, uint64_t rows, uint64_t row) {
+    mark_rows(t, rows, row);
+    t->sat = 1;
+}
 
 static uint32_t build_tensor_list(const qxgen_spec *sp, gen_tensor *v) {
     uint32_t n = 0;
     char nm[QXF_NAME_MAX];
-    const int ol = sp->outliers != 0, ol2 = sp->outliers == 2;
+    const int ol = sp->outliers == 1 || sp->outliers == 2, ol2 = sp->outliers == 2, sat = sp->outliers == 3;
     const uint64_t H = 2048, V = sp->vocab, E = sp->experts, F = 768;
     if (sp->with_embedding) add_tensor(v, &n, "token_embd.weight", QXT_Q4_K, 2, H, V, 0, 0, sp->seed);
     if (sp->with_head) {
@@ -250,15 +265,19 @@ static uint32_t build_tensor_list(const qxgen_spec *sp, gen_tensor *v) {
         T("attn_norm.weight", QXT_F32, 1, H, 0, 0, DIST_NORM_W);
         if (ol) mark_norm(&v[n - 1], ol2 ? 2 : 1);
         T("attn_q.weight", QXT_IQ4_XS, 2, H, 4096, 0, 0);
+        if (sat) mark_sat(&v[n - 1], 4096, 100);
         T("attn_k.weight", QXT_IQ4_XS, 2, H, 512, 0, 0);
+        if (sat) mark_sat(&v[n - 1], 512, 7);
         const uint32_t k4 = sp->mix ? l % 4 : 0;
         const uint32_t t_vo = (k4 == 1 || k4 == 3) ? QXT_Q5_K : QXT_IQ4_XS;
         const uint32_t t_gu = (k4 == 1 || k4 == 3) ? QXT_IQ2_S : QXT_IQ2_XS;
         const uint32_t t_dn = k4 == 0 ? QXT_IQ3_XXS : k4 == 1 ? QXT_IQ4_XS : QXT_IQ3_S;
         T("attn_v.weight", t_vo, 2, H, 512, 0, 0);
         if (ol) mark_rows(&v[n - 1], 128, 3);
+        if (sat) mark_sat(&v[n - 1], 512, 3);
         T("attn_output.weight", t_vo, 2, 4096, H, 0, 0);
         if (ol) mark_rows(&v[n - 1], H, 11);
+        if (sat) mark_sat(&v[n - 1], H, 11);
         T("attn_q_norm.weight", QXT_F32, 1, 128, 0, 0, DIST_NORM_W);
         if (ol) mark_norm(&v[n - 1], 1);
         T("attn_k_norm.weight", QXT_F32, 1, 128, 0, 0, DIST_NORM_W);
@@ -268,9 +287,12 @@ static uint32_t build_tensor_list(const qxgen_spec *sp, gen_tensor *v) {
         T("ffn_gate_inp.weight", QXT_F32, 2, H, E, 0, DIST_ROUTER);
         T("ffn_gate_exps.weight", t_gu, 3, H, F, E, 0);
         if (ol2) mark_rows(&v[n - 1], F, 7);
+        if (sat) mark_sat(&v[n - 1], F, 7);
         T("ffn_up_exps.weight", t_gu, 3, H, F, E, 0);
+        if (sat) mark_sat(&v[n - 1], F, 9);
         T("ffn_down_exps.weight", t_dn, 3, F, H, E, 0);
         if (ol2) mark_rows(&v[n - 1], H, 13);
+        if (sat) mark_sat(&v[n - 1], H, 13);
 #undef T
     }
     return n;
@@ -286,7 +308,7 @@ static uint32_t dtype_for(uint32_t type) {
 }
 
 static int write_fd(int fd, const qxgen_spec *spec, uint64_t *size_out, char *err, uint64_t err_len) {
-    if (!spec || spec->layers > 48 || spec->experts < 8 || spec->experts > 128 || !spec->vocab ||
+    if (!spec || spec->layers > 48 || spec->experts < 8 || spec->experts > 128 || !spec->vocab || spec->outliers > 3 ||
         (!spec->layers && !spec->with_head && !spec->with_embedding)) {
         set_err(err, err_len, "invalid generator spec"); return 0;
     }

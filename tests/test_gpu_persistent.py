@@ -92,6 +92,15 @@ def outlier_model(request):
     m.close()
 
 
+@pytest.fixture(scope="module")
+def sat_model():
+    m = qxg.MemModel(LAYERS, VOCAB, EXPERTS, seed=91, outliers=3)
+    om = qxo.Model(m.path)
+    yield m, om
+    om.close()
+    m.close()
+
+
 def open_ctx(path, chunks=None):
     """A persistent-path context; chunks None keeps the library's default threshold."""
     c = qxg.Context(0)
@@ -277,6 +286,40 @@ def test_outliers_same_input(outlier_model, chunks):
             head = pos >= len(prompt) - 1
             worst, top = replay_step(c, om, okv, pos, tok, head, moe_tol)
             say(f"outliers {pattern} {'walk' if chunks == WALK else 'chunked'}: position {pos} worst rel L2 {worst:.2e}")
+            tok = top if head else prompt[pos + 1]
+    finally:
+        c.close()
+
+
+SAT_TOL = 1e-4
+
+
+@pytest.mark.parametrize("chunks", [WALK, CHUNKS], ids=["walk", "chunked"])
+def test_saturated_scales_same_input(sat_model, chunks):
+    """Exponent-31 fp16 block scales (+inf, -inf, NaN and NaN with the sign bit, which the
+    reference reads as +-65504: src/qx_format.c:1854-1876) in every block of a Q, K, V and O
+    row of each layer and of a gate, up and down row of every expert.  The persistent
+    decode's packed layouts hold these scales saturated and its dots convert them with the
+    plain half conversion, so a scale field the packing missed (an infinity or NaN on the
+    device) or a lost sign shows here (an error of 1e-2 or more, or a non-finite value).  A
+    4-token prompt and 3 greedy steps, every step replayed layer by layer; the residual
+    stream reaches ~1e18.  Halves held to 1e-4: the saturated O row multiplies the context's
+    eight ~3.5e9 entries (the saturated V row's, one per q head of kv head 0), and its 4096
+    terms cancel ~290-fold (sum 4.6e15 of magnitudes 1.3e18, layer 3, position 1), so the
+    f32 sums of the digit dots reach 1.4e-5 of the row; measured: the per-phase kernels,
+    which convert the unsaturated scales themselves, give the same 1.445e-5 against the
+    oracle and agree with the persistent path to 3e-13."""
+    m, om = sat_model
+    c = open_ctx(m.path, chunks)
+    try:
+        c.kv_create(LAYERS, 16)
+        okv = qxo.KV(LAYERS, 16)
+        prompt = [5, 900, 17, 4000]
+        tok = prompt[0]
+        for pos in range(len(prompt) + 3):
+            head = pos >= len(prompt) - 1
+            worst, top = replay_step(c, om, okv, pos, tok, head, SAT_TOL, SAT_TOL)
+            say(f"saturated scales {'walk' if chunks == WALK else 'chunked'}: position {pos} worst rel L2 {worst:.2e}")
             tok = top if head else prompt[pos + 1]
     finally:
         c.close()
