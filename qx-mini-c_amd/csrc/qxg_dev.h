@@ -444,7 +444,10 @@ constexpr int DIG_STRIDE = 28;   // 16-byte aligned rows for ds_read_b128
 // scale 2^-k stay normal floats (groups below 2^-104 keep fewer than 22 bits).  A
 // non-finite group (mx passed as 0) gives p2 = 0; its values are discarded by the
 // caller's finiteness flag.  Digits: L = X mod 256 (signed), M the next byte of
-// (X - L) / 256, H = the rest.
+// (X - L) / 256, H = the rest, each in [-128, 127].  They come out of one subtraction:
+// X + 0x808080 (in [0, 2^24) for |X| <= 2^22) has bytes L + 128, M + 128, H + 128 (the
+// bias absorbs every borrow), so a byte transpose of four values and an XOR with 0x80 per
+// byte give the three planes.
 DEV void digits8(const float *y, float mx, uint32_t &ph0, uint32_t &ph1, uint32_t &pm0, uint32_t &pm1, uint32_t &pl0,
                  uint32_t &pl1, float &scale) {
     int e = 0;
@@ -452,26 +455,21 @@ DEV void digits8(const float *y, float mx, uint32_t &ph0, uint32_t &ph1, uint32_
     const int k = min(22 - e, 126);
     const float p2 = mx > 0.0f ? __uint_as_float((uint32_t)(k + 127) << 23) : 0.0f;
     scale = mx > 0.0f ? __uint_as_float((uint32_t)(127 - k) << 23) : 0.0f;
-    // per value: L = byte 0 of X; t1 = X - L has M in byte 1; X1 = t1 / 256 and
-    // t3 = X1 - sext(byte 0 of X1) has H in byte 1
-    uint32_t xl[8], xm[8], xh[8];
+    uint32_t xb[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int X = (int)(__float_as_uint(fmaf(y[i], p2, 12582912.0f)) - 0x4B400000u);
-        const int t1 = X - (int)(int8_t)X;
-        const int X1 = t1 >> 8;
-        xl[i] = (uint32_t)X;
-        xm[i] = (uint32_t)t1;
-        xh[i] = (uint32_t)(X1 - (int)(int8_t)X1);
+    for (int i = 0; i < 8; ++i) xb[i] = __float_as_uint(fmaf(y[i], p2, 12582912.0f)) - (0x4B400000u - 0x808080u);
+    // values v0..v3 -> [v0 b0, v1 b0, v0 b1, v1 b1] and [v0 b2, v1 b2, 0, 0] per pair, then merges
+    uint32_t pl[2], pm[2], ph[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const uint32_t *v = xb + 4 * q;
+        const uint32_t t0 = perm(v[1], v[0], 0x05010400u), t1 = perm(v[3], v[2], 0x05010400u);
+        const uint32_t u0 = perm(v[1], v[0], 0x0c0c0602u), u1 = perm(v[3], v[2], 0x0c0c0602u);
+        pl[q] = perm(t1, t0, 0x05040100u) ^ 0x80808080u;
+        pm[q] = perm(t1, t0, 0x07060302u) ^ 0x80808080u;
+        ph[q] = perm(u1, u0, 0x05040100u) ^ 0x80808080u;
     }
-    // byte B of 4 words -> one word: two pair packs, then one merge
-    auto pack4 = [](const uint32_t *v, uint32_t sel) {
-        const uint32_t lo = perm(v[1], v[0], sel), hi = perm(v[3], v[2], sel);
-        return perm(hi, lo, 0x05040100u);
-    };
-    pl0 = pack4(xl, 0x0c0c0400u); pl1 = pack4(xl + 4, 0x0c0c0400u);
-    pm0 = pack4(xm, 0x0c0c0501u); pm1 = pack4(xm + 4, 0x0c0c0501u);
-    ph0 = pack4(xh, 0x0c0c0501u); ph1 = pack4(xh + 4, 0x0c0c0501u);
+    pl0 = pl[0]; pl1 = pl[1]; pm0 = pm[0]; pm1 = pm[1]; ph0 = ph[0]; ph1 = ph[1];
 }
 
 // The vector (and norm weights) as loaded by one thread: 8 consecutive values per

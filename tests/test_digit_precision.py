@@ -37,6 +37,45 @@ def digits(y, group=32):
     return out.reshape(-1).astype(np.float32)
 
 
+def _perm(hi, lo, sel):
+    """v_perm_b32 for selector bytes 0..7 (bytes of lo, then hi) and 0x0c (zero)."""
+    src = [(lo >> (8 * i)) & 255 for i in range(4)] + [(hi >> (8 * i)) & 255 for i in range(4)]
+    out = np.zeros_like(lo)
+    for i in range(4):
+        s = (sel >> (8 * i)) & 255
+        out |= (np.zeros_like(lo) if s == 0x0C else src[s]) << (8 * i)
+    return out
+
+
+def test_digit_planes_from_one_subtraction():
+    """digits8's split of X (|X| <= 2^22) into signed bytes L, M, H with X = 65536 H + 256 M
+    + L: taken from the bytes of X + 0x808080 (each digit + 128) and packed four values a word
+    by its byte transpose, the planes equal the sequential peel (L = sext(X mod 256), then M
+    from (X - L) / 256, then H), for every X in range."""
+    X = np.arange(-(1 << 22), (1 << 22) + 1, dtype=np.int64)
+    sext = lambda v: ((v & 255) ^ 128) - 128
+    L = sext(X)
+    X1 = (X - L) >> 8
+    M = sext(X1)
+    H = (X1 - M) >> 8
+    assert np.array_equal(65536 * H + 256 * M + L, X)
+    assert H.min() >= -128 and H.max() <= 127
+    xb = X + 0x808080
+    assert xb.min() >= 0 and xb.max() < (1 << 24)
+    for d, sh in ((L, 0), (M, 8), (H, 16)):
+        assert np.array_equal(((xb >> sh) & 255) - 128, d)
+    # the byte transpose of four consecutive values (the device's perm selectors)
+    rng = np.random.default_rng(5)
+    v = [(rng.integers(-(1 << 22), (1 << 22) + 1, 4096) + 0x808080).astype(np.uint64) for _ in range(4)]
+    t0, t1 = _perm(v[1], v[0], 0x05010400), _perm(v[3], v[2], 0x05010400)
+    u0, u1 = _perm(v[1], v[0], 0x0C0C0602), _perm(v[3], v[2], 0x0C0C0602)
+    planes = (_perm(t1, t0, 0x05040100) ^ 0x80808080, _perm(t1, t0, 0x07060302) ^ 0x80808080,
+              _perm(u1, u0, 0x05040100) ^ 0x80808080)
+    for byte, plane in enumerate(planes):
+        want = sum(((((v[j] >> (8 * byte)) & 255) - 128) & 255) << (8 * j) for j in range(4))
+        assert np.array_equal(plane, want)
+
+
 def expert_matvec(om, name, e, rows, in_dims, block_bytes, x):
     """(float) of the double dot of expert e's rows with f32 x: the oracle's matvec, the
     reference's arithmetic (src/qx_format.c:4739-4787)."""
