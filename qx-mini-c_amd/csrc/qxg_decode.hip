@@ -173,7 +173,7 @@ struct AttnS {
     uint32_t qok;
     AttnW w[NWV];
     int8_t kq[512], vq[512];        // the position's INT8 K and V rows (cache store)
-    float ctx[NWV][4][128];         // per wave and position subgroup: context partial sums
+    float ctx[NWV][128];            // per wave: context partial sums
     double m[NWV], l[NWV];          // per wave: running maximum and denominator
 };
 struct AttnK {                      // stage A by kv head and position chunk (attention_chunk_part)
@@ -905,8 +905,14 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
         if (t0 + 128 < n) cur = nxt;
     }
     DMARK(l, 23);
+    // the wave's four 16-lane rows (positions 4 i + p4) summed by the wave itself, so the
+    // merge below reads one partial per wave
 #pragma unroll
-    for (int i = 0; i < 8; ++i) A.ctx[w][p4][8 * dg + i] = acc[i];
+    for (int i = 0; i < 8; ++i) acc[i] = rows4_sum(acc[i]);
+    if (p4 == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) A.ctx[w][8 * dg + i] = acc[i];
+    }
     if (lane == 0) { A.m[w] = m; A.l[w] = lsum; }
     __syncthreads();
     DMARK(l, 24);
@@ -925,8 +931,7 @@ DEV void attention(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep, cons
         float o = 0.0f;
 #pragma unroll
         for (int v = 0; v < NWV; ++v) {
-            const float part = (A.ctx[v][0][tid] + A.ctx[v][1][tid]) + (A.ctx[v][2][tid] + A.ctx[v][3][tid]);
-            o = fmaf((float)(fw[v] * invL), part, o);
+            o = fmaf((float)(fw[v] * invL), A.ctx[v][tid], o);
         }
         xstf(gpw(a.xch) + XO_CX + (l & 1) * XN_CX + 128 * h + tid, ep + 1, o);   // the CX phase
         if (rrow >= 0 && a.d_wsum && tid == 0) {   // the head's sum of normalised weights (the state loop's softmax_sum)
