@@ -1143,9 +1143,7 @@ DEV bool attention_chunk_part(const QxDArgs &a, uint32_t l, uint32_t pos, uint32
         for (int b = 0; b < 8; ++b) acc[b] = fmaf(pv, (float)(int8_t)((((b < 4) ? x.x : x.y) >> (8 * (b & 3))) & 255u), acc[b]);
     }
 #pragma unroll
-    for (int b = 0; b < 8; ++b) acc[b] += __shfl_xor(acc[b], 16);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) acc[b] += __shfl_xor(acc[b], 32);
+    for (int b = 0; b < 8; ++b) acc[b] = rows4_sum_pairs(acc[b]);
     // ---- the wave's partial result, 8 records of 16 dimensions: lanes 0..31 the context sums
     // (lane (p4 < 2, dg): dims 8 dg + 4 p4 .. of record dg / 2), lanes 32..63 the maximum and
     // the denominator
@@ -1206,8 +1204,7 @@ DEV bool attention_merge(const QxDArgs &a, uint32_t l, uint32_t pos, uint32_t ep
         const int dd = lane & 15, cg = lane >> 4;
         float o = 0.0f;
         for (uint32_t cc = (uint32_t)cg; cc < nch; cc += 4) o = fmaf(wt[cc], __uint_as_float(rw[QXD_PREC * cc + dd]), o);
-        o += __shfl_xor(o, 16);
-        o += __shfl_xor(o, 32);
+        o = rows4_sum_pairs(o);
         if (lane < 16) xstf(X + XO_CX + par * XN_CX + 128 * h + 16 * dgm + lane, ep, o);   // the CX phase
     }
     DMARK(l, 39);

@@ -652,6 +652,15 @@ DEV float rows4_sum(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// The same sum in the order of xor-16 then xor-32 shuffles, (row 0 + row 1) + (row 2 + row 3)
+// in every lane, bit for bit what two __shfl_xor steps give, without their LDS round trips.
+DEV float rows4_sum_pairs(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), true, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), true, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // R per-lane partial sums (one per row, R in {1,2,4,8}) reduced over the wave:
 // up to two split rounds inside each quad (a lane keeps half of the rows and adds
 // its partner's half), then row16 sums, then the four 16-lane rows (rows4_sum) and
