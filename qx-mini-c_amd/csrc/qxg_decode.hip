@@ -66,11 +66,11 @@ extern "C" int qxd_trace_read(unsigned long long *out) {
 // chunk records of the chunked stage A's merge), in units of 64 cycles (s_sleep).  A workgroup reaches a poll right after storing its own
 // outputs, ahead of most producers, and poll rounds issued while the words are still in
 // flight only load the memory system that the producers' stores and the weight copies go
-// through.  Measured on the benchmark: 16 (~0.43 us) each and 24 for the merge; longer or
-// shorter was slower, a sleep between rounds was slower, and delaying the other polls gave
-// nothing.
+// through.  Measured on the benchmark: 24 (~0.64 us) for x and the merge, 16 (~0.43 us) for
+// x' and h; longer or shorter was slower, a sleep between rounds was slower, and delaying
+// the other polls gave nothing.
 #ifndef QXD_SLEEP_X
-#define QXD_SLEEP_X 16
+#define QXD_SLEEP_X 24
 #endif
 #ifndef QXD_SLEEP_XP
 #define QXD_SLEEP_XP 16
