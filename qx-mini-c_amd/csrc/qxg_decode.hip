@@ -62,13 +62,15 @@ extern "C" int qxd_trace_read(unsigned long long *out) {
 #define DMARKT(layer, point, thread) ((void)0)
 #endif
 
-// First-round delays of four exchange polls (x in stage Q, x' in stage G, h in stage D, the
-// chunk records of the chunked stage A's merge), in units of 64 cycles (s_sleep).  A workgroup reaches a poll right after storing its own
+// First-round delays of five exchange polls (x in stage Q, x' in stage G, h in stage D, the
+// chunk records of the chunked stage A's merge and, in the chunked kernel, the context in
+// stage O), in units of 64 cycles (s_sleep).  A workgroup reaches a poll right after storing its own
 // outputs, ahead of most producers, and poll rounds issued while the words are still in
 // flight only load the memory system that the producers' stores and the weight copies go
 // through.  Measured on the benchmark: 24 (~0.64 us) for x and the merge, 16 (~0.43 us) for
-// x' and h; longer or shorter was slower, a sleep between rounds was slower, and delaying
-// the other polls gave nothing.
+// x', h and the chunked kernel's context (every workgroup publishes 16 merged dimensions,
+// then polls all 4096); longer or shorter was slower, a sleep between rounds was slower, and
+// delaying the other polls (the walk kernel's context among them) gave nothing.
 #ifndef QXD_SLEEP_X
 #define QXD_SLEEP_X 24
 #endif
@@ -80,6 +82,9 @@ extern "C" int qxd_trace_read(unsigned long long *out) {
 #endif
 #ifndef QXD_SLEEP_MG
 #define QXD_SLEEP_MG 24
+#endif
+#ifndef QXD_SLEEP_CX
+#define QXD_SLEEP_CX 16
 #endif
 #define QXD_SLEEP(n) \
     do { \
@@ -1520,6 +1525,7 @@ DEV void decode_steps(const QxDArgs &args) {
             {
                 const int tid = tix(), lane = tid & 63, wave = tid >> 6, ib = lane & 7;
                 // sentinels: words 128 h and 128 h + 64 (the two store instructions of head h)
+                if constexpr (CHUNKED) QXD_SLEEP(QXD_SLEEP_CX);
                 if (!wait_xch2<4>(X + XO_CX + par * XN_CX, 4096, ep + 2, S.u.m.vin, Ident(), S, ctl))
                     return;
                 DMARK(l, 5);
