@@ -364,6 +364,32 @@ def test_q8k_same_input(model, chunks):
         om.close()
 
 
+@pytest.mark.parametrize("chunks", [WALK, CHUNKS], ids=["walk", "chunked"])
+def test_q8k_saturated_scales_same_input(sat_model, chunks):
+    """The exponent-31 block scales of test_saturated_scales_same_input through the Q8_K
+    instantiation (its dots read the same saturated layouts): a 4-token prompt and 3 greedy
+    steps replayed layer by layer by the oracle in q8_k_compat, halves at REQ_TOL (the
+    q8_k_compat bar, above the f32 test's 1e-4), logits at 1e-5."""
+    m, _ = sat_model
+    om = qxo.Model(m.path, activation="q8_k_compat")
+    c = open_ctx(m.path, chunks)
+    c.set_activation("q8_k_compat")
+    try:
+        assert c.persistent_path()
+        c.kv_create(LAYERS, 16)
+        okv = qxo.KV(LAYERS, 16)
+        prompt = [5, 900, 17, 4000]
+        tok = prompt[0]
+        for pos in range(len(prompt) + 3):
+            head = pos >= len(prompt) - 1
+            worst, top = replay_step(c, om, okv, pos, tok, head, moe_tol=REQ_TOL, att_tol=REQ_TOL)
+            say(f"q8k saturated scales {'walk' if chunks == WALK else 'chunked'}: position {pos} worst rel L2 {worst:.2e}")
+            tok = top if head else prompt[pos + 1]
+    finally:
+        c.close()
+        om.close()
+
+
 def test_q8k_generate_matches_steps(model):
     """q8_k_compat: one persistent launch over a prompt and 6 greedy tokens gives the
     tokens of the step-by-step calls (the same kernel, step by step)."""
